@@ -1,0 +1,153 @@
+"""Benchmark: SB-shape route n-gram memory layer forward on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one forward of the SB-shape memory layer (d 1024, 184 routes, bf16 tables,
+8 x 2048 tokens, hidden-state router) over resident synthetic inputs: router GEMM +
+sign-pack, query projection, fused gather + sink readout, output projection, causal
+conv.  Prints one JSON line with whole-job tokens/s, the fused kernel's roofline
+(algorithmic bytes / HIP-event duration) and a CPU baseline (the oracle's PyTorch-CPU
+restatement of the reference forward, timed on a bounded sample).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT), str(ROOT / "lngram-decode_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "memory-layer tokens/s + % HBM roofline at SB shape; draft-step latency (us)"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """Oracle's PyTorch-CPU restatement of the reference SB forward (bf16, reference op order) on a
+    bounded sample of the SB workload: 1 x 64-token windows, repeated for ~``seconds``."""
+    import numpy as np
+    import torch
+
+    from lngram_hip import workloads
+    from oracle import memory as om
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    w = workloads.SB.with_shape(1, 64)
+    mem = workloads.build_memory(w, seed=0, device="cpu")
+    sd = {k: v.detach() for k, v in mem.state_dict().items()}
+    p = {k[len("module."):]: v for k, v in sd.items() if k.startswith("module.")}
+    p["router.weight"] = sd["router.weight"]
+    cfg = om.MemCfg(w.d_model, w.routes, w.mem_dim, w.q_heads, w.kv_heads, w.head_dim, eps=w.norm_eps)
+    h = workloads.make_hidden(w, seed=1)
+    ones = torch.ones(w.d_model, dtype=w.dtype)
+    n_tok, t0 = 0, time.perf_counter()
+    while True:
+        h_norm = om.rms_norm(h, ones, w.norm_eps)
+        q = om.router_logits(h_norm, p["router.weight"], work=torch.float32)
+        codes = om.pack_route_codes(q.numpy(), 4)
+        om.memory_forward(p, cfg, h, codes)
+        n_tok += w.tokens
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    del np
+    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"SB shape (d1024, R184, bf16) 1x64-token windows, {n_tok} tokens in {el:.1f} s, "
+                      "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the hot path is single-GPU; --gpus {args.gpus} is not supported)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from lngram_hip import _lib, ops, workloads
+
+    if not _lib.LIB_PATH.exists():
+        import __graft_entry__
+
+        __graft_entry__.build()
+    dev = torch.device("cuda:0")
+    w = workloads.SB
+    log(f"building {w.name}")
+    mem = workloads.build_memory(w, seed=0, device=dev)
+    h = workloads.make_hidden(w, seed=1, device=dev)
+    h_norm = ops.rmsnorm(h, torch.ones(w.d_model, dtype=w.dtype, device=dev), w.norm_eps)
+    torch.cuda.synchronize()
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            mem(h, h_norm)
+        torch.cuda.synchronize()
+        log(f"warmup done ({args.warmup}), timing {args.steps} steps")
+        with ops.KernelTimer("memory_readout_fused") as kt:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                mem(h, h_norm)
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+        fused_ms = kt.mean_ms()
+    ms = el / args.steps * 1e3
+    tok_s = w.tokens / (el / args.steps)
+    # fused kernel algorithmic bytes per launch: rows (R x 2 orders x 256 B) + query + codes read,
+    # head output written
+    es = 2
+    fused_bytes = w.tokens * (w.routes * 2 * w.mem_dim * es + 2 * w.d_model * es + w.routes)
+    achieved = fused_bytes / (fused_ms * 1e-3) / 1e9
+    layer_bytes = w.tokens * w.algorithmic_bytes_per_token() + w.weight_bytes()
+    layer_gbs = layer_bytes / (el / args.steps) / 1e9
+    log(f"{ms:.3f} ms/step, {tok_s / 1e6:.2f} M tok/s, fused kernel {fused_ms * 1e3:.1f} us "
+        f"({achieved:.0f} GB/s)")
+
+    result = {
+        "metric": METRIC,
+        "value": tok_s,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) hidden states, N(0,0.02) weights/tables)",
+        "config": {"workload": "SB-shape layer-1 memory forward, hidden-state router", "d_model": w.d_model,
+                   "routes": w.routes, "mem_dim": w.mem_dim, "batch": w.batch, "seq_len": w.seq,
+                   "table_params": w.routes * (256 + 4096) * w.mem_dim},
+        "roofline": {"bound": "hbm", "kernel": "k_readout_fused", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": fused_bytes, "avg_ms": fused_ms},
+        "layer_hbm_frac": layer_gbs / HBM_PEAK_GBS,
+        "layer_algorithmic_bytes": layer_bytes,
+    }
+    if not args.no_cpu:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

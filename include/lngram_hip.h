@@ -1,0 +1,158 @@
+/*
+ * lngram_hip.h -- C ABI of the MI355X (gfx950) route n-gram memory hot path.
+ *
+ * Conventions (every entry point):
+ *   - Tensors are caller-owned device buffers, row-major and contiguous.
+ *   - Calls are ordered on `stream` (a hipStream_t passed as void*), allocate
+ *     nothing, keep no pointer after return, and return 0 or a negative LNG_E_*.
+ *   - lng_last_error() returns a thread-local message for the last failure.
+ *   - No mutable globals: calls are reentrant from any host thread.
+ *   - dtype codes: LNG_F32, LNG_BF16, LNG_F16, LNG_U8, LNG_I32, LNG_I64.
+ *
+ * Each declaration names the reference interface (file:line in the reference
+ * repository) whose computation it replaces.
+ */
+#ifndef LNGRAM_HIP_H
+#define LNGRAM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { LNG_F32 = 0, LNG_BF16 = 1, LNG_F16 = 2, LNG_U8 = 3, LNG_I32 = 4, LNG_I64 = 5 };
+enum {
+  LNG_OK = 0,
+  LNG_E_ARG = -1,      /* bad shape / argument */
+  LNG_E_DTYPE = -2,    /* unsupported dtype combination */
+  LNG_E_HIP = -3,      /* HIP launch / runtime error */
+  LNG_E_RANGE = -4     /* value out of range (token id, index) */
+};
+
+int lng_abi_version(void);
+const char* lng_last_error(void);
+
+/* ---------------------------------------------------------------- K1: router */
+/* y[M,N] (fp32) = x[M,K] . w[N,K]^T.  LngramMemory.route_logits
+ * (ffnmem/memory/wrapper.py:98-101).  bf16 x bf16 runs on MFMA with fp32
+ * accumulation (products of bf16 values are exact in fp32); f32 x f32 runs in
+ * fp32 FMA.  If `codes` is non-null the epilogue also sign-packs every `bits`
+ * consecutive channels into route codes (lngram_v2.py:74-89, :1012-1017) of
+ * dtype codes_dtype (LNG_U8 or LNG_I32), shape [M, N/bits]; `logits` may be null. */
+int lng_router_codes(const void* x, int x_dtype, const void* w, int w_dtype, int64_t M, int64_t K,
+                     int64_t N, int32_t bits, float* logits, void* codes, int codes_dtype, void* stream);
+
+/* codes[M, C/bits] = pack(logits[M, C] > 0).  quantize_route_logits
+ * (lngram_v2.py:1012-1017 -> pack_bits_to_route_codes :74-89). */
+int lng_pack_route_codes(const float* logits, int64_t M, int64_t C, int32_t bits, void* codes,
+                         int codes_dtype, void* stream);
+
+/* ---------------------------------------------------------------- K2: addresses / rows */
+/* addr[B, T-order+1, R] = sum_k codes[b, t'+k, r] << (k*bits).
+ * _aligned_ngram_address (lngram_v2.py:314-325).  out_dtype LNG_I32 or LNG_I64. */
+int lng_ngram_address(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R,
+                      int32_t order, int32_t bits, void* out, int out_dtype, void* stream);
+
+/* rows[B, T, route_end-route_start, n_orders] (int32): global table row of each
+ * order-n n-gram ending at t, or -1 where _lookup_route_chunk masks it to zero
+ * (lngram_v2.py:1047-1092, _valid_mask :1027-1045).  segment_ids [B,T] int32 and
+ * valid_tokens [B,T] uint8 may be null. */
+int lng_ngram_rows(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R,
+                   int32_t route_start, int32_t route_end, const int32_t* orders, int32_t n_orders,
+                   int32_t bits, const int32_t* segment_ids, const uint8_t* valid_tokens,
+                   int32_t* rows, void* stream);
+
+/* ---------------------------------------------------------------- K3: gather / readout */
+/* Route tokens out[B, T_out, route_end-route_start, n_orders*mem_dim] in the
+ * tables' dtype (LNG_F32 / LNG_BF16 / LNG_F16): _lookup_route_chunk in eval
+ * (lngram_v2.py:1047-1113).  tables[i] is the [R*2^(bits*orders[i]), mem_dim]
+ * table of order orders[i].  T_out = T, or target_length if > 0 (last positions). */
+int lng_route_tokens(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R,
+                     int32_t route_start, int32_t route_end, const int32_t* orders, int32_t n_orders,
+                     int32_t bits, const void* const* tables, int table_dtype, int32_t mem_dim,
+                     const int32_t* segment_ids, const uint8_t* valid_tokens, int32_t target_length,
+                     void* out, void* stream);
+
+/* out[rows, dim] = RMSNorm(x) * w with the reference rounding: normalise in fp32,
+ * round to the storage dtype, multiply by w.  lngram_v2.RMSNorm
+ * (lngram_v2.py:36-53) and model.RMSNorm (model.py:39-48). */
+int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps,
+                void* out, void* stream);
+
+/* y[M,N] = x[M,K] . w[N,K]^T in `dtype` (fp32 accumulation, output rounded to
+ * dtype).  nn.Linear without bias as used by readout_q_proj / readout_kv_proj /
+ * readout_o_proj (lngram_v2.py:1115-1131, :1354-1359) and the draft head. */
+int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, int64_t K, void* y,
+               void* stream);
+
+/* RouteNgramMemoryV2._manual_gqa (lngram_v2.py:1899-1920) with the sink
+ * denominator of _real_route_probabilities (:1887-1897): query [BT, KV*G, hd],
+ * key/value [BT, KV, R, hd] -> out [BT, KV*G, hd].  Scores are rounded to the
+ * storage dtype before the fp32 scale, probabilities before the value product. */
+int lng_sink_attention(const void* query, const void* key, const void* value, int dtype, int64_t BT,
+                       int32_t kv_heads, int32_t groups, int32_t R, int32_t head_dim, float scale,
+                       float sink_logit, void* out, void* stream);
+
+/* Same, with element strides {bt, kv_head, route} for key and value (the head
+ * dim is contiguous): accepts the permuted views _project_memory returns
+ * (lngram_v2.py:1120-1131) without a copy. */
+int lng_sink_attention_strided(const void* query, const void* key, const void* value, int dtype, int64_t BT,
+                               int32_t kv_heads, int32_t groups, int32_t R, int32_t head_dim,
+                               const int64_t* key_strides, const int64_t* value_strides, float scale,
+                               float sink_logit, void* out, void* stream);
+
+/* _real_route_probabilities (lngram_v2.py:1887-1897): probs[M,R] (fp32) from
+ * scores[M,R] (fp32) with a zero-value sink logit in the denominator. */
+int lng_sink_probabilities(const float* scores, int64_t M, int32_t R, float sink_logit, float* probs,
+                           void* stream);
+
+/* DepthwiseCausalConv.forward (lngram_v2.py:273-286) and, with residual != 0,
+ * the _finish residual (:1354-1359): out = [mixed +] SiLU(conv_dil(RMSNorm(mixed))),
+ * taps conv_w[d, K] oldest->newest, zero left padding.  mixed/out [B, T, d]. */
+int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, int dtype, int64_t B,
+                    int64_t T, int32_t d, int32_t K, int32_t dilation, float eps, int residual, void* out,
+                    void* stream);
+
+/* Fused memory readout (the metric kernel).  Replaces, in eval, the chain
+ * _lookup_route_chunk -> _project_memory -> _manual_gqa of
+ * RouteNgramMemoryV2.forward (lngram_v2.py:1361-1407) by the associativity
+ *   score_{h,g,r} = s_r * ((w_mem . Wk[h]^T q_{h,g}) . x_r) * scale,
+ *   o_{h,g}       = Wv[h] (w_mem . sum_r p_{h,g,r} s_r x_r)
+ * with an online softmax seeded by the sink (m, l) = (b0, 1).  bf16 only;
+ * shape: orders (2,3), mem_dim 128, 16 query heads x 64, 4 KV heads.
+ *   q       [N_tok, 16*64]  projected query (readout_q_proj output)
+ *   codes   [B, T, R] uint8 route codes
+ *   table2  [R*256, 128], table3 [R*4096, 128]
+ *   wk_t    [4, 256, 64]    key weight, per head transposed (f-major)
+ *   wv      [4, 64, 256]    value weight (kv_proj rows 256..511)
+ *   w_mem   [256]           readout_memory_norm.weight
+ *   head_out[N_tok, 16*64]  attention output (input of readout_o_proj) */
+int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int64_t T, int32_t R,
+                             const void* table2, const void* table3, const void* wk_t, const void* wv,
+                             const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
+                             void* stream);
+
+/* ---------------------------------------------------------------- K4: SSM scan */
+/* s[B,T,N] (fp32): s_t = a*s_{t-1} + (1-a)*u_t, s_{-1} = s0 (zero if null).
+ * chunked_scan / sequential_scan (ffnmem/memory/ssm.py:58-91) and the carried
+ * state of ssm_continue (ffnmem/infer.py:125-137).  `workspace` holds
+ * lng_ssm_workspace_bytes(B, T, N) bytes of per-chunk end states. */
+size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N);
+int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
+                 float* workspace, float* s, void* stream);
+
+/* ---------------------------------------------------------------- K5: drafting */
+/* Tree acceptance (drafting/tree.py:205-220): from the root take the first child
+ * (index order) whose token equals argmax[cur]; repeat.  path[n] receives the
+ * node path (root first), *path_len its length, new_tokens[n] the accepted
+ * tokens followed by argmax at the last path node (path_len entries). */
+int lng_tree_accept(const int32_t* parent, const int64_t* node_tokens, const int64_t* argmax, int32_t n,
+                    int32_t* path, int32_t* path_len, int64_t* new_tokens, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LNGRAM_HIP_H */

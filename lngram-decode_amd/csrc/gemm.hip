@@ -1,0 +1,251 @@
+// Dense projections: y[M,N] = x[M,K] . w[N,K]^T (nn.Linear without bias).
+//
+// bf16 runs on MFMA (v_mfma_f32_16x16x32_bf16, fp32 accumulation): a 256-thread
+// block computes a 128 (w rows) x 128 (x rows) tile, each wave a 64x64 quarter
+// as 4x4 MFMA tiles, with K staged through double-buffered LDS in steps of 64.
+// The MFMA "A" operand is the weight, so each lane ends up holding 4
+// consecutive output channels of one token: a packed store for plain outputs,
+// and exactly one route's 4 sign bits for the router epilogue.
+// fp32 runs on a VALU tile kernel (the tiny fp32 layer and fp32 routers).
+#include "common.h"
+
+namespace lng {
+
+enum { EPI_BF16 = 0, EPI_F32 = 1, EPI_ROUTER = 2 };
+
+constexpr int GB = 128;     // block tile (both operands)
+constexpr int GK = 64;      // K step per LDS stage
+constexpr int GLD = GK + 8; // padded LDS row (bf16): 144 B stride, conflict-free b128 reads
+
+template <int EPI>
+__global__ __launch_bounds__(256) void k_gemm_nt_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
+                                                      int64_t N, int64_t M, int64_t K, void* __restrict__ out,
+                                                      float* __restrict__ logits, void* __restrict__ codes,
+                                                      int codes_dt, int64_t routes) {
+  __shared__ __attribute__((aligned(16))) bf16 Ws[2][GB * GLD];
+  __shared__ __attribute__((aligned(16))) bf16 Xs[2][GB * GLD];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * GB;  // weight rows (output channels)
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * GB;  // x rows (tokens)
+  const int nk = static_cast<int>((K + GK - 1) / GK);
+
+  // global -> register staging: 128 rows x 8 chunks of 16 B per operand, 4 chunks per thread
+  u32x4 rw[4], rx[4];
+  auto gload = [&](int kt) {
+    const int64_t kb = static_cast<int64_t>(kt) * GK;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + c * 256;
+      const int row = idx >> 3, kc = idx & 7;
+      const int64_t k = kb + kc * 8;
+      u32x4 z = {0u, 0u, 0u, 0u};
+      rw[c] = (n0 + row < N && k < K) ? *reinterpret_cast<const u32x4*>(W + (n0 + row) * K + k) : z;
+      rx[c] = (m0 + row < M && k < K) ? *reinterpret_cast<const u32x4*>(X + (m0 + row) * K + k) : z;
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int idx = tid + c * 256;
+      const int row = idx >> 3, kc = idx & 7;
+      *reinterpret_cast<u32x4*>(&Ws[buf][row * GLD + kc * 8]) = rw[c];
+      *reinterpret_cast<u32x4*>(&Xs[buf][row * GLD + kc * 8]) = rx[c];
+    }
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < GK / 32; ++ks) {
+      bf16x8 a[4], b[4];
+      const int kof = ks * 32 + 8 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = *reinterpret_cast<const bf16x8*>(&Ws[cur][(wr * 64 + i * 16 + (lane & 15)) * GLD + kof]);
+        b[i] = *reinterpret_cast<const bf16x8*>(&Xs[cur][(wc * 64 + i * 16 + (lane & 15)) * GLD + kof]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // epilogue: lane holds out[m][n .. n+3] for n = n0 + wr*64 + i*16 + 4*(lane>>4), m = m0 + wc*64 + j*16 + lane%16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + wr * 64 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = m0 + wc * 64 + j * 16 + (lane & 15);
+      if (m >= M) continue;
+      const f32x4 v = acc[i][j];
+      if (EPI == EPI_BF16) {
+        bf16* o = static_cast<bf16*>(out) + m * N + n;
+        if (n + 3 < N && (N & 3) == 0) {
+          bf16x4 pk = {static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]),
+                       static_cast<bf16>(v[3])};
+          *reinterpret_cast<bf16x4*>(o) = pk;
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = static_cast<bf16>(v[e]);
+        }
+      } else if (EPI == EPI_F32) {
+        float* o = static_cast<float*>(out) + m * N + n;
+        if (n + 3 < N && (N & 3) == 0) {
+          *reinterpret_cast<f32x4*>(o) = v;
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = v[e];
+        }
+      } else {  // router: 4 bits per route, n is a multiple of 4
+        if (n >= N) continue;
+        if (logits) *reinterpret_cast<f32x4*>(logits + m * N + n) = v;
+        const int code = (v[0] > 0.f ? 1 : 0) | (v[1] > 0.f ? 2 : 0) | (v[2] > 0.f ? 4 : 0) | (v[3] > 0.f ? 8 : 0);
+        const int64_t r = n >> 2;
+        if (codes_dt == LNG_U8)
+          static_cast<uint8_t*>(codes)[m * routes + r] = static_cast<uint8_t>(code);
+        else
+          static_cast<int32_t*>(codes)[m * routes + r] = code;
+      }
+    }
+  }
+}
+
+// fp32 VALU tile GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
+// K staged through LDS 16 at a time.  A/B element types may be float or bf16.
+template <typename TA, typename TB, typename TO>
+__global__ __launch_bounds__(256) void k_gemm_nt_f32(const TA* __restrict__ X, const TB* __restrict__ W, int64_t M,
+                                                     int64_t N, int64_t K, TO* __restrict__ Y) {
+  __shared__ float xs[16][64 + 1];
+  __shared__ float ws[16][64 + 1];
+  const int tid = threadIdx.x;
+  const int tx = tid & 15, ty = tid >> 4;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * 64, n0 = static_cast<int64_t>(blockIdx.x) * 64;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < K; k0 += 16) {
+    for (int e = tid; e < 16 * 64; e += 256) {
+      const int r = e >> 4, kk = e & 15;
+      const int64_t k = k0 + kk;
+      xs[kk][r] = (m0 + r < M && k < K) ? to_f32(X[(m0 + r) * K + k]) : 0.f;
+      ws[kk][r] = (n0 + r < N && k < K) ? to_f32(W[(n0 + r) * K + k]) : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float xv[4], wv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xv[i] = xs[kk][ty * 4 + i];
+        wv[i] = ws[kk][tx * 4 + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xv[i], wv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t m = m0 + ty * 4 + i;
+    if (m >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t n = n0 + tx * 4 + j;
+      if (n < N) Y[m * N + n] = from_f32<TO>(acc[i][j]);
+    }
+  }
+}
+
+template <int EPI>
+static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, void* out, float* logits,
+                       void* codes, int codes_dt, int64_t routes, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(cdiv(N, GB)), static_cast<unsigned>(cdiv(M, GB)));
+  hipLaunchKernelGGL(k_gemm_nt_bf16<EPI>, grid, dim3(256), 0, s, w, x, N, M, K, out, logits, codes, codes_dt, routes);
+  return check_launch("gemm_bf16");
+}
+
+template <typename TA, typename TB, typename TO>
+static int launch_f32(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(cdiv(N, 64)), static_cast<unsigned>(cdiv(M, 64)));
+  hipLaunchKernelGGL((k_gemm_nt_f32<TA, TB, TO>), grid, dim3(256), 0, s, static_cast<const TA*>(x),
+                     static_cast<const TB*>(w), M, N, K, static_cast<TO*>(y));
+  return check_launch("gemm_f32");
+}
+
+// Shared entry for bf16 MFMA linears (used by other translation units).
+int linear_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s) {
+  return launch_mfma<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, y, nullptr,
+                               nullptr, 0, 0, s);
+}
+
+}  // namespace lng
+
+using namespace lng;
+
+extern "C" {
+
+int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, int64_t K, void* y, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(LNG_E_ARG, "linear: bad shape");
+  if (M == 0) return LNG_OK;
+  hipStream_t s = as_stream(stream);
+  if (dtype == LNG_BF16) {
+    if (K % 8) return fail(LNG_E_ARG, "linear: bf16 needs K % 8 == 0");
+    return linear_bf16(x, w, M, N, K, y, s);
+  }
+  if (dtype == LNG_F32) return launch_f32<float, float, float>(x, w, M, N, K, y, s);
+  return fail(LNG_E_DTYPE, "linear: dtype must be f32 or bf16");
+}
+
+int lng_router_codes(const void* x, int x_dtype, const void* w, int w_dtype, int64_t M, int64_t K, int64_t N,
+                     int32_t bits, float* logits, void* codes, int codes_dtype, void* stream) {
+  if (M < 0 || K <= 0 || N <= 0 || bits <= 0 || bits > 8 || N % bits)
+    return fail(LNG_E_ARG, "router_codes: bad shape");
+  if (codes && codes_dtype != LNG_U8 && codes_dtype != LNG_I32) return fail(LNG_E_DTYPE, "router_codes: codes u8/i32");
+  if (!codes && !logits) return fail(LNG_E_ARG, "router_codes: nothing to write");
+  if (M == 0) return LNG_OK;
+  hipStream_t s = as_stream(stream);
+  const int64_t routes = N / bits;
+  if (x_dtype == LNG_BF16 && w_dtype == LNG_BF16 && K % 8 == 0) {
+    if (codes && bits == 4)
+      return launch_mfma<EPI_ROUTER>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, nullptr,
+                                     logits, codes, codes_dtype, routes, s);
+    if (!logits) return fail(LNG_E_ARG, "router_codes: bits != 4 needs a logits buffer");
+    if (int rc = launch_mfma<EPI_F32>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, logits,
+                                      nullptr, nullptr, 0, 0, s))
+      return rc;
+  } else {
+    if (!logits) return fail(LNG_E_ARG, "router_codes: fp32 router needs a logits buffer");
+    int rc;
+    if (x_dtype == LNG_F32 && w_dtype == LNG_F32)
+      rc = launch_f32<float, float, float>(x, w, M, N, K, logits, s);
+    else if (x_dtype == LNG_BF16 && w_dtype == LNG_F32)
+      rc = launch_f32<bf16, float, float>(x, w, M, N, K, logits, s);
+    else if (x_dtype == LNG_F32 && w_dtype == LNG_BF16)
+      rc = launch_f32<float, bf16, float>(x, w, M, N, K, logits, s);
+    else if (x_dtype == LNG_BF16 && w_dtype == LNG_BF16)
+      rc = launch_f32<bf16, bf16, float>(x, w, M, N, K, logits, s);
+    else
+      return fail(LNG_E_DTYPE, "router_codes: x/w must be f32 or bf16");
+    if (rc) return rc;
+  }
+  if (!codes) return LNG_OK;
+  return lng_pack_route_codes(logits, M, N, bits, codes, codes_dtype, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+"""ctypes binding of ``liblngram_hip.so`` (the gfx950 C ABI declared in ``include/lngram_hip.h``).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime torch has
+already loaded (same SONAME), which makes torch's stream handles valid arguments.
+There is no fallback: if the library is missing, every op raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (loads the HIP runtime this library must share)
+
+LIB_PATH = Path(__file__).resolve().parent / "liblngram_hip.so"
+
+# dtype codes (include/lngram_hip.h)
+F32, BF16, F16, U8, I32, I64 = 0, 1, 2, 3, 4, 5
+
+_p = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+_f = ctypes.c_float
+_int = ctypes.c_int
+_P64 = ctypes.POINTER(ctypes.c_int64)
+_P32 = ctypes.POINTER(ctypes.c_int32)
+
+# name -> (restype, argtypes); must cover every function declared in the header
+SIGNATURES = {
+    "lng_abi_version": (_int, []),
+    "lng_last_error": (ctypes.c_char_p, []),
+    "lng_router_codes": (_int, [_p, _int, _p, _int, _i64, _i64, _i64, _i32, _p, _p, _int, _p]),
+    "lng_pack_route_codes": (_int, [_p, _i64, _i64, _i32, _p, _int, _p]),
+    "lng_ngram_address": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _p, _int, _p]),
+    "lng_ngram_rows": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32, _p, _p, _p, _p]),
+    "lng_route_tokens": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32,
+                                ctypes.POINTER(_p), _int, _i32, _p, _p, _i32, _p, _p]),
+    "lng_rmsnorm": (_int, [_p, _p, _int, _i64, _i32, _f, _p, _p]),
+    "lng_linear": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _p]),
+    "lng_sink_attention": (_int, [_p, _p, _p, _int, _i64, _i32, _i32, _i32, _i32, _f, _f, _p, _p]),
+    "lng_sink_attention_strided": (_int, [_p, _p, _p, _int, _i64, _i32, _i32, _i32, _i32, _P64, _P64,
+                                          _f, _f, _p, _p]),
+    "lng_sink_probabilities": (_int, [_p, _i64, _i32, _f, _p, _p]),
+    "lng_causal_conv": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
+    "lng_memory_readout_fused": (_int, [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _p, _f, _f, _f, _p, _p]),
+    "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
+    "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p, _p]),
+    "lng_tree_accept": (_int, [_p, _p, _p, _i32, _p, _p, _p, _p]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+def load(path: Path | str | None = None) -> ctypes.CDLL:
+    """The loaded library (loaded once).  Raises ``LibraryMissing`` if it was not built."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = Path(path) if path else LIB_PATH
+        if not p.exists():
+            raise LibraryMissing(f"{p} not built: run `python lngram-decode_amd/build.py` "
+                                 "(or __graft_entry__.build()); there is no CPU fallback")
+        lib = ctypes.CDLL(str(p))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().lng_last_error()
+        raise RuntimeError(f"{what} failed ({rc}): {msg.decode() if msg else ''}")

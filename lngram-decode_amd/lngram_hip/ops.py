@@ -1,0 +1,359 @@
+"""Tensor-level wrappers of the gfx950 kernels.
+
+Every op takes device tensors (torch on ROCm), allocates its outputs with torch,
+and enqueues the kernel on the current stream of the tensors' device.  CPU tensors
+are rejected: there is no CPU path in the product.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from ._lib import BF16, F16, F32, I32, I64, U8, check
+
+_DT = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16, torch.uint8: U8, torch.int32: I32,
+       torch.int64: I64}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {dt}") from None
+
+
+def _dev(*ts) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError("lngram_hip ops need tensors on a ROCm GPU device; there is no CPU path "
+                               f"(got a tensor on {t.device})")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _c(t: torch.Tensor | None) -> torch.Tensor | None:
+    """Contiguous with a 16-byte aligned base (vector loads)."""
+    if t is None:
+        return None
+    if not t.is_contiguous() or t.data_ptr() % 16:
+        t = t.contiguous()
+        if t.data_ptr() % 16:
+            t = t.clone()
+    return t
+
+
+def _ptr(t: torch.Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def lib():
+    return _lib.load()
+
+
+class KernelTimer:
+    """Records HIP events around every launch of the named ops on their stream while active.
+
+        with ops.KernelTimer("memory_readout_fused") as kt:
+            ...                       # launches are bracketed by events
+        kt.mean_ms()                  # average device duration per launch (synchronises)
+    """
+
+    _active: list = []
+
+    def __init__(self, *names: str):
+        self.names = set(names)
+        self.events: list = []
+
+    def __enter__(self):
+        KernelTimer._active.append(self)
+        return self
+
+    def __exit__(self, *exc):
+        KernelTimer._active.remove(self)
+        return False
+
+    def durations_ms(self) -> list:
+        if self.events:
+            self.events[-1][1].synchronize()
+        return [s.elapsed_time(e) for s, e in self.events]
+
+    def mean_ms(self) -> float:
+        d = self.durations_ms()
+        return sum(d) / len(d) if d else float("nan")
+
+
+def _timed(name: str, dev: torch.device, launch):
+    timers = [t for t in KernelTimer._active if name in t.names]
+    if not timers:
+        return launch()
+    st = torch.cuda.current_stream(dev)
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record(st)
+    rc = launch()
+    e.record(st)
+    for t in timers:
+        t.events.append((s, e))
+    return rc
+
+
+# ----------------------------------------------------------------------------- K1
+def router_codes(x: torch.Tensor, w: torch.Tensor, bits: int, want_logits: bool = True,
+                 codes_dtype: torch.dtype = torch.int32):
+    """``(logits fp32 [..., N] or None, codes [..., N/bits])`` for ``x [..., K] . w[N, K]^T``."""
+    dev = _dev(x, w)
+    x2 = _c(x.reshape(-1, x.shape[-1]))
+    w = _c(w)
+    m, k = x2.shape
+    n = w.shape[0]
+    if w.shape[1] != k:
+        raise ValueError(f"router weight {tuple(w.shape)} does not match input dim {k}")
+    lead = x.shape[:-1]
+    logits = torch.empty(*lead, n, dtype=torch.float32, device=dev) if want_logits or not (
+        x.dtype == w.dtype == torch.bfloat16 and bits == 4 and k % 8 == 0) else None
+    codes = torch.empty(*lead, n // bits, dtype=codes_dtype, device=dev)
+    check(lib().lng_router_codes(_ptr(x2), dtype_code(x2.dtype), _ptr(w), dtype_code(w.dtype), m, k, n, bits,
+                                 _ptr(logits), _ptr(codes), dtype_code(codes_dtype), _stream(dev)), "router_codes")
+    return (logits if want_logits else None), codes
+
+
+def pack_route_codes(logits: torch.Tensor, bits: int, codes_dtype: torch.dtype = torch.int32) -> torch.Tensor:
+    dev = _dev(logits)
+    lg = _c(logits.float())
+    c = lg.shape[-1]
+    if c % bits:
+        raise ValueError(f"route logits dim={c} must be divisible by bits={bits}")
+    out = torch.empty(*lg.shape[:-1], c // bits, dtype=codes_dtype, device=dev)
+    check(lib().lng_pack_route_codes(_ptr(lg), lg.numel() // c, c, bits, _ptr(out), dtype_code(codes_dtype),
+                                     _stream(dev)), "pack_route_codes")
+    return out
+
+
+# ----------------------------------------------------------------------------- K2
+def _codes_ok(codes: torch.Tensor) -> torch.Tensor:
+    if codes.dtype not in (torch.uint8, torch.int32, torch.int64):
+        codes = codes.to(torch.int32)
+    return _c(codes)
+
+
+def ngram_address(codes: torch.Tensor, order: int, bits: int, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    dev = _dev(codes)
+    b, t, r = codes.shape
+    out_dtype = out_dtype or (torch.int64 if codes.dtype == torch.int64 else torch.int32)
+    cc = _codes_ok(codes)
+    out = torch.empty(b, max(t - order + 1, 0), r, dtype=out_dtype, device=dev)
+    check(lib().lng_ngram_address(_ptr(cc), dtype_code(cc.dtype), b, t, r, order, bits, _ptr(out),
+                                  dtype_code(out_dtype), _stream(dev)), "ngram_address")
+    return out
+
+
+def _orders(orders) -> ctypes.Array:
+    arr = (ctypes.c_int32 * len(orders))(*[int(o) for o in orders])
+    return arr
+
+
+def _seg(segment_ids, valid_tokens):
+    seg = None if segment_ids is None else _c(segment_ids.to(torch.int32))
+    val = None if valid_tokens is None else _c(valid_tokens.to(torch.uint8))
+    return seg, val
+
+
+def ngram_rows(codes: torch.Tensor, orders, bits: int, route_start: int = 0, route_end: int | None = None,
+               segment_ids=None, valid_tokens=None) -> torch.Tensor:
+    """int32 ``[B, T, route_end-route_start, len(orders)]``, -1 where the row is masked."""
+    dev = _dev(codes, segment_ids, valid_tokens)
+    b, t, r = codes.shape
+    route_end = r if route_end is None else route_end
+    cc = _codes_ok(codes)
+    seg, val = _seg(segment_ids, valid_tokens)
+    out = torch.empty(b, t, route_end - route_start, len(orders), dtype=torch.int32, device=dev)
+    check(lib().lng_ngram_rows(_ptr(cc), dtype_code(cc.dtype), b, t, r, route_start, route_end, _orders(orders),
+                               len(orders), bits, _ptr(seg), _ptr(val), _ptr(out), _stream(dev)), "ngram_rows")
+    return out
+
+
+def route_tokens(codes: torch.Tensor, tables, orders, bits: int, route_start: int = 0, route_end: int | None = None,
+                 segment_ids=None, valid_tokens=None, target_length: int | None = None) -> torch.Tensor:
+    """Route tokens ``[B, T_out, R', len(orders)*mem_dim]`` gathered from ``tables`` (one per order)."""
+    dev = _dev(codes, *tables, segment_ids, valid_tokens)
+    b, t, r = codes.shape
+    route_end = r if route_end is None else route_end
+    tabs = [_c(tb) for tb in tables]
+    dt = tabs[0].dtype
+    mem_dim = tabs[0].shape[1]
+    for tb in tabs:
+        if tb.dtype != dt or tb.shape[1] != mem_dim:
+            raise ValueError("all n-gram tables must share dtype and width")
+    cc = _codes_ok(codes)
+    seg, val = _seg(segment_ids, valid_tokens)
+    t_out = t if not target_length else int(target_length)
+    out = torch.empty(b, t_out, route_end - route_start, len(orders) * mem_dim, dtype=dt, device=dev)
+    tp = (ctypes.c_void_p * len(tabs))(*[tb.data_ptr() for tb in tabs])
+    check(lib().lng_route_tokens(_ptr(cc), dtype_code(cc.dtype), b, t, r, route_start, route_end, _orders(orders),
+                                 len(orders), bits, tp, dtype_code(dt), mem_dim, _ptr(seg), _ptr(val),
+                                 int(target_length or 0), _ptr(out), _stream(dev)), "route_tokens")
+    return out
+
+
+# ----------------------------------------------------------------------------- K3 pieces
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    dev = _dev(x, w)
+    xc = _c(x)
+    wc = _c(w.to(x.dtype))
+    out = torch.empty_like(xc)
+    d = x.shape[-1]
+    check(lib().lng_rmsnorm(_ptr(xc), _ptr(wc), dtype_code(x.dtype), xc.numel() // d, d, eps, _ptr(out),
+                            _stream(dev)), "rmsnorm")
+    return out
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """``x [..., K] . w[N, K]^T`` in x's dtype (fp32 accumulation)."""
+    dev = _dev(x, w)
+    k = x.shape[-1]
+    x2 = _c(x.reshape(-1, k))
+    wc = _c(w.to(x.dtype))
+    n = wc.shape[0]
+    if wc.shape[1] != k:
+        raise ValueError(f"weight {tuple(w.shape)} does not match input dim {k}")
+    out = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+    check(lib().lng_linear(_ptr(x2), _ptr(wc), dtype_code(x.dtype), x2.shape[0], n, k, _ptr(out), _stream(dev)),
+          "linear")
+    return out
+
+
+def sink_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scale: float,
+                   sink_logit: float) -> torch.Tensor:
+    """query ``[B, T, KV, G, hd]``; key/value ``[B, T, KV, R, hd]`` (head dim contiguous, any other
+    strides) -> ``[B, T, KV, G, hd]``."""
+    dev = _dev(query, key, value)
+    b, t, kv, g, hd = query.shape
+    r = key.shape[3]
+    q = _c(query)
+    if key.stride(-1) != 1:
+        key = key.contiguous()
+    if value.stride(-1) != 1:
+        value = value.contiguous()
+    if key.dtype != q.dtype or value.dtype != q.dtype:
+        raise TypeError("query, key and value must share a dtype")
+
+    def bt_strides(x):
+        # (b, t) must collapse into one stride
+        sb, st = x.stride(0), x.stride(1)
+        if b > 1 and sb != st * t:
+            return None
+        return (st, x.stride(2), x.stride(3))
+
+    ks, vs = bt_strides(key), bt_strides(value)
+    if ks is None:
+        key = key.contiguous()
+        ks = bt_strides(key)
+    if vs is None:
+        value = value.contiguous()
+        vs = bt_strides(value)
+    out = torch.empty(b, t, kv, g, hd, dtype=q.dtype, device=dev)
+    ka = (ctypes.c_int64 * 3)(*ks)
+    va = (ctypes.c_int64 * 3)(*vs)
+    check(lib().lng_sink_attention_strided(_ptr(q), ctypes.c_void_p(key.data_ptr()), ctypes.c_void_p(value.data_ptr()),
+                                           dtype_code(q.dtype), b * t, kv, g, r, hd, ka, va, scale, sink_logit,
+                                           _ptr(out), _stream(dev)), "sink_attention")
+    return out
+
+
+def sink_probabilities(scores: torch.Tensor, sink_logit: float) -> torch.Tensor:
+    dev = _dev(scores)
+    s = _c(scores.float())
+    r = s.shape[-1]
+    out = torch.empty_like(s)
+    check(lib().lng_sink_probabilities(_ptr(s), s.numel() // r, r, sink_logit, _ptr(out), _stream(dev)),
+          "sink_probabilities")
+    return out
+
+
+def causal_conv(mixed: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor, dilation: int,
+                eps: float, residual: bool = True) -> torch.Tensor:
+    """``[mixed +] SiLU(conv(RMSNorm(mixed)))`` for mixed ``[B, T, d]``, conv weight ``[d, 1, K]``."""
+    dev = _dev(mixed, norm_w, conv_w)
+    m = _c(mixed)
+    b, t, d = m.shape
+    cw = _c(conv_w.reshape(d, -1).to(m.dtype))
+    nw = _c(norm_w.to(m.dtype))
+    out = torch.empty_like(m)
+    check(lib().lng_causal_conv(_ptr(m), _ptr(nw), _ptr(cw), dtype_code(m.dtype), b, t, d, cw.shape[1], dilation,
+                                eps, int(bool(residual)), _ptr(out), _stream(dev)), "causal_conv")
+    return out
+
+
+def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Tensor, table3: torch.Tensor,
+                         wk_t: torch.Tensor, wv: torch.Tensor, w_mem: torch.Tensor, eps: float, scale: float,
+                         sink_logit: float) -> torch.Tensor:
+    """Fused gather + sink readout (bf16, 16 heads x 64, 4 KV heads, orders (2,3), mem_dim 128).
+
+    q ``[B, T, 1024]``, codes ``[B, T, R]`` uint8 -> head output ``[B, T, 1024]``."""
+    dev = _dev(q, codes, table2, table3, wk_t, wv, w_mem)
+    b, t, r = codes.shape
+    qc = _c(q)
+    cc = _c(codes.to(torch.uint8))
+    if qc.dtype != torch.bfloat16 or qc.shape[-1] != 1024:
+        raise ValueError("fused readout expects a bf16 [B, T, 1024] query")
+    if table2.shape != (r * 256, 128) or table3.shape != (r * 4096, 128):
+        raise ValueError("fused readout expects tables [R*256,128] and [R*4096,128]")
+    if wk_t.shape != (4, 256, 64) or wv.shape != (4, 64, 256) or w_mem.shape != (256,):
+        raise ValueError("fused readout weight shapes")
+    out = torch.empty(b, t, 1024, dtype=torch.bfloat16, device=dev)
+    t2, t3, wkc, wvc, wmc = _c(table2), _c(table3), _c(wk_t), _c(wv), _c(w_mem.to(torch.bfloat16))
+    rc = _timed("memory_readout_fused", dev, lambda: lib().lng_memory_readout_fused(
+        _ptr(qc), _ptr(cc), b, t, r, _ptr(t2), _ptr(t3), _ptr(wkc), _ptr(wvc), _ptr(wmc), eps, scale, sink_logit,
+        _ptr(out), _stream(dev)))
+    check(rc, "memory_readout_fused")
+    return out
+
+
+# ----------------------------------------------------------------------------- K4
+def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -> torch.Tensor:
+    """``s_t = a s_{t-1} + (1 - a) u_t`` (fp32) for u ``[B, T, N]``, a ``[N]``, s0 ``[B, N]`` or None."""
+    dev = _dev(a, u, s0)
+    uc = _c(u.float())
+    ac = _c(a.float())
+    s0c = None if s0 is None else _c(s0.float())
+    b, t, n = uc.shape
+    out = torch.empty_like(uc)
+    ws_bytes = lib().lng_ssm_workspace_bytes(b, t, n)
+    ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=dev)
+    check(lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws), _ptr(out), _stream(dev)), "ssm_scan")
+    return out
+
+
+# ----------------------------------------------------------------------------- K5
+def tree_accept(parent: torch.Tensor, node_tokens: torch.Tensor, argmax: torch.Tensor):
+    """Device tree acceptance -> ``(path int32 [n], path_len int32 [1], new_tokens int64 [n])``
+    (valid entries: the first ``path_len``)."""
+    dev = _dev(parent, node_tokens, argmax)
+    n = parent.numel()
+    p = _c(parent.to(torch.int32))
+    nt = _c(node_tokens.to(torch.int64))
+    am = _c(argmax.to(torch.int64))
+    path = torch.empty(n, dtype=torch.int32, device=dev)
+    plen = torch.empty(1, dtype=torch.int32, device=dev)
+    new = torch.empty(n, dtype=torch.int64, device=dev)
+    check(lib().lng_tree_accept(_ptr(p), _ptr(nt), _ptr(am), n, _ptr(path), _ptr(plen), _ptr(new), _stream(dev)),
+          "tree_accept")
+    return path, plen, new
+
+
+def sink_logit_for(routes: int, mass: float = 0.5) -> float:
+    return math.log(routes * (1.0 - mass) / mass)

@@ -1,0 +1,105 @@
+"""Synthetic workloads of the route n-gram memory hot path (shapes + seeded weights/inputs).
+
+The shapes are the reference configurations the benchmark and the parity tests run:
+
+- ``TINY``  tiny CPU-scale layer: d 128, 8 routes, mem_dim 32, 4 query heads x 32, 2 KV heads, fp32, 4 x 128
+- ``SB``    SB-shape layer-1 memory with a hidden-state router: d 1024, 184 routes, bf16, 8 x 2048
+- ``SDB``   SD-B token-routed memory (182 routes, embed2 router) for decode / drafting
+- ``SDC``   SD-C: 181 routes, embed2_ssm router over a 256-channel diagonal SSM, 8 x 4096
+
+Weights follow the module initialisers (tables, router, Q/KV projections ~N(0, 0.02));
+the zero-initialised output projection and conv are re-drawn as N(0, 0.02) and N(0, 0.2)
+so that the output depends on the memory, all norm weights are ones.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, replace
+
+import torch
+
+
+@dataclass(frozen=True)
+class MemoryWorkload:
+    name: str
+    d_model: int
+    routes: int
+    mem_dim: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    batch: int
+    seq: int
+    dtype: torch.dtype
+    router_input: str = "hidden"
+    ssm_dim: int = 0
+    vocab: int = 0
+    norm_eps: float = 1e-5
+
+    @property
+    def tokens(self) -> int:
+        return self.batch * self.seq
+
+    def with_shape(self, batch: int, seq: int) -> "MemoryWorkload":
+        return replace(self, batch=batch, seq=seq)
+
+    def mem_cfg(self) -> dict:
+        cfg = {"routes": self.routes, "mem_dim": self.mem_dim, "kv_heads": self.kv_heads, "q_heads": self.q_heads,
+               "head_dim": self.head_dim, "execution_mode": "full"}
+        if self.router_input != "hidden":
+            cfg["router_input"] = self.router_input
+        return cfg
+
+    def algorithmic_bytes_per_token(self) -> int:
+        """HBM bytes one token of the layer forward must move at minimum: h and h_norm (or the
+        router features) read, one table row per (route, order) read, the output written."""
+        es = torch.finfo(self.dtype).bits // 8
+        rows = self.routes * 2 * self.mem_dim * es
+        act = self.d_model * es
+        if self.router_input == "hidden":
+            return 2 * act + rows + act
+        # embed2(_ssm): h + E[x_t] read (E[x_{t-1}] is the previous token's row), s_t, out
+        return 2 * act + self.ssm_dim * es + rows + act
+
+    def weight_bytes(self) -> int:
+        es = torch.finfo(self.dtype).bits // 8
+        d, inner = self.d_model, self.q_heads * self.head_dim
+        dt = 2 * self.mem_dim
+        fin = {"hidden": d, "embed2": 2 * d, "embed2_ssm": 2 * d + self.ssm_dim}[self.router_input]
+        router = self.routes * 4 * fin
+        proj = inner * d + 2 * self.kv_heads * self.head_dim * dt + d * inner
+        return (router + proj + 4 * d + dt + 2 * d) * es
+
+
+TINY = MemoryWorkload("tiny d128 R8 fp32 4x128", 128, 8, 32, 4, 2, 32, 4, 128, torch.float32)
+SB = MemoryWorkload("sb d1024 R184 bf16 8x2048", 1024, 184, 128, 16, 4, 64, 8, 2048, torch.bfloat16)
+SDB = MemoryWorkload("sdb d1024 R182 bf16 decode", 1024, 182, 128, 16, 4, 64, 1, 2048, torch.bfloat16,
+                     router_input="embed2", vocab=32768)
+SDC = MemoryWorkload("sdc d1024 R181 N256 bf16 8x4096", 1024, 181, 128, 16, 4, 64, 8, 4096, torch.bfloat16,
+                     router_input="embed2_ssm", ssm_dim=256, vocab=32768)
+
+
+def build_memory(w: MemoryWorkload, seed: int = 0, device: str | torch.device = "cpu"):
+    """``LngramMemory`` of workload ``w`` with synthetic weights, eval mode, in ``w.dtype`` on ``device``."""
+    from ffnmem.memory.wrapper import LngramMemory
+
+    torch.manual_seed(seed)
+    mem = LngramMemory(w.d_model, w.mem_cfg(), init_std=0.02, norm_eps=w.norm_eps, ssm_dim=w.ssm_dim)
+    g = torch.Generator().manual_seed(seed + 1)
+    m = mem.module
+    with torch.no_grad():
+        m.readout_o_proj.weight.copy_(torch.randn(m.readout_o_proj.weight.shape, generator=g) * 0.02)
+        m.short_conv.conv.weight.copy_(torch.randn(m.short_conv.conv.weight.shape, generator=g) * 0.2)
+    return mem.to(w.dtype).to(device).eval()
+
+
+def make_hidden(w: MemoryWorkload, seed: int = 1, device: str | torch.device = "cpu") -> torch.Tensor:
+    """Hidden states ``h ~ N(0, 1)`` ``[B, T, d]`` in ``w.dtype``."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(w.batch, w.seq, w.d_model, generator=g).to(w.dtype).to(device)
+
+
+def make_tokens(w: MemoryWorkload, seed: int = 2, device: str | torch.device = "cpu") -> torch.Tensor:
+    """Token ids uniform over the vocabulary ``[B, T]``."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, w.vocab, (w.batch, w.seq), generator=g).to(device)

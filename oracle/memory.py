@@ -1,0 +1,356 @@
+"""Oracle: CPU restatement of the route n-gram memory forward (test infrastructure only).
+
+Integer work (codes, addresses, rows) is numpy; floating-point work is torch on the
+CPU in the op order of the reference, parameterised by dtype:
+
+- ``torch.float64``  : a high-precision restatement (the tight oracle);
+- ``torch.float32``  : the reference's fp32 path;
+- ``torch.bfloat16`` : the reference's bf16 path (``load_model(dtype=bfloat16)``
+  semantics: every module op in bf16 with its own rounding, the router in fp32).
+
+Every function cites the reference lines it restates.  Parameters are passed as a
+plain dict keyed like the reference module's ``state_dict`` (``tables.ngram_2.weight``,
+``readout_q_proj.weight``, ... and ``router.weight`` for the wrapper).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+
+# ----------------------------------------------------------------------------- config
+@dataclass(frozen=True)
+class MemCfg:
+    """Shape of one memory layer (reference: ``wrapper.py:50-95`` + ``lngram_v2.py:842-1010``)."""
+
+    d_model: int
+    routes: int
+    mem_dim: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    bits: int = 4
+    orders: tuple = (2, 3)
+    eps: float = 1e-5
+    conv_kernel: int = 4
+    sink_mass: float = 0.5
+
+    @property
+    def route_token_dim(self) -> int:
+        return len(self.orders) * self.mem_dim
+
+    @property
+    def groups(self) -> int:
+        return self.q_heads // self.kv_heads
+
+    @property
+    def conv_dilation(self) -> int:
+        # lngram_v2.py:1000-1010 -- dilation defaults to the largest n-gram order
+        return max(self.orders)
+
+    @property
+    def sink_logit(self) -> float:
+        # lngram_v2.py:1877-1885 -- b0 = log(R (1 - m) / m)
+        return math.log(self.routes * (1.0 - self.sink_mass) / self.sink_mass)
+
+    @property
+    def softmax_scale(self) -> float:
+        return self.head_dim ** -0.5
+
+
+# ----------------------------------------------------------------------------- integer parts
+def pack_route_codes(logits, bits: int) -> np.ndarray:
+    """Route codes from router logits.
+
+    Follows ``lngram_v2.py:1012-1017`` (``q_logits > 0``) and ``:74-89``
+    (bit i of route r is channel ``r*bits + i``; code = sum bit_i << i).  Strict ``>``:
+    0, -0 and NaN give bit 0.  Returns int32 ``[..., R]``.
+    """
+    q = np.asarray(logits)
+    *lead, c = q.shape
+    if c % bits:
+        raise ValueError("channels must be divisible by bits")
+    b = (q > 0).reshape(*lead, c // bits, bits).astype(np.int32)
+    return (b << np.arange(bits, dtype=np.int32)).sum(-1).astype(np.int32)
+
+
+def ngram_address(codes, order: int, bits: int) -> np.ndarray:
+    """``_aligned_ngram_address`` (``lngram_v2.py:314-325``).
+
+    ``addr[b, t', r] = sum_k codes[b, t'+k, r] << (k*bits)`` for ``t' = 0 .. T-order``:
+    the oldest code of the window is the least significant digit.
+    """
+    c = np.asarray(codes).astype(np.int64)
+    b, t, r = c.shape
+    n_valid = t - order + 1
+    if n_valid <= 0:
+        return np.zeros((b, 0, r), np.int64)
+    out = np.zeros((b, n_valid, r), np.int64)
+    for k in range(order):
+        out |= c[:, k:k + n_valid] << (k * bits)
+    return out
+
+
+def valid_mask(order: int, batch: int, time: int, segment_ids=None, valid_tokens=None) -> np.ndarray:
+    """``_valid_mask`` (``lngram_v2.py:1027-1045``): position t has an order-n row iff
+    ``t >= n-1`` and the window's first and last positions share a segment (and the
+    last position is a valid token)."""
+    v = np.zeros((batch, time), bool)
+    if time < order:
+        return v
+    s = np.ones((batch, time - order + 1), bool)
+    if segment_ids is not None:
+        seg = np.asarray(segment_ids)
+        s &= seg[:, : time - order + 1] == seg[:, order - 1:]
+    if valid_tokens is not None:
+        s &= np.asarray(valid_tokens, bool)[:, order - 1:]
+    v[:, order - 1:] = s
+    return v
+
+
+def route_rows(codes, orders, bits: int, route_start: int = 0, route_end: int | None = None,
+               segment_ids=None, valid_tokens=None) -> np.ndarray:
+    """Global table rows read by ``_lookup_route_chunk`` (``lngram_v2.py:1047-1092``).
+
+    Returns int64 ``[B, T, route_end-route_start, len(orders)]``; ``row = r * 2^(bits*n)
+    + addr`` (``:1064-1084``) and ``-1`` where the reference multiplies the row by a
+    zero validity mask (``:1085-1092``).
+    """
+    c = np.asarray(codes).astype(np.int64)
+    b, t, r_all = c.shape
+    route_end = r_all if route_end is None else route_end
+    rr = np.arange(route_start, route_end, dtype=np.int64)
+    out = np.full((b, t, route_end - route_start, len(orders)), -1, np.int64)
+    for oi, n in enumerate(orders):
+        vm = valid_mask(n, b, t, segment_ids, valid_tokens)
+        addr = ngram_address(c[:, :, route_start:route_end], n, bits)
+        if addr.shape[1] == 0:
+            continue
+        rows = rr[None, None, :] * (1 << (bits * n)) + addr
+        blk = out[:, n - 1:, :, oi]
+        blk[...] = rows
+        out[..., oi] = np.where(vm[..., None], out[..., oi], -1)
+    return out
+
+
+def route_tokens(tables: dict, codes, orders, bits: int, route_start: int = 0, route_end: int | None = None,
+                 segment_ids=None, valid_tokens=None, target_length: int | None = None) -> torch.Tensor:
+    """Route tokens ``[B, T, R', len(orders)*mem_dim]`` (``lngram_v2.py:1047-1113``):
+    per order the gathered row (zero where invalid), concatenated over orders in the
+    feature dimension (2-gram first), optionally the last ``target_length`` positions."""
+    rows = route_rows(codes, orders, bits, route_start, route_end, segment_ids, valid_tokens)
+    parts = []
+    for oi, n in enumerate(orders):
+        tab = tables[n]
+        sel = torch.from_numpy(rows[..., oi])
+        got = tab[sel.clamp_min(0)]
+        parts.append(got * (sel >= 0).unsqueeze(-1).to(got.dtype))
+    out = torch.cat(parts, -1)
+    if target_length is not None:
+        out = out[:, -int(target_length):]
+    return out
+
+
+# ----------------------------------------------------------------------------- float parts
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm as the reference rounds it: normalise in fp32 (fp64 for fp64 input),
+    round to the input dtype, then multiply by the weight in that dtype.
+
+    Covers both ``lngram_v2.RMSNorm`` (``F.rms_norm``, ``lngram_v2.py:36-53``) and
+    ``model.RMSNorm`` (``model.py:39-48``), which round identically.
+    """
+    work = torch.float64 if x.dtype == torch.float64 else torch.float32
+    xf = x.to(work)
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return y.to(x.dtype) * w.to(x.dtype)
+
+
+def rms_norm_fp32(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """``cpu_drafter._rms`` (``drafting/cpu_drafter.py:64-65``): everything in x's dtype."""
+    return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+
+
+def sink_probabilities(scores: torch.Tensor, sink_logit: float) -> torch.Tensor:
+    """``_real_route_probabilities`` (``lngram_v2.py:1887-1897``): softmax over routes
+    with one extra zero-value logit ``b0`` in the denominator, in fp32 (fp64 stays fp64)."""
+    s = scores if scores.dtype == torch.float64 else scores.float()
+    sink = torch.tensor(sink_logit, dtype=s.dtype)
+    m = torch.maximum(s.amax(-1, keepdim=True), sink)
+    ex = torch.exp(s - m)
+    return ex / (ex.sum(-1, keepdim=True) + torch.exp(sink - m))
+
+
+def _p(params: dict, key: str, dtype) -> torch.Tensor:
+    return params[key].to(dtype)
+
+
+def project_query(params: dict, cfg: MemCfg, h: torch.Tensor) -> torch.Tensor:
+    """``_project_query`` (``lngram_v2.py:1115-1118``): ``W_q RMSNorm(h)`` -> [B, T, H, hd]."""
+    dt = h.dtype
+    x = rms_norm(h, _p(params, "readout_query_norm.weight", dt), cfg.eps)
+    q = F.linear(x, _p(params, "readout_q_proj.weight", dt))
+    return q.view(*h.shape[:-1], cfg.q_heads, cfg.head_dim)
+
+
+def project_memory(params: dict, cfg: MemCfg, tokens: torch.Tensor):
+    """``_project_memory`` (``lngram_v2.py:1120-1131``): memory RMSNorm over Dt, KV
+    projection, split keys first, reshape to ``[B, T, KV, R, hd]`` each."""
+    dt = tokens.dtype
+    x = rms_norm(tokens, _p(params, "readout_memory_norm.weight", dt), cfg.eps)
+    kv = F.linear(x, _p(params, "readout_kv_proj.weight", dt))
+    kh = cfg.kv_heads * cfg.head_dim
+    key, value = kv[..., :kh], kv[..., kh:]
+    b, t, r, _ = key.shape
+    key = key.reshape(b, t, r, cfg.kv_heads, cfg.head_dim).permute(0, 1, 3, 2, 4)
+    value = value.reshape(b, t, r, cfg.kv_heads, cfg.head_dim).permute(0, 1, 3, 2, 4)
+    return key, value
+
+
+def manual_gqa(cfg: MemCfg, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor) -> torch.Tensor:
+    """v2 ``_manual_gqa`` (``lngram_v2.py:1899-1920``): query heads grouped as
+    ``[KV, G]`` (head = kv*G + g); scores = (q . k) in the storage dtype, then fp32 times
+    ``hd^-0.5``; sink softmax; ``p.to(v.dtype) @ v``."""
+    b, t = query.shape[:2]
+    g = query.reshape(b, t, cfg.kv_heads, cfg.groups, cfg.head_dim)
+    scores = torch.matmul(g, key.transpose(-1, -2).contiguous())
+    scores = (scores if scores.dtype == torch.float64 else scores.float()) * cfg.softmax_scale
+    p = sink_probabilities(scores, cfg.sink_logit)
+    out = torch.matmul(p.to(value.dtype), value)
+    return out.reshape(b, t, cfg.q_heads, cfg.head_dim)
+
+
+def causal_conv(params: dict, cfg: MemCfg, mixed: torch.Tensor, segment_ids=None) -> torch.Tensor:
+    """``DepthwiseCausalConv.forward`` (``lngram_v2.py:273-286``, ``:244-271`` for
+    segments): ``SiLU(conv(RMSNorm(mixed)))`` with kernel K, dilation = max order, zero
+    left padding ``(K-1)*dil``, no bias.  Tap j reads lag ``(K-1-j)*dil`` (Conv1d stores
+    taps oldest -> newest)."""
+    dt = mixed.dtype
+    x = rms_norm(mixed, _p(params, "short_conv.norm.weight", dt), cfg.eps)
+    w = _p(params, "short_conv.conv.weight", dt)  # [d, 1, K]
+    k, dil = cfg.conv_kernel, cfg.conv_dilation
+    if segment_ids is None:
+        xin = F.pad(x.transpose(1, 2), ((k - 1) * dil, 0))
+        y = F.conv1d(xin, w, None, 1, 0, dil, x.shape[-1]).transpose(1, 2)
+        return F.silu(y)
+    seg = torch.as_tensor(np.asarray(segment_ids))
+    out = torch.zeros_like(x)
+    b, t, c = x.shape
+    for tap in range(k):
+        lag = (k - 1 - tap) * dil
+        if lag == 0:
+            sh, ok = x, torch.ones(b, t, 1, dtype=torch.bool)
+        else:
+            sh = F.pad(x[:, :-lag], (0, 0, lag, 0)) if lag < t else torch.zeros_like(x)
+            ok = torch.zeros(b, t, 1, dtype=torch.bool)
+            if lag < t:
+                ok[:, lag:, 0] = seg[:, lag:] == seg[:, :-lag]
+        out = out + sh * ok.to(sh.dtype) * w[:, 0, tap].view(1, 1, c)
+    return F.silu(out)
+
+
+def finish(params: dict, cfg: MemCfg, head: torch.Tensor, segment_ids=None) -> torch.Tensor:
+    """``_finish`` (``lngram_v2.py:1354-1359``): ``mixed = W_o head``; ``mixed + conv(mixed)``."""
+    b, t = head.shape[:2]
+    mixed = F.linear(head.reshape(b, t, -1), _p(params, "readout_o_proj.weight", head.dtype))
+    return mixed + causal_conv(params, cfg, mixed, segment_ids)
+
+
+def memory_forward(params: dict, cfg: MemCfg, h: torch.Tensor, codes, segment_ids=None,
+                   dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``RouteNgramMemoryV2.forward`` in ``full`` mode, eval (``lngram_v2.py:1361-1407``):
+    query from ``h``, route tokens from ``codes``, project, sink GQA, finish."""
+    dt = dtype or h.dtype
+    h = h.to(dt)
+    tables = {n: params[f"tables.ngram_{n}.weight"].to(dt) for n in cfg.orders}
+    q = project_query(params, cfg, h)
+    tok = route_tokens(tables, codes, cfg.orders, cfg.bits, segment_ids=segment_ids)
+    key, value = project_memory(params, cfg, tok)
+    head = manual_gqa(cfg, q, key, value)
+    return finish(params, cfg, head, segment_ids)
+
+
+def router_logits(x: torch.Tensor, w: torch.Tensor, work=torch.float64) -> torch.Tensor:
+    """``LngramMemory.route_logits`` (``wrapper.py:98-101``): ``F.linear(x.float(), W.float())``.
+
+    ``work=float64`` gives the exact-product, near-exact-sum oracle (for bf16 operands
+    every product is exact); ``work=float32`` is the reference's own precision.
+    """
+    return F.linear(x.to(work), w.to(work))
+
+
+def lngram_forward(params: dict, cfg: MemCfg, h: torch.Tensor, h_norm: torch.Tensor,
+                   router_in: torch.Tensor | None = None, dtype: torch.dtype | None = None,
+                   codes=None):
+    """``LngramMemory.forward`` in eval (``wrapper.py:103-125``): router logits on
+    ``h_norm`` (or ``router_in``), sign-packed codes, module forward with the raw ``h``.
+
+    ``codes`` (optional) replaces the router's codes, so outputs can be compared given
+    identical codes.  Returns ``(out, codes, q_logits_fp64)``.
+    """
+    x = h_norm if router_in is None else router_in
+    q = router_logits(x, params["router.weight"].to(x.dtype))
+    if codes is None:
+        codes = pack_route_codes(q.numpy(), cfg.bits)
+    out = memory_forward(params, cfg, h, codes, dtype=dtype)
+    return out, codes, q
+
+
+# ----------------------------------------------------------------------------- SD router / SSM
+def router_features(emb: torch.Tensor, start: torch.Tensor, prev_w: torch.Tensor, cur_w: torch.Tensor,
+                    eps: float, ssm_state: torch.Tensor | None = None) -> torch.Tensor:
+    """``TokenRouterFeatures.forward`` (``router.py:50-59``): ``concat(RMSNorm(E[x_{t-1}]
+    or start), RMSNorm(E[x_t])[, s_t cast to the feature dtype])``."""
+    b = emb.shape[0]
+    prev = torch.cat((start.to(emb.dtype).expand(b, 1, -1), emb[:, :-1]), 1)
+    parts = [rms_norm(prev, prev_w, eps), rms_norm(emb, cur_w, eps)]
+    if ssm_state is not None:
+        parts.append(ssm_state.to(parts[0].dtype))
+    return torch.cat(parts, -1)
+
+
+def ssm_inputs(emb: torch.Tensor, norm_w: torch.Tensor, w_in: torch.Tensor, eps: float,
+               work=torch.float32) -> torch.Tensor:
+    """``DiagonalSSM.inputs`` (``ssm.py:41-43``): ``W_in RMSNorm(E[x])`` in fp32."""
+    x = emb.to(work)
+    xn = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    return F.linear(xn * norm_w.to(work), w_in.to(work))
+
+
+def ssm_scan(a, u, s0=None) -> np.ndarray:
+    """Diagonal SSM states (``ssm.py:58-65`` sequential form, ``infer.py:125-137`` for a
+    carried state): ``s_t = a s_{t-1} + (1-a) u_t``, ``s_{-1} = s0`` (zero if None), in fp64.
+
+    a ``[N]``, u ``[B, T, N]``, s0 ``[B, N]`` -> s ``[B, T, N]`` (numpy fp64).
+    """
+    a = np.asarray(a, np.float64)
+    u = np.asarray(u, np.float64)
+    b, t, n = u.shape
+    s = np.zeros((b, n)) if s0 is None else np.asarray(s0, np.float64).copy()
+    out = np.empty((b, t, n))
+    for i in range(t):
+        s = a * s + (1.0 - a) * u[:, i]
+        out[:, i] = s
+    return out
+
+
+def ssm_scan_closed_form_constant(a, u_const, t: int, s0=None) -> np.ndarray:
+    """Closed form of the recurrence for a constant input: ``s_t = u + a^{t+1} (s0 - u)``."""
+    a = np.asarray(a, np.float64)
+    u = np.asarray(u_const, np.float64)
+    s0 = np.zeros_like(u) if s0 is None else np.asarray(s0, np.float64)
+    k = np.arange(1, t + 1, dtype=np.float64)[:, None]
+    return u[None] + (a[None] ** k) * (s0 - u)[None]
+
+
+# ----------------------------------------------------------------------------- comparison metric
+def rel_err(got, want) -> float:
+    """Norm-relative error ``||got - want|| / ||want||`` in fp64."""
+    g = torch.as_tensor(got).double()
+    w = torch.as_tensor(want).double()
+    den = float(w.norm())
+    return float((g - w).norm()) / (den if den > 0 else 1.0)

@@ -1,0 +1,238 @@
+"""Parity of the individual gfx950 kernels against the oracle (GPU).
+
+Integer work is compared bit-exactly; floating-point work against the fp64 / reference-
+rounding oracle with the tolerance written in each test.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from lngram_hip import ops
+from oracle import cint
+from oracle import memory as om
+
+pytestmark = pytest.mark.gpu
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+# ----------------------------------------------------------------------------- K2: addresses, rows, gather
+@pytest.mark.parametrize("cdt", [torch.uint8, torch.int32, torch.int64])
+def test_ngram_address_bit_exact(dev, cdt):
+    rng = np.random.default_rng(0)
+    codes = rng.integers(0, 16, (3, 37, 11))
+    for order in (1, 2, 3):
+        got = ops.ngram_address(torch.as_tensor(codes).to(cdt).to(dev), order, 4)
+        np.testing.assert_array_equal(_np(got), om.ngram_address(codes, order, 4))
+    # reference KAT (tests/test_index_layout.py:28-33)
+    kat = torch.tensor([[[3], [5], [7], [9]]], dtype=cdt, device=dev)
+    assert int(ops.ngram_address(kat, 2, 4)[0, 0, 0]) == 3 + 16 * 5
+    assert int(ops.ngram_address(kat, 3, 4)[0, 1, 0]) == 5 + 16 * 7 + 256 * 9
+    assert ops.ngram_address(kat[:, :1], 2, 4).shape == (1, 0, 1)
+
+
+def test_ngram_rows_bit_exact_with_segments(dev):
+    rng = np.random.default_rng(1)
+    b, t, r = 4, 29, 184
+    codes = rng.integers(0, 16, (b, t, r))
+    seg = np.cumsum(rng.random((b, t)) < 0.15, axis=1).astype(np.int32)
+    valid = rng.random((b, t)) < 0.85
+    ct = torch.as_tensor(codes, dtype=torch.uint8, device=dev)
+    for s, v in ((None, None), (seg, None), (None, valid), (seg, valid)):
+        got = ops.ngram_rows(ct, (2, 3), 4, 0, r, None if s is None else torch.as_tensor(s, device=dev),
+                             None if v is None else torch.as_tensor(v, device=dev))
+        want = cint.ngram_rows(codes, (2, 3), 4, s, v)
+        np.testing.assert_array_equal(_np(got), want)
+    got = ops.ngram_rows(ct, (2, 3), 4, 17, 60)
+    np.testing.assert_array_equal(_np(got), om.route_rows(codes, (2, 3), 4, 17, 60))
+
+
+@pytest.mark.parametrize("tdt", [torch.float32, torch.bfloat16, torch.float16])
+def test_route_tokens_bit_exact(dev, tdt):
+    rng = np.random.default_rng(2)
+    b, t, r, md = 2, 13, 9, 32
+    codes = rng.integers(0, 16, (b, t, r))
+    tables = {n: (torch.randn(r * 16 ** n, md) * 0.02).to(tdt) for n in (2, 3)}
+    seg = np.cumsum(rng.random((b, t)) < 0.2, axis=1).astype(np.int32)
+    ct = torch.as_tensor(codes, dtype=torch.int32, device=dev)
+    tl = [tables[2].to(dev), tables[3].to(dev)]
+    cases = [dict(), dict(route_start=2, route_end=7), dict(segment_ids=seg), dict(target_length=3),
+             dict(valid_tokens=rng.random((b, t)) < 0.7)]
+    for kw in cases:
+        dkw = {k: (torch.as_tensor(v, device=dev) if isinstance(v, np.ndarray) else v) for k, v in kw.items()}
+        got = ops.route_tokens(ct, tl, (2, 3), 4, **dkw)
+        want = om.route_tokens(tables, codes, (2, 3), 4, **kw)
+        assert got.dtype == tdt
+        np.testing.assert_array_equal(_np(got.float()), want.float().numpy())
+
+
+def test_route_tokens_sb_width_and_odd_width(dev):
+    rng = np.random.default_rng(3)
+    for md in (128, 3):  # 256-byte rows (vector path) and 6-byte rows (2-byte path)
+        r = 5
+        codes = rng.integers(0, 16, (1, 9, r))
+        tables = {n: torch.randn(r * 16 ** n, md).to(torch.bfloat16) for n in (2, 3)}
+        got = ops.route_tokens(torch.as_tensor(codes, device=dev), [tables[2].to(dev), tables[3].to(dev)], (2, 3), 4)
+        want = om.route_tokens(tables, codes, (2, 3), 4)
+        np.testing.assert_array_equal(_np(got.float()), want.float().numpy())
+
+
+def test_empty_and_short_sequences(dev):
+    tab = [torch.zeros(4 * 256, 8, device=dev), torch.zeros(4 * 4096, 8, device=dev)]
+    out = ops.route_tokens(torch.zeros(2, 0, 4, dtype=torch.uint8, device=dev), tab, (2, 3), 4)
+    assert out.shape == (2, 0, 4, 16)
+    out = ops.route_tokens(torch.ones(1, 1, 4, dtype=torch.uint8, device=dev), tab, (2, 3), 4)
+    assert out.shape == (1, 1, 4, 16) and float(out.abs().max()) == 0
+
+
+# ----------------------------------------------------------------------------- K1: router + codes
+def test_pack_route_codes_bit_exact(dev):
+    q = torch.randn(57, 4 * 23)
+    q[0, :8] = torch.tensor([0.0, -0.0, float("nan"), 1e-30, -1e-30, 5.0, -5.0, 0.0])
+    got = ops.pack_route_codes(q.to(dev), 4)
+    np.testing.assert_array_equal(_np(got), cint.pack_codes(q.numpy(), 4))
+    assert _np(got)[0, :2].tolist() == [8, 2]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(300, 1024, 736), (37, 128, 32), (129, 2304, 724)])
+def test_router_logits_and_codes(dev, dtype, shape):
+    m, k, n = shape
+    g = torch.Generator().manual_seed(m + k)
+    x = torch.randn(m, k, generator=g).to(dtype)
+    w = (torch.randn(n, k, generator=g) * 0.02).to(dtype)
+    q64 = om.router_logits(x, w).numpy()
+    logits, codes = ops.router_codes(x.to(dev), w.to(dev), 4, want_logits=True, codes_dtype=torch.uint8)
+    # fp32 accumulation error bound: |err| <= K * 2^-24 * sum|x w|  (tolerance written here)
+    bound = k * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T).numpy()
+    assert (np.abs(_np(logits) - q64) <= bound + 1e-12).all()
+    want = om.pack_route_codes(q64, 4)
+    tau = 2e-5  # near-tie band: codes compared bit-exactly where every bit's |q| > tau
+    clear = (np.abs(q64) > tau).reshape(m, n // 4, 4).all(-1)
+    got = _np(codes).astype(np.int32)
+    assert (got[clear] == want[clear]).all()
+    assert (got != want).mean() < 1e-3
+    _, codes_only = ops.router_codes(x.to(dev), w.to(dev), 4, want_logits=False, codes_dtype=torch.int32)
+    np.testing.assert_array_equal(_np(codes_only), got)
+
+
+# ----------------------------------------------------------------------------- K3 pieces
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rmsnorm(dev, dtype):
+    x = torch.randn(33, 1024).to(dtype)
+    w = (1 + 0.1 * torch.randn(1024)).to(dtype)
+    got = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5).cpu()
+    want = om.rms_norm(x, w, 1e-5)
+    if dtype == torch.float32:
+        torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-6)
+    else:  # one bf16 rounding step apart at most
+        assert (got.float() - want.float()).abs().max() <= 2 ** -7 * want.float().abs().max()
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
+@pytest.mark.parametrize("mnk", [(513, 1024, 1024), (7, 33, 64), (130, 256, 256)])
+def test_linear(dev, dtype, tol, mnk):
+    m, n, k = mnk
+    x = torch.randn(m, k).to(dtype)
+    w = (torch.randn(n, k) * 0.05).to(dtype)
+    got = ops.linear(x.to(dev), w.to(dev)).cpu()
+    want = x.double() @ w.double().T
+    assert om.rel_err(got, want) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_sink_attention_and_probabilities(dev, dtype, tol):
+    cfg = om.MemCfg(1024, 184, 128, 16, 4, 64)
+    b, t = 2, 5
+    q = torch.randn(b, t, cfg.q_heads, cfg.head_dim).to(dtype)
+    kv = torch.randn(b, t, cfg.routes, 2 * cfg.kv_heads * cfg.head_dim).to(dtype)
+    kh = cfg.kv_heads * cfg.head_dim
+    key = kv[..., :kh].view(b, t, cfg.routes, cfg.kv_heads, cfg.head_dim).permute(0, 1, 3, 2, 4)
+    val = kv[..., kh:].view(b, t, cfg.routes, cfg.kv_heads, cfg.head_dim).permute(0, 1, 3, 2, 4)
+    want = om.manual_gqa(cfg, q, key, val)
+    ref64 = om.manual_gqa(cfg, q.double(), key.double(), val.double())
+    kvd = kv.to(dev)
+    keyd = kvd[..., :kh].view(b, t, cfg.routes, cfg.kv_heads, cfg.head_dim).permute(0, 1, 3, 2, 4)
+    vald = kvd[..., kh:].view(b, t, cfg.routes, cfg.kv_heads, cfg.head_dim).permute(0, 1, 3, 2, 4)
+    got = ops.sink_attention(q.to(dev).view(b, t, cfg.kv_heads, cfg.groups, cfg.head_dim), keyd, vald,
+                             cfg.softmax_scale, cfg.sink_logit).reshape(b, t, cfg.q_heads, cfg.head_dim).cpu()
+    assert om.rel_err(got, want) < tol
+    assert om.rel_err(got, ref64) < tol
+    scores = torch.randn(40, 184) * 3
+    p = ops.sink_probabilities(scores.to(dev), cfg.sink_logit).cpu()
+    torch.testing.assert_close(p.double(), om.sink_probabilities(scores.double(), cfg.sink_logit), rtol=1e-5,
+                               atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_causal_conv(dev, dtype, tol):
+    cfg = om.MemCfg(256, 4, 16, 4, 2, 64)
+    p = {"short_conv.norm.weight": 1 + 0.1 * torch.randn(256), "short_conv.conv.weight": 0.2 * torch.randn(256, 1, 4)}
+    mixed = (torch.randn(3, 37, 256) * 0.01).to(dtype)
+    want = mixed + om.causal_conv(p, cfg, mixed)
+    ref64 = mixed.double() + om.causal_conv(p, cfg, mixed.double())
+    got = ops.causal_conv(mixed.to(dev), p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev),
+                          3, cfg.eps).cpu()
+    assert om.rel_err(got, want) < tol and om.rel_err(got, ref64) < tol
+    got2 = ops.causal_conv(mixed.to(dev), p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev),
+                           3, cfg.eps, residual=False).cpu()
+    assert om.rel_err(got2, ref64 - mixed.double()) < tol
+
+
+# ----------------------------------------------------------------------------- K4: scan
+@pytest.mark.parametrize("b,t,n", [(8, 4096, 256), (3, 301, 16), (2, 1, 8), (1, 64, 64), (1, 65, 70)])
+def test_ssm_scan(dev, b, t, n):
+    g = torch.Generator().manual_seed(t)
+    a = 0.9 + 0.099 * torch.rand(n, generator=g)
+    u = torch.randn(b, t, n, generator=g)
+    s0 = torch.randn(b, n, generator=g)
+    for init in (None, s0):
+        got = ops.ssm_scan(a.to(dev), u.to(dev), None if init is None else init.to(dev)).cpu().numpy()
+        want = om.ssm_scan(a.numpy(), u.numpy(), None if init is None else init.numpy())
+        assert np.abs(got - want).max() < 1e-5 * max(1.0, np.abs(want).max())  # 1e-5 (fp32 tolerance)
+
+
+def test_ssm_scan_constant_input_closed_form(dev):
+    a = torch.tensor([0.9, 0.95, 0.999, 0.5])
+    u = torch.tensor([1.0, -2.0, 0.5, 3.0])
+    got = ops.ssm_scan(a.to(dev), u.expand(1, 1000, 4).contiguous().to(dev)).cpu().numpy()[0]
+    want = om.ssm_scan_closed_form_constant(a.numpy(), u.numpy(), 1000)
+    assert np.abs(got - want).max() < 1e-5
+
+
+# ----------------------------------------------------------------------------- K5: tree acceptance
+PARENT = (-1, 0, 1, 0, 3, 1)
+
+
+@pytest.mark.parametrize("argmax,path,new", [
+    ([3, 9, 9, 4, 8, 9], [0, 3, 4], [3, 4, 8]),     # reference tests/test_live_tree.py:44-52
+    ([1, 5, 9, 9, 9, 6], [0, 1, 5], [1, 5, 6]),
+    ([9, 9, 9, 9, 9, 9], [0], [9]),
+])
+def test_tree_accept_known_answers(dev, argmax, path, new):
+    toks = [7, 1, 2, 3, 4, 5]
+    p, plen, nt = ops.tree_accept(torch.tensor(PARENT, device=dev), torch.tensor(toks, device=dev),
+                                  torch.tensor(argmax, device=dev))
+    ln = int(plen[0])
+    assert _np(p)[:ln].tolist() == path and _np(nt)[:ln].tolist() == new
+    assert cint.tree_accept(PARENT, toks, argmax) == (path, new)
+
+
+def test_tree_accept_random_trees(dev):
+    rng = np.random.default_rng(7)
+    for _ in range(50):
+        n = int(rng.integers(1, 20))
+        parent = [-1] + [int(rng.integers(0, i)) for i in range(1, n)]
+        toks = rng.integers(0, 4, n).tolist()
+        am = rng.integers(0, 4, n).tolist()
+        p, plen, nt = ops.tree_accept(torch.tensor(parent, device=dev), torch.tensor(toks, device=dev),
+                                      torch.tensor(am, device=dev))
+        ln = int(plen[0])
+        assert (_np(p)[:ln].tolist(), _np(nt)[:ln].tolist()) == cint.tree_accept(parent, toks, am)
