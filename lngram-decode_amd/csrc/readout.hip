@@ -91,29 +91,31 @@ __device__ __forceinline__ bf16x8 zero8() {
   return z;
 }
 
+constexpr int FR_MAXR = 256;     // routes whose codes fit the per-wave LDS code cache
+
 // Row sources of one route chunk (32 routes = 2 tiles of 16) for this lane:
 // lane (li, lg) covers route c0 + 16*tt + li, features 64*lg .. 64*lg+63 of the
 // 256-wide route token (lg 0,1: 2-gram row halves; lg 2,3: 3-gram row halves).
+// The codes of the token at t, t-1, t-2 sit in LDS (cs[k][r] = code at t-k), so a
+// row address never waits on a dependent global load.
 struct FusedCtx {
-  const uint8_t* codes;
+  const uint8_t* cs;  // [3][FR_MAXR] in LDS
   const bf16* table2;
   const bf16* table3;
-  int64_t tok;
   int64_t t;
   int32_t R;
   int li, lg;
   bool tok_ok;
   __device__ __forceinline__ const bf16* src(int rho) const {
     if (!tok_ok || rho >= R) return nullptr;
-    const int64_t base = tok * R + rho;
     if (lg < 2) {
       if (t < 1) return nullptr;
-      const int64_t c0 = codes[base] & 15, c1 = codes[base - R] & 15;
+      const int64_t c0 = cs[rho], c1 = cs[FR_MAXR + rho];
       const int64_t row = static_cast<int64_t>(rho) * 256 + c1 + 16 * c0;
       return table2 + row * 128 + 64 * lg;
     }
     if (t < 2) return nullptr;
-    const int64_t c0 = codes[base] & 15, c1 = codes[base - R] & 15, c2 = codes[base - 2 * R] & 15;
+    const int64_t c0 = cs[rho], c1 = cs[FR_MAXR + rho], c2 = cs[2 * FR_MAXR + rho];
     const int64_t row = static_cast<int64_t>(rho) * 4096 + c2 + 16 * c1 + 256 * c0;
     return table3 + row * 128 + 64 * (lg - 2);
   }
@@ -127,19 +129,37 @@ struct FusedCtx {
   }
 };
 
-__global__ __launch_bounds__(256, 1) void k_readout_fused(const bf16* __restrict__ q, const uint8_t* __restrict__ codes,
+// LDS: one 32-row region per wave/token, reused as qkw (rows 0..15, phase A -> B), the
+// route chunk being transposed (rows 0..31, phase B) and u (rows 0..15, phase B -> C),
+// plus the token's codes.  70.6 KB per block: two blocks (8 waves) per CU.
+__global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict__ q, const uint8_t* __restrict__ codes,
                                                           int64_t B, int64_t T, int32_t R,
                                                           const bf16* __restrict__ table2,
                                                           const bf16* __restrict__ table3,
                                                           const bf16* __restrict__ wk_t, const bf16* __restrict__ wv,
                                                           const bf16* __restrict__ w_mem, float eps, float scale,
                                                           float sink, bf16* __restrict__ head_out) {
-  __shared__ __attribute__((aligned(16))) bf16 qs[FR_TOK][FR_H][FR_LD];  // qkw per token, later u
-  __shared__ __attribute__((aligned(16))) bf16 xs[4][32][FR_LD];         // per-wave route chunk
+  __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
+  __shared__ uint8_t csh[FR_TOK][3 * FR_MAXR];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   const int64_t ntok = B * T;
   const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * FR_TOK;
+
+  // ---------------- stage 0: this wave's token codes (t, t-1, t-2) into LDS, first gather in flight
+  const int64_t tok = tok0 + w;
+  const bool tok_ok = tok < ntok;
+  const int64_t tpos = tok_ok ? tok % T : 0;
+  for (int r = lane; r < R; r += 64) {
+    csh[w][r] = tok_ok ? (codes[tok * R + r] & 15) : 0;
+    csh[w][FR_MAXR + r] = (tok_ok && tpos >= 1) ? (codes[(tok - 1) * R + r] & 15) : 0;
+    csh[w][2 * FR_MAXR + r] = (tok_ok && tpos >= 2) ? (codes[(tok - 2) * R + r] & 15) : 0;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  FusedCtx ctx{csh[w], table2, table3, tpos, R, li, lg, tok_ok};
+  bf16x8 xa[2][8];
+  ctx.load(0, xa);
 
   // ---------------- phase A: qkw[t][4h+g][f] = scale * w_mem[f] * (Wk[h]^T q[t][4h+g])[f], wave = head h
   {
@@ -162,17 +182,15 @@ __global__ __launch_bounds__(256, 1) void k_readout_fused(const bf16* __restrict
       bf16x4 o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(w_mem[f + i]) * scale);
-      *reinterpret_cast<bf16x4*>(&qs[li >> 2][hg][f]) = o;
+      *reinterpret_cast<bf16x4*>(&xs[li >> 2][hg][f]) = o;
     }
   }
   __syncthreads();
 
   // ---------------- phase B: one token per wave, routes in chunks of 32
-  const int64_t tok = tok0 + w;
-  FusedCtx ctx{codes, table2, table3, tok, tok < ntok ? tok % T : 0, R, li, lg, tok < ntok};
   bf16x8 qb[8];
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&qs[w][li][64 * lg + 8 * kk]);
+  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][li][64 * lg + 8 * kk]);
 
   float m_run = sink, l_part = 0.f;
   f32x4 acc[16];
@@ -237,13 +255,15 @@ __global__ __launch_bounds__(256, 1) void k_readout_fused(const bf16* __restrict
     for (int ft = 0; ft < 16; ++ft)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[ft][i] *= aD[i];
-    // route chunk to LDS (row layout), then transposed reads as the B operand of P.X
+    // route chunk to LDS (row layout), then transposed reads as the B operand of P.X;
+    // the registers are refilled with the next chunk while the MFMAs below run
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) *reinterpret_cast<bf16x8*>(&xs[w][16 * tt + li][64 * lg + 8 * kk]) = x[tt][kk];
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    if (c0 + 32 < R) ctx.load(c0 + 32, x);
     // ds_read_b64_tr_b16: lane i of each 16-lane group receives element i%4 of the 8-byte
     // chunks addressed by lanes i/4 + 4c (c = 0..3), i.e. X[4g + c][16ft + i] here.  The
     // two halves are joined with a shuffle: element-wise bit casts of the returned
@@ -262,15 +282,7 @@ __global__ __launch_bounds__(256, 1) void k_readout_fused(const bf16* __restrict
     __builtin_amdgcn_wave_barrier();
   };
 
-  bf16x8 xa[2][8], xb[2][8];
-  ctx.load(0, xa);
-  for (int c0 = 0; c0 < R; c0 += 64) {
-    if (c0 + 32 < R) ctx.load(c0 + 32, xb);
-    process(c0, xa);
-    if (c0 + 32 >= R) break;
-    if (c0 + 64 < R) ctx.load(c0 + 64, xa);
-    process(c0 + 32, xb);
-  }
+  for (int c0 = 0; c0 < R; c0 += 32) process(c0, xa);
 
   // normalise and stage u = w_mem . U / l for the value projection
   float lt = l_part + __shfl_xor(l_part, 16, 64);
@@ -285,7 +297,7 @@ __global__ __launch_bounds__(256, 1) void k_readout_fused(const bf16* __restrict
     const int f = 16 * ft + li;
     const float wm = to_f32(w_mem[f]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) qs[w][4 * lg + i][f] = static_cast<bf16>(acc[ft][i] * iD[i] * wm);
+    for (int i = 0; i < 4; ++i) xs[w][4 * lg + i][f] = static_cast<bf16>(acc[ft][i] * iD[i] * wm);
   }
   __syncthreads();
 
@@ -300,7 +312,7 @@ __global__ __launch_bounds__(256, 1) void k_readout_fused(const bf16* __restrict
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
         const bf16x8 a = ld16(wv + (static_cast<int64_t>(h) * FR_HD + 16 * dt + li) * FR_DT + 32 * ks + 8 * lg);
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&qs[li >> 2][hg][32 * ks + 8 * lg]);
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&xs[li >> 2][hg][32 * ks + 8 * lg]);
         d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, d, 0, 0, 0);
       }
       if (tc < ntok) {
@@ -363,6 +375,7 @@ int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int
                              const void* table3, const void* wk_t, const void* wv, const void* w_mem, float eps,
                              float scale, float sink_logit, void* head_out, void* stream) {
   if (B < 0 || T < 0 || R <= 0) return fail(LNG_E_ARG, "memory_readout_fused: bad shape");
+  if (R > FR_MAXR) return fail(LNG_E_ARG, "memory_readout_fused: at most 256 routes");
   const int64_t ntok = B * T;
   if (ntok == 0) return LNG_OK;
   const int64_t blocks = cdiv(ntok, FR_TOK);

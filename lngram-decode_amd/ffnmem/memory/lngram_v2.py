@@ -329,7 +329,8 @@ class _RouteNgramMemoryBase(nn.Module):
     # ------------------------------------------------------------------ fused path
     def _fused_shape_ok(self, hidden_states: Tensor) -> bool:
         return (hidden_states.dtype == torch.bfloat16 and self.ngrams == (2, 3) and self.memory_dim == 128
-                and self.bits_per_route == 4 and self.readout_num_heads == 16 and self.readout_head_dim == 64
+                and self.bits_per_route == 4 and self.num_routes <= 256
+                and self.readout_num_heads == 16 and self.readout_head_dim == 64
                 and self.readout_num_kv_heads == 4 and self.readout_kv_proj.weight.dtype == torch.bfloat16
                 and all(t.weight.dtype == torch.bfloat16 for t in self.tables.values()))
 

@@ -186,6 +186,18 @@ def test_causal_conv(dev, dtype, tol):
     assert om.rel_err(got2, ref64 - mixed.double()) < tol
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+def test_causal_conv_generic_shape(dev, dtype, tol):
+    # kernel 3, dilation 2, odd width: the general (non-specialised) conv kernel
+    cfg = om.MemCfg(100, 4, 16, 4, 2, 25, orders=(2,), conv_kernel=3)
+    p = {"short_conv.norm.weight": 1 + 0.1 * torch.randn(100), "short_conv.conv.weight": 0.2 * torch.randn(100, 1, 3)}
+    mixed = (torch.randn(2, 21, 100) * 0.01).to(dtype)
+    ref64 = mixed.double() + om.causal_conv(p, cfg, mixed.double())
+    got = ops.causal_conv(mixed.to(dev), p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev),
+                          cfg.conv_dilation, cfg.eps).cpu()
+    assert om.rel_err(got, ref64) < tol
+
+
 # ----------------------------------------------------------------------------- K4: scan
 @pytest.mark.parametrize("b,t,n", [(8, 4096, 256), (3, 301, 16), (2, 1, 8), (1, 64, 64), (1, 65, 70)])
 def test_ssm_scan(dev, b, t, n):
