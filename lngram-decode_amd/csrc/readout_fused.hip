@@ -1,0 +1,307 @@
+// Fused route gather + sink readout for the bf16 memory layer (16 query heads x 64,
+// 4 KV heads, n-gram orders (2, 3), mem_dim 128): the metric kernel.
+//
+// Per token t and query head hg = 4h + g (h the KV head), with x_r the 256-wide route
+// token (2-gram row | 3-gram row) and s_r = rsqrt(mean(x_r^2) + eps):
+//   qkw_hg = scale * w_mem . (Wk[h]^T q_hg)                   (phase A, MFMA)
+//   score  = s_r * (qkw_hg . x_r)                              (phase B, MFMA)
+//   U_hg   = sum_r p_{hg,r} s_r x_r, online softmax seeded by the sink (m, l) = (b0, 1)
+//   o_hg   = Wv[h] (w_mem . U_hg / l_hg)                       (phase C, MFMA)
+// which equals the reference's RMSNorm -> KV projection -> sink GQA without ever
+// forming keys or values.
+//
+// Block = 4 waves = 4 tokens.  Phases A and C are cooperative (wave = KV head, the 16
+// MFMA columns = 4 tokens x 4 groups); phase B is one token per wave, routes in
+// chunks of 32.  A chunk is gathered with whole-row loads (16 lanes x 16 B = one
+// 256-byte table row per quarter wave), parked in the wave's LDS region in row layout,
+// read back as the score MFMA's A operand (ds_read_b128) and, transposed, as the
+// B operand of P.X (ds_read_b64_tr_b16).  The next chunk's rows are in flight while a
+// chunk is processed.
+#include "common.h"
+
+namespace lng {
+
+constexpr int FR_TOK = 4;          // tokens per block (one per wave in phase B)
+constexpr int FR_H = 16;           // query heads
+constexpr int FR_HD = 64;          // head dim
+constexpr int FR_DT = 256;         // route token dim (2 orders x 128)
+constexpr int FR_LD = FR_DT + 8;   // padded LDS row (bf16): 528 B, conflict-free 16-row access
+constexpr int FR_MAXR = 256;       // max routes (row-index slots per token)
+constexpr int FR_RB = FR_MAXR / 2;
+
+__device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 z;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = static_cast<bf16>(0.f);
+  return z;
+}
+__device__ __forceinline__ float sumsq8(const bf16x8 v, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 0, 1), __builtin_shufflevector(v, v, 0, 1), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 2, 3), __builtin_shufflevector(v, v, 2, 3), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 4, 5), __builtin_shufflevector(v, v, 4, 5), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(v, v, 6, 7), __builtin_shufflevector(v, v, 6, 7), acc,
+                                        false);
+  return acc;
+}
+
+// LDS (75.8 KB per block, two blocks per CU): per wave a 32-row region reused as qkw
+// (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B) and u (rows 0..15,
+// phase B -> C); per wave the token's row indices [order][route parity][route / 2]
+// (-1 = zero row).
+__global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict__ q, const uint8_t* __restrict__ codes,
+                                                          int64_t B, int64_t T, int32_t R,
+                                                          const bf16* __restrict__ table2,
+                                                          const bf16* __restrict__ table3,
+                                                          const bf16* __restrict__ wk_t, const bf16* __restrict__ wv,
+                                                          const bf16* __restrict__ w_mem, float eps, float scale,
+                                                          float sink, bf16* __restrict__ head_out) {
+  __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
+  __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][2][FR_RB];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int li = lane & 15, lg = lane >> 4;
+  const int64_t ntok = B * T;
+  const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * FR_TOK;
+  const int64_t tok = tok0 + w;
+  const bool tok_ok = tok < ntok;
+  const int64_t tpos = tok_ok ? tok % T : 0;
+
+  // ---------------- stage 0: row indices of this wave's token (codes at t, t-1, t-2)
+  {
+    uint8_t cv[3][FR_MAXR / 64];
+#pragma unroll
+    for (int k = 0; k < FR_MAXR / 64; ++k) {
+      const int r = lane + 64 * k;
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+        cv[p][k] = (tok_ok && r < R && tpos >= p) ? static_cast<uint8_t>(codes[(tok - p) * R + r] & 15) : 0;
+    }
+#pragma unroll
+    for (int k = 0; k < FR_MAXR / 64; ++k) {
+      const int r = lane + 64 * k;
+      int32_t r2 = -1, r3 = -1;
+      if (tok_ok && r < R) {
+        if (tpos >= 1) r2 = r * 256 + cv[1][k] + 16 * cv[0][k];
+        if (tpos >= 2) r3 = r * 4096 + cv[2][k] + 16 * cv[1][k] + 256 * cv[0][k];
+      }
+      rowsh[w][0][r & 1][r >> 1] = r2;
+      rowsh[w][1][r & 1][r >> 1] = r3;
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+
+  // chunk gather: instruction m, lane: route c0 + 2m + lane/32, order (lane/16)&1, 16-byte piece lane%16
+  const int g_ord = (lane >> 4) & 1, g_par = lane >> 5, g_piece = lane & 15;
+  const bf16* g_tab = g_ord ? table3 : table2;
+  auto gather = [&](int c0, u32x4 (&g)[16]) {
+    const int32_t* rp = &rowsh[w][g_ord][g_par][c0 >> 1];
+    int32_t rows[16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int32_t __attribute__((ext_vector_type(4))) r4 =
+          *reinterpret_cast<const int32_t __attribute__((ext_vector_type(4)))*>(rp + 4 * v);
+      rows[4 * v] = r4[0];
+      rows[4 * v + 1] = r4[1];
+      rows[4 * v + 2] = r4[2];
+      rows[4 * v + 3] = r4[3];
+    }
+#pragma unroll
+    for (int m = 0; m < 16; ++m) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      g[m] = rows[m] >= 0 ? *reinterpret_cast<const u32x4*>(g_tab + static_cast<int64_t>(rows[m]) * 128 + 8 * g_piece)
+                          : z;
+    }
+  };
+  auto stash = [&](const u32x4 (&g)[16]) {
+#pragma unroll
+    for (int m = 0; m < 16; ++m)
+      *reinterpret_cast<u32x4*>(&xs[w][2 * m + g_par][g_ord * 128 + 8 * g_piece]) = g[m];
+  };
+
+  u32x4 g[16];
+  gather(0, g);  // first chunk in flight during phase A
+
+  // ---------------- phase A: qkw[t][4h+g][f] = scale * w_mem[f] * (Wk[h]^T q[t][4h+g])[f], wave = head h
+  {
+    const int h = w;
+    const int64_t tq = tok0 + (li >> 2);
+    const int hg = h * 4 + (li & 3);
+    bf16x8 bq[2], wa[16][2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      bq[ks] = tq < ntok ? ld16(q + tq * (FR_H * FR_HD) + hg * FR_HD + 32 * ks + 8 * lg) : zero8();
+#pragma unroll
+    for (int ft = 0; ft < 16; ++ft)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        wa[ft][ks] = ld16(wk_t + (static_cast<int64_t>(h) * FR_DT + 16 * ft + li) * FR_HD + 32 * ks + 8 * lg);
+#pragma unroll
+    for (int ft = 0; ft < 16; ++ft) {
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[ft][ks], bq[ks], d, 0, 0, 0);
+      const int f = 16 * ft + 4 * lg;
+      bf16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(w_mem[f + i]) * scale);
+      *reinterpret_cast<bf16x4*>(&xs[li >> 2][hg][f]) = o;
+    }
+  }
+  __syncthreads();
+
+  // ---------------- phase B: one token per wave
+  bf16x8 qb[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][li][64 * lg + 8 * kk]);
+
+  float m_run = sink, l_part = 0.f;
+  f32x4 acc[16];
+#pragma unroll
+  for (int ft = 0; ft < 16; ++ft) acc[ft] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < R; c0 += 32) {
+    stash(g);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (c0 + 32 < R) gather(c0 + 32, g);
+
+    // scores: A = route rows (lane: route 16tt + li, features 64lg + 8kk..), B = qkw
+    float sr[2];
+    f32x4 sc[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      bf16x8 x[8];
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) x[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][16 * tt + li][64 * lg + 8 * kk]);
+      float ss = 0.f;
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) ss = sumsq8(x[kk], ss);
+      ss += __shfl_xor(ss, 16, 64);
+      ss += __shfl_xor(ss, 32, 64);
+      sr[tt] = 1.0f / sqrtf(ss * (1.0f / FR_DT) + eps);  // route c0 + 16tt + li
+      sc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[kk], qb[kk], sc[tt], 0, 0, 0);
+    }
+    // sc[tt][i]: route c0 + 16tt + 4lg + i, head hg = li
+    float sD[2][4], s[2][4];
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sD[tt][i] = __shfl(sr[tt], 4 * lg + i, 64);
+        const int r = c0 + 16 * tt + 4 * lg + i;
+        s[tt][i] = r < R ? sc[tt][i] * sD[tt][i] : -INFINITY;
+        cmax = fmaxf(cmax, s[tt][i]);
+      }
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
+    cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
+    const float m_new = fmaxf(m_run, cmax);
+    const float alpha = expf(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    bf16x8 pa;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = expf(s[tt][i] - m_new);
+        psum += p;
+        pa[4 * tt + i] = static_cast<bf16>(p * sD[tt][i]);
+      }
+    l_part = l_part * alpha + psum;
+    float aD[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) aD[i] = __shfl(alpha, 4 * lg + i, 64);
+#pragma unroll
+    for (int ft = 0; ft < 16; ++ft)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[ft][i] *= aD[i];
+    // U += P . X with X transposed out of LDS: ds_read_b64_tr_b16 gives lane i of each
+    // 16-lane group element i%4 of the 8-byte chunks addressed by lanes i/4 + 4c
+    // (c = 0..3), i.e. X[4g + c][16ft + i] here.  The halves are joined with a shuffle
+    // (element-wise bit casts of the returned vector are miscompiled to element 0).
+#pragma unroll
+    for (int ft = 0; ft < 16; ++ft) {
+      const int col = 16 * ft + 4 * (li & 3);
+      const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (__attribute__((address_space(3))) bf16x4*)(&xs[w][4 * lg + (li >> 2)][col]));
+      const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+          (__attribute__((address_space(3))) bf16x4*)(&xs[w][16 + 4 * lg + (li >> 2)][col]));
+      const bf16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
+      acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, acc[ft], 0, 0, 0);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+  }
+
+  // normalise and stage u = w_mem . U / l for the value projection
+  float lt = l_part + __shfl_xor(l_part, 16, 64);
+  lt += __shfl_xor(lt, 32, 64);
+  lt += expf(sink - m_run);
+  const float inv = 1.0f / lt;
+  float iD[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) iD[i] = __shfl(inv, 4 * lg + i, 64);
+#pragma unroll
+  for (int ft = 0; ft < 16; ++ft) {
+    const int f = 16 * ft + li;
+    const float wm = to_f32(w_mem[f]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xs[w][4 * lg + i][f] = static_cast<bf16>(acc[ft][i] * iD[i] * wm);
+  }
+  __syncthreads();
+
+  // ---------------- phase C: o[t][4h+g][d] = Wv[h][d] . u[t][4h+g], wave = head h
+  {
+    const int h = w;
+    const int64_t tc = tok0 + (li >> 2);
+    const int hg = h * 4 + (li & 3);
+    bf16x8 va[4][8], ub[8];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+        va[dt][ks] = ld16(wv + (static_cast<int64_t>(h) * FR_HD + 16 * dt + li) * FR_DT + 32 * ks + 8 * lg);
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) ub[ks] = *reinterpret_cast<const bf16x8*>(&xs[li >> 2][hg][32 * ks + 8 * lg]);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][ks], ub[ks], d, 0, 0, 0);
+      if (tc < ntok) {
+        bf16x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i]);
+        *reinterpret_cast<bf16x4*>(head_out + tc * (FR_H * FR_HD) + hg * FR_HD + 16 * dt + 4 * lg) = o;
+      }
+    }
+  }
+}
+
+}  // namespace lng
+
+using namespace lng;
+
+extern "C" int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int64_t T, int32_t R,
+                                        const void* table2, const void* table3, const void* wk_t, const void* wv,
+                                        const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
+                                        void* stream) {
+  if (B < 0 || T < 0 || R <= 0) return fail(LNG_E_ARG, "memory_readout_fused: bad shape");
+  if (R > FR_MAXR) return fail(LNG_E_ARG, "memory_readout_fused: at most 256 routes");
+  const int64_t ntok = B * T;
+  if (ntok == 0) return LNG_OK;
+  const int64_t blocks = cdiv(ntok, FR_TOK);
+  if (blocks > 0x7fffffffLL) return fail(LNG_E_ARG, "memory_readout_fused: too many tokens");
+  hipLaunchKernelGGL(k_readout_fused, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
+                     static_cast<const bf16*>(q), codes, B, T, R, static_cast<const bf16*>(table2),
+                     static_cast<const bf16*>(table3), static_cast<const bf16*>(wk_t), static_cast<const bf16*>(wv),
+                     static_cast<const bf16*>(w_mem), eps, scale, sink_logit, static_cast<bf16*>(head_out));
+  return check_launch("memory_readout_fused");
+}
