@@ -115,6 +115,21 @@ int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, i
                     int64_t T, int32_t d, int32_t K, int32_t dilation, float eps, int residual, void* out,
                     void* stream);
 
+/* bf16 y[M,N] = x[M,K] . w[N,K]^T (K % 32 == 0) that also writes the RMSNorm
+ * statistics of its bf16 output rows for the following short conv: rowsq[p*M + m]
+ * holds partial sums of squares, p < lng_linear_rowsq_partials(N).  readout_o_proj
+ * feeding DepthwiseCausalConv's norm (lngram_v2.py:1354-1359, :273-286). */
+int32_t lng_linear_rowsq_partials(int64_t N);
+int lng_linear_rowsq(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, float* rowsq,
+                     void* stream);
+
+/* lng_causal_conv for bf16, kernel 4, dilation 3, taking the row statistics from
+ * lng_linear_rowsq instead of recomputing them (same rounding as lng_causal_conv).
+ * n_partials <= 16, i.e. d <= 2048. */
+int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_partials, const void* norm_w,
+                          const void* conv_w, int64_t B, int64_t T, int32_t d, int32_t K, int32_t dilation,
+                          float eps, int residual, void* out, void* stream);
+
 /* Fused memory readout (the metric kernel).  Replaces, in eval, the chain
  * _lookup_route_chunk -> _project_memory -> _manual_gqa of
  * RouteNgramMemoryV2.forward (lngram_v2.py:1361-1407) by the associativity

@@ -126,6 +126,274 @@ __global__ __launch_bounds__(256) void k_gemm_nt_bf16(const bf16* __restrict__ W
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// DMA-pipelined bf16 GEMM (K % 32 == 0): global_load_lds_dwordx4 writes each 1 KB piece of a
+// tile straight into LDS (no register staging); a ring of 4 K-stages (32 wide) keeps three
+// stages in flight while one is consumed.  Tile rows are 64 B (4 x 16 B pieces); piece p of
+// row r is stored at slot p ^ ((r >> 2) & 3), which makes the MFMA operand reads
+// (16 B per lane, 16 rows per instruction) bank-conflict free.  The DMA lane that fills a
+// slot fetches the matching swizzled piece from global memory.
+constexpr int DK = 32;              // K per stage
+constexpr int DSLOTS = 4;           // ring depth
+constexpr int DTILE = GB * DK;      // bf16 per operand tile (128 x 32)
+
+__device__ __forceinline__ int dswz(int row, int piece) { return piece ^ ((row >> 2) & 3); }
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void k_gemm_dma_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
+                                                          int64_t N, int64_t M, int64_t K, void* __restrict__ out,
+                                                          float* __restrict__ logits, void* __restrict__ codes,
+                                                          int codes_dt, int64_t routes) {
+  __shared__ __attribute__((aligned(16))) bf16 ring[DSLOTS][2][DTILE];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * GB;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * GB;
+  const int nk = static_cast<int>(K / DK);
+
+  // DMA assignment: each wave fills 2 x 1 KB of each operand tile per stage (16 rows x 64 B
+  // per instruction); lane -> (row, slot) and the global piece that belongs in that slot.
+  const int d_row0 = wave * 32 + (lane >> 2);  // rows d_row0 and d_row0 + 16
+  const int d_slot = lane & 3;
+  const int64_t wrow0 = n0 + d_row0 < N ? n0 + d_row0 : N - 1;
+  const int64_t wrow1 = n0 + d_row0 + 16 < N ? n0 + d_row0 + 16 : N - 1;
+  const int64_t xrow0 = m0 + d_row0 < M ? m0 + d_row0 : M - 1;
+  const int64_t xrow1 = m0 + d_row0 + 16 < M ? m0 + d_row0 + 16 : M - 1;
+  const int p0 = dswz(d_row0, d_slot), p1 = dswz(d_row0 + 16, d_slot);
+  const bf16* w0 = W + wrow0 * K + 8 * p0;
+  const bf16* w1 = W + wrow1 * K + 8 * p1;
+  const bf16* x0 = X + xrow0 * K + 8 * p0;
+  const bf16* x1 = X + xrow1 * K + 8 * p1;
+  auto issue = [&](int kt) {
+    const int s = kt % DSLOTS;
+    const int64_t kb = static_cast<int64_t>(kt) * DK;
+    bf16* wt = &ring[s][0][wave * 32 * DK];
+    bf16* xt = &ring[s][1][wave * 32 * DK];
+    __builtin_amdgcn_global_load_lds(w0 + kb, (__attribute__((address_space(3))) void*)wt, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(w1 + kb, (__attribute__((address_space(3))) void*)(wt + 16 * DK), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(x0 + kb, (__attribute__((address_space(3))) void*)xt, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(x1 + kb, (__attribute__((address_space(3))) void*)(xt + 16 * DK), 16, 0, 0);
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < DSLOTS - 1 && s < nk; ++s) issue(s);
+  const int rsel = lane & 15, psel = lane >> 4;
+  for (int kt = 0; kt < nk; ++kt) {
+    // stage kt landed: later stages may still be in flight (4 DMA ops each)
+    const int ahead = nk - 1 - kt;
+    if (ahead >= 2)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (ahead == 1)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // every wave's DMA for stage kt has landed and every wave is done reading slot
+    // (kt - 1) % DSLOTS; a plain barrier (no release fence: that would wait for the
+    // stages still in flight)
+    __builtin_amdgcn_s_barrier();
+    if (kt + DSLOTS - 1 < nk) issue(kt + DSLOTS - 1);
+    const int s = kt % DSLOTS;
+    bf16x8 a[4], b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ra = wr * 64 + i * 16 + rsel, rb = wc * 64 + i * 16 + rsel;
+      a[i] = *reinterpret_cast<const bf16x8*>(&ring[s][0][ra * DK + 8 * dswz(ra, psel)]);
+      b[i] = *reinterpret_cast<const bf16x8*>(&ring[s][1][rb * DK + 8 * dswz(rb, psel)]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + wr * 64 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = m0 + wc * 64 + j * 16 + (lane & 15);
+      if (m >= M) continue;
+      const f32x4 v = acc[i][j];
+      if (EPI == EPI_BF16) {
+        bf16* o = static_cast<bf16*>(out) + m * N + n;
+        if (n + 3 < N && (N & 3) == 0) {
+          bf16x4 pk = {static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]),
+                       static_cast<bf16>(v[3])};
+          *reinterpret_cast<bf16x4*>(o) = pk;
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = static_cast<bf16>(v[e]);
+        }
+      } else if (EPI == EPI_F32) {
+        float* o = static_cast<float*>(out) + m * N + n;
+        if (n + 3 < N && (N & 3) == 0) {
+          *reinterpret_cast<f32x4*>(o) = v;
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = v[e];
+        }
+      } else {
+        if (n >= N) continue;
+        if (logits) *reinterpret_cast<f32x4*>(logits + m * N + n) = v;
+        const int code = (v[0] > 0.f ? 1 : 0) | (v[1] > 0.f ? 2 : 0) | (v[2] > 0.f ? 4 : 0) | (v[3] > 0.f ? 8 : 0);
+        const int64_t r = n >> 2;
+        if (codes_dt == LNG_U8)
+          static_cast<uint8_t*>(codes)[m * routes + r] = static_cast<uint8_t>(code);
+        else
+          static_cast<int32_t*>(codes)[m * routes + r] = code;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Large-M variant: 256 (W rows) x 256 (X rows) tile, 8 waves (2 x 4, each 128 x 64), same
+// DMA ring (4 stages of K = 32, 128 KB LDS, one block per CU).  Twice the MFMA work per
+// stage and half the L2 traffic of the 128-tile kernel, so three stages in flight cover the
+// load latency.
+constexpr int GB2 = 256;
+constexpr int DTILE2 = GB2 * DK;
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void k_gemm_dma256_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
+                                                             int64_t N, int64_t M, int64_t K, void* __restrict__ out,
+                                                             float* __restrict__ logits, void* __restrict__ codes,
+                                                             int codes_dt, int64_t routes,
+                                                             float* __restrict__ rowsq) {
+  __shared__ __attribute__((aligned(16))) bf16 ring[DSLOTS][2][DTILE2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wr = wave >> 2, wc = wave & 3;  // wave tile: W rows wr*128 .. +128, X rows wc*64 .. +64
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * GB2;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * GB2;
+  const int nk = static_cast<int>(K / DK);
+
+  // DMA: each wave fills rows wave*32 .. +32 of both tiles (2 instructions per tile per stage)
+  const int d_row0 = wave * 32 + (lane >> 2);
+  const int d_slot = lane & 3;
+  const int p0 = dswz(d_row0, d_slot), p1 = dswz(d_row0 + 16, d_slot);
+  const int64_t wrow0 = n0 + d_row0 < N ? n0 + d_row0 : N - 1;
+  const int64_t wrow1 = n0 + d_row0 + 16 < N ? n0 + d_row0 + 16 : N - 1;
+  const int64_t xrow0 = m0 + d_row0 < M ? m0 + d_row0 : M - 1;
+  const int64_t xrow1 = m0 + d_row0 + 16 < M ? m0 + d_row0 + 16 : M - 1;
+  const bf16* w0 = W + wrow0 * K + 8 * p0;
+  const bf16* w1 = W + wrow1 * K + 8 * p1;
+  const bf16* x0 = X + xrow0 * K + 8 * p0;
+  const bf16* x1 = X + xrow1 * K + 8 * p1;
+  auto issue = [&](int kt) {
+    const int s = kt % DSLOTS;
+    const int64_t kb = static_cast<int64_t>(kt) * DK;
+    bf16* wt = &ring[s][0][wave * 32 * DK];
+    bf16* xt = &ring[s][1][wave * 32 * DK];
+    __builtin_amdgcn_global_load_lds(w0 + kb, (__attribute__((address_space(3))) void*)wt, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(w1 + kb, (__attribute__((address_space(3))) void*)(wt + 16 * DK), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(x0 + kb, (__attribute__((address_space(3))) void*)xt, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(x1 + kb, (__attribute__((address_space(3))) void*)(xt + 16 * DK), 16, 0, 0);
+  };
+
+  f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int s = 0; s < DSLOTS - 1 && s < nk; ++s) issue(s);
+  const int rsel = lane & 15, psel = lane >> 4;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int ahead = nk - 1 - kt;
+    if (ahead >= 2)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (ahead == 1)
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    if (kt + DSLOTS - 1 < nk) issue(kt + DSLOTS - 1);
+    const int s = kt % DSLOTS;
+    bf16x8 a[8], b[4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int ra = wr * 128 + i * 16 + rsel;
+      a[i] = *reinterpret_cast<const bf16x8*>(&ring[s][0][ra * DK + 8 * dswz(ra, psel)]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int rb = wc * 64 + j * 16 + rsel;
+      b[j] = *reinterpret_cast<const bf16x8*>(&ring[s][1][rb * DK + 8 * dswz(rb, psel)]);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+  }
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int64_t n = n0 + wr * 128 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t m = m0 + wc * 64 + j * 16 + (lane & 15);
+      if (m >= M) continue;
+      const f32x4 v = acc[i][j];
+      if (EPI == EPI_BF16) {
+        bf16* o = static_cast<bf16*>(out) + m * N + n;
+        if (n + 3 < N && (N & 3) == 0) {
+          bf16x4 pk = {static_cast<bf16>(v[0]), static_cast<bf16>(v[1]), static_cast<bf16>(v[2]),
+                       static_cast<bf16>(v[3])};
+          *reinterpret_cast<bf16x4*>(o) = pk;
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = static_cast<bf16>(v[e]);
+        }
+      } else if (EPI == EPI_F32) {
+        float* o = static_cast<float*>(out) + m * N + n;
+        if (n + 3 < N && (N & 3) == 0) {
+          *reinterpret_cast<f32x4*>(o) = v;
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < N) o[e] = v[e];
+        }
+      } else {
+        if (n >= N) continue;
+        if (logits) *reinterpret_cast<f32x4*>(logits + m * N + n) = v;
+        const int code = (v[0] > 0.f ? 1 : 0) | (v[1] > 0.f ? 2 : 0) | (v[2] > 0.f ? 4 : 0) | (v[3] > 0.f ? 8 : 0);
+        const int64_t r = n >> 2;
+        if (codes_dt == LNG_U8)
+          static_cast<uint8_t*>(codes)[m * routes + r] = static_cast<uint8_t>(code);
+        else
+          static_cast<int32_t*>(codes)[m * routes + r] = code;
+      }
+    }
+  }
+  // partial sums of squares of the bf16-rounded output rows (RMSNorm statistics for a
+  // following row norm): one partial per (256-wide N tile, wave row half), fixed order
+  if (EPI == EPI_BF16 && rowsq) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float ps = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t n = n0 + wr * 128 + i * 16 + 4 * (lane >> 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float r = static_cast<float>(static_cast<bf16>(acc[i][j][e]));
+          ps = (n + e < N) ? fmaf(r, r, ps) : ps;
+        }
+      }
+      ps += __shfl_xor(ps, 16, 64);
+      ps += __shfl_xor(ps, 32, 64);
+      const int64_t m = m0 + wc * 64 + j * 16 + (lane & 15);
+      if (lane < 16 && m < M) rowsq[(static_cast<int64_t>(blockIdx.x) * 2 + wr) * M + m] = ps;
+    }
+  }
+}
+
 // fp32 VALU tile GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
 // K staged through LDS 16 at a time.  A/B element types may be float or bf16.
 template <typename TA, typename TB, typename TO>
@@ -174,9 +442,20 @@ __global__ __launch_bounds__(256) void k_gemm_nt_f32(const TA* __restrict__ X, c
 
 template <int EPI>
 static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, void* out, float* logits,
-                       void* codes, int codes_dt, int64_t routes, hipStream_t s) {
+                       void* codes, int codes_dt, int64_t routes, hipStream_t s, float* rowsq = nullptr) {
+  if (K % DK == 0 && (M >= 4096 || rowsq)) {
+    dim3 g2(static_cast<unsigned>(cdiv(N, GB2)), static_cast<unsigned>(cdiv(M, GB2)));
+    hipLaunchKernelGGL(k_gemm_dma256_bf16<EPI>, g2, dim3(512), 0, s, w, x, N, M, K, out, logits, codes, codes_dt,
+                       routes, rowsq);
+    return check_launch("gemm_bf16_256");
+  }
   dim3 grid(static_cast<unsigned>(cdiv(N, GB)), static_cast<unsigned>(cdiv(M, GB)));
-  hipLaunchKernelGGL(k_gemm_nt_bf16<EPI>, grid, dim3(256), 0, s, w, x, N, M, K, out, logits, codes, codes_dt, routes);
+  if (K % DK == 0)
+    hipLaunchKernelGGL(k_gemm_dma_bf16<EPI>, grid, dim3(256), 0, s, w, x, N, M, K, out, logits, codes, codes_dt,
+                       routes);
+  else
+    hipLaunchKernelGGL(k_gemm_nt_bf16<EPI>, grid, dim3(256), 0, s, w, x, N, M, K, out, logits, codes, codes_dt,
+                       routes);
   return check_launch("gemm_bf16");
 }
 
@@ -199,6 +478,18 @@ int linear_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, v
 using namespace lng;
 
 extern "C" {
+
+int32_t lng_linear_rowsq_partials(int64_t N) { return static_cast<int32_t>(2 * cdiv(N, GB2)); }
+
+int lng_linear_rowsq(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, float* rowsq,
+                     void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(LNG_E_ARG, "linear_rowsq: bad shape");
+  if (K % DK) return fail(LNG_E_ARG, "linear_rowsq: needs K % 32 == 0");
+  if (!rowsq) return fail(LNG_E_ARG, "linear_rowsq: rowsq buffer required");
+  if (M == 0) return LNG_OK;
+  return launch_mfma<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, y, nullptr,
+                               nullptr, 0, 0, as_stream(stream), rowsq);
+}
 
 int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, int64_t K, void* y, void* stream) {
   if (M < 0 || N <= 0 || K <= 0) return fail(LNG_E_ARG, "linear: bad shape");

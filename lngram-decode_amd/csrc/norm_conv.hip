@@ -26,6 +26,40 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const T* __restrict__ x, const 
   for (int c = lane; c < dim; c += 64) o[c] = from_f32<T>(round_to<T>(to_f32(xr[c]) * r) * to_f32(w[c]));
 }
 
+// Vectorised RMSNorm for dim = NV * 512 (bf16: 16-byte loads): one wave per row, the
+// whole row is loaded into registers before the reduction (one memory latency per row).
+template <int NV>
+__global__ __launch_bounds__(256) void k_rmsnorm_bf16_vec(const bf16* __restrict__ x, const bf16* __restrict__ w,
+                                                          int64_t rows, float eps, bf16* __restrict__ out) {
+  constexpr int dim = NV * 512;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bf16* xr = x + row * dim;
+  bf16x8 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = *reinterpret_cast<const bf16x8*>(xr + (i * 64 + lane) * 8);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = static_cast<float>(v[i][j]);
+      ss = fmaf(f, f, ss);
+    }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + (i * 64 + lane) * 8);
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      o[j] = static_cast<bf16>(round_to<bf16>(static_cast<float>(v[i][j]) * r) * static_cast<float>(wv[j]));
+    *reinterpret_cast<bf16x8*>(out + row * dim + (i * 64 + lane) * 8) = o;
+  }
+}
+
 constexpr int CONV_TT = 16;  // positions per block
 
 // out[b,t,c] = [mixed +] SiLU(sum_j w[c,j] * xn[b, t - (K-1-j)*dil, c]), xn = RMSNorm(mixed).
@@ -184,6 +218,176 @@ __global__ __launch_bounds__(128) void k_causal_conv_k4d3(const T* __restrict__ 
   }
 }
 
+// bf16, kernel 4, dilation 3, with the row sums of squares already reduced by the
+// producing GEMM (rowsq[p][m], P <= MAXP partials per row m = b*T + t, summed in fixed
+// order; slots p >= P add an exact zero).  Block = (b, RSQ_TT positions), thread = 8
+// channels: the thread loads the RSQ_TT + 9 rows its outputs depend on (all loads issued
+// before the block barrier), the first RSQ_ROWS threads turn the partials into the row
+// scales in LDS, then each row is normalised once and scattered into the (up to) four
+// outputs whose taps read it.  SiLU uses the hardware exp2 and reciprocal.
+constexpr int RSQ_MAXP = 16;
+constexpr int RSQ_TT = 8;
+constexpr int RSQ_ROWS = RSQ_TT + 9;
+
+template <int MAXP>
+__global__ __launch_bounds__(256) void k_causal_conv_k4d3_rowsq(const bf16* __restrict__ mixed,
+                                                               const float* __restrict__ rowsq, int32_t P,
+                                                               const bf16* __restrict__ norm_w,
+                                                               const bf16* __restrict__ conv_w, uint32_t M,
+                                                               uint32_t T_len, uint32_t d8, float eps, int residual,
+                                                               bf16* __restrict__ out) {
+  __shared__ float srow[RSQ_ROWS];
+  const uint32_t tid = threadIdx.x;
+  const int t0 = static_cast<int>(blockIdx.x) * RSQ_TT;
+  const int T = static_cast<int>(T_len);
+  const size_t row0 = static_cast<size_t>(blockIdx.y) * T_len;
+  const uint32_t d = d8 * 8u;
+  auto clamp_t = [&](int tp) { return tp < 0 ? 0 : (tp >= T ? T - 1 : tp); };
+  if (tid < RSQ_ROWS) {
+    const size_t m = row0 + clamp_t(t0 - 9 + static_cast<int>(tid));
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < MAXP; ++p) {
+      const float v = rowsq[static_cast<size_t>(p < P ? p : 0) * M + m];
+      ss += p < P ? v : 0.f;
+    }
+    srow[tid] = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+  }
+  const bool active = tid < d8;
+  const uint32_t c = (active ? tid : 0u) * 8u;
+  bf16x8 x[RSQ_ROWS];
+#pragma unroll
+  for (int r = 0; r < RSQ_ROWS; ++r)
+    x[r] = *reinterpret_cast<const bf16x8*>(mixed + (row0 + clamp_t(t0 - 9 + r)) * d + c);
+  const bf16x8 nwv = *reinterpret_cast<const bf16x8*>(norm_w + c);
+  bf16x8 cw[4];  // taps of channels c .. c+7: cw[q][4*i + k] = conv_w[c + 2q + i][k]
+#pragma unroll
+  for (int q = 0; q < 4; ++q) cw[q] = *reinterpret_cast<const bf16x8*>(conv_w + static_cast<size_t>(c) * 4 + 8 * q);
+  __syncthreads();
+  if (!active) return;
+  float acc[RSQ_TT][8];
+#pragma unroll
+  for (int i = 0; i < RSQ_TT; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+#pragma unroll
+  for (int r = 0; r < RSQ_ROWS; ++r) {
+    const int tp = t0 - 9 + r;
+    if (tp < 0 || tp >= T) continue;  // zero left padding; rows past T feed no stored output
+    const float s = srow[r];
+    float xn[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      xn[j] = round_to<bf16>(round_to<bf16>(static_cast<float>(x[r][j]) * s) * static_cast<float>(nwv[j]));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = r - 3 * k;  // output t0 + i reads this row with tap k
+      if (i < 0 || i >= RSQ_TT) continue;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(static_cast<float>(cw[j >> 1][4 * (j & 1) + k]), xn[j], acc[i][j]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RSQ_TT; ++i) {
+    if (t0 + i >= T) break;
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float y = round_to<bf16>(acc[i][j]);
+      const float e = __builtin_amdgcn_exp2f(-y * 1.4426950408889634f);
+      const float act = round_to<bf16>(y * __builtin_amdgcn_rcpf(1.0f + e));
+      o[j] = static_cast<bf16>(residual ? static_cast<float>(x[i + 9][j]) + act : act);
+    }
+    *reinterpret_cast<bf16x8*>(out + (row0 + t0 + i) * d + c) = o;
+  }
+}
+
+// bf16, kernel 4, dilation 3, single pass: block = (b, 16 positions), d/8 threads, each
+// thread keeps its 8 channels of all 25 rows (16 + 9 causal halo) in registers.  Row
+// norms are reduced across the block (wave sums, then LDS), then the conv runs from the
+// registers.  Every load of the block is issued before the first reduction.
+constexpr int C43R_ROWS = C43_TT + C43_HALO;
+
+__global__ __launch_bounds__(256) void k_causal_conv_k4d3_bf16_reg(const bf16* __restrict__ mixed,
+                                                                   const bf16* __restrict__ norm_w,
+                                                                   const bf16* __restrict__ conv_w, int64_t T_len,
+                                                                   int32_t d, float eps, int residual,
+                                                                   bf16* __restrict__ out) {
+  __shared__ float part[16][C43R_ROWS];  // per-wave partial sums of squares
+  __shared__ float scale[C43R_ROWS];
+  const int64_t b = blockIdx.y;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * C43_TT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nwave = (blockDim.x + 63) >> 6;
+  const int c = tid * 8;
+  const bool cok = c < d;
+  const bf16* base = mixed + b * T_len * d;
+  bf16x8 rows[C43R_ROWS];
+#pragma unroll
+  for (int i = 0; i < C43R_ROWS; ++i) {
+    const int64_t t = t0 - C43_HALO + i;
+    if (cok && t >= 0 && t < T_len) {
+      rows[i] = *reinterpret_cast<const bf16x8*>(base + t * d + c);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) rows[i][j] = static_cast<bf16>(0.f);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < C43R_ROWS; ++i) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = static_cast<float>(rows[i][j]);
+      ss = fmaf(f, f, ss);
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) part[wave][i] = ss;
+  }
+  __syncthreads();
+  if (tid < C43R_ROWS) {
+    float ss = 0.f;
+    for (int k = 0; k < nwave; ++k) ss += part[k][tid];
+    const int64_t t = t0 - C43_HALO + tid;
+    scale[tid] = (t >= 0 && t < T_len) ? 1.0f / sqrtf(ss / static_cast<float>(d) + eps) : 0.f;
+  }
+  __syncthreads();
+  if (!cok) return;
+  const bf16x8 nwv = *reinterpret_cast<const bf16x8*>(norm_w + c);
+  float w[4][8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) w[k][j] = static_cast<float>(conv_w[(c + j) * 4 + k]);
+  // normalised rows, rounded to bf16 as the reference stores them
+  bf16x8 xn[C43R_ROWS];
+#pragma unroll
+  for (int i = 0; i < C43R_ROWS; ++i) {
+    const float s = scale[i];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      xn[i][j] = static_cast<bf16>(round_to<bf16>(static_cast<float>(rows[i][j]) * s) * static_cast<float>(nwv[j]));
+  }
+#pragma unroll
+  for (int tt = 0; tt < C43_TT; ++tt) {
+    const int64_t t = t0 + tt;
+    if (t >= T_len) break;
+    const int i = tt + C43_HALO;  // row index of position t
+    bf16x8 o;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float acc = w[0][j] * static_cast<float>(xn[i - 9][j]);
+      acc = fmaf(w[1][j], static_cast<float>(xn[i - 6][j]), acc);
+      acc = fmaf(w[2][j], static_cast<float>(xn[i - 3][j]), acc);
+      acc = fmaf(w[3][j], static_cast<float>(xn[i][j]), acc);
+      const float y = round_to<bf16>(acc);
+      const float act = round_to<bf16>(y / (1.0f + expf(-y)));
+      o[j] = static_cast<bf16>(residual ? static_cast<float>(rows[i][j]) + act : act);
+    }
+    *reinterpret_cast<bf16x8*>(out + (b * T_len + t) * d + c) = o;
+  }
+}
+
 }  // namespace lng
 
 using namespace lng;
@@ -196,6 +400,20 @@ int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t d
   if (rows == 0) return LNG_OK;
   dim3 grid(static_cast<unsigned>(cdiv(rows, 4)));
   hipStream_t s = as_stream(stream);
+  if (dtype == LNG_BF16 && dim % 512 == 0 && dim <= 2048) {
+    const bf16* xp = static_cast<const bf16*>(x);
+    const bf16* wp = static_cast<const bf16*>(w);
+    bf16* op = static_cast<bf16*>(out);
+    if (dim == 512)
+      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<1>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    else if (dim == 1024)
+      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<2>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    else if (dim == 1536)
+      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<3>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    else
+      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<4>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    return check_launch("rmsnorm_bf16_vec");
+  }
   if (dtype == LNG_F32)
     hipLaunchKernelGGL(k_rmsnorm<float>, grid, dim3(256), 0, s, static_cast<const float*>(x),
                        static_cast<const float*>(w), rows, dim, eps, static_cast<float*>(out));
@@ -207,6 +425,41 @@ int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t d
   return check_launch("rmsnorm");
 }
 
+int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_partials, const void* norm_w,
+                          const void* conv_w, int64_t B, int64_t T, int32_t d, int32_t K, int32_t dilation, float eps,
+                          int residual, void* out, void* stream) {
+  if (B < 0 || T < 0 || d <= 0 || d % 8 || n_partials <= 0) return fail(LNG_E_ARG, "causal_conv_rowsq: bad shape");
+  if (K != 4 || dilation != 3) return fail(LNG_E_ARG, "causal_conv_rowsq: kernel 4 / dilation 3 only");
+  if (mixed == out) return fail(LNG_E_ARG, "causal_conv_rowsq: out must not alias mixed");
+  if (n_partials > RSQ_MAXP || d > 2048 || B > 65535)
+    return fail(LNG_E_ARG, "causal_conv_rowsq: needs d <= 2048 (at most 16 partials) and B <= 65535");
+  const int64_t n = B * T * (d / 8);
+  if (n == 0) return LNG_OK;
+  if (n >= (int64_t{1} << 31) || B * T * d >= (int64_t{1} << 32))
+    return fail(LNG_E_ARG, "causal_conv_rowsq: tensor too large for 32-bit indexing");
+  const dim3 grid(static_cast<unsigned>(cdiv(T, RSQ_TT)), static_cast<unsigned>(B));
+  const dim3 block(static_cast<unsigned>(cdiv(d / 8, 64) * 64));
+  const uint32_t M = static_cast<uint32_t>(B * T), Tl = static_cast<uint32_t>(T), d8 = static_cast<uint32_t>(d / 8);
+  const bf16* mx = static_cast<const bf16*>(mixed);
+  const bf16* nw = static_cast<const bf16*>(norm_w);
+  const bf16* cw = static_cast<const bf16*>(conv_w);
+  bf16* o = static_cast<bf16*>(out);
+  hipStream_t s = as_stream(stream);
+  if (n_partials <= 2)
+    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<2>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M, Tl, d8,
+                       eps, residual, o);
+  else if (n_partials <= 4)
+    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<4>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M, Tl, d8,
+                       eps, residual, o);
+  else if (n_partials <= 8)
+    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<8>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M, Tl, d8,
+                       eps, residual, o);
+  else
+    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<RSQ_MAXP>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M,
+                       Tl, d8, eps, residual, o);
+  return check_launch("causal_conv_rowsq");
+}
+
 int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, int dtype, int64_t B, int64_t T,
                     int32_t d, int32_t K, int32_t dilation, float eps, int residual, void* out, void* stream) {
   if (B < 0 || T < 0 || d <= 0 || K <= 0 || dilation <= 0) return fail(LNG_E_ARG, "causal_conv: bad shape");
@@ -215,6 +468,14 @@ int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, i
   const int halo = (K - 1) * dilation;
   if (halo > 4096) return fail(LNG_E_ARG, "causal_conv: receptive field too large");
   hipStream_t s = as_stream(stream);
+  if (K == 4 && dilation == 3 && d % 8 == 0 && d <= 2048 && dtype == LNG_BF16) {
+    dim3 g43(static_cast<unsigned>(cdiv(T, C43_TT)), static_cast<unsigned>(B));
+    const int threads = static_cast<int>(cdiv(d / 8, 64) * 64);
+    hipLaunchKernelGGL(k_causal_conv_k4d3_bf16_reg, g43, dim3(threads), 0, s, static_cast<const bf16*>(mixed),
+                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), T, d, eps, residual,
+                       static_cast<bf16*>(out));
+    return check_launch("causal_conv_k4d3_bf16");
+  }
   if (K == 4 && dilation == 3 && d % 8 == 0 && (dtype == LNG_F32 || dtype == LNG_BF16)) {
     dim3 g43(static_cast<unsigned>(cdiv(T, C43_TT)), static_cast<unsigned>(B));
     if (dtype == LNG_F32)

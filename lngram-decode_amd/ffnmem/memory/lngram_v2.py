@@ -139,6 +139,18 @@ class DepthwiseCausalConv(nn.Module):
         return ops.causal_conv(values, self.norm.weight, self.conv.weight, self.dilation, self.norm.eps,
                                residual=True)
 
+    def takes_row_stats(self, dtype: torch.dtype) -> bool:
+        """Whether :meth:`forward_residual_stats` applies (bf16, kernel 4, dilation 3, no bias)."""
+        return (dtype == torch.bfloat16 and self.kernel_size == 4 and self.dilation == 3
+                and self.conv.bias is None and self.hidden_size % 8 == 0 and self.hidden_size <= 2048)
+
+    def forward_residual_stats(self, values: Tensor, rowsq: Tensor) -> Tensor:
+        """:meth:`forward_residual` with the RMSNorm row statistics computed by the producing
+        projection (``ops.linear_rowsq``)."""
+        self._check(values, None)
+        return ops.causal_conv_rowsq(values, rowsq, self.norm.weight, self.conv.weight, self.dilation,
+                                     self.norm.eps, residual=True)
+
 
 class _RouteNgramMemoryBase(nn.Module):
     """Hard route n-gram tables followed by a GQA route-memory readout (``lngram_v2.py:842-1010``)."""
@@ -321,9 +333,13 @@ class _RouteNgramMemoryBase(nn.Module):
     def _finish(self, head_output: Tensor, segment_ids: Optional[Tensor]) -> Tensor:
         """``mixed = W_o head``; ``mixed + short_conv(mixed)`` (``lngram_v2.py:1354-1359``)."""
         b, t, _, _ = head_output.shape
-        mixed = ops.linear(head_output.reshape(b, t, self.readout_inner_dim), self.readout_o_proj.weight)
         if segment_ids is not None:
             raise NotImplementedError("packed-segment causal conv is not part of the MI355X path")
+        flat = head_output.reshape(b, t, self.readout_inner_dim)
+        if self.short_conv.takes_row_stats(flat.dtype) and self.readout_inner_dim % 32 == 0:
+            mixed, rowsq = ops.linear_rowsq(flat, self.readout_o_proj.weight)
+            return self.short_conv.forward_residual_stats(mixed, rowsq)
+        mixed = ops.linear(flat, self.readout_o_proj.weight)
         return self.short_conv.forward_residual(mixed)
 
     # ------------------------------------------------------------------ fused path

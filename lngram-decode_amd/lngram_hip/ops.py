@@ -236,6 +236,42 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def linear_rowsq(x: torch.Tensor, w: torch.Tensor):
+    """bf16 ``x [..., K] . w[N, K]^T`` plus the partial row sums of squares of the bf16 output
+    (``[P, rows]`` fp32) that :func:`causal_conv_rowsq` consumes."""
+    dev = _dev(x, w)
+    k = x.shape[-1]
+    x2 = _c(x.reshape(-1, k))
+    wc = _c(w.to(x.dtype))
+    n = wc.shape[0]
+    if x.dtype != torch.bfloat16 or k % 32:
+        raise ValueError("linear_rowsq needs bf16 operands and K % 32 == 0")
+    p = int(lib().lng_linear_rowsq_partials(n))
+    out = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+    rowsq = torch.empty(p, x2.shape[0], dtype=torch.float32, device=dev)
+    rc = _timed("linear", dev, lambda: lib().lng_linear_rowsq(_ptr(x2), _ptr(wc), x2.shape[0], n, k, _ptr(out),
+                                                                _ptr(rowsq), _stream(dev)))
+    check(rc, "linear_rowsq")
+    return out, rowsq
+
+
+def causal_conv_rowsq(mixed: torch.Tensor, rowsq: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor,
+                      dilation: int, eps: float, residual: bool = True) -> torch.Tensor:
+    """:func:`causal_conv` (bf16, kernel 4, dilation 3) with row statistics from :func:`linear_rowsq`."""
+    dev = _dev(mixed, rowsq, norm_w, conv_w)
+    m = _c(mixed)
+    b, t, d = m.shape
+    cw = _c(conv_w.reshape(d, -1).to(m.dtype))
+    nw = _c(norm_w.to(m.dtype))
+    rs = _c(rowsq)
+    out = torch.empty_like(m)
+    rc = _timed("causal_conv", dev, lambda: lib().lng_causal_conv_rowsq(
+        _ptr(m), _ptr(rs), rs.shape[0], _ptr(nw), _ptr(cw), b, t, d, cw.shape[1], dilation, eps, int(bool(residual)),
+        _ptr(out), _stream(dev)))
+    check(rc, "causal_conv_rowsq")
+    return out
+
+
 def sink_attention(query: torch.Tensor, key: torch.Tensor, value: torch.Tensor, scale: float,
                    sink_logit: float) -> torch.Tensor:
     """query ``[B, T, KV, G, hd]``; key/value ``[B, T, KV, R, hd]`` (head dim contiguous, any other

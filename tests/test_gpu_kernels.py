@@ -102,7 +102,7 @@ def test_pack_route_codes_bit_exact(dev):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(300, 1024, 736), (37, 128, 32), (129, 2304, 724)])
+@pytest.mark.parametrize("shape", [(300, 1024, 736), (37, 128, 32), (129, 2304, 724), (4500, 1024, 736)])
 def test_router_logits_and_codes(dev, dtype, shape):
     m, k, n = shape
     g = torch.Generator().manual_seed(m + k)
@@ -137,7 +137,8 @@ def test_rmsnorm(dev, dtype):
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
-@pytest.mark.parametrize("mnk", [(513, 1024, 1024), (7, 33, 64), (130, 256, 256)])
+@pytest.mark.parametrize("mnk", [(513, 1024, 1024), (7, 33, 64), (130, 256, 256), (4100, 1000, 1024),
+                                 (8192, 1024, 96)])
 def test_linear(dev, dtype, tol, mnk):
     m, n, k = mnk
     x = torch.randn(m, k).to(dtype)
@@ -184,6 +185,34 @@ def test_causal_conv(dev, dtype, tol):
     got2 = ops.causal_conv(mixed.to(dev), p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev),
                            3, cfg.eps, residual=False).cpu()
     assert om.rel_err(got2, ref64 - mixed.double()) < tol
+
+
+@pytest.mark.parametrize("b,t,d,k", [(2, 300, 1024, 1024), (3, 37, 1000, 64), (1, 5, 8, 32)])
+def test_linear_rowsq_and_conv_from_row_stats(dev, b, t, d, k):
+    # o_proj with fused row statistics, then the conv that consumes them: the statistics are the
+    # sums of squares of the bf16 outputs, the conv matches the oracle with the reference rounding
+    g = torch.Generator().manual_seed(d + t)
+    x = torch.randn(b, t, k, generator=g).to(torch.bfloat16)
+    w = (torch.randn(d, k, generator=g) * 0.05).to(torch.bfloat16)
+    y, rowsq = ops.linear_rowsq(x.to(dev), w.to(dev))
+    y, rowsq = y.cpu(), rowsq.cpu()
+    assert om.rel_err(y, x.double() @ w.double().T) < 1e-2
+    assert rowsq.shape[1] == b * t
+    ss = y.double().pow(2).sum(-1).reshape(-1)
+    torch.testing.assert_close(rowsq.double().sum(0), ss, rtol=1e-5, atol=1e-6)
+    cfg = om.MemCfg(d, 4, 16, 4, 2, 64)
+    p = {"short_conv.norm.weight": 1 + 0.1 * torch.randn(d, generator=g),
+         "short_conv.conv.weight": 0.2 * torch.randn(d, 1, 4, generator=g)}
+    nw, cw = p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev)
+    got = ops.causal_conv_rowsq(y.to(dev), rowsq.to(dev), nw, cw, 3, cfg.eps).cpu()
+    want = y + om.causal_conv(p, cfg, y)
+    ref64 = y.double() + om.causal_conv(p, cfg, y.double())
+    assert om.rel_err(got, want) < 2e-2 and om.rel_err(got, ref64) < 2e-2
+    # same kernel inputs through the self-normalising conv: equal up to the summation order
+    other = ops.causal_conv(y.to(dev), nw, cw, 3, cfg.eps).cpu()
+    assert om.rel_err(got, other) < 8e-3
+    with pytest.raises(RuntimeError):
+        ops.causal_conv_rowsq(y.to(dev), rowsq.to(dev), nw, cw, 2, cfg.eps)
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
