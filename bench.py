@@ -67,6 +67,19 @@ def cpu_baseline(seconds: float) -> dict:
                       "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)"}
 
 
+def measured_traffic():
+    """HBM-side bytes per launch of the fused readout at this workload, from the committed
+    hardware-counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor a
+    plain copy of known size reads for the same counter); None if the summary is absent."""
+    f = ROOT / "profiles" / "readout_fused_sb_traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return int(json.loads(f.read_text())["traffic_bytes"])
+    except (ValueError, KeyError):
+        return None
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -74,6 +87,9 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB before warmup (known-size kernel that scales "
+                         "hardware byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the hot path is single-GPU; --gpus {args.gpus} is not supported)",
@@ -95,6 +111,15 @@ def main() -> None:
     h = workloads.make_hidden(w, seed=1, device=dev)
     h_norm = ops.rmsnorm(h, torch.ones(w.d_model, dtype=w.dtype, device=dev), w.norm_eps)
     torch.cuda.synchronize()
+    if args.copy_calibration > 0:
+        n = args.copy_calibration << 20
+        src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {n} bytes read, {n} bytes written")
+        del src, dst
 
     with torch.no_grad():
         for _ in range(args.warmup):
@@ -118,6 +143,7 @@ def main() -> None:
     achieved = fused_bytes / (fused_ms * 1e-3) / 1e9
     layer_bytes = w.tokens * w.algorithmic_bytes_per_token() + w.weight_bytes()
     layer_gbs = layer_bytes / (el / args.steps) / 1e9
+    traffic = measured_traffic()
     log(f"{ms:.3f} ms/step, {tok_s / 1e6:.2f} M tok/s, fused kernel {fused_ms * 1e3:.1f} us "
         f"({achieved:.0f} GB/s)")
 
@@ -138,7 +164,7 @@ def main() -> None:
                    "routes": w.routes, "mem_dim": w.mem_dim, "batch": w.batch, "seq_len": w.seq,
                    "table_params": w.routes * (256 + 4096) * w.mem_dim},
         "roofline": {"bound": "hbm", "kernel": "k_readout_fused", "achieved": achieved, "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes": fused_bytes, "avg_ms": fused_ms},
         "layer_hbm_frac": layer_gbs / HBM_PEAK_GBS,
         "layer_algorithmic_bytes": layer_bytes,
