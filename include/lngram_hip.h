@@ -159,6 +159,98 @@ int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int
                  float* workspace, float* s, void* stream);
 
 /* ---------------------------------------------------------------- K5: drafting */
+/* A token-routed drafter (the per-token algorithm of RefDrafter, drafting/cpu_drafter.py:76-289,
+ * and of drafter.cpp:152-545) over caller-owned device buffers.  Weights are the bundle arrays
+ * (export_drafter.py:22-31) plus three precomposed fp32 matrices of the draft readout:
+ *   qk  [q_heads*Dt, d] = softmax_scale * diag(mem_norm) Wk[h]^T W_q[qh] diag(q_norm)
+ *   qks [q_heads*Dt, N] = softmax_scale * diag(mem_norm) Wk[h]^T W_sq[qh]      (query_ssm)
+ *   ov  [d, q_heads*Dt] = W_o[:, qh] Wv[h] diag(mem_norm)        (qh = h*groups + g)
+ * State rows: token id, route codes [R] and SSM state [N] per position.  Rows 0 .. L-1 are
+ * the committed positions, *length holds L on the device; rows past the committed capacity
+ * hold hypothetical and tree positions.  A row spec names a row: v >= 0 absolute, v < 0 the
+ * committed row L + v (-1 = last committed), LNG_ROW_NONE = before the sequence start. */
+#define LNG_ROW_NONE (-2147483647 - 1)
+#define LNG_DR_MAX_D 2048
+#define LNG_DR_MAX_N 256
+#define LNG_DR_MAX_DT 256
+#define LNG_DR_MAX_QH 16
+#define LNG_DR_MAX_CH 8
+#define LNG_DR_MAX_P 16
+#define LNG_DR_MAX_K 8
+
+typedef struct lng_drafter {
+  int32_t d, V, R, bits, mem_dim, dt, n_orders, orders[4], maxn;
+  int32_t q_heads, kv_heads, head_dim, ssm_dim, router_ssm, query_ssm;
+  int32_t emb_dtype, table_dtype, router_dtype;
+  float router_eps, ssm_eps, draft_eps, mem_eps, sink_logit;
+  const void* emb;                      /* [V, d]                      */
+  const void* tables[4];                /* [R * 2^(bits*n), mem_dim]   */
+  const void* router;                   /* [R*bits, 2d (+N)]           */
+  const float* router_start;            /* [d] (fp32, like every vector below) */
+  const float* router_prev_norm;
+  const float* router_cur_norm;
+  const float* ssm_norm;                /* [d]     (ssm_dim > 0)       */
+  const float* ssm_w_in;                /* [N, d]                      */
+  const float* ssm_decay;               /* [N]                         */
+  const float* qk;
+  const float* qks;
+  const float* ov;
+  const float* out_norm;                /* [d]                         */
+  int64_t* tokens;                      /* [rows]                      */
+  uint8_t* codes;                       /* [rows, R]                   */
+  float* ssm;                           /* [rows, N]                   */
+  const int32_t* length;                /* device int32: L             */
+  int32_t rows;
+} lng_drafter;
+
+/* sizeof(lng_drafter), for bindings that mirror the struct. */
+size_t lng_drafter_size(void);
+
+/* Bytes of `work` for up to `max_positions` (<= LNG_DR_MAX_P) readout positions, top-k <=
+ * `max_k`, online counts over up to `max_pairs` committed pairs. */
+size_t lng_drafter_workspace_bytes(const lng_drafter* D, int32_t max_positions, int32_t max_k, int32_t max_pairs);
+
+/* Process n new positions: SSM step and router codes (cpu_drafter.py:147-164,
+ * drafter.cpp:396-425).  List form: rows[j] / prev[j] are row specs (prev = the previous
+ * position, LNG_ROW_NONE for the first token of a sequence), n <= LNG_DR_MAX_P; positions are
+ * processed in order, so a position may follow an earlier one of the same call.  Range form:
+ * absolute rows base .. base+n-1 in sequence, the first after prev0.  With
+ * codes_from_router == 0 the codes rows are left as written by the caller (commit with the
+ * target's codes). */
+int lng_drafter_advance(const lng_drafter* D, const int32_t* rows, const int32_t* prev, int32_t n,
+                        int codes_from_router, void* work, size_t work_bytes, void* stream);
+int lng_drafter_advance_range(const lng_drafter* D, int32_t base, int32_t prev0, int32_t n, int codes_from_router,
+                              void* work, size_t work_bytes, void* stream);
+
+/* Draft readout + full-vocabulary top-k for P positions (cpu_drafter.py:208-270,
+ * drafter.cpp:477-556).  windows [P, maxn] (host) are row specs of each position's n-gram
+ * window, oldest first, the position itself last.  ids/scores [P, k] (device) receive the
+ * top-k by (logit desc, id asc); with online != 0 the logits are mixed with code-keyed online
+ * counts over the committed pairs (drafters.py:117-142) and ranked by, and reported as, the
+ * log of the mixed probability.  Child j of the call (child_rows/child_parent/child_rank, host,
+ * n_children <= 64) receives token ids[parent][rank] (top-1 if absent) in D->tokens.
+ * logits [P, V] (device) may be null.  `counts` [P, V] int32 (device) must be zero before the
+ * first call; every call leaves it zero. */
+int lng_drafter_readout(const lng_drafter* D, const int32_t* windows, int32_t P, int32_t k, int online, float kappa,
+                        const int32_t* child_rows, const int32_t* child_parent, const int32_t* child_rank,
+                        int32_t n_children, void* work, size_t work_bytes, int32_t* counts, int64_t* ids,
+                        float* scores, float* logits, void* stream);
+
+/* Route tokens [P, R, Dt] (table dtype) of the n-grams ending at each window's last position
+ * (tree_route_tokens, drafting/tree.py:130-136; window_route_tokens, drafters.py:110-114). */
+int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, void* out, void* stream);
+
+/* One draft-tree step (draft_tree, drafting/tree.py:243-257, batched by depth): node 0 is the
+ * last committed token, node i >= 1 lives at absolute row node_row0 + i; parent/rank (host, n
+ * <= 64) as TreeSpec (tree.py:37-51).  Every parent's readout of one depth runs together;
+ * node i receives the rank[i]-th candidate of its parent (top-1 if absent).  Then every node
+ * gets its codes and, if route_tokens is non-null, the verification gather [n, R, Dt]
+ * (tree_ngram_codes + tree_route_tokens, tree.py:114-136).  The root's token is copied to row
+ * node_row0, so rows node_row0 .. node_row0+n-1 hold every node's token (tree_accept input). */
+int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n, int32_t node_row0,
+                     int online, float kappa, void* work, size_t work_bytes, int32_t* counts, void* route_tokens,
+                     void* stream);
+
 /* Tree acceptance (drafting/tree.py:205-220): from the root take the first child
  * (index order) whose token equals argmax[cur]; repeat.  path[n] receives the
  * node path (root first), *path_len its length, new_tokens[n] the accepted

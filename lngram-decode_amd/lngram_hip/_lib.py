@@ -26,6 +26,25 @@ _int = ctypes.c_int
 _P64 = ctypes.POINTER(ctypes.c_int64)
 _P32 = ctypes.POINTER(ctypes.c_int32)
 
+ROW_NONE = -2147483648  # LNG_ROW_NONE
+
+
+class Drafter(ctypes.Structure):
+    """``lng_drafter`` (include/lngram_hip.h): shapes, device weight pointers and state rows."""
+
+    _fields_ = [(n, ctypes.c_int32) for n in ("d", "V", "R", "bits", "mem_dim", "dt", "n_orders")] + [
+        ("orders", ctypes.c_int32 * 4), ("maxn", ctypes.c_int32)] + [
+        (n, ctypes.c_int32) for n in ("q_heads", "kv_heads", "head_dim", "ssm_dim", "router_ssm", "query_ssm",
+                                      "emb_dtype", "table_dtype", "router_dtype")] + [
+        (n, ctypes.c_float) for n in ("router_eps", "ssm_eps", "draft_eps", "mem_eps", "sink_logit")] + [
+        ("emb", ctypes.c_void_p), ("tables", ctypes.c_void_p * 4), ("router", ctypes.c_void_p)] + [
+        (n, ctypes.c_void_p) for n in ("router_start", "router_prev_norm", "router_cur_norm", "ssm_norm", "ssm_w_in",
+                                       "ssm_decay", "qk", "qks", "ov", "out_norm", "tokens", "codes", "ssm",
+                                       "length")] + [("rows", ctypes.c_int32)]
+
+
+_PD = ctypes.POINTER(Drafter)
+
 # name -> (restype, argtypes); must cover every function declared in the header
 SIGNATURES = {
     "lng_abi_version": (_int, []),
@@ -50,6 +69,14 @@ SIGNATURES = {
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p, _p]),
     "lng_tree_accept": (_int, [_p, _p, _p, _i32, _p, _p, _p, _p]),
+    "lng_drafter_size": (ctypes.c_size_t, []),
+    "lng_drafter_workspace_bytes": (ctypes.c_size_t, [_PD, _i32, _i32, _i32]),
+    "lng_drafter_advance": (_int, [_PD, _P32, _P32, _i32, _int, _p, ctypes.c_size_t, _p]),
+    "lng_drafter_advance_range": (_int, [_PD, _i32, _i32, _i32, _int, _p, ctypes.c_size_t, _p]),
+    "lng_drafter_readout": (_int, [_PD, _P32, _i32, _i32, _int, _f, _P32, _P32, _P32, _i32, _p, ctypes.c_size_t,
+                                   _p, _p, _p, _p, _p]),
+    "lng_drafter_gather": (_int, [_PD, _P32, _i32, _p, _p]),
+    "lng_drafter_tree": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, _p, ctypes.c_size_t, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

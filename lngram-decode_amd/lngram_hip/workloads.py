@@ -103,3 +103,77 @@ def make_tokens(w: MemoryWorkload, seed: int = 2, device: str | torch.device = "
     """Token ids uniform over the vocabulary ``[B, T]``."""
     g = torch.Generator().manual_seed(seed)
     return torch.randint(0, w.vocab, (w.batch, w.seq), generator=g).to(device)
+
+
+# ----------------------------------------------------------------------------- drafter (decode) workloads
+@dataclass(frozen=True)
+class DraftWorkload:
+    """Shape of a token-routed drafter (bundle ``config`` of ``drafting/export_drafter.py``)."""
+
+    name: str
+    d_model: int
+    vocab: int
+    routes: int
+    mem_dim: int
+    kv_heads: int
+    head_dim: int
+    q_heads: int
+    ssm_dim: int = 0
+    context: int = 2048
+    dtype: torch.dtype = torch.bfloat16
+    eps: float = 1e-5
+
+    def config(self) -> dict:
+        import math
+
+        ssm = self.ssm_dim > 0
+        return {"kind": "sd_c" if ssm else "sd_b", "router_kind": "embed2_ssm" if ssm else "embed2",
+                "d_model": self.d_model, "vocab": self.vocab, "routes": self.routes, "bits": 4, "ngrams": [2, 3],
+                "mem_dim": self.mem_dim, "kv_heads": self.kv_heads, "head_dim": self.head_dim,
+                "q_heads": self.q_heads, "groups": self.q_heads // self.kv_heads,
+                "route_token_dim": 2 * self.mem_dim, "ssm_dim": self.ssm_dim, "query_ssm": ssm,
+                "norm_eps": self.eps, "ssm_eps": self.eps, "router_eps": self.eps, "draft_eps": self.eps,
+                "mem_eps": self.eps, "softmax_scale": self.head_dim ** -0.5, "sink_logit": math.log(self.routes),
+                "sketch_k": 0, "shortlist_cap": 0, "table_dtype": "bf16" if self.dtype == torch.bfloat16 else "fp32",
+                "layer": 0}
+
+    def table_params(self) -> int:
+        return self.routes * (16 ** 2 + 16 ** 3) * self.mem_dim
+
+
+SDB_DRAFT = DraftWorkload("sdb drafter d1024 V32768 R182 bf16", 1024, 32768, 182, 128, 4, 64, 4)
+SDC_DRAFT = DraftWorkload("sdc drafter d1024 V32768 R181 N256 bf16", 1024, 32768, 181, 128, 4, 64, 4, ssm_dim=256)
+TINY_DRAFT = DraftWorkload("tiny drafter d64 V512 R6", 64, 512, 6, 16, 2, 16, 4, context=96)
+TINY_DRAFT_SSM = DraftWorkload("tiny drafter d64 V512 R5 N8", 64, 512, 5, 16, 2, 16, 4, ssm_dim=8, context=96)
+
+
+def build_draft_bundle(w: DraftWorkload, seed: int = 0) -> tuple[dict, dict]:
+    """(config, tensors) of a synthetic drafter on the CPU: every weight ~N(0, 0.02) drawn in fp32
+    and stored in ``w.dtype`` (the SSM decay ~U[0.9, 0.999] stays fp32), norm weights ones."""
+    g = torch.Generator().manual_seed(seed)
+    d, r, n = w.d_model, w.routes, w.ssm_dim
+    kh, inner, dt = w.kv_heads * w.head_dim, w.q_heads * w.head_dim, 2 * w.mem_dim
+    feat = 2 * d + (n if n else 0)
+
+    def rnd(*shape):
+        return (torch.randn(*shape, generator=g) * 0.02).to(w.dtype)
+
+    def ones(k):
+        return torch.ones(k, dtype=w.dtype)
+
+    t = {"embedding": rnd(w.vocab, d), "table_2": rnd(r * 16 ** 2, w.mem_dim), "table_3": rnd(r * 16 ** 3, w.mem_dim),
+         "mem_norm": ones(dt), "kv_proj": rnd(2 * kh, dt), "router": rnd(r * 4, feat),
+         "router_prev_norm": ones(d), "router_cur_norm": ones(d), "router_start": rnd(d),
+         "q_norm": ones(d), "w_q": rnd(inner, d), "w_o": rnd(d, inner), "out_norm": ones(d)}
+    if n:
+        t["ssm_norm"] = ones(d)
+        t["ssm_w_in"] = rnd(n, d)
+        t["ssm_decay"] = 0.9 + 0.099 * torch.rand(n, generator=g)
+        t["w_sq"] = rnd(inner, n)
+    return w.config(), t
+
+
+def make_context(w: DraftWorkload, seed: int = 0) -> list:
+    """Context token ids ~U[0, vocab) (batch 1)."""
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(0, w.vocab, (w.context,), generator=g).tolist()

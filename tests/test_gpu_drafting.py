@@ -1,0 +1,199 @@
+"""Parity of the GPU drafter (``drafting.gpu_drafter.GpuDrafter``) with the drafting oracle (GPU).
+
+Route codes are compared bit-exactly outside the near-tie band |router logit| < 2e-5 (the oracle's
+fp64 logits decide which entries are ties); readouts are compared with identical committed codes
+(``commit(tokens, codes=...)``), so a tie cannot leak into the windows.  Logits: absolute error
+<= 1e-4 (the reference's C++-vs-PyTorch drafter tolerance, ``tests/test_live_drafter.py:105-121``);
+draft tokens, top-k ids and tree node tokens: equal.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from drafting import tree as dtree
+from drafting.gpu_drafter import GpuDrafter
+from lngram_hip import workloads as wl
+from oracle import drafting as od
+
+pytestmark = pytest.mark.gpu
+
+TAU = 2e-5
+SPEC16 = dtree.tree16()
+
+
+def _bundle(kind: str, seed: int = 5):
+    w = {"sdb": wl.TINY_DRAFT, "sdc": wl.TINY_DRAFT_SSM}[kind]
+    cfg, t = wl.build_draft_bundle(w, seed=seed)
+    g = torch.Generator().manual_seed(9)
+    for k in ("router_prev_norm", "router_cur_norm", "q_norm", "out_norm", "mem_norm"):
+        t[k] = (1 + 0.2 * torch.randn(t[k].shape, generator=g)).to(t[k].dtype)
+    return cfg, t
+
+
+def _oracle_codes_and_ties(o: od.DrafterOracle, toks: list):
+    """Oracle codes of a committed sequence and a mask [T, R] of routes with a near-tie bit."""
+    o.reset()
+    ties = []
+    cur = o._cursor()
+    for tok in toks:
+        s = None
+        if o.has_ssm:
+            e = o.E[tok]
+            u = o.ssm_w_in @ od._rms(e, o.ssm_norm, o.cfg["ssm_eps"])
+            s = o.ssm_a * (cur.s if cur.s is not None else torch.zeros_like(u)) + (1 - o.ssm_a) * u
+        lg = o.router_logits(cur.tok if cur.t >= 0 else -1, tok, s)
+        ties.append((lg.abs() < TAU).view(o.R, o.bits).any(-1).numpy())
+        cur = o._advance(cur, tok)
+    o.commit(toks)
+    return o.committed_codes(), np.stack(ties)
+
+
+@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+def test_commit_codes_match_oracle(dev, kind):
+    cfg, t = _bundle(kind)
+    toks = torch.randint(0, cfg["vocab"], (70,), generator=torch.Generator().manual_seed(1)).tolist()
+    o = od.DrafterOracle(cfg, t)
+    want, ties = _oracle_codes_and_ties(o, toks)
+    g = GpuDrafter((cfg, t), device=dev, max_len=128)
+    g.commit(toks[:33])
+    g.commit(toks[33:])                      # in two pieces: the second continues the first
+    got = g.committed_codes()
+    assert got.shape == want.shape
+    assert (got[~ties] == want[~ties]).all()
+    if kind == "sdc":                         # SSM states follow the recurrence
+        s_want = torch.stack(o._ssm).numpy()
+        s_got = g.ssm_d[:len(toks), :g.N].cpu().numpy()
+        np.testing.assert_allclose(s_got, s_want, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+def test_trace_logits_match_oracle(dev, kind):
+    cfg, t = _bundle(kind)
+    toks = torch.randint(0, cfg["vocab"], (37,), generator=torch.Generator().manual_seed(2)).tolist()
+    o = od.DrafterOracle(cfg, t)
+    codes, lg = o.trace(toks)
+    g = GpuDrafter((cfg, t), device=dev, max_len=64)
+    c_got, ids, l_got = g.trace(toks, codes=codes)
+    np.testing.assert_array_equal(c_got, codes)
+    assert ids.shape == (37, cfg["vocab"]) and (ids[0] == np.arange(cfg["vocab"])).all()
+    assert np.abs(l_got - lg).max() < 1e-4
+    assert (l_got.argmax(1) == lg.argmax(1)).all()
+    assert g.length == 0                     # trace leaves the committed state alone
+
+
+@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+@pytest.mark.parametrize("online", [False, True])
+def test_draft_matches_oracle(dev, kind, online):
+    cfg, t = _bundle(kind)
+    gen = torch.Generator().manual_seed(3)
+    pat = torch.randint(0, cfg["vocab"], (6,), generator=gen).tolist()
+    toks = pat * 5 + torch.randint(0, cfg["vocab"], (11,), generator=gen).tolist() + pat[:3]
+    o = od.DrafterOracle(cfg, t, online=online)
+    codes, _ = _oracle_codes_and_ties(od.DrafterOracle(cfg, t), toks)
+    o.reset()
+    o.commit(toks, codes=codes)
+    g = GpuDrafter((cfg, t), device=dev, max_len=96, online=online)
+    g.commit(toks, codes=codes)
+    for hyp, gamma, k, last in (((), 4, 3, False), (tuple(pat[3:5]), 3, 4, True), ((), 1, 1, False)):
+        want = o.draft(gamma, hyp=hyp, topk=k, last_codes=last)
+        got = g.draft(gamma, hyp=hyp, topk=k, last_codes=last)
+        assert got.tokens == want.tokens, (hyp, gamma)
+        np.testing.assert_array_equal(got.topk_ids, want.topk_ids)
+        np.testing.assert_allclose(got.topk_logits, want.topk_logits, rtol=0, atol=1e-4)
+        np.testing.assert_array_equal(got.codes, want.codes)
+    assert g.length == len(toks)
+    # rollback: truncate then draft equals a drafter that never saw the tail
+    g.truncate(20)
+    o2 = od.DrafterOracle(cfg, t, online=online)
+    o2.commit(toks[:20], codes=codes[:20])
+    assert g.draft(3).tokens == o2.draft(3).tokens
+
+
+@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+@pytest.mark.parametrize("online", [False, True])
+def test_draft_tree_and_verify_gather_match_oracle(dev, kind, online):
+    cfg, t = _bundle(kind)
+    toks = torch.randint(0, cfg["vocab"], (50,), generator=torch.Generator().manual_seed(4)).tolist()
+    codes, _ = _oracle_codes_and_ties(od.DrafterOracle(cfg, t), toks)
+    o = od.DrafterOracle(cfg, t, online=online)
+    o.commit(toks, codes=codes)
+    g = GpuDrafter((cfg, t), device=dev, max_len=64, online=online)
+    g.commit(toks, codes=codes)
+    for spec in (SPEC16, dtree.default_tree(), dtree.chain_tree(5)):
+        ospec = od.TreeSpec(spec.parent, spec.rank)
+        want = od.draft_tree(o, ospec)
+        assert g.draft_tree(spec) == want
+        # node codes (drafter's router along each node's path) and the verification gather
+        node_tok, rt = g.tree_step(spec, route_tokens=True)
+        assert node_tok.cpu().tolist() == want
+        node_codes = np.zeros((spec.n, cfg["routes"]), np.int64)
+        node_codes[0] = codes[-1]
+        for i in range(1, spec.n):
+            path = od.tree_path(spec.parent, i)
+            c = o.draft(1, hyp=[want[a] for a in path[1:]], last_codes=True).codes
+            node_codes[i] = c[len(path) - 2]
+        got_codes = g.codes_d[g.tree_row0 + 1: g.tree_row0 + spec.n].cpu().numpy()
+        np.testing.assert_array_equal(got_codes, node_codes[1:])
+        hist = codes[None, -3:-1].astype(np.int64)
+        nodes = node_codes[None].copy()
+        ctx, ok = od.tree_ngram_codes(spec.parent, nodes, hist, 2)
+        tables = {n: t[f"table_{n}"] for n in cfg["ngrams"]}
+        rt_want = od.tree_route_tokens(tables, cfg["ngrams"], cfg["bits"], ctx, ok)[0]
+        torch.testing.assert_close(rt.cpu(), rt_want.to(rt.dtype), rtol=0, atol=0)
+
+
+def test_tree_accept_on_device_known_answers(dev):
+    parent = (-1, 0, 1, 0, 3, 1)
+    toks = [7, 1, 2, 3, 4, 5]
+    for am, path, new in (([3, 9, 9, 4, 8, 9], [0, 3, 4], [3, 4, 8]), ([1, 5, 9, 9, 9, 6], [0, 1, 5], [1, 5, 6]),
+                          ([9] * 6, [0], [9])):
+        assert dtree.tree_accept(parent, toks, torch.tensor(am, device=dev)) == (path, new)
+
+
+def test_api_errors(dev):
+    cfg, t = _bundle("sdb")
+    g = GpuDrafter((cfg, t), device=dev, max_len=16)
+    with pytest.raises(ValueError):
+        g.draft(1)
+    with pytest.raises(ValueError):
+        g.commit([cfg["vocab"]])
+    g.commit([1, 2, 3])
+    with pytest.raises(ValueError):
+        g.truncate(4)
+    with pytest.raises(ValueError):
+        g.commit([1, 2], codes=np.full((2, cfg["routes"]), 16))
+    with pytest.raises(ValueError):
+        g.commit(list(range(14)))
+    assert g.length == 3
+
+
+def test_sdb_shape_tree_step_matches_oracle(dev):
+    # SD-B drafter shape: d 1024, V 32768, R 182, bf16 weights, 2048-token context, 16-node tree
+    w = wl.SDB_DRAFT
+    cfg, t = wl.build_draft_bundle(w, seed=0)
+    ctx = wl.make_context(w, seed=0)
+    o = od.DrafterOracle(cfg, t)
+    g = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8)
+    g.commit(ctx)
+    got = g.committed_codes()
+    # the oracle's own codes for the last 64 positions (the windows the tree reads), with ties
+    tail = 64
+    o.commit(ctx[: -tail], codes=got[: -tail])
+    cur = o._cursor()
+    n_tie = n_bad = 0
+    for i, tok in enumerate(ctx[-tail:]):
+        lg = o.router_logits(cur.tok, tok, None)
+        tie = (lg.abs() < TAU).view(o.R, o.bits).any(-1).numpy()
+        cur = o._advance(cur, tok)
+        want = cur.hist[-1]
+        n_tie += int(tie.sum())
+        n_bad += int((got[len(ctx) - tail + i] != want)[~tie].sum())
+    assert n_bad == 0
+    o.reset()
+    o.commit(ctx, codes=got)
+    spec = od.TreeSpec(SPEC16.parent, SPEC16.rank)
+    want = od.draft_tree(o, spec)
+    assert g.draft_tree(SPEC16) == want
