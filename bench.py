@@ -67,6 +67,63 @@ def cpu_baseline(seconds: float) -> dict:
                       "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)"}
 
 
+def draft_step(dev, iters: int, warmup: int) -> dict:
+    """SD-B decode draft step on one GPU: the 2048-token context is committed, then one step =
+    16-node draft tree (10 parent readouts in 4 depths, top-3, online counts over the context) +
+    codes of every node + verification gather [16, 182, 256] + greedy acceptance against a
+    synthetic verifier argmax, ending when the accepted path and bonus token are on the host."""
+    import numpy as np
+    import torch
+
+    from drafting import tree as dtree
+    from drafting.gpu_drafter import GpuDrafter
+    from lngram_hip import ops, workloads
+
+    w = workloads.SDB_DRAFT
+    cfg, t = workloads.build_draft_bundle(w, seed=0)
+    g = GpuDrafter((cfg, t), device=dev, max_len=w.context + 64, online=True)
+    g.commit(workloads.make_context(w, seed=0))
+    spec = dtree.tree16()
+    n = spec.n
+    first_child = [next((c for c in range(n) if spec.parent[c] == i), i) for i in range(n)]
+    fc = torch.tensor(first_child, dtype=torch.long, device=dev)
+    parent = torch.tensor(spec.parent, dtype=torch.int32, device=dev)
+    host = torch.empty(2 * n + 1, dtype=torch.int64).pin_memory()
+    out = {}
+    for case in ("all_accept", "reject_at_root"):
+        wall, gpu = [], []
+        for i in range(warmup + iters):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            e0.record()
+            node_tok, rt = g.tree_step(spec, route_tokens=True)
+            if case == "all_accept":
+                argmax = node_tok[fc]                               # the verifier agrees with every top-1 child
+            else:
+                argmax = torch.full((n,), -1, dtype=torch.int64, device=dev)  # matches no drafted token
+            path, plen, new = ops.tree_accept(parent, node_tok, argmax)
+            e1.record()
+            host[:n].copy_(new, non_blocking=True)
+            host[n:2 * n].copy_(path.to(torch.int64), non_blocking=True)
+            host[2 * n:].copy_(plen.to(torch.int64), non_blocking=True)
+            torch.cuda.current_stream(dev).synchronize()
+            el = time.perf_counter() - t0
+            if i >= warmup:
+                wall.append(el * 1e6)
+                gpu.append(e0.elapsed_time(e1) * 1e3)
+        k = int(host[2 * n])
+        out[case] = {"median_us": float(np.median(wall)), "p99_us": float(np.percentile(wall, 99)),
+                     "gpu_median_us": float(np.median(gpu)), "accepted": k - 1}
+    e_bytes = w.vocab * w.d_model * 2
+    alg = 4 * e_bytes + n * w.routes * 2 * w.mem_dim * 2 * 2 + 10 * w.routes * 2 * w.mem_dim * 2
+    med = out["all_accept"]["gpu_median_us"]
+    return {"workload": "SD-B decode draft step: d1024 V32768 R182 bf16, context 2048, gamma 4, 16-node tree, "
+                        "online counts, verify-gather [16,182,256], greedy accept",
+            "unit": "us", "iters": iters, **out, "target_us": 50.0,
+            "algorithmic_bytes": alg, "achieved_GBs": alg / (med * 1e-6) / 1e9}
+
+
 def measured_traffic():
     """HBM-side bytes per launch of the fused readout at this workload, from the committed
     hardware-counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor a
@@ -87,6 +144,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--draft-iters", type=int, default=200)
+    ap.add_argument("--no-draft", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before warmup (known-size kernel that scales "
                          "hardware byte counters)")
@@ -169,6 +228,9 @@ def main() -> None:
         "layer_hbm_frac": layer_gbs / HBM_PEAK_GBS,
         "layer_algorithmic_bytes": layer_bytes,
     }
+    if not args.no_draft:
+        log("draft step")
+        result["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

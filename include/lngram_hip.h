@@ -201,6 +201,27 @@ typedef struct lng_drafter {
   float* ssm;                           /* [rows, N]                   */
   const int32_t* length;                /* device int32: L             */
   int32_t rows;
+  /* Per-token tables of the token-only drafter (router_ssm == query_ssm == 0).  When every one
+   * is non-null the readout runs in two launches per call:
+   *   lut_prev  [V, R*bits] fp32   router[:, :d]   (RMSNorm(E[v]) * prev_norm)
+   *   lut_cur   [V, R*bits] fp32   router[:, d:2d] (RMSNorm(E[v]) * cur_norm)
+   *   lut_start [R*bits]    fp32   router[:, :d]   (RMSNorm(start) * prev_norm)
+   *   lut_qk    [V, q_heads*Dt] fp32   qk (E[v] * rsqrt(mean(E[v]^2) + draft_eps))
+   *   lut_out   [V, q_heads*hd] fp32   E[v] diag(out_norm) W_o
+   *   gram_out  [q_heads*hd, q_heads*hd] fp32   W_o^T W_o
+   *   wv_t      [kv_heads, Dt, hd] (wv_dtype)   Wv[h]^T, the value rows of kv_proj transposed
+   *   mem_norm  [Dt] fp32   readout_memory_norm weight
+   *   sync      int32 [64], zero before the first call; every call leaves it zero. */
+  const float* lut_prev;
+  const float* lut_cur;
+  const float* lut_start;
+  const float* lut_qk;
+  const float* lut_out;
+  const float* gram_out;
+  const void* wv_t;
+  const float* mem_norm;
+  int32_t wv_dtype;
+  int32_t* sync;
 } lng_drafter;
 
 /* sizeof(lng_drafter), for bindings that mirror the struct. */

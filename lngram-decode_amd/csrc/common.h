@@ -46,15 +46,30 @@ template <typename T>
 __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
 
 // ------------------------------------------------------------------ wave reductions (wave64)
+// Inclusive scans inside each 16-lane row with DPP row_shr:1,2,4,8 (VALU data movement, no LDS
+// round trip), then the four row totals (lanes 15, 31, 47, 63) read as scalars.  Every lane
+// receives the result.  Call from converged code: inactive lanes would contribute stale values.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row_shr(float x, float identity) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, identity),
+                                                                __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_f(float x, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
+}
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_row_shr<0x111>(v, 0.f);
+  v += dpp_row_shr<0x112>(v, 0.f);
+  v += dpp_row_shr<0x114>(v, 0.f);
+  v += dpp_row_shr<0x118>(v, 0.f);
+  return (lane_f(v, 15) + lane_f(v, 31)) + (lane_f(v, 47) + lane_f(v, 63));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
+  v = fmaxf(v, dpp_row_shr<0x111>(v, -INFINITY));
+  v = fmaxf(v, dpp_row_shr<0x112>(v, -INFINITY));
+  v = fmaxf(v, dpp_row_shr<0x114>(v, -INFINITY));
+  v = fmaxf(v, dpp_row_shr<0x118>(v, -INFINITY));
+  return fmaxf(fmaxf(lane_f(v, 15), lane_f(v, 31)), fmaxf(lane_f(v, 47), lane_f(v, 63)));
 }
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }

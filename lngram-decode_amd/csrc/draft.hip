@@ -732,12 +732,804 @@ __global__ __launch_bounds__(256) void k_draft_gather(lng_drafter D, DrWin W, TT
   }
 }
 
+// ------------------------------------------------------------------ fast path
+// Token-only drafters (no SSM input): router halves, the query-key product and the output
+// projection are per-token lookup tables (lng_drafter.lut_*), so one depth of a draft is two
+// launches: k_fast_attend (codes of new positions, attention partials per route chunk, online
+// matches; the last block of each position merges them into r * o) and k_fast_logits (vocabulary
+// scores against lut_out; the last block selects the top-k and writes the children's tokens).
+constexpr int FA_RC = 16;     // routes per attention block
+constexpr int FA_TB = 64;     // pairs per online block
+constexpr int FL_VB = 128;    // vocabulary rows per logits block
+constexpr int FL_I = 256;     // q_heads * head_dim handled by the fast logits kernel
+
+struct FastLevel {
+  int32_t P;
+  int32_t slot[DR_MAXP][DR_MAXN];  // window row specs, oldest first, last = the position itself
+  int32_t prev[DR_MAXP];           // row spec of the preceding position (router's previous token)
+  int32_t fresh[DR_MAXP];          // != 0: the position's codes are computed (and stored) here
+};
+
+__device__ __forceinline__ int dr_lut_code(const lng_drafter& D, int64_t ptok, int64_t tok, int r) {
+  if (!dr_tok_ok(D, tok)) return 0;
+  const int RB = D.R * D.bits;
+  const float* a = dr_tok_ok(D, ptok) ? D.lut_prev + ptok * RB : D.lut_start;
+  const float* b = D.lut_cur + tok * RB;
+  int code = 0;
+  for (int i = 0; i < D.bits; ++i) code |= ((a[r * D.bits + i] + b[r * D.bits + i]) > 0.f ? 1 : 0) << i;
+  return code;
+}
+
+// Block-wide "am I the last block of this group" after every block wrote its results.  The
+// barrier drains the block's stores to L2; thread 0 releases them at agent scope (L2 write-back)
+// and counts the block in; the last block resets the counter and acquires the other blocks'
+// results (every wave invalidates its caches).
+__device__ __forceinline__ bool dr_last_block(int32_t* counter, int32_t total, int* flag) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = old == total - 1;
+    if (*flag) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (*flag == 0) return false;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return true;
+}
+
+// Sum over each 16-lane row (DPP row_shr:1,2,4,8 inclusive scan): valid in lanes 15, 31, 47, 63.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_row_shr<0x111>(v, 0.f);
+  v += dpp_row_shr<0x112>(v, 0.f);
+  v += dpp_row_shr<0x114>(v, 0.f);
+  v += dpp_row_shr<0x118>(v, 0.f);
+  return v;
+}
+
+// sync[] layout (int32, zero between calls)
+constexpr int SY_ATT = 0;    // [16] attention-launch block counters, per position
+constexpr int SY_LOG = 16;   // logits-launch block counter
+constexpr int SY_TOT = 32;   // [16] online weight totals, per position
+constexpr int SY_NC = 48;    // [16] online candidates appended, per position
+
+constexpr int FS_CAND = 8192;      // online candidates per position (tokens with counts)
+
+// Per-lane top-K list, sorted by (score desc, id asc); empty slots hold (-inf, INT_MAX).
+struct TopK {
+  float v[DR_MAXK];
+  int i[DR_MAXK];
+  __device__ __forceinline__ void clear() {
+#pragma unroll
+    for (int k = 0; k < DR_MAXK; ++k) v[k] = -INFINITY, i[k] = INT_MAX;
+  }
+  __device__ __forceinline__ void insert(float x, int id, int K) {
+#pragma unroll
+    for (int k = 0; k < DR_MAXK; ++k) {
+      if (k < K && (x > v[k] || (x == v[k] && id < i[k]))) {
+        const float tv = v[k];
+        const int ti = i[k];
+        v[k] = x, i[k] = id;
+        x = tv, id = ti;
+      }
+    }
+  }
+  __device__ __forceinline__ void pop() {
+#pragma unroll
+    for (int k = 0; k + 1 < DR_MAXK; ++k) v[k] = v[k + 1], i[k] = i[k + 1];
+    v[DR_MAXK - 1] = -INFINITY, i[DR_MAXK - 1] = INT_MAX;
+  }
+};
+
+// K rounds of wave argmax over the lanes' lists -> sel_v/sel_i (lane 0 holds them all).
+__device__ __forceinline__ void wave_select(TopK& t, int K, float* sel_v, int* sel_i) {
+  for (int k = 0; k < K; ++k) {
+    float bv = t.v[0];
+    int bi = t.i[0];
+    for (int off = 32; off > 0; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
+    }
+    sel_v[k] = bi == INT_MAX ? -INFINITY : bv;
+    sel_i[k] = bi == INT_MAX ? -1 : bi;
+    if (t.i[0] == bi && bi != INT_MAX) t.pop();
+  }
+}
+
+// Code of route r for (previous token, token) from the router tables (bits <= 4: one 16-byte load
+// per table row).
+__device__ __forceinline__ int dr_lut_code4(const lng_drafter& D, int64_t ptok, int64_t tok, int r) {
+  if (!dr_tok_ok(D, tok)) return 0;
+  const int RB = D.R * D.bits;
+  const float* a = dr_tok_ok(D, ptok) ? D.lut_prev + ptok * RB : D.lut_start;
+  const float* b = D.lut_cur + tok * RB;
+  if (D.bits == 4) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(a + 4 * r);
+    const f32x4 y = *reinterpret_cast<const f32x4*>(b + 4 * r);
+    return ((x[0] + y[0]) > 0.f ? 1 : 0) | ((x[1] + y[1]) > 0.f ? 2 : 0) | ((x[2] + y[2]) > 0.f ? 4 : 0) |
+           ((x[3] + y[3]) > 0.f ? 8 : 0);
+  }
+  return dr_lut_code(D, ptok, tok, r);
+}
+
+// grid (nch + nob, P): blocks [0, nch) attention over route chunks, [nch, nch + nob) online matches.
+// Attention block c of position j writes the record part[j, c] = (o_c[QH*hd], y_c[QH][I], m_c[QH],
+// l_c[QH]): o_c = Wv (mem_norm . U_c) per query head, y_c[qh] = (W_o^T W_o)[:, qh block] o_c[qh]
+// (both linear in U_c, so the last block merges them with the softmax weights).  Online blocks add
+// their pairs' match counts to counts[j, next token] and to the position's total.  The last block
+// of position j writes ro[j] = r_j * o_j, r_j = rsqrt(|W_o o_j|^2 / d + eps).
+constexpr int FA_MAXCH = 16;  // attention chunks per position (R <= 256)
+constexpr int FA_DW = (((FA_TB + DR_MAXN) * 256 + 8) / 4);
+
+__device__ __forceinline__ int fa_rec(int QH, int hd, int I) { return QH * hd + QH * I + 2 * QH; }
+
+__global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F, int32_t nch, int32_t nob,
+                                                     int32_t online, float* __restrict__ part,
+                                                     int32_t* __restrict__ counts, float* __restrict__ ro) {
+  __shared__ __attribute__((aligned(16))) float xs[FA_RC][LNG_DR_MAX_DT];
+  __shared__ __attribute__((aligned(16))) float qs[LNG_DR_MAX_QH * LNG_DR_MAX_DT];
+  __shared__ __attribute__((aligned(16))) float us[LNG_DR_MAX_QH * LNG_DR_MAX_DT];
+  __shared__ float sx[FA_RC];
+  __shared__ float sc[LNG_DR_MAX_QH][FA_RC];
+  __shared__ float pr[LNG_DR_MAX_QH][FA_RC];
+  __shared__ float ml[LNG_DR_MAX_QH][2];
+  __shared__ int64_t rowsh[FA_RC][DR_MAXN];
+  __shared__ uint8_t wc[DR_MAXN][256];      // window codes of the position, per route
+  __shared__ int32_t qaddr[4][256];
+  __shared__ uint32_t cw[FA_DW];           // staged committed codes (bytes)
+  __shared__ int32_t red[4][FA_TB];
+  __shared__ int32_t srow[DR_MAXN];
+  __shared__ int64_t toks[2];
+  __shared__ int last_flag;
+  __shared__ float redf[4];
+  const int j = blockIdx.y;
+  // descriptor fields used in loops, read once (kernel-argument loads otherwise repeat per use)
+  const int bits = D.bits, maxn = D.maxn, n_ord = D.n_orders;
+  const int ord0 = D.orders[0], ord1 = D.orders[1], ord2 = D.orders[2], ord3 = D.orders[3];
+  const void* const tab0 = D.tables[0];
+  const void* const tab1 = D.tables[1];
+  const void* const tab2 = D.tables[2];
+  const void* const tab3 = D.tables[3];
+  auto ord_at = [&](int oi) { return oi == 0 ? ord0 : (oi == 1 ? ord1 : (oi == 2 ? ord2 : ord3)); };
+  auto tab_at = [&](int oi) { return oi == 0 ? tab0 : (oi == 1 ? tab1 : (oi == 2 ? tab2 : tab3)); };
+  const int L = *D.length;
+  const int Dt = D.dt, QH = D.q_heads, hd = D.head_dim, md = D.mem_dim, R = D.R;
+  const int I = QH * hd, QD = QH * Dt, G = QH / D.kv_heads;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int mask = (1 << bits) - 1;
+  if (threadIdx.x < DR_MAXN) srow[threadIdx.x] = threadIdx.x < maxn ? dr_resolve(F.slot[j][threadIdx.x], L) : -1;
+  if (threadIdx.x == 0) {
+    const int32_t cr = dr_resolve(F.slot[j][maxn - 1], L);
+    const int32_t pv = dr_resolve(F.prev[j], L);
+    toks[0] = cr >= 0 ? D.tokens[cr] : -1;
+    toks[1] = pv >= 0 ? D.tokens[pv] : -1;
+  }
+  __syncthreads();
+  const int32_t cur_row = srow[maxn - 1];
+  const int64_t tok = toks[0], ptok = toks[1];
+  const bool fresh = F.fresh[j] != 0;
+  const bool is_attn = static_cast<int>(blockIdx.x) < nch;
+  // window codes of the routes this block needs: [r0, r0 + nr) (attention) or all (online)
+  const int r0 = is_attn ? blockIdx.x * FA_RC : 0;
+  const int nr = is_attn ? min(FA_RC, R - r0) : R;
+  for (int e = threadIdx.x; e < nr * maxn; e += 256) {
+    const int k = e / nr, rr = e % nr, r = r0 + rr;
+    const int32_t row = srow[k];
+    int c = 0;
+    if (k == maxn - 1 && fresh)
+      c = dr_lut_code4(D, ptok, tok, r);
+    else if (row >= 0)
+      c = D.codes[static_cast<int64_t>(row) * R + r] & mask;
+    wc[k][rr] = static_cast<uint8_t>(c);
+  }
+  __syncthreads();
+  auto addr_of = [&](int oi, int rr) -> int32_t {  // address of order oi for route r0 + rr, -1 if invalid
+    const int n = ord_at(oi);
+    int32_t addr = 0;
+    for (int k = 0; k < n; ++k) {
+      const int slot = maxn - n + k;
+      if (srow[slot] < 0) return -1;
+      addr |= static_cast<int32_t>(wc[slot][rr]) << (k * bits);
+    }
+    return addr;
+  };
+  if (is_attn) {
+    // ---------------- attention over routes [r0, r0 + nr)
+    if (fresh && cur_row >= 0)
+      for (int rr = threadIdx.x; rr < nr; rr += 256) D.codes[static_cast<int64_t>(cur_row) * R + r0 + rr] = wc[maxn - 1][rr];
+    for (int e = threadIdx.x; e < nr * n_ord; e += 256) {
+      const int rr = e / n_ord, oi = e % n_ord;
+      const int32_t a = addr_of(oi, rr);
+      rowsh[rr][oi] = a < 0 ? -1 : static_cast<int64_t>(r0 + rr) * (int64_t{1} << (bits * ord_at(oi))) + a;
+    }
+    const bool tok_ok = dr_tok_ok(D, tok);
+    for (int i = 4 * threadIdx.x; i < QD; i += 1024)
+      *reinterpret_cast<f32x4*>(&qs[i]) = tok_ok ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * QD + i)
+                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    if (D.table_dtype == LNG_BF16 && md % 8 == 0) {
+      const int pieces = md / 8;
+      for (int e = threadIdx.x; e < nr * n_ord * pieces; e += 256) {
+        const int pc = e % pieces, ro_ = e / pieces, oi = ro_ % n_ord, rr = ro_ / n_ord;
+        const int64_t row = rowsh[rr][oi];
+        bf16x8 v8 = bf16x8{};
+        if (row >= 0) v8 = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(tab_at(oi)) + row * md + 8 * pc);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xs[rr][oi * md + 8 * pc + q] = static_cast<float>(v8[q]);
+      }
+    } else {
+      for (int e = threadIdx.x; e < nr * Dt; e += 256) {
+        const int rr = e / Dt, i = e % Dt, oi = i / md;
+        const int64_t row = rowsh[rr][oi];
+        xs[rr][i] = row >= 0 ? ld_any(tab_at(oi), D.table_dtype, row * md + (i % md)) : 0.f;
+      }
+    }
+    __syncthreads();
+    // scores: 16 lanes per route (lane part p covers features p, p+16, ...), row-level DPP sums
+    {
+      const int rr = threadIdx.x >> 4, p = threadIdx.x & 15;
+      float x[LNG_DR_MAX_DT / 16];
+#pragma unroll
+      for (int q = 0; q < LNG_DR_MAX_DT / 16; ++q) x[q] = (rr < nr && 16 * q < Dt) ? xs[rr][16 * q + p] : 0.f;
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < LNG_DR_MAX_DT / 16; ++q) ss = fmaf(x[q], x[q], ss);
+      ss = row16_sum(ss);
+      const float sv = 1.0f / sqrtf(ss / static_cast<float>(Dt) + D.mem_eps);
+      if (p == 15 && rr < nr) sx[rr] = sv;
+      for (int qh = 0; qh < QH; ++qh) {
+        float a = 0.f;
+#pragma unroll
+        for (int q = 0; q < LNG_DR_MAX_DT / 16; ++q)
+          if (16 * q < Dt) a = fmaf(qs[qh * Dt + 16 * q + p], x[q], a);
+        a = row16_sum(a);
+        if (p == 15 && rr < nr) sc[qh][rr] = sv * a;
+      }
+    }
+    __syncthreads();
+    if (threadIdx.x < QH) {
+      const int qh = threadIdx.x;
+      float m = -INFINITY;
+      for (int rr = 0; rr < nr; ++rr) m = fmaxf(m, sc[qh][rr]);
+      float l = 0.f;
+      for (int rr = 0; rr < nr; ++rr) {
+        const float pp = expf(sc[qh][rr] - m);
+        l += pp;
+        pr[qh][rr] = pp * sx[rr];
+      }
+      ml[qh][0] = m;
+      ml[qh][1] = l;
+    }
+    __syncthreads();
+    // U[qh] = mem_norm . sum_r p_r s_r x_r (4 features per thread)
+    for (int e = 4 * threadIdx.x; e < QD; e += 1024) {
+      const int qh = e / Dt, i = e % Dt;
+      f32x4 u = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int rr = 0; rr < FA_RC; ++rr)
+        if (rr < nr) {
+          const f32x4 xv = *reinterpret_cast<const f32x4*>(&xs[rr][i]);
+          const float pv = pr[qh][rr];
+          u[0] = fmaf(pv, xv[0], u[0]);
+          u[1] = fmaf(pv, xv[1], u[1]);
+          u[2] = fmaf(pv, xv[2], u[2]);
+          u[3] = fmaf(pv, xv[3], u[3]);
+        }
+      const f32x4 mn = *reinterpret_cast<const f32x4*>(D.mem_norm + i);
+      *reinterpret_cast<f32x4*>(&us[e]) = f32x4{u[0] * mn[0], u[1] * mn[1], u[2] * mn[2], u[3] * mn[3]};
+    }
+    __syncthreads();
+    float* rec = part + (static_cast<int64_t>(j) * nch + blockIdx.x) * fa_rec(QH, hd, I);
+    // o_c[qh][oe] = sum_i Wv[h][oe][i] U[qh][i]: item (qh, 8 outputs, 32 rows), 16-byte loads of the
+    // transposed weight, all in flight; partial sums meet in LDS (xs is free now)
+    float* ob = &xs[0][0];  // [QH][Dt/32][hd]
+    {
+      const int nrb = Dt / 32, nob8 = hd / 8;
+      for (int it = threadIdx.x; it < QH * nob8 * nrb; it += 256) {
+        const int qh = it / (nob8 * nrb), rem = it % (nob8 * nrb), o8 = rem % nob8, rb = rem / nob8;
+        const int h = qh / G;
+        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (D.wv_dtype == LNG_BF16) {
+          const bf16* wt = static_cast<const bf16*>(D.wv_t) + (static_cast<int64_t>(h) * Dt + 32 * rb) * hd + 8 * o8;
+          bf16x8 wv8[32];
+#pragma unroll
+          for (int q = 0; q < 32; ++q) wv8[q] = *reinterpret_cast<const bf16x8*>(wt + static_cast<int64_t>(q) * hd);
+#pragma unroll
+          for (int q = 0; q < 32; ++q) {
+            const float uq = us[qh * Dt + 32 * rb + q];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[e] = fmaf(static_cast<float>(wv8[q][e]), uq, acc[e]);
+          }
+        } else {
+          const float* wt = static_cast<const float*>(D.wv_t) + (static_cast<int64_t>(h) * Dt + 32 * rb) * hd + 8 * o8;
+          for (int q0 = 0; q0 < 32; q0 += 16) {
+            f32x4 wa[16], wb[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              wa[q] = *reinterpret_cast<const f32x4*>(wt + static_cast<int64_t>(q0 + q) * hd);
+              wb[q] = *reinterpret_cast<const f32x4*>(wt + static_cast<int64_t>(q0 + q) * hd + 4);
+            }
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              const float uq = us[qh * Dt + 32 * rb + q0 + q];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                acc[e] = fmaf(wa[q][e], uq, acc[e]);
+                acc[4 + e] = fmaf(wb[q][e], uq, acc[4 + e]);
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ob[(qh * nrb + rb) * hd + 8 * o8 + e] = acc[e];
+      }
+      __syncthreads();
+      for (int e = threadIdx.x; e < I; e += 256) {
+        const int qh = e / hd, oe = e % hd;
+        float a = 0.f;
+        for (int rb = 0; rb < nrb; ++rb) a += ob[(qh * nrb + rb) * hd + oe];
+        rec[e] = a;
+        us[e] = a;  // o_c, reused below
+      }
+    }
+    __syncthreads();
+    // y_c[qh][k] = sum_{e in qh block} Gram[k][e] o_c[e]: thread = 4 consecutive k, the qh block's
+    // rows streamed in 16-byte loads (Gram is symmetric: row e = column e)
+    for (int it = threadIdx.x; it < QH * (I / 4); it += 256) {
+      const int qh = it / (I / 4), k4 = it % (I / 4);
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
+      for (int e0 = 0; e0 < hd; e0 += 32) {
+        f32x4 gv[32];
+#pragma unroll
+        for (int q = 0; q < 32; ++q)
+          gv[q] = e0 + q < hd ? *reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(qh * hd + e0 + q) * I + 4 * k4)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 32; ++q) {
+          const float oe = e0 + q < hd ? us[qh * hd + e0 + q] : 0.f;
+          y[0] = fmaf(gv[q][0], oe, y[0]);
+          y[1] = fmaf(gv[q][1], oe, y[1]);
+          y[2] = fmaf(gv[q][2], oe, y[2]);
+          y[3] = fmaf(gv[q][3], oe, y[3]);
+        }
+      }
+      *reinterpret_cast<f32x4*>(rec + I + qh * I + 4 * k4) = y;
+    }
+    if (threadIdx.x < QH) {
+      rec[I + QH * I + threadIdx.x] = ml[threadIdx.x][0];
+      rec[I + QH * I + QH + threadIdx.x] = ml[threadIdx.x][1];
+    }
+  } else {
+    // ---------------- online counts over pairs [t0, t0 + FA_TB) (thread = route)
+    const int t0 = (blockIdx.x - nch) * FA_TB;
+    const int npairs = L - 1;
+    const int r = threadIdx.x;
+    const bool rv = r < R;
+    for (int oi = 0; oi < n_ord; ++oi) qaddr[oi][r] = rv ? addr_of(oi, r) : -1;
+    int nt = 0;
+    int64_t a_al = 0;
+    if (t0 < npairs) {
+      // stage the committed codes of positions t0 - maxn + 1 .. t0 + nt - 1 (contiguous bytes)
+      const int tb = max(t0 - (maxn - 1), 0);
+      const int te = min(t0 + FA_TB, npairs);  // exclusive
+      const int64_t a0 = static_cast<int64_t>(tb) * R, a1 = static_cast<int64_t>(te) * R;
+      a_al = a0 & ~int64_t{3};
+      const int ndw = static_cast<int>((a1 - a_al + 3) / 4);
+      const uint32_t* src = reinterpret_cast<const uint32_t*>(D.codes + a_al);
+      constexpr int PQ = (FA_DW + 255) / 256;
+      uint32_t tmp[PQ];
+#pragma unroll
+      for (int q = 0; q < PQ; ++q) {
+        const int e = threadIdx.x + 256 * q;
+        tmp[q] = e < ndw ? src[e] : 0u;
+      }
+#pragma unroll
+      for (int q = 0; q < PQ; ++q) {
+        const int e = threadIdx.x + 256 * q;
+        if (e < ndw) cw[e] = tmp[q];
+      }
+      nt = te - t0;
+    }
+    __syncthreads();
+    if (t0 < npairs) {
+      const uint8_t* cb = reinterpret_cast<const uint8_t*>(cw);
+      // Codes as 8-bit digits (oldest least significant); a position before the sequence start is
+      // the digit 0xFF and an unusable query has the digit 0x80, neither of which a code can equal.
+      uint32_t pre[DR_MAXN - 1], cur[FA_TB];
+#pragma unroll
+      for (int k = 0; k < DR_MAXN - 1; ++k) {
+        const int t = t0 - (maxn - 1) + k;
+        pre[k] = (k < maxn - 1 && t >= 0 && rv) ? (cb[static_cast<int64_t>(t) * R + r - a_al] & mask) : 0xFFu;
+      }
+#pragma unroll
+      for (int tt = 0; tt < FA_TB; ++tt) cur[tt] = cb[static_cast<int64_t>(t0 + tt) * R + r - a_al] & mask;
+      uint32_t q8[4], sho[4];
+#pragma unroll
+      for (int oi = 0; oi < 4; ++oi) {
+        const bool used = oi < n_ord;
+        const int n = used ? ord_at(oi) : 1;
+        const int32_t qa = (rv && used) ? qaddr[oi][r] : -1;
+        uint32_t q = 0;
+        for (int k = 0; k < n; ++k) q |= ((static_cast<uint32_t>(qa) >> (bits * k)) & mask) << (8 * k);
+        q8[oi] = qa >= 0 ? q : 0x80808080u;
+        sho[oi] = static_cast<uint32_t>(8 * (maxn - n));
+      }
+      const int sh = 8 * (maxn - 1);
+      uint32_t amax = 0xFFFFFFFFu;
+#pragma unroll
+      for (int k = 0; k < DR_MAXN - 1; ++k)
+        if (k < maxn - 1) amax = (amax >> 8) | (pre[k] << sh);
+#pragma unroll
+      for (int tt = 0; tt < FA_TB; ++tt) {
+        amax = (amax >> 8) | (cur[tt] << sh);
+        int cnt = 0;
+#pragma unroll
+        for (int oi = 0; oi < 4; ++oi) cnt += __popcll(__ballot(q8[oi] == (amax >> sho[oi])));
+        if (lane == 0) red[w][tt] = cnt;
+      }
+      __syncthreads();
+      int s = 0;
+      if (threadIdx.x < nt) {
+        const int t = t0 + threadIdx.x;
+        s = (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
+        if (s > 0) atomicAdd(&counts[static_cast<int64_t>(j) * D.V + D.tokens[t + 1]], s);
+      }
+      // the block's total weight (exact integer) into the position's total
+      const float bs = block_sum256(static_cast<float>(s), redf);
+      if (threadIdx.x == 0 && bs > 0.f) atomicAdd(&D.sync[SY_TOT + j], static_cast<int32_t>(bs));
+    }
+  }
+  // ---------------- last block of position j: merge, hidden norm
+  if (!dr_last_block(&D.sync[SY_ATT + j], nch + nob, &last_flag)) return;
+  const float b0 = D.sink_logit;
+  const int RS = fa_rec(QH, hd, I);
+  const float* rj = part + static_cast<int64_t>(j) * nch * RS;
+  // merge weights per (chunk, head): f = e^{m_c - M} / (e^{b0 - M} + sum_c l_c e^{m_c - M})
+  __shared__ float wgt[FA_MAXCH][LNG_DR_MAX_QH];
+  if (threadIdx.x < QH) {
+    const int qh = threadIdx.x;
+    float pm[FA_MAXCH], pl[FA_MAXCH];
+#pragma unroll
+    for (int c = 0; c < FA_MAXCH; ++c) {
+      pm[c] = c < nch ? rj[c * RS + I + QH * I + qh] : -INFINITY;
+      pl[c] = c < nch ? rj[c * RS + I + QH * I + QH + qh] : 0.f;
+    }
+    float M = b0;
+#pragma unroll
+    for (int c = 0; c < FA_MAXCH; ++c) M = fmaxf(M, pm[c]);
+    float l = expf(b0 - M);
+    float f[FA_MAXCH];
+#pragma unroll
+    for (int c = 0; c < FA_MAXCH; ++c) {
+      f[c] = c < nch ? expf(pm[c] - M) : 0.f;
+      l = fmaf(pl[c], f[c], l);
+    }
+#pragma unroll
+    for (int c = 0; c < FA_MAXCH; ++c) wgt[c][qh] = f[c] / l;
+  }
+  __syncthreads();
+  // o[e] = sum_c f_{c,qh(e)} o_c[e];  y[k] = sum_c sum_qh f_{c,qh} y_c[qh][k]  (loads batched:
+  // every chunk's value for 4 heads at a time)
+  float acc = 0.f;
+  for (int e = threadIdx.x; e < I; e += 256) {
+    const int qh = e / hd;
+    float ov[FA_MAXCH];
+#pragma unroll
+    for (int c = 0; c < FA_MAXCH; ++c) ov[c] = c < nch ? rj[c * RS + e] : 0.f;
+    float o = 0.f, y = 0.f;
+#pragma unroll
+    for (int c = 0; c < FA_MAXCH; ++c) o = fmaf(c < nch ? wgt[c][qh] : 0.f, ov[c], o);
+    for (int q0 = 0; q0 < QH; q0 += 4) {
+      float yv[FA_MAXCH][4];
+#pragma unroll
+      for (int c = 0; c < FA_MAXCH; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) yv[c][q] = (c < nch && q0 + q < QH) ? rj[c * RS + I + (q0 + q) * I + e] : 0.f;
+#pragma unroll
+      for (int c = 0; c < FA_MAXCH; ++c)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (c < nch && q0 + q < QH) y = fmaf(wgt[c][q0 + q], yv[c][q], y);
+    }
+    us[e] = o;
+    acc = fmaf(o, y, acc);
+  }
+  const float ss = block_sum256(acc, redf);
+  const float rn = 1.0f / sqrtf(ss / static_cast<float>(D.d) + D.draft_eps);
+  for (int e = threadIdx.x; e < I; e += 256) ro[static_cast<int64_t>(j) * I + e] = rn * us[e];
+}
+
+// grid (nblk): scores of a slice of FL_VB vocabulary rows for every position against lut_out (fp32
+// MFMA), per position the slice's max, sum of exponentials and top-K by logit among tokens without
+// online counts; tokens with counts go to the position's candidate list (their counts are read
+// and returned to zero here).  The last block selects every position's top-K (wave per position:
+// by logit, or by the online-mixed probability) and writes the children's tokens.
+__global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, int32_t K, int32_t online, float kappa,
+                                                     const float* __restrict__ ro, float* __restrict__ logits_out,
+                                                     float* __restrict__ lpart, int32_t* __restrict__ counts,
+                                                     int32_t* __restrict__ cand, DrChildren C,
+                                                     int64_t* __restrict__ ids, float* __restrict__ scores) {
+  __shared__ __attribute__((aligned(16))) float rs[DR_MAXP][FL_I];
+  __shared__ float lt[DR_MAXP][FL_VB];
+  __shared__ int last_flag;
+  __shared__ float sel_v[4][DR_MAXK];
+  __shared__ int sel_i[4][DR_MAXK];
+  const int I = D.q_heads * D.head_dim;
+  const int64_t V = D.V;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int e = threadIdx.x; e < P * I; e += 256) rs[e / I][e % I] = ro[e];
+  __syncthreads();
+  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * FL_VB;
+  // fp32 MFMA 16x16x4: D[row][j] += sum_k EO[row][k] ro[j][k].  Lane l feeds A[row l%16][k-slot
+  // l/16] and B[k-slot l/16][column l%16]; k-slot l/16 of step (s, q) is feature 16s + 4(l/16) + q
+  // (A and B use the same feature order, so the sum is unchanged).  Wave w: tiles 2w, 2w+1.
+  const int col = lane & 15, kq = lane >> 4;
+  const int nks = I / 16;
+  f32x4 bq[FL_I / 16];
+#pragma unroll
+  for (int st = 0; st < FL_I / 16; ++st)
+    bq[st] = (st < nks && col < P) ? *reinterpret_cast<const f32x4*>(&rs[col][16 * st + 4 * kq]) : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int tile = 2 * w; tile < 2 * w + 2; ++tile) {
+    const int64_t vrow = v0 + tile * 16 + col;
+    f32x4 a[FL_I / 16];
+#pragma unroll
+    for (int st = 0; st < FL_I / 16; ++st)
+      a[st] = (st < nks && vrow < V) ? *reinterpret_cast<const f32x4*>(D.lut_out + vrow * I + 16 * st + 4 * kq)
+                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < FL_I / 16; ++st) {
+      if (st < nks) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][0], bq[st][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][1], bq[st][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][2], bq[st][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][3], bq[st][3], acc, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int vl = tile * 16 + 4 * kq + r;
+      const int64_t v = v0 + vl;
+      if (col < P) {
+        lt[col][vl] = v < V ? acc[r] : -INFINITY;
+        if (logits_out && v < V) logits_out[static_cast<int64_t>(col) * V + v] = acc[r];
+      }
+    }
+  }
+  __syncthreads();
+  const int nblk = gridDim.x;
+  for (int jj = w; jj < P; jj += 4) {
+    float* o = lpart + (static_cast<int64_t>(jj) * nblk + blockIdx.x) * (2 + 2 * K);
+    const float x0 = lt[jj][lane], x1 = lt[jj][lane + 64];
+    const float m = wave_max(fmaxf(x0, x1));
+    const float s = wave_sum((x0 == -INFINITY ? 0.f : expf(x0 - m)) + (x1 == -INFINITY ? 0.f : expf(x1 - m)));
+    const int64_t va = v0 + lane, vb = v0 + 64 + lane;
+    int ca = 0, cb = 0;
+    if (online) {
+      int32_t* cj = counts + static_cast<int64_t>(jj) * V;
+      ca = va < V ? cj[va] : 0;
+      cb = vb < V ? cj[vb] : 0;
+      // tokens with counts: append (id, logit bits, count) to the position's list, clear the count
+      const uint64_t ma = __ballot(ca > 0), mb = __ballot(cb > 0);
+      const int na = __popcll(ma), nb = __popcll(mb);
+      if (na + nb > 0) {
+        int base = 0;
+        if (lane == 0) base = atomicAdd(&D.sync[SY_NC + jj], na + nb);
+        base = __shfl(base, 0, 64);
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        if (ca > 0 && base + __popcll(ma & below) < FS_CAND) {
+          const int slot = base + __popcll(ma & below);
+          int32_t* c3 = cand + (static_cast<int64_t>(jj) * FS_CAND + slot) * 3;
+          c3[0] = static_cast<int32_t>(va);
+          c3[1] = __float_as_int(x0);
+          c3[2] = ca;
+          cj[va] = 0;
+        }
+        if (cb > 0 && base + na + __popcll(mb & below) < FS_CAND) {
+          const int slot = base + na + __popcll(mb & below);
+          int32_t* c3 = cand + (static_cast<int64_t>(jj) * FS_CAND + slot) * 3;
+          c3[0] = static_cast<int32_t>(vb);
+          c3[1] = __float_as_int(x1);
+          c3[2] = cb;
+          cj[vb] = 0;
+        }
+      }
+    }
+    if (lane == 0) {
+      o[0] = m;
+      o[1] = s;
+    }
+    TopK t;
+    t.clear();
+    if (x0 != -INFINITY && ca == 0) t.insert(x0, static_cast<int>(va), K);
+    if (x1 != -INFINITY && cb == 0) t.insert(x1, static_cast<int>(vb), K);
+    float sv[DR_MAXK];
+    int si[DR_MAXK];
+    wave_select(t, K, sv, si);
+    if (lane == 0)
+      for (int k = 0; k < K; ++k) {
+        o[2 + k] = sv[k];
+        o[2 + K + k] = __int_as_float(si[k]);
+      }
+  }
+  if (!dr_last_block(&D.sync[SY_LOG], nblk, &last_flag)) return;
+  // ---------------- selection: wave w handles positions w, w + 4, ...
+  for (int j = w; j < P; j += 4) {
+    const float* lp = lpart + static_cast<int64_t>(j) * nblk * (2 + 2 * K);
+    constexpr int NB = 4;  // records per lane (nblk <= 256)
+    float rm[NB], rsum[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int b = lane + 64 * q;
+      rm[q] = b < nblk ? lp[b * (2 + 2 * K)] : -INFINITY;
+      rsum[q] = b < nblk ? lp[b * (2 + 2 * K) + 1] : 0.f;
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int q = 0; q < NB; ++q) m = fmaxf(m, rm[q]);
+    const float M = wave_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < NB; ++q) s += rm[q] == -INFINITY ? 0.f : rsum[q] * expf(rm[q] - M);
+    const float S = wave_sum(s);
+    const float tj = online ? static_cast<float>(D.sync[SY_TOT + j]) : 0.f;
+    const float n_eff = tj / static_cast<float>(D.R * D.n_orders);
+    const float lam = tj > 0.f ? n_eff / (n_eff + kappa) : 0.f;
+    auto mixed = [&](float lg, float cnt) {
+      return logf((1.f - lam) * expf(lg - M) / S + (tj > 0.f ? lam * cnt / tj : 0.f));
+    };
+    TopK t;
+    t.clear();
+    // candidates A: every block's top-K among tokens without counts (all loads in flight)
+    float av[NB][DR_MAXK];
+    int ai[NB][DR_MAXK];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) {
+      const int b = lane + 64 * q;
+#pragma unroll
+      for (int k = 0; k < DR_MAXK; ++k) {
+        const bool ok = b < nblk && k < K;
+        av[q][k] = ok ? lp[b * (2 + 2 * K) + 2 + k] : -INFINITY;
+        ai[q][k] = ok ? __float_as_int(lp[b * (2 + 2 * K) + 2 + K + k]) : -1;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < NB; ++q)
+#pragma unroll
+      for (int k = 0; k < DR_MAXK; ++k)
+        if (ai[q][k] >= 0) t.insert(online ? mixed(av[q][k], 0.f) : av[q][k], ai[q][k], K);
+    if (online) {
+      // candidates B: tokens with online counts
+      const int nc = min(D.sync[SY_NC + j], FS_CAND);
+      for (int e0 = 0; e0 < nc; e0 += 64 * 8) {
+        int cid[8], ccn[8];
+        float clg[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int e = e0 + q * 64 + lane;
+          const int32_t* c3 = cand + (static_cast<int64_t>(j) * FS_CAND + e) * 3;
+          cid[q] = e < nc ? c3[0] : -1;
+          clg[q] = e < nc ? __int_as_float(c3[1]) : 0.f;
+          ccn[q] = e < nc ? c3[2] : 0;
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+          if (cid[q] >= 0) t.insert(mixed(clg[q], static_cast<float>(ccn[q])), cid[q], K);
+      }
+    }
+    wave_select(t, K, sel_v[w], sel_i[w]);
+    if (lane < K) {
+      ids[static_cast<int64_t>(j) * K + lane] = sel_i[w][lane];
+      scores[static_cast<int64_t>(j) * K + lane] = sel_v[w][lane];
+    }
+    if (lane == 0 && online) {
+      D.sync[SY_TOT + j] = 0;
+      D.sync[SY_NC + j] = 0;
+    }
+    for (int e = lane; e < C.n; e += 64) {
+      if (C.parent[e] != j) continue;
+      const int t2 = sel_i[w][C.rank[e]];
+      D.tokens[C.row[e]] = t2 >= 0 ? t2 : sel_i[w][0];
+    }
+  }
+}
+
+// Codes of positions (fast path): codes[row_j][r] from the router tables.   grid (cdiv(R, 256), n)
+__global__ __launch_bounds__(256) void k_fast_codes(lng_drafter D, DrAdv A) {
+  const int j = blockIdx.y;
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= D.R || j >= A.n) return;
+  const int L = *D.length;
+  const int32_t row = A.range ? A.base + j : dr_resolve(A.row[j], L);
+  const int32_t pv = A.range ? (j == 0 ? dr_resolve(A.prev0, L) : A.base + j - 1) : dr_resolve(A.prev[j], L);
+  if (row < 0) return;
+  const int64_t tok = D.tokens[row];
+  const int64_t ptok = pv >= 0 ? D.tokens[pv] : -1;
+  D.codes[static_cast<int64_t>(row) * D.R + r] = static_cast<uint8_t>(dr_lut_code(D, ptok, tok, r));
+}
+
+// Verification gather of tree nodes (fast path): the codes of fresh nodes come from the router
+// tables (and are stored), the rest of each window from the state.     grid (cdiv(R, 32), P)
+template <typename TT>
+__global__ __launch_bounds__(256) void k_fast_gather(lng_drafter D, FastLevel F, int32_t root_dst, TT* __restrict__ out) {
+  __shared__ int32_t srow[DR_MAXN];
+  __shared__ int64_t rowsh[32][DR_MAXN];
+  __shared__ uint8_t wc[DR_MAXN][32];
+  __shared__ int64_t toks[2];
+  const int j = blockIdx.y;
+  // descriptor fields used in loops, read once (kernel-argument loads otherwise repeat per use)
+  const int bits = D.bits, maxn = D.maxn, n_ord = D.n_orders;
+  const int ord0 = D.orders[0], ord1 = D.orders[1], ord2 = D.orders[2], ord3 = D.orders[3];
+  auto ord_at = [&](int oi) { return oi == 0 ? ord0 : (oi == 1 ? ord1 : (oi == 2 ? ord2 : ord3)); };
+  const int L = *D.length;
+  const int R = D.R, mask = (1 << bits) - 1;
+  if (threadIdx.x < DR_MAXN) srow[threadIdx.x] = threadIdx.x < maxn ? dr_resolve(F.slot[j][threadIdx.x], L) : -1;
+  if (threadIdx.x == 0) {
+    const int32_t cr = dr_resolve(F.slot[j][maxn - 1], L);
+    const int32_t pv = dr_resolve(F.prev[j], L);
+    toks[0] = cr >= 0 ? D.tokens[cr] : -1;
+    toks[1] = pv >= 0 ? D.tokens[pv] : -1;
+  }
+  if (root_dst >= 0 && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)
+    D.tokens[root_dst] = L > 0 ? D.tokens[L - 1] : -1;
+  __syncthreads();
+  const bool fresh = F.fresh[j] != 0;
+  const int r0 = blockIdx.x * 32;
+  const int nr = min(32, R - r0);
+  const int32_t cur_row = srow[maxn - 1];
+  if (threadIdx.x < nr * maxn) {
+    const int k = threadIdx.x / nr, rr = threadIdx.x % nr, r = r0 + rr;
+    int c = 0;
+    if (k == maxn - 1 && fresh)
+      c = dr_lut_code4(D, toks[1], toks[0], r);
+    else if (srow[k] >= 0)
+      c = D.codes[static_cast<int64_t>(srow[k]) * R + r] & mask;
+    wc[k][rr] = static_cast<uint8_t>(c);
+  }
+  __syncthreads();
+  if (fresh && cur_row >= 0 && threadIdx.x < nr) D.codes[static_cast<int64_t>(cur_row) * R + r0 + threadIdx.x] = wc[maxn - 1][threadIdx.x];
+  if (threadIdx.x < nr * n_ord) {
+    const int rr = threadIdx.x / n_ord, oi = threadIdx.x % n_ord;
+    const int n = ord_at(oi);
+    int64_t addr = 0;
+    bool ok = true;
+    for (int k = 0; k < n; ++k) {
+      const int slot = maxn - n + k;
+      ok = ok && srow[slot] >= 0;
+      addr |= static_cast<int64_t>(wc[slot][rr]) << (k * bits);
+    }
+    rowsh[rr][oi] = ok ? static_cast<int64_t>(r0 + rr) * (int64_t{1} << (bits * n)) + addr : -1;
+  }
+  __syncthreads();
+  const int md = D.mem_dim, Dt = D.dt;
+  const TT* const* tabs = reinterpret_cast<const TT* const*>(D.tables);
+  constexpr int VE = 16 / sizeof(TT);  // elements per 16-byte piece
+  if (md % VE == 0) {
+    typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+    const int pieces = md / VE;
+    for (int e = threadIdx.x; e < nr * n_ord * pieces; e += 256) {
+      const int pc = e % pieces, ro_ = e / pieces, oi = ro_ % n_ord, rr = ro_ / n_ord;
+      const int64_t row = rowsh[rr][oi];
+      piece_t v = {0u, 0u, 0u, 0u};
+      if (row >= 0) v = *reinterpret_cast<const piece_t*>(tabs[oi] + row * md + VE * pc);
+      *reinterpret_cast<piece_t*>(out + (static_cast<int64_t>(j) * R + r0 + rr) * Dt + oi * md + VE * pc) = v;
+    }
+  } else {
+    for (int e = threadIdx.x; e < nr * Dt; e += 256) {
+      const int rr = e / Dt, i = e % Dt, oi = i / md;
+      const int64_t row = rowsh[rr][oi];
+      out[(static_cast<int64_t>(j) * R + r0 + rr) * Dt + i] = row >= 0 ? tabs[oi][row * md + (i % md)] : TT(0.f);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ host side
 namespace {
 
 struct DrLayout {
-  size_t u, qkw, part, hid, logits, lpart, w, total;
-  int nch, nblk;
+  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, ncand, total;
+  int nch, nblk, fnch, fnblk;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -760,8 +1552,24 @@ DrLayout dr_layout(const lng_drafter& D, int P, int K, int max_pairs) {
   l.logits = take(sizeof(float) * static_cast<size_t>(P) * D.V);
   l.lpart = take(sizeof(float) * static_cast<size_t>(P) * l.nblk * (2 + 2 * K));
   l.w = take(sizeof(int32_t) * static_cast<size_t>(P) * std::max(max_pairs, 1));
+  l.fnch = static_cast<int>(cdiv(D.R, FA_RC));
+  l.fnblk = static_cast<int>(cdiv(D.V, FL_VB));
+  const int I = D.q_heads * D.head_dim;
+  l.fpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnch * (D.q_heads * D.head_dim + D.q_heads * I + 2 * D.q_heads));
+  l.ro = take(sizeof(float) * P * I);
+  l.tot = 0;
+  l.flpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnblk * (2 + 2 * K));
+  l.cand = take(sizeof(int32_t) * static_cast<size_t>(P) * FS_CAND * 3);
+  l.ncand = 0;
   l.total = off;
   return l;
+}
+
+bool dr_fast(const lng_drafter& D) {
+  const int I = D.q_heads * D.head_dim;
+  return D.lut_prev && D.lut_cur && D.lut_start && D.lut_qk && D.lut_out && D.gram_out && D.wv_t && D.sync &&
+         !D.router_ssm && !D.query_ssm && I <= FL_I && I % 16 == 0 && D.dt % 64 == 0 &&
+         static_cast<int64_t>(D.V) * DR_MAXK <= 524288;
 }
 
 int dr_check(const lng_drafter* D, const char* what) {
@@ -789,6 +1597,12 @@ bool spec_ok(const lng_drafter& D, int32_t v) { return v == LNG_ROW_NONE || v < 
 
 int dr_advance(const lng_drafter& D, const DrAdv& A, int from_router, float* u, hipStream_t s) {
   if (A.n == 0) return LNG_OK;
+  if (dr_fast(D)) {
+    if (!from_router) return LNG_OK;
+    hipLaunchKernelGGL(k_fast_codes, dim3(static_cast<unsigned>(cdiv(D.R, 256)), static_cast<unsigned>(A.n)),
+                       dim3(256), 0, s, D, A);
+    return check_launch("drafter_advance(fast codes)");
+  }
   const bool has_ssm = D.ssm_dim > 0 && D.ssm && D.ssm_w_in;
   if (has_ssm) {
     hipLaunchKernelGGL(k_draft_ssm_u, dim3(static_cast<unsigned>(cdiv(D.ssm_dim, 16)), static_cast<unsigned>(cdiv(A.n, 4))),
@@ -818,10 +1632,40 @@ int dr_windows(const lng_drafter& D, const int32_t* windows, int32_t P, DrWin& W
   return LNG_OK;
 }
 
+int dr_readout_fast(const lng_drafter& D, const FastLevel& F, int K, int online, float kappa, const DrChildren& C,
+                    char* work, size_t work_bytes, int32_t* counts, int64_t* ids, float* scores, float* logits_out,
+                    hipStream_t s) {
+  const int P = F.P;
+  const int max_pairs = D.rows;
+  const DrLayout l = dr_layout(D, P, K, online ? max_pairs : 1);
+  if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter: workspace too small");
+  if (online && !counts) return fail(LNG_E_ARG, "drafter: online counts need the counts buffer");
+  const int nob = online ? static_cast<int>(cdiv(max_pairs, FA_TB)) : 0;
+  if (online && D.rows > FS_CAND + 1) return fail(LNG_E_ARG, "drafter: online counts cover at most 8192 pairs");
+  hipLaunchKernelGGL(k_fast_attend, dim3(static_cast<unsigned>(l.fnch + nob), static_cast<unsigned>(P)), dim3(256), 0, s,
+                     D, F, l.fnch, nob, online, reinterpret_cast<float*>(work + l.fpart), counts,
+                     reinterpret_cast<float*>(work + l.ro));
+  if (int rc = check_launch("drafter_readout(fast attend)")) return rc;
+  hipLaunchKernelGGL(k_fast_logits, dim3(static_cast<unsigned>(l.fnblk)), dim3(256), 0, s, D, P, K, online, kappa,
+                     reinterpret_cast<const float*>(work + l.ro), logits_out, reinterpret_cast<float*>(work + l.flpart),
+                     counts, reinterpret_cast<int32_t*>(work + l.cand), C, ids, scores);
+  return check_launch("drafter_readout(fast logits)");
+}
+
 int dr_readout(const lng_drafter& D, const DrWin& W, int K, int online, float kappa, const DrChildren& C,
                char* work, size_t work_bytes, int32_t* counts, int64_t* ids, float* scores, float* logits_out,
                hipStream_t s) {
   const int P = W.n;
+  if (dr_fast(D)) {
+    FastLevel F{};
+    F.P = P;
+    for (int j = 0; j < P; ++j) {
+      for (int k = 0; k < DR_MAXN; ++k) F.slot[j][k] = W.slot[j][k];
+      F.prev[j] = LNG_ROW_NONE;
+      F.fresh[j] = 0;
+    }
+    return dr_readout_fast(D, F, K, online, kappa, C, work, work_bytes, counts, ids, scores, logits_out, s);
+  }
   const int max_pairs = D.rows;  // the online kernel's grid covers any committed length
   const DrLayout l = dr_layout(D, P, K, online ? max_pairs : 1);
   if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter: workspace too small");
@@ -991,6 +1835,7 @@ int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t*
     }
   };
   hipStream_t s = as_stream(stream);
+  const bool fast = dr_fast(*D);
   const int maxd = *std::max_element(depth.begin(), depth.end());
   std::vector<char> coded(n, 0);
   coded[0] = 1;
@@ -1007,6 +1852,33 @@ int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t*
     if (parents.empty()) continue;
     for (size_t p0 = 0; p0 < parents.size(); p0 += DR_MAXP) {
       const int P = static_cast<int>(std::min<size_t>(DR_MAXP, parents.size() - p0));
+      DrChildren C{};
+      for (int i = 1; i < n; ++i)
+        for (int j = 0; j < P; ++j)
+          if (parent[i] == parents[p0 + j]) {
+            C.row[C.n] = node_row0 + i;
+            C.parent[C.n] = static_cast<int8_t>(j);
+            C.rank[C.n] = static_cast<int8_t>(rank[i]);
+            ++C.n;
+          }
+      if (fast) {
+        // the parents' codes are computed inside the attention launch
+        FastLevel F{};
+        F.P = P;
+        std::vector<int32_t> win(D->maxn);
+        for (int j = 0; j < P; ++j) {
+          const int i = parents[p0 + j];
+          window(i, win.data());
+          for (int k = 0; k < D->maxn; ++k) F.slot[j][k] = win[k];
+          F.prev[j] = i == 0 ? -2 : spec(parent[i]);
+          F.fresh[j] = coded[i] ? 0 : 1;
+          coded[i] = 1;
+        }
+        if (int rc = dr_readout_fast(*D, F, K, online, kappa, C, static_cast<char*>(work), need, counts, lvl_ids,
+                                     lvl_sc, nullptr, s))
+          return rc;
+        continue;
+      }
       // codes of the parents of this depth (their tokens were chosen one depth up)
       DrAdv A{};
       for (int j = 0; j < P; ++j) {
@@ -1025,19 +1897,37 @@ int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t*
         window(parents[p0 + j], win.data());
         for (int k = 0; k < D->maxn; ++k) W.slot[j][k] = win[k];
       }
-      DrChildren C{};
-      for (int i = 1; i < n; ++i)
-        for (int j = 0; j < P; ++j)
-          if (parent[i] == parents[p0 + j]) {
-            C.row[C.n] = node_row0 + i;
-            C.parent[C.n] = static_cast<int8_t>(j);
-            C.rank[C.n] = static_cast<int8_t>(rank[i]);
-            ++C.n;
-          }
       if (int rc = dr_readout(*D, W, K, online, kappa, C, static_cast<char*>(work), need, counts, lvl_ids, lvl_sc,
                               nullptr, s))
         return rc;
     }
+  }
+  if (fast && route_tokens) {
+    // leaves' codes, the root token next to the nodes, and the verification gather in one launch each
+    const int es = dtype_size(D->table_dtype);
+    for (int p0 = 0; p0 < n; p0 += DR_MAXP) {
+      FastLevel F{};
+      F.P = std::min(DR_MAXP, n - p0);
+      std::vector<int32_t> win(D->maxn);
+      for (int j = 0; j < F.P; ++j) {
+        const int i = p0 + j;
+        window(i, win.data());
+        for (int k = 0; k < D->maxn; ++k) F.slot[j][k] = win[k];
+        F.prev[j] = i == 0 ? -2 : spec(parent[i]);
+        F.fresh[j] = coded[i] ? 0 : 1;
+      }
+      char* out = static_cast<char*>(route_tokens) + static_cast<size_t>(p0) * D->R * D->dt * es;
+      const dim3 g(static_cast<unsigned>(cdiv(D->R, 32)), static_cast<unsigned>(F.P));
+      const int32_t root_dst = p0 == 0 ? node_row0 : -1;
+      if (D->table_dtype == LNG_BF16)
+        hipLaunchKernelGGL(k_fast_gather<bf16>, g, dim3(256), 0, s, *D, F, root_dst, reinterpret_cast<bf16*>(out));
+      else if (D->table_dtype == LNG_F16)
+        hipLaunchKernelGGL(k_fast_gather<_Float16>, g, dim3(256), 0, s, *D, F, root_dst, reinterpret_cast<_Float16*>(out));
+      else
+        hipLaunchKernelGGL(k_fast_gather<float>, g, dim3(256), 0, s, *D, F, root_dst, reinterpret_cast<float*>(out));
+      if (int rc = check_launch("drafter_tree(fast gather)")) return rc;
+    }
+    return LNG_OK;
   }
   // codes of the nodes that were never a parent (leaves), in index order, 16 at a time
   std::vector<int> rest;

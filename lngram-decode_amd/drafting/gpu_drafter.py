@@ -57,7 +57,7 @@ class GpuDrafter:
     name = "gpu"
 
     def __init__(self, bundle, topk: int = 3, shortlist_cap: int | None = None, device=None, max_len: int = 4096,
-                 online: bool = False, kappa: float = 1.0):
+                 online: bool = False, kappa: float = 1.0, tables: bool = True):
         c, t = _bundle_parts(bundle)
         self.cfg = c
         self.topk = int(topk)
@@ -102,6 +102,9 @@ class GpuDrafter:
         if self.N:
             self.vec.update({k: f32(k) for k in ("ssm_norm", "ssm_w_in", "ssm_decay")})
         self._compose(t, dev)
+        self.luts = None
+        if tables and not (self.router_ssm or self.query_ssm) and self.qh * self.hd <= 256:
+            self._build_luts(t, dev)
 
         rows = self.max_len + _TREE_ROWS + _HYP_ROWS
         self.rows = rows
@@ -153,6 +156,32 @@ class GpuDrafter:
             if qks else None
         self.ov = torch.stack(ov, 1).mul(mem_norm[None, None]).reshape(self.d, self.qh * self.dt).contiguous()
 
+    def _build_luts(self, t: dict, dev) -> None:
+        """Per-token tables of the token-only drafter (``lng_drafter.lut_*``), fp32."""
+        c = self.cfg
+        d, kh = self.d, self.kv * self.hd
+        ef = self.emb.float()
+        rw = self.router.float()
+        ones = torch.ones(d, dtype=torch.float32, device=dev)
+        reps = float(c["router_eps"])
+        lut = {}
+        lut["lut_prev"] = ops.linear(ops.rmsnorm(ef, self.vec["router_prev_norm"], reps), rw[:, :d].contiguous())
+        lut["lut_cur"] = ops.linear(ops.rmsnorm(ef, self.vec["router_cur_norm"], reps), rw[:, d:2 * d].contiguous())
+        lut["lut_start"] = ops.linear(ops.rmsnorm(self.vec["router_start"][None], self.vec["router_prev_norm"], reps),
+                                      rw[:, :d].contiguous())[0].contiguous()
+        lut["lut_qk"] = ops.linear(ops.rmsnorm(ef, ones, float(c["draft_eps"])), self.qk)
+        w_o_t = t["w_o"].to(dev, torch.float32).t().contiguous()                  # [I, d]
+        lut["lut_out"] = ops.linear(ef * self.vec["out_norm"][None], w_o_t)
+        lut["gram_out"] = ops.linear(w_o_t, w_o_t)
+        kvp = t["kv_proj"].to(dev)
+        wdt = torch.bfloat16 if kvp.dtype == torch.bfloat16 else torch.float32
+        lut["wv_t"] = kvp[kh:].to(wdt).view(self.kv, self.hd, self.dt).transpose(1, 2).contiguous()  # [kv, Dt, hd]
+        lut["mem_norm"] = t["mem_norm"].to(dev, torch.float32).contiguous()
+        self.wv_dtype = ops.dtype_code(wdt)
+        self.luts = lut
+        self.sync = torch.zeros(64, dtype=torch.int32, device=dev)
+        del ef
+
     def _descriptor(self, tok, codes, ssm, length, rows) -> _lib.Drafter:
         c = self.cfg
         D = _lib.Drafter()
@@ -177,6 +206,11 @@ class GpuDrafter:
         D.qks = self.qks.data_ptr() if self.qks is not None else None
         D.tokens, D.codes, D.ssm, D.length = tok.data_ptr(), codes.data_ptr(), ssm.data_ptr(), length.data_ptr()
         D.rows = rows
+        if self.luts is not None:
+            for k, v in self.luts.items():
+                setattr(D, k, v.data_ptr())
+            D.sync = self.sync.data_ptr()
+            D.wv_dtype = self.wv_dtype
         return D
 
     def _stream(self) -> int:
@@ -227,6 +261,8 @@ class GpuDrafter:
             L = self.length
             if L + n > self.max_len:
                 raise ValueError(f"context full: {L} + {n} > {self.max_len}")
+            if self.online and L + n > 8193:
+                raise ValueError("online counts cover at most 8192 committed pairs")
             self.tok_d[L:L + n] = torch.tensor(toks, dtype=torch.int64).to(self.device)
             if codes is not None:
                 ca = np.asarray(codes)

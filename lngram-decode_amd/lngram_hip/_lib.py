@@ -40,7 +40,9 @@ class Drafter(ctypes.Structure):
         ("emb", ctypes.c_void_p), ("tables", ctypes.c_void_p * 4), ("router", ctypes.c_void_p)] + [
         (n, ctypes.c_void_p) for n in ("router_start", "router_prev_norm", "router_cur_norm", "ssm_norm", "ssm_w_in",
                                        "ssm_decay", "qk", "qks", "ov", "out_norm", "tokens", "codes", "ssm",
-                                       "length")] + [("rows", ctypes.c_int32)]
+                                       "length")] + [("rows", ctypes.c_int32)] + [
+        (n, ctypes.c_void_p) for n in ("lut_prev", "lut_cur", "lut_start", "lut_qk", "lut_out", "gram_out", "wv_t",
+                                       "mem_norm")] + [("wv_dtype", ctypes.c_int32), ("sync", ctypes.c_void_p)]
 
 
 _PD = ctypes.POINTER(Drafter)

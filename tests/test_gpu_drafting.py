@@ -24,13 +24,23 @@ TAU = 2e-5
 SPEC16 = dtree.tree16()
 
 
+KINDS = ["sdb", "sdb_generic", "sdc"]
+
+
 def _bundle(kind: str, seed: int = 5):
-    w = {"sdb": wl.TINY_DRAFT, "sdc": wl.TINY_DRAFT_SSM}[kind]
+    w = {"sdb": wl.TINY_DRAFT, "sdb_generic": wl.TINY_DRAFT, "sdc": wl.TINY_DRAFT_SSM}[kind]
     cfg, t = wl.build_draft_bundle(w, seed=seed)
     g = torch.Generator().manual_seed(9)
     for k in ("router_prev_norm", "router_cur_norm", "q_norm", "out_norm", "mem_norm"):
         t[k] = (1 + 0.2 * torch.randn(t[k].shape, generator=g)).to(t[k].dtype)
     return cfg, t
+
+
+def _gpu(kind, cfg, t, dev, **kw) -> GpuDrafter:
+    """sdb: per-token tables (two launches per readout); sdb_generic / sdc: the general kernels."""
+    g = GpuDrafter((cfg, t), device=dev, tables=kind == "sdb", **kw)
+    assert (g.luts is not None) == (kind == "sdb")
+    return g
 
 
 def _oracle_codes_and_ties(o: od.DrafterOracle, toks: list):
@@ -51,13 +61,13 @@ def _oracle_codes_and_ties(o: od.DrafterOracle, toks: list):
     return o.committed_codes(), np.stack(ties)
 
 
-@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+@pytest.mark.parametrize("kind", KINDS)
 def test_commit_codes_match_oracle(dev, kind):
     cfg, t = _bundle(kind)
     toks = torch.randint(0, cfg["vocab"], (70,), generator=torch.Generator().manual_seed(1)).tolist()
     o = od.DrafterOracle(cfg, t)
     want, ties = _oracle_codes_and_ties(o, toks)
-    g = GpuDrafter((cfg, t), device=dev, max_len=128)
+    g = _gpu(kind, cfg, t, dev, max_len=128)
     g.commit(toks[:33])
     g.commit(toks[33:])                      # in two pieces: the second continues the first
     got = g.committed_codes()
@@ -69,13 +79,13 @@ def test_commit_codes_match_oracle(dev, kind):
         np.testing.assert_allclose(s_got, s_want, rtol=1e-5, atol=1e-6)
 
 
-@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+@pytest.mark.parametrize("kind", KINDS)
 def test_trace_logits_match_oracle(dev, kind):
     cfg, t = _bundle(kind)
     toks = torch.randint(0, cfg["vocab"], (37,), generator=torch.Generator().manual_seed(2)).tolist()
     o = od.DrafterOracle(cfg, t)
     codes, lg = o.trace(toks)
-    g = GpuDrafter((cfg, t), device=dev, max_len=64)
+    g = _gpu(kind, cfg, t, dev, max_len=64)
     c_got, ids, l_got = g.trace(toks, codes=codes)
     np.testing.assert_array_equal(c_got, codes)
     assert ids.shape == (37, cfg["vocab"]) and (ids[0] == np.arange(cfg["vocab"])).all()
@@ -84,7 +94,7 @@ def test_trace_logits_match_oracle(dev, kind):
     assert g.length == 0                     # trace leaves the committed state alone
 
 
-@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("online", [False, True])
 def test_draft_matches_oracle(dev, kind, online):
     cfg, t = _bundle(kind)
@@ -95,7 +105,7 @@ def test_draft_matches_oracle(dev, kind, online):
     codes, _ = _oracle_codes_and_ties(od.DrafterOracle(cfg, t), toks)
     o.reset()
     o.commit(toks, codes=codes)
-    g = GpuDrafter((cfg, t), device=dev, max_len=96, online=online)
+    g = _gpu(kind, cfg, t, dev, max_len=96, online=online)
     g.commit(toks, codes=codes)
     for hyp, gamma, k, last in (((), 4, 3, False), (tuple(pat[3:5]), 3, 4, True), ((), 1, 1, False)):
         want = o.draft(gamma, hyp=hyp, topk=k, last_codes=last)
@@ -112,7 +122,7 @@ def test_draft_matches_oracle(dev, kind, online):
     assert g.draft(3).tokens == o2.draft(3).tokens
 
 
-@pytest.mark.parametrize("kind", ["sdb", "sdc"])
+@pytest.mark.parametrize("kind", KINDS)
 @pytest.mark.parametrize("online", [False, True])
 def test_draft_tree_and_verify_gather_match_oracle(dev, kind, online):
     cfg, t = _bundle(kind)
@@ -120,7 +130,7 @@ def test_draft_tree_and_verify_gather_match_oracle(dev, kind, online):
     codes, _ = _oracle_codes_and_ties(od.DrafterOracle(cfg, t), toks)
     o = od.DrafterOracle(cfg, t, online=online)
     o.commit(toks, codes=codes)
-    g = GpuDrafter((cfg, t), device=dev, max_len=64, online=online)
+    g = _gpu(kind, cfg, t, dev, max_len=64, online=online)
     g.commit(toks, codes=codes)
     for spec in (SPEC16, dtree.default_tree(), dtree.chain_tree(5)):
         ospec = od.TreeSpec(spec.parent, spec.rank)
