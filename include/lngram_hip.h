@@ -177,6 +177,7 @@ int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int
 #define LNG_DR_MAX_CH 8
 #define LNG_DR_MAX_P 16
 #define LNG_DR_MAX_K 8
+#define LNG_DR_SYNC_INTS 4160  /* int32 entries of lng_drafter.sync */
 
 typedef struct lng_drafter {
   int32_t d, V, R, bits, mem_dim, dt, n_orders, orders[4], maxn;
@@ -211,7 +212,8 @@ typedef struct lng_drafter {
    *   gram_out  [q_heads*hd, q_heads*hd] fp32   W_o^T W_o
    *   wv_t      [kv_heads, Dt, hd] (wv_dtype)   Wv[h]^T, the value rows of kv_proj transposed
    *   mem_norm  [Dt] fp32   readout_memory_norm weight
-   *   sync      int32 [64], zero before the first call; every call leaves it zero. */
+   *   sync      int32 [LNG_DR_SYNC_INTS], zero before the first call; every call leaves it
+   *             zero (block counters, online totals and per-block candidate counts). */
   const float* lut_prev;
   const float* lut_cur;
   const float* lut_start;

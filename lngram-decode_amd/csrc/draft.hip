@@ -791,49 +791,68 @@ __device__ __forceinline__ float row16_sum(float v) {
 constexpr int SY_ATT = 0;    // [16] attention-launch block counters, per position
 constexpr int SY_LOG = 16;   // logits-launch block counter
 constexpr int SY_TOT = 32;   // [16] online weight totals, per position
-constexpr int SY_NC = 48;    // [16] online candidates appended, per position
+constexpr int SY_NNZ = 64;   // [16][256] count-bearing tokens per (position, logits block)
+constexpr int SY_NNZ_STRIDE = 256;
+static_assert(SY_NNZ + DR_MAXP * SY_NNZ_STRIDE == LNG_DR_SYNC_INTS, "sync layout");
 
-constexpr int FS_CAND = 8192;      // online candidates per position (tokens with counts)
-
-// Per-lane top-K list, sorted by (score desc, id asc); empty slots hold (-inf, INT_MAX).
+// Per-lane top-KM list, sorted by (score desc, id asc); empty slots hold (-inf, INT_MAX).
+template <int KM>
 struct TopK {
-  float v[DR_MAXK];
-  int i[DR_MAXK];
+  float v[KM];
+  int i[KM];
   __device__ __forceinline__ void clear() {
 #pragma unroll
-    for (int k = 0; k < DR_MAXK; ++k) v[k] = -INFINITY, i[k] = INT_MAX;
+    for (int k = 0; k < KM; ++k) v[k] = -INFINITY, i[k] = INT_MAX;
   }
-  __device__ __forceinline__ void insert(float x, int id, int K) {
+  __device__ __forceinline__ void insert(float x, int id) {
 #pragma unroll
-    for (int k = 0; k < DR_MAXK; ++k) {
-      if (k < K && (x > v[k] || (x == v[k] && id < i[k]))) {
-        const float tv = v[k];
-        const int ti = i[k];
-        v[k] = x, i[k] = id;
-        x = tv, id = ti;
-      }
+    for (int k = 0; k < KM; ++k) {
+      const bool sw = x > v[k] || (x == v[k] && id < i[k]);
+      const float tv = v[k];
+      const int ti = i[k];
+      v[k] = sw ? x : tv;
+      i[k] = sw ? id : ti;
+      x = sw ? tv : x;
+      id = sw ? ti : id;
     }
   }
   __device__ __forceinline__ void pop() {
 #pragma unroll
-    for (int k = 0; k + 1 < DR_MAXK; ++k) v[k] = v[k + 1], i[k] = i[k + 1];
-    v[DR_MAXK - 1] = -INFINITY, i[DR_MAXK - 1] = INT_MAX;
+    for (int k = 0; k + 1 < KM; ++k) v[k] = v[k + 1], i[k] = i[k + 1];
+    v[KM - 1] = -INFINITY, i[KM - 1] = INT_MAX;
   }
 };
 
-// K rounds of wave argmax over the lanes' lists -> sel_v/sel_i (lane 0 holds them all).
-__device__ __forceinline__ void wave_select(TopK& t, int K, float* sel_v, int* sel_i) {
-  for (int k = 0; k < K; ++k) {
-    float bv = t.v[0];
-    int bi = t.i[0];
-    for (int off = 32; off > 0; off >>= 1) {
-      const float ov = __shfl_xor(bv, off, 64);
-      const int oi = __shfl_xor(bi, off, 64);
-      if (ov > bv || (ov == bv && oi < bi)) bv = ov, bi = oi;
-    }
-    sel_v[k] = bi == INT_MAX ? -INFINITY : bv;
-    sel_i[k] = bi == INT_MAX ? -1 : bi;
-    if (t.i[0] == bi && bi != INT_MAX) t.pop();
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x111, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x112, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x114, 0xf, 0xf, false));
+  v = min(v, __builtin_amdgcn_update_dpp(INT_MAX, v, 0x118, 0xf, 0xf, false));
+  return min(min(__builtin_amdgcn_readlane(v, 15), __builtin_amdgcn_readlane(v, 31)),
+             min(__builtin_amdgcn_readlane(v, 47), __builtin_amdgcn_readlane(v, 63)));
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+  return (__builtin_amdgcn_readlane(v, 15) + __builtin_amdgcn_readlane(v, 31)) +
+         (__builtin_amdgcn_readlane(v, 47) + __builtin_amdgcn_readlane(v, 63));
+}
+
+// KM rounds of wave argmax (largest score, then smallest id) over the lanes' lists: sv/si receive
+// the wave's top-KM in order, identical in every lane; (-inf, -1) where fewer entries exist.  Ids
+// are distinct across the wave.  Call from converged code.
+template <int KM>
+__device__ __forceinline__ void wave_topk(TopK<KM>& t, float* sv, int* si) {
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    const float m = wave_max(t.v[0]);
+    const int id = wave_min_i(t.v[0] == m ? t.i[0] : INT_MAX);
+    sv[k] = id == INT_MAX ? -INFINITY : m;
+    si[k] = id == INT_MAX ? -1 : id;
+    if (t.i[0] == id && id != INT_MAX) t.pop();
   }
 }
 
@@ -1173,7 +1192,12 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
       if (threadIdx.x < nt) {
         const int t = t0 + threadIdx.x;
         s = (red[0][threadIdx.x] + red[1][threadIdx.x]) + (red[2][threadIdx.x] + red[3][threadIdx.x]);
-        if (s > 0) atomicAdd(&counts[static_cast<int64_t>(j) * D.V + D.tokens[t + 1]], s);
+        if (s > 0) {
+          // a token's first count also counts it in its logits block (dense candidate offsets)
+          const int64_t tok = D.tokens[t + 1];
+          if (atomicAdd(&counts[static_cast<int64_t>(j) * D.V + tok], s) == 0)
+            atomicAdd(&D.sync[SY_NNZ + j * SY_NNZ_STRIDE + static_cast<int>(tok / FL_VB)], 1);
+        }
       }
       // the block's total weight (exact integer) into the position's total
       const float bs = block_sum256(static_cast<float>(s), redf);
@@ -1240,27 +1264,70 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   for (int e = threadIdx.x; e < I; e += 256) ro[static_cast<int64_t>(j) * I + e] = rn * us[e];
 }
 
-// grid (nblk): scores of a slice of FL_VB vocabulary rows for every position against lut_out (fp32
-// MFMA), per position the slice's max, sum of exponentials and top-K by logit among tokens without
-// online counts; tokens with counts go to the position's candidate list (their counts are read
-// and returned to zero here).  The last block selects every position's top-K (wave per position:
-// by logit, or by the online-mixed probability) and writes the children's tokens.
+// grid (nblk <= 256): scores of a slice of FL_VB vocabulary rows for every position against lut_out
+// (fp32 MFMA).  Per (position, block) the record lpart[j][b] = [max, sum of exponentials, number of
+// tokens with online counts, -, top-KM logits, top-KM ids] over the slice's tokens without counts.
+// The tokens with counts go to the position's dense list cand[j][0 .. n) as (id, logit bits,
+// count, 0), block b from the prefix of the per-block numbers that the attention launch counted
+// (sync[SY_NNZ]); their counts are returned to zero here.  The last block selects every
+// position's top-K: G = 4 / P waves per position when P <= 2, else one (positions w, w + 4, ...);
+// each wave ranks every block's top-KM and its share of the list, by logit or by the
+// online-mixed probability (1 - lam) softmax + lam count / total (the log is taken of the
+// winners only), then writes the children's tokens.
+constexpr int FL_NBL = 4;     // blocks per lane in the selection: nblk <= 256
+constexpr int FL_CH = 12;     // count-bearing tokens per lane per load batch
+static_assert(FL_NBL * 64 == SY_NNZ_STRIDE, "one counter per logits block");
+
+// Count-bearing tokens of one position in the logits blocks before block b (nnz: that position's
+// per-block counters).  Every lane receives it.
+__device__ __forceinline__ int fl_prefix(const int32_t* nnz, int b, int lane) {
+  int s = 0;
+#pragma unroll
+  for (int q = 0; q < FL_NBL; ++q) {
+    const int bb = FL_NBL * lane + q;
+    const int v = nnz[bb];
+    s += bb < b ? v : 0;
+  }
+  return wave_sum_i(s);
+}
+
+template <int KM>
+__host__ __device__ constexpr int fl_rs() { return 4 + 2 * KM; }
+
+template <int KM>
 __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, int32_t K, int32_t online, float kappa,
                                                      const float* __restrict__ ro, float* __restrict__ logits_out,
                                                      float* __restrict__ lpart, int32_t* __restrict__ counts,
-                                                     int32_t* __restrict__ cand, DrChildren C,
+                                                     int4* __restrict__ cand, DrChildren C,
                                                      int64_t* __restrict__ ids, float* __restrict__ scores) {
+  constexpr int RS = fl_rs<KM>();
   __shared__ __attribute__((aligned(16))) float rs[DR_MAXP][FL_I];
   __shared__ float lt[DR_MAXP][FL_VB];
   __shared__ int last_flag;
-  __shared__ float sel_v[4][DR_MAXK];
-  __shared__ int sel_i[4][DR_MAXK];
+  __shared__ float sel_v[4][KM];
+  __shared__ int sel_i[4][KM];
   const int I = D.q_heads * D.head_dim;
   const int64_t V = D.V;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * FL_VB;
+  const int64_t va = v0 + lane, vb = v0 + 64 + lane;
+  // kernel-argument children (one per lane) and the online total of the position this wave selects
+  // for: loaded here, used by the last block
+  const int c_row = lane < C.n ? C.row[lane] : 0;
+  const int c_par = lane < C.n ? C.parent[lane] : -1;
+  const int c_rank = lane < C.n ? C.rank[lane] : 0;
+  const int G = P == 1 ? 4 : (P == 2 ? 2 : 1);  // selection waves per position
+  const int tot0 = online && w / G < P ? D.sync[SY_TOT + w / G] : 0;
+  // online counts of this wave's first position: in flight during the products
+  int ca = 0, cb = 0, pre0 = 0;
+  if (online && w < P) {
+    const int32_t* cj = counts + static_cast<int64_t>(w) * V;
+    ca = va < V ? cj[va] : 0;
+    cb = vb < V ? cj[vb] : 0;
+    pre0 = fl_prefix(D.sync + SY_NNZ + w * SY_NNZ_STRIDE, blockIdx.x, lane);
+  }
   for (int e = threadIdx.x; e < P * I; e += 256) rs[e / I][e % I] = ro[e];
   __syncthreads();
-  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * FL_VB;
   // fp32 MFMA 16x16x4: D[row][j] += sum_k EO[row][k] ro[j][k].  Lane l feeds A[row l%16][k-slot
   // l/16] and B[k-slot l/16][column l%16]; k-slot l/16 of step (s, q) is feature 16s + 4(l/16) + q
   // (A and B use the same feature order, so the sum is unchanged).  Wave w: tiles 2w, 2w+1.
@@ -1299,138 +1366,156 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
   }
   __syncthreads();
   const int nblk = gridDim.x;
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
   for (int jj = w; jj < P; jj += 4) {
-    float* o = lpart + (static_cast<int64_t>(jj) * nblk + blockIdx.x) * (2 + 2 * K);
+    float* o = lpart + (static_cast<int64_t>(jj) * nblk + blockIdx.x) * RS;
     const float x0 = lt[jj][lane], x1 = lt[jj][lane + 64];
-    const float m = wave_max(fmaxf(x0, x1));
-    const float s = wave_sum((x0 == -INFINITY ? 0.f : expf(x0 - m)) + (x1 == -INFINITY ? 0.f : expf(x1 - m)));
-    const int64_t va = v0 + lane, vb = v0 + 64 + lane;
-    int ca = 0, cb = 0;
-    if (online) {
-      int32_t* cj = counts + static_cast<int64_t>(jj) * V;
+    if (online && jj != w) {
+      const int32_t* cj = counts + static_cast<int64_t>(jj) * V;
       ca = va < V ? cj[va] : 0;
       cb = vb < V ? cj[vb] : 0;
-      // tokens with counts: append (id, logit bits, count) to the position's list, clear the count
+    }
+    const float m = wave_max(fmaxf(x0, x1));
+    const float s = wave_sum((x0 == -INFINITY ? 0.f : expf(x0 - m)) + (x1 == -INFINITY ? 0.f : expf(x1 - m)));
+    int nbk = 0;
+    if (online) {
+      // tokens with counts: (id, logit bits, count) into the position's list, counts cleared
+      int32_t* cj = counts + static_cast<int64_t>(jj) * V;
+      // (at most FL_VB per earlier block: stays inside the list whatever the counters hold)
+      const int pre = min(jj == w ? pre0 : fl_prefix(D.sync + SY_NNZ + jj * SY_NNZ_STRIDE, blockIdx.x, lane),
+                          FL_VB * static_cast<int>(blockIdx.x));
+      int4* dst = cand + static_cast<int64_t>(jj) * nblk * FL_VB + pre;
       const uint64_t ma = __ballot(ca > 0), mb = __ballot(cb > 0);
-      const int na = __popcll(ma), nb = __popcll(mb);
-      if (na + nb > 0) {
-        int base = 0;
-        if (lane == 0) base = atomicAdd(&D.sync[SY_NC + jj], na + nb);
-        base = __shfl(base, 0, 64);
-        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-        if (ca > 0 && base + __popcll(ma & below) < FS_CAND) {
-          const int slot = base + __popcll(ma & below);
-          int32_t* c3 = cand + (static_cast<int64_t>(jj) * FS_CAND + slot) * 3;
-          c3[0] = static_cast<int32_t>(va);
-          c3[1] = __float_as_int(x0);
-          c3[2] = ca;
-          cj[va] = 0;
-        }
-        if (cb > 0 && base + na + __popcll(mb & below) < FS_CAND) {
-          const int slot = base + na + __popcll(mb & below);
-          int32_t* c3 = cand + (static_cast<int64_t>(jj) * FS_CAND + slot) * 3;
-          c3[0] = static_cast<int32_t>(vb);
-          c3[1] = __float_as_int(x1);
-          c3[2] = cb;
-          cj[vb] = 0;
-        }
+      const int na = __popcll(ma);
+      nbk = na + __popcll(mb);
+      if (ca > 0) {
+        dst[__popcll(ma & below)] = int4{static_cast<int>(va), __float_as_int(x0), ca, 0};
+        cj[va] = 0;
+      }
+      if (cb > 0) {
+        dst[na + __popcll(mb & below)] = int4{static_cast<int>(vb), __float_as_int(x1), cb, 0};
+        cj[vb] = 0;
       }
     }
+    TopK<KM> t;
+    t.clear();
+    // (-inf, INT_MAX) never enters a list: the inserts need no branch
+    const bool oka = x0 != -INFINITY && ca == 0, okb = x1 != -INFINITY && cb == 0;
+    t.insert(oka ? x0 : -INFINITY, oka ? static_cast<int>(va) : INT_MAX);
+    t.insert(okb ? x1 : -INFINITY, okb ? static_cast<int>(vb) : INT_MAX);
+    float sv[KM];
+    int si[KM];
+    wave_topk(t, sv, si);
     if (lane == 0) {
       o[0] = m;
       o[1] = s;
-    }
-    TopK t;
-    t.clear();
-    if (x0 != -INFINITY && ca == 0) t.insert(x0, static_cast<int>(va), K);
-    if (x1 != -INFINITY && cb == 0) t.insert(x1, static_cast<int>(vb), K);
-    float sv[DR_MAXK];
-    int si[DR_MAXK];
-    wave_select(t, K, sv, si);
-    if (lane == 0)
-      for (int k = 0; k < K; ++k) {
-        o[2 + k] = sv[k];
-        o[2 + K + k] = __int_as_float(si[k]);
+      o[2] = __int_as_float(nbk);
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        o[4 + k] = sv[k];
+        o[4 + KM + k] = __int_as_float(si[k]);
       }
+    }
   }
   if (!dr_last_block(&D.sync[SY_LOG], nblk, &last_flag)) return;
-  // ---------------- selection: wave w handles positions w, w + 4, ...
-  for (int j = w; j < P; j += 4) {
-    const float* lp = lpart + static_cast<int64_t>(j) * nblk * (2 + 2 * K);
-    constexpr int NB = 4;  // records per lane (nblk <= 256)
-    float rm[NB], rsum[NB];
+  // ---------------- selection
+  const int g = w % G;
+  for (int j = w / G; j < P; j += 4 / G) {
+    const float* lp = lpart + static_cast<int64_t>(j) * nblk * RS;
+    // records of blocks 4 lane + q (all in flight at once)
+    float rm[FL_NBL], rsm[FL_NBL], av[FL_NBL][KM];
+    int rnb[FL_NBL], ai[FL_NBL][KM];
 #pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const int b = lane + 64 * q;
-      rm[q] = b < nblk ? lp[b * (2 + 2 * K)] : -INFINITY;
-      rsum[q] = b < nblk ? lp[b * (2 + 2 * K) + 1] : 0.f;
+    for (int q = 0; q < FL_NBL; ++q) {
+      // unconditional loads (block index clamped into the records), then masked
+      const int b = FL_NBL * lane + q;
+      const bool ok = b < nblk;
+      const float* rec = lp + static_cast<int64_t>(min(b, nblk - 1)) * RS;
+      const float r0 = rec[0], r1 = rec[1], r2 = rec[2];
+      rm[q] = ok ? r0 : -INFINITY;
+      rsm[q] = ok ? r1 : 0.f;
+      rnb[q] = ok && online ? __float_as_int(r2) : 0;
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        const bool mine = ok && q % G == g;
+        const float x = rec[4 + k], id = rec[4 + KM + k];
+        av[q][k] = mine ? x : -INFINITY;
+        ai[q][k] = mine ? __float_as_int(id) : -1;
+      }
     }
     float m = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < NB; ++q) m = fmaxf(m, rm[q]);
+    for (int q = 0; q < FL_NBL; ++q) m = fmaxf(m, rm[q]);
     const float M = wave_max(m);
     float s = 0.f;
 #pragma unroll
-    for (int q = 0; q < NB; ++q) s += rm[q] == -INFINITY ? 0.f : rsum[q] * expf(rm[q] - M);
+    for (int q = 0; q < FL_NBL; ++q) s += rm[q] == -INFINITY ? 0.f : rsm[q] * expf(rm[q] - M);
     const float S = wave_sum(s);
-    const float tj = online ? static_cast<float>(D.sync[SY_TOT + j]) : 0.f;
+    const float tj = online ? static_cast<float>(j == w / G ? tot0 : D.sync[SY_TOT + j]) : 0.f;
     const float n_eff = tj / static_cast<float>(D.R * D.n_orders);
     const float lam = tj > 0.f ? n_eff / (n_eff + kappa) : 0.f;
-    auto mixed = [&](float lg, float cnt) {
-      return logf((1.f - lam) * expf(lg - M) / S + (tj > 0.f ? lam * cnt / tj : 0.f));
-    };
-    TopK t;
+    // online ranking value: (1 - lam) exp(logit - M) / S + lam count / total (log taken at the end)
+    const float mix_a = (1.f - lam) / S, mix_b = tj > 0.f ? lam / tj : 0.f;
+    TopK<KM> t;
     t.clear();
-    // candidates A: every block's top-K among tokens without counts (all loads in flight)
-    float av[NB][DR_MAXK];
-    int ai[NB][DR_MAXK];
 #pragma unroll
-    for (int q = 0; q < NB; ++q) {
-      const int b = lane + 64 * q;
+    for (int q = 0; q < FL_NBL; ++q)
 #pragma unroll
-      for (int k = 0; k < DR_MAXK; ++k) {
-        const bool ok = b < nblk && k < K;
-        av[q][k] = ok ? lp[b * (2 + 2 * K) + 2 + k] : -INFINITY;
-        ai[q][k] = ok ? __float_as_int(lp[b * (2 + 2 * K) + 2 + K + k]) : -1;
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < NB; ++q)
-#pragma unroll
-      for (int k = 0; k < DR_MAXK; ++k)
-        if (ai[q][k] >= 0) t.insert(online ? mixed(av[q][k], 0.f) : av[q][k], ai[q][k], K);
+      for (int k = 0; k < KM; ++k)
+        t.insert(ai[q][k] < 0 ? -INFINITY : online ? mix_a * expf(av[q][k] - M) : av[q][k],
+                 ai[q][k] < 0 ? INT_MAX : ai[q][k]);
     if (online) {
-      // candidates B: tokens with online counts
-      const int nc = min(D.sync[SY_NC + j], FS_CAND);
-      for (int e0 = 0; e0 < nc; e0 += 64 * 8) {
-        int cid[8], ccn[8];
-        float clg[8];
+      // the position's count-bearing tokens: e = 64 (G t + g) + lane
+      const int nc = wave_sum_i((rnb[0] + rnb[1]) + (rnb[2] + rnb[3]));
+      if (g == 0)  // every block has read the per-block counters: clear them for the next call
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int e = e0 + q * 64 + lane;
-          const int32_t* c3 = cand + (static_cast<int64_t>(j) * FS_CAND + e) * 3;
-          cid[q] = e < nc ? c3[0] : -1;
-          clg[q] = e < nc ? __int_as_float(c3[1]) : 0.f;
-          ccn[q] = e < nc ? c3[2] : 0;
+        for (int q = 0; q < FL_NBL; ++q) D.sync[SY_NNZ + j * SY_NNZ_STRIDE + FL_NBL * lane + q] = 0;
+      const int4* cj = cand + static_cast<int64_t>(j) * nblk * FL_VB;
+      for (int e0 = 64 * g; e0 < nc; e0 += 64 * G * FL_CH) {
+        int4 cr[FL_CH];
+#pragma unroll
+        for (int u = 0; u < FL_CH; ++u) cr[u] = cj[min(e0 + 64 * G * u + lane, nc - 1)];
+#pragma unroll
+        for (int u = 0; u < FL_CH; ++u) {
+          const bool ok = e0 + 64 * G * u + lane < nc;
+          t.insert(ok ? fmaf(mix_b, static_cast<float>(cr[u].z), mix_a * expf(__int_as_float(cr[u].y) - M)) : -INFINITY,
+                   ok ? cr[u].x : INT_MAX);
         }
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-          if (cid[q] >= 0) t.insert(mixed(clg[q], static_cast<float>(ccn[q])), cid[q], K);
       }
     }
-    wave_select(t, K, sel_v[w], sel_i[w]);
+    float sv[KM];
+    int si[KM];
+    wave_topk(t, sv, si);
+    if (G > 1) {
+      // merge the group's lists: wave g == 0 ranks the G * KM winners again
+      if (lane == 0)
+#pragma unroll
+        for (int k = 0; k < KM; ++k) sel_v[w][k] = sv[k], sel_i[w][k] = si[k];
+      __syncthreads();
+      if (g != 0) continue;
+      t.clear();
+      if (lane < G * KM && sel_i[w + lane / KM][lane % KM] >= 0)
+        t.insert(sel_v[w + lane / KM][lane % KM], sel_i[w + lane / KM][lane % KM]);
+      wave_topk(t, sv, si);
+      __builtin_amdgcn_wave_barrier();
+    }
+    if (lane == 0)
+#pragma unroll
+      for (int k = 0; k < KM; ++k) {
+        sel_v[w][k] = online ? (si[k] >= 0 ? logf(sv[k]) : -INFINITY) : sv[k];
+        sel_i[w][k] = si[k];
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     if (lane < K) {
       ids[static_cast<int64_t>(j) * K + lane] = sel_i[w][lane];
       scores[static_cast<int64_t>(j) * K + lane] = sel_v[w][lane];
     }
-    if (lane == 0 && online) {
-      D.sync[SY_TOT + j] = 0;
-      D.sync[SY_NC + j] = 0;
-    }
-    for (int e = lane; e < C.n; e += 64) {
-      if (C.parent[e] != j) continue;
-      const int t2 = sel_i[w][C.rank[e]];
-      D.tokens[C.row[e]] = t2 >= 0 ? t2 : sel_i[w][0];
+    if (lane == 0 && online) D.sync[SY_TOT + j] = 0;
+    if (c_par == j) {
+      const int t2 = sel_i[w][c_rank];
+      D.tokens[c_row] = t2 >= 0 ? t2 : sel_i[w][0];
     }
   }
 }
@@ -1528,7 +1613,7 @@ __global__ __launch_bounds__(256) void k_fast_gather(lng_drafter D, FastLevel F,
 namespace {
 
 struct DrLayout {
-  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, ncand, total;
+  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, total;
   int nch, nblk, fnch, fnblk;
 };
 
@@ -1558,9 +1643,8 @@ DrLayout dr_layout(const lng_drafter& D, int P, int K, int max_pairs) {
   l.fpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnch * (D.q_heads * D.head_dim + D.q_heads * I + 2 * D.q_heads));
   l.ro = take(sizeof(float) * P * I);
   l.tot = 0;
-  l.flpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnblk * (2 + 2 * K));
-  l.cand = take(sizeof(int32_t) * static_cast<size_t>(P) * FS_CAND * 3);
-  l.ncand = 0;
+  l.flpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnblk * fl_rs<DR_MAXK>());
+  l.cand = take(sizeof(int4) * static_cast<size_t>(P) * l.fnblk * FL_VB);
   l.total = off;
   return l;
 }
@@ -1569,7 +1653,7 @@ bool dr_fast(const lng_drafter& D) {
   const int I = D.q_heads * D.head_dim;
   return D.lut_prev && D.lut_cur && D.lut_start && D.lut_qk && D.lut_out && D.gram_out && D.wv_t && D.sync &&
          !D.router_ssm && !D.query_ssm && I <= FL_I && I % 16 == 0 && D.dt % 64 == 0 &&
-         static_cast<int64_t>(D.V) * DR_MAXK <= 524288;
+         cdiv(D.V, FL_VB) <= FL_NBL * 64;
 }
 
 int dr_check(const lng_drafter* D, const char* what) {
@@ -1641,14 +1725,23 @@ int dr_readout_fast(const lng_drafter& D, const FastLevel& F, int K, int online,
   if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter: workspace too small");
   if (online && !counts) return fail(LNG_E_ARG, "drafter: online counts need the counts buffer");
   const int nob = online ? static_cast<int>(cdiv(max_pairs, FA_TB)) : 0;
-  if (online && D.rows > FS_CAND + 1) return fail(LNG_E_ARG, "drafter: online counts cover at most 8192 pairs");
   hipLaunchKernelGGL(k_fast_attend, dim3(static_cast<unsigned>(l.fnch + nob), static_cast<unsigned>(P)), dim3(256), 0, s,
                      D, F, l.fnch, nob, online, reinterpret_cast<float*>(work + l.fpart), counts,
                      reinterpret_cast<float*>(work + l.ro));
   if (int rc = check_launch("drafter_readout(fast attend)")) return rc;
-  hipLaunchKernelGGL(k_fast_logits, dim3(static_cast<unsigned>(l.fnblk)), dim3(256), 0, s, D, P, K, online, kappa,
-                     reinterpret_cast<const float*>(work + l.ro), logits_out, reinterpret_cast<float*>(work + l.flpart),
-                     counts, reinterpret_cast<int32_t*>(work + l.cand), C, ids, scores);
+  auto logits = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(l.fnblk)), dim3(256), 0, s, D, P, K, online, kappa,
+                       reinterpret_cast<const float*>(work + l.ro), logits_out,
+                       reinterpret_cast<float*>(work + l.flpart), counts, reinterpret_cast<int4*>(work + l.cand), C,
+                       ids, scores);
+  };
+  switch (K) {
+    case 1: logits(k_fast_logits<1>); break;
+    case 2: logits(k_fast_logits<2>); break;
+    case 3: logits(k_fast_logits<3>); break;
+    case 4: logits(k_fast_logits<4>); break;
+    default: logits(k_fast_logits<DR_MAXK>); break;
+  }
   return check_launch("drafter_readout(fast logits)");
 }
 

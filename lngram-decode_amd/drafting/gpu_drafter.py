@@ -179,7 +179,7 @@ class GpuDrafter:
         lut["mem_norm"] = t["mem_norm"].to(dev, torch.float32).contiguous()
         self.wv_dtype = ops.dtype_code(wdt)
         self.luts = lut
-        self.sync = torch.zeros(64, dtype=torch.int32, device=dev)
+        self.sync = torch.zeros(_lib.DR_SYNC_INTS, dtype=torch.int32, device=dev)
         del ef
 
     def _descriptor(self, tok, codes, ssm, length, rows) -> _lib.Drafter:
@@ -261,8 +261,6 @@ class GpuDrafter:
             L = self.length
             if L + n > self.max_len:
                 raise ValueError(f"context full: {L} + {n} > {self.max_len}")
-            if self.online and L + n > 8193:
-                raise ValueError("online counts cover at most 8192 committed pairs")
             self.tok_d[L:L + n] = torch.tensor(toks, dtype=torch.int64).to(self.device)
             if codes is not None:
                 ca = np.asarray(codes)

@@ -27,6 +27,7 @@ _P64 = ctypes.POINTER(ctypes.c_int64)
 _P32 = ctypes.POINTER(ctypes.c_int32)
 
 ROW_NONE = -2147483648  # LNG_ROW_NONE
+DR_SYNC_INTS = 4160  # LNG_DR_SYNC_INTS
 
 
 class Drafter(ctypes.Structure):
