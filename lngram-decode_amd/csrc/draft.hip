@@ -760,22 +760,35 @@ __device__ __forceinline__ int dr_lut_code(const lng_drafter& D, int64_t ptok, i
   return code;
 }
 
-// Block-wide "am I the last block of this group" after every block wrote its results.  The
-// barrier drains the block's stores to L2; thread 0 releases them at agent scope (L2 write-back)
-// and counts the block in; the last block resets the counter and acquires the other blocks'
-// results (every wave invalidates its caches).
+// Records that one block hands to the last block of its group go through the device-coherent
+// level: agent-scope relaxed stores and loads (sc1 on gfx950) bypass the XCD-private L2 copies,
+// so the hand-off needs no L2 write-back (buffer_wbl2) per block and no L2 invalidate in the
+// reader.  Every block's threads wait until their coherent stores are complete (vmcnt(0)), the
+// barrier collects the block, thread 0 counts it in; the last block resets the counter.
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(int32_t* p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int32_t ld_dev(const int32_t* p) {
+  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+constexpr int WAITCNT_VM0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt left open
+
 __device__ __forceinline__ bool dr_last_block(int32_t* counter, int32_t total, int* flag) {
+  __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
   __syncthreads();
   if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     const int old = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *flag = old == total - 1;
     if (*flag) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
-  if (*flag == 0) return false;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  return true;
+  return *flag != 0;
 }
 
 // Sum over each 16-lane row (DPP row_shr:1,2,4,8 inclusive scan): valid in lanes 15, 31, 47, 63.
@@ -1088,7 +1101,7 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
         const int qh = e / hd, oe = e % hd;
         float a = 0.f;
         for (int rb = 0; rb < nrb; ++rb) a += ob[(qh * nrb + rb) * hd + oe];
-        rec[e] = a;
+        st_dev(rec + e, a);
         us[e] = a;  // o_c, reused below
       }
     }
@@ -1113,11 +1126,12 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
           y[3] = fmaf(gv[q][3], oe, y[3]);
         }
       }
-      *reinterpret_cast<f32x4*>(rec + I + qh * I + 4 * k4) = y;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) st_dev(rec + I + qh * I + 4 * k4 + q, y[q]);
     }
     if (threadIdx.x < QH) {
-      rec[I + QH * I + threadIdx.x] = ml[threadIdx.x][0];
-      rec[I + QH * I + QH + threadIdx.x] = ml[threadIdx.x][1];
+      st_dev(rec + I + QH * I + threadIdx.x, ml[threadIdx.x][0]);
+      st_dev(rec + I + QH * I + QH + threadIdx.x, ml[threadIdx.x][1]);
     }
   } else {
     // ---------------- online counts over pairs [t0, t0 + FA_TB) (thread = route)
@@ -1216,8 +1230,8 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
     float pm[FA_MAXCH], pl[FA_MAXCH];
 #pragma unroll
     for (int c = 0; c < FA_MAXCH; ++c) {
-      pm[c] = c < nch ? rj[c * RS + I + QH * I + qh] : -INFINITY;
-      pl[c] = c < nch ? rj[c * RS + I + QH * I + QH + qh] : 0.f;
+      pm[c] = c < nch ? ld_dev(rj + c * RS + I + QH * I + qh) : -INFINITY;
+      pl[c] = c < nch ? ld_dev(rj + c * RS + I + QH * I + QH + qh) : 0.f;
     }
     float M = b0;
 #pragma unroll
@@ -1240,7 +1254,7 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
     const int qh = e / hd;
     float ov[FA_MAXCH];
 #pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) ov[c] = c < nch ? rj[c * RS + e] : 0.f;
+    for (int c = 0; c < FA_MAXCH; ++c) ov[c] = c < nch ? ld_dev(rj + c * RS + e) : 0.f;
     float o = 0.f, y = 0.f;
 #pragma unroll
     for (int c = 0; c < FA_MAXCH; ++c) o = fmaf(c < nch ? wgt[c][qh] : 0.f, ov[c], o);
@@ -1249,7 +1263,7 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
 #pragma unroll
       for (int c = 0; c < FA_MAXCH; ++c)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) yv[c][q] = (c < nch && q0 + q < QH) ? rj[c * RS + I + (q0 + q) * I + e] : 0.f;
+        for (int q = 0; q < 4; ++q) yv[c][q] = (c < nch && q0 + q < QH) ? ld_dev(rj + c * RS + I + (q0 + q) * I + e) : 0.f;
 #pragma unroll
       for (int c = 0; c < FA_MAXCH; ++c)
 #pragma unroll
@@ -1389,11 +1403,17 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
       const int na = __popcll(ma);
       nbk = na + __popcll(mb);
       if (ca > 0) {
-        dst[__popcll(ma & below)] = int4{static_cast<int>(va), __float_as_int(x0), ca, 0};
+        int32_t* dp = reinterpret_cast<int32_t*>(dst + __popcll(ma & below));
+        st_dev(dp, static_cast<int32_t>(va));
+        st_dev(dp + 1, __float_as_int(x0));
+        st_dev(dp + 2, ca);
         cj[va] = 0;
       }
       if (cb > 0) {
-        dst[na + __popcll(mb & below)] = int4{static_cast<int>(vb), __float_as_int(x1), cb, 0};
+        int32_t* dp = reinterpret_cast<int32_t*>(dst + na + __popcll(mb & below));
+        st_dev(dp, static_cast<int32_t>(vb));
+        st_dev(dp + 1, __float_as_int(x1));
+        st_dev(dp + 2, cb);
         cj[vb] = 0;
       }
     }
@@ -1407,13 +1427,13 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
     int si[KM];
     wave_topk(t, sv, si);
     if (lane == 0) {
-      o[0] = m;
-      o[1] = s;
-      o[2] = __int_as_float(nbk);
+      st_dev(o, m);
+      st_dev(o + 1, s);
+      st_dev(o + 2, __int_as_float(nbk));
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
-        o[4 + k] = sv[k];
-        o[4 + KM + k] = __int_as_float(si[k]);
+        st_dev(o + 4 + k, sv[k]);
+        st_dev(o + 4 + KM + k, __int_as_float(si[k]));
       }
     }
   }
@@ -1431,14 +1451,14 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
       const int b = FL_NBL * lane + q;
       const bool ok = b < nblk;
       const float* rec = lp + static_cast<int64_t>(min(b, nblk - 1)) * RS;
-      const float r0 = rec[0], r1 = rec[1], r2 = rec[2];
+      const float r0 = ld_dev(rec), r1 = ld_dev(rec + 1), r2 = ld_dev(rec + 2);
       rm[q] = ok ? r0 : -INFINITY;
       rsm[q] = ok ? r1 : 0.f;
       rnb[q] = ok && online ? __float_as_int(r2) : 0;
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
         const bool mine = ok && q % G == g;
-        const float x = rec[4 + k], id = rec[4 + KM + k];
+        const float x = ld_dev(rec + 4 + k), id = ld_dev(rec + 4 + KM + k);
         av[q][k] = mine ? x : -INFINITY;
         ai[q][k] = mine ? __float_as_int(id) : -1;
       }
@@ -1474,7 +1494,10 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
       for (int e0 = 64 * g; e0 < nc; e0 += 64 * G * FL_CH) {
         int4 cr[FL_CH];
 #pragma unroll
-        for (int u = 0; u < FL_CH; ++u) cr[u] = cj[min(e0 + 64 * G * u + lane, nc - 1)];
+        for (int u = 0; u < FL_CH; ++u) {
+          const int32_t* cp = reinterpret_cast<const int32_t*>(cj + min(e0 + 64 * G * u + lane, nc - 1));
+          cr[u] = int4{ld_dev(cp), ld_dev(cp + 1), ld_dev(cp + 2), 0};
+        }
 #pragma unroll
         for (int u = 0; u < FL_CH; ++u) {
           const bool ok = e0 + 64 * G * u + lane < nc;
