@@ -124,6 +124,125 @@ def draft_step(dev, iters: int, warmup: int) -> dict:
             "algorithmic_bytes": alg, "achieved_GBs": alg / (med * 1e-6) / 1e9}
 
 
+def _time_steps(step, steps: int, warmup: int, *kernels: str):
+    """Mean wall ms per step over ``steps`` timed steps (after ``warmup``), bracketed by device
+    synchronisations, and the mean HIP-event ms of each named kernel over the timed steps."""
+    import contextlib
+
+    import torch
+
+    from lngram_hip import ops
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        with contextlib.ExitStack() as stack:
+            timers = {k: stack.enter_context(ops.KernelTimer(k)) for k in kernels}
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+    return el / steps * 1e3, {k: t.mean_ms() for k, t in timers.items()}
+
+
+def tiny_forward(dev, steps: int, warmup: int) -> dict:
+    """Tiny layer (d 128, 8 routes, mem_dim 32, fp32, 4 x 128 tokens): launch-bound, tokens/s only."""
+    import torch
+
+    from lngram_hip import ops, workloads
+
+    w = workloads.TINY
+    mem = workloads.build_memory(w, seed=0, device=dev)
+    h = workloads.make_hidden(w, seed=1, device=dev)
+    ones = torch.ones(w.d_model, device=dev)
+    ms, _ = _time_steps(lambda: mem(h, ops.rmsnorm(h, ones, w.norm_eps)), steps, warmup)
+    return {"workload": "tiny layer: d128, R8, mem_dim 32, 4 query heads x 32, fp32, 4 x 128 tokens, hidden router",
+            "tokens_per_s": w.tokens / (ms * 1e-3), "ms_per_step": ms,
+            "note": "launch-bound (512 tokens): the roofline fraction is not meaningful"}
+
+
+def sdc_forward(dev, steps: int, warmup: int) -> dict:
+    """SD-C layer: 8 x 4096 tokens, 181 routes; one step = diagonal SSM scan of u [8, 4096, 256] fp32
+    (decays U[0.9, 0.999]) + router features concat(RMSNorm(E[x_{t-1}]), RMSNorm(E[x_t]), s_t) from
+    token ids (V 32768, bf16) + memory forward (router GEMM 2304 -> 724 + sign-pack, query RMSNorm +
+    projection, fused gather + readout, output projection, causal conv)."""
+    import torch
+
+    from lngram_hip import workloads
+
+    w = workloads.SDC
+    mem = workloads.build_memory(w, seed=0, device=dev)
+    g = torch.Generator().manual_seed(7)
+    E = (torch.randn(w.vocab, w.d_model, generator=g) * 0.02).to(w.dtype).to(dev)
+    tok = torch.randint(0, w.vocab, (w.batch, w.seq), generator=g).to(dev)
+    a = (0.9 + 0.099 * torch.rand(w.ssm_dim, generator=g)).to(dev)
+    u = torch.randn(w.batch, w.seq, w.ssm_dim, generator=g).to(dev)
+    h = workloads.make_hidden(w, seed=1, device=dev)
+    feats = mem.router_features
+
+    def step():
+        from lngram_hip import ops
+        s = ops.ssm_scan(a, u)
+        x = feats.from_ids(tok, E, s)
+        return mem(h, None, router_in=x)
+
+    ms, kms = _time_steps(step, steps, warmup, "ssm_scan", "memory_readout_fused")
+    scan_ms, fused_ms = kms["ssm_scan"], kms["memory_readout_fused"]
+    n = w.tokens
+    scan_bytes = 2 * n * w.ssm_dim * 4
+    layer_bytes = n * w.algorithmic_bytes_per_token() + w.weight_bytes() + scan_bytes
+    fused_bytes = n * (w.routes * 2 * w.mem_dim * 2 + 2 * w.d_model * 2 + w.routes)
+    return {"workload": "SD-C layer: 8 x 4096 tokens, R181, d1024 bf16, 256-channel SSM scan (fp32) + embed2_ssm "
+                        "router features + memory forward",
+            "tokens_per_s": n / (ms * 1e-3), "ms_per_step": ms, "algorithmic_bytes": layer_bytes,
+            "layer_hbm_frac": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "scan": {"kernel": "k_ssm_chunk_end + k_ssm_apply", "avg_ms": scan_ms, "algorithmic_bytes": scan_bytes,
+                     "achieved_GBs": scan_bytes / (scan_ms * 1e-3) / 1e9,
+                     "hbm_frac": scan_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+            "readout": {"kernel": "k_readout_fused", "avg_ms": fused_ms, "algorithmic_bytes": fused_bytes,
+                        "achieved_GBs": fused_bytes / (fused_ms * 1e-3) / 1e9,
+                        "hbm_frac": fused_bytes / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+
+
+def scaled_gather(dev, steps: int, warmup: int) -> dict:
+    """Scaled-table stress: 16 x 4096 tokens, 184 routes, orders (2, 3), each route's order block
+    grown 64x (51,249,152 rows x 128 bf16 = 13.1 GB, HBM-resident), uniformly random codes; one
+    step = one gather + sum launch (one row per token, route and order; fp32 sums [16, 4096, 128])."""
+    import torch
+
+    from lngram_hip import ops
+
+    B, T, R, orders, sl, md = 16, 4096, 184, (2, 3), 6, 128
+    n2, n3 = R << (sl + 8), R << (sl + 12)
+    table = torch.empty(n2 + n3, md, dtype=torch.bfloat16, device=dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    for s0 in range(0, n2 + n3, 1 << 24):
+        blk = table[s0:s0 + (1 << 24)]
+        blk.normal_(0.0, 0.02, generator=g)
+    tabs = [table[:n2], table[n2:]]
+    codes = torch.randint(0, 16, (B, T, R), device=dev, dtype=torch.uint8)
+    for _ in range(warmup):
+        ops.gather_sum_scaled(tabs, codes, orders, 4, sl, seed=2024)
+    torch.cuda.synchronize()
+    with ops.KernelTimer("gather_sum_scaled") as kt:
+        for i in range(steps):
+            ops.gather_sum_scaled(tabs, codes, orders, 4, sl, seed=2024 + i)
+        torch.cuda.synchronize()
+    ms = kt.mean_ms()
+    rows = B * R * ((T - 1) + (T - 2))                      # t >= n-1 reads a row
+    alg = rows * md * 2 + B * T * md * 4 + B * T * R       # rows + fp32 out + codes
+    gbs = alg / (ms * 1e-3) / 1e9
+    del table, tabs, codes
+    torch.cuda.empty_cache()
+    return {"workload": "scaled-table gather + sum: B16 x T4096, R184, orders (2,3), 64x table "
+                        "(51,249,152 x 128 bf16 = 13.1 GB), uniform random codes",
+            "kernel": "k_gather_sum_scaled", "tokens_per_s": B * T / (ms * 1e-3), "avg_ms": ms,
+            "algorithmic_bytes": alg, "achieved_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "steps": steps}
+
+
 def measured_traffic():
     """HBM-side bytes per launch of the fused readout at this workload, from the committed
     hardware-counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor a
@@ -146,6 +265,8 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--draft-iters", type=int, default=200)
     ap.add_argument("--no-draft", action="store_true")
+    ap.add_argument("--no-scaled", action="store_true")
+    ap.add_argument("--no-sdc", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before warmup (known-size kernel that scales "
                          "hardware byte counters)")
@@ -231,6 +352,14 @@ def main() -> None:
     if not args.no_draft:
         log("draft step")
         result["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
+    if not args.no_scaled:
+        log("scaled-table gather")
+        result["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 2)
+    if not args.no_sdc:
+        log("SD-C forward")
+        result["sdc_forward"] = sdc_forward(dev, max(3, args.steps // 2), 2)
+        log("tiny forward")
+        result["tiny_forward"] = tiny_forward(dev, 50, 5)
     if not args.no_cpu:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -49,6 +49,17 @@ int lng_router_codes(const void* x, int x_dtype, const void* w, int w_dtype, int
 int lng_pack_route_codes(const float* logits, int64_t M, int64_t C, int32_t bits, void* codes,
                          int codes_dtype, void* stream);
 
+/* out[B*T, 2d+N] = concat(RMSNorm(E[x_{t-1}] or start; prev_w), RMSNorm(E[x_t]; cur_w)[, s_t])
+ * in `dtype` (bf16 or fp32): TokenRouterFeatures.forward (ffnmem/memory/router.py:50-59) with
+ * model.RMSNorm's rounding (ffnmem/model.py:39-48: normalise in fp32, round, times the weight).
+ * Rows: token_ids != null -> emb is the [vocab, d] table and row t is emb[token_ids[t]] (an id
+ * outside [0, vocab) reads a zero row); token_ids == null -> emb is [B*T, d] (E[x] already
+ * gathered).  ssm_state [B*T, N] fp32 (embed2_ssm) or null with N = 0.  d * elem and
+ * (2d + N) * elem must be multiples of 16 bytes, d <= 4096 (bf16) / 2048 (fp32). */
+int lng_router_features(const void* emb, int dtype, const int64_t* token_ids, int64_t vocab, int64_t B, int64_t T,
+                        int32_t d, const void* start, const void* prev_w, const void* cur_w, float eps,
+                        const float* ssm_state, int32_t N, void* out, void* stream);
+
 /* ---------------------------------------------------------------- K2: addresses / rows */
 /* addr[B, T-order+1, R] = sum_k codes[b, t'+k, r] << (k*bits).
  * _aligned_ngram_address (lngram_v2.py:314-325).  out_dtype LNG_I32 or LNG_I64. */
@@ -148,6 +159,20 @@ int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int
                              const void* table2, const void* table3, const void* wk_t, const void* wv,
                              const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
                              void* stream);
+
+/* out[B*T, mem_dim] (fp32) = sum over routes r and orders n (t >= n-1) of table_n[row, :] with
+ *   row = (r * S + slot) * 2^(bits n) + addr_n,   S = 2^scale_log2,
+ *   addr_n = sum_k (codes[b, t-n+1+k, r] & (2^bits-1)) << (bits k)      (oldest code least significant),
+ *   slot = mix32(seed ^ mix32((b*T + t) * 0x9E3779B1 + r*n_orders + i)) & (S-1)  (i = order index,
+ *   mix32 = MurmurHash3 fmix32, uint32 arithmetic).
+ * The row gather of _lookup_route_chunk (lngram_v2.py:1058, :1064-1092) with its zero rows for
+ * t < n-1, over tables grown S times per route (the scaled-table configuration of
+ * serving/scaled_tables.py:1-22 kept at R routes), summed instead of read out.  S = 1 gives the
+ * reference's global rows r*16^n + addr.  tables[i] (bf16 or fp32, [R*S*2^(bits n_i), mem_dim])
+ * must hold every row; mem_dim * element size must be 16 B times a divisor of 64. */
+int lng_gather_sum_scaled(const void* const* tables, int table_dtype, int32_t mem_dim, const uint8_t* codes,
+                          int64_t B, int64_t T, int32_t R, const int32_t* orders, int32_t n_orders, int32_t bits,
+                          int32_t scale_log2, uint32_t seed, float* out, void* stream);
 
 /* ---------------------------------------------------------------- K4: SSM scan */
 /* s[B,T,N] (fp32): s_t = a*s_{t-1} + (1-a)*u_t, s_{-1} = s0 (zero if null).

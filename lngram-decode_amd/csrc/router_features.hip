@@ -1,0 +1,115 @@
+// Token-only router input of SD-B / SD-C (TokenRouterFeatures.forward, ffnmem/memory/router.py:50-59):
+//
+//   x[p] = concat(RMSNorm_prev(E[x_{t-1}] or start), RMSNorm_cur(E[x_t]) [, s[p] in the feature dtype])
+//
+// with model.RMSNorm's rounding (model.py:39-48): normalise in fp32, round to the feature dtype,
+// multiply by the weight in that dtype.  The rows come either from a token-id array and the
+// embedding table (the embedding gather fused in) or from a materialised emb [B*T, d].
+//
+// One wave per position: the two d-wide rows are read as 16-byte pieces held in registers
+// (at most FE_MAXP per lane), squared-summed with a wave reduction, scaled and stored.
+#include "common.h"
+
+namespace lng {
+
+constexpr int FE_MAXP = 8;  // 16-byte pieces per lane and row: d <= 4096 (bf16) / 2048 (fp32)
+
+struct FeArgs {
+  const void* emb;         // [V, d] table (with ids) or [n_tok, d] rows (ids == nullptr)
+  const int64_t* ids;      // [n_tok] token ids or nullptr
+  int64_t V, T, n_tok;
+  const void* start;       // [d]
+  const void* prev_w;      // [d]
+  const void* cur_w;       // [d]
+  const float* ssm;        // [n_tok, N] or nullptr
+  int32_t d, N;
+  float eps;
+};
+
+template <typename TT>
+__device__ __forceinline__ void fe_norm_row(const TT* src, const TT* w, int d, float eps, TT* dst, int lane) {
+  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+  constexpr int VE = 16 / sizeof(TT);
+  const int np = d / VE;
+  piece_t v[FE_MAXP];
+#pragma unroll
+  for (int i = 0; i < FE_MAXP; ++i) {
+    const int pc = i * 64 + lane;
+    v[i] = (src && pc < np) ? *reinterpret_cast<const piece_t*>(src + pc * VE) : piece_t{0u, 0u, 0u, 0u};
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < FE_MAXP; ++i) {
+    const TT* e = reinterpret_cast<const TT*>(&v[i]);
+#pragma unroll
+    for (int j = 0; j < VE; ++j) {
+      const float f = to_f32(e[j]);
+      ss = fmaf(f, f, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+#pragma unroll
+  for (int i = 0; i < FE_MAXP; ++i) {
+    const int pc = i * 64 + lane;
+    if (pc >= np) continue;
+    const piece_t wp = *reinterpret_cast<const piece_t*>(w + pc * VE);
+    const TT* e = reinterpret_cast<const TT*>(&v[i]);
+    const TT* ww = reinterpret_cast<const TT*>(&wp);
+    piece_t o;
+    TT* oe = reinterpret_cast<TT*>(&o);
+#pragma unroll
+    for (int j = 0; j < VE; ++j) oe[j] = from_f32<TT>(round_to<TT>(to_f32(e[j]) * r) * to_f32(ww[j]));
+    *reinterpret_cast<piece_t*>(dst + pc * VE) = o;
+  }
+}
+
+// grid (cdiv(n_tok, 4)), block 256: wave w owns position 4 * blockIdx.x + w.
+template <typename TT>
+__global__ __launch_bounds__(256) void k_router_features(FeArgs A, TT* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (p >= A.n_tok) return;
+  const int64_t t = p % A.T;
+  const TT* emb = static_cast<const TT*>(A.emb);
+  const int d = A.d;
+  auto row = [&](int64_t q) -> const TT* {  // embedding row of position q (nullptr: id outside [0, V))
+    if (!A.ids) return emb + q * d;
+    const int64_t id = A.ids[q];
+    return (id >= 0 && id < A.V) ? emb + id * d : nullptr;
+  };
+  const int64_t od = 2 * static_cast<int64_t>(d) + A.N;
+  TT* o = out + p * od;
+  const TT* prev = t == 0 ? static_cast<const TT*>(A.start) : row(p - 1);
+  fe_norm_row<TT>(prev, static_cast<const TT*>(A.prev_w), d, A.eps, o, lane);
+  fe_norm_row<TT>(row(p), static_cast<const TT*>(A.cur_w), d, A.eps, o + d, lane);
+  if (A.ssm)
+    for (int i = lane; i < A.N; i += 64) o[2 * d + i] = from_f32<TT>(A.ssm[p * A.N + i]);
+}
+
+}  // namespace lng
+
+using namespace lng;
+
+extern "C" int lng_router_features(const void* emb, int dtype, const int64_t* token_ids, int64_t vocab, int64_t B,
+                                   int64_t T, int32_t d, const void* start, const void* prev_w, const void* cur_w,
+                                   float eps, const float* ssm_state, int32_t N, void* out, void* stream) {
+  if (!emb || !start || !prev_w || !cur_w || !out) return fail(LNG_E_ARG, "router_features: null pointer");
+  if (dtype != LNG_BF16 && dtype != LNG_F32) return fail(LNG_E_DTYPE, "router_features: dtype must be bf16 or fp32");
+  if (B < 0 || T < 0 || N < 0 || (N > 0) != (ssm_state != nullptr))
+    return fail(LNG_E_ARG, "router_features: bad shape (ssm_state and N > 0 go together)");
+  if (token_ids && vocab <= 0) return fail(LNG_E_ARG, "router_features: vocab must be positive with token ids");
+  const int es = dtype_size(dtype), ve = 16 / es;
+  if (d <= 0 || d % ve || d / ve > FE_MAXP * 64 || ((2 * static_cast<int64_t>(d) + N) * es) % 16)
+    return fail(LNG_E_ARG, "router_features: d must be a multiple of 16 bytes (at most 8 KB) and the feature row "
+                           "(2 d + N elements) a multiple of 16 bytes");
+  FeArgs A{emb, token_ids, vocab, T, B * T, start, prev_w, cur_w, ssm_state, d, N, eps};
+  if (A.n_tok == 0) return LNG_OK;
+  const dim3 grid(static_cast<unsigned>(cdiv(A.n_tok, 4)));
+  hipStream_t s = as_stream(stream);
+  if (dtype == LNG_BF16)
+    hipLaunchKernelGGL(k_router_features<bf16>, grid, dim3(256), 0, s, A, static_cast<bf16*>(out));
+  else
+    hipLaunchKernelGGL(k_router_features<float>, grid, dim3(256), 0, s, A, static_cast<float*>(out));
+  return check_launch("router_features");
+}

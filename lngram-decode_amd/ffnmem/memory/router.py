@@ -46,14 +46,27 @@ class TokenRouterFeatures(nn.Module):
 
     def forward(self, emb: Tensor, ssm_state: Tensor | None = None) -> Tensor:
         """emb ``[B, T, d]``; ssm_state ``[B, T, N]`` for ``embed2_ssm``."""
+        if self.kind == "embed2_ssm" and ssm_state is None:
+            raise ValueError("embed2_ssm router needs the SSM state")
+        s = ssm_state if self.kind == "embed2_ssm" else None
+        n = 0 if s is None else s.shape[-1]
+        if ops.router_features_ok(emb.shape[-1], n, emb.dtype):
+            return ops.router_features(emb, self.start, self.prev_norm.weight, self.cur_norm.weight, self.prev_norm.eps,
+                                       ssm_state=s)
         b = emb.shape[0]
         prev = torch.cat((self.start.to(emb.dtype).expand(b, 1, -1), emb[:, :-1]), dim=1)
         parts = [self.prev_norm(prev), self.cur_norm(emb)]
-        if self.kind == "embed2_ssm":
-            if ssm_state is None:
-                raise ValueError("embed2_ssm router needs the SSM state")
-            parts.append(ssm_state.to(parts[0].dtype))
+        if s is not None:
+            parts.append(s.to(parts[0].dtype))
         return torch.cat(parts, dim=-1)
+
+    def from_ids(self, token_ids: Tensor, table: Tensor, ssm_state: Tensor | None = None) -> Tensor:
+        """``forward(table[token_ids], ssm_state)`` with the embedding gather fused into the kernel
+        (not in the reference module: the model gathers ``emb`` itself)."""
+        if self.kind == "embed2_ssm" and ssm_state is None:
+            raise ValueError("embed2_ssm router needs the SSM state")
+        return ops.router_features(table, self.start, self.prev_norm.weight, self.cur_norm.weight, self.prev_norm.eps,
+                                   ssm_state=ssm_state if self.kind == "embed2_ssm" else None, token_ids=token_ids)
 
     def step(self, emb_prev: Tensor | None, emb_cur: Tensor, ssm_state: Tensor | None = None) -> Tensor:
         """One position (decode / drafter): ``emb_prev`` None at t = 0."""

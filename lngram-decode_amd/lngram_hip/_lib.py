@@ -54,6 +54,7 @@ SIGNATURES = {
     "lng_last_error": (ctypes.c_char_p, []),
     "lng_router_codes": (_int, [_p, _int, _p, _int, _i64, _i64, _i64, _i32, _p, _p, _int, _p]),
     "lng_pack_route_codes": (_int, [_p, _i64, _i64, _i32, _p, _int, _p]),
+    "lng_router_features": (_int, [_p, _int, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _f, _p, _i32, _p, _p]),
     "lng_ngram_address": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _p, _int, _p]),
     "lng_ngram_rows": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32, _p, _p, _p, _p]),
     "lng_route_tokens": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32,
@@ -69,6 +70,8 @@ SIGNATURES = {
     "lng_linear_rowsq": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "lng_causal_conv_rowsq": (_int, [_p, _p, _i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
     "lng_memory_readout_fused": (_int, [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _p, _f, _f, _f, _p, _p]),
+    "lng_gather_sum_scaled": (_int, [ctypes.POINTER(_p), _int, _i32, _p, _i64, _i64, _i32, _P32, _i32, _i32, _i32,
+                                     ctypes.c_uint32, _p, _p]),
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p, _p]),
     "lng_tree_accept": (_int, [_p, _p, _p, _i32, _p, _p, _p, _p]),

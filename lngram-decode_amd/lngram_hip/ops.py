@@ -143,6 +143,43 @@ def pack_route_codes(logits: torch.Tensor, bits: int, codes_dtype: torch.dtype =
     return out
 
 
+def router_features(emb: torch.Tensor, start: torch.Tensor, prev_w: torch.Tensor, cur_w: torch.Tensor, eps: float,
+                    ssm_state: torch.Tensor | None = None, token_ids: torch.Tensor | None = None) -> torch.Tensor:
+    """``concat(RMSNorm(E[x_{t-1}] or start), RMSNorm(E[x_t])[, s_t])`` ``[B, T, 2d (+N)]`` in the
+    embedding dtype.  ``token_ids [B, T]`` given: ``emb`` is the ``[V, d]`` table (gather fused in);
+    otherwise ``emb [B, T, d]`` holds the gathered rows."""
+    dev = _dev(emb, start, prev_w, cur_w, ssm_state, token_ids)
+    dt = emb.dtype
+    d = emb.shape[-1]
+    if token_ids is not None:
+        b, t = token_ids.shape
+        ids = _c(token_ids.to(torch.int64))
+        vocab = emb.shape[0]
+    else:
+        b, t = emb.shape[:2]
+        ids, vocab = None, 0
+    n = 0
+    sc = None
+    if ssm_state is not None:
+        if ssm_state.shape[:2] != (b, t):
+            raise ValueError(f"ssm_state {tuple(ssm_state.shape)} does not match [B, T] = [{b}, {t}]")
+        n = ssm_state.shape[-1]
+        sc = _c(ssm_state.float())
+    ec = _c(emb)
+    out = torch.empty(b, t, 2 * d + n, dtype=dt, device=dev)
+    check(lib().lng_router_features(_ptr(ec), dtype_code(dt), _ptr(ids), vocab, b, t, d, _ptr(_c(start.to(dt))),
+                                    _ptr(_c(prev_w.to(dt))), _ptr(_c(cur_w.to(dt))), eps, _ptr(sc), n, _ptr(out),
+                                    _stream(dev)), "router_features")
+    return out
+
+
+def router_features_ok(d: int, n: int, dtype: torch.dtype) -> bool:
+    """Shapes ``lng_router_features`` takes."""
+    es = torch.finfo(dtype).bits // 8 if dtype.is_floating_point else 0
+    return dtype in (torch.bfloat16, torch.float32) and (d * es) % 16 == 0 and d * es <= 8192 and \
+        ((2 * d + n) * es) % 16 == 0
+
+
 # ----------------------------------------------------------------------------- K2
 def _codes_ok(codes: torch.Tensor) -> torch.Tensor:
     if codes.dtype not in (torch.uint8, torch.int32, torch.int64):
@@ -359,6 +396,31 @@ def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Ten
     return out
 
 
+def gather_sum_scaled(tables, codes: torch.Tensor, orders, bits: int, scale_log2: int, seed: int) -> torch.Tensor:
+    """fp32 ``[B, T, mem_dim]``: per token, the sum of one row per (route, order) of tables grown
+    ``2**scale_log2`` times per route (``lng_gather_sum_scaled``); ``codes [B, T, R]`` uint8,
+    ``tables[i]`` ``[R * 2**scale_log2 * 2**(bits * orders[i]), mem_dim]`` bf16 or fp32."""
+    dev = _dev(codes, *tables)
+    b, t, r = codes.shape
+    tabs = [_c(tb) for tb in tables]
+    dt = tabs[0].dtype
+    md = tabs[0].shape[1]
+    if len(tabs) != len(orders):
+        raise ValueError("one table per order")
+    for tb, n in zip(tabs, orders):
+        if tb.dtype != dt or tb.shape != (r << (int(scale_log2) + bits * int(n)), md):
+            raise ValueError(f"table of order {n} must be [R * 2^scale_log2 * 2^(bits n), mem_dim] = "
+                             f"[{r << (int(scale_log2) + bits * int(n))}, {md}] {dt}, got {tuple(tb.shape)} {tb.dtype}")
+    cc = _c(codes.to(torch.uint8))
+    out = torch.empty(b, t, md, dtype=torch.float32, device=dev)
+    tp = (ctypes.c_void_p * len(tabs))(*[tb.data_ptr() for tb in tabs])
+    rc = _timed("gather_sum_scaled", dev, lambda: lib().lng_gather_sum_scaled(
+        tp, dtype_code(dt), md, _ptr(cc), b, t, r, _orders(orders), len(orders), bits, int(scale_log2),
+        ctypes.c_uint32(int(seed) & 0xFFFFFFFF), _ptr(out), _stream(dev)))
+    check(rc, "gather_sum_scaled")
+    return out
+
+
 # ----------------------------------------------------------------------------- K4
 def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -> torch.Tensor:
     """``s_t = a s_{t-1} + (1 - a) u_t`` (fp32) for u ``[B, T, N]``, a ``[N]``, s0 ``[B, N]`` or None."""
@@ -370,7 +432,9 @@ def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -
     out = torch.empty_like(uc)
     ws_bytes = lib().lng_ssm_workspace_bytes(b, t, n)
     ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=dev)
-    check(lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws), _ptr(out), _stream(dev)), "ssm_scan")
+    rc = _timed("ssm_scan", dev, lambda: lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws), _ptr(out),
+                                                            _stream(dev)))
+    check(rc, "ssm_scan")
     return out
 
 

@@ -58,8 +58,8 @@ class MemoryWorkload:
         act = self.d_model * es
         if self.router_input == "hidden":
             return 2 * act + rows + act
-        # embed2(_ssm): h + E[x_t] read (E[x_{t-1}] is the previous token's row), s_t, out
-        return 2 * act + self.ssm_dim * es + rows + act
+        # embed2(_ssm): h + E[x_t] read (E[x_{t-1}] is the previous token's row), s_t (fp32), out
+        return 2 * act + self.ssm_dim * 4 + rows + act
 
     def weight_bytes(self) -> int:
         es = torch.finfo(self.dtype).bits // 8

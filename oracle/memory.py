@@ -156,6 +156,63 @@ def route_tokens(tables: dict, codes, orders, bits: int, route_start: int = 0, r
     return out
 
 
+def mix32(h) -> np.ndarray:
+    """MurmurHash3's 32-bit finaliser ``fmix32`` (Appleby, MurmurHash3.cpp, public domain) in uint32
+    arithmetic: ``h ^= h >> 16; h *= 0x85ebca6b; h ^= h >> 13; h *= 0xc2b2ae35; h ^= h >> 16``.
+    Not from the reference: it defines the slot choice of the scaled-table workload."""
+    h = np.asarray(h, dtype=np.uint64) & 0xFFFFFFFF
+    h ^= h >> 16
+    h = (h * 0x85EBCA6B) & 0xFFFFFFFF
+    h ^= h >> 13
+    h = (h * 0xC2B2AE35) & 0xFFFFFFFF
+    h ^= h >> 16
+    return h
+
+
+def scaled_rows(codes, orders, bits: int, scale_log2: int, seed: int) -> np.ndarray:
+    """Rows read from tables grown ``S = 2**scale_log2`` times per route (the scaled-table
+    configuration: ``serving/scaled_tables.py:1-22`` grows the table, here at a fixed route count).
+
+    int64 ``[B, T, R, len(orders)]``: ``row = (r*S + slot) * 2^(bits n) + addr_n``, -1 where
+    ``route_rows`` (``lngram_v2.py:1047-1092``) masks the row (t < n-1).  ``addr_n`` is the
+    reference's aligned address of the codes masked to ``bits``; ``slot = mix32(seed ^
+    mix32(p * 0x9E3779B1 + r * n_orders + i)) & (S-1)`` with ``p = b*T + t`` and ``i`` the order's
+    index.  With ``scale_log2 = 0`` the rows are the reference's global rows."""
+    c = np.asarray(codes).astype(np.int64) & ((1 << bits) - 1)
+    b, t, r = c.shape
+    base = route_rows(c, orders, bits)                        # r * 2^(bits n) + addr, or -1
+    S = 1 << scale_log2
+    p = np.arange(b * t, dtype=np.uint64).reshape(b, t, 1, 1)
+    i = (np.arange(r, dtype=np.uint64)[:, None] * len(orders) + np.arange(len(orders), dtype=np.uint64)[None, :])
+    slot = (mix32(np.uint64(seed & 0xFFFFFFFF) ^ mix32((p * 0x9E3779B1 + i[None, None]) & 0xFFFFFFFF))
+            & np.uint64(S - 1)).astype(np.int64)
+    blk = np.array([1 << (bits * n) for n in orders], np.int64)
+    rr = np.arange(r, dtype=np.int64)[:, None]
+    rows = base + (rr * (S - 1) + slot) * blk                 # (r S + slot) 2^(bits n) + addr
+    return np.where(base >= 0, rows, -1)
+
+
+def gather_sum_scaled(tables, codes, orders, bits: int, scale_log2: int, seed: int,
+                      positions=None) -> np.ndarray:
+    """fp64 ``[B, T, mem_dim]`` (or ``[len(positions), mem_dim]`` for flat token indices
+    ``positions``): the sum over routes and orders of the rows of ``scaled_rows`` (a masked row
+    adds nothing).  ``tables`` are torch tensors (any device) indexed by the computed rows."""
+    rows = scaled_rows(codes, orders, bits, scale_log2, seed)
+    b, t, r, no = rows.shape
+    flat = rows.reshape(b * t, r, no)
+    if positions is not None:
+        flat = flat[np.asarray(positions)]
+    md = tables[0].shape[1]
+    out = np.zeros((flat.shape[0], md), np.float64)
+    for oi in range(no):
+        sel = flat[:, :, oi]
+        ok = sel >= 0
+        idx = torch.from_numpy(np.where(ok, sel, 0).reshape(-1)).to(tables[oi].device)
+        got = tables[oi][idx].double().cpu().numpy().reshape(flat.shape[0], r, md)
+        out += (got * ok[..., None]).sum(1)
+    return out if positions is not None else out.reshape(b, t, md)
+
+
 # ----------------------------------------------------------------------------- float parts
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """RMSNorm as the reference rounds it: normalise in fp32 (fp64 for fp64 input),

@@ -1,0 +1,85 @@
+"""SD-C memory forward (token-routed memory over a diagonal SSM) against the oracle (GPU).
+
+Pipeline: s = scan(a, u) (fp32) -> router_in = concat(RMSNorm(E[x_{t-1}] or start),
+RMSNorm(E[x_t]), s) in bf16 -> router GEMM + sign-pack -> fused gather + readout + finish.
+Router features: within one rounding of the feature dtype of the oracle
+(``TokenRouterFeatures.forward``, router.py:50-59).  Codes: bit-exact outside the near-tie
+band.  Output: 2e-2 norm-relative (bf16) given identical codes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from lngram_hip import ops, workloads
+from oracle import memory as om
+
+from .test_gpu_memory import cfg_of, codes_check, oracle_params
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype,d,n,ids", [(torch.bfloat16, 64, 16, True), (torch.bfloat16, 1024, 256, False),
+                                           (torch.float32, 32, 0, True), (torch.float32, 48, 8, False)])
+def test_router_features_match_oracle(dev, dtype, d, n, ids):
+    g = torch.Generator().manual_seed(d + n)
+    B, T, V = 3, 17, 50
+    table = torch.randn(V, d, generator=g).to(dtype)
+    tok = torch.randint(0, V, (B, T), generator=g)
+    if ids:
+        tok[1, 4] = V + 3                                    # outside the vocabulary: a zero row
+    start = (torch.randn(d, generator=g) * 0.02).to(dtype)
+    pw = (1 + 0.2 * torch.randn(d, generator=g)).to(dtype)
+    cw = (1 + 0.2 * torch.randn(d, generator=g)).to(dtype)
+    s = torch.randn(B, T, n, generator=g) if n else None
+    emb = table[tok.clamp_max(V - 1)] * (tok < V)[..., None].to(dtype)
+    want = om.router_features(emb, start, pw, cw, 1e-5, s)
+    kw = dict(ssm_state=None if s is None else s.to(dev))
+    if ids:
+        got = ops.router_features(table.to(dev), start.to(dev), pw.to(dev), cw.to(dev), 1e-5,
+                                  token_ids=tok.to(dev), **kw).cpu()
+    else:
+        got = ops.router_features(emb.to(dev), start.to(dev), pw.to(dev), cw.to(dev), 1e-5, **kw).cpu()
+    assert got.dtype == dtype and got.shape == want.shape
+    tol = 4e-3 if dtype == torch.bfloat16 else 2e-6           # one rounding of the feature dtype
+    assert om.rel_err(got.double(), want.double()) < tol
+    assert (got - want).abs().max() <= tol * want.abs().max()
+
+
+def _sdc_pipeline(w, dev, seed=0):
+    mem = workloads.build_memory(w, seed=seed, device=dev)
+    g = torch.Generator().manual_seed(seed + 7)
+    E = (torch.randn(w.vocab, w.d_model, generator=g) * 0.02).to(w.dtype)
+    tok = torch.randint(0, w.vocab, (w.batch, w.seq), generator=g)
+    a = 0.9 + 0.099 * torch.rand(w.ssm_dim, generator=g)
+    u = torch.randn(w.batch, w.seq, w.ssm_dim, generator=g)
+    h = workloads.make_hidden(w, seed=seed + 1)
+    return mem, E, tok, a, u, h
+
+
+def test_sdc_shape_forward(dev):
+    w = workloads.SDC.with_shape(2, 48)
+    mem, E, tok, a, u, h = _sdc_pipeline(w, dev)
+    feats = mem.router_features
+    s = ops.ssm_scan(a.to(dev), u.to(dev))
+    x = feats.from_ids(tok.to(dev), E.to(dev), s)
+    x2 = feats(E.to(dev)[tok.to(dev)], s)                    # the reference signature, same kernel
+    assert torch.equal(x, x2)
+    out = mem(h.to(dev), None, router_in=x).cpu()
+    _, codes_gpu = mem.route_codes(x)
+    # oracle
+    p = oracle_params(mem)
+    fsd = {k: v.detach().cpu() for k, v in feats.state_dict().items()}
+    s_ref = torch.from_numpy(om.ssm_scan(a.numpy(), u.numpy())).float()
+    assert om.rel_err(s.cpu().double(), s_ref.double()) < 1e-5
+    x_ref = om.router_features(E[tok], fsd["start"], fsd["prev_norm.weight"], fsd["cur_norm.weight"], w.norm_eps,
+                               s_ref)
+    assert om.rel_err(x.cpu().double(), x_ref.double()) < 4e-3
+    q64 = om.router_logits(x.cpu(), p["router.weight"]).numpy()   # codes of the GPU's own features
+    codes, _ = codes_check(codes_gpu.cpu().numpy().astype(np.int32), q64)
+    ref = om.memory_forward(p, cfg_of(w), h, codes)
+    assert om.rel_err(out, ref) < 2e-2
+    ref64 = om.memory_forward(p, cfg_of(w), h.double(), codes)
+    assert om.rel_err(out, ref64) < 2e-2
