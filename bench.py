@@ -67,6 +67,41 @@ def cpu_baseline(seconds: float) -> dict:
                       "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)"}
 
 
+def draft_cpu_baseline(seconds: float) -> dict:
+    """The oracle's C++ port of the reference CPU drafter (``drafter.cpp`` per-token algorithm, fp32,
+    bf16 tables, OpenMP over routes and vocabulary rows, online counts on) timed on the host cores:
+    draft_tree over the 16-node tree + tree acceptance after the same 2048-token SD-B context, repeated
+    for about ``seconds``."""
+    import numpy as np
+
+    from drafting import tree as dtree
+    from lngram_hip import workloads
+    from oracle import drafting as od
+    from oracle.cdrafter import CppDrafterPort
+
+    threads = len(os.sched_getaffinity(0))
+    w = workloads.SDB_DRAFT
+    cfg, t = workloads.build_draft_bundle(w, seed=0)
+    c = CppDrafterPort(cfg, t, threads=threads, online=True)
+    t0 = time.perf_counter()
+    c.commit(workloads.make_context(w, seed=0))
+    commit_s = time.perf_counter() - t0
+    spec = dtree.tree16()
+    steps = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        node = c.draft_tree(spec)
+        od.tree_accept(spec.parent, node, [node[i] for i in range(spec.n)])
+        steps.append((time.perf_counter() - t0) * 1e6)
+        if time.perf_counter() - t_all >= seconds:
+            break
+    return {"value": float(np.median(steps)), "unit": "us per draft step", "cores": threads, "kind": "port",
+            "sample": f"{len(steps)} draft steps (16-node tree, 10 parent readouts over the full 32768 vocabulary, "
+                      f"online counts) after committing the 2048-token context ({commit_s:.1f} s); C++ port of "
+                      "drafting/cpu/drafter.cpp with OpenMP"}
+
+
 def draft_step(dev, iters: int, warmup: int) -> dict:
     """SD-B decode draft step on one GPU: the 2048-token context is committed, then one step =
     16-node draft tree (10 parent readouts in 4 depths, top-3, online counts over the context) +
@@ -352,6 +387,9 @@ def main() -> None:
     if not args.no_draft:
         log("draft step")
         result["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
+        if not args.no_cpu:
+            log("draft step cpu baseline")
+            result["draft_step_us"]["cpu_baseline"] = draft_cpu_baseline(args.cpu_seconds)
     if not args.no_scaled:
         log("scaled-table gather")
         result["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 2)
