@@ -203,6 +203,7 @@ int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int
 #define LNG_DR_MAX_P 16
 #define LNG_DR_MAX_K 8
 #define LNG_DR_SYNC_INTS 4160  /* int32 entries of lng_drafter.sync */
+#define LNG_DR_TREE_SYNC_BYTES 16640  /* error word + counters at the start of the one-launch tree's workspace */
 
 typedef struct lng_drafter {
   int32_t d, V, R, bits, mem_dim, dt, n_orders, orders[4], maxn;
@@ -298,6 +299,28 @@ int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, 
 int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n, int32_t node_row0,
                      int online, float kappa, void* work, size_t work_bytes, int32_t* counts, void* route_tokens,
                      void* stream);
+
+/* The whole draft tree of lng_drafter_tree in ONE cooperative launch (token-only drafters with
+ * the per-token tables, bf16 tables, R <= 192, <= 2 orders, q_heads <= 8, q_heads*Dt <= 1024,
+ * q_heads*head_dim <= 256; n <= 32 nodes, <= 8 depths with parents, <= 8 parents per depth).
+ * Same results as lng_drafter_tree (tokens of every node in rows node_row0 .., node codes, the
+ * verification gather [n, R, Dt] if route_tokens is non-null).  One block per CU stays resident:
+ * each depth's parents run their readouts, every block scores its vocabulary slice (and its
+ * online-count matches) against them, writer blocks select the children's tokens; blocks meet
+ * through device-coherent counters (bounded waits).  `work` holds
+ * lng_drafter_tree_fused_workspace(D) bytes, zero before the first call; `seq` must increase by
+ * one per call on the same workspace (counters are double-buffered by seq & 1).  The int32 at byte
+ * offset 0 of `work` is a sticky error word (0 = ok; bit 0 = a wait timed out, bit 1 = no committed
+ * token, bit 2 = counters were not zero): after an error zero the first LNG_DR_TREE_SYNC_BYTES
+ * bytes and restart seq.  stamps (optional, device int64 [grid][40]) receive the 100 MHz
+ * real-time counter at phase boundaries of each
+ * block.  Returns LNG_E_ARG without launching when the drafter or tree is outside the limits
+ * above (lng_drafter_tree then runs it); the workspace size is 0 for a drafter outside them. */
+size_t lng_drafter_tree_fused_workspace(const lng_drafter* D);
+int lng_drafter_tree_fused(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n,
+                           int32_t node_row0, int online, float kappa, uint32_t seq, void* work, size_t work_bytes,
+                           void* route_tokens, long long* stamps, void* stream);
+
 
 /* Tree acceptance (drafting/tree.py:205-220): from the root take the first child
  * (index order) whose token equals argmax[cur]; repeat.  path[n] receives the

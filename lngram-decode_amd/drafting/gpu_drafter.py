@@ -57,7 +57,7 @@ class GpuDrafter:
     name = "gpu"
 
     def __init__(self, bundle, topk: int = 3, shortlist_cap: int | None = None, device=None, max_len: int = 4096,
-                 online: bool = False, kappa: float = 1.0, tables: bool = True):
+                 online: bool = False, kappa: float = 1.0, tables: bool = True, fused: bool = False):
         c, t = _bundle_parts(bundle)
         self.cfg = c
         self.topk = int(topk)
@@ -123,6 +123,15 @@ class GpuDrafter:
             raise ValueError("drafter shape outside the kernels' limits")
         self.work = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
         self.counts = torch.zeros(16, self.V, dtype=torch.int32, device=dev)
+        # one-launch draft tree (lng_drafter_tree_fused) for token-only drafters with tables: opt-in;
+        # at the SD-B shape it measures about the same as the per-depth launches, which stay the default
+        self.tree_work = None
+        self._tree_seq = 0
+        self._fused_specs: dict = {}
+        if fused and self.luts is not None:
+            fb = self.lib.lng_drafter_tree_fused_workspace(ctypes.byref(self.D))
+            if fb:
+                self.tree_work = torch.zeros(int(fb), dtype=torch.uint8, device=dev)
         self.ids_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.int64, device=dev)
         self.sc_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.float32, device=dev)
         self.reset()
@@ -343,12 +352,34 @@ class GpuDrafter:
         out = None
         if route_tokens:
             out = torch.empty(n, self.R, self.dt, dtype=self.tables[0].dtype, device=self.device)
-        check(self.lib.lng_drafter_tree(ctypes.byref(self.D), self._i32(spec.parent), self._i32(spec.rank), n,
-                                        self.tree_row0, int(self.online), self.kappa, self.work.data_ptr(),
-                                        self.work.numel(), self.counts.data_ptr(),
+        parent, rank = self._i32(spec.parent), self._i32(spec.rank)
+        key = (tuple(spec.parent), tuple(spec.rank))
+        if self.tree_work is not None and self._fused_specs.get(key, True):
+            rc = self.lib.lng_drafter_tree_fused(ctypes.byref(self.D), parent, rank, n, self.tree_row0,
+                                                 int(self.online), self.kappa, self._tree_seq,
+                                                 self.tree_work.data_ptr(), self.tree_work.numel(),
+                                                 out.data_ptr() if out is not None else None, None, self._stream())
+            if rc == 0:
+                self._tree_seq += 1
+                self._fused_specs[key] = True
+                return self.tok_d[self.tree_row0: self.tree_row0 + n], out
+            self._fused_specs[key] = False     # tree outside the one-launch limits: per-depth launches
+        check(self.lib.lng_drafter_tree(ctypes.byref(self.D), parent, rank, n, self.tree_row0, int(self.online),
+                                        self.kappa, self.work.data_ptr(), self.work.numel(), self.counts.data_ptr(),
                                         out.data_ptr() if out is not None else None, self._stream()),
               "drafter tree")
         return self.tok_d[self.tree_row0: self.tree_row0 + n], out
+
+    def tree_error(self) -> int:
+        """Error word of the one-launch tree (synchronises): 0 = ok; non-zero clears it and raises."""
+        if self.tree_work is None:
+            return 0
+        err = int(self.tree_work[:4].view(torch.int32).item())
+        if err:
+            self.tree_work[:_lib.TREE_SYNC_BYTES].zero_()
+            self._tree_seq = 0
+            raise RuntimeError(f"drafter tree (one launch): a device wait failed (error word {err})")
+        return 0
 
     def trace(self, tokens, codes=None, full: bool = False):
         """Teacher-forced pass from an empty state: (codes [T, R] uint8, ids [T, V] int64,

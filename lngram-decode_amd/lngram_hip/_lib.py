@@ -28,6 +28,7 @@ _P32 = ctypes.POINTER(ctypes.c_int32)
 
 ROW_NONE = -2147483648  # LNG_ROW_NONE
 DR_SYNC_INTS = 4160  # LNG_DR_SYNC_INTS
+TREE_SYNC_BYTES = 16640  # LNG_DR_TREE_SYNC_BYTES: error word (offset 0) + counters of the one-launch tree
 
 
 class Drafter(ctypes.Structure):
@@ -74,6 +75,9 @@ SIGNATURES = {
                                      ctypes.c_uint32, _p, _p]),
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p, _p]),
+    "lng_drafter_tree_fused_workspace": (ctypes.c_size_t, [_PD]),
+    "lng_drafter_tree_fused": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, ctypes.c_uint32, _p, ctypes.c_size_t, _p,
+                                      _p, _p]),
     "lng_tree_accept": (_int, [_p, _p, _p, _i32, _p, _p, _p, _p]),
     "lng_drafter_size": (ctypes.c_size_t, []),
     "lng_drafter_workspace_bytes": (ctypes.c_size_t, [_PD, _i32, _i32, _i32]),

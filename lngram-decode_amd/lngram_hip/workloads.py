@@ -144,6 +144,7 @@ class DraftWorkload:
 SDB_DRAFT = DraftWorkload("sdb drafter d1024 V32768 R182 bf16", 1024, 32768, 182, 128, 4, 64, 4)
 SDC_DRAFT = DraftWorkload("sdc drafter d1024 V32768 R181 N256 bf16", 1024, 32768, 181, 128, 4, 64, 4, ssm_dim=256)
 TINY_DRAFT = DraftWorkload("tiny drafter d64 V512 R6", 64, 512, 6, 16, 2, 16, 4, context=96)
+TINY_DRAFT_FAST = DraftWorkload("tiny drafter d64 V1000 R7 mem_dim 32", 64, 1000, 7, 32, 2, 16, 4, context=96)
 TINY_DRAFT_SSM = DraftWorkload("tiny drafter d64 V512 R5 N8", 64, 512, 5, 16, 2, 16, 4, ssm_dim=8, context=96)
 
 

@@ -24,11 +24,12 @@ TAU = 2e-5
 SPEC16 = dtree.tree16()
 
 
-KINDS = ["sdb", "sdb_generic", "sdc"]
+KINDS = ["sdb", "sdb_generic", "sdc", "sdb_fast"]
 
 
 def _bundle(kind: str, seed: int = 5):
-    w = {"sdb": wl.TINY_DRAFT, "sdb_generic": wl.TINY_DRAFT, "sdc": wl.TINY_DRAFT_SSM}[kind]
+    w = {"sdb": wl.TINY_DRAFT, "sdb_generic": wl.TINY_DRAFT, "sdc": wl.TINY_DRAFT_SSM,
+         "sdb_fast": wl.TINY_DRAFT_FAST}[kind]
     cfg, t = wl.build_draft_bundle(w, seed=seed)
     g = torch.Generator().manual_seed(9)
     for k in ("router_prev_norm", "router_cur_norm", "q_norm", "out_norm", "mem_norm"):
@@ -37,9 +38,12 @@ def _bundle(kind: str, seed: int = 5):
 
 
 def _gpu(kind, cfg, t, dev, **kw) -> GpuDrafter:
-    """sdb: per-token tables (two launches per readout); sdb_generic / sdc: the general kernels."""
-    g = GpuDrafter((cfg, t), device=dev, tables=kind == "sdb", **kw)
-    assert (g.luts is not None) == (kind == "sdb")
+    """sdb / sdb_fast: per-token tables (two launches per readout; sdb_fast has Dt = 64, so its
+    trees run in one launch); sdb_generic / sdc: the general kernels."""
+    kw.setdefault("fused", kind == "sdb_fast")
+    g = GpuDrafter((cfg, t), device=dev, tables=kind in ("sdb", "sdb_fast"), **kw)
+    assert (g.luts is not None) == (kind in ("sdb", "sdb_fast"))
+    assert (g.tree_work is not None) == (kind == "sdb_fast")
     return g
 
 
@@ -145,6 +149,7 @@ def test_draft_tree_and_verify_gather_match_oracle(dev, kind, online):
             path = od.tree_path(spec.parent, i)
             c = o.draft(1, hyp=[want[a] for a in path[1:]], last_codes=True).codes
             node_codes[i] = c[len(path) - 2]
+        assert g.tree_error() == 0
         got_codes = g.codes_d[g.tree_row0 + 1: g.tree_row0 + spec.n].cpu().numpy()
         np.testing.assert_array_equal(got_codes, node_codes[1:])
         hist = codes[None, -3:-1].astype(np.int64)
@@ -207,3 +212,30 @@ def test_sdb_shape_tree_step_matches_oracle(dev):
     spec = od.TreeSpec(SPEC16.parent, SPEC16.rank)
     want = od.draft_tree(o, spec)
     assert g.draft_tree(SPEC16) == want
+
+
+def test_sdb_shape_one_launch_tree_matches_per_depth_launches_and_oracle(dev):
+    """SD-B drafter shape with online counts: the one-launch tree equals the per-depth launches
+    (node tokens, node codes, verification gather, bit for bit) and the oracle's draft tree."""
+    w = wl.SDB_DRAFT
+    cfg, t = wl.build_draft_bundle(w, seed=0)
+    ctx = wl.make_context(w, seed=0)
+    g1 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8, online=True, fused=True)
+    g0 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8, online=True, fused=False)
+    assert g1.tree_work is not None and g0.tree_work is None
+    g1.commit(ctx)
+    g0.commit(ctx, codes=g1.committed_codes())
+    o = od.DrafterOracle(cfg, t, online=True)
+    o.commit(ctx, codes=g1.committed_codes())
+    want = od.draft_tree(o, od.TreeSpec(SPEC16.parent, SPEC16.rank))
+    for rep in range(3):                                     # repeated calls reuse the counters
+        print(f"[sdb one-launch tree] call {rep}", flush=True)
+        n1, r1 = g1.tree_step(SPEC16, route_tokens=True)
+        n0, r0 = g0.tree_step(SPEC16, route_tokens=True)
+        torch.cuda.synchronize()
+        assert g1.tree_error() == 0
+        assert g1._fused_specs[(tuple(SPEC16.parent), tuple(SPEC16.rank))]
+        assert n1.cpu().tolist() == n0.cpu().tolist() == want
+        assert torch.equal(r1, r0)
+        rows = slice(g1.tree_row0, g1.tree_row0 + SPEC16.n)
+        assert torch.equal(g1.codes_d[rows][1:], g0.codes_d[rows][1:])
