@@ -134,6 +134,11 @@ int32_t lng_linear_rowsq_partials(int64_t N);
 int lng_linear_rowsq(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, float* rowsq,
                      void* stream);
 
+/* rowsq[m] (fp32) = sum_c x[m, c]^2 over bf16 rows [rows, d]: the RMSNorm statistic of the short
+ * conv's input (DepthwiseCausalConv, lngram_v2.py:273-286) as one partial for lng_causal_conv_rowsq,
+ * for output projections that do not produce it in their epilogue. */
+int lng_row_sumsq(const void* x, int64_t rows, int32_t d, float* rowsq, void* stream);
+
 /* lng_causal_conv for bf16, kernel 4, dilation 3, taking the row statistics from
  * lng_linear_rowsq instead of recomputing them (same rounding as lng_causal_conv).
  * n_partials <= 16, i.e. d <= 2048. */

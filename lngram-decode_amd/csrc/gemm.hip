@@ -7,6 +7,8 @@
 // consecutive output channels of one token: a packed store for plain outputs,
 // and exactly one route's 4 sign bits for the router epilogue.
 // fp32 runs on a VALU tile kernel (the tiny fp32 layer and fp32 routers).
+#include <cstdlib>
+
 #include "common.h"
 
 namespace lng {
@@ -467,6 +469,8 @@ static int launch_f32(const void* x, const void* w, int64_t M, int64_t N, int64_
   return check_launch("gemm_f32");
 }
 
+int linear_bf16_lt(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s);
+
 // Shared entry for bf16 MFMA linears (used by other translation units).
 int linear_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s) {
   return launch_mfma<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, y, nullptr,
@@ -497,6 +501,12 @@ int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, in
   hipStream_t s = as_stream(stream);
   if (dtype == LNG_BF16) {
     if (K % 8) return fail(LNG_E_ARG, "linear: bf16 needs K % 8 == 0");
+    // large plain projections: hipBLASLt (no epilogue to fuse); otherwise the MFMA kernels here
+    static const bool lt_off = std::getenv("LNGRAM_NO_HIPBLASLT") != nullptr;
+    if (!lt_off && M >= 1024 && N >= 256 && K >= 256) {
+      const int rc = linear_bf16_lt(x, w, M, N, K, y, s);
+      if (rc != LNG_E_ARG) return rc;
+    }
     return linear_bf16(x, w, M, N, K, y, s);
   }
   if (dtype == LNG_F32) return launch_f32<float, float, float>(x, w, M, N, K, y, s);

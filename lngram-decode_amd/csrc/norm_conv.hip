@@ -302,6 +302,27 @@ __global__ __launch_bounds__(256) void k_causal_conv_k4d3_rowsq(const bf16* __re
   }
 }
 
+// rowsq[m] = sum_c x[m, c]^2 of bf16 rows (the RMSNorm statistic of the short conv, in the one-
+// partial layout k_causal_conv_k4d3_rowsq reads).  One wave per row, 16-byte loads.
+__global__ __launch_bounds__(256) void k_row_sumsq_bf16(const bf16* __restrict__ x, int64_t rows, int32_t d,
+                                                        float* __restrict__ rowsq) {
+  const int lane = threadIdx.x & 63;
+  const int64_t m = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (m >= rows) return;
+  const bf16* xr = x + m * d;
+  float ss = 0.f;
+  for (int c = 8 * lane; c < d; c += 512) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(xr + c);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float f = static_cast<float>(v[j]);
+      ss = fmaf(f, f, ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) rowsq[m] = ss;
+}
+
 // bf16, kernel 4, dilation 3, single pass: block = (b, 16 positions), d/8 threads, each
 // thread keeps its 8 channels of all 25 rows (16 + 9 causal halo) in registers.  Row
 // norms are reduced across the block (wave sums, then LDS), then the conv runs from the
@@ -501,6 +522,14 @@ int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, i
   else
     return fail(LNG_E_DTYPE, "causal_conv: dtype must be f32 or bf16");
   return check_launch("causal_conv");
+}
+
+int lng_row_sumsq(const void* x, int64_t rows, int32_t d, float* rowsq, void* stream) {
+  if (rows < 0 || d <= 0 || d % 8 || !x || !rowsq) return fail(LNG_E_ARG, "row_sumsq: bf16 rows with d % 8 == 0");
+  if (rows == 0) return LNG_OK;
+  hipLaunchKernelGGL(k_row_sumsq_bf16, dim3(static_cast<unsigned>(cdiv(rows, 4))), dim3(256), 0, as_stream(stream),
+                     static_cast<const bf16*>(x), rows, d, rowsq);
+  return check_launch("row_sumsq");
 }
 
 }  // extern "C"

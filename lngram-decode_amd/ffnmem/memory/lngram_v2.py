@@ -337,7 +337,12 @@ class _RouteNgramMemoryBase(nn.Module):
             raise NotImplementedError("packed-segment causal conv is not part of the MI355X path")
         flat = head_output.reshape(b, t, self.readout_inner_dim)
         if self.short_conv.takes_row_stats(flat.dtype) and self.readout_inner_dim % 32 == 0:
-            mixed, rowsq = ops.linear_rowsq(flat, self.readout_o_proj.weight)
+            if b * t >= 1024:
+                # large batches: the projection on hipBLASLt, the row statistics in a separate pass
+                mixed = ops.linear(flat, self.readout_o_proj.weight)
+                rowsq = ops.row_sumsq(mixed)
+            else:
+                mixed, rowsq = ops.linear_rowsq(flat, self.readout_o_proj.weight)
             return self.short_conv.forward_residual_stats(mixed, rowsq)
         mixed = ops.linear(flat, self.readout_o_proj.weight)
         return self.short_conv.forward_residual(mixed)

@@ -292,6 +292,19 @@ def linear_rowsq(x: torch.Tensor, w: torch.Tensor):
     return out, rowsq
 
 
+def row_sumsq(x: torch.Tensor) -> torch.Tensor:
+    """``[1, rows]`` fp32 sums of squares of the bf16 rows of ``x`` (the layout of
+    :func:`linear_rowsq`'s statistics with one partial)."""
+    dev = _dev(x)
+    if x.dtype != torch.bfloat16:
+        raise ValueError("row_sumsq needs bf16 rows")
+    d = x.shape[-1]
+    xc = _c(x.reshape(-1, d))
+    out = torch.empty(1, xc.shape[0], dtype=torch.float32, device=dev)
+    check(lib().lng_row_sumsq(_ptr(xc), xc.shape[0], d, _ptr(out), _stream(dev)), "row_sumsq")
+    return out
+
+
 def causal_conv_rowsq(mixed: torch.Tensor, rowsq: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor,
                       dilation: int, eps: float, residual: bool = True) -> torch.Tensor:
     """:func:`causal_conv` (bf16, kernel 4, dilation 3) with row statistics from :func:`linear_rowsq`."""

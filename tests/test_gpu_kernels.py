@@ -277,3 +277,22 @@ def test_tree_accept_random_trees(dev):
                                       torch.tensor(am, device=dev))
         ln = int(plen[0])
         assert (_np(p)[:ln].tolist(), _np(nt)[:ln].tolist()) == cint.tree_accept(parent, toks, am)
+
+
+def test_large_linear_and_row_sumsq(dev):
+    """Large bf16 projection (hipBLASLt) against the MFMA kernel with the row-statistics epilogue and
+    fp64; the separate row sums of squares against the epilogue's partials and fp64."""
+    g = torch.Generator().manual_seed(21)
+    x = (torch.randn(4096, 1024, generator=g) * 0.5).bfloat16()
+    w = (torch.randn(768, 1024, generator=g) * 0.02).bfloat16()
+    y_lt = ops.linear(x.to(dev), w.to(dev))
+    y_mf, rsq = ops.linear_rowsq(x.to(dev), w.to(dev))
+    ref = x.double() @ w.double().T
+    assert om.rel_err(y_lt.cpu().double(), ref) < 1e-2
+    d = (y_lt.float() - y_mf.float()).abs()
+    assert float(d.max()) <= float(y_mf.float().abs().max()) * 2 ** -7     # at most a bf16 rounding apart
+    s = ops.row_sumsq(y_mf)
+    want = (y_mf.double() ** 2).sum(-1)
+    assert s.shape == (1, 4096)
+    torch.testing.assert_close(s[0].double(), want, rtol=1e-5, atol=0)
+    torch.testing.assert_close(s[0], rsq.sum(0), rtol=1e-5, atol=0)
