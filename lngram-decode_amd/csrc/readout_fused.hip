@@ -97,6 +97,8 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
   // chunk gather: instruction m, lane: route c0 + 2m + lane/32, order (lane/16)&1, 16-byte piece lane%16
   const int g_ord = (lane >> 4) & 1, g_par = lane >> 5, g_piece = lane & 15;
   const bf16* g_tab = g_ord ? table3 : table2;
+  // every row of a token at t >= 2 exists (both orders): its loads need no mask
+  const bool all_rows = tpos >= 2;
   auto gather = [&](int c0, u32x4 (&g)[16]) {
     const int32_t* rp = &rowsh[w][g_ord][g_par][c0 >> 1];
     int32_t rows[16];
@@ -109,11 +111,18 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
       rows[4 * v + 2] = r4[2];
       rows[4 * v + 3] = r4[3];
     }
+    if (all_rows) {
+      // routes past R hold row -1 too: clamp them to row 0 (their scores are masked below)
 #pragma unroll
-    for (int m = 0; m < 16; ++m) {
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      g[m] = rows[m] >= 0 ? *reinterpret_cast<const u32x4*>(g_tab + static_cast<int64_t>(rows[m]) * 128 + 8 * g_piece)
-                          : z;
+      for (int m = 0; m < 16; ++m)
+        g[m] = *reinterpret_cast<const u32x4*>(g_tab + static_cast<int64_t>(max(rows[m], 0)) * 128 + 8 * g_piece);
+    } else {
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const u32x4 z = {0u, 0u, 0u, 0u};
+        g[m] = rows[m] >= 0 ? *reinterpret_cast<const u32x4*>(g_tab + static_cast<int64_t>(rows[m]) * 128 + 8 * g_piece)
+                            : z;
+      }
     }
   };
   auto stash = [&](const u32x4 (&g)[16]) {
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
       for (int kk = 0; kk < 8; ++kk) ss = sumsq8(x[kk], ss);
       ss += __shfl_xor(ss, 16, 64);
       ss += __shfl_xor(ss, 32, 64);
-      sr[tt] = 1.0f / sqrtf(ss * (1.0f / FR_DT) + eps);  // route c0 + 16tt + li
+      sr[tt] = __builtin_amdgcn_rsqf(ss * (1.0f / FR_DT) + eps);  // route c0 + 16tt + li
       sc[tt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) sc[tt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x[kk], qb[kk], sc[tt], 0, 0, 0);
@@ -202,7 +211,7 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
     cmax = fmaxf(cmax, __shfl_xor(cmax, 16, 64));
     cmax = fmaxf(cmax, __shfl_xor(cmax, 32, 64));
     const float m_new = fmaxf(m_run, cmax);
-    const float alpha = expf(m_run - m_new);
+    const float alpha = __builtin_amdgcn_exp2f((m_run - m_new) * 1.4426950408889634f);
     m_run = m_new;
     float psum = 0.f;
     bf16x8 pa;
@@ -210,7 +219,7 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
     for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = expf(s[tt][i] - m_new);
+        const float p = __builtin_amdgcn_exp2f((s[tt][i] - m_new) * 1.4426950408889634f);
         psum += p;
         pa[4 * tt + i] = static_cast<bf16>(p * sD[tt][i]);
       }
@@ -218,10 +227,13 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
     float aD[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) aD[i] = __shfl(alpha, 4 * lg + i, 64);
+    // the running max seldom moves past the sink logit: rescale only when some lane's did
+    if (__ballot(alpha != 1.f) != 0ull) {
 #pragma unroll
-    for (int ft = 0; ft < 16; ++ft)
+      for (int ft = 0; ft < 16; ++ft)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[ft][i] *= aD[i];
+        for (int i = 0; i < 4; ++i) acc[ft][i] *= aD[i];
+    }
     // U += P . X with X transposed out of LDS: ds_read_b64_tr_b16 gives lane i of each
     // 16-lane group element i%4 of the 8-byte chunks addressed by lanes i/4 + 4c
     // (c = 0..3), i.e. X[4g + c][16ft + i] here.  The halves are joined with a shuffle
@@ -243,7 +255,7 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
   // normalise and stage u = w_mem . U / l for the value projection
   float lt = l_part + __shfl_xor(l_part, 16, 64);
   lt += __shfl_xor(lt, 32, 64);
-  lt += expf(sink - m_run);
+  lt += __builtin_amdgcn_exp2f((sink - m_run) * 1.4426950408889634f);
   const float inv = 1.0f / lt;
   float iD[4];
 #pragma unroll
