@@ -275,14 +275,15 @@ def scaled_gather(dev, steps: int, warmup: int) -> dict:
     return {"workload": "scaled-table gather + sum: B16 x T4096, R184, orders (2,3), 64x table "
                         "(51,249,152 x 128 bf16 = 13.1 GB), uniform random codes",
             "kernel": "k_gather_sum_scaled", "tokens_per_s": B * T / (ms * 1e-3), "avg_ms": ms,
-            "algorithmic_bytes": alg, "achieved_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "steps": steps}
+            "algorithmic_bytes": alg, "achieved_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "steps": steps,
+            "traffic": measured_traffic("gather_sum_scaled_traffic.json")}
 
 
-def measured_traffic():
-    """HBM-side bytes per launch of the fused readout at this workload, from the committed
-    hardware-counter summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor a
-    plain copy of known size reads for the same counter); None if the summary is absent."""
-    f = ROOT / "profiles" / "readout_fused_sb_traffic.json"
+def measured_traffic(name: str = "readout_fused_sb_traffic.json"):
+    """HBM-side bytes per launch of a kernel at its workload, from the committed hardware-counter
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor a plain copy of known
+    size reads for the same counter); None if the summary is absent."""
+    f = ROOT / "profiles" / name
     if not f.exists():
         return None
     try:
