@@ -60,6 +60,12 @@ class GpuDrafter:
                  online: bool = False, kappa: float = 1.0, tables: bool = True, fused: bool = False):
         c, t = _bundle_parts(bundle)
         self.cfg = c
+        # RefDrafter scores a sketch shortlist when the cap is positive and the bundle carries
+        # sketches (cpu_drafter.py:105, :179-181); this drafter scores the full vocabulary only.
+        cap = int(c.get("shortlist_cap", 0) if shortlist_cap is None else shortlist_cap)
+        if cap > 0 and any(f"sketch_ids_{n}" in t for n in c["ngrams"]):
+            raise NotImplementedError("sketch shortlist scoring is not on this path: the GPU drafter scores the "
+                                      "full vocabulary; pass shortlist_cap=0 for full-vocabulary drafting")
         self.topk = int(topk)
         self.online, self.kappa = bool(online), float(kappa)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())

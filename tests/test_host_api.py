@@ -100,6 +100,23 @@ def test_no_cpu_compute_path():
         lngram_v2.pack_bits_to_route_codes(torch.zeros(1, 2, 8, dtype=torch.bool), 4)
 
 
+def test_drafter_refuses_sketch_shortlist_and_cpu():
+    from drafting.gpu_drafter import GpuDrafter
+
+    cfg, t = workloads.build_draft_bundle(workloads.TINY_DRAFT, seed=0)
+    sk = dict(t)
+    for n in cfg["ngrams"]:
+        sk[f"sketch_ids_{n}"] = torch.zeros(4, 2, dtype=torch.int32)
+        sk[f"sketch_counts_{n}"] = torch.ones(4, 2, dtype=torch.int32)
+    with pytest.raises(NotImplementedError, match="shortlist"):
+        GpuDrafter((cfg, sk), shortlist_cap=8, device="cpu")
+    # a zero cap (or no sketches) is full-vocabulary drafting; this host has no GPU path
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        GpuDrafter((cfg, sk), shortlist_cap=0, device="cpu")
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        GpuDrafter((cfg, t), shortlist_cap=8, device="cpu")
+
+
 def test_storage_dtype_rule():
     assert lngram_v2.route_code_storage_dtype(4) == torch.uint8
     assert lngram_v2.route_code_storage_dtype(12) == torch.int16
