@@ -67,6 +67,79 @@ def cpu_baseline(seconds: float) -> dict:
                       "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)"}
 
 
+def sdc_cpu_baseline(seconds: float) -> dict:
+    """SD-C layer on the host cores, oracle restatements in the reference's op order: the SSM
+    recurrence (fp64, ``ssm.py:58-65``), router features (``router.py:50-59``), fp32 router logits
+    + sign-pack, and the bf16 module forward; 1 x 64-token windows repeated for ~``seconds``."""
+    import torch
+
+    from lngram_hip import workloads
+    from oracle import memory as om
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    w = workloads.SDC.with_shape(1, 64)
+    mem = workloads.build_memory(w, seed=0, device="cpu")
+    sd = {k: v.detach() for k, v in mem.state_dict().items()}
+    p = {k[len("module."):]: v for k, v in sd.items() if k.startswith("module.")}
+    p["router.weight"] = sd["router.weight"]
+    fsd = {k: v.detach() for k, v in mem.router_features.state_dict().items()}
+    cfg = om.MemCfg(w.d_model, w.routes, w.mem_dim, w.q_heads, w.kv_heads, w.head_dim, eps=w.norm_eps)
+    g = torch.Generator().manual_seed(7)
+    E = (torch.randn(w.vocab, w.d_model, generator=g) * 0.02).to(w.dtype)
+    tok = torch.randint(0, w.vocab, (w.batch, w.seq), generator=g)
+    a = (0.9 + 0.099 * torch.rand(w.ssm_dim, generator=g)).numpy()
+    u = torch.randn(w.batch, w.seq, w.ssm_dim, generator=g).numpy()
+    h = workloads.make_hidden(w, seed=1)
+    n_tok, t0 = 0, time.perf_counter()
+    while True:
+        s = torch.from_numpy(om.ssm_scan(a, u)).float()
+        x = om.router_features(E[tok], fsd["start"], fsd["prev_norm.weight"], fsd["cur_norm.weight"], w.norm_eps, s)
+        q = om.router_logits(x, p["router.weight"], work=torch.float32)
+        om.memory_forward(p, cfg, h, om.pack_route_codes(q.numpy(), 4))
+        n_tok += w.tokens
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"SD-C shape (d1024, R181, N256, bf16) 1x64-token windows, {n_tok} tokens in {el:.1f} s: "
+                      "oracle SSM recurrence + router features + fp32 router + PyTorch-CPU module forward"}
+
+
+def scaled_cpu_baseline(seconds: float) -> dict:
+    """Scaled-table gather + sum on the host cores: the oracle's row formula (hashed slots), then
+    the reference's embedding gather in bf16 and an fp32 sum over routes and orders (PyTorch-CPU), on
+    a table grown 4x instead of 64x (0.8 GB instead of 13.1 GB, so that it is quick to fill; every
+    row read is still a random 256 B row far outside the host's caches); 1 x 4096-token batches
+    repeated for ~``seconds``."""
+    import torch
+
+    from oracle import memory as om
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    R, T, orders, sl, md = 184, 4096, (2, 3), 2, 128
+    n2, n3 = R << (sl + 8), R << (sl + 12)
+    g = torch.Generator().manual_seed(0)
+    blk = (torch.randn(1 << 12, md, generator=g) * 0.02).to(torch.bfloat16)   # tiled: quick to fill
+    tabs = [blk.repeat(n >> 12, 1) for n in (n2, n3)]            # row counts are multiples of 4096
+    codes = torch.randint(0, 16, (1, T, R), generator=g, dtype=torch.uint8).numpy()
+    n_tok, t0, i = 0, time.perf_counter(), 0
+    while True:
+        om.gather_sum_rows_torch(tabs, om.scaled_rows(codes, orders, 4, sl, seed=2024 + i))
+        n_tok += T
+        i += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    rows = R * ((T - 1) + (T - 2))
+    gbs = i * (rows * md * 2 + T * md * 4 + T * R) / el / 1e9
+    del tabs
+    return {"value": n_tok / el, "unit": "tokens/s", "GBs": gbs, "cores": threads, "kind": "port",
+            "sample": f"184 routes, orders (2,3), table grown 4x ({(n2 + n3) * md * 2 / 1e9:.1f} GB bf16), "
+                      f"{i} x 4096-token batches in {el:.1f} s: oracle row formula + PyTorch-CPU gather, fp32 sum"}
+
+
 def draft_cpu_baseline(seconds: float) -> dict:
     """The oracle's C++ port of the reference CPU drafter (``drafter.cpp`` per-token algorithm, fp32,
     bf16 tables, OpenMP over routes and vocabulary rows, online counts on) timed on the host cores:
@@ -279,6 +352,29 @@ def scaled_gather(dev, steps: int, warmup: int) -> dict:
             "traffic": measured_traffic("gather_sum_scaled_traffic.json")}
 
 
+def copy_bandwidth(dev, mib: int = 2048, reps: int = 10) -> float:
+    """Bytes read + written per second by a plain device-to-device copy of ``mib`` MiB (HIP
+    events over ``reps`` copies): the bandwidth a streaming kernel reaches on this GPU, reported
+    beside the nominal 8 TB/s peak that every fraction here is taken against."""
+    import torch
+
+    n = mib << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * n * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
+    return gbs
+
+
 def measured_traffic(name: str = "readout_fused_sb_traffic.json"):
     """HBM-side bytes per launch of a kernel at its workload, from the committed hardware-counter
     summary (FETCH_SIZE + WRITE_SIZE per dispatch, each scaled by the factor a plain copy of known
@@ -384,6 +480,7 @@ def main() -> None:
                      "algorithmic_bytes": fused_bytes, "avg_ms": fused_ms},
         "layer_hbm_frac": layer_gbs / HBM_PEAK_GBS,
         "layer_algorithmic_bytes": layer_bytes,
+        "copy_GBs": copy_bandwidth(dev),
     }
     if not args.no_draft:
         log("draft step")
@@ -394,9 +491,15 @@ def main() -> None:
     if not args.no_scaled:
         log("scaled-table gather")
         result["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 2)
+        if not args.no_cpu:
+            log("scaled-table gather cpu baseline")
+            result["scaled_gather"]["cpu_baseline"] = scaled_cpu_baseline(min(args.cpu_seconds, 8.0))
     if not args.no_sdc:
         log("SD-C forward")
         result["sdc_forward"] = sdc_forward(dev, max(3, args.steps // 2), 2)
+        if not args.no_cpu:
+            log("SD-C cpu baseline")
+            result["sdc_forward"]["cpu_baseline"] = sdc_cpu_baseline(min(args.cpu_seconds, 8.0))
         log("tiny forward")
         result["tiny_forward"] = tiny_forward(dev, 50, 5)
     if not args.no_cpu:

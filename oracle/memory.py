@@ -213,6 +213,22 @@ def gather_sum_scaled(tables, codes, orders, bits: int, scale_log2: int, seed: i
     return out if positions is not None else out.reshape(b, t, md)
 
 
+def gather_sum_rows_torch(tables, rows: np.ndarray) -> torch.Tensor:
+    """The gather of ``_lookup_route_chunk`` (``lngram_v2.py:1084-1092``: embedding lookup in the
+    table dtype, masked rows multiplied by 0) followed by an fp32 sum over routes and orders, in
+    PyTorch on the tables' device: fp32 ``[B, T, mem_dim]`` from int64 rows ``[B, T, R, n_orders]``
+    (-1 = masked).  The CPU-timed form of ``gather_sum_scaled``; the tests hold it to that fp64
+    restatement."""
+    b, t, r, no = rows.shape
+    out = torch.zeros(b * t, tables[0].shape[1], dtype=torch.float32)
+    for oi in range(no):
+        sel = torch.from_numpy(rows[..., oi].reshape(b * t, r))
+        ok = sel >= 0
+        got = torch.nn.functional.embedding(sel.clamp_min(0), tables[oi]) * ok[..., None].to(tables[oi].dtype)
+        out += got.float().sum(1)
+    return out.reshape(b, t, -1)
+
+
 # ----------------------------------------------------------------------------- float parts
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     """RMSNorm as the reference rounds it: normalise in fp32 (fp64 for fp64 input),

@@ -89,3 +89,15 @@ def test_gather_sum_of_constant_tables_counts_rows():
     out = om.gather_sum_scaled(tabs, c, (2, 3), 4, 1, 0)
     want = np.array([0, 3, 6, 6, 6], float)                # t=0: none, t=1: 2-grams, t>=2: both
     assert (out[..., 0] == want[None]).all()
+
+
+def test_torch_gather_sum_agrees_with_the_fp64_restatement():
+    g = torch.Generator().manual_seed(5)
+    c = np.random.default_rng(6).integers(0, 16, (2, 9, 5))
+    tabs = [torch.randn(5 * 4 * 256, 16, generator=g).to(torch.bfloat16),
+            torch.randn(5 * 4 * 4096, 16, generator=g).to(torch.bfloat16)]
+    want = om.gather_sum_scaled(tabs, c, (2, 3), 4, 2, 11)
+    got = om.gather_sum_rows_torch(tabs, om.scaled_rows(c, (2, 3), 4, 2, 11))
+    assert got.dtype == torch.float32 and got.shape == want.shape
+    assert om.rel_err(got.double(), torch.from_numpy(want)) < 1e-6   # bf16 rows are exact in fp32
+    assert (got[:, 0] == 0).all()                                     # t = 0 reads no row
