@@ -13,8 +13,10 @@
 // the memory path with the readout replaced by a plain sum.  Positions t < n-1 read nothing (the
 // reference's zero rows).  Table n holds R * S * 16^n rows, so every row read lies inside it.
 //
-// Layout: one wave per token.  A row of `row_bytes` = mem_dim * elem bytes is read as
-// P = row_bytes / 16 pieces by P consecutive lanes, so one wave load moves 64/P whole rows
+// Layout: one wave per token.  The wave first forms every row index of its token (codes from
+// LDS, the slot hash) into an LDS list, so the load loop that follows issues its loads back to
+// back with no dependent work in between.  A row of `row_bytes` = mem_dim * elem bytes is read
+// as P = row_bytes / 16 pieces by P consecutive lanes, so one wave load moves 64/P whole rows
 // (4 rows of 256 B for bf16 x 128).  Each lane keeps the fp32 sums of its piece's elements over
 // the rows its lane group reads; the groups are folded with cross-lane permutes at the end.
 // Eight loads per lane are in flight before the first is summed.
@@ -46,13 +48,15 @@ struct GsArgs {
 };
 
 // grid (cdiv(n_tok, 4)), block 256: wave w owns token 4 * blockIdx.x + w.
-// TT = element type (bf16 or float); P = 16-byte pieces per row (divides 64).
-template <typename TT, int P>
+// TT = element type (bf16 or float); P = 16-byte pieces per row (divides 64); RT = the type of
+// the staged row indices (int32_t when every table has fewer than 2^31 rows, else int64_t).
+template <typename TT, int P, typename RT>
 __global__ __launch_bounds__(256) void k_gather_sum_scaled(GsArgs A, const uint8_t* __restrict__ codes,
                                                            float* __restrict__ out) {
   constexpr int VE = 16 / sizeof(TT);  // elements per piece
   constexpr int RPI = 64 / P;          // rows per wave load
   __shared__ uint8_t cs[4][GS_MAXN][GS_MAXR];
+  __shared__ RT rows_l[4][GS_MAXR * GS_MAXN + 64];  // row index of row i of the token, -1 = masked
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t p = static_cast<int64_t>(blockIdx.x) * 4 + w;
   const bool live = p < A.n_tok;
@@ -72,8 +76,8 @@ __global__ __launch_bounds__(256) void k_gather_sum_scaled(GsArgs A, const uint8
   const uint32_t smask = (1u << A.scale_log2) - 1u, cmask = (1u << bits) - 1u;
   const uint32_t pmix = static_cast<uint32_t>(p) * 0x9E3779B1u;
   const int64_t row_bytes = static_cast<int64_t>(P) * 16;
-  // byte offset of row i of this token (i = r * n_orders + oi), -1 where the row is masked
-  auto row_off = [&](int i) -> int64_t {
+  // row index of row i of this token (i = r * n_orders + oi), -1 where the row is masked
+  auto row_of = [&](int i) -> int64_t {
     const int r = i / n_ord, oi = i - r * n_ord;
     const int n = A.order[oi];
     if (!live || t < n - 1) return -1;
@@ -81,21 +85,25 @@ __global__ __launch_bounds__(256) void k_gather_sum_scaled(GsArgs A, const uint8
     for (int k = 0; k < n; ++k) addr |= (static_cast<uint32_t>(cs[w][maxn - n + k][r]) & cmask) << (bits * k);
     const uint32_t slot = mix32(A.seed ^ mix32(pmix + static_cast<uint32_t>(i))) & smask;
     const int64_t block = int64_t{1} << (bits * n);
-    const int64_t row = (static_cast<int64_t>(r) * (smask + 1) + slot) * block + addr;
-    return row * row_bytes;
+    return (static_cast<int64_t>(r) * (smask + 1) + slot) * block + addr;
   };
+  const int steps = (nrows + RPI - 1) / RPI;
+  for (int i = lane; i < steps * RPI; i += 64) rows_l[w][i] = i < nrows ? static_cast<RT>(row_of(i)) : RT(-1);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   float acc[VE];
 #pragma unroll
   for (int e = 0; e < VE; ++e) acc[e] = 0.f;
-  const int steps = (nrows + RPI - 1) / RPI;
   for (int s0 = 0; s0 < steps; s0 += GS_UNROLL) {
     u32x4 v[GS_UNROLL];
 #pragma unroll
     for (int u = 0; u < GS_UNROLL; ++u) {
       const int i = (s0 + u) * RPI + g;
-      const int64_t off = (s0 + u < steps && i < nrows) ? row_off(i) : -1;
+      const int64_t row = s0 + u < steps ? static_cast<int64_t>(rows_l[w][i]) : -1;
       const int oi = i % n_ord;
-      v[u] = off >= 0 ? *reinterpret_cast<const u32x4*>(A.tab[oi] + off + 16 * pc) : u32x4{0u, 0u, 0u, 0u};
+      v[u] = row >= 0 ? *reinterpret_cast<const u32x4*>(A.tab[oi] + row * row_bytes + 16 * pc)
+                      : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int u = 0; u < GS_UNROLL; ++u) {
@@ -142,6 +150,7 @@ extern "C" int lng_gather_sum_scaled(const void* const* tables, int table_dtype,
     return fail(LNG_E_ARG, "gather_sum_scaled: mem_dim * element size must be 16 B times a divisor of 64");
   GsArgs A{};
   A.maxn = 0;
+  bool rows32 = true;  // every table holds fewer than 2^31 rows
   for (int i = 0; i < n_orders; ++i) {
     if (orders[i] < 1 || orders[i] > GS_MAXN || !tables[i])
       return fail(LNG_E_ARG, "gather_sum_scaled: orders must lie in [1, 4] with a table each");
@@ -150,6 +159,7 @@ extern "C" int lng_gather_sum_scaled(const void* const* tables, int table_dtype,
     A.tab[i] = static_cast<const char*>(tables[i]);
     A.order[i] = orders[i];
     A.maxn = std::max(A.maxn, orders[i]);
+    rows32 = rows32 && (static_cast<int64_t>(R) << (scale_log2 + bits * orders[i])) <= INT32_MAX;
   }
   A.n_orders = n_orders;
   A.bits = bits;
@@ -163,26 +173,25 @@ extern "C" int lng_gather_sum_scaled(const void* const* tables, int table_dtype,
   const dim3 grid(static_cast<unsigned>(cdiv(A.n_tok, 4)));
   hipStream_t s = as_stream(stream);
   auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, A, codes, out); };
+  auto by_piece = [&](auto tt, auto rt) {
+    using TT = decltype(tt);
+    using RT = decltype(rt);
+    switch (P) {
+      case 1: go(k_gather_sum_scaled<TT, 1, RT>); break;
+      case 2: go(k_gather_sum_scaled<TT, 2, RT>); break;
+      case 4: go(k_gather_sum_scaled<TT, 4, RT>); break;
+      case 8: go(k_gather_sum_scaled<TT, 8, RT>); break;
+      case 16: go(k_gather_sum_scaled<TT, 16, RT>); break;
+      case 32: go(k_gather_sum_scaled<TT, 32, RT>); break;
+      default: go(k_gather_sum_scaled<TT, 64, RT>); break;
+    }
+  };
   if (table_dtype == LNG_BF16) {
-    switch (P) {
-      case 1: go(k_gather_sum_scaled<bf16, 1>); break;
-      case 2: go(k_gather_sum_scaled<bf16, 2>); break;
-      case 4: go(k_gather_sum_scaled<bf16, 4>); break;
-      case 8: go(k_gather_sum_scaled<bf16, 8>); break;
-      case 16: go(k_gather_sum_scaled<bf16, 16>); break;
-      case 32: go(k_gather_sum_scaled<bf16, 32>); break;
-      default: go(k_gather_sum_scaled<bf16, 64>); break;
-    }
+    if (rows32) by_piece(bf16{}, int32_t{});
+    else by_piece(bf16{}, int64_t{});
   } else {
-    switch (P) {
-      case 1: go(k_gather_sum_scaled<float, 1>); break;
-      case 2: go(k_gather_sum_scaled<float, 2>); break;
-      case 4: go(k_gather_sum_scaled<float, 4>); break;
-      case 8: go(k_gather_sum_scaled<float, 8>); break;
-      case 16: go(k_gather_sum_scaled<float, 16>); break;
-      case 32: go(k_gather_sum_scaled<float, 32>); break;
-      default: go(k_gather_sum_scaled<float, 64>); break;
-    }
+    if (rows32) by_piece(float{}, int32_t{});
+    else by_piece(float{}, int64_t{});
   }
   return check_launch("gather_sum_scaled");
 }
