@@ -10,9 +10,10 @@
 // which equals the reference's RMSNorm -> KV projection -> sink GQA without ever
 // forming keys or values.
 //
-// Block = 4 waves = 4 tokens.  Phases A and C are cooperative (wave = KV head, the 16
-// MFMA columns = 4 tokens x 4 groups); phase B is one token per wave, routes in
-// chunks of 32.  A chunk is gathered with whole-row loads (16 lanes x 16 B = one
+// Block = 8 waves = 8 tokens.  Phases A and C are cooperative: wave w takes KV head w & 3 and
+// half of that head's weight rows (features in A, head dims in C), for two MFMA column tiles
+// of 16 = 4 tokens x 4 groups, so every weight row is fetched once per 8 tokens.  Phase B is
+// one token per wave, routes in chunks of 32.  A chunk is gathered with whole-row loads (16 lanes x 16 B = one
 // 256-byte table row per quarter wave), parked in the wave's LDS region in row layout,
 // read back as the score MFMA's A operand (ds_read_b128) and, transposed, as the
 // B operand of P.X (ds_read_b64_tr_b16).  The next chunk's rows are in flight while a
@@ -21,7 +22,7 @@
 
 namespace lng {
 
-constexpr int FR_TOK = 4;          // tokens per block (one per wave in phase B)
+constexpr int FR_TOK = 8;          // tokens per block (one per wave in phase B)
 constexpr int FR_H = 16;           // query heads
 constexpr int FR_HD = 64;          // head dim
 constexpr int FR_DT = 256;         // route token dim (2 orders x 128)
@@ -48,11 +49,11 @@ __device__ __forceinline__ float sumsq8(const bf16x8 v, float acc) {
   return acc;
 }
 
-// LDS (75.8 KB per block, two blocks per CU): per wave a 32-row region reused as qkw
-// (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B) and u (rows 0..15,
+// LDS (148.5 KB per block, one block of 8 waves per CU): per wave a 32-row region reused as
+// qkw (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B) and u (rows 0..15,
 // phase B -> C); per wave the token's row indices [order][route parity][route / 2]
-// (-1 = zero row).
-__global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict__ q, const uint8_t* __restrict__ codes,
+// (-1 = zero row); the memory-norm weight.
+__global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict__ q, const uint8_t* __restrict__ codes,
                                                           int64_t B, int64_t T, int32_t R,
                                                           const bf16* __restrict__ table2,
                                                           const bf16* __restrict__ table3,
@@ -61,8 +62,27 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
                                                           float sink, bf16* __restrict__ head_out) {
   __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
   __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][2][FR_RB];
+  __shared__ __attribute__((aligned(16))) bf16 wms[FR_DT];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
+  if (threadIdx.x < FR_DT) wms[threadIdx.x] = w_mem[threadIdx.x];
+
+  // phase-A operands first (no dependence on the codes), so their latency overlaps stage 0:
+  // wave w takes head h = w & 3 and features 128 (w >> 2) .. +127; column tile tt = tokens 4tt .. 4tt+3
+  const int a_h = w & 3, a_f0 = 128 * (w >> 2), a_hg = a_h * 4 + (li & 3);
+  bf16x8 bq[2][2], wa[8][2];
+#pragma unroll
+  for (int tt = 0; tt < 2; ++tt) {
+    const int64_t tq = static_cast<int64_t>(blockIdx.x) * FR_TOK + 4 * tt + (li >> 2);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      bq[tt][ks] = tq < B * T ? ld16(q + tq * (FR_H * FR_HD) + a_hg * FR_HD + 32 * ks + 8 * lg) : zero8();
+  }
+#pragma unroll
+  for (int ft = 0; ft < 8; ++ft)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      wa[ft][ks] = ld16(wk_t + (static_cast<int64_t>(a_h) * FR_DT + a_f0 + 16 * ft + li) * FR_HD + 32 * ks + 8 * lg);
   const int64_t ntok = B * T;
   const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * FR_TOK;
   const int64_t tok = tok0 + w;
@@ -134,30 +154,21 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
   u32x4 g[16];
   gather(0, g);  // first chunk in flight during phase A
 
-  // ---------------- phase A: qkw[t][4h+g][f] = scale * w_mem[f] * (Wk[h]^T q[t][4h+g])[f], wave = head h
-  {
-    const int h = w;
-    const int64_t tq = tok0 + (li >> 2);
-    const int hg = h * 4 + (li & 3);
-    bf16x8 bq[2], wa[16][2];
+  // ---------------- phase A: qkw[t][4h+g][f] = scale * w_mem[f] * (Wk[h]^T q[t][4h+g])[f]
+  __syncthreads();  // wms
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      bq[ks] = tq < ntok ? ld16(q + tq * (FR_H * FR_HD) + hg * FR_HD + 32 * ks + 8 * lg) : zero8();
+  for (int ft = 0; ft < 8; ++ft) {
+    const int f = a_f0 + 16 * ft + 4 * lg;
+    const bf16x4 wm4 = *reinterpret_cast<const bf16x4*>(&wms[f]);
 #pragma unroll
-    for (int ft = 0; ft < 16; ++ft)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        wa[ft][ks] = ld16(wk_t + (static_cast<int64_t>(h) * FR_DT + 16 * ft + li) * FR_HD + 32 * ks + 8 * lg);
-#pragma unroll
-    for (int ft = 0; ft < 16; ++ft) {
+    for (int tt = 0; tt < 2; ++tt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[ft][ks], bq[ks], d, 0, 0, 0);
-      const int f = 16 * ft + 4 * lg;
+      for (int ks = 0; ks < 2; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[ft][ks], bq[tt][ks], d, 0, 0, 0);
       bf16x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(w_mem[f + i]) * scale);
-      *reinterpret_cast<bf16x4*>(&xs[li >> 2][hg][f]) = o;
+      for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(wm4[i]) * scale);
+      *reinterpret_cast<bf16x4*>(&xs[4 * tt + (li >> 2)][a_hg][f]) = o;
     }
   }
   __syncthreads();
@@ -252,6 +263,16 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
     __builtin_amdgcn_wave_barrier();
   }
 
+  // phase-C operands (wave w: head h = w & 3, head dims 32 (w >> 2) .. +31), loaded before the
+  // block-wide barrier below so that their latency overlaps it
+  const int c_h = w & 3, c_dh = 2 * (w >> 2), c_hg = c_h * 4 + (li & 3);
+  bf16x8 va[2][8];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      va[dt][ks] = ld16(wv + (static_cast<int64_t>(c_h) * FR_HD + 16 * (c_dh + dt) + li) * FR_DT + 32 * ks + 8 * lg);
+
   // normalise and stage u = w_mem . U / l for the value projection
   float lt = l_part + __shfl_xor(l_part, 16, 64);
   lt += __shfl_xor(lt, 32, 64);
@@ -263,27 +284,22 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
 #pragma unroll
   for (int ft = 0; ft < 16; ++ft) {
     const int f = 16 * ft + li;
-    const float wm = to_f32(w_mem[f]);
+    const float wm = to_f32(wms[f]);
 #pragma unroll
     for (int i = 0; i < 4; ++i) xs[w][4 * lg + i][f] = static_cast<bf16>(acc[ft][i] * iD[i] * wm);
   }
   __syncthreads();
 
-  // ---------------- phase C: o[t][4h+g][d] = Wv[h][d] . u[t][4h+g], wave = head h
-  {
-    const int h = w;
-    const int64_t tc = tok0 + (li >> 2);
-    const int hg = h * 4 + (li & 3);
-    bf16x8 va[4][8], ub[8];
+  // ---------------- phase C: o[t][4h+g][d] = Wv[h][d] . u[t][4h+g]; column tile tt = tokens 4tt .. 4tt+3
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+  for (int tt = 0; tt < 2; ++tt) {
+    const int64_t tc = tok0 + 4 * tt + (li >> 2);
+    bf16x8 ub[8];
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks)
-        va[dt][ks] = ld16(wv + (static_cast<int64_t>(h) * FR_HD + 16 * dt + li) * FR_DT + 32 * ks + 8 * lg);
+    for (int ks = 0; ks < 8; ++ks)
+      ub[ks] = *reinterpret_cast<const bf16x8*>(&xs[4 * tt + (li >> 2)][c_hg][32 * ks + 8 * lg]);
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) ub[ks] = *reinterpret_cast<const bf16x8*>(&xs[li >> 2][hg][32 * ks + 8 * lg]);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
+    for (int dt = 0; dt < 2; ++dt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][ks], ub[ks], d, 0, 0, 0);
@@ -291,7 +307,7 @@ __global__ __launch_bounds__(256, 2) void k_readout_fused(const bf16* __restrict
         bf16x4 o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i]);
-        *reinterpret_cast<bf16x4*>(head_out + tc * (FR_H * FR_HD) + hg * FR_HD + 16 * dt + 4 * lg) = o;
+        *reinterpret_cast<bf16x4*>(head_out + tc * (FR_H * FR_HD) + c_hg * FR_HD + 16 * (c_dh + dt) + 4 * lg) = o;
       }
     }
   }
@@ -311,7 +327,7 @@ extern "C" int lng_memory_readout_fused(const void* q, const uint8_t* codes, int
   if (ntok == 0) return LNG_OK;
   const int64_t blocks = cdiv(ntok, FR_TOK);
   if (blocks > 0x7fffffffLL) return fail(LNG_E_ARG, "memory_readout_fused: too many tokens");
-  hipLaunchKernelGGL(k_readout_fused, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, as_stream(stream),
+  hipLaunchKernelGGL(k_readout_fused, dim3(static_cast<unsigned>(blocks)), dim3(64 * FR_TOK), 0, as_stream(stream),
                      static_cast<const bf16*>(q), codes, B, T, R, static_cast<const bf16*>(table2),
                      static_cast<const bf16*>(table3), static_cast<const bf16*>(wk_t), static_cast<const bf16*>(wv),
                      static_cast<const bf16*>(w_mem), eps, scale, sink_logit, static_cast<bf16*>(head_out));
