@@ -153,17 +153,23 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
  *   o_{h,g}       = Wv[h] (w_mem . sum_r p_{h,g,r} s_r x_r)
  * with an online softmax seeded by the sink (m, l) = (b0, 1).  bf16 only;
  * shape: orders (2,3), mem_dim 128, 16 query heads x 64, 4 KV heads.
- *   q       [N_tok, 16*64]  projected query (readout_q_proj output)
- *   codes   [B, T, R] uint8 route codes
- *   table2  [R*256, 128], table3 [R*4096, 128]
- *   wk_t    [4, 256, 64]    key weight, per head transposed (f-major)
- *   wv      [4, 64, 256]    value weight (kv_proj rows 256..511)
- *   w_mem   [256]           readout_memory_norm.weight
- *   head_out[N_tok, 16*64]  attention output (input of readout_o_proj) */
+ *   q        [N_tok, 16*64]  projected query (readout_q_proj output)
+ *   codes    [B, T, R] uint8 route codes
+ *   table2   [R*256, 128], table3 [R*4096, 128]
+ *   kv_pack  [LNG_READOUT_PACK_ELEMS] bf16, readout_kv_proj.weight in the kernel's operand
+ *            order, made by lng_memory_readout_pack (once per weight version)
+ *   w_mem    [256]           readout_memory_norm.weight
+ *   head_out [N_tok, 16*64]  attention output (input of readout_o_proj) */
+#define LNG_READOUT_PACK_ELEMS 131072
 int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int64_t T, int32_t R,
-                             const void* table2, const void* table3, const void* wk_t, const void* wv,
-                             const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
-                             void* stream);
+                             const void* table2, const void* table3, const void* kv_pack, const void* w_mem,
+                             float eps, float scale, float sink_logit, void* head_out, void* stream);
+
+/* kv_pack [LNG_READOUT_PACK_ELEMS] bf16 from readout_kv_proj.weight kv [512, 256] bf16 (rows
+ * 0..255 the keys, 256..511 the values of the 4 KV heads, lngram_v2.py:1120-1131): the key
+ * and value weights rearranged so that every weight load of lng_memory_readout_fused reads
+ * one contiguous kilobyte.  A pure permutation (no arithmetic). */
+int lng_memory_readout_pack(const void* kv, void* kv_pack, void* stream);
 
 /* out[B*T, mem_dim] (fp32) = sum over routes r and orders n (t >= n-1) of table_n[row, :] with
  *   row = (r * S + slot) * 2^(bits n) + addr_n,   S = 2^scale_log2,

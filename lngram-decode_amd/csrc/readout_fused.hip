@@ -10,10 +10,11 @@
 // which equals the reference's RMSNorm -> KV projection -> sink GQA without ever
 // forming keys or values.
 //
-// Block = 8 waves = 8 tokens.  Phases A and C are cooperative: wave w takes KV head w & 3 and
-// half of that head's weight rows (features in A, head dims in C), for two MFMA column tiles
-// of 16 = 4 tokens x 4 groups, so every weight row is fetched once per 8 tokens.  Phase B is
-// one token per wave, routes in chunks of 32.  A chunk is gathered with whole-row loads (16 lanes x 16 B = one
+// Block = TOK waves = TOK tokens (TOK = 4 or 8).  Phases A and C are cooperative: wave w takes
+// KV head w & 3 and a TOK/4-th share of that head's weight rows (features in A, head dims in
+// C), for TOK/4 MFMA column tiles of 16 = 4 tokens x 4 groups, so every weight row is fetched
+// once per block.  The weights come packed in MFMA operand order (lng_memory_readout_pack): one
+// weight load is one contiguous kilobyte.  Phase B is one token per wave, routes in chunks of 32.  A chunk is gathered with whole-row loads (16 lanes x 16 B = one
 // 256-byte table row per quarter wave), parked in the wave's LDS region in row layout,
 // read back as the score MFMA's A operand (ds_read_b128) and, transposed, as the
 // B operand of P.X (ds_read_b64_tr_b16).  The next chunk's rows are in flight while a
@@ -22,13 +23,19 @@
 
 namespace lng {
 
-constexpr int FR_TOK = 8;          // tokens per block (one per wave in phase B)
 constexpr int FR_H = 16;           // query heads
 constexpr int FR_HD = 64;          // head dim
 constexpr int FR_DT = 256;         // route token dim (2 orders x 128)
 constexpr int FR_LD = FR_DT + 8;   // padded LDS row (bf16): 528 B, conflict-free 16-row access
 constexpr int FR_MAXR = 256;       // max routes (row-index slots per token)
 constexpr int FR_RB = FR_MAXR / 2;
+// packed KV weight (bf16 elements): keys [h 4][ft 16][ks 2][lane 64][8] = Wk^T[h][16ft + lane%16][32ks + 8(lane/16) ..+8],
+// then values [h 4][dt 4][ks 8][lane 64][8] = Wv[h][16dt + lane%16][32ks + 8(lane/16) ..+8]
+constexpr int FR_PK_V = 4 * 16 * 2 * 64 * 8;
+static_assert(2 * FR_PK_V == LNG_READOUT_PACK_ELEMS, "packed KV weight size");
+#ifndef LNG_READOUT_TOK
+#define LNG_READOUT_TOK 4
+#endif
 
 __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ bf16x8 zero8() {
@@ -49,15 +56,17 @@ __device__ __forceinline__ float sumsq8(const bf16x8 v, float acc) {
   return acc;
 }
 
-// LDS (148.5 KB per block, one block of 8 waves per CU): per wave a 32-row region reused as
-// qkw (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B) and u (rows 0..15,
-// phase B -> C); per wave the token's row indices [order][route parity][route / 2]
-// (-1 = zero row); the memory-norm weight.
-__global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict__ q, const uint8_t* __restrict__ codes,
+// LDS (TOK = 8: 148.5 KB, one block per CU; TOK = 4: 74.3 KB, two blocks per CU): per wave a
+// 32-row region reused as qkw (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B)
+// and u (rows 0..15, phase B -> C); per wave the token's row indices [order][route parity]
+// [route / 2] (-1 = zero row); the memory-norm weight.
+template <int FR_TOK>
+__global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const bf16* __restrict__ q,
+                                                          const uint8_t* __restrict__ codes,
                                                           int64_t B, int64_t T, int32_t R,
                                                           const bf16* __restrict__ table2,
                                                           const bf16* __restrict__ table3,
-                                                          const bf16* __restrict__ wk_t, const bf16* __restrict__ wv,
+                                                          const bf16* __restrict__ kv_pack,
                                                           const bf16* __restrict__ w_mem, float eps, float scale,
                                                           float sink, bf16* __restrict__ head_out) {
   __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
@@ -68,21 +77,22 @@ __global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict
   if (threadIdx.x < FR_DT) wms[threadIdx.x] = w_mem[threadIdx.x];
 
   // phase-A operands first (no dependence on the codes), so their latency overlaps stage 0:
-  // wave w takes head h = w & 3 and features 128 (w >> 2) .. +127; column tile tt = tokens 4tt .. 4tt+3
-  const int a_h = w & 3, a_f0 = 128 * (w >> 2), a_hg = a_h * 4 + (li & 3);
-  bf16x8 bq[2][2], wa[8][2];
+  // wave w takes head h = w & 3 and feature tiles ft0 .. ft0 + NFT-1; column tile tt = tokens 4tt .. 4tt+3
+  constexpr int NTT = FR_TOK / 4, NFT = 16 / NTT, NDT = 4 / NTT;
+  const int a_h = w & 3, a_ft0 = NFT * (w >> 2), a_hg = a_h * 4 + (li & 3);
+  bf16x8 bq[NTT][2], wa[NFT][2];
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
+  for (int tt = 0; tt < NTT; ++tt) {
     const int64_t tq = static_cast<int64_t>(blockIdx.x) * FR_TOK + 4 * tt + (li >> 2);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
       bq[tt][ks] = tq < B * T ? ld16(q + tq * (FR_H * FR_HD) + a_hg * FR_HD + 32 * ks + 8 * lg) : zero8();
   }
 #pragma unroll
-  for (int ft = 0; ft < 8; ++ft)
+  for (int ft = 0; ft < NFT; ++ft)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      wa[ft][ks] = ld16(wk_t + (static_cast<int64_t>(a_h) * FR_DT + a_f0 + 16 * ft + li) * FR_HD + 32 * ks + 8 * lg);
+      wa[ft][ks] = ld16(kv_pack + (((a_h * 16 + a_ft0 + ft) * 2 + ks) * 64 + lane) * 8);
   const int64_t ntok = B * T;
   const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * FR_TOK;
   const int64_t tok = tok0 + w;
@@ -157,11 +167,11 @@ __global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict
   // ---------------- phase A: qkw[t][4h+g][f] = scale * w_mem[f] * (Wk[h]^T q[t][4h+g])[f]
   __syncthreads();  // wms
 #pragma unroll
-  for (int ft = 0; ft < 8; ++ft) {
-    const int f = a_f0 + 16 * ft + 4 * lg;
+  for (int ft = 0; ft < NFT; ++ft) {
+    const int f = 16 * (a_ft0 + ft) + 4 * lg;
     const bf16x4 wm4 = *reinterpret_cast<const bf16x4*>(&wms[f]);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
+    for (int tt = 0; tt < NTT; ++tt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[ft][ks], bq[tt][ks], d, 0, 0, 0);
@@ -263,15 +273,15 @@ __global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict
     __builtin_amdgcn_wave_barrier();
   }
 
-  // phase-C operands (wave w: head h = w & 3, head dims 32 (w >> 2) .. +31), loaded before the
-  // block-wide barrier below so that their latency overlaps it
-  const int c_h = w & 3, c_dh = 2 * (w >> 2), c_hg = c_h * 4 + (li & 3);
-  bf16x8 va[2][8];
+  // phase-C operands (wave w: head h = w & 3, head-dim tiles dt0 .. dt0 + NDT-1), loaded before
+  // the block-wide barrier below so that their latency overlaps it
+  const int c_h = w & 3, c_dh = NDT * (w >> 2), c_hg = c_h * 4 + (li & 3);
+  bf16x8 va[NDT][8];
 #pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      va[dt][ks] = ld16(wv + (static_cast<int64_t>(c_h) * FR_HD + 16 * (c_dh + dt) + li) * FR_DT + 32 * ks + 8 * lg);
+      va[dt][ks] = ld16(kv_pack + FR_PK_V + (((c_h * 4 + c_dh + dt) * 8 + ks) * 64 + lane) * 8);
 
   // normalise and stage u = w_mem . U / l for the value projection
   float lt = l_part + __shfl_xor(l_part, 16, 64);
@@ -292,14 +302,14 @@ __global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict
 
   // ---------------- phase C: o[t][4h+g][d] = Wv[h][d] . u[t][4h+g]; column tile tt = tokens 4tt .. 4tt+3
 #pragma unroll
-  for (int tt = 0; tt < 2; ++tt) {
+  for (int tt = 0; tt < NTT; ++tt) {
     const int64_t tc = tok0 + 4 * tt + (li >> 2);
     bf16x8 ub[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
       ub[ks] = *reinterpret_cast<const bf16x8*>(&xs[4 * tt + (li >> 2)][c_hg][32 * ks + 8 * lg]);
 #pragma unroll
-    for (int dt = 0; dt < 2; ++dt) {
+    for (int dt = 0; dt < NDT; ++dt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[dt][ks], ub[ks], d, 0, 0, 0);
@@ -313,23 +323,50 @@ __global__ __launch_bounds__(512, 1) void k_readout_fused(const bf16* __restrict
   }
 }
 
+// kv [512, 256] -> packed operand order (one thread per 16-byte piece, 16384 pieces).
+__global__ __launch_bounds__(256) void k_readout_pack(const bf16* __restrict__ kv, bf16* __restrict__ pk) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= 2 * FR_PK_V / 8) return;
+  bf16x8 v;
+  if (p < FR_PK_V / 8) {  // keys: Wk^T[h][f][d] = kv[64h + d][f]
+    const int lane = p & 63, ks = (p >> 6) & 1, ft = (p >> 7) & 15, h = p >> 11;
+    const int f = 16 * ft + (lane & 15), d0 = 32 * ks + 8 * (lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = kv[(64 * h + d0 + j) * FR_DT + f];
+  } else {  // values: Wv[h][d][f] = kv[256 + 64h + d][f]
+    const int pv = p - FR_PK_V / 8;
+    const int lane = pv & 63, ks = (pv >> 6) & 7, dt = (pv >> 9) & 3, h = pv >> 11;
+    const int d = 16 * dt + (lane & 15), f0 = 32 * ks + 8 * (lane >> 4);
+    v = ld16(kv + (256 + 64 * h + d) * FR_DT + f0);
+  }
+  *reinterpret_cast<bf16x8*>(pk + 8 * static_cast<int64_t>(p)) = v;
+}
+
 }  // namespace lng
 
 using namespace lng;
 
 extern "C" int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int64_t T, int32_t R,
-                                        const void* table2, const void* table3, const void* wk_t, const void* wv,
+                                        const void* table2, const void* table3, const void* kv_pack,
                                         const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
                                         void* stream) {
+  constexpr int FR_TOK = LNG_READOUT_TOK;
   if (B < 0 || T < 0 || R <= 0) return fail(LNG_E_ARG, "memory_readout_fused: bad shape");
   if (R > FR_MAXR) return fail(LNG_E_ARG, "memory_readout_fused: at most 256 routes");
   const int64_t ntok = B * T;
   if (ntok == 0) return LNG_OK;
   const int64_t blocks = cdiv(ntok, FR_TOK);
   if (blocks > 0x7fffffffLL) return fail(LNG_E_ARG, "memory_readout_fused: too many tokens");
-  hipLaunchKernelGGL(k_readout_fused, dim3(static_cast<unsigned>(blocks)), dim3(64 * FR_TOK), 0, as_stream(stream),
-                     static_cast<const bf16*>(q), codes, B, T, R, static_cast<const bf16*>(table2),
-                     static_cast<const bf16*>(table3), static_cast<const bf16*>(wk_t), static_cast<const bf16*>(wv),
+  hipLaunchKernelGGL(k_readout_fused<FR_TOK>, dim3(static_cast<unsigned>(blocks)), dim3(64 * FR_TOK), 0,
+                     as_stream(stream), static_cast<const bf16*>(q), codes, B, T, R, static_cast<const bf16*>(table2),
+                     static_cast<const bf16*>(table3), static_cast<const bf16*>(kv_pack),
                      static_cast<const bf16*>(w_mem), eps, scale, sink_logit, static_cast<bf16*>(head_out));
   return check_launch("memory_readout_fused");
+}
+
+extern "C" int lng_memory_readout_pack(const void* kv, void* kv_pack, void* stream) {
+  if (!kv || !kv_pack) return fail(LNG_E_ARG, "memory_readout_pack: null pointer");
+  hipLaunchKernelGGL(k_readout_pack, dim3(2 * FR_PK_V / 8 / 256), dim3(256), 0, as_stream(stream),
+                     static_cast<const bf16*>(kv), static_cast<bf16*>(kv_pack));
+  return check_launch("memory_readout_pack");
 }

@@ -355,17 +355,14 @@ class _RouteNgramMemoryBase(nn.Module):
                 and self.readout_num_kv_heads == 4 and self.readout_kv_proj.weight.dtype == torch.bfloat16
                 and all(t.weight.dtype == torch.bfloat16 for t in self.tables.values()))
 
-    def _fused_weights(self) -> tuple:
-        """Per-head transposed key weight ``[4, 256, 64]`` and value weight ``[4, 64, 256]`` (cached per
-        weight version)."""
+    def _fused_weights(self) -> Tensor:
+        """The fused readout's packed KV weight (``ops.memory_readout_pack`` of
+        ``readout_kv_proj.weight``), cached per weight version."""
         w = self.readout_kv_proj.weight
         key = (w.data_ptr(), w._version, w.device)
         if self._fused_cache is None or self._fused_cache[0] != key:
-            kh = self.readout_kv_inner_dim
-            wk_t = w[:kh].detach().reshape(4, 64, 256).transpose(1, 2).contiguous()
-            wv = w[kh:].detach().reshape(4, 64, 256).contiguous()
-            self._fused_cache = (key, wk_t, wv)
-        return self._fused_cache[1], self._fused_cache[2]
+            self._fused_cache = (key, ops.memory_readout_pack(w.detach()))
+        return self._fused_cache[1]
 
     def forward(self, hidden_states: Tensor, route_codes_btr: Tensor, q_logits: Optional[Tensor] = None,
                 segment_ids: Optional[Tensor] = None, valid_tokens: Optional[Tensor] = None) -> Tensor:
@@ -389,9 +386,9 @@ class _RouteNgramMemoryBase(nn.Module):
         self._check_inference(q_btrm)
         query = self._project_query(hidden_states)
         if segment_ids is None and valid_tokens is None and self._fused_shape_ok(hidden_states):
-            wk_t, wv = self._fused_weights()
+            kv_pack = self._fused_weights()
             head = ops.memory_readout_fused(query.view(b, t, self.readout_inner_dim), route_codes_btr,
-                                            self.tables["ngram_2"].weight, self.tables["ngram_3"].weight, wk_t, wv,
+                                            self.tables["ngram_2"].weight, self.tables["ngram_3"].weight, kv_pack,
                                             self.readout_memory_norm.weight, self.readout_memory_norm.eps,
                                             self.softmax_scale, self.readout_sink_logit)
             head_output = head.view(b, t, self.readout_num_heads, self.readout_head_dim)

@@ -29,6 +29,7 @@ _P32 = ctypes.POINTER(ctypes.c_int32)
 ROW_NONE = -2147483648  # LNG_ROW_NONE
 DR_SYNC_INTS = 4160  # LNG_DR_SYNC_INTS
 TREE_SYNC_BYTES = 16640  # LNG_DR_TREE_SYNC_BYTES: error word (offset 0) + counters of the one-launch tree
+READOUT_PACK_ELEMS = 131072  # LNG_READOUT_PACK_ELEMS: bf16 elements of the fused readout's packed KV weight
 
 
 class Drafter(ctypes.Structure):
@@ -71,7 +72,8 @@ SIGNATURES = {
     "lng_linear_rowsq": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "lng_row_sumsq": (_int, [_p, _i64, _i32, _p, _p]),
     "lng_causal_conv_rowsq": (_int, [_p, _p, _i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
-    "lng_memory_readout_fused": (_int, [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _p, _f, _f, _f, _p, _p]),
+    "lng_memory_readout_fused": (_int, [_p, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f, _f, _f, _p, _p]),
+    "lng_memory_readout_pack": (_int, [_p, _p, _p]),
     "lng_gather_sum_scaled": (_int, [ctypes.POINTER(_p), _int, _i32, _p, _i64, _i64, _i32, _P32, _i32, _i32, _i32,
                                      ctypes.c_uint32, _p, _p]),
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),

@@ -384,13 +384,26 @@ def causal_conv(mixed: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor,
     return out
 
 
+def memory_readout_pack(kv: torch.Tensor) -> torch.Tensor:
+    """``readout_kv_proj.weight`` ``[512, 256]`` bf16 -> the fused readout's packed KV weight
+    (``lng_memory_readout_pack``: a permutation into the kernel's operand order)."""
+    dev = _dev(kv)
+    kc = _c(kv)
+    if kc.dtype != torch.bfloat16 or kc.shape != (512, 256):
+        raise ValueError("fused readout packs a bf16 [512, 256] kv_proj weight")
+    out = torch.empty(_lib.READOUT_PACK_ELEMS, dtype=torch.bfloat16, device=dev)
+    check(lib().lng_memory_readout_pack(_ptr(kc), _ptr(out), _stream(dev)), "memory_readout_pack")
+    return out
+
+
 def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Tensor, table3: torch.Tensor,
-                         wk_t: torch.Tensor, wv: torch.Tensor, w_mem: torch.Tensor, eps: float, scale: float,
+                         kv_pack: torch.Tensor, w_mem: torch.Tensor, eps: float, scale: float,
                          sink_logit: float) -> torch.Tensor:
     """Fused gather + sink readout (bf16, 16 heads x 64, 4 KV heads, orders (2,3), mem_dim 128).
 
-    q ``[B, T, 1024]``, codes ``[B, T, R]`` uint8 -> head output ``[B, T, 1024]``."""
-    dev = _dev(q, codes, table2, table3, wk_t, wv, w_mem)
+    q ``[B, T, 1024]``, codes ``[B, T, R]`` uint8, ``kv_pack`` from ``memory_readout_pack`` ->
+    head output ``[B, T, 1024]``."""
+    dev = _dev(q, codes, table2, table3, kv_pack, w_mem)
     b, t, r = codes.shape
     qc = _c(q)
     cc = _c(codes.to(torch.uint8))
@@ -398,12 +411,12 @@ def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Ten
         raise ValueError("fused readout expects a bf16 [B, T, 1024] query")
     if table2.shape != (r * 256, 128) or table3.shape != (r * 4096, 128):
         raise ValueError("fused readout expects tables [R*256,128] and [R*4096,128]")
-    if wk_t.shape != (4, 256, 64) or wv.shape != (4, 64, 256) or w_mem.shape != (256,):
+    if kv_pack.shape != (_lib.READOUT_PACK_ELEMS,) or kv_pack.dtype != torch.bfloat16 or w_mem.shape != (256,):
         raise ValueError("fused readout weight shapes")
     out = torch.empty(b, t, 1024, dtype=torch.bfloat16, device=dev)
-    t2, t3, wkc, wvc, wmc = _c(table2), _c(table3), _c(wk_t), _c(wv), _c(w_mem.to(torch.bfloat16))
+    t2, t3, kp, wmc = _c(table2), _c(table3), _c(kv_pack), _c(w_mem.to(torch.bfloat16))
     rc = _timed("memory_readout_fused", dev, lambda: lib().lng_memory_readout_fused(
-        _ptr(qc), _ptr(cc), b, t, r, _ptr(t2), _ptr(t3), _ptr(wkc), _ptr(wvc), _ptr(wmc), eps, scale, sink_logit,
+        _ptr(qc), _ptr(cc), b, t, r, _ptr(t2), _ptr(t3), _ptr(kp), _ptr(wmc), eps, scale, sink_logit,
         _ptr(out), _stream(dev)))
     check(rc, "memory_readout_fused")
     return out
