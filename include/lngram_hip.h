@@ -261,6 +261,10 @@ typedef struct lng_drafter {
   const float* mem_norm;
   int32_t wv_dtype;
   int32_t* sync;
+  /* Optional (may be null): lut_out in the vocabulary kernel's MFMA operand order, fp32
+   * [ceil(V/16)][q_heads*hd/16][64][4]: element (t, s, l, e) = lut_out[16t + l%16][16s + 4(l/16) + e]
+   * (zero past row V-1), so that each load of a 16-row tile moves one contiguous kilobyte. */
+  const float* lut_out_pk;
 } lng_drafter;
 
 /* sizeof(lng_drafter), for bindings that mirror the struct. */

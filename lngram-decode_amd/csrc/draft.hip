@@ -780,6 +780,27 @@ __device__ __forceinline__ int32_t ld_dev(const int32_t* p) {
 }
 constexpr int WAITCNT_VM0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt left open
 
+// 16-byte device-coherent hand-off through raw buffer operations with the sc1 cache policy (the
+// policy the agent-scope relaxed loads and stores above use), one instruction per 16 bytes.
+constexpr int BUF_DW3 = 0x00020000;  // raw buffer descriptor word 3 (gfx9 family)
+constexpr int CPOL_SC1 = 16;         // cache policy bit sc1
+// base and bytes must be the same in every active lane: they are taken from the first one, so the
+// descriptor lives in scalar registers (a per-lane descriptor would serialise every access).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_buf(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
+  const int n = static_cast<int>(__builtin_amdgcn_readfirstlane(bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, n,
+                                           BUF_DW3);
+}
+__device__ __forceinline__ f32x4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SC1));
+}
+__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, CPOL_SC1);
+}
+
 __device__ __forceinline__ bool dr_last_block(int32_t* counter, int32_t total, int* flag) {
   __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
   __syncthreads();
@@ -867,6 +888,34 @@ __device__ __forceinline__ void wave_topk(TopK<KM>& t, float* sv, int* si) {
     sv[k] = id == INT_MAX ? -INFINITY : m;
     si[k] = id == INT_MAX ? -1 : id;
     if (t.i[0] == id && id != INT_MAX) t.pop();
+  }
+}
+
+// The wave's top-KM over every lane's N items, ranked by (value desc, id asc): sv/si receive it in
+// order, identical in every lane; (-inf, -1) where fewer items exist.  Per round: the lanes'
+// maxima, the wave maximum, the smallest id holding it, the winner's removal -- plain max, min and
+// select instructions, independent across items.  Ids are distinct; empty items are
+// (-inf, INT_MAX) and every real value is finite.  v/id are consumed.
+template <int KM, int N>
+__device__ __forceinline__ void wave_topk_items(float (&v)[N], int (&id)[N], float* sv, int* si) {
+#pragma unroll
+  for (int k = 0; k < KM; ++k) {
+    float m = v[0];
+#pragma unroll
+    for (int a = 1; a < N; ++a) m = fmaxf(m, v[a]);
+    const float M = wave_max(m);
+    int c = INT_MAX;
+#pragma unroll
+    for (int a = 0; a < N; ++a) c = min(c, v[a] == M ? id[a] : INT_MAX);
+    const int I = wave_min_i(c);
+    sv[k] = I == INT_MAX ? -INFINITY : M;
+    si[k] = I == INT_MAX ? -1 : I;
+#pragma unroll
+    for (int a = 0; a < N; ++a) {
+      const bool hit = id[a] == I;
+      v[a] = hit ? -INFINITY : v[a];
+      id[a] = hit ? INT_MAX : id[a];
+    }
   }
 }
 
@@ -1307,7 +1356,7 @@ __device__ __forceinline__ int fl_prefix(const int32_t* nnz, int b, int lane) {
 }
 
 template <int KM>
-__host__ __device__ constexpr int fl_rs() { return 4 + 2 * KM; }
+__host__ __device__ constexpr int fl_rs() { return 4 + 4 * ((2 * KM + 3) / 4); }  // whole 16-byte pieces
 
 template <int KM>
 __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, int32_t K, int32_t online, float kappa,
@@ -1333,6 +1382,9 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
   const int c_rank = lane < C.n ? C.rank[lane] : 0;
   const int G = P == 1 ? 4 : (P == 2 ? 2 : 1);  // selection waves per position
   const int tot0 = online && w / G < P ? D.sync[SY_TOT + w / G] : 0;
+  // count-bearing tokens of this wave's (first) selection position: its per-block counters are
+  // final once the attention launch ended, so the selection can size its list loads up front
+  const int nc0 = online && w / G < P ? fl_prefix(D.sync + SY_NNZ + (w / G) * SY_NNZ_STRIDE, gridDim.x, lane) : 0;
   // online counts of this wave's first position: in flight during the products
   int ca = 0, cb = 0, pre0 = 0;
   if (online && w < P) {
@@ -1352,13 +1404,22 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
 #pragma unroll
   for (int st = 0; st < FL_I / 16; ++st)
     bq[st] = (st < nks && col < P) ? *reinterpret_cast<const f32x4*>(&rs[col][16 * st + 4 * kq]) : f32x4{0.f, 0.f, 0.f, 0.f};
+  const float* const pk = D.lut_out_pk;
   for (int tile = 2 * w; tile < 2 * w + 2; ++tile) {
     const int64_t vrow = v0 + tile * 16 + col;
     f32x4 a[FL_I / 16];
+    if (pk) {  // packed tiles: one contiguous kilobyte per load (rows past V are zero)
+      const float* tp = pk + (((v0 >> 4) + tile) * nks) * 256 + 4 * lane;
 #pragma unroll
-    for (int st = 0; st < FL_I / 16; ++st)
-      a[st] = (st < nks && vrow < V) ? *reinterpret_cast<const f32x4*>(D.lut_out + vrow * I + 16 * st + 4 * kq)
-                                     : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int st = 0; st < FL_I / 16; ++st)
+        a[st] = (st < nks && v0 + tile * 16 < V) ? *reinterpret_cast<const f32x4*>(tp + 256 * st)
+                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+#pragma unroll
+      for (int st = 0; st < FL_I / 16; ++st)
+        a[st] = (st < nks && vrow < V) ? *reinterpret_cast<const f32x4*>(D.lut_out + vrow * I + 16 * st + 4 * kq)
+                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < FL_I / 16; ++st) {
@@ -1403,18 +1464,15 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
       const uint64_t ma = __ballot(ca > 0), mb = __ballot(cb > 0);
       const int na = __popcll(ma);
       nbk = na + __popcll(mb);
+      const __amdgpu_buffer_rsrc_t db = dev_buf(dst, static_cast<uint32_t>(nbk) * 16u);
       if (ca > 0) {
-        int32_t* dp = reinterpret_cast<int32_t*>(dst + __popcll(ma & below));
-        st_dev(dp, static_cast<int32_t>(va));
-        st_dev(dp + 1, __float_as_int(x0));
-        st_dev(dp + 2, ca);
+        st_dev4(db, 16u * __popcll(ma & below),
+                f32x4{__int_as_float(static_cast<int32_t>(va)), x0, __int_as_float(ca), 0.f});
         cj[va] = 0;
       }
       if (cb > 0) {
-        int32_t* dp = reinterpret_cast<int32_t*>(dst + na + __popcll(mb & below));
-        st_dev(dp, static_cast<int32_t>(vb));
-        st_dev(dp + 1, __float_as_int(x1));
-        st_dev(dp + 2, cb);
+        st_dev4(db, 16u * (na + __popcll(mb & below)),
+                f32x4{__int_as_float(static_cast<int32_t>(vb)), x1, __int_as_float(cb), 0.f});
         cj[vb] = 0;
       }
     }
@@ -1428,14 +1486,20 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
     int si[KM];
     wave_topk(t, sv, si);
     if (lane == 0) {
-      st_dev(o, m);
-      st_dev(o + 1, s);
-      st_dev(o + 2, __int_as_float(nbk));
+      float rv[RS];
+#pragma unroll
+      for (int e = 0; e < RS; ++e) rv[e] = 0.f;
+      rv[0] = m;
+      rv[1] = s;
+      rv[2] = __int_as_float(nbk);
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
-        st_dev(o + 4 + k, sv[k]);
-        st_dev(o + 4 + KM + k, __int_as_float(si[k]));
+        rv[4 + k] = sv[k];
+        rv[4 + KM + k] = __int_as_float(si[k]);
       }
+      const __amdgpu_buffer_rsrc_t ob = dev_buf(o, RS * 4u);
+#pragma unroll
+      for (int q = 0; q < RS / 4; ++q) st_dev4(ob, 16u * q, f32x4{rv[4 * q], rv[4 * q + 1], rv[4 * q + 2], rv[4 * q + 3]});
     }
   }
   if (!dr_last_block(&D.sync[SY_LOG], nblk, &last_flag)) return;
@@ -1443,25 +1507,39 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
   const int g = w % G;
   for (int j = w / G; j < P; j += 4 / G) {
     const float* lp = lpart + static_cast<int64_t>(j) * nblk * RS;
+    // the position's count-bearing tokens (the list's first batch, e = 64 (G u + g) + lane, is
+    // loaded together with the records: one round trip for both)
+    const int nc = online ? (j == w / G ? nc0 : fl_prefix(D.sync + SY_NNZ + j * SY_NNZ_STRIDE, nblk, lane)) : 0;
+    const int4* cj = cand + static_cast<int64_t>(j) * nblk * FL_VB;
+    const __amdgpu_buffer_rsrc_t cbuf = dev_buf(cj, static_cast<uint32_t>(max(nc, 1)) * 16u);
+    f32x4 cr0[FL_CH];
+    if (online && nc > 0) {
+#pragma unroll
+      for (int u = 0; u < FL_CH; ++u) cr0[u] = ld_dev4(cbuf, 16u * min(64 * g + 64 * G * u + lane, nc - 1));
+    }
     // records of blocks 4 lane + q (all in flight at once)
     float rm[FL_NBL], rsm[FL_NBL], av[FL_NBL][KM];
-    int rnb[FL_NBL], ai[FL_NBL][KM];
+    int ai[FL_NBL][KM];
+    const __amdgpu_buffer_rsrc_t lbuf = dev_buf(lp, static_cast<uint32_t>(nblk) * RS * 4u);
+    f32x4 rq[FL_NBL][RS / 4];
+#pragma unroll
+    for (int q = 0; q < FL_NBL; ++q)  // unconditional loads (block index clamped into the records)
+#pragma unroll
+      for (int p4 = 0; p4 < RS / 4; ++p4)
+        rq[q][p4] = ld_dev4(lbuf, 4u * (min(FL_NBL * lane + q, nblk - 1) * RS + 4 * p4));
 #pragma unroll
     for (int q = 0; q < FL_NBL; ++q) {
-      // unconditional loads (block index clamped into the records), then masked
       const int b = FL_NBL * lane + q;
       const bool ok = b < nblk;
-      const float* rec = lp + static_cast<int64_t>(min(b, nblk - 1)) * RS;
-      const float r0 = ld_dev(rec), r1 = ld_dev(rec + 1), r2 = ld_dev(rec + 2);
-      rm[q] = ok ? r0 : -INFINITY;
-      rsm[q] = ok ? r1 : 0.f;
-      rnb[q] = ok && online ? __float_as_int(r2) : 0;
+      float rv[RS];
+      __builtin_memcpy(rv, &rq[q][0], sizeof(rv));
+      rm[q] = ok ? rv[0] : -INFINITY;
+      rsm[q] = ok ? rv[1] : 0.f;
 #pragma unroll
       for (int k = 0; k < KM; ++k) {
         const bool mine = ok && q % G == g;
-        const float x = ld_dev(rec + 4 + k), id = ld_dev(rec + 4 + KM + k);
-        av[q][k] = mine ? x : -INFINITY;
-        ai[q][k] = mine ? __float_as_int(id) : -1;
+        av[q][k] = mine ? rv[4 + k] : -INFINITY;
+        ai[q][k] = mine ? __float_as_int(rv[4 + KM + k]) : -1;
       }
     }
     float m = -INFINITY;
@@ -1477,39 +1555,55 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
     const float lam = tj > 0.f ? n_eff / (n_eff + kappa) : 0.f;
     // online ranking value: (1 - lam) exp(logit - M) / S + lam count / total (log taken at the end)
     const float mix_a = (1.f - lam) / S, mix_b = tj > 0.f ? lam / tj : 0.f;
-    TopK<KM> t;
-    t.clear();
+    // the wave's items: the blocks' top-KM lists and the list's first batch, ranked together
+    float sv[KM];
+    int si[KM];
+    {
+      constexpr int NI = FL_NBL * KM + FL_CH;
+      float iv[NI];
+      int ii[NI];
 #pragma unroll
-    for (int q = 0; q < FL_NBL; ++q)
+      for (int q = 0; q < FL_NBL; ++q)
 #pragma unroll
-      for (int k = 0; k < KM; ++k)
-        t.insert(ai[q][k] < 0 ? -INFINITY : online ? mix_a * expf(av[q][k] - M) : av[q][k],
-                 ai[q][k] < 0 ? INT_MAX : ai[q][k]);
+        for (int k = 0; k < KM; ++k) {
+          iv[q * KM + k] = ai[q][k] < 0 ? -INFINITY : online ? mix_a * expf(av[q][k] - M) : av[q][k];
+          ii[q * KM + k] = ai[q][k] < 0 ? INT_MAX : ai[q][k];
+        }
+#pragma unroll
+      for (int u = 0; u < FL_CH; ++u) {
+        const bool ok = online && 64 * g + 64 * G * u + lane < nc;
+        iv[FL_NBL * KM + u] =
+            ok ? fmaf(mix_b, static_cast<float>(__float_as_int(cr0[u][2])), mix_a * expf(cr0[u][1] - M)) : -INFINITY;
+        ii[FL_NBL * KM + u] = ok ? __float_as_int(cr0[u][0]) : INT_MAX;
+      }
+      wave_topk_items<KM, NI>(iv, ii, sv, si);
+    }
     if (online) {
-      // the position's count-bearing tokens: e = 64 (G t + g) + lane
-      const int nc = wave_sum_i((rnb[0] + rnb[1]) + (rnb[2] + rnb[3]));
       if (g == 0)  // every block has read the per-block counters: clear them for the next call
 #pragma unroll
         for (int q = 0; q < FL_NBL; ++q) D.sync[SY_NNZ + j * SY_NNZ_STRIDE + FL_NBL * lane + q] = 0;
-      const int4* cj = cand + static_cast<int64_t>(j) * nblk * FL_VB;
-      for (int e0 = 64 * g; e0 < nc; e0 += 64 * G * FL_CH) {
-        int4 cr[FL_CH];
+      // further batches of the list: ranked with the winners so far (lane k holds winner k)
+      for (int e0 = 64 * g + 64 * G * FL_CH; e0 < nc; e0 += 64 * G * FL_CH) {
+        f32x4 cr[FL_CH];
 #pragma unroll
-        for (int u = 0; u < FL_CH; ++u) {
-          const int32_t* cp = reinterpret_cast<const int32_t*>(cj + min(e0 + 64 * G * u + lane, nc - 1));
-          cr[u] = int4{ld_dev(cp), ld_dev(cp + 1), ld_dev(cp + 2), 0};
-        }
+        for (int u = 0; u < FL_CH; ++u) cr[u] = ld_dev4(cbuf, 16u * min(e0 + 64 * G * u + lane, nc - 1));
+        constexpr int NB = FL_CH + 1;
+        float bv[NB];
+        int bi[NB];
+        bv[0] = -INFINITY, bi[0] = INT_MAX;
+#pragma unroll
+        for (int k = 0; k < KM; ++k)
+          if (lane == k && si[k] >= 0) bv[0] = sv[k], bi[0] = si[k];
 #pragma unroll
         for (int u = 0; u < FL_CH; ++u) {
           const bool ok = e0 + 64 * G * u + lane < nc;
-          t.insert(ok ? fmaf(mix_b, static_cast<float>(cr[u].z), mix_a * expf(__int_as_float(cr[u].y) - M)) : -INFINITY,
-                   ok ? cr[u].x : INT_MAX);
+          bv[1 + u] = ok ? fmaf(mix_b, static_cast<float>(__float_as_int(cr[u][2])), mix_a * expf(cr[u][1] - M))
+                         : -INFINITY;
+          bi[1 + u] = ok ? __float_as_int(cr[u][0]) : INT_MAX;
         }
+        wave_topk_items<KM, NB>(bv, bi, sv, si);
       }
     }
-    float sv[KM];
-    int si[KM];
-    wave_topk(t, sv, si);
     if (G > 1) {
       // merge the group's lists: wave g == 0 ranks the G * KM winners again
       if (lane == 0)
@@ -1517,10 +1611,12 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
         for (int k = 0; k < KM; ++k) sel_v[w][k] = sv[k], sel_i[w][k] = si[k];
       __syncthreads();
       if (g != 0) continue;
-      t.clear();
-      if (lane < G * KM && sel_i[w + lane / KM][lane % KM] >= 0)
-        t.insert(sel_v[w + lane / KM][lane % KM], sel_i[w + lane / KM][lane % KM]);
-      wave_topk(t, sv, si);
+      float mv[1];
+      int mi[1];
+      const bool have = lane < G * KM && sel_i[w + lane / KM][lane % KM] >= 0;
+      mv[0] = have ? sel_v[w + lane / KM][lane % KM] : -INFINITY;
+      mi[0] = have ? sel_i[w + lane / KM][lane % KM] : INT_MAX;
+      wave_topk_items<KM, 1>(mv, mi, sv, si);
       __builtin_amdgcn_wave_barrier();
     }
     if (lane == 0)

@@ -187,6 +187,8 @@ class GpuDrafter:
         lut["lut_qk"] = ops.linear(ops.rmsnorm(ef, ones, float(c["draft_eps"])), self.qk)
         w_o_t = t["w_o"].to(dev, torch.float32).t().contiguous()                  # [I, d]
         lut["lut_out"] = ops.linear(ef * self.vec["out_norm"][None], w_o_t)
+        if (self.qh * self.hd) % 16 == 0:
+            lut["lut_out_pk"] = self._pack_tiles(lut["lut_out"])
         lut["gram_out"] = ops.linear(w_o_t, w_o_t)
         kvp = t["kv_proj"].to(dev)
         wdt = torch.bfloat16 if kvp.dtype == torch.bfloat16 else torch.float32
@@ -196,6 +198,17 @@ class GpuDrafter:
         self.luts = lut
         self.sync = torch.zeros(_lib.DR_SYNC_INTS, dtype=torch.int32, device=dev)
         del ef
+
+    @staticmethod
+    def _pack_tiles(x: torch.Tensor) -> torch.Tensor:
+        """``[V, I]`` fp32 -> ``lng_drafter.lut_out_pk`` order ``[ceil(V/16)][I/16][64][4]`` (a permutation;
+        zero rows pad V to a multiple of 16)."""
+        v, i = x.shape
+        vp = -(-v // 16) * 16
+        xp = torch.zeros(vp, i, dtype=x.dtype, device=x.device)
+        xp[:v] = x
+        # (tile, col, step, kq, e) -> (tile, step, kq, col, e); lane = 16 kq + col
+        return xp.view(vp // 16, 16, i // 16, 4, 4).permute(0, 2, 3, 1, 4).contiguous().view(-1)
 
     def _descriptor(self, tok, codes, ssm, length, rows) -> _lib.Drafter:
         c = self.cfg

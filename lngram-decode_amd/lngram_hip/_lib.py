@@ -45,7 +45,8 @@ class Drafter(ctypes.Structure):
                                        "ssm_decay", "qk", "qks", "ov", "out_norm", "tokens", "codes", "ssm",
                                        "length")] + [("rows", ctypes.c_int32)] + [
         (n, ctypes.c_void_p) for n in ("lut_prev", "lut_cur", "lut_start", "lut_qk", "lut_out", "gram_out", "wv_t",
-                                       "mem_norm")] + [("wv_dtype", ctypes.c_int32), ("sync", ctypes.c_void_p)]
+                                       "mem_norm")] + [("wv_dtype", ctypes.c_int32), ("sync", ctypes.c_void_p),
+                                                        ("lut_out_pk", ctypes.c_void_p)]
 
 
 _PD = ctypes.POINTER(Drafter)
