@@ -936,15 +936,16 @@ __device__ __forceinline__ int dr_lut_code4(const lng_drafter& D, int64_t ptok, 
 }
 
 // grid (nch + nob, P): blocks [0, nch) attention over route chunks, [nch, nch + nob) online matches.
-// Attention block c of position j writes the record part[j, c] = (o_c[QH*hd], y_c[QH][I], m_c[QH],
-// l_c[QH]): o_c = Wv (mem_norm . U_c) per query head, y_c[qh] = (W_o^T W_o)[:, qh block] o_c[qh]
-// (both linear in U_c, so the last block merges them with the softmax weights).  Online blocks add
-// their pairs' match counts to counts[j, next token] and to the position's total.  The last block
-// of position j writes ro[j] = r_j * o_j, r_j = rsqrt(|W_o o_j|^2 / d + eps).
+// Attention block c of position j writes the record part[j, c] = (o_c[QH*hd], m_c[QH], l_c[QH])
+// with o_c = Wv (mem_norm . U_c) per query head (linear in U_c, so the last block merges the
+// chunks with the softmax weights).  Online blocks add their pairs' match counts to
+// counts[j, next token] and to the position's total.  The last block of position j merges o_j,
+// applies the Gram matrix y = (W_o^T W_o) o_j and writes ro[j] = r_j * o_j,
+// r_j = rsqrt(o_j . y / d + eps) = rsqrt(|W_o o_j|^2 / d + eps).
 constexpr int FA_MAXCH = 16;  // attention chunks per position (R <= 256)
 constexpr int FA_DW = (((FA_TB + DR_MAXN) * 256 + 8) / 4);
 
-__device__ __forceinline__ int fa_rec(int QH, int hd, int I) { return QH * hd + QH * I + 2 * QH; }
+__device__ __host__ __forceinline__ int fa_rec(int QH, int I) { return I + 4 * ((2 * QH + 3) / 4); }
 
 __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F, int32_t nch, int32_t nob,
                                                      int32_t online, float* __restrict__ part,
@@ -995,6 +996,15 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   // window codes of the routes this block needs: [r0, r0 + nr) (attention) or all (online)
   const int r0 = is_attn ? blockIdx.x * FA_RC : 0;
   const int nr = is_attn ? min(FA_RC, R - r0) : R;
+  // the position's query-key row (attention blocks): in flight with the code lookups below
+  const bool tok_ok = dr_tok_ok(D, tok);
+  f32x4 qrow[LNG_DR_MAX_QH * LNG_DR_MAX_DT / 1024];
+  if (is_attn)
+#pragma unroll
+    for (int q = 0; q < LNG_DR_MAX_QH * LNG_DR_MAX_DT / 1024; ++q) {
+      const int i = 4 * threadIdx.x + 1024 * q;
+      qrow[q] = (tok_ok && i < QD) ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * QD + i) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   for (int e = threadIdx.x; e < nr * maxn; e += 256) {
     const int k = e / nr, rr = e % nr, r = r0 + rr;
     const int32_t row = srow[k];
@@ -1025,10 +1035,11 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
       const int32_t a = addr_of(oi, rr);
       rowsh[rr][oi] = a < 0 ? -1 : static_cast<int64_t>(r0 + rr) * (int64_t{1} << (bits * ord_at(oi))) + a;
     }
-    const bool tok_ok = dr_tok_ok(D, tok);
-    for (int i = 4 * threadIdx.x; i < QD; i += 1024)
-      *reinterpret_cast<f32x4*>(&qs[i]) = tok_ok ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * QD + i)
-                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < LNG_DR_MAX_QH * LNG_DR_MAX_DT / 1024; ++q) {
+      const int i = 4 * threadIdx.x + 1024 * q;
+      if (i < QD) *reinterpret_cast<f32x4*>(&qs[i]) = qrow[q];
+    }
     __syncthreads();
     if (D.table_dtype == LNG_BF16 && md % 8 == 0) {
       const int pieces = md / 8;
@@ -1102,7 +1113,7 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
       *reinterpret_cast<f32x4*>(&us[e]) = f32x4{u[0] * mn[0], u[1] * mn[1], u[2] * mn[2], u[3] * mn[3]};
     }
     __syncthreads();
-    float* rec = part + (static_cast<int64_t>(j) * nch + blockIdx.x) * fa_rec(QH, hd, I);
+    float* rec = part + (static_cast<int64_t>(j) * nch + blockIdx.x) * fa_rec(QH, I);
     // o_c[qh][oe] = sum_i Wv[h][oe][i] U[qh][i]: item (qh, 8 outputs, 32 rows), 16-byte loads of the
     // transposed weight, all in flight; partial sums meet in LDS (xs is free now)
     float* ob = &xs[0][0];  // [QH][Dt/32][hd]
@@ -1155,33 +1166,9 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
         us[e] = a;  // o_c, reused below
       }
     }
-    __syncthreads();
-    // y_c[qh][k] = sum_{e in qh block} Gram[k][e] o_c[e]: thread = 4 consecutive k, the qh block's
-    // rows streamed in 16-byte loads (Gram is symmetric: row e = column e)
-    for (int it = threadIdx.x; it < QH * (I / 4); it += 256) {
-      const int qh = it / (I / 4), k4 = it % (I / 4);
-      f32x4 y = {0.f, 0.f, 0.f, 0.f};
-      for (int e0 = 0; e0 < hd; e0 += 32) {
-        f32x4 gv[32];
-#pragma unroll
-        for (int q = 0; q < 32; ++q)
-          gv[q] = e0 + q < hd ? *reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(qh * hd + e0 + q) * I + 4 * k4)
-                              : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < 32; ++q) {
-          const float oe = e0 + q < hd ? us[qh * hd + e0 + q] : 0.f;
-          y[0] = fmaf(gv[q][0], oe, y[0]);
-          y[1] = fmaf(gv[q][1], oe, y[1]);
-          y[2] = fmaf(gv[q][2], oe, y[2]);
-          y[3] = fmaf(gv[q][3], oe, y[3]);
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) st_dev(rec + I + qh * I + 4 * k4 + q, y[q]);
-    }
     if (threadIdx.x < QH) {
-      st_dev(rec + I + QH * I + threadIdx.x, ml[threadIdx.x][0]);
-      st_dev(rec + I + QH * I + QH + threadIdx.x, ml[threadIdx.x][1]);
+      st_dev(rec + I + threadIdx.x, ml[threadIdx.x][0]);
+      st_dev(rec + I + QH + threadIdx.x, ml[threadIdx.x][1]);
     }
   } else {
     // ---------------- online counts over pairs [t0, t0 + FA_TB) (thread = route)
@@ -1271,17 +1258,36 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   // ---------------- last block of position j: merge, hidden norm
   if (!dr_last_block(&D.sync[SY_ATT + j], nch + nob, &last_flag)) return;
   const float b0 = D.sink_logit;
-  const int RS = fa_rec(QH, hd, I);
+  const int RS = fa_rec(QH, I);
   const float* rj = part + static_cast<int64_t>(j) * nch * RS;
+  const __amdgpu_buffer_rsrc_t rb = dev_buf(rj, static_cast<uint32_t>(nch * RS) * 4u);
+  // loads in the order they are needed (the memory counter completes them in order): the chunks'
+  // (m, l) pieces, then every chunk's o_c
+  const int npc = (2 * QH + 3) / 4;  // 16-byte (m, l) pieces per chunk
+  __shared__ __attribute__((aligned(16))) float mlb[FA_MAXCH][2 * LNG_DR_MAX_QH];
+  f32x4 mlp = {0.f, 0.f, 0.f, 0.f};
+  const bool ml_ld = threadIdx.x < nch * npc;
+  if (ml_ld) mlp = ld_dev4(rb, 4u * ((threadIdx.x / npc) * RS + I + 4 * (threadIdx.x % npc)));
+  // o_c: thread (c4 = t / 64, e4 = t % 64) loads o_c[4 e4 .. +3] of chunks c4, c4 + 4, ... (I <= 256)
+  const int e4 = threadIdx.x & 63, c4 = threadIdx.x >> 6;
+  f32x4 ov[FA_MAXCH / 4];
+#pragma unroll
+  for (int q = 0; q < FA_MAXCH / 4; ++q) {
+    const int c = c4 + 4 * q;
+    ov[q] = (c < nch && 4 * e4 < I) ? ld_dev4(rb, 4u * (c * RS + 4 * e4)) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (ml_ld) *reinterpret_cast<f32x4*>(&mlb[threadIdx.x / npc][4 * (threadIdx.x % npc)]) = mlp;
+  __syncthreads();
   // merge weights per (chunk, head): f = e^{m_c - M} / (e^{b0 - M} + sum_c l_c e^{m_c - M})
   __shared__ float wgt[FA_MAXCH][LNG_DR_MAX_QH];
+  __shared__ __attribute__((aligned(16))) float opart[4][LNG_DR_MAX_QH * LNG_DR_MAX_DT / 4];
   if (threadIdx.x < QH) {
     const int qh = threadIdx.x;
     float pm[FA_MAXCH], pl[FA_MAXCH];
 #pragma unroll
     for (int c = 0; c < FA_MAXCH; ++c) {
-      pm[c] = c < nch ? ld_dev(rj + c * RS + I + QH * I + qh) : -INFINITY;
-      pl[c] = c < nch ? ld_dev(rj + c * RS + I + QH * I + QH + qh) : 0.f;
+      pm[c] = c < nch ? mlb[c][qh] : -INFINITY;
+      pl[c] = c < nch ? mlb[c][QH + qh] : 0.f;
     }
     float M = b0;
 #pragma unroll
@@ -1297,31 +1303,46 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
     for (int c = 0; c < FA_MAXCH; ++c) wgt[c][qh] = f[c] / l;
   }
   __syncthreads();
-  // o[e] = sum_c f_{c,qh(e)} o_c[e];  y[k] = sum_c sum_qh f_{c,qh} y_c[qh][k]  (loads batched:
-  // every chunk's value for 4 heads at a time)
-  float acc = 0.f;
-  for (int e = threadIdx.x; e < I; e += 256) {
-    const int qh = e / hd;
-    float ov[FA_MAXCH];
+  // o = sum_c f_{c, qh(e)} o_c: partial sums over the thread's chunks, then over the four groups
+  if (4 * e4 < I) {
+    const int qh = (4 * e4) / hd;
+    f32x4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) ov[c] = c < nch ? ld_dev(rj + c * RS + e) : 0.f;
-    float o = 0.f, y = 0.f;
-#pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) o = fmaf(c < nch ? wgt[c][qh] : 0.f, ov[c], o);
-    for (int q0 = 0; q0 < QH; q0 += 4) {
-      float yv[FA_MAXCH][4];
-#pragma unroll
-      for (int c = 0; c < FA_MAXCH; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) yv[c][q] = (c < nch && q0 + q < QH) ? ld_dev(rj + c * RS + I + (q0 + q) * I + e) : 0.f;
-#pragma unroll
-      for (int c = 0; c < FA_MAXCH; ++c)
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (c < nch && q0 + q < QH) y = fmaf(wgt[c][q0 + q], yv[c][q], y);
+    for (int q = 0; q < FA_MAXCH / 4; ++q) {
+      const int c = c4 + 4 * q;
+      const float f = c < nch ? wgt[c][qh] : 0.f;
+      o[0] = fmaf(f, ov[q][0], o[0]);
+      o[1] = fmaf(f, ov[q][1], o[1]);
+      o[2] = fmaf(f, ov[q][2], o[2]);
+      o[3] = fmaf(f, ov[q][3], o[3]);
     }
-    us[e] = o;
-    acc = fmaf(o, y, acc);
+    *reinterpret_cast<f32x4*>(&opart[c4][4 * e4]) = o;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < I; e += 256) us[e] = (opart[0][e] + opart[1][e]) + (opart[2][e] + opart[3][e]);
+  __syncthreads();
+  // o . (Gram o): thread (k4 = e4, quarter c4) sums Gram[e][4 k4 .. +3] o[e] over its quarter of e
+  // (Gram is symmetric; one row e is a contiguous kilobyte across the wave), 16 rows per batch
+  float acc = 0.f;
+  if (4 * e4 < I) {
+    const int ne = (I + 3) / 4, eb = c4 * ne, ee = min(I, eb + ne);
+    f32x4 y = {0.f, 0.f, 0.f, 0.f};
+    for (int e0 = eb; e0 < ee; e0 += 16) {
+      f32x4 gv[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q)
+        gv[q] = e0 + q < ee ? *reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(e0 + q) * I + 4 * e4)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const float oe = e0 + q < ee ? us[e0 + q] : 0.f;
+        y[0] = fmaf(gv[q][0], oe, y[0]);
+        y[1] = fmaf(gv[q][1], oe, y[1]);
+        y[2] = fmaf(gv[q][2], oe, y[2]);
+        y[3] = fmaf(gv[q][3], oe, y[3]);
+      }
+    }
+    acc = (y[0] * us[4 * e4] + y[1] * us[4 * e4 + 1]) + (y[2] * us[4 * e4 + 2] + y[3] * us[4 * e4 + 3]);
   }
   const float ss = block_sum256(acc, redf);
   const float rn = 1.0f / sqrtf(ss / static_cast<float>(D.d) + D.draft_eps);
@@ -2583,7 +2604,7 @@ DrLayout dr_layout(const lng_drafter& D, int P, int K, int max_pairs) {
   l.fnch = static_cast<int>(cdiv(D.R, FA_RC));
   l.fnblk = static_cast<int>(cdiv(D.V, FL_VB));
   const int I = D.q_heads * D.head_dim;
-  l.fpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnch * (D.q_heads * D.head_dim + D.q_heads * I + 2 * D.q_heads));
+  l.fpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnch * fa_rec(D.q_heads, D.q_heads * D.head_dim));
   l.ro = take(sizeof(float) * P * I);
   l.tot = 0;
   l.flpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnblk * fl_rs<DR_MAXK>());
@@ -2595,7 +2616,7 @@ DrLayout dr_layout(const lng_drafter& D, int P, int K, int max_pairs) {
 bool dr_fast(const lng_drafter& D) {
   const int I = D.q_heads * D.head_dim;
   return D.lut_prev && D.lut_cur && D.lut_start && D.lut_qk && D.lut_out && D.gram_out && D.wv_t && D.sync &&
-         !D.router_ssm && !D.query_ssm && I <= FL_I && I % 16 == 0 && D.dt % 64 == 0 &&
+         !D.router_ssm && !D.query_ssm && I <= FL_I && I % 16 == 0 && D.head_dim % 4 == 0 && D.dt % 64 == 0 &&
          cdiv(D.V, FL_VB) <= FL_NBL * 64;
 }
 
