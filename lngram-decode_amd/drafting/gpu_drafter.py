@@ -134,6 +134,7 @@ class GpuDrafter:
         self.tree_work = None
         self._tree_seq = 0
         self._fused_specs: dict = {}
+        self._graphs: dict = {}          # (parent, rank, route_tokens) -> (captured tree step, out)
         if fused and self.luts is not None:
             fb = self.lib.lng_drafter_tree_fused_workspace(ctypes.byref(self.D))
             if fb:
@@ -359,10 +360,27 @@ class GpuDrafter:
         self.tree_step(spec, route_tokens=False)
         return self.tok_d[self.tree_row0: self.tree_row0 + spec.n].cpu().tolist()
 
-    def tree_step(self, spec, route_tokens: bool = True):
+    def tree_step(self, spec, route_tokens: bool = True, graph: bool = False):
         """Draft the tree on the device and (optionally) gather its verification route tokens
         ``[n, R, Dt]``; returns (node tokens int64 [n] (device view), route tokens or None).
-        No host synchronisation."""
+        No host synchronisation.
+
+        ``graph=True`` replays the step's launches from a HIP graph captured on the first call for
+        this tree shape (the launches read the drafter state from device memory, so one capture
+        serves every later step).  The route tokens then live in a buffer owned by the capture:
+        each replay overwrites the previous step's."""
+        if graph and self.tree_work is None:
+            key = (tuple(spec.parent), tuple(spec.rank), bool(route_tokens))
+            ent = self._graphs.get(key)
+            if ent is None:
+                self.tree_step(spec, route_tokens)          # eager once: argument errors surface here
+                torch.cuda.synchronize(self.device)
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    node, out = self.tree_step(spec, route_tokens)
+                ent = self._graphs[key] = (g, out)
+            ent[0].replay()
+            return self.tok_d[self.tree_row0: self.tree_row0 + spec.n], ent[1]
         n = spec.n
         if n > _TREE_ROWS:
             raise ValueError(f"at most {_TREE_ROWS} tree nodes")

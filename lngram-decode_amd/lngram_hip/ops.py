@@ -465,17 +465,26 @@ def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -
 
 
 # ----------------------------------------------------------------------------- K5
-def tree_accept(parent: torch.Tensor, node_tokens: torch.Tensor, argmax: torch.Tensor):
+def tree_accept(parent: torch.Tensor, node_tokens: torch.Tensor, argmax: torch.Tensor, out=None):
     """Device tree acceptance -> ``(path int32 [n], path_len int32 [1], new_tokens int64 [n])``
-    (valid entries: the first ``path_len``)."""
+    (valid entries: the first ``path_len``).  ``out`` = (path, path_len, new_tokens) writes into
+    caller tensors of those dtypes and sizes (e.g. views of one buffer, so that one copy brings
+    the whole result to the host)."""
     dev = _dev(parent, node_tokens, argmax)
     n = parent.numel()
     p = _c(parent.to(torch.int32))
     nt = _c(node_tokens.to(torch.int64))
     am = _c(argmax.to(torch.int64))
-    path = torch.empty(n, dtype=torch.int32, device=dev)
-    plen = torch.empty(1, dtype=torch.int32, device=dev)
-    new = torch.empty(n, dtype=torch.int64, device=dev)
+    if out is None:
+        path = torch.empty(n, dtype=torch.int32, device=dev)
+        plen = torch.empty(1, dtype=torch.int32, device=dev)
+        new = torch.empty(n, dtype=torch.int64, device=dev)
+    else:
+        path, plen, new = out
+        if (path.dtype, plen.dtype, new.dtype) != (torch.int32, torch.int32, torch.int64) or \
+                path.numel() < n or plen.numel() < 1 or new.numel() < n or \
+                not all(x.is_contiguous() and x.device == p.device for x in (path, plen, new)):
+            raise ValueError("tree_accept out: contiguous int32 [n], int32 [1], int64 [n] on the device")
     check(lib().lng_tree_accept(_ptr(p), _ptr(nt), _ptr(am), n, _ptr(path), _ptr(plen), _ptr(new), _stream(dev)),
           "tree_accept")
     return path, plen, new

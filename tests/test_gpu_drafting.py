@@ -239,3 +239,30 @@ def test_sdb_shape_one_launch_tree_matches_per_depth_launches_and_oracle(dev):
         assert torch.equal(r1, r0)
         rows = slice(g1.tree_row0, g1.tree_row0 + SPEC16.n)
         assert torch.equal(g1.codes_d[rows][1:], g0.codes_d[rows][1:])
+
+
+def test_sdb_shape_graph_tree_step_replays_match_eager(dev):
+    """The captured tree step (one HIP graph per tree shape) equals the eager launches on every
+    replay, with eager drafter work (commits, truncations) between the replays."""
+    w = wl.SDB_DRAFT
+    cfg, t = wl.build_draft_bundle(w, seed=0)
+    ctx = wl.make_context(w, seed=0)
+    g = GpuDrafter((cfg, t), device=dev, max_len=w.context + 16, online=True)
+    g.commit(ctx[:-6])
+    extra = list(ctx[-6:])
+    for rnd in range(4):
+        node_e, rt_e = g.tree_step(SPEC16, route_tokens=True)
+        node_e, rt_e = node_e.clone(), rt_e.clone()
+        node_g, rt_g = g.tree_step(SPEC16, route_tokens=True, graph=True)
+        torch.cuda.synchronize()
+        assert torch.equal(node_g, node_e), rnd
+        assert torch.equal(rt_g, rt_e), rnd
+        # eager work between replays: the committed state moves on, and is rolled back once
+        g.commit(extra[rnd: rnd + 1])
+        if rnd == 2:
+            g.truncate(g.length - 1)
+            g.commit(extra[rnd: rnd + 1])
+    node_e = g.tree_step(SPEC16, route_tokens=False)[0].clone()
+    node_g = g.tree_step(SPEC16, route_tokens=False, graph=True)[0]
+    torch.cuda.synchronize()
+    assert torch.equal(node_g, node_e)
