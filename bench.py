@@ -395,8 +395,10 @@ def measured_traffic(name: str = "readout_fused_sb_traffic.json"):
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the GPU reaches its steady clocks after some tens of milliseconds of load: 50 warmup
+    # forwards (~20 ms), then 100 timed ones (~40 ms)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--draft-iters", type=int, default=200)
@@ -494,13 +496,13 @@ def main() -> None:
             result["draft_step_us"]["cpu_baseline"] = draft_cpu_baseline(args.cpu_seconds)
     if not args.no_scaled:
         log("scaled-table gather")
-        result["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 2)
+        result["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 5)
         if not args.no_cpu:
             log("scaled-table gather cpu baseline")
             result["scaled_gather"]["cpu_baseline"] = scaled_cpu_baseline(min(args.cpu_seconds, 8.0))
     if not args.no_sdc:
         log("SD-C forward")
-        result["sdc_forward"] = sdc_forward(dev, max(3, args.steps // 2), 2)
+        result["sdc_forward"] = sdc_forward(dev, max(3, args.steps // 2), 5)
         if not args.no_cpu:
             log("SD-C cpu baseline")
             result["sdc_forward"]["cpu_baseline"] = sdc_cpu_baseline(min(args.cpu_seconds, 8.0))
