@@ -323,89 +323,146 @@ __global__ __launch_bounds__(256) void k_row_sumsq_bf16(const bf16* __restrict__
   if (lane == 0) rowsq[m] = ss;
 }
 
-// bf16, kernel 4, dilation 3, single pass: block = (b, 16 positions), d/8 threads, each
-// thread keeps its 8 channels of all 25 rows (16 + 9 causal halo) in registers.  Row
-// norms are reduced across the block (wave sums, then LDS), then the conv runs from the
-// registers.  Every load of the block is issued before the first reduction.
-constexpr int C43R_ROWS = C43_TT + C43_HALO;
+// bf16, kernel 4, dilation 3, single pass: block = (b, CF_TT positions) x all channels, d/4
+// threads of 4 channels.  Each thread loads its 4 channels of the CF_TT + 9 rows (the causal
+// halo included) once; a row's sum of squares is a bf16 dot product per lane, summed over 16
+// lanes with DPP and over the block's 16-lane groups in LDS in a fixed order.  Then the rows are
+// normalised in order and the outputs formed as soon as their last tap is ready.  The rounding
+// sequence is the one of k_causal_conv_k4d3_rowsq: normalise in fp32, round, scale by the
+// weight, round, taps in order with fp32 accumulation (v_dot2_f32_bf16 adds a tap pair's exact
+// bf16 products with one rounding), round, SiLU (hardware exp2 and reciprocal), round, add the
+// residual.  A normalised row r is rounded straight into the pairs (r - 3, r) and (r, r + 3),
+// the operands of the dot products of the outputs that read it.
+constexpr int CF_HALO = 9;
+constexpr int CF_MAXG = 32;  // 16-lane groups per block: d <= 2048
 
-__global__ __launch_bounds__(256) void k_causal_conv_k4d3_bf16_reg(const bf16* __restrict__ mixed,
-                                                                   const bf16* __restrict__ norm_w,
-                                                                   const bf16* __restrict__ conv_w, int64_t T_len,
-                                                                   int32_t d, float eps, int residual,
-                                                                   bf16* __restrict__ out) {
-  __shared__ float part[16][C43R_ROWS];  // per-wave partial sums of squares
-  __shared__ float scale[C43R_ROWS];
-  const int64_t b = blockIdx.y;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * C43_TT;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nwave = (blockDim.x + 63) >> 6;
-  const int c = tid * 8;
-  const bool cok = c < d;
-  const bf16* base = mixed + b * T_len * d;
-  bf16x8 rows[C43R_ROWS];
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// v[k] summed over each 16-lane row of the wave, returned in every lane of the row (fixed
+// order); the N sums advance step by step together, so no DPP read waits on the add before it
+template <int CTRL, int N>
+__device__ __forceinline__ void dpp_add_step(float (&v)[N]) {
 #pragma unroll
-  for (int i = 0; i < C43R_ROWS; ++i) {
-    const int64_t t = t0 - C43_HALO + i;
-    if (cok && t >= 0 && t < T_len) {
-      rows[i] = *reinterpret_cast<const bf16x8*>(base + t * d + c);
-    } else {
+  for (int k = 0; k < N; ++k)
+    v[k] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v[k]), CTRL, 0xF, 0xF, true));
+}
+template <int N>
+__device__ __forceinline__ void row16_sums(float (&v)[N]) {
+  dpp_add_step<0xB1>(v);   // xor 1
+  dpp_add_step<0x4E>(v);   // xor 2
+  dpp_add_step<0x141>(v);  // half-row mirror
+  dpp_add_step<0x140>(v);  // row mirror
+}
+
+__device__ __forceinline__ bf16x2 pk2(float a, float b) { return __builtin_convertvector(f32x2{a, b}, bf16x2); }
+__device__ __forceinline__ float lo_f(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float hi_f(uint32_t u) { return __uint_as_float(u & 0xFFFF0000u); }
+
+template <int TT>
+__global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __restrict__ mixed,
+                                                                const bf16* __restrict__ norm_w,
+                                                                const bf16* __restrict__ conv_w, uint32_t T_len,
+                                                                uint32_t d4, float eps, int residual,
+                                                                bf16* __restrict__ out) {
+  constexpr int ROWS = TT + CF_HALO;
+  __shared__ float part[CF_MAXG][ROWS];
+  __shared__ float srow[ROWS];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ngrp = static_cast<int>(blockDim.x >> 4);
+  const int t0 = static_cast<int>(blockIdx.x) * TT;
+  const int T = static_cast<int>(T_len);
+  const size_t row0 = static_cast<size_t>(blockIdx.y) * T_len;
+  const uint32_t d = d4 * 4u;
+  const bool active = static_cast<uint32_t>(tid) < d4;
+  const uint32_t c = (active ? static_cast<uint32_t>(tid) : 0u) * 4u;
+  auto clamp_t = [&](int tp) { return tp < 0 ? 0 : (tp >= T ? T - 1 : tp); };
+  uint2 x[ROWS];  // channels c .. c+3 of row t0 - 9 + r
 #pragma unroll
-      for (int j = 0; j < 8; ++j) rows[i][j] = static_cast<bf16>(0.f);
+  for (int r = 0; r < ROWS; ++r)
+    x[r] = *reinterpret_cast<const uint2*>(mixed + (row0 + clamp_t(t0 - CF_HALO + r)) * d + c);
+  const uint2 nwv = *reinterpret_cast<const uint2*>(norm_w + c);
+  const uint4 cw01 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(c) * 4);      // channels c, c+1
+  const uint4 cw23 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(c) * 4 + 8);  // channels c+2, c+3
+  const float live = active ? 1.f : 0.f;
+#pragma unroll
+  for (int r0 = 0; r0 < ROWS; r0 += 3) {
+    float ss[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      const int r = r0 + k < ROWS ? r0 + k : ROWS - 1;
+      const float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x[r].x),
+                                                      __builtin_bit_cast(bf16x2, x[r].x), 0.f, false);
+      ss[k] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x[r].y), __builtin_bit_cast(bf16x2, x[r].y), a,
+                                              false) * live;
     }
-  }
+    row16_sums(ss);
 #pragma unroll
-  for (int i = 0; i < C43R_ROWS; ++i) {
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float f = static_cast<float>(rows[i][j]);
-      ss = fmaf(f, f, ss);
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) part[wave][i] = ss;
+    for (int k = 0; k < 3; ++k)
+      if (r0 + k < ROWS && (lane & 15) == 0) part[tid >> 4][r0 + k] = ss[k];
   }
   __syncthreads();
-  if (tid < C43R_ROWS) {
+  if (tid < ROWS) {
     float ss = 0.f;
-    for (int k = 0; k < nwave; ++k) ss += part[k][tid];
-    const int64_t t = t0 - C43_HALO + tid;
-    scale[tid] = (t >= 0 && t < T_len) ? 1.0f / sqrtf(ss / static_cast<float>(d) + eps) : 0.f;
+    for (int g = 0; g < ngrp; ++g) ss += part[g][tid];
+    // rows before the sequence start are the zero left padding
+    srow[tid] = t0 - CF_HALO + tid < 0 ? 0.f : 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
   }
   __syncthreads();
-  if (!cok) return;
-  const bf16x8 nwv = *reinterpret_cast<const bf16x8*>(norm_w + c);
-  float w[4][8];
+  if (!active) return;
+  const float nw[4] = {lo_f(nwv.x), hi_f(nwv.x), lo_f(nwv.y), hi_f(nwv.y)};
+  // tap pairs of channel c + j: (w0, w1) and (w2, w3)
+  const uint32_t wa[4] = {cw01.x, cw01.z, cw23.x, cw23.z};
+  const uint32_t wb[4] = {cw01.y, cw01.w, cw23.y, cw23.w};
+  float yn[ROWS][4];   // normalised rows (bf16 values up to the last rounding, fp32)
+  bf16x2 q[ROWS][4];   // q[r][j] = (yn[r][j], yn[r + 3][j]) rounded to bf16
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
+  for (int r = 0; r < ROWS; ++r) {
+    const float s = srow[r];
+    const float xf[4] = {lo_f(x[r].x), hi_f(x[r].x), lo_f(x[r].y), hi_f(x[r].y)};
+    const uint32_t p0 = __builtin_bit_cast(uint32_t, pk2(xf[0] * s, xf[1] * s));
+    const uint32_t p1 = __builtin_bit_cast(uint32_t, pk2(xf[2] * s, xf[3] * s));
+    yn[r][0] = lo_f(p0) * nw[0];
+    yn[r][1] = hi_f(p0) * nw[1];
+    yn[r][2] = lo_f(p1) * nw[2];
+    yn[r][3] = hi_f(p1) * nw[3];
+    if (r >= 3) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) w[k][j] = static_cast<float>(conv_w[(c + j) * 4 + k]);
-  // normalised rows, rounded to bf16 as the reference stores them
-  bf16x8 xn[C43R_ROWS];
-#pragma unroll
-  for (int i = 0; i < C43R_ROWS; ++i) {
-    const float s = scale[i];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      xn[i][j] = static_cast<bf16>(round_to<bf16>(static_cast<float>(rows[i][j]) * s) * static_cast<float>(nwv[j]));
-  }
-#pragma unroll
-  for (int tt = 0; tt < C43_TT; ++tt) {
-    const int64_t t = t0 + tt;
-    if (t >= T_len) break;
-    const int i = tt + C43_HALO;  // row index of position t
-    bf16x8 o;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float acc = w[0][j] * static_cast<float>(xn[i - 9][j]);
-      acc = fmaf(w[1][j], static_cast<float>(xn[i - 6][j]), acc);
-      acc = fmaf(w[2][j], static_cast<float>(xn[i - 3][j]), acc);
-      acc = fmaf(w[3][j], static_cast<float>(xn[i][j]), acc);
-      const float y = round_to<bf16>(acc);
-      const float act = round_to<bf16>(y / (1.0f + expf(-y)));
-      o[j] = static_cast<bf16>(residual ? static_cast<float>(rows[i][j]) + act : act);
+      for (int j = 0; j < 4; ++j) q[r - 3][j] = pk2(yn[r - 3][j], yn[r][j]);
     }
-    *reinterpret_cast<bf16x8*>(out + (b * T_len + t) * d + c) = o;
+    if (r >= CF_HALO) {
+      // output t = t0 + i reads rows i, i+3 (taps 0, 1) and i+6, i+9 (taps 2, 3); row i + 9 = r
+      const int i = r - CF_HALO;
+      const int t = t0 + i;
+      if (t < T) {
+        float y[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = __builtin_amdgcn_fdot2_f32_bf16(q[i][j], __builtin_bit_cast(bf16x2, wa[j]), 0.f, false);
+          y[j] = __builtin_amdgcn_fdot2_f32_bf16(q[i + 6][j], __builtin_bit_cast(bf16x2, wb[j]), a, false);
+        }
+        const uint32_t yp0 = __builtin_bit_cast(uint32_t, pk2(y[0], y[1]));
+        const uint32_t yp1 = __builtin_bit_cast(uint32_t, pk2(y[2], y[3]));
+        const float yr[4] = {lo_f(yp0), hi_f(yp0), lo_f(yp1), hi_f(yp1)};
+        float act[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(-yr[j] * 1.4426950408889634f);
+          act[j] = yr[j] * __builtin_amdgcn_rcpf(1.0f + e);
+        }
+        uint2 o;
+        if (residual) {
+          const uint32_t ap0 = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+          const uint32_t ap1 = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+          o.x = __builtin_bit_cast(uint32_t, pk2(xf[0] + lo_f(ap0), xf[1] + hi_f(ap0)));
+          o.y = __builtin_bit_cast(uint32_t, pk2(xf[2] + lo_f(ap1), xf[3] + hi_f(ap1)));
+        } else {
+          o.x = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+          o.y = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+        }
+        *reinterpret_cast<uint2*>(out + (row0 + t) * d + c) = o;
+      }
+    }
   }
 }
 
@@ -489,12 +546,13 @@ int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, i
   const int halo = (K - 1) * dilation;
   if (halo > 4096) return fail(LNG_E_ARG, "causal_conv: receptive field too large");
   hipStream_t s = as_stream(stream);
-  if (K == 4 && dilation == 3 && d % 8 == 0 && d <= 2048 && dtype == LNG_BF16) {
-    dim3 g43(static_cast<unsigned>(cdiv(T, C43_TT)), static_cast<unsigned>(B));
-    const int threads = static_cast<int>(cdiv(d / 8, 64) * 64);
-    hipLaunchKernelGGL(k_causal_conv_k4d3_bf16_reg, g43, dim3(threads), 0, s, static_cast<const bf16*>(mixed),
-                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), T, d, eps, residual,
-                       static_cast<bf16*>(out));
+  if (K == 4 && dilation == 3 && d % 4 == 0 && d <= 2048 && dtype == LNG_BF16 && B <= 65535) {
+    constexpr int TT = 32;
+    dim3 g43(static_cast<unsigned>(cdiv(T, TT)), static_cast<unsigned>(B));
+    const int threads = static_cast<int>(cdiv(d / 4, 64) * 64);
+    hipLaunchKernelGGL(k_causal_conv_k4d3_fused<TT>, g43, dim3(threads), 0, s, static_cast<const bf16*>(mixed),
+                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w),
+                       static_cast<uint32_t>(T), static_cast<uint32_t>(d / 4), eps, residual, static_cast<bf16*>(out));
     return check_launch("causal_conv_k4d3_bf16");
   }
   if (K == 4 && dilation == 3 && d % 8 == 0 && (dtype == LNG_F32 || dtype == LNG_BF16)) {

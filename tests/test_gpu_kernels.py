@@ -188,7 +188,7 @@ def test_causal_conv(dev, dtype, tol):
     assert om.rel_err(got2, ref64 - mixed.double()) < tol
 
 
-@pytest.mark.parametrize("b,t,d,k", [(2, 300, 1024, 1024), (3, 37, 1000, 64), (1, 5, 8, 32)])
+@pytest.mark.parametrize("b,t,d,k", [(2, 300, 1024, 1024), (3, 37, 1000, 64), (1, 5, 8, 32), (2, 70, 2048, 64)])
 def test_linear_rowsq_and_conv_from_row_stats(dev, b, t, d, k):
     # o_proj with fused row statistics, then the conv that consumes them: the statistics are the
     # sums of squares of the bf16 outputs, the conv matches the oracle with the reference rounding
