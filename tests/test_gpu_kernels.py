@@ -124,6 +124,19 @@ def test_router_logits_and_codes(dev, dtype, shape):
     np.testing.assert_array_equal(_np(codes_only), got)
 
 
+def test_router_codes_two_bit_routes_large(dev):
+    # bits != 4 at a large batch: fp32 logits from the wide-tile MFMA kernel, then the pack kernel
+    m, k, n = 4500, 1024, 736
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(m, k, generator=g).bfloat16()
+    w = (torch.randn(n, k, generator=g) * 0.02).bfloat16()
+    q64 = om.router_logits(x, w).numpy()
+    logits, codes = ops.router_codes(x.to(dev), w.to(dev), 2, want_logits=True, codes_dtype=torch.int32)
+    bound = k * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T).numpy()
+    assert (np.abs(_np(logits) - q64) <= bound + 1e-12).all()
+    np.testing.assert_array_equal(_np(codes), om.pack_route_codes(_np(logits).astype(np.float64), 2))
+
+
 # ----------------------------------------------------------------------------- K3 pieces
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rmsnorm(dev, dtype):
