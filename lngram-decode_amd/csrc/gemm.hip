@@ -413,7 +413,7 @@ __device__ __forceinline__ int wswz(int row, int piece) { return piece ^ ((row >
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
                                                            int64_t N, int64_t M, int64_t K, int n_tiles,
-                                                           float* __restrict__ y, void* __restrict__ codes,
+                                                           int xcd_local, float* __restrict__ y, void* __restrict__ codes,
                                                            int codes_dt, int64_t routes) {
   static_assert(EPI == EPI_F32 || EPI == EPI_ROUTER, "fp32 outputs and router codes only");
   constexpr int TN = WT_N / WT_WN, TM = WT_M / WT_WM, FI = TN / 16, FJ = TM / 16;
@@ -421,8 +421,12 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WT_WN, wm = wave / WT_WN;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x % n_tiles) * WT_N;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.x / n_tiles) * WT_M;
+  // block -> tiles: with xcd_local, the n_tiles blocks of one X tile are dispatched to the same XCD
+  // (blocks go to XCDs round-robin, block b to XCD b % 8), so the X tile comes from HBM into one L2
+  const int b = static_cast<int>(blockIdx.x);
+  const int slot = xcd_local ? b >> 3 : b;
+  const int64_t n0 = static_cast<int64_t>(slot % n_tiles) * WT_N;
+  const int64_t m0 = (static_cast<int64_t>(xcd_local ? (b & 7) * xcd_local : 0) + slot / n_tiles) * WT_M;
   const int nk = static_cast<int>(K / DK);
   // DMA: tile rows 0 .. WT_N-1 are W rows, the rest X rows; wave w fills rows
   // 16 * (w * WT_DPW + d) .. +16 of both, 4 lanes (16 B pieces) per row
@@ -559,8 +563,11 @@ static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64
   if constexpr (EPI != EPI_BF16) {
     if (K % DK == 0 && M >= 4096 && N > GB2 && N <= 2 * WT_N && (N & 3) == 0) {
       const int n_tiles = static_cast<int>(cdiv(N, WT_N));
-      const dim3 g(static_cast<unsigned>(n_tiles * cdiv(M, WT_M)));
-      hipLaunchKernelGGL(k_gemm_wide_bf16<EPI>, g, dim3(512), 0, s, w, x, N, M, K, n_tiles,
+      const int64_t m_tiles = cdiv(M, WT_M);
+      // X tiles per XCD when the grid divides evenly over the 8 XCDs, else 0 (plain order)
+      const int xcd_local = m_tiles % 8 == 0 ? static_cast<int>(m_tiles / 8) : 0;
+      const dim3 g(static_cast<unsigned>(n_tiles * m_tiles));
+      hipLaunchKernelGGL(k_gemm_wide_bf16<EPI>, g, dim3(512), 0, s, w, x, N, M, K, n_tiles, xcd_local,
                          logits ? logits : static_cast<float*>(out), codes, codes_dt, routes);
       return check_launch("gemm_bf16_wide");
     }

@@ -65,17 +65,23 @@ def lib():
 
 
 class KernelTimer:
-    """Records HIP events around every launch of the named ops on their stream while active.
+    """Records HIP events around the launches of the named ops on their stream while active:
+    every launch, or every ``every``-th one (a timing event pair costs a few microseconds of
+    device time, so a long timed loop brackets a sample of its launches).
 
-        with ops.KernelTimer("memory_readout_fused") as kt:
-            ...                       # launches are bracketed by events
-        kt.mean_ms()                  # average device duration per launch (synchronises)
+        with ops.KernelTimer("memory_readout_fused", every=5) as kt:
+            ...                       # launches 0, 5, 10, ... are bracketed by events
+        kt.mean_ms()                  # average device duration per bracketed launch (synchronises)
     """
 
     _active: list = []
 
-    def __init__(self, *names: str):
+    def __init__(self, *names: str, every: int = 1):
+        if every < 1:
+            raise ValueError("every must be >= 1")
         self.names = set(names)
+        self.every = int(every)
+        self.launches = 0
         self.events: list = []
 
     def __enter__(self):
@@ -97,7 +103,12 @@ class KernelTimer:
 
 
 def _timed(name: str, dev: torch.device, launch):
-    timers = [t for t in KernelTimer._active if name in t.names]
+    timers = []
+    for t in KernelTimer._active:
+        if name in t.names:
+            if t.launches % t.every == 0:
+                timers.append(t)
+            t.launches += 1
     if not timers:
         return launch()
     st = torch.cuda.current_stream(dev)
