@@ -398,17 +398,18 @@ __global__ __launch_bounds__(512, 1) void k_gemm_dma256_bf16(const bf16* __restr
 
 // ---------------------------------------------------------------------------------------
 // Wide-N variant for large M and N of a few hundred (the route routers, N = 724 .. 736):
-// 384 (W rows) x 128 (X rows) tile, 8 waves (4 x 2, each 96 x 64), the same 4-stage DMA ring
-// (128 KB LDS, one block per CU).  N = 736 splits into two tiles, so 16384 tokens make 256
-// blocks, one per CU, where the 256 x 256 tile leaves a quarter of the CUs idle.  Rows are
-// swizzled with piece p ^ ((r >> 1) & 3): within every 8 lanes (8 rows of one 16 B piece) the
-// reads cover 8 distinct 16 B bank groups.  Epilogues: fp32 outputs (optional for the router)
-// and the router's sign codes.
-constexpr int WT_N = 384, WT_M = 128, WT_WN = 4, WT_WM = 2;
+// 384 (W rows) x 128 (X rows) tile, 8 waves (4 x 2, each 96 x 64 of 16x16x32 MFMAs).  N = 736
+// splits into two tiles, so 16384 tokens make 256 blocks, one per CU, where the 256 x 256 tile
+// leaves a quarter of the CUs idle.  K advances 64 per stage: every row of a stage is one whole
+// 128 B line, fetched by one DMA lane group (8 lanes x 16 B), in a 2-slot ring (2 x 64 KB of
+// LDS): stage k + 1 is in flight while stage k is multiplied.  Piece p of row r sits at slot
+// p ^ (r & 7), so the 8 rows that 8 consecutive lanes read land in 8 distinct 16 B bank groups.
+// Epilogues: fp32 outputs (optional for the router) and the router's sign codes.
+constexpr int WT_N = 384, WT_M = 128, WT_WN = 4, WT_WM = 2, WT_K = 64;
 constexpr int WT_ROWS = WT_N + WT_M;
-constexpr int WT_DPW = WT_ROWS / 16 / (WT_WN * WT_WM);  // DMA instructions per wave per stage
+constexpr int WT_DPW = WT_ROWS / 8 / (WT_WN * WT_WM);  // DMA instructions (8 rows each) per wave per stage
 
-__device__ __forceinline__ int wswz(int row, int piece) { return piece ^ ((row >> 1) & 3); }
+__device__ __forceinline__ int wswz(int row, int piece) { return piece ^ (row & 7); }
 
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
@@ -417,7 +418,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
                                                            int codes_dt, int64_t routes) {
   static_assert(EPI == EPI_F32 || EPI == EPI_ROUTER, "fp32 outputs and router codes only");
   constexpr int TN = WT_N / WT_WN, TM = WT_M / WT_WM, FI = TN / 16, FJ = TM / 16;
-  __shared__ __attribute__((aligned(16))) bf16 ring[DSLOTS][WT_ROWS * DK];
+  __shared__ __attribute__((aligned(16))) bf16 ring[2][WT_ROWS * WT_K];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave % WT_WN, wm = wave / WT_WN;
@@ -427,14 +428,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
   const int slot = xcd_local ? b >> 3 : b;
   const int64_t n0 = static_cast<int64_t>(slot % n_tiles) * WT_N;
   const int64_t m0 = (static_cast<int64_t>(xcd_local ? (b & 7) * xcd_local : 0) + slot / n_tiles) * WT_M;
-  const int nk = static_cast<int>(K / DK);
+  const int nk = static_cast<int>(K / WT_K);
   // DMA: tile rows 0 .. WT_N-1 are W rows, the rest X rows; wave w fills rows
-  // 16 * (w * WT_DPW + d) .. +16 of both, 4 lanes (16 B pieces) per row
+  // 8 * (w * WT_DPW + d) .. +8, 8 lanes (16 B pieces) per row
   const bf16* src[WT_DPW];
 #pragma unroll
   for (int d = 0; d < WT_DPW; ++d) {
-    const int row = (wave * WT_DPW + d) * 16 + (lane >> 2);
-    const int piece = wswz(row, lane & 3);
+    const int row = (wave * WT_DPW + d) * 8 + (lane >> 3);
+    const int piece = wswz(row, lane & 7);
     if (row < WT_N) {
       const int64_t r = n0 + row < N ? n0 + row : N - 1;
       src[d] = W + r * K + 8 * piece;
@@ -444,15 +445,14 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
     }
   }
   auto issue = [&](int kt) {
-    bf16* base = &ring[kt % DSLOTS][wave * WT_DPW * 16 * DK];
-    const int64_t kb = static_cast<int64_t>(kt) * DK;
+    bf16* base = &ring[kt & 1][wave * WT_DPW * 8 * WT_K];
+    const int64_t kb = static_cast<int64_t>(kt) * WT_K;
 #pragma unroll
     for (int d = 0; d < WT_DPW; ++d) {
-      bf16* dst = base + d * 16 * DK;
+      bf16* dst = base + d * 8 * WT_K;
       __builtin_amdgcn_global_load_lds(src[d] + kb, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
     }
   };
-  static_assert(WT_DPW == 4, "the waits below count 4 DMA instructions per stage");
 
   f32x4 acc[FI][FJ];
 #pragma unroll
@@ -460,34 +460,35 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
 #pragma unroll
     for (int j = 0; j < FJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = 0; s < DSLOTS - 1 && s < nk; ++s) issue(s);
+  issue(0);
   const int rsel = lane & 15, psel = lane >> 4;
   for (int kt = 0; kt < nk; ++kt) {
-    const int ahead = nk - 1 - kt;
-    if (ahead >= 2)
-      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else if (ahead == 1)
-      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // stage kt (the only one in flight) landed for this wave; the barrier makes it landed for all
+    // and every wave done with slot (kt + 1) & 1, which stage kt + 1 then refills
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
-    if (kt + DSLOTS - 1 < nk) issue(kt + DSLOTS - 1);
-    const bf16* st = &ring[kt % DSLOTS][0];
-    bf16x8 a[FI], b[FJ];
+    asm volatile("" ::: "memory");
+    if (kt + 1 < nk) issue(kt + 1);
+    const bf16* st = &ring[kt & 1][0];
 #pragma unroll
-    for (int i = 0; i < FI; ++i) {
-      const int ra = wn * TN + i * 16 + rsel;
-      a[i] = *reinterpret_cast<const bf16x8*>(st + ra * DK + 8 * wswz(ra, psel));
+    for (int kk = 0; kk < WT_K / 32; ++kk) {
+      bf16x8 a[FI], bv[FJ];
+#pragma unroll
+      for (int i = 0; i < FI; ++i) {
+        const int ra = wn * TN + i * 16 + rsel;
+        a[i] = *reinterpret_cast<const bf16x8*>(st + ra * WT_K + 8 * wswz(ra, 4 * kk + psel));
+      }
+#pragma unroll
+      for (int j = 0; j < FJ; ++j) {
+        const int rb = WT_N + wm * TM + j * 16 + rsel;
+        bv[j] = *reinterpret_cast<const bf16x8*>(st + rb * WT_K + 8 * wswz(rb, 4 * kk + psel));
+      }
+#pragma unroll
+      for (int i = 0; i < FI; ++i)
+#pragma unroll
+        for (int j = 0; j < FJ; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bv[j], acc[i][j], 0, 0, 0);
     }
-#pragma unroll
-    for (int j = 0; j < FJ; ++j) {
-      const int rb = WT_N + wm * TM + j * 16 + rsel;
-      b[j] = *reinterpret_cast<const bf16x8*>(st + rb * DK + 8 * wswz(rb, psel));
-    }
-#pragma unroll
-    for (int i = 0; i < FI; ++i)
-#pragma unroll
-      for (int j = 0; j < FJ; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
   }
 
 #pragma unroll
@@ -561,7 +562,7 @@ template <int EPI>
 static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, void* out, float* logits,
                        void* codes, int codes_dt, int64_t routes, hipStream_t s, float* rowsq = nullptr) {
   if constexpr (EPI != EPI_BF16) {
-    if (K % DK == 0 && M >= 4096 && N > GB2 && N <= 2 * WT_N && (N & 3) == 0) {
+    if (K % WT_K == 0 && M >= 4096 && N > GB2 && N <= 2 * WT_N && (N & 3) == 0) {
       const int n_tiles = static_cast<int>(cdiv(N, WT_N));
       const int64_t m_tiles = cdiv(M, WT_M);
       // X tiles per XCD when the grid divides evenly over the 8 XCDs, else 0 (plain order)
