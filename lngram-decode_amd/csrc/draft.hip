@@ -947,6 +947,9 @@ constexpr int FA_DW = (((FA_TB + DR_MAXN) * 256 + 8) / 4);
 
 __device__ __host__ __forceinline__ int fa_rec(int QH, int I) { return I + 4 * ((2 * QH + 3) / 4); }
 
+// QH_T, DT_T, HD_T: q_heads, dt and head_dim fixed at compile time (0 = read from the drafter), so
+// the per-head and per-feature loops of a common shape unroll without predication
+template <int QH_T, int DT_T, int HD_T>
 __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F, int32_t nch, int32_t nob,
                                                      int32_t online, float* __restrict__ part,
                                                      int32_t* __restrict__ counts, float* __restrict__ ro) {
@@ -977,7 +980,8 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   auto ord_at = [&](int oi) { return oi == 0 ? ord0 : (oi == 1 ? ord1 : (oi == 2 ? ord2 : ord3)); };
   auto tab_at = [&](int oi) { return oi == 0 ? tab0 : (oi == 1 ? tab1 : (oi == 2 ? tab2 : tab3)); };
   const int L = *D.length;
-  const int Dt = D.dt, QH = D.q_heads, hd = D.head_dim, md = D.mem_dim, R = D.R;
+  const int Dt = DT_T ? DT_T : D.dt, QH = QH_T ? QH_T : D.q_heads, hd = HD_T ? HD_T : D.head_dim;
+  const int md = D.mem_dim, R = D.R;
   const int I = QH * hd, QD = QH * Dt, G = QH / D.kv_heads;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int mask = (1 << bits) - 1;
@@ -2689,9 +2693,15 @@ int dr_readout_fast(const lng_drafter& D, const FastLevel& F, int K, int online,
   if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter: workspace too small");
   if (online && !counts) return fail(LNG_E_ARG, "drafter: online counts need the counts buffer");
   const int nob = online ? static_cast<int>(cdiv(max_pairs, FA_TB)) : 0;
-  hipLaunchKernelGGL(k_fast_attend, dim3(static_cast<unsigned>(l.fnch + nob), static_cast<unsigned>(P)), dim3(256), 0, s,
-                     D, F, l.fnch, nob, online, reinterpret_cast<float*>(work + l.fpart), counts,
-                     reinterpret_cast<float*>(work + l.ro));
+  {
+    const dim3 ga(static_cast<unsigned>(l.fnch + nob), static_cast<unsigned>(P));
+    float* fpart = reinterpret_cast<float*>(work + l.fpart);
+    float* fro = reinterpret_cast<float*>(work + l.ro);
+    if (D.q_heads == 4 && D.dt == 256 && D.head_dim == 64)  // the SD drafters' shape
+      hipLaunchKernelGGL((k_fast_attend<4, 256, 64>), ga, dim3(256), 0, s, D, F, l.fnch, nob, online, fpart, counts, fro);
+    else
+      hipLaunchKernelGGL((k_fast_attend<0, 0, 0>), ga, dim3(256), 0, s, D, F, l.fnch, nob, online, fpart, counts, fro);
+  }
   if (int rc = check_launch("drafter_readout(fast attend)")) return rc;
   auto logits = [&](auto kern) {
     hipLaunchKernelGGL(kern, dim3(static_cast<unsigned>(l.fnblk)), dim3(256), 0, s, D, P, K, online, kappa,
