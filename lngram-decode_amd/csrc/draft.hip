@@ -1285,26 +1285,30 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   // merge weights per (chunk, head): f = e^{m_c - M} / (e^{b0 - M} + sum_c l_c e^{m_c - M})
   __shared__ float wgt[FA_MAXCH][LNG_DR_MAX_QH];
   __shared__ __attribute__((aligned(16))) float opart[4][LNG_DR_MAX_QH * LNG_DR_MAX_DT / 4];
-  if (threadIdx.x < QH) {
-    const int qh = threadIdx.x;
-    float pm[FA_MAXCH], pl[FA_MAXCH];
-#pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) {
-      pm[c] = c < nch ? mlb[c][qh] : -INFINITY;
-      pl[c] = c < nch ? mlb[c][QH + qh] : 0.f;
-    }
+  // one thread per (chunk, head) takes its exponential, one thread per head then sums l in chunk
+  // order, and the weights follow: the exponentials run side by side instead of in one chain
+  __shared__ float fex[FA_MAXCH][LNG_DR_MAX_QH];
+  __shared__ float hm[LNG_DR_MAX_QH], hl[LNG_DR_MAX_QH];
+  for (int t = threadIdx.x; t < FA_MAXCH * QH; t += 256) {
+    const int c = t / QH, qh = t % QH;
     float M = b0;
 #pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) M = fmaxf(M, pm[c]);
-    float l = expf(b0 - M);
-    float f[FA_MAXCH];
+    for (int cc = 0; cc < FA_MAXCH; ++cc) M = fmaxf(M, cc < nch ? mlb[cc][qh] : -INFINITY);
+    fex[c][qh] = c < nch ? expf(mlb[c][qh] - M) : 0.f;
+    if (c == 0) hm[qh] = M;
+  }
+  __syncthreads();
+  if (threadIdx.x < QH) {
+    const int qh = threadIdx.x;
+    float l = expf(b0 - hm[qh]);
 #pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) {
-      f[c] = c < nch ? expf(pm[c] - M) : 0.f;
-      l = fmaf(pl[c], f[c], l);
-    }
-#pragma unroll
-    for (int c = 0; c < FA_MAXCH; ++c) wgt[c][qh] = f[c] / l;
+    for (int c = 0; c < FA_MAXCH; ++c) l = fmaf(c < nch ? mlb[c][QH + qh] : 0.f, fex[c][qh], l);
+    hl[qh] = l;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < FA_MAXCH * QH; t += 256) {
+    const int c = t / QH, qh = t % QH;
+    wgt[c][qh] = fex[c][qh] / hl[qh];
   }
   __syncthreads();
   // o = sum_c f_{c, qh(e)} o_c: partial sums over the thread's chunks, then over the four groups
@@ -1326,19 +1330,19 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   for (int e = threadIdx.x; e < I; e += 256) us[e] = (opart[0][e] + opart[1][e]) + (opart[2][e] + opart[3][e]);
   __syncthreads();
   // o . (Gram o): thread (k4 = e4, quarter c4) sums Gram[e][4 k4 .. +3] o[e] over its quarter of e
-  // (Gram is symmetric; one row e is a contiguous kilobyte across the wave), 16 rows per batch
+  // (Gram is symmetric; one row e is a contiguous kilobyte across the wave), 32 rows per batch
   float acc = 0.f;
   if (4 * e4 < I) {
     const int ne = (I + 3) / 4, eb = c4 * ne, ee = min(I, eb + ne);
     f32x4 y = {0.f, 0.f, 0.f, 0.f};
-    for (int e0 = eb; e0 < ee; e0 += 16) {
-      f32x4 gv[16];
+    for (int e0 = eb; e0 < ee; e0 += 32) {
+      f32x4 gv[32];
 #pragma unroll
-      for (int q = 0; q < 16; ++q)
+      for (int q = 0; q < 32; ++q)
         gv[q] = e0 + q < ee ? *reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(e0 + q) * I + 4 * e4)
                             : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
+      for (int q = 0; q < 32; ++q) {
         const float oe = e0 + q < ee ? us[e0 + q] : 0.f;
         y[0] = fmaf(gv[q][0], oe, y[0]);
         y[1] = fmaf(gv[q][1], oe, y[1]);
