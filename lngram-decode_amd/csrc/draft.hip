@@ -1387,7 +1387,8 @@ __device__ __forceinline__ int fl_prefix(const int32_t* nnz, int b, int lane) {
 template <int KM>
 __host__ __device__ constexpr int fl_rs() { return 4 + 4 * ((2 * KM + 3) / 4); }  // whole 16-byte pieces
 
-template <int KM>
+// I_T: q_heads * head_dim fixed at compile time (0 = read from the drafter)
+template <int KM, int I_T>
 __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, int32_t K, int32_t online, float kappa,
                                                      const float* __restrict__ ro, float* __restrict__ logits_out,
                                                      float* __restrict__ lpart, int32_t* __restrict__ counts,
@@ -1399,7 +1400,7 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
   __shared__ int last_flag;
   __shared__ float sel_v[4][KM];
   __shared__ int sel_i[4][KM];
-  const int I = D.q_heads * D.head_dim;
+  const int I = I_T ? I_T : D.q_heads * D.head_dim;
   const int64_t V = D.V;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int64_t v0 = static_cast<int64_t>(blockIdx.x) * FL_VB;
@@ -1434,29 +1435,36 @@ __global__ __launch_bounds__(256) void k_fast_logits(lng_drafter D, int32_t P, i
   for (int st = 0; st < FL_I / 16; ++st)
     bq[st] = (st < nks && col < P) ? *reinterpret_cast<const f32x4*>(&rs[col][16 * st + 4 * kq]) : f32x4{0.f, 0.f, 0.f, 0.f};
   const float* const pk = D.lut_out_pk;
-  for (int tile = 2 * w; tile < 2 * w + 2; ++tile) {
+  // both tiles' operands are loaded before either tile's products: one memory round trip per wave
+  f32x4 a2[2][FL_I / 16];
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2) {
+    const int tile = 2 * w + t2;
     const int64_t vrow = v0 + tile * 16 + col;
-    f32x4 a[FL_I / 16];
     if (pk) {  // packed tiles: one contiguous kilobyte per load (rows past V are zero)
       const float* tp = pk + (((v0 >> 4) + tile) * nks) * 256 + 4 * lane;
 #pragma unroll
       for (int st = 0; st < FL_I / 16; ++st)
-        a[st] = (st < nks && v0 + tile * 16 < V) ? *reinterpret_cast<const f32x4*>(tp + 256 * st)
-                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
+        a2[t2][st] = (st < nks && v0 + tile * 16 < V) ? *reinterpret_cast<const f32x4*>(tp + 256 * st)
+                                                     : f32x4{0.f, 0.f, 0.f, 0.f};
     } else {
 #pragma unroll
       for (int st = 0; st < FL_I / 16; ++st)
-        a[st] = (st < nks && vrow < V) ? *reinterpret_cast<const f32x4*>(D.lut_out + vrow * I + 16 * st + 4 * kq)
-                                       : f32x4{0.f, 0.f, 0.f, 0.f};
+        a2[t2][st] = (st < nks && vrow < V) ? *reinterpret_cast<const f32x4*>(D.lut_out + vrow * I + 16 * st + 4 * kq)
+                                           : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  }
+#pragma unroll
+  for (int t2 = 0; t2 < 2; ++t2) {
+    const int tile = 2 * w + t2;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < FL_I / 16; ++st) {
       if (st < nks) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][0], bq[st][0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][1], bq[st][1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][2], bq[st][2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[st][3], bq[st][3], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[t2][st][0], bq[st][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[t2][st][1], bq[st][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[t2][st][2], bq[st][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a2[t2][st][3], bq[st][3], acc, 0, 0, 0);
       }
     }
 #pragma unroll
@@ -2713,12 +2721,13 @@ int dr_readout_fast(const lng_drafter& D, const FastLevel& F, int K, int online,
                        reinterpret_cast<float*>(work + l.flpart), counts, reinterpret_cast<int4*>(work + l.cand), C,
                        ids, scores);
   };
+  const bool i256 = D.q_heads * D.head_dim == 256;  // the SD drafters' 4 x 64
   switch (K) {
-    case 1: logits(k_fast_logits<1>); break;
-    case 2: logits(k_fast_logits<2>); break;
-    case 3: logits(k_fast_logits<3>); break;
-    case 4: logits(k_fast_logits<4>); break;
-    default: logits(k_fast_logits<DR_MAXK>); break;
+    case 1: i256 ? logits(k_fast_logits<1, 256>) : logits(k_fast_logits<1, 0>); break;
+    case 2: i256 ? logits(k_fast_logits<2, 256>) : logits(k_fast_logits<2, 0>); break;
+    case 3: i256 ? logits(k_fast_logits<3, 256>) : logits(k_fast_logits<3, 0>); break;
+    case 4: i256 ? logits(k_fast_logits<4, 256>) : logits(k_fast_logits<4, 0>); break;
+    default: i256 ? logits(k_fast_logits<DR_MAXK, 256>) : logits(k_fast_logits<DR_MAXK, 0>); break;
   }
   return check_launch("drafter_readout(fast logits)");
 }
