@@ -907,15 +907,12 @@ __device__ __forceinline__ void wave_topk_items(float (&v)[N], int (&id)[N], flo
     int c = INT_MAX;
 #pragma unroll
     for (int a = 0; a < N; ++a) c = min(c, v[a] == M ? id[a] : INT_MAX);
-    const int I = wave_min_i(c);
+    // no item left (every value -inf, taken ones included): no winner
+    const int I = M == -INFINITY ? INT_MAX : wave_min_i(c);
     sv[k] = I == INT_MAX ? -INFINITY : M;
     si[k] = I == INT_MAX ? -1 : I;
 #pragma unroll
-    for (int a = 0; a < N; ++a) {
-      const bool hit = id[a] == I;
-      v[a] = hit ? -INFINITY : v[a];
-      id[a] = hit ? INT_MAX : id[a];
-    }
+    for (int a = 0; a < N; ++a) v[a] = id[a] == I ? -INFINITY : v[a];  // a taken item keeps its id
   }
 }
 
@@ -947,9 +944,10 @@ constexpr int FA_DW = (((FA_TB + DR_MAXN) * 256 + 8) / 4);
 
 __device__ __host__ __forceinline__ int fa_rec(int QH, int I) { return I + 4 * ((2 * QH + 3) / 4); }
 
-// QH_T, DT_T, HD_T: q_heads, dt and head_dim fixed at compile time (0 = read from the drafter), so
-// the per-head and per-feature loops of a common shape unroll without predication
-template <int QH_T, int DT_T, int HD_T>
+// QH_T, DT_T, HD_T, NO_T, MX_T: q_heads, dt, head_dim, the number of orders and the longest order
+// fixed at compile time (0 = read from the drafter), so the per-head, per-feature and per-order
+// loops of a common shape unroll without predication
+template <int QH_T, int DT_T, int HD_T, int NO_T, int MX_T>
 __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F, int32_t nch, int32_t nob,
                                                      int32_t online, float* __restrict__ part,
                                                      int32_t* __restrict__ counts, float* __restrict__ ro) {
@@ -971,7 +969,7 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
   __shared__ float redf[4];
   const int j = blockIdx.y;
   // descriptor fields used in loops, read once (kernel-argument loads otherwise repeat per use)
-  const int bits = D.bits, maxn = D.maxn, n_ord = D.n_orders;
+  const int bits = D.bits, maxn = MX_T ? MX_T : D.maxn, n_ord = NO_T ? NO_T : D.n_orders;
   const int ord0 = D.orders[0], ord1 = D.orders[1], ord2 = D.orders[2], ord3 = D.orders[3];
   const void* const tab0 = D.tables[0];
   const void* const tab1 = D.tables[1];
@@ -2709,10 +2707,12 @@ int dr_readout_fast(const lng_drafter& D, const FastLevel& F, int K, int online,
     const dim3 ga(static_cast<unsigned>(l.fnch + nob), static_cast<unsigned>(P));
     float* fpart = reinterpret_cast<float*>(work + l.fpart);
     float* fro = reinterpret_cast<float*>(work + l.ro);
-    if (D.q_heads == 4 && D.dt == 256 && D.head_dim == 64)  // the SD drafters' shape
-      hipLaunchKernelGGL((k_fast_attend<4, 256, 64>), ga, dim3(256), 0, s, D, F, l.fnch, nob, online, fpart, counts, fro);
+    if (D.q_heads == 4 && D.dt == 256 && D.head_dim == 64 && D.n_orders == 2 && D.maxn == 3)  // the SD drafters
+      hipLaunchKernelGGL((k_fast_attend<4, 256, 64, 2, 3>), ga, dim3(256), 0, s, D, F, l.fnch, nob, online, fpart, counts,
+                         fro);
     else
-      hipLaunchKernelGGL((k_fast_attend<0, 0, 0>), ga, dim3(256), 0, s, D, F, l.fnch, nob, online, fpart, counts, fro);
+      hipLaunchKernelGGL((k_fast_attend<0, 0, 0, 0, 0>), ga, dim3(256), 0, s, D, F, l.fnch, nob, online, fpart, counts,
+                         fro);
   }
   if (int rc = check_launch("drafter_readout(fast attend)")) return rc;
   auto logits = [&](auto kern) {
