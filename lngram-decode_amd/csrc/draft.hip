@@ -1007,6 +1007,19 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
       const int i = 4 * threadIdx.x + 1024 * q;
       qrow[q] = (tok_ok && i < QD) ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * QD + i) : f32x4{0.f, 0.f, 0.f, 0.f};
     }
+  // the value weight of the thread's first o_c item (bf16 Wv, attention blocks): it depends on
+  // nothing the block computes, so its 32 loads are issued now and land during the codes, gather
+  // and scores phases
+  const int items_w = QH * (hd / 8) * (Dt / 32);
+  const bool wv_pre = is_attn && D.wv_dtype == LNG_BF16 && static_cast<int>(threadIdx.x) < items_w;
+  bf16x8 wv8[32];
+  if (wv_pre) {
+    const int it = threadIdx.x, nob8 = hd / 8, nrb = Dt / 32;
+    const int qh = it / (nob8 * nrb), rem = it % (nob8 * nrb), o8 = rem % nob8, rb = rem / nob8;
+    const bf16* wt = static_cast<const bf16*>(D.wv_t) + (static_cast<int64_t>(qh / G) * Dt + 32 * rb) * hd + 8 * o8;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) wv8[q] = *reinterpret_cast<const bf16x8*>(wt + static_cast<int64_t>(q) * hd);
+  }
   for (int e = threadIdx.x; e < nr * maxn; e += 256) {
     const int k = e / nr, rr = e % nr, r = r0 + rr;
     const int32_t row = srow[k];
@@ -1127,9 +1140,9 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
         float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
         if (D.wv_dtype == LNG_BF16) {
           const bf16* wt = static_cast<const bf16*>(D.wv_t) + (static_cast<int64_t>(h) * Dt + 32 * rb) * hd + 8 * o8;
-          bf16x8 wv8[32];
+          if (it != static_cast<int>(threadIdx.x))  // the first item was loaded at kernel entry
 #pragma unroll
-          for (int q = 0; q < 32; ++q) wv8[q] = *reinterpret_cast<const bf16x8*>(wt + static_cast<int64_t>(q) * hd);
+            for (int q = 0; q < 32; ++q) wv8[q] = *reinterpret_cast<const bf16x8*>(wt + static_cast<int64_t>(q) * hd);
 #pragma unroll
           for (int q = 0; q < 32; ++q) {
             const float uq = us[qh * Dt + 32 * rb + q];
