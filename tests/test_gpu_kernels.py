@@ -103,7 +103,7 @@ def test_pack_route_codes_bit_exact(dev):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("shape", [(300, 1024, 736), (37, 128, 32), (129, 2304, 724), (4500, 1024, 736),
-                                   (4100, 2304, 724)])
+                                   (4100, 2304, 724), (4200, 1056, 736)])
 def test_router_logits_and_codes(dev, dtype, shape):
     m, k, n = shape
     g = torch.Generator().manual_seed(m + k)
