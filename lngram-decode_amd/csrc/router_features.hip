@@ -7,7 +7,8 @@
 // embedding table (the embedding gather fused in) or from a materialised emb [B*T, d].
 //
 // One wave per position: the two d-wide rows are read as 16-byte pieces held in registers
-// (at most FE_MAXP per lane), squared-summed with a wave reduction, scaled and stored.
+// (at most FE_MAXP per lane), both rows' loads issued before either is reduced, squared-summed
+// with a wave reduction, scaled and stored.
 #include "common.h"
 
 namespace lng {
@@ -26,20 +27,27 @@ struct FeArgs {
   float eps;
 };
 
-template <typename TT>
-__device__ __forceinline__ void fe_norm_row(const TT* src, const TT* w, int d, float eps, TT* dst, int lane) {
-  typedef uint32_t piece_t __attribute__((ext_vector_type(4)));
+typedef uint32_t fe_piece_t __attribute__((ext_vector_type(4)));
+
+// The pieces of one d-wide row that lane `lane` holds (pieces lane, lane + 64, ...; PPL of them).
+template <typename TT, int PPL>
+__device__ __forceinline__ void fe_load_row(const TT* src, int np, int lane, fe_piece_t (&v)[PPL]) {
   constexpr int VE = 16 / sizeof(TT);
-  const int np = d / VE;
-  piece_t v[FE_MAXP];
 #pragma unroll
-  for (int i = 0; i < FE_MAXP; ++i) {
+  for (int i = 0; i < PPL; ++i) {
     const int pc = i * 64 + lane;
-    v[i] = (src && pc < np) ? *reinterpret_cast<const piece_t*>(src + pc * VE) : piece_t{0u, 0u, 0u, 0u};
+    v[i] = (src && pc < np) ? *reinterpret_cast<const fe_piece_t*>(src + pc * VE) : fe_piece_t{0u, 0u, 0u, 0u};
   }
+}
+
+// RMSNorm of the row held in v (model.py:39-48 rounding), stored at dst.
+template <typename TT, int PPL>
+__device__ __forceinline__ void fe_norm_store(const fe_piece_t (&v)[PPL], const TT* w, int d, int np, float eps, TT* dst,
+                                              int lane) {
+  constexpr int VE = 16 / sizeof(TT);
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < FE_MAXP; ++i) {
+  for (int i = 0; i < PPL; ++i) {
     const TT* e = reinterpret_cast<const TT*>(&v[i]);
 #pragma unroll
     for (int j = 0; j < VE; ++j) {
@@ -50,29 +58,33 @@ __device__ __forceinline__ void fe_norm_row(const TT* src, const TT* w, int d, f
   ss = wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
 #pragma unroll
-  for (int i = 0; i < FE_MAXP; ++i) {
+  for (int i = 0; i < PPL; ++i) {
     const int pc = i * 64 + lane;
     if (pc >= np) continue;
-    const piece_t wp = *reinterpret_cast<const piece_t*>(w + pc * VE);
+    const fe_piece_t wp = *reinterpret_cast<const fe_piece_t*>(w + pc * VE);
     const TT* e = reinterpret_cast<const TT*>(&v[i]);
     const TT* ww = reinterpret_cast<const TT*>(&wp);
-    piece_t o;
+    fe_piece_t o;
     TT* oe = reinterpret_cast<TT*>(&o);
 #pragma unroll
     for (int j = 0; j < VE; ++j) oe[j] = from_f32<TT>(round_to<TT>(to_f32(e[j]) * r) * to_f32(ww[j]));
-    *reinterpret_cast<piece_t*>(dst + pc * VE) = o;
+    *reinterpret_cast<fe_piece_t*>(dst + pc * VE) = o;
   }
 }
 
-// grid (cdiv(n_tok, 4)), block 256: wave w owns position 4 * blockIdx.x + w.
-template <typename TT>
+// grid (cdiv(n_tok, 4)), block 256: wave w owns position 4 * blockIdx.x + w.  PPL = 16-byte pieces
+// per lane and row (d / (64 VE) rounded up).  The two rows and the SSM state are requested before
+// either row is reduced: one memory round trip per position.
+template <typename TT, int PPL>
 __global__ __launch_bounds__(256) void k_router_features(FeArgs A, TT* __restrict__ out) {
+  constexpr int VE = 16 / sizeof(TT);
+  constexpr int SQ = 4;  // SSM values per lane held in registers (N <= 256); the rest stream
   const int lane = threadIdx.x & 63;
   const int64_t p = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (p >= A.n_tok) return;
   const int64_t t = p % A.T;
   const TT* emb = static_cast<const TT*>(A.emb);
-  const int d = A.d;
+  const int d = A.d, np = d / VE;
   auto row = [&](int64_t q) -> const TT* {  // embedding row of position q (nullptr: id outside [0, V))
     if (!A.ids) return emb + q * d;
     const int64_t id = A.ids[q];
@@ -81,10 +93,23 @@ __global__ __launch_bounds__(256) void k_router_features(FeArgs A, TT* __restric
   const int64_t od = 2 * static_cast<int64_t>(d) + A.N;
   TT* o = out + p * od;
   const TT* prev = t == 0 ? static_cast<const TT*>(A.start) : row(p - 1);
-  fe_norm_row<TT>(prev, static_cast<const TT*>(A.prev_w), d, A.eps, o, lane);
-  fe_norm_row<TT>(row(p), static_cast<const TT*>(A.cur_w), d, A.eps, o + d, lane);
-  if (A.ssm)
-    for (int i = lane; i < A.N; i += 64) o[2 * d + i] = from_f32<TT>(A.ssm[p * A.N + i]);
+  const TT* cur = row(p);
+  fe_piece_t vp[PPL], vc[PPL];
+  fe_load_row<TT, PPL>(prev, np, lane, vp);
+  fe_load_row<TT, PPL>(cur, np, lane, vc);
+  float sq[SQ];
+  if (A.ssm) {
+#pragma unroll
+    for (int k = 0; k < SQ; ++k) sq[k] = lane + 64 * k < A.N ? A.ssm[p * A.N + lane + 64 * k] : 0.f;
+  }
+  fe_norm_store<TT, PPL>(vp, static_cast<const TT*>(A.prev_w), d, np, A.eps, o, lane);
+  fe_norm_store<TT, PPL>(vc, static_cast<const TT*>(A.cur_w), d, np, A.eps, o + d, lane);
+  if (A.ssm) {
+#pragma unroll
+    for (int k = 0; k < SQ; ++k)
+      if (lane + 64 * k < A.N) o[2 * d + lane + 64 * k] = from_f32<TT>(sq[k]);
+    for (int i = lane + 64 * SQ; i < A.N; i += 64) o[2 * d + i] = from_f32<TT>(A.ssm[p * A.N + i]);
+  }
 }
 
 }  // namespace lng
@@ -107,9 +132,21 @@ extern "C" int lng_router_features(const void* emb, int dtype, const int64_t* to
   if (A.n_tok == 0) return LNG_OK;
   const dim3 grid(static_cast<unsigned>(cdiv(A.n_tok, 4)));
   hipStream_t s = as_stream(stream);
+  const int ppl = static_cast<int>(cdiv(d / ve, 64));  // pieces per lane and row
+  auto go = [&](auto tt) {
+    using TT = decltype(tt);
+    TT* o = static_cast<TT*>(out);
+    switch (ppl) {
+      case 1: hipLaunchKernelGGL((k_router_features<TT, 1>), grid, dim3(256), 0, s, A, o); break;
+      case 2: hipLaunchKernelGGL((k_router_features<TT, 2>), grid, dim3(256), 0, s, A, o); break;
+      case 3:
+      case 4: hipLaunchKernelGGL((k_router_features<TT, 4>), grid, dim3(256), 0, s, A, o); break;
+      default: hipLaunchKernelGGL((k_router_features<TT, FE_MAXP>), grid, dim3(256), 0, s, A, o); break;
+    }
+  };
   if (dtype == LNG_BF16)
-    hipLaunchKernelGGL(k_router_features<bf16>, grid, dim3(256), 0, s, A, static_cast<bf16*>(out));
+    go(bf16{});
   else
-    hipLaunchKernelGGL(k_router_features<float>, grid, dim3(256), 0, s, A, static_cast<float*>(out));
+    go(float{});
   return check_launch("router_features");
 }

@@ -22,7 +22,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype,d,n,ids", [(torch.bfloat16, 64, 16, True), (torch.bfloat16, 1024, 256, False),
-                                           (torch.float32, 32, 0, True), (torch.float32, 48, 8, False)])
+                                           (torch.float32, 32, 0, True), (torch.float32, 48, 8, False),
+                                           (torch.float32, 1024, 300, True), (torch.bfloat16, 2560, 8, False)])
 def test_router_features_match_oracle(dev, dtype, d, n, ids):
     g = torch.Generator().manual_seed(d + n)
     B, T, V = 3, 17, 50
