@@ -86,10 +86,14 @@ int lng_route_tokens(const void* codes, int codes_dtype, int64_t B, int64_t T, i
                      const int32_t* segment_ids, const uint8_t* valid_tokens, int32_t target_length,
                      void* out, void* stream);
 
-/* out[rows, dim] = RMSNorm(x) * w with the reference rounding: normalise in fp32,
- * round to the storage dtype, multiply by w.  lngram_v2.RMSNorm
- * (lngram_v2.py:36-53) and model.RMSNorm (model.py:39-48). */
-int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps,
+/* out[rows, dim] = RMSNorm(x) * w with one of the reference's two roundings:
+ * LNG_NORM_MODEL  model.RMSNorm (model.py:39-48): normalise in fp32, round to the storage
+ *                 dtype, multiply by w, round;
+ * LNG_NORM_FUSED  lngram_v2.RMSNorm (lngram_v2.py:36-53, F.rms_norm): normalise and multiply
+ *                 by w in fp32, round once.
+ * The two agree in fp32. */
+enum { LNG_NORM_MODEL = 0, LNG_NORM_FUSED = 1 };
+int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps, int32_t mode,
                 void* out, void* stream);
 
 /* y[M,N] = x[M,K] . w[N,K]^T in `dtype` (fp32 accumulation, output rounded to

@@ -1,14 +1,25 @@
 // RMSNorm rows and the readout's short causal convolution (+ residual).
 //
-// Rounding follows the reference: normalise in fp32, round to the storage type,
-// multiply by the weight and round again; the conv accumulates in fp32 and
-// rounds its output, SiLU and the residual add each round once more.
+// The reference has two RMSNorms that round differently in bf16:
+// - model.RMSNorm (ffnmem/model.py:39-48; h_norm, router features, draft head, SSM input):
+//   normalise in fp32, round to the storage type, multiply by the weight, round again;
+// - lngram_v2.RMSNorm (lngram_v2.py:36-53, F.rms_norm; the readout's query, memory and
+//   short-conv norms): normalise and apply the weight in fp32, round once.
+// The short conv normalises with the second; it accumulates its taps in fp32 and rounds its
+// output, SiLU and the residual add each once more.
 #include "common.h"
 
 namespace lng {
 
 // One wave per row; 4 rows per 256-thread block.
-template <typename T>
+// One normalised element: FUSED = F.rms_norm (weight applied in fp32, one rounding), else
+// model.RMSNorm (round, multiply by the weight, round).
+template <typename T, bool FUSED>
+__device__ __forceinline__ float norm_elem(float x, float r, float w) {
+  return FUSED ? round_to<T>(x * r * w) : round_to<T>(round_to<T>(x * r) * w);
+}
+
+template <typename T, bool FUSED>
 __global__ __launch_bounds__(256) void k_rmsnorm(const T* __restrict__ x, const T* __restrict__ w, int64_t rows,
                                                  int32_t dim, float eps, T* __restrict__ out) {
   const int lane = threadIdx.x & 63;
@@ -23,12 +34,12 @@ __global__ __launch_bounds__(256) void k_rmsnorm(const T* __restrict__ x, const 
   ss = wave_sum(ss);
   const float r = 1.0f / sqrtf(ss / static_cast<float>(dim) + eps);
   T* o = out + row * dim;
-  for (int c = lane; c < dim; c += 64) o[c] = from_f32<T>(round_to<T>(to_f32(xr[c]) * r) * to_f32(w[c]));
+  for (int c = lane; c < dim; c += 64) o[c] = from_f32<T>(norm_elem<T, FUSED>(to_f32(xr[c]), r, to_f32(w[c])));
 }
 
 // Vectorised RMSNorm for dim = NV * 512 (bf16: 16-byte loads): one wave per row, the
 // whole row is loaded into registers before the reduction (one memory latency per row).
-template <int NV>
+template <int NV, bool FUSED>
 __global__ __launch_bounds__(256) void k_rmsnorm_bf16_vec(const bf16* __restrict__ x, const bf16* __restrict__ w,
                                                           int64_t rows, float eps, bf16* __restrict__ out) {
   constexpr int dim = NV * 512;
@@ -55,7 +66,7 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bf16_vec(const bf16* __restrict
     bf16x8 o;
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      o[j] = static_cast<bf16>(round_to<bf16>(static_cast<float>(v[i][j]) * r) * static_cast<float>(wv[j]));
+      o[j] = static_cast<bf16>(norm_elem<bf16, FUSED>(static_cast<float>(v[i][j]), r, static_cast<float>(wv[j])));
     *reinterpret_cast<bf16x8*>(out + row * dim + (i * 64 + lane) * 8) = o;
   }
 }
@@ -101,7 +112,7 @@ __global__ __launch_bounds__(256) void k_causal_conv(const T* __restrict__ mixed
         const int lag = (K - 1 - j) * dil;
         const int64_t ts = t - lag;
         if (ts < 0) continue;
-        const float xn = round_to<T>(round_to<T>(to_f32(base[ts * d + c]) * scale[tt + halo - lag]) * nw);
+        const float xn = norm_elem<T, true>(to_f32(base[ts * d + c]), scale[tt + halo - lag], nw);
         acc = fmaf(to_f32(conv_w[c * K + j]), xn, acc);
       }
       const float y = round_to<T>(acc);
@@ -192,7 +203,7 @@ __global__ __launch_bounds__(128) void k_causal_conv_k4d3(const T* __restrict__ 
         load8(base + t * d + c, x);
         const float s = scale[step];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) hist[0][j] = round_to<T>(round_to<T>(x[j] * s) * nw[j]);
+        for (int j = 0; j < 8; ++j) hist[0][j] = norm_elem<T, true>(x[j], s, nw[j]);
       } else {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -278,7 +289,7 @@ __global__ __launch_bounds__(256) void k_causal_conv_k4d3_rowsq(const bf16* __re
     float xn[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      xn[j] = round_to<bf16>(round_to<bf16>(static_cast<float>(x[r][j]) * s) * static_cast<float>(nwv[j]));
+      xn[j] = norm_elem<bf16, true>(static_cast<float>(x[r][j]), s, static_cast<float>(nwv[j]));
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int i = r - 3 * k;  // output t0 + i reads this row with tap k
@@ -328,8 +339,8 @@ __global__ __launch_bounds__(256) void k_row_sumsq_bf16(const bf16* __restrict__
 // halo included) once; a row's sum of squares is a bf16 dot product per lane, summed over 16
 // lanes with DPP and over the block's 16-lane groups in LDS in a fixed order.  Then the rows are
 // normalised in order and the outputs formed as soon as their last tap is ready.  The rounding
-// sequence is the one of k_causal_conv_k4d3_rowsq: normalise in fp32, round, scale by the
-// weight, round, taps in order with fp32 accumulation (v_dot2_f32_bf16 adds a tap pair's exact
+// sequence is the one of k_causal_conv_k4d3_rowsq: normalise and scale by the weight in fp32,
+// round once, taps in order with fp32 accumulation (v_dot2_f32_bf16 adds a tap pair's exact
 // bf16 products with one rounding), round, SiLU (hardware exp2 and reciprocal), round, add the
 // residual.  A normalised row r is rounded straight into the pairs (r - 3, r) and (r, r + 3),
 // the operands of the dot products of the outputs that read it.
@@ -414,18 +425,14 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
   // tap pairs of channel c + j: (w0, w1) and (w2, w3)
   const uint32_t wa[4] = {cw01.x, cw01.z, cw23.x, cw23.z};
   const uint32_t wb[4] = {cw01.y, cw01.w, cw23.y, cw23.w};
-  float yn[ROWS][4];   // normalised rows (bf16 values up to the last rounding, fp32)
+  float yn[ROWS][4];   // normalised rows times the weight, fp32 (rounded once, into q)
   bf16x2 q[ROWS][4];   // q[r][j] = (yn[r][j], yn[r + 3][j]) rounded to bf16
 #pragma unroll
   for (int r = 0; r < ROWS; ++r) {
     const float s = srow[r];
     const float xf[4] = {lo_f(x[r].x), hi_f(x[r].x), lo_f(x[r].y), hi_f(x[r].y)};
-    const uint32_t p0 = __builtin_bit_cast(uint32_t, pk2(xf[0] * s, xf[1] * s));
-    const uint32_t p1 = __builtin_bit_cast(uint32_t, pk2(xf[2] * s, xf[3] * s));
-    yn[r][0] = lo_f(p0) * nw[0];
-    yn[r][1] = hi_f(p0) * nw[1];
-    yn[r][2] = lo_f(p1) * nw[2];
-    yn[r][3] = hi_f(p1) * nw[3];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) yn[r][j] = xf[j] * s * nw[j];
     if (r >= 3) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) q[r - 3][j] = pk2(yn[r - 3][j], yn[r][j]);
@@ -466,41 +473,48 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
   }
 }
 
+template <bool FUSED>
+int rmsnorm_launch(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps, void* out,
+                          hipStream_t s) {
+  dim3 grid(static_cast<unsigned>(cdiv(rows, 4)));
+  if (dtype == LNG_BF16 && dim % 512 == 0 && dim <= 2048) {
+    const bf16* xp = static_cast<const bf16*>(x);
+    const bf16* wp = static_cast<const bf16*>(w);
+    bf16* op = static_cast<bf16*>(out);
+    if (dim == 512)
+      hipLaunchKernelGGL((k_rmsnorm_bf16_vec<1, FUSED>), grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    else if (dim == 1024)
+      hipLaunchKernelGGL((k_rmsnorm_bf16_vec<2, FUSED>), grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    else if (dim == 1536)
+      hipLaunchKernelGGL((k_rmsnorm_bf16_vec<3, FUSED>), grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    else
+      hipLaunchKernelGGL((k_rmsnorm_bf16_vec<4, FUSED>), grid, dim3(256), 0, s, xp, wp, rows, eps, op);
+    return check_launch("rmsnorm_bf16_vec");
+  }
+  if (dtype == LNG_F32)
+    hipLaunchKernelGGL((k_rmsnorm<float, FUSED>), grid, dim3(256), 0, s, static_cast<const float*>(x),
+                       static_cast<const float*>(w), rows, dim, eps, static_cast<float*>(out));
+  else if (dtype == LNG_BF16)
+    hipLaunchKernelGGL((k_rmsnorm<bf16, FUSED>), grid, dim3(256), 0, s, static_cast<const bf16*>(x),
+                       static_cast<const bf16*>(w), rows, dim, eps, static_cast<bf16*>(out));
+  else
+    return fail(LNG_E_DTYPE, "rmsnorm: dtype must be f32 or bf16");
+  return check_launch("rmsnorm");
+}
+
 }  // namespace lng
 
 using namespace lng;
 
 extern "C" {
 
-int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps, void* out,
-                void* stream) {
+int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps, int32_t mode,
+                void* out, void* stream) {
   if (rows < 0 || dim <= 0) return fail(LNG_E_ARG, "rmsnorm: bad shape");
+  if (mode != LNG_NORM_MODEL && mode != LNG_NORM_FUSED) return fail(LNG_E_ARG, "rmsnorm: unknown rounding mode");
   if (rows == 0) return LNG_OK;
-  dim3 grid(static_cast<unsigned>(cdiv(rows, 4)));
-  hipStream_t s = as_stream(stream);
-  if (dtype == LNG_BF16 && dim % 512 == 0 && dim <= 2048) {
-    const bf16* xp = static_cast<const bf16*>(x);
-    const bf16* wp = static_cast<const bf16*>(w);
-    bf16* op = static_cast<bf16*>(out);
-    if (dim == 512)
-      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<1>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
-    else if (dim == 1024)
-      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<2>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
-    else if (dim == 1536)
-      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<3>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
-    else
-      hipLaunchKernelGGL(k_rmsnorm_bf16_vec<4>, grid, dim3(256), 0, s, xp, wp, rows, eps, op);
-    return check_launch("rmsnorm_bf16_vec");
-  }
-  if (dtype == LNG_F32)
-    hipLaunchKernelGGL(k_rmsnorm<float>, grid, dim3(256), 0, s, static_cast<const float*>(x),
-                       static_cast<const float*>(w), rows, dim, eps, static_cast<float*>(out));
-  else if (dtype == LNG_BF16)
-    hipLaunchKernelGGL(k_rmsnorm<bf16>, grid, dim3(256), 0, s, static_cast<const bf16*>(x), static_cast<const bf16*>(w),
-                       rows, dim, eps, static_cast<bf16*>(out));
-  else
-    return fail(LNG_E_DTYPE, "rmsnorm: dtype must be f32 or bf16");
-  return check_launch("rmsnorm");
+  return mode == LNG_NORM_FUSED ? rmsnorm_launch<true>(x, w, dtype, rows, dim, eps, out, as_stream(stream))
+                                : rmsnorm_launch<false>(x, w, dtype, rows, dim, eps, out, as_stream(stream));
 }
 
 int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_partials, const void* norm_w,

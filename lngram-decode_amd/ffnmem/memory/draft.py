@@ -13,7 +13,8 @@ from torch import Tensor, nn
 
 from lngram_hip import ops
 
-from .lngram_v2 import RMSNorm, RouteNgramMemoryV2
+from ..model import RMSNorm
+from .lngram_v2 import RouteNgramMemoryV2
 
 
 def lookup_rows_at(m: RouteNgramMemoryV2, codes: Tensor, q_logits: Tensor | None, b_idx: Tensor,

@@ -42,8 +42,8 @@ def _normal_init(weight: Tensor, std: float) -> None:
 
 
 class RMSNorm(nn.Module):
-    """RMSNorm (``lngram_v2.py:36-53``): normalise in fp32, round to the input dtype,
-    multiply by ``weight``.  Runs ``lng_rmsnorm``."""
+    """RMSNorm (``lngram_v2.py:36-53``): ``F.rms_norm`` semantics, the row normalised and
+    multiplied by ``weight`` in fp32 and rounded once to the input dtype.  Runs ``lng_rmsnorm``."""
 
     def __init__(self, hidden_size: int, eps: float = 1e-6, device=None, dtype=None):
         super().__init__()
@@ -54,7 +54,7 @@ class RMSNorm(nn.Module):
     def forward(self, hidden_states: Tensor) -> Tensor:
         if hidden_states.shape[-1] != self.hidden_size:
             raise ValueError(f"RMSNorm expects last dim {self.hidden_size}, got {hidden_states.shape[-1]}")
-        return ops.rmsnorm(hidden_states, self.weight, self.eps)
+        return ops.rmsnorm(hidden_states, self.weight, self.eps, fused=True)
 
 
 def build_lngram_norm(normalization: str, hidden_size: int, eps: float, device=None, dtype=None) -> nn.Module:

@@ -13,7 +13,7 @@ from torch import Tensor, nn
 
 from lngram_hip import ops
 
-from .lngram_v2 import RMSNorm
+from ..model import RMSNorm
 
 ROUTER_INPUTS = ("hidden", "embed2", "embed2_ssm")
 

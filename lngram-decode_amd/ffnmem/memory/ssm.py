@@ -18,7 +18,7 @@ from torch import Tensor, nn
 
 from lngram_hip import ops
 
-from .lngram_v2 import RMSNorm
+from ..model import RMSNorm
 
 
 class DiagonalSSM(nn.Module):

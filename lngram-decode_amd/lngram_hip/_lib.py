@@ -27,6 +27,7 @@ _P64 = ctypes.POINTER(ctypes.c_int64)
 _P32 = ctypes.POINTER(ctypes.c_int32)
 
 ROW_NONE = -2147483648  # LNG_ROW_NONE
+NORM_MODEL, NORM_FUSED = 0, 1  # LNG_NORM_MODEL / LNG_NORM_FUSED
 DR_SYNC_INTS = 4160  # LNG_DR_SYNC_INTS
 TREE_SYNC_BYTES = 16640  # LNG_DR_TREE_SYNC_BYTES: error word (offset 0) + counters of the one-launch tree
 READOUT_PACK_ELEMS = 131072  # LNG_READOUT_PACK_ELEMS: bf16 elements of the fused readout's packed KV weight
@@ -62,7 +63,7 @@ SIGNATURES = {
     "lng_ngram_rows": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32, _p, _p, _p, _p]),
     "lng_route_tokens": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32,
                                 ctypes.POINTER(_p), _int, _i32, _p, _p, _i32, _p, _p]),
-    "lng_rmsnorm": (_int, [_p, _p, _int, _i64, _i32, _f, _p, _p]),
+    "lng_rmsnorm": (_int, [_p, _p, _int, _i64, _i32, _f, _i32, _p, _p]),
     "lng_linear": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _p]),
     "lng_sink_attention": (_int, [_p, _p, _p, _int, _i64, _i32, _i32, _i32, _i32, _f, _f, _p, _p]),
     "lng_sink_attention_strided": (_int, [_p, _p, _p, _int, _i64, _i32, _i32, _i32, _i32, _P64, _P64,

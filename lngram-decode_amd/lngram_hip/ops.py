@@ -258,13 +258,17 @@ def route_tokens(codes: torch.Tensor, tables, orders, bits: int, route_start: in
 
 
 # ----------------------------------------------------------------------------- K3 pieces
-def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, fused: bool = False) -> torch.Tensor:
+    """RMSNorm over the last dim.  ``fused=False``: ``model.RMSNorm`` (``model.py:39-48``: round the
+    normalised row, multiply by the weight, round); ``fused=True``: ``lngram_v2.RMSNorm``
+    (``lngram_v2.py:36-53``, ``F.rms_norm``: weight applied in fp32, one rounding)."""
     dev = _dev(x, w)
     xc = _c(x)
     wc = _c(w.to(x.dtype))
     out = torch.empty_like(xc)
     d = x.shape[-1]
-    check(lib().lng_rmsnorm(_ptr(xc), _ptr(wc), dtype_code(x.dtype), xc.numel() // d, d, eps, _ptr(out),
+    mode = _lib.NORM_FUSED if fused else _lib.NORM_MODEL
+    check(lib().lng_rmsnorm(_ptr(xc), _ptr(wc), dtype_code(x.dtype), xc.numel() // d, d, eps, mode, _ptr(out),
                             _stream(dev)), "rmsnorm")
     return out
 

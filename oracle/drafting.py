@@ -7,7 +7,9 @@ arithmetic):
   from ``concat(RMSNorm(E[x_{t-1}] or start), RMSNorm(E[x_t])[, s_t])``, v2 n-gram rows,
   ``DraftReadout.hidden`` (memory RMSNorm -> KV projection -> sink softmax over routes ->
   ``W_o`` -> RMSNorm), logits against the tied embedding, top-k by (logit desc, index asc);
-  stateful commit / draft / truncate / trace.  Full-vocab scoring (no sketch shortlist).
+  stateful commit / draft / truncate / trace.  Scoring is over the full vocabulary, or over the
+  count-sketch shortlist of ``cpu_drafter.py:179-206`` when the bundle carries sketches and a
+  positive ``shortlist_cap`` (``sketch_shortlist`` below).
 - code-keyed online counts (``OnlineCounts.mix``, ``drafting/drafters.py:117-142``), applied
   to the drafter's softmax when ``online=True``;
 - the tree structure and verification helpers of ``drafting/tree.py:37-136, :205-257``.
@@ -63,7 +65,7 @@ class DraftOut:
 
 
 class DrafterOracle:
-    """``RefDrafter`` (``cpu_drafter.py:76-289``) without a sketch shortlist, in ``dtype``.
+    """``RefDrafter`` (``cpu_drafter.py:76-289``) in ``dtype``.
 
     ``online=True`` mixes the draft softmax with code-keyed online counts over the committed
     (row at t, token t+1) pairs (``drafters.py:117-142``, ``:193-201``); the ranking is then by
@@ -73,7 +75,7 @@ class DrafterOracle:
     name = "oracle"
 
     def __init__(self, config: dict, tensors: dict, topk: int = 3, dtype=torch.float64, online: bool = False,
-                 kappa: float = 1.0):
+                 kappa: float = 1.0, shortlist_cap: int | None = None):
         c = self.cfg = dict(config)
         self.dtype = dtype
         self.topk = int(topk)
@@ -94,6 +96,15 @@ class DrafterOracle:
         self.q_norm, self.w_q, self.w_o, self.out_norm = t["q_norm"], t["w_q"], t["w_o"], t["out_norm"]
         self.w_sq = t.get("w_sq")
         self.shifts = torch.arange(self.bits, dtype=torch.int32)
+        # count sketches (cpu_drafter.py:99-103): ids / counts per order, fallback tokens, cap
+        self.sk_ids = {n: np.asarray(t[f"sketch_ids_{n}"]).astype(np.int64) for n in self.ngrams
+                       if f"sketch_ids_{n}" in t}
+        self.sk_cnt = {n: np.asarray(t[f"sketch_counts_{n}"]).astype(np.int64) for n in self.sk_ids}
+        fb = t.get("fallback")
+        self.fallback = [] if fb is None else [int(x) for x in np.asarray(fb).ravel()]
+        self.cap = int(c.get("shortlist_cap", 0)) if shortlist_cap is None else int(shortlist_cap)
+        if self.online and self.cap > 0 and self.sk_ids:
+            raise ValueError("online counts mix a full-vocabulary softmax; the shortlist drafter has none")
         self.reset()
 
     # ------------------------------------------------------------------ state (cpu_drafter.py:110-144)
@@ -201,6 +212,24 @@ class DrafterOracle:
     def logits(self, cur: _Cursor) -> torch.Tensor:
         return self.E @ self.hidden(cur)
 
+    # ------------------------------------------------------------------ shortlist (cpu_drafter.py:179-206)
+    def shortlist(self, rows: dict) -> list | None:
+        """The shortlist at the rows of one position, or None for full-vocabulary scoring."""
+        if self.cap <= 0 or not self.sk_ids:
+            return None
+        return sketch_shortlist(self.sk_ids, self.sk_cnt, self.fallback, rows, self.cap)
+
+    def readout(self, cur: _Cursor, full: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+        """(candidate token ids, logits) at the cursor (``cpu_drafter.py:238-244``): the shortlist
+        when there is one (and ``full`` is off), else the whole vocabulary."""
+        rows = self.rows(cur)
+        h = self.hidden(cur, rows)
+        sl = None if full else self.shortlist(rows)
+        if sl is None:
+            return torch.arange(self.V), self.E @ h
+        ids = torch.tensor(sl, dtype=torch.long)
+        return ids, self.E[ids] @ h
+
     # ------------------------------------------------------------------ online counts (drafters.py:117-142)
     def online_mix(self, p: torch.Tensor, cur: _Cursor, n_pairs: int) -> torch.Tensor:
         """``OnlineCounts.mix`` for one query at the cursor, keys = the first ``n_pairs``
@@ -244,9 +273,12 @@ class DrafterOracle:
         lg = np.full((gamma, k), -np.inf, np.float32)
         toks = []
         for i in range(gamma):
-            scores = self.distribution(cur, n_pairs)
+            if self.online:
+                cand, scores = torch.arange(self.V), self.distribution(cur, n_pairs)
+            else:
+                cand, scores = self.readout(cur)
             order = top_order(scores, k)
-            ids[i, :len(order)] = order.numpy()
+            ids[i, :len(order)] = cand[order].numpy()
             lg[i, :len(order)] = scores[order].numpy()
             toks.append(int(ids[i, 0]))
             if i + 1 < gamma or last_codes:
@@ -274,6 +306,51 @@ class DrafterOracle:
         finally:
             self._tokens, self._codes, self._ssm = saved
         return out_c, out_l
+
+
+    def trace_readout(self, tokens, codes=None, full: bool = False):
+        """``RefDrafter.trace`` (``cpu_drafter.py:272-289``): per position (codes [T, R], candidate ids
+        [T, S] (-1 pad), logits [T, S] (-inf pad)), S = vocab if ``full`` or no shortlist, else cap;
+        a position whose shortlist is empty scores the whole vocabulary, cut to S."""
+        tokens = [int(x) for x in tokens]
+        full_vocab = full or self.cap <= 0 or not self.sk_ids
+        s_dim = self.V if full_vocab else self.cap
+        n = len(tokens)
+        out_c = np.zeros((n, self.R), np.uint8)
+        out_i = np.full((n, s_dim), -1, np.int64)
+        out_l = np.full((n, s_dim), -np.inf, np.float64)
+        cur = _Cursor(-1, -1, None, ())
+        for t, tok in enumerate(tokens):
+            cur = self._advance(cur, tok, None if codes is None else np.asarray(codes[t], np.uint8))
+            out_c[t] = cur.hist[-1]
+            ids, lg = self.readout(cur, full)
+            m = min(len(ids), s_dim)
+            out_i[t, :m], out_l[t, :m] = ids[:m].numpy(), lg[:m].double().numpy()
+        return out_c, out_i, out_l
+
+
+def sketch_shortlist(sk_ids: dict, sk_cnt: dict, fallback, rows: dict, cap: int) -> list | None:
+    """The deterministic shortlist of ``RefDrafter._shortlist`` (``cpu_drafter.py:179-206``,
+    ``drafter.cpp:438-474``): the counts of every sketch slot (count > 0) of the position's rows,
+    over orders and routes, summed per token; tokens ordered by (total desc, id asc) and cut to
+    ``cap``; then the ``fallback`` tokens not yet present, in their order, up to ``cap``.  None
+    when that leaves it empty.  ``rows``: order -> int64 [R] global rows, or None before n-1."""
+    total: dict = {}
+    for n, r in rows.items():
+        if r is None or n not in sk_ids:
+            continue
+        for tok, cnt in zip(sk_ids[n][r].ravel().tolist(), sk_cnt[n][r].ravel().tolist()):
+            if cnt > 0:
+                total[tok] = total.get(tok, 0) + cnt
+    out = sorted(total, key=lambda v: (-total[v], v))[:cap]
+    seen = set(out)
+    for f in fallback:
+        if len(out) >= cap:
+            break
+        if f not in seen:
+            out.append(f)
+            seen.add(f)
+    return out or None
 
 
 # ----------------------------------------------------------------------------- rows helpers

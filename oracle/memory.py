@@ -231,16 +231,23 @@ def gather_sum_rows_torch(tables, rows: np.ndarray) -> torch.Tensor:
 
 # ----------------------------------------------------------------------------- float parts
 def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """RMSNorm as the reference rounds it: normalise in fp32 (fp64 for fp64 input),
-    round to the input dtype, then multiply by the weight in that dtype.
-
-    Covers both ``lngram_v2.RMSNorm`` (``F.rms_norm``, ``lngram_v2.py:36-53``) and
-    ``model.RMSNorm`` (``model.py:39-48``), which round identically.
-    """
+    """``model.RMSNorm`` (``model.py:39-48``), the norm of ``h_norm`` and of the token router
+    features: normalise in fp32 (fp64 for fp64 input), round to the input dtype, then multiply
+    by the weight in that dtype (two roundings for bf16)."""
     work = torch.float64 if x.dtype == torch.float64 else torch.float32
     xf = x.to(work)
     y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
     return y.to(x.dtype) * w.to(x.dtype)
+
+
+def rms_norm_v2(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """``lngram_v2.RMSNorm`` (``lngram_v2.py:36-53``), the memory module's query, memory and
+    short-conv norms: ``F.rms_norm``, which normalises and applies the weight in fp32 and rounds
+    once to the input dtype (fp64 stays fp64)."""
+    work = torch.float64 if x.dtype == torch.float64 else torch.float32
+    xf = x.to(work)
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.to(x.dtype).to(work)
+    return y.to(x.dtype)
 
 
 def rms_norm_fp32(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -265,7 +272,7 @@ def _p(params: dict, key: str, dtype) -> torch.Tensor:
 def project_query(params: dict, cfg: MemCfg, h: torch.Tensor) -> torch.Tensor:
     """``_project_query`` (``lngram_v2.py:1115-1118``): ``W_q RMSNorm(h)`` -> [B, T, H, hd]."""
     dt = h.dtype
-    x = rms_norm(h, _p(params, "readout_query_norm.weight", dt), cfg.eps)
+    x = rms_norm_v2(h, _p(params, "readout_query_norm.weight", dt), cfg.eps)
     q = F.linear(x, _p(params, "readout_q_proj.weight", dt))
     return q.view(*h.shape[:-1], cfg.q_heads, cfg.head_dim)
 
@@ -274,7 +281,7 @@ def project_memory(params: dict, cfg: MemCfg, tokens: torch.Tensor):
     """``_project_memory`` (``lngram_v2.py:1120-1131``): memory RMSNorm over Dt, KV
     projection, split keys first, reshape to ``[B, T, KV, R, hd]`` each."""
     dt = tokens.dtype
-    x = rms_norm(tokens, _p(params, "readout_memory_norm.weight", dt), cfg.eps)
+    x = rms_norm_v2(tokens, _p(params, "readout_memory_norm.weight", dt), cfg.eps)
     kv = F.linear(x, _p(params, "readout_kv_proj.weight", dt))
     kh = cfg.kv_heads * cfg.head_dim
     key, value = kv[..., :kh], kv[..., kh:]
@@ -303,7 +310,7 @@ def causal_conv(params: dict, cfg: MemCfg, mixed: torch.Tensor, segment_ids=None
     left padding ``(K-1)*dil``, no bias.  Tap j reads lag ``(K-1-j)*dil`` (Conv1d stores
     taps oldest -> newest)."""
     dt = mixed.dtype
-    x = rms_norm(mixed, _p(params, "short_conv.norm.weight", dt), cfg.eps)
+    x = rms_norm_v2(mixed, _p(params, "short_conv.norm.weight", dt), cfg.eps)
     w = _p(params, "short_conv.conv.weight", dt)  # [d, 1, K]
     k, dil = cfg.conv_kernel, cfg.conv_dilation
     if segment_ids is None:

@@ -1,0 +1,114 @@
+"""Seeded inputs and parameters shared by the golden-fixture generator and the tests that read
+the fixtures (test infrastructure only).
+
+Every array is drawn from numpy's legacy ``RandomState``, whose streams are fixed across numpy
+versions, with a seed derived from the array's name.  A fixture therefore stores only the
+outputs that the reference computed (plus small integer inputs); the tests rebuild the
+floating-point inputs and parameters here and hand them to the oracle.
+
+Parameter rules (by state-dict key or bundle array name):
+
+- norm weights (``*norm*``) and the SSM decay are drawn around their natural values
+  (``1 + 0.1 N(0,1)`` and ``U[0.6, 0.99]``), so a swapped or dropped weight shows;
+- the short-conv weight is ``N(0, 0.2)``; every other weight, table and the start vector is
+  ``N(0, 0.02)``, drawn in fp32 and cast afterwards, like the reference's ``_normal_init``.
+"""
+
+from __future__ import annotations
+
+import zlib
+
+import numpy as np
+
+
+def _seed(name: str, base: int) -> int:
+    return (zlib.crc32(name.encode()) ^ (base * 0x9E3779B1)) & 0x7FFFFFFF
+
+
+def normal(name: str, shape, std: float = 1.0, mean: float = 0.0, base: int = 0) -> np.ndarray:
+    rs = np.random.RandomState(_seed(name, base))
+    return (mean + std * rs.standard_normal(tuple(shape))).astype(np.float32)
+
+
+def uniform(name: str, shape, lo: float, hi: float, base: int = 0) -> np.ndarray:
+    rs = np.random.RandomState(_seed(name, base))
+    return rs.uniform(lo, hi, tuple(shape)).astype(np.float32)
+
+
+def integers(name: str, shape, lo: int, hi: int, base: int = 0) -> np.ndarray:
+    rs = np.random.RandomState(_seed(name, base))
+    return rs.randint(lo, hi, tuple(shape)).astype(np.int64)
+
+
+def param(name: str, shape, base: int = 0) -> np.ndarray:
+    """One parameter by the rules above (fp32)."""
+    if "norm" in name:
+        return normal(name, shape, 0.1, 1.0, base)
+    if "conv.weight" in name:
+        return normal(name, shape, 0.2, 0.0, base)
+    if name in ("ssm_decay",):
+        return uniform(name, shape, 0.6, 0.99, base)
+    return normal(name, shape, 0.02, 0.0, base)
+
+
+def state(shapes: dict, base: int = 0) -> dict:
+    """A state dict ``{key: fp32 array}`` for ``{key: shape}``."""
+    return {k: param(k, s, base) for k, s in shapes.items()}
+
+
+# ------------------------------------------------------------------ configurations
+# Tiny fp32 memory layer: the C1 widths (d 128, 8 routes, mem_dim 32, 4 query heads x 32, 2 KV heads).
+TINY_MEM = dict(d_model=128, cfg=dict(routes=8, mem_dim=32, head_dim=32, q_heads=4, kv_heads=2))
+# bf16 memory layer at the SB widths (d 1024, mem_dim 128, 16 query heads x 64, 4 KV heads), 32 routes.
+SB_MEM = dict(d_model=1024, cfg=dict(routes=32, mem_dim=128, head_dim=64, q_heads=16, kv_heads=4))
+
+# Tiny drafter bundles (bundle_config keys of drafting/export_drafter.py:212-215).
+_DRAFT_BASE = dict(d_model=64, vocab=96, routes=4, bits=4, ngrams=[2, 3], mem_dim=16, kv_heads=2, head_dim=16,
+                   q_heads=4, norm_eps=1e-5, ssm_eps=1e-5, router_eps=1e-5, draft_eps=1e-5, mem_eps=1e-5,
+                   softmax_scale=0.25, sink_logit=float(np.log(4.0)), table_dtype="fp16", layer=1)
+
+
+def drafter_config(kind: str, sketch_k: int = 0, cap: int = 0) -> dict:
+    """``sdb`` (embed2 router, no SSM) or ``sdc`` (embed2_ssm router, SSM state in the query)."""
+    c = dict(_DRAFT_BASE)
+    if kind == "sdb":
+        c.update(kind="sd_b", router_kind="embed2", ssm_dim=0, query_ssm=False)
+    elif kind == "sdc":
+        c.update(kind="sd_c", router_kind="embed2_ssm", ssm_dim=8, query_ssm=True)
+    else:
+        raise ValueError(kind)
+    c.update(sketch_k=sketch_k, shortlist_cap=cap if sketch_k else 0)
+    c["groups"] = c["q_heads"] // c["kv_heads"]
+    c["route_token_dim"] = len(c["ngrams"]) * c["mem_dim"]
+    return c
+
+
+def drafter_arrays(cfg: dict, base: int = 0) -> dict:
+    """Bundle arrays (``export_drafter.py:15-33`` layout) for ``cfg``: fp32 weights, fp16 tables,
+    uint16 / uint32 sketches and an int32 fallback list when ``sketch_k > 0``."""
+    d, V, R, md = cfg["d_model"], cfg["vocab"], cfg["routes"], cfg["mem_dim"]
+    kh, inner, dt = cfg["kv_heads"] * cfg["head_dim"], cfg["q_heads"] * cfg["head_dim"], cfg["route_token_dim"]
+    n_state = cfg["ssm_dim"]
+    feat = 2 * d + (n_state if cfg["router_kind"] == "embed2_ssm" else 0)
+    shapes = {"embedding": (V, d), "mem_norm": (dt,), "kv_proj": (2 * kh, dt), "router": (R * cfg["bits"], feat),
+              "router_prev_norm": (d,), "router_cur_norm": (d,), "router_start": (d,), "q_norm": (d,),
+              "w_q": (inner, d), "w_o": (d, inner), "out_norm": (d,)}
+    if n_state:
+        shapes.update(ssm_norm=(d,), ssm_w_in=(n_state, d), ssm_decay=(n_state,))
+    if cfg["query_ssm"]:
+        shapes["w_sq"] = (inner, n_state)
+    out = state(shapes, base)
+    # the embedding is the draft query input and the unembedding: unit scale keeps logits O(1)
+    out["embedding"] = normal("embedding", (V, d), 1.0, 0.0, base)
+    for n in cfg["ngrams"]:
+        rows = R * (1 << (cfg["bits"] * n))
+        out[f"table_{n}"] = normal(f"table_{n}", (rows, md), 0.02, 0.0, base).astype(np.float16)
+    k = int(cfg.get("sketch_k", 0))
+    if k:
+        for n in cfg["ngrams"]:
+            rows = R * (1 << (cfg["bits"] * n))
+            out[f"sketch_ids_{n}"] = integers(f"sketch_ids_{n}", (rows, k), 0, V, base).astype(np.uint16)
+            cnt = integers(f"sketch_counts_{n}", (rows, k), 0, 4, base)
+            out[f"sketch_counts_{n}"] = cnt.astype(np.uint32)   # count 0 = empty slot
+        out["fallback"] = integers("fallback", (12,), 0, V, base).astype(np.int32)
+    return out

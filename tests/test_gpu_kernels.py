@@ -139,15 +139,22 @@ def test_router_codes_two_bit_routes_large(dev):
 
 # ----------------------------------------------------------------------------- K3 pieces
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_rmsnorm(dev, dtype):
-    x = torch.randn(33, 1024).to(dtype)
-    w = (1 + 0.1 * torch.randn(1024)).to(dtype)
-    got = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5).cpu()
-    want = om.rms_norm(x, w, 1e-5)
+@pytest.mark.parametrize("fused", [False, True])
+@pytest.mark.parametrize("dim", [1024, 200])
+def test_rmsnorm(dev, dtype, fused, dim):
+    # model.RMSNorm (two roundings) and lngram_v2.RMSNorm (F.rms_norm, one rounding): the golden
+    # fixtures pin both oracle forms to the reference; the kernel may differ from them only where
+    # its sum of squares (another summation order) moves a value across a rounding boundary
+    x = torch.randn(33, dim).to(dtype)
+    w = (1 + 0.1 * torch.randn(dim)).to(dtype)
+    got = ops.rmsnorm(x.to(dev), w.to(dev), 1e-5, fused=fused).cpu()
+    want = (om.rms_norm_v2 if fused else om.rms_norm)(x, w, 1e-5)
     if dtype == torch.float32:
         torch.testing.assert_close(got, want, rtol=1e-6, atol=1e-6)
-    else:  # one bf16 rounding step apart at most
-        assert (got.float() - want.float()).abs().max() <= 2 ** -7 * want.float().abs().max()
+    else:
+        diff = (got.float() - want.float()).abs()
+        assert diff.max() <= 2 ** -7 * want.float().abs().max()
+        assert (diff > 0).float().mean() < 0.01
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 1e-2)])
@@ -196,6 +203,8 @@ def test_causal_conv(dev, dtype, tol):
     got = ops.causal_conv(mixed.to(dev), p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev),
                           3, cfg.eps).cpu()
     assert om.rel_err(got, want) < tol and om.rel_err(got, ref64) < tol
+    # the reference's rounding sequence (F.rms_norm, one rounding), not just its tolerance
+    assert om.rel_err(got, want) < tol / 10
     got2 = ops.causal_conv(mixed.to(dev), p["short_conv.norm.weight"].to(dev), p["short_conv.conv.weight"].to(dev),
                            3, cfg.eps, residual=False).cpu()
     assert om.rel_err(got2, ref64 - mixed.double()) < tol
