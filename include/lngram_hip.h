@@ -66,14 +66,26 @@ int lng_router_features(const void* emb, int dtype, const int64_t* token_ids, in
 int lng_ngram_address(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R,
                       int32_t order, int32_t bits, void* out, int out_dtype, void* stream);
 
-/* rows[B, T, route_end-route_start, n_orders] (int32): global table row of each
- * order-n n-gram ending at t, or -1 where _lookup_route_chunk masks it to zero
- * (lngram_v2.py:1047-1092, _valid_mask :1027-1045).  segment_ids [B,T] int32 and
- * valid_tokens [B,T] uint8 may be null. */
+/* rows[B, T, route_end-route_start, n_orders] (rows_dtype LNG_I32 or LNG_I64): global
+ * table row of each order-n n-gram ending at t, or -1 where _lookup_route_chunk masks it
+ * to zero (lngram_v2.py:1047-1092, _valid_mask :1027-1045).  segment_ids [B,T] int32 and
+ * valid_tokens [B,T] uint8 may be null.  int32 rows return LNG_E_RANGE when R * 2^(bits*n)
+ * exceeds int32, where the reference's index_dtype becomes int64 (lngram_v2.py:951-959). */
 int lng_ngram_rows(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R,
                    int32_t route_start, int32_t route_end, const int32_t* orders, int32_t n_orders,
                    int32_t bits, const int32_t* segment_ids, const uint8_t* valid_tokens,
-                   int32_t* rows, void* stream);
+                   void* rows, int rows_dtype, void* stream);
+
+/* Code-keyed online counts mixed into a batch of next-token distributions
+ * (OnlineCounts.mix, drafting/drafters.py:117-142).  keys[T, R, n_orders]: rows of the
+ * committed pairs t (row at t, token nxt[t] = x[t+1]; -1 where t < n-1); q[N, R, n_orders]:
+ * the query windows' rows (-1 = invalid); pair t counts for query j iff t <= deadline[j].
+ * out[N, V] = (1-lam) p + lam * sc / max(tot, 1e-9), lam = n_eff/(n_eff+kappa),
+ * n_eff = tot / (R n_orders).  w_work holds N*T floats.  The count term is added with
+ * atomics, so its summation order (not its value) varies between calls. */
+int lng_online_mix(const int32_t* keys, const int64_t* nxt, int32_t T, const int32_t* q,
+                   const int64_t* deadline, int32_t N, int32_t R, int32_t n_orders, const float* p,
+                   int64_t V, float kappa, float* w_work, float* out, void* stream);
 
 /* ---------------------------------------------------------------- K3: gather / readout */
 /* Route tokens out[B, T_out, route_end-route_start, n_orders*mem_dim] in the

@@ -85,8 +85,9 @@ struct OrderList {
   int32_t v[8];
 };
 
+template <typename RowT>
 __global__ void k_ngram_rows(CodeView codes, int64_t B, int64_t T, int32_t R, int32_t rs, int32_t re, OrderList ords,
-                             int32_t bits, const int32_t* seg, const uint8_t* valid, int32_t* __restrict__ rows) {
+                             int32_t bits, const int32_t* seg, const uint8_t* valid, RowT* __restrict__ rows) {
   const int32_t rw = re - rs;
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= B * T * rw * ords.n) return;
@@ -94,7 +95,7 @@ __global__ void k_ngram_rows(CodeView codes, int64_t B, int64_t T, int32_t R, in
   const int32_t r = rs + static_cast<int32_t>((i / ords.n) % rw);
   const int64_t bt = i / (static_cast<int64_t>(ords.n) * rw);
   const int64_t t = bt % T, b = bt / T;
-  rows[i] = static_cast<int32_t>(ngram_row(codes, T, R, b, t, r, ords.v[oi], bits, seg, valid));
+  rows[i] = static_cast<RowT>(ngram_row(codes, T, R, b, t, r, ords.v[oi], bits, seg, valid));
 }
 
 // One thread copies one `vec`-byte piece of an output route token.  Output
@@ -153,7 +154,7 @@ using namespace lng;
 
 extern "C" {
 
-int lng_abi_version(void) { return 1; }
+int lng_abi_version(void) { return 2; }
 
 const char* lng_last_error(void) { return g_last_error.c_str(); }
 
@@ -194,17 +195,29 @@ static int make_orders(const int32_t* orders, int32_t n_orders, int32_t bits, Or
 
 int lng_ngram_rows(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R, int32_t route_start,
                    int32_t route_end, const int32_t* orders, int32_t n_orders, int32_t bits,
-                   const int32_t* segment_ids, const uint8_t* valid_tokens, int32_t* rows, void* stream) {
+                   const int32_t* segment_ids, const uint8_t* valid_tokens, void* rows, int rows_dtype,
+                   void* stream) {
   if (!code_dtype_ok(codes_dtype)) return fail(LNG_E_DTYPE, "ngram_rows: codes dtype");
+  if (rows_dtype != LNG_I32 && rows_dtype != LNG_I64) return fail(LNG_E_DTYPE, "ngram_rows: rows i32/i64");
   if (B < 0 || T < 0 || R <= 0 || route_start < 0 || route_end > R || route_start > route_end || bits <= 0)
     return fail(LNG_E_ARG, "ngram_rows: bad shape");
   OrderList ol;
   if (int rc = make_orders(orders, n_orders, bits, &ol)) return rc;
+  // the largest row is R * 2^(bits * n) - 1 (lngram_v2.py:951-959 switches to int64 past int32)
+  if (rows_dtype == LNG_I32)
+    for (int i = 0; i < n_orders; ++i)
+      if ((static_cast<int64_t>(R) << (bits * orders[i])) - 1 > INT32_MAX)
+        return fail(LNG_E_RANGE, "ngram_rows: rows exceed int32 at this route count and order; ask for int64 rows");
   const int64_t n = B * T * (route_end - route_start) * n_orders;
   if (n == 0) return LNG_OK;
-  hipLaunchKernelGGL(k_ngram_rows, dim3(cdiv(n, 256)), dim3(256), 0, as_stream(stream),
-                     CodeView{codes, codes_dtype}, B, T, R, route_start, route_end, ol, bits, segment_ids,
-                     valid_tokens, rows);
+  if (rows_dtype == LNG_I32)
+    hipLaunchKernelGGL(k_ngram_rows<int32_t>, dim3(cdiv(n, 256)), dim3(256), 0, as_stream(stream),
+                       CodeView{codes, codes_dtype}, B, T, R, route_start, route_end, ol, bits, segment_ids,
+                       valid_tokens, static_cast<int32_t*>(rows));
+  else
+    hipLaunchKernelGGL(k_ngram_rows<int64_t>, dim3(cdiv(n, 256)), dim3(256), 0, as_stream(stream),
+                       CodeView{codes, codes_dtype}, B, T, R, route_start, route_end, ol, bits, segment_ids,
+                       valid_tokens, static_cast<int64_t*>(rows));
   return check_launch("ngram_rows");
 }
 

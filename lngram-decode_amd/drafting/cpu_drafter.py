@@ -1,6 +1,7 @@
 """Drafter API entry points (``drafting/cpu_drafter.py`` of the reference): ``DraftOut`` and
-``make_drafter``.  On this path every drafter runs on the GPU (``GpuDrafter``); the reference's
-CPU implementations (``RefDrafter`` in PyTorch, ``CppDrafter`` in C++) are not part of it."""
+``make_drafter``.  On this path every drafter runs on the GPU (``GpuDrafter``), whichever
+implementation a caller asks for; the reference's CPU implementations (``RefDrafter`` in PyTorch,
+``CppDrafter`` in C++) are not part of it."""
 
 from __future__ import annotations
 
@@ -25,9 +26,12 @@ class DraftOut:
 
 
 def make_drafter(bundle, impl: str = "auto", **kw):
-    """``make_drafter`` (``cpu_drafter.py:392-397``): ``impl`` gpu | auto -> ``GpuDrafter``."""
-    if impl not in ("gpu", "auto"):
-        raise NotImplementedError(f"impl={impl!r}: the MI355X path provides the GPU drafter only (impl='gpu')")
+    """``make_drafter`` (``cpu_drafter.py:392-397``).  Every ``impl`` the reference accepts -- ``ref``
+    (its PyTorch drafter), ``cpp`` (its C++ drafter), ``auto`` -- and ``gpu`` build the GPU drafter,
+    which has the same API and results; ``threads`` (the C++ drafter's worker count) has no
+    meaning on the GPU and is dropped."""
+    if impl not in ("ref", "cpp", "auto", "gpu"):
+        raise ValueError(f"impl must be ref | cpp | auto | gpu, got {impl!r}")
     kw.pop("threads", None)
     from .gpu_drafter import GpuDrafter
 

@@ -9,6 +9,7 @@ over the R routes, ``W_o`` -> RMSNorm, and logits against the tied embedding
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 from torch import Tensor, nn
 
 from lngram_hip import ops
@@ -20,18 +21,17 @@ from .lngram_v2 import RouteNgramMemoryV2
 def lookup_rows_at(m: RouteNgramMemoryV2, codes: Tensor, q_logits: Tensor | None, b_idx: Tensor,
                    t_idx: Tensor) -> Tensor:
     """Route tokens ``[N, R, len(ngrams)*mem_dim]`` of the n-grams ending at ``(b_idx[i], t_idx[i])``
-    (``draft.py:26-47``): a ``route_history_length + 1`` code window per position, positions
-    before the sequence start as their own segment (so n-grams crossing t = 0 are zero)."""
+    (``draft.py:26-47``), equal to the full lookup at those positions.  The codes are padded with
+    ``route_history_length`` slots before position 0; each position's window is the slice of the
+    padded sequence that ends at it, and the pad slots are not real, so an n-gram that reaches
+    before the sequence start reads the zero row.  ``q_logits`` (the training surrogate's input) is
+    not used in eval."""
+    from drafting.drafters import window_route_tokens
+
     hist = m.route_history_length
-    offs = torch.arange(hist + 1, device=codes.device)
-    win_t = t_idx[:, None] - hist + offs[None, :]
-    real = win_t >= 0
-    win_t = win_t.clamp_min(0)
-    win_codes = codes[b_idx[:, None], win_t] * real[..., None].to(codes.dtype)
-    seg = real.to(torch.int32)
-    tokens = ops.route_tokens(win_codes, [m.tables[f"ngram_{n}"].weight for n in m.ngrams], m.ngrams,
-                              m.bits_per_route, 0, m.num_routes, seg, None, 1)
-    return tokens[:, -1]
+    padded = F.pad(codes, (0, 0, hist, 0))                     # slot hist + t holds position t
+    span = t_idx[:, None] + torch.arange(hist + 1, device=codes.device)[None, :]
+    return window_route_tokens(m, padded[b_idx[:, None], span], span >= hist)
 
 
 class DraftReadout(nn.Module):

@@ -44,38 +44,38 @@ class TokenRouterFeatures(nn.Module):
         self.start = nn.Parameter(torch.empty(d_model))
         nn.init.normal_(self.start, mean=0.0, std=init_std)
 
-    def forward(self, emb: Tensor, ssm_state: Tensor | None = None) -> Tensor:
-        """emb ``[B, T, d]``; ssm_state ``[B, T, N]`` for ``embed2_ssm``."""
+    def _features(self, emb: Tensor, ssm_state: Tensor | None, token_ids: Tensor | None = None) -> Tensor:
         if self.kind == "embed2_ssm" and ssm_state is None:
             raise ValueError("embed2_ssm router needs the SSM state")
         s = ssm_state if self.kind == "embed2_ssm" else None
         n = 0 if s is None else s.shape[-1]
-        if ops.router_features_ok(emb.shape[-1], n, emb.dtype):
-            return ops.router_features(emb, self.start, self.prev_norm.weight, self.cur_norm.weight, self.prev_norm.eps,
-                                       ssm_state=s)
-        b = emb.shape[0]
-        prev = torch.cat((self.start.to(emb.dtype).expand(b, 1, -1), emb[:, :-1]), dim=1)
-        parts = [self.prev_norm(prev), self.cur_norm(emb)]
-        if s is not None:
-            parts.append(s.to(parts[0].dtype))
-        return torch.cat(parts, dim=-1)
+        if not ops.router_features_ok(emb.shape[-1], n, emb.dtype):
+            raise NotImplementedError(f"lng_router_features takes fp32/bf16 features whose rows are 16-byte "
+                                      f"multiples up to 8 KB (d={emb.shape[-1]}, state {n}, {emb.dtype})")
+        return ops.router_features(emb, self.start, self.prev_norm.weight, self.cur_norm.weight, self.prev_norm.eps,
+                                   ssm_state=s, token_ids=token_ids)
+
+    def forward(self, emb: Tensor, ssm_state: Tensor | None = None) -> Tensor:
+        """emb ``[B, T, d]``; ssm_state ``[B, T, N]`` for ``embed2_ssm`` -> ``[B, T, 2d (+ N)]``, one
+        ``lng_router_features`` launch."""
+        return self._features(emb, ssm_state)
 
     def from_ids(self, token_ids: Tensor, table: Tensor, ssm_state: Tensor | None = None) -> Tensor:
         """``forward(table[token_ids], ssm_state)`` with the embedding gather fused into the kernel
         (not in the reference module: the model gathers ``emb`` itself)."""
-        if self.kind == "embed2_ssm" and ssm_state is None:
-            raise ValueError("embed2_ssm router needs the SSM state")
-        return ops.router_features(table, self.start, self.prev_norm.weight, self.cur_norm.weight, self.prev_norm.eps,
-                                   ssm_state=ssm_state if self.kind == "embed2_ssm" else None, token_ids=token_ids)
+        return self._features(table, ssm_state, token_ids)
 
     def step(self, emb_prev: Tensor | None, emb_cur: Tensor, ssm_state: Tensor | None = None) -> Tensor:
-        """One position (decode / drafter): ``emb_prev`` None at t = 0."""
-        if emb_prev is None:
-            emb_prev = self.start.to(emb_cur.dtype).expand_as(emb_cur)
-        parts = [self.prev_norm(emb_prev), self.cur_norm(emb_cur)]
+        """One position (decode / drafter), ``[B, d]`` inputs; ``emb_prev`` None at t = 0.  The kernel
+        runs on the two-position sequence (previous, current) and the last position is kept: its
+        previous-token half reads ``emb_prev`` (at t = 0 the one-position sequence reads ``start``)."""
+        seq = emb_cur[:, None] if emb_prev is None else torch.stack((emb_prev.to(emb_cur.dtype), emb_cur), 1)
+        s = None
         if self.kind == "embed2_ssm":
-            parts.append(ssm_state.to(parts[0].dtype))
-        return torch.cat(parts, dim=-1)
+            if ssm_state is None:
+                raise ValueError("embed2_ssm router needs the SSM state")
+            s = ssm_state[:, None].expand(-1, seq.shape[1], -1)
+        return self._features(seq, s)[:, -1]
 
 
 class TokenRouter(nn.Module):

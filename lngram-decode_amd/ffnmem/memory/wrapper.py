@@ -166,13 +166,3 @@ class LngramMemory(nn.Module):
     def active_table_params_per_token(self) -> int:
         return self.routes * len(self.module.ngrams) * self.module.memory_dim
 
-
-def param_group_of(name: str, param: nn.Parameter) -> str:
-    """Optimizer group of a full-model parameter name (``wrapper.py:241-254``)."""
-    if ".memory.module.tables." in name or ".memory.rank1_tables." in name:
-        return "tables"
-    if ".memory.router." in name or ".memory.token_router.proj." in name:
-        return "router"
-    if param.ndim < 2:
-        return "no_decay"
-    return "decay"

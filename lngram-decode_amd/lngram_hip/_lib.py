@@ -60,7 +60,8 @@ SIGNATURES = {
     "lng_pack_route_codes": (_int, [_p, _i64, _i64, _i32, _p, _int, _p]),
     "lng_router_features": (_int, [_p, _int, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _f, _p, _i32, _p, _p]),
     "lng_ngram_address": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _p, _int, _p]),
-    "lng_ngram_rows": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32, _p, _p, _p, _p]),
+    "lng_ngram_rows": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32, _p, _p, _p, _int, _p]),
+    "lng_online_mix": (_int, [_p, _p, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _f, _p, _p, _p]),
     "lng_route_tokens": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32,
                                 ctypes.POINTER(_p), _int, _i32, _p, _p, _i32, _p, _p]),
     "lng_rmsnorm": (_int, [_p, _p, _int, _i64, _i32, _f, _i32, _p, _p]),

@@ -221,16 +221,41 @@ def _seg(segment_ids, valid_tokens):
 
 
 def ngram_rows(codes: torch.Tensor, orders, bits: int, route_start: int = 0, route_end: int | None = None,
-               segment_ids=None, valid_tokens=None) -> torch.Tensor:
-    """int32 ``[B, T, route_end-route_start, len(orders)]``, -1 where the row is masked."""
+               segment_ids=None, valid_tokens=None, rows_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """``[B, T, route_end-route_start, len(orders)]`` global rows, -1 where the row is masked.
+    int32 unless the largest row needs int64 (the reference's ``index_dtype``,
+    ``lngram_v2.py:951-959``) or ``rows_dtype`` asks for int64."""
     dev = _dev(codes, segment_ids, valid_tokens)
     b, t, r = codes.shape
     route_end = r if route_end is None else route_end
+    if rows_dtype is None:
+        wide = any(r * (1 << (bits * int(n))) - 1 > 2 ** 31 - 1 for n in orders)
+        rows_dtype = torch.int64 if wide else torch.int32
     cc = _codes_ok(codes)
     seg, val = _seg(segment_ids, valid_tokens)
-    out = torch.empty(b, t, route_end - route_start, len(orders), dtype=torch.int32, device=dev)
+    out = torch.empty(b, t, route_end - route_start, len(orders), dtype=rows_dtype, device=dev)
     check(lib().lng_ngram_rows(_ptr(cc), dtype_code(cc.dtype), b, t, r, route_start, route_end, _orders(orders),
-                               len(orders), bits, _ptr(seg), _ptr(val), _ptr(out), _stream(dev)), "ngram_rows")
+                               len(orders), bits, _ptr(seg), _ptr(val), _ptr(out), dtype_code(rows_dtype),
+                               _stream(dev)), "ngram_rows")
+    return out
+
+
+def online_mix(keys: torch.Tensor, nxt: torch.Tensor, q: torch.Tensor, deadline: torch.Tensor, p: torch.Tensor,
+               kappa: float = 1.0) -> torch.Tensor:
+    """``OnlineCounts.mix`` (``drafting/drafters.py:117-142``): keys ``[T, R, n_orders]`` int32 rows of
+    the committed pairs, ``nxt [T]`` their next tokens, q ``[N, R, n_orders]`` int32 query rows,
+    ``deadline [N]``, p ``[N, V]`` fp32 -> the mixed ``[N, V]`` fp32."""
+    dev = _dev(keys, nxt, q, deadline, p)
+    t, r, no = keys.shape
+    n, v = p.shape
+    if q.shape != (n, r, no) or nxt.shape != (t,) or deadline.shape != (n,):
+        raise ValueError("online_mix: keys [T, R, n], nxt [T], q [N, R, n], deadline [N], p [N, V]")
+    kc, qc = _c(keys.to(torch.int32)), _c(q.to(torch.int32))
+    xc, dc, pc = _c(nxt.to(torch.int64)), _c(deadline.to(torch.int64)), _c(p.to(torch.float32))
+    work = torch.empty(max(n * t, 1), dtype=torch.float32, device=dev)
+    out = torch.empty(n, v, dtype=torch.float32, device=dev)
+    check(lib().lng_online_mix(_ptr(kc), _ptr(xc), t, _ptr(qc), _ptr(dc), n, r, no, _ptr(pc), v, float(kappa),
+                               _ptr(work), _ptr(out), _stream(dev)), "online_mix")
     return out
 
 

@@ -53,15 +53,22 @@ def test_every_declared_symbol_is_exported_and_bound(lib):
 
 
 def test_version_and_argument_errors(lib):
-    assert lib.lng_abi_version() == 1
+    assert lib.lng_abi_version() == 2
     # rejected before any GPU work: negative M
     rc = lib.lng_linear(None, None, 0, -1, 4, 4, None, None)
     assert rc == -1
     assert b"linear" in lib.lng_last_error()
     rc = lib.lng_pack_route_codes(None, 4, 7, 4, None, 3, None)  # C not divisible by bits
     assert rc == -1
-    rc = lib.lng_ngram_rows(None, 9, 1, 1, 1, 0, 1, (ctypes.c_int32 * 1)(2), 1, 4, None, None, None, None)
+    rc = lib.lng_ngram_rows(None, 9, 1, 1, 1, 0, 1, (ctypes.c_int32 * 1)(2), 1, 4, None, None, None, 4, None)
     assert rc == -2  # bad codes dtype
+    # int32 rows past the int32 range are refused: 130 routes x 2^(8*3) rows
+    rc = lib.lng_ngram_rows(None, 3, 1, 1, 130, 0, 130, (ctypes.c_int32 * 1)(3), 1, 8, None, None, None, 4, None)
+    assert rc == -4 and b"int32" in lib.lng_last_error()
+    rc = lib.lng_rmsnorm(None, None, 0, 1, 8, 1e-5, 7, None, None)
+    assert rc == -1 and b"rounding" in lib.lng_last_error()
+    rc = lib.lng_online_mix(None, None, 4, None, None, 1, 2, 2, None, 10, 0.0, None, None, None)
+    assert rc == -1 and b"kappa" in lib.lng_last_error()
     rc = lib.lng_route_tokens(None, 3, 1, 4, 2, 0, 2, (ctypes.c_int32 * 1)(2), 1, 4, None, 1, 8, None, None, 9,
                               None, None)
     assert rc == -1 and b"target_length" in lib.lng_last_error()

@@ -2,9 +2,9 @@
 
 Route codes are compared bit-exactly outside the near-tie band |router logit| < 2e-5 (the oracle's
 fp64 logits decide which entries are ties); readouts are compared with identical committed codes
-(``commit(tokens, codes=...)``), so a tie cannot leak into the windows.  Logits: absolute error
-<= 1e-4 (the reference's C++-vs-PyTorch drafter tolerance, ``tests/test_live_drafter.py:105-121``);
-draft tokens, top-k ids and tree node tokens: equal.
+(``commit(tokens, codes=...)``), so a tie cannot leak into the windows.  Logits (fp32 on the GPU)
+against the fp64 oracle: norm-relative error < 1e-5, and no entry further than 1e-5 of the largest
+logit magnitude from it; draft tokens, top-k ids and tree node tokens: equal.
 """
 
 from __future__ import annotations
@@ -35,6 +35,16 @@ def _bundle(kind: str, seed: int = 5):
     for k in ("router_prev_norm", "router_cur_norm", "q_norm", "out_norm", "mem_norm"):
         t[k] = (1 + 0.2 * torch.randn(t[k].shape, generator=g)).to(t[k].dtype)
     return cfg, t
+
+
+def _assert_logits(got: np.ndarray, want: np.ndarray, rel: float = 1e-5) -> None:
+    """fp32 logits against fp64: same finite entries, norm-relative and scaled max-abs bounds."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    ok = np.isfinite(want)
+    assert (np.isfinite(got) == ok).all()
+    d, w = got[ok] - want[ok], want[ok]
+    assert np.linalg.norm(d) <= rel * np.linalg.norm(w), np.linalg.norm(d) / np.linalg.norm(w)
+    assert np.abs(d).max() <= rel * np.abs(w).max(), np.abs(d).max() / np.abs(w).max()
 
 
 def _gpu(kind, cfg, t, dev, **kw) -> GpuDrafter:
@@ -93,7 +103,7 @@ def test_trace_logits_match_oracle(dev, kind):
     c_got, ids, l_got = g.trace(toks, codes=codes)
     np.testing.assert_array_equal(c_got, codes)
     assert ids.shape == (37, cfg["vocab"]) and (ids[0] == np.arange(cfg["vocab"])).all()
-    assert np.abs(l_got - lg).max() < 1e-4
+    _assert_logits(l_got, lg)
     assert (l_got.argmax(1) == lg.argmax(1)).all()
     assert g.length == 0                     # trace leaves the committed state alone
 
@@ -116,7 +126,7 @@ def test_draft_matches_oracle(dev, kind, online):
         got = g.draft(gamma, hyp=hyp, topk=k, last_codes=last)
         assert got.tokens == want.tokens, (hyp, gamma)
         np.testing.assert_array_equal(got.topk_ids, want.topk_ids)
-        np.testing.assert_allclose(got.topk_logits, want.topk_logits, rtol=0, atol=1e-4)
+        _assert_logits(got.topk_logits, want.topk_logits)
         np.testing.assert_array_equal(got.codes, want.codes)
     assert g.length == len(toks)
     # rollback: truncate then draft equals a drafter that never saw the tail
