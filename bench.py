@@ -314,7 +314,7 @@ def sdc_forward(dev, steps: int, warmup: int) -> dict:
                         "router features + memory forward",
             "tokens_per_s": n / (ms * 1e-3), "ms_per_step": ms, "algorithmic_bytes": layer_bytes,
             "layer_hbm_frac": layer_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "scan": {"kernel": "k_ssm_chunk_end + k_ssm_apply", "avg_ms": scan_ms, "algorithmic_bytes": scan_bytes,
+            "scan": {"kernel": "k_ssm_scan", "avg_ms": scan_ms, "algorithmic_bytes": scan_bytes,
                      "achieved_GBs": scan_bytes / (scan_ms * 1e-3) / 1e9,
                      "hbm_frac": scan_bytes / (scan_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
             "readout": {"kernel": "k_readout_fused", "avg_ms": fused_ms, "algorithmic_bytes": fused_bytes,

@@ -202,13 +202,17 @@ int lng_gather_sum_scaled(const void* const* tables, int table_dtype, int32_t me
                           int32_t scale_log2, uint32_t seed, float* out, void* stream);
 
 /* ---------------------------------------------------------------- K4: SSM scan */
-/* s[B,T,N] (fp32): s_t = a*s_{t-1} + (1-a)*u_t, s_{-1} = s0 (zero if null).
+/* s[B,T,N] (fp32): s_t = a*s_{t-1} + (1-a)*u_t, s_{-1} = s0[B,N] (zero if null).
  * chunked_scan / sequential_scan (ffnmem/memory/ssm.py:58-91) and the carried
- * state of ssm_continue (ffnmem/infer.py:125-137).  `workspace` holds
- * lng_ssm_workspace_bytes(B, T, N) bytes of per-chunk end states. */
+ * state of ssm_continue (ffnmem/infer.py:125-137), in one pass over u.  `workspace`
+ * (workspace_bytes >= lng_ssm_workspace_bytes(B, T, N)) holds the tiles' hand-off
+ * records; zero it once before its first use.  `epoch` tags this call's records: give every
+ * call on one workspace a different value (a counter; values are taken mod 2^30).  Calls that
+ * share a workspace must not overlap.  The int32 at byte 0 of the workspace gets a nonzero bit
+ * if a hand-off wait ran out (the call's result is then wrong). */
 size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N);
 int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
-                 float* workspace, float* s, void* stream);
+                 void* workspace, size_t workspace_bytes, uint32_t epoch, float* s, void* stream);
 
 /* ---------------------------------------------------------------- K5: drafting */
 /* A token-routed drafter (the per-token algorithm of RefDrafter, drafting/cpu_drafter.py:76-289,

@@ -766,41 +766,6 @@ __device__ __forceinline__ int dr_lut_code(const lng_drafter& D, int64_t ptok, i
 // so the hand-off needs no L2 write-back (buffer_wbl2) per block and no L2 invalidate in the
 // reader.  Every block's threads wait until their coherent stores are complete (vmcnt(0)), the
 // barrier collects the block, thread 0 counts it in; the last block resets the counter.
-__device__ __forceinline__ void st_dev(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev(int32_t* p, int32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ int32_t ld_dev(const int32_t* p) {
-  return __hip_atomic_load(const_cast<int32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-constexpr int WAITCNT_VM0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt left open
-
-// 16-byte device-coherent hand-off through raw buffer operations with the sc1 cache policy (the
-// policy the agent-scope relaxed loads and stores above use), one instruction per 16 bytes.
-constexpr int BUF_DW3 = 0x00020000;  // raw buffer descriptor word 3 (gfx9 family)
-constexpr int CPOL_SC1 = 16;         // cache policy bit sc1
-// base and bytes must be the same in every active lane: they are taken from the first one, so the
-// descriptor lives in scalar registers (a per-lane descriptor would serialise every access).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_buf(const void* base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32));
-  const int n = static_cast<int>(__builtin_amdgcn_readfirstlane(bytes));
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>((static_cast<uint64_t>(hi) << 32) | lo), 0, n,
-                                           BUF_DW3);
-}
-__device__ __forceinline__ f32x4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, CPOL_SC1));
-}
-__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, byte_off, 0, CPOL_SC1);
-}
-
 __device__ __forceinline__ bool dr_last_block(int32_t* counter, int32_t total, int* flag) {
   __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
   __syncthreads();

@@ -1,66 +1,285 @@
-// Diagonal SSM scan: s_t = a * s_{t-1} + (1 - a) * u_t, s_{-1} = s0 (or 0).
+// Diagonal SSM scan: s_t = a * s_{t-1} + (1 - a) * u_t, s_{-1} = s0 (or 0)
+// (ffnmem/memory/ssm.py:37-91; the carried-state continuation of ffnmem/infer.py:125-137).
 //
-// Reduce-then-scan over time chunks of SSM_L steps, one wave per (batch,
-// 64-channel group, chunk), lanes = channels so every step is one coalesced
-// 256-byte row access:
-//   k_ssm_chunk_end : zero-initial scan of each chunk -> its end state e_c
-//   k_ssm_apply     : carry_c = a^L carry_{c-1} + e_{c-1} (short loop over the
-//                     preceding chunk ends, fp64), then the chunk is re-scanned
-//                     from carry_c with the plain fp32 recurrence.
+// One pass: every element of u is read once and every state written once.  A block owns one tile,
+// (batch b, 256-channel group g, span of SSM_WAVES * SSM_LW consecutive steps); each wave takes
+// SSM_LW steps of it and each lane 4 channels, so one step of a wave is one coalesced 1 KB access.
+//   1. a wave loads its inputs into registers and scans them from a zero state (end e_w);
+//   2. wave 0 folds the waves' ends into the tile's aggregate (its end state from a zero start;
+//      the first tile of a sequence starts from s0 instead, so its aggregate is its end state)
+//      and publishes it;
+//   3. the carry into the tile is the fold of the aggregates of the SSM_WIN tiles before it
+//      (tile k back weighted by the decay a^(k * span)), plus, past that window, the
+//      published end state of the tile just before it; the 8 waves fetch those records at once;
+//   4. the tile publishes its end state; every wave re-scans its registers from its carry in and
+//      writes s.
+// Records are self-validating: every element is a 64-bit (value, tag) pair written and read with
+// single 64-bit accesses at the device-coherent level, the tag holding the call's epoch and the
+// record kind, so a reader needs no separate flag and a writer no completion wait.  A tile waits
+// only on tiles with smaller block indices (tiles run in span-major order), which the in-order
+// dispatcher has started before it and which publish their aggregate before they wait on anything;
+// waits are bounded all the same (an error bit in the workspace header reports one that ran out).
 #include "common.h"
 
 namespace lng {
 
-constexpr int SSM_L = 64;
+constexpr int SSM_WAVES = 8;          // waves per block
+constexpr int SSM_GC = 256;           // channels per group (64 lanes x 4)
+constexpr int SSM_LW = 16;            // steps per wave
+constexpr int SSM_SPAN = SSM_WAVES * SSM_LW;
+constexpr int SSM_WIN = 32;           // aggregates folded per look-back; the record before comes inclusive
+constexpr int SSM_PER_WAVE = (SSM_WIN + 1 + SSM_WAVES - 1) / SSM_WAVES;
+// workspace: a 256-byte header (error bits), then one record per tile: its aggregate and its end
+// state, 256 (value, tag) pairs each
+constexpr size_t SSM_HDR = 256;
+constexpr size_t SSM_REC = 2 * SSM_GC * sizeof(uint64_t);
+constexpr uint32_t SSM_AGG = 1u, SSM_INC = 2u;
+constexpr int SSM_SPIN_LIMIT = 1 << 22;  // sleeps of ~64 cycles: well past any real wait
 
-__global__ __launch_bounds__(64) void k_ssm_chunk_end(const float* __restrict__ a, const float* __restrict__ u,
-                                                      int64_t T, int32_t N, int32_t C, float* __restrict__ ends) {
-  const int n = blockIdx.y * 64 + threadIdx.x;
-  const int c = blockIdx.x;
-  const int64_t b = blockIdx.z;
-  if (n >= N) return;
-  const float an = a[n], bn = 1.0f - an;
-  const int64_t t0 = static_cast<int64_t>(c) * SSM_L;
-  const int64_t t1 = t0 + SSM_L < T ? t0 + SSM_L : T;
-  const float* ub = u + (b * T) * N + n;
-  float x[SSM_L];
-#pragma unroll
-  for (int i = 0; i < SSM_L; ++i) x[i] = (t0 + i < t1) ? ub[(t0 + i) * N] : 0.f;
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < SSM_L; ++i)
-    if (t0 + i < t1) s = fmaf(an, s, bn * x[i]);
-  ends[(b * C + c) * N + n] = s;
+// (value, tag) pairs move as single 64-bit buffer accesses with the cache policy CPOL; sc1 puts
+// them at the device-coherent level, past the XCD-private L2s, where every XCD reads the same copy
+// (which XCD runs a block is up to the dispatcher: records through one XCD's L2 (sc0) were seen
+// stale by blocks on another)
+template <int CPOL>
+__device__ __forceinline__ void st_pair(__amdgpu_buffer_rsrc_t r, uint32_t off, float v, uint32_t tag) {
+  const uint64_t w = (static_cast<uint64_t>(tag) << 32) | __float_as_uint(v);
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned int, w), r,
+                                        off, 0, CPOL);
+}
+template <int CPOL>
+__device__ __forceinline__ uint64_t ld_pair(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CPOL));
 }
 
-__global__ __launch_bounds__(64) void k_ssm_apply(const float* __restrict__ a, const float* __restrict__ u,
-                                                  const float* __restrict__ s0, int64_t T, int32_t N, int32_t C,
-                                                  const float* __restrict__ ends, float* __restrict__ s_out) {
-  const int n = blockIdx.y * 64 + threadIdx.x;
-  const int c = blockIdx.x;
-  const int64_t b = blockIdx.z;
-  if (n >= N) return;
-  const float an = a[n], bn = 1.0f - an;
-  // a^L in fp64 by repeated squaring (SSM_L is a power of two)
-  double aL = an;
-  for (int k = 1; k < SSM_L; k <<= 1) aL *= aL;
-  double carry = s0 ? static_cast<double>(s0[b * N + n]) : 0.0;
-  for (int q = 0; q < c; ++q) carry = aL * carry + static_cast<double>(ends[(b * C + q) * N + n]);
-  const int64_t t0 = static_cast<int64_t>(c) * SSM_L;
-  const int64_t t1 = t0 + SSM_L < T ? t0 + SSM_L : T;
-  const float* ub = u + (b * T) * N + n;
-  float* sb = s_out + (b * T) * N + n;
-  float x[SSM_L];
+template <bool VEC>
+__device__ __forceinline__ void load4(const float* p, int c, int N, float (&v)[4]) {
+  if (VEC) {
+    const f32x4 q = c < N ? *reinterpret_cast<const f32x4*>(p + c) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int i = 0; i < SSM_L; ++i) x[i] = (t0 + i < t1) ? ub[(t0 + i) * N] : 0.f;
-  float s = static_cast<float>(carry);
+    for (int j = 0; j < 4; ++j) v[j] = q[j];
+  } else {
 #pragma unroll
-  for (int i = 0; i < SSM_L; ++i) {
-    if (t0 + i < t1) {
-      s = fmaf(an, s, bn * x[i]);
-      sb[(t0 + i) * N] = s;
+    for (int j = 0; j < 4; ++j) v[j] = c + j < N ? p[c + j] : 0.f;
+  }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void store4(float* p, int c, int N, const float (&v)[4]) {
+  if (VEC) {
+    if (c < N) *reinterpret_cast<f32x4*>(p + c) = f32x4{v[0], v[1], v[2], v[3]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c + j < N) p[c + j] = v[j];
+  }
+}
+
+__device__ __forceinline__ float pow_f(float x, int n) {
+  float r = 1.0f;
+  while (n > 0) {
+    if (n & 1) r *= x;
+    x *= x;
+    n >>= 1;
+  }
+  return r;
+}
+
+template <bool VEC, int CPOL>
+__global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, const float* __restrict__ u,
+                                                  const float* __restrict__ s0, int32_t T, int32_t N, int32_t G,
+                                                  int32_t chains, uint8_t* __restrict__ ws, uint32_t ws_bytes,
+                                                  uint32_t epoch, float* __restrict__ s_out) {
+  __shared__ float s_end[SSM_WAVES][SSM_GC];   // wave ends from a zero start
+  __shared__ float s_term[SSM_WAVES][SSM_GC];  // the waves' terms of the tile's aggregate
+  __shared__ float s_part[SSM_WAVES][SSM_GC];  // the waves' shares of the carry
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // span-major tile order: every tile's predecessors have smaller block indices
+  const int tile = static_cast<int>(blockIdx.x);
+  const int span = tile / chains, chain = tile % chains;
+  const int g = chain % G, b = chain / G;
+  const int c = g * SSM_GC + lane * 4;
+  const int ts = span * SSM_SPAN;              // first step of the tile
+  const int t0 = ts + wave * SSM_LW;           // first step of this wave
+  const int nw = max(0, min(SSM_LW, T - t0));  // steps of this wave
+  float av[4], bv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    av[j] = c + j < N ? a[c + j] : 0.f;
+    bv[j] = 1.0f - av[j];
+  }
+  const float* ub = u + static_cast<int64_t>(b) * T * N;
+  float x[SSM_LW][4];
+#pragma unroll
+  for (int i = 0; i < SSM_LW; ++i) {
+    if (i < nw) {
+      load4<VEC>(ub + static_cast<int64_t>(t0 + i) * N, c, N, x[i]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[i][j] = 0.f;
     }
   }
+  float e[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < SSM_LW; ++i)
+    if (i < nw) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) e[j] = fmaf(av[j], e[j], bv[j] * x[i][j]);
+    }
+  // decays: a^SSM_LW per wave, at = a^SSM_SPAN per full tile, A = a^(steps of this tile); the
+  // wave's term of the aggregate e_w a^(steps after it); the carry weights at^k of its records
+  const int n_tile = max(0, min(SSM_SPAN, T - ts));
+  const int after = max(0, n_tile - (wave * SSM_LW + nw));
+  const int m = min(span, SSM_WIN);            // aggregates folded into the carry
+  const bool past = span > SSM_WIN;            // ... then the end state of the tile before them
+  float pw[4], A[4], coef[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pw[j] = pow_f(av[j], SSM_LW);
+    A[j] = pow_f(av[j], n_tile);
+    coef[j] = pow_f(pow_f(pw[j], SSM_WAVES), wave);
+    s_end[wave][lane * 4 + j] = e[j];
+    s_term[wave][lane * 4 + j] = e[j] * pow_f(av[j], after);
+  }
+  __syncthreads();
+
+  // record of tile k (byte offsets): aggregate at REC*k, end state at REC*k + 8*SSM_GC; lane owns 4 pairs
+  const __amdgpu_buffer_rsrc_t wsb = dev_buf(ws, ws_bytes);
+  auto rec_off = [&](int k, bool end_state) {
+    return static_cast<uint32_t>(SSM_HDR + static_cast<size_t>(k) * SSM_REC) + (end_state ? 8u * SSM_GC : 0u);
+  };
+  const uint32_t tag_agg = (epoch << 2) | SSM_AGG, tag_inc = (epoch << 2) | SSM_INC;
+  float E[4] = {0.f, 0.f, 0.f, 0.f};  // the tile's end state from a zero start
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    for (int w = 0; w < SSM_WAVES; ++w) E[j] += s_term[w][lane * 4 + j];
+  if (wave == 0) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      // the first tile of a chain starts from s0: its aggregate is its end state
+      const float agg = (span == 0 && s0 && c + j < N) ? fmaf(A[j], s0[static_cast<int64_t>(b) * N + c + j], E[j])
+                                                        : E[j];
+      st_pair<CPOL>(wsb, rec_off(tile, false) + 32u * lane + 8u * j, agg, tag_agg);
+    }
+  }
+  // carry = sum_{k < m} at^k agg[k back] (+ at^m end state [m back]); this wave takes k = wave,
+  // wave + 8, ...  First a light probe, one load per record of the last pair its writer stores (lane i
+  // of the wave probes the wave's record i); then every lane reads its pairs and checks their tags,
+  // re-reading what is still missing.  (Polling with whole records from every wave of every tile
+  // slowed the whole grid down.)
+  {
+    const int k = wave + SSM_WAVES * lane;
+    const bool mine = lane < SSM_PER_WAVE && (k < m || (past && k == m));
+    const uint32_t poff = mine ? rec_off(tile - (k + 1) * chains, k >= m) + 8u * (SSM_GC - 1) : 0u;
+    const uint32_t pwant = k < m ? tag_agg : tag_inc;
+    for (int spins = 0; spins < SSM_SPIN_LIMIT; ++spins) {
+      const bool ok = !mine || static_cast<uint32_t>(ld_pair<CPOL>(wsb, poff) >> 32) == pwant;
+      if (__ballot(!ok) == 0) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+  uint32_t off[SSM_PER_WAVE], want[SSM_PER_WAVE];
+  bool need[SSM_PER_WAVE];
+  uint64_t q[SSM_PER_WAVE][4];
+#pragma unroll
+  for (int i = 0; i < SSM_PER_WAVE; ++i) {
+    const int k = wave + SSM_WAVES * i;
+    need[i] = k < m || (past && k == m);
+    want[i] = k < m ? tag_agg : tag_inc;
+    off[i] = need[i] ? rec_off(tile - (k + 1) * chains, k >= m) + 32u * lane : 0u;
+    if (need[i]) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[i][j] = ld_pair<CPOL>(wsb, off[i] + 8u * j);
+    }
+  }
+  for (int spins = 0;; ++spins) {
+    bool again = false;
+#pragma unroll
+    for (int i = 0; i < SSM_PER_WAVE; ++i) {
+      if (!need[i]) continue;
+      const bool ok = static_cast<uint32_t>(q[i][0] >> 32) == want[i] && static_cast<uint32_t>(q[i][1] >> 32) == want[i] &&
+                      static_cast<uint32_t>(q[i][2] >> 32) == want[i] && static_cast<uint32_t>(q[i][3] >> 32) == want[i];
+      need[i] = __ballot(!ok) != 0;  // still missing somewhere in the wave
+      again |= need[i];
+    }
+    if (!again) break;
+    if (spins >= SSM_SPIN_LIMIT) {
+      if (lane == 0)
+        __hip_atomic_fetch_or(reinterpret_cast<int32_t*>(ws), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;  // give up (the result is flagged wrong)
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < SSM_PER_WAVE; ++i)
+      if (need[i]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q[i][j] = ld_pair<CPOL>(wsb, off[i] + 8u * j);
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float at8 = pow_f(pw[j], SSM_WAVES * SSM_WAVES);  // at^8
+    float part = 0.f, cf = coef[j];
+#pragma unroll
+    for (int i = 0; i < SSM_PER_WAVE; ++i) {
+      const int k = wave + SSM_WAVES * i;
+      if (k < m || (past && k == m)) part = fmaf(cf, __uint_as_float(static_cast<uint32_t>(q[i][j])), part);
+      cf *= at8;
+    }
+    s_part[wave][lane * 4 + j] = part;
+  }
+  __syncthreads();
+  // every wave sums the shares (same order in every wave), wave 0 publishes the tile's end state,
+  // and each wave carries the tile's carry through the waves before it
+  float st[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float carry = 0.f;
+    for (int w = 0; w < SSM_WAVES; ++w) carry += s_part[w][lane * 4 + j];
+    if (span == 0) carry = (s0 && c + j < N) ? s0[static_cast<int64_t>(b) * N + c + j] : 0.f;
+    if (wave == 0) st_pair<CPOL>(wsb, rec_off(tile, true) + 32u * lane + 8u * j, fmaf(A[j], carry, E[j]), tag_inc);
+    for (int w = 0; w < wave; ++w) carry = fmaf(pw[j], carry, s_end[w][lane * 4 + j]);
+    st[j] = carry;
+  }
+  if (nw > 0) {
+    float* sb = s_out + static_cast<int64_t>(b) * T * N;
+#pragma unroll
+    for (int i = 0; i < SSM_LW; ++i) {
+      if (i < nw) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) st[j] = fmaf(av[j], st[j], bv[j] * x[i][j]);
+        store4<VEC>(sb + static_cast<int64_t>(t0 + i) * N, c, N, st);
+      }
+    }
+  }
+}
+
+int64_t ssm_tiles(int64_t B, int64_t T, int32_t N) { return B * cdiv(N, SSM_GC) * cdiv(T, SSM_SPAN); }
+
+size_t ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
+  return SSM_HDR + static_cast<size_t>(ssm_tiles(B, T, N)) * SSM_REC;
+}
+
+int ssm_scan_launch(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, uint8_t* ws,
+                    size_t ws_bytes, uint32_t epoch, float* s, hipStream_t st) {
+  if (B < 0 || T < 0 || N <= 0) return fail(LNG_E_ARG, "ssm_scan: bad shape");
+  if (B == 0 || T == 0) return LNG_OK;
+  if (T > INT32_MAX / 2 || static_cast<int64_t>(N) * T > (int64_t{1} << 40))
+    return fail(LNG_E_ARG, "ssm_scan: sequence too long");
+  const int64_t tiles = ssm_tiles(B, T, N);
+  if (tiles > INT32_MAX || ssm_workspace_bytes(B, T, N) > UINT32_MAX) return fail(LNG_E_ARG, "ssm_scan: too many tiles");
+  if (!ws || ws_bytes < ssm_workspace_bytes(B, T, N))
+    return fail(LNG_E_ARG, "ssm_scan: workspace too small (lng_ssm_workspace_bytes)");
+  const int32_t G = static_cast<int32_t>(cdiv(N, SSM_GC));
+  const int32_t chains = static_cast<int32_t>(B * G);
+  const int32_t Ti = static_cast<int32_t>(T);
+  const uint32_t ep = epoch & 0x3FFFFFFFu;
+  const uint32_t wsb = static_cast<uint32_t>(ssm_workspace_bytes(B, T, N));
+  const dim3 grid(static_cast<unsigned>(tiles)), blk(512);
+  if (N % 4 == 0)
+    hipLaunchKernelGGL((k_ssm_scan<true, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb, ep, s);
+  else
+    hipLaunchKernelGGL((k_ssm_scan<false, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb, ep, s);
+  return check_launch("ssm_scan");
 }
 
 }  // namespace lng
@@ -70,22 +289,14 @@ using namespace lng;
 extern "C" {
 
 size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
-  return static_cast<size_t>(B) * static_cast<size_t>(cdiv(T, SSM_L)) * static_cast<size_t>(N) * sizeof(float);
+  if (B < 0 || T < 0 || N <= 0) return 0;
+  return ssm_workspace_bytes(B, T, N);
 }
 
-int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, float* workspace,
-                 float* s, void* stream) {
-  if (B < 0 || T < 0 || N <= 0) return fail(LNG_E_ARG, "ssm_scan: bad shape");
-  if (B == 0 || T == 0) return LNG_OK;
-  if (!workspace) return fail(LNG_E_ARG, "ssm_scan: workspace required (lng_ssm_workspace_bytes)");
-  const int64_t C = cdiv(T, SSM_L);
-  if (C > 65535 || B > 65535) return fail(LNG_E_ARG, "ssm_scan: sequence too long");
-  dim3 grid(static_cast<unsigned>(C), static_cast<unsigned>(cdiv(N, 64)), static_cast<unsigned>(B));
-  hipStream_t st = as_stream(stream);
-  hipLaunchKernelGGL(k_ssm_chunk_end, grid, dim3(64), 0, st, a, u, T, N, static_cast<int32_t>(C), workspace);
-  if (int rc = check_launch("ssm_chunk_end")) return rc;
-  hipLaunchKernelGGL(k_ssm_apply, grid, dim3(64), 0, st, a, u, s0, T, N, static_cast<int32_t>(C), workspace, s);
-  return check_launch("ssm_apply");
+int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, void* workspace,
+                 size_t workspace_bytes, uint32_t epoch, float* s, void* stream) {
+  return ssm_scan_launch(a, u, s0, B, T, N, static_cast<uint8_t*>(workspace), workspace_bytes, epoch, s,
+                         as_stream(stream));
 }
 
 }  // extern "C"

@@ -5,8 +5,8 @@
     s[t] = a * s[t-1] + (1 - a) * u[t],    s[-1] = 0
 
 Both scan functions of the reference (``chunked_scan`` and ``sequential_scan``,
-``ssm.py:58-91``) compute the same recurrence; here both run ``lng_ssm_scan``
-(reduce-then-scan over 64-step chunks on the GPU).
+``ssm.py:58-91``) compute the same recurrence; here both run ``lng_ssm_scan`` (one pass
+over the inputs, tiles of 128 steps chained by a decoupled look-back on the GPU).
 """
 
 from __future__ import annotations

@@ -9,6 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
 
 import torch
 
@@ -488,6 +489,22 @@ def gather_sum_scaled(tables, codes: torch.Tensor, orders, bits: int, scale_log2
 
 
 # ----------------------------------------------------------------------------- K4
+_ssm_ws: dict = {}
+_ssm_ws_lock = threading.Lock()
+
+
+def _ssm_workspace(dev: torch.device, nbytes: int) -> tuple[torch.Tensor, int]:
+    """The scan's hand-off workspace for (device, current stream) and the next epoch for it: zeroed
+    once when it is made or grown, then reused with a new epoch per call."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    with _ssm_ws_lock:
+        ws, epoch = _ssm_ws.get(key, (None, 0))
+        if ws is None or ws.numel() < nbytes:
+            ws, epoch = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev), 0
+        _ssm_ws[key] = (ws, epoch + 1)
+        return ws, epoch & 0x3FFFFFFF
+
+
 def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -> torch.Tensor:
     """``s_t = a s_{t-1} + (1 - a) u_t`` (fp32) for u ``[B, T, N]``, a ``[N]``, s0 ``[B, N]`` or None."""
     dev = _dev(a, u, s0)
@@ -496,15 +513,13 @@ def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -
     s0c = None if s0 is None else _c(s0.float())
     b, t, n = uc.shape
     out = torch.empty_like(uc)
-    ws_bytes = lib().lng_ssm_workspace_bytes(b, t, n)
-    ws = torch.empty(max(1, ws_bytes // 4), dtype=torch.float32, device=dev)
-    rc = _timed("ssm_scan", dev, lambda: lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws), _ptr(out),
-                                                            _stream(dev)))
+    ws, epoch = _ssm_workspace(dev, lib().lng_ssm_workspace_bytes(b, t, n))
+    rc = _timed("ssm_scan", dev, lambda: lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws),
+                                                            ws.numel(), epoch, _ptr(out), _stream(dev)))
     check(rc, "ssm_scan")
     return out
 
 
-# ----------------------------------------------------------------------------- K5
 def tree_accept(parent: torch.Tensor, node_tokens: torch.Tensor, argmax: torch.Tensor, out=None):
     """Device tree acceptance -> ``(path int32 [n], path_len int32 [1], new_tokens int64 [n])``
     (valid entries: the first ``path_len``).  ``out`` = (path, path_len, new_tokens) writes into

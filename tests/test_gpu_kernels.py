@@ -263,6 +263,20 @@ def test_ssm_scan(dev, b, t, n):
         assert np.abs(got - want).max() < 1e-5 * max(1.0, np.abs(want).max())  # 1e-5 (fp32 tolerance)
 
 
+def test_ssm_scan_workspace_reuse_across_shapes(dev):
+    # one workspace across calls of different shapes (larger, smaller, channel groups of 256 and a
+    # width that is not a multiple of 4): every call equals the recurrence, so the in-kernel reset
+    # of the counters and the epoch-tagged flags leave nothing stale behind
+    g = torch.Generator().manual_seed(5)
+    for b, t, n in ((2, 1000, 300), (8, 4096, 256), (1, 130, 7), (3, 257, 512), (8, 4096, 256), (1, 1, 4)):
+        a = 0.5 + 0.499 * torch.rand(n, generator=g)
+        u = torch.randn(b, t, n, generator=g)
+        s0 = torch.randn(b, n, generator=g)
+        got = ops.ssm_scan(a.to(dev), u.to(dev), s0.to(dev)).cpu().numpy()
+        want = om.ssm_scan(a.numpy(), u.numpy(), s0.numpy())
+        assert np.abs(got - want).max() < 1e-5 * max(1.0, np.abs(want).max()), (b, t, n)
+
+
 def test_ssm_scan_constant_input_closed_form(dev):
     a = torch.tensor([0.9, 0.95, 0.999, 0.5])
     u = torch.tensor([1.0, -2.0, 0.5, 3.0])
