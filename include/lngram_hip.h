@@ -214,6 +214,15 @@ size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N);
 int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
                  void* workspace, size_t workspace_bytes, uint32_t epoch, float* s, void* stream);
 
+/* lng_ssm_scan without a workspace argument and without any allocation: the hand-off records live
+ * in a static device array of the library (8.4 MB per GPU, held until the process ends), which
+ * limits the shape to B * ceil(N/256) * ceil(T/128) <= 2048 tiles (LNG_E_ARG beyond).  No
+ * counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops).  Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (other streams, other threads) race; calls in one stream are fine. */
+int lng_ssm_scan_static(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
+                        float* s, void* stream);
+
 /* ---------------------------------------------------------------- K5: drafting */
 /* A token-routed drafter (the per-token algorithm of RefDrafter, drafting/cpu_drafter.py:76-289,
  * and of drafter.cpp:152-545) over caller-owned device buffers.  Weights are the bundle arrays

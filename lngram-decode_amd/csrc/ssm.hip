@@ -21,6 +21,9 @@
 // waits are bounded all the same (an error bit in the workspace header reports one that ran out).
 #include "common.h"
 
+#include <atomic>
+#include <mutex>
+
 namespace lng {
 
 constexpr int SSM_WAVES = 8;          // waves per block
@@ -282,11 +285,53 @@ int ssm_scan_launch(const float* a, const float* u, const float* s0, int64_t B, 
   return check_launch("ssm_scan");
 }
 
+// ------------------------------------------------------------------ the allocation-free entry point
+// Hand-off records in a file-scope device array (zeroed when the library's code object is loaded),
+// sized for SSM_STATIC_TILES tiles.  Host code reaches it only through the address that
+// hipGetSymbolAddress returns for the current device, looked up on the first call on each device.
+constexpr int64_t SSM_STATIC_TILES = 2048;
+constexpr size_t SSM_STATIC_BYTES = SSM_HDR + SSM_STATIC_TILES * SSM_REC;  // 8.4 MB per device
+static __device__ __align__(256) uint8_t scratch[SSM_STATIC_BYTES];
+
+constexpr int SSM_MAX_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static uint8_t* g_scratch_ptr[SSM_MAX_DEVICES];
+static std::atomic<uint32_t> g_scratch_epoch[SSM_MAX_DEVICES];
+
+static int scratch_of_current_device(uint8_t** ptr, int* dev) {
+  if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= SSM_MAX_DEVICES)
+    return fail(LNG_E_HIP, "ssm_scan_static: no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[*dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(LNG_E_HIP, std::string("ssm_scan_static: hipGetSymbolAddress: ") + hipGetErrorString(e));
+    g_scratch_ptr[*dev] = static_cast<uint8_t*>(p);
+  }
+  *ptr = g_scratch_ptr[*dev];
+  return LNG_OK;
+}
+
 }  // namespace lng
 
 using namespace lng;
 
 extern "C" {
+
+int lng_ssm_scan_static(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, float* s,
+                        void* stream) {
+  if (B < 0 || T < 0 || N <= 0) return fail(LNG_E_ARG, "ssm_scan_static: bad shape");
+  if (B == 0 || T == 0) return LNG_OK;
+  if (ssm_tiles(B, T, N) > SSM_STATIC_TILES)
+    return fail(LNG_E_ARG, "ssm_scan_static: B * ceil(N/256) * ceil(T/128) exceeds the 2048 tiles of its static "
+                           "scratch; use lng_ssm_scan with a workspace");
+  uint8_t* ws = nullptr;
+  int dev = 0;
+  if (int rc = scratch_of_current_device(&ws, &dev)) return rc;
+  const uint32_t epoch = g_scratch_epoch[dev].fetch_add(1, std::memory_order_relaxed);
+  return ssm_scan_launch(a, u, s0, B, T, N, ws, SSM_STATIC_BYTES, epoch, s, as_stream(stream));
+}
 
 size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
   if (B < 0 || T < 0 || N <= 0) return 0;
