@@ -170,6 +170,10 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
  * with an online softmax seeded by the sink (m, l) = (b0, 1).  bf16 only;
  * shape: orders (2,3), mem_dim 128, 16 query heads x 64, 4 KV heads.
  *   q        [N_tok, 16*64]  projected query (readout_q_proj output)
+ *   q_rows   null, or [N_tok, 16*64] bf16: the query projection's input rows, when q was projected
+ *            from them with readout_query_norm.weight folded into readout_q_proj.weight
+ *            (lng_fold_columns); the kernel then scales each token's query by its row's
+ *            rsqrt(mean(row^2) + q_eps), which completes that RMSNorm (lngram_v2.py:1115-1118)
  *   codes    [B, T, R] uint8 route codes
  *   table2   [R*256, 128], table3 [R*4096, 128]
  *   kv_pack  [LNG_READOUT_PACK_ELEMS] bf16, readout_kv_proj.weight in the kernel's operand
@@ -177,9 +181,14 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
  *   w_mem    [256]           readout_memory_norm.weight
  *   head_out [N_tok, 16*64]  attention output (input of readout_o_proj) */
 #define LNG_READOUT_PACK_ELEMS 131072
-int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int64_t T, int32_t R,
-                             const void* table2, const void* table3, const void* kv_pack, const void* w_mem,
-                             float eps, float scale, float sink_logit, void* head_out, void* stream);
+int lng_memory_readout_fused(const void* q, const void* q_rows, float q_eps, const uint8_t* codes, int64_t B,
+                             int64_t T, int32_t R, const void* table2, const void* table3, const void* kv_pack,
+                             const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
+                             void* stream);
+
+/* out[N, K] = w[N, K] * s[K] (bf16, one rounding): a row RMSNorm's weight folded into the projection
+ * that follows it (readout_query_norm.weight into readout_q_proj.weight, lngram_v2.py:1115-1118). */
+int lng_fold_columns(const void* w, const void* s, int64_t N, int64_t K, void* out, void* stream);
 
 /* kv_pack [LNG_READOUT_PACK_ELEMS] bf16 from readout_kv_proj.weight kv [512, 256] bf16 (rows
  * 0..255 the keys, 256..511 the values of the 4 KV heads, lngram_v2.py:1120-1131): the key

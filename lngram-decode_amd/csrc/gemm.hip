@@ -7,8 +7,6 @@
 // consecutive output channels of one token: a packed store for plain outputs,
 // and exactly one route's 4 sign bits for the router epilogue.
 // fp32 runs on a VALU tile kernel (the tiny fp32 layer and fp32 routers).
-#include <cstdlib>
-
 #include "common.h"
 
 namespace lng {
@@ -597,6 +595,14 @@ static int launch_f32(const void* x, const void* w, int64_t M, int64_t N, int64_
   return check_launch("gemm_f32");
 }
 
+// out[n, k] = bf16(w[n, k] * s[k]): a row RMSNorm's weight folded into the projection after it
+__global__ void k_fold_columns(const bf16* __restrict__ w, const bf16* __restrict__ s, int64_t N, int64_t K,
+                               bf16* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= N * K) return;
+  out[i] = static_cast<bf16>(static_cast<float>(w[i]) * static_cast<float>(s[i % K]));
+}
+
 int linear_bf16_lt(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s);
 
 // Shared entry for bf16 MFMA linears (used by other translation units).
@@ -610,6 +616,14 @@ int linear_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, v
 using namespace lng;
 
 extern "C" {
+
+int lng_fold_columns(const void* w, const void* s, int64_t N, int64_t K, void* out, void* stream) {
+  if (N <= 0 || K <= 0) return fail(LNG_E_ARG, "fold_columns: bad shape");
+  const int64_t n = N * K;
+  hipLaunchKernelGGL(k_fold_columns, dim3(static_cast<unsigned>(cdiv(n, 256))), dim3(256), 0, as_stream(stream),
+                     static_cast<const bf16*>(w), static_cast<const bf16*>(s), N, K, static_cast<bf16*>(out));
+  return check_launch("fold_columns");
+}
 
 int32_t lng_linear_rowsq_partials(int64_t N) { return static_cast<int32_t>(2 * cdiv(N, GB2)); }
 
@@ -629,9 +643,10 @@ int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, in
   hipStream_t s = as_stream(stream);
   if (dtype == LNG_BF16) {
     if (K % 8) return fail(LNG_E_ARG, "linear: bf16 needs K % 8 == 0");
-    // large plain projections: hipBLASLt (no epilogue to fuse); otherwise the MFMA kernels here
-    static const bool lt_off = std::getenv("LNGRAM_NO_HIPBLASLT") != nullptr;
-    if (!lt_off && M >= 1024 && N >= 256 && K >= 256) {
+    // large plain projections (no epilogue to fuse) run on hipBLASLt, the library GEMM, which is
+    // faster on them than the kernels here; shapes it has no algorithm for, and the rest, run the
+    // MFMA kernels of this file.  The choice depends on the shape alone.
+    if (M >= 1024 && N >= 256 && K >= 256) {
       const int rc = linear_bf16_lt(x, w, M, N, K, y, s);
       if (rc != LNG_E_ARG) return rc;
     }

@@ -68,6 +68,13 @@ const LtPlan* lt_plan(hipblasLtHandle_t* handle, int64_t M, int64_t N, int64_t K
     if (ok) p.algo = res[0].algo;
     if (pref) hipblasLtMatmulPreferenceDestroy(pref);
   }
+  if (!ok) {  // no plan for this shape: keep the verdict, release the descriptors
+    if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
+    for (hipblasLtMatrixLayout_t l : {p.la, p.lb, p.lc})
+      if (l) hipblasLtMatrixLayoutDestroy(l);
+    p.desc = nullptr;
+    p.la = p.lb = p.lc = nullptr;
+  }
   p.ok = ok;
   auto& slot = g_lt_plans[key] = p;
   return ok ? &slot : nullptr;

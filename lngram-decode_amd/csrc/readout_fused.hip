@@ -62,6 +62,7 @@ __device__ __forceinline__ float sumsq8(const bf16x8 v, float acc) {
 // [route / 2] (-1 = zero row); the memory-norm weight.
 template <int FR_TOK>
 __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const bf16* __restrict__ q,
+                                                          const bf16* __restrict__ q_rows, float q_eps,
                                                           const uint8_t* __restrict__ codes,
                                                           int64_t B, int64_t T, int32_t R,
                                                           const bf16* __restrict__ table2,
@@ -72,9 +73,21 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
   __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][2][FR_RB];
   __shared__ __attribute__((aligned(16))) bf16 wms[FR_DT];
+  __shared__ float qscale[FR_TOK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int li = lane & 15, lg = lane >> 4;
   if (threadIdx.x < FR_DT) wms[threadIdx.x] = w_mem[threadIdx.x];
+  // With q_rows, q is the projection of the raw rows with the query RMSNorm's weight folded into
+  // it, and each token's query is scaled here by its row's rsqrt(mean(row^2) + q_eps): wave w
+  // reduces the row of token w (2 KB, two 16 B pieces per lane)
+  const int64_t ntok_all = B * T;
+  bf16x8 hq[2];
+  const int64_t tq_own = static_cast<int64_t>(blockIdx.x) * FR_TOK + w;
+  if (q_rows) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      hq[k] = tq_own < ntok_all ? ld16(q_rows + tq_own * (FR_H * FR_HD) + 8 * (lane + 64 * k)) : zero8();
+  }
 
   // phase-A operands first (no dependence on the codes), so their latency overlaps stage 0:
   // wave w takes head h = w & 3 and feature tiles ft0 .. ft0 + NFT-1; column tile tt = tokens 4tt .. 4tt+3
@@ -164,8 +177,15 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   u32x4 g[16];
   gather(0, g);  // first chunk in flight during phase A
 
+  if (q_rows) {
+    const float ss = wave_sum(sumsq8(hq[1], sumsq8(hq[0], 0.f)));
+    if (lane == 0) qscale[w] = __builtin_amdgcn_rsqf(ss * (1.0f / (FR_H * FR_HD)) + q_eps);
+  } else if (lane == 0) {
+    qscale[w] = 1.0f;
+  }
+
   // ---------------- phase A: qkw[t][4h+g][f] = scale * w_mem[f] * (Wk[h]^T q[t][4h+g])[f]
-  __syncthreads();  // wms
+  __syncthreads();  // wms, qscale
 #pragma unroll
   for (int ft = 0; ft < NFT; ++ft) {
     const int f = 16 * (a_ft0 + ft) + 4 * lg;
@@ -175,9 +195,10 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wa[ft][ks], bq[tt][ks], d, 0, 0, 0);
+      const float sc_t = scale * qscale[4 * tt + (li >> 2)];
       bf16x4 o;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(wm4[i]) * scale);
+      for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(wm4[i]) * sc_t);
       *reinterpret_cast<bf16x4*>(&xs[4 * tt + (li >> 2)][a_hg][f]) = o;
     }
   }
@@ -346,7 +367,8 @@ __global__ __launch_bounds__(256) void k_readout_pack(const bf16* __restrict__ k
 
 using namespace lng;
 
-extern "C" int lng_memory_readout_fused(const void* q, const uint8_t* codes, int64_t B, int64_t T, int32_t R,
+extern "C" int lng_memory_readout_fused(const void* q, const void* q_rows, float q_eps, const uint8_t* codes,
+                                        int64_t B, int64_t T, int32_t R,
                                         const void* table2, const void* table3, const void* kv_pack,
                                         const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
                                         void* stream) {
@@ -358,7 +380,8 @@ extern "C" int lng_memory_readout_fused(const void* q, const uint8_t* codes, int
   const int64_t blocks = cdiv(ntok, FR_TOK);
   if (blocks > 0x7fffffffLL) return fail(LNG_E_ARG, "memory_readout_fused: too many tokens");
   hipLaunchKernelGGL(k_readout_fused<FR_TOK>, dim3(static_cast<unsigned>(blocks)), dim3(64 * FR_TOK), 0,
-                     as_stream(stream), static_cast<const bf16*>(q), codes, B, T, R, static_cast<const bf16*>(table2),
+                     as_stream(stream), static_cast<const bf16*>(q), static_cast<const bf16*>(q_rows), q_eps, codes,
+                     B, T, R, static_cast<const bf16*>(table2),
                      static_cast<const bf16*>(table3), static_cast<const bf16*>(kv_pack),
                      static_cast<const bf16*>(w_mem), eps, scale, sink_logit, static_cast<bf16*>(head_out));
   return check_launch("memory_readout_fused");

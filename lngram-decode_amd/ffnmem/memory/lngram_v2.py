@@ -256,6 +256,7 @@ class _RouteNgramMemoryBase(nn.Module):
                                               eps=rmsnorm_eps, normalization=normalization, bias=conv_bias,
                                               zero_init=conv_zero_init, device=device, dtype=dtype)
         self._fused_cache: tuple | None = None
+        self._q_fold_cache: tuple | None = None
 
     # ------------------------------------------------------------------ codes
     def quantize_route_logits(self, q_logits: Tensor) -> Tensor:
@@ -353,6 +354,16 @@ class _RouteNgramMemoryBase(nn.Module):
                 and self.readout_num_kv_heads == 4 and self.readout_kv_proj.weight.dtype == torch.bfloat16
                 and all(t.weight.dtype == torch.bfloat16 for t in self.tables.values()))
 
+    def _folded_query_weight(self) -> Tensor:
+        """``readout_q_proj.weight`` with ``readout_query_norm.weight`` folded into its columns
+        (``ops.fold_columns``), cached per weight version: the fused path projects the raw hidden
+        states with it and lets the readout kernel apply each row's RMS scale."""
+        w, n = self.readout_q_proj.weight, self.readout_query_norm.weight
+        key = (w.data_ptr(), w._version, n.data_ptr(), n._version, w.device)
+        if self._q_fold_cache is None or self._q_fold_cache[0] != key:
+            self._q_fold_cache = (key, ops.fold_columns(w.detach(), n.detach()))
+        return self._q_fold_cache[1]
+
     def _fused_weights(self) -> Tensor:
         """The fused readout's packed KV weight (``ops.memory_readout_pack`` of
         ``readout_kv_proj.weight``), cached per weight version."""
@@ -382,15 +393,19 @@ class _RouteNgramMemoryBase(nn.Module):
                 raise ValueError(f"q_logits shape={tuple(q_logits.shape)}, expected {expected}")
             q_btrm = q_logits.reshape(b, t, self.num_routes, self.bits_per_route)
         self._check_inference(q_btrm)
-        query = self._project_query(hidden_states)
         if segment_ids is None and valid_tokens is None and self._fused_shape_ok(hidden_states):
+            # the query RMSNorm's weight is folded into the projection and its row scale applied in
+            # the readout kernel, so the normalised hidden states are never written out
             kv_pack = self._fused_weights()
-            head = ops.memory_readout_fused(query.view(b, t, self.readout_inner_dim), route_codes_btr,
-                                            self.tables["ngram_2"].weight, self.tables["ngram_3"].weight, kv_pack,
-                                            self.readout_memory_norm.weight, self.readout_memory_norm.eps,
-                                            self.softmax_scale, self.readout_sink_logit)
+            q_raw = ops.linear(hidden_states, self._folded_query_weight())
+            head = ops.memory_readout_fused(q_raw, route_codes_btr, self.tables["ngram_2"].weight,
+                                            self.tables["ngram_3"].weight, kv_pack, self.readout_memory_norm.weight,
+                                            self.readout_memory_norm.eps, self.softmax_scale,
+                                            self.readout_sink_logit, q_rows=hidden_states,
+                                            q_eps=self.readout_query_norm.eps)
             head_output = head.view(b, t, self.readout_num_heads, self.readout_head_dim)
         else:
+            query = self._project_query(hidden_states)
             tokens = self._lookup_route_chunk(route_codes_btr, q_btrm, 0, self.num_routes, segment_ids, valid_tokens)
             key, value = self._project_memory(tokens)
             head_output = self._manual_gqa(query, key, value)

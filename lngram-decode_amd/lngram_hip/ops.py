@@ -437,14 +437,28 @@ def memory_readout_pack(kv: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def fold_columns(w: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
+    """``w[N, K] * s[K]`` in bf16 (one rounding): a row RMSNorm's weight folded into the projection after it."""
+    dev = _dev(w, s)
+    wc, sc = _c(w.to(torch.bfloat16)), _c(s.to(torch.bfloat16))
+    n, k = wc.shape
+    if sc.shape != (k,):
+        raise ValueError("fold_columns: w [N, K], s [K]")
+    out = torch.empty_like(wc)
+    check(lib().lng_fold_columns(_ptr(wc), _ptr(sc), n, k, _ptr(out), _stream(dev)), "fold_columns")
+    return out
+
+
 def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Tensor, table3: torch.Tensor,
                          kv_pack: torch.Tensor, w_mem: torch.Tensor, eps: float, scale: float,
-                         sink_logit: float) -> torch.Tensor:
+                         sink_logit: float, q_rows: torch.Tensor | None = None, q_eps: float = 0.0) -> torch.Tensor:
     """Fused gather + sink readout (bf16, 16 heads x 64, 4 KV heads, orders (2,3), mem_dim 128).
 
     q ``[B, T, 1024]``, codes ``[B, T, R]`` uint8, ``kv_pack`` from ``memory_readout_pack`` ->
-    head output ``[B, T, 1024]``."""
-    dev = _dev(q, codes, table2, table3, kv_pack, w_mem)
+    head output ``[B, T, 1024]``.  With ``q_rows [B, T, 1024]`` (the projection's input rows; q was
+    projected with the query RMSNorm's weight folded in), each token's query is scaled by its row's
+    ``rsqrt(mean(row^2) + q_eps)`` inside the kernel."""
+    dev = _dev(q, codes, table2, table3, kv_pack, w_mem, q_rows)
     b, t, r = codes.shape
     qc = _c(q)
     cc = _c(codes.to(torch.uint8))
@@ -454,11 +468,16 @@ def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Ten
         raise ValueError("fused readout expects tables [R*256,128] and [R*4096,128]")
     if kv_pack.shape != (_lib.READOUT_PACK_ELEMS,) or kv_pack.dtype != torch.bfloat16 or w_mem.shape != (256,):
         raise ValueError("fused readout weight shapes")
+    qr = None
+    if q_rows is not None:
+        qr = _c(q_rows)
+        if qr.dtype != torch.bfloat16 or qr.shape != qc.shape:
+            raise ValueError("fused readout: q_rows must be bf16 and shaped like q")
     out = torch.empty(b, t, 1024, dtype=torch.bfloat16, device=dev)
     t2, t3, kp, wmc = _c(table2), _c(table3), _c(kv_pack), _c(w_mem.to(torch.bfloat16))
     rc = _timed("memory_readout_fused", dev, lambda: lib().lng_memory_readout_fused(
-        _ptr(qc), _ptr(cc), b, t, r, _ptr(t2), _ptr(t3), _ptr(kp), _ptr(wmc), eps, scale, sink_logit,
-        _ptr(out), _stream(dev)))
+        _ptr(qc), _ptr(qr), float(q_eps), _ptr(cc), b, t, r, _ptr(t2), _ptr(t3), _ptr(kp), _ptr(wmc), eps, scale,
+        sink_logit, _ptr(out), _stream(dev)))
     check(rc, "memory_readout_fused")
     return out
 
