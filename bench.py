@@ -178,17 +178,17 @@ def draft_cpu_baseline(seconds: float) -> dict:
                       "drafting/cpu/drafter.cpp with OpenMP"}
 
 
-def draft_step(dev, iters: int, warmup: int) -> dict:
-    """SD-B decode draft step on one GPU: the 2048-token context is committed, then one step =
-    16-node draft tree (10 parent readouts in 4 depths, top-3, online counts over the context) +
-    codes of every node + verification gather [16, 182, 256] + greedy acceptance against a
-    synthetic verifier argmax, ending when the accepted path and bonus token are on the host."""
-    import numpy as np
+def draft_step(dev, iters: int, warmup: int):
+    """Set up, and return the timing run of, the SD-B decode draft step on one GPU: the 2048-token
+    context is committed, then one step = 16-node draft tree (10 parent readouts in 4 depths, top-3,
+    online counts over the context) + codes of every node + verification gather [16, 182, 256] +
+    greedy acceptance against a synthetic verifier argmax, ending when the accepted path and bonus
+    token are on the host."""
     import torch
 
     from drafting import tree as dtree
     from drafting.gpu_drafter import GpuDrafter
-    from lngram_hip import ops, workloads
+    from lngram_hip import workloads
 
     w = workloads.SDB_DRAFT
     cfg, t = workloads.build_draft_bundle(w, seed=0)
@@ -205,6 +205,21 @@ def draft_step(dev, iters: int, warmup: int) -> dict:
     res_new, res_path = res[:8 * n].view(torch.int64), res[8 * n:12 * n].view(torch.int32)
     res_len = res[12 * n:12 * n + 4].view(torch.int32)
     host = torch.empty(16 * n + 16, dtype=torch.uint8).pin_memory()
+
+    def run() -> dict:
+        return _draft_run(g, spec, fc, parent, res, res_new, res_path, res_len, host, w, iters, warmup)
+
+    return run
+
+
+def _draft_run(g, spec, fc, parent, res, res_new, res_path, res_len, host, w, iters: int, warmup: int) -> dict:
+    import numpy as np
+    import torch
+
+    from lngram_hip import ops
+
+    dev = res.device
+    n = spec.n
     out = {}
     for case in ("all_accept", "reject_at_root"):
         wall, gpu = [], []
@@ -263,8 +278,9 @@ def _time_steps(step, steps: int, warmup: int, *kernels: str):
     return el / steps * 1e3, {k: t.mean_ms() for k, t in timers.items()}
 
 
-def tiny_forward(dev, steps: int, warmup: int) -> dict:
-    """Tiny layer (d 128, 8 routes, mem_dim 32, fp32, 4 x 128 tokens): launch-bound, tokens/s only."""
+def tiny_forward(dev, steps: int, warmup: int):
+    """Set up, and return the timing run of, the tiny layer (d 128, 8 routes, mem_dim 32, fp32,
+    4 x 128 tokens): launch-bound, tokens/s only."""
     import torch
 
     from lngram_hip import ops, workloads
@@ -273,15 +289,23 @@ def tiny_forward(dev, steps: int, warmup: int) -> dict:
     mem = workloads.build_memory(w, seed=0, device=dev)
     h = workloads.make_hidden(w, seed=1, device=dev)
     ones = torch.ones(w.d_model, device=dev)
-    ms, _ = _time_steps(lambda: mem(h, ops.rmsnorm(h, ones, w.norm_eps)), steps, warmup)
+
+    def run() -> dict:
+        ms, _ = _time_steps(lambda: mem(h, ops.rmsnorm(h, ones, w.norm_eps)), steps, warmup)
+        return _tiny_result(w, ms)
+
+    return run
+
+
+def _tiny_result(w, ms: float) -> dict:
     return {"workload": "tiny layer: d128, R8, mem_dim 32, 4 query heads x 32, fp32, 4 x 128 tokens, hidden router",
             "tokens_per_s": w.tokens / (ms * 1e-3), "ms_per_step": ms,
             "note": "launch-bound (512 tokens): the roofline fraction is not meaningful"}
 
 
-def sdc_forward(dev, steps: int, warmup: int) -> dict:
-    """SD-C layer: 8 x 4096 tokens, 181 routes; one step = diagonal SSM scan of u [8, 4096, 256] fp32
-    (decays U[0.9, 0.999]) + router features concat(RMSNorm(E[x_{t-1}]), RMSNorm(E[x_t]), s_t) from
+def sdc_forward(dev, steps: int, warmup: int):
+    """Set up, and return the timing run of, the SD-C layer: 8 x 4096 tokens, 181 routes; one step =
+    diagonal SSM scan of u [8, 4096, 256] fp32 (decays U[0.9, 0.999]) + router features concat(RMSNorm(E[x_{t-1}]), RMSNorm(E[x_t]), s_t) from
     token ids (V 32768, bf16) + memory forward (router GEMM 2304 -> 724 + sign-pack, query RMSNorm +
     projection, fused gather + readout, output projection, causal conv)."""
     import torch
@@ -304,7 +328,14 @@ def sdc_forward(dev, steps: int, warmup: int) -> dict:
         x = feats.from_ids(tok, E, s)
         return mem(h, None, router_in=x)
 
-    ms, kms = _time_steps(step, steps, warmup, "ssm_scan", "memory_readout_fused")
+    def run() -> dict:
+        ms, kms = _time_steps(step, steps, warmup, "ssm_scan", "memory_readout_fused")
+        return _sdc_result(w, ms, kms)
+
+    return run
+
+
+def _sdc_result(w, ms: float, kms: dict) -> dict:
     scan_ms, fused_ms = kms["ssm_scan"], kms["memory_readout_fused"]
     n = w.tokens
     scan_bytes = 2 * n * w.ssm_dim * 4
@@ -322,13 +353,12 @@ def sdc_forward(dev, steps: int, warmup: int) -> dict:
                         "hbm_frac": fused_bytes / (fused_ms * 1e-3) / 1e9 / HBM_PEAK_GBS}}
 
 
-def scaled_gather(dev, steps: int, warmup: int) -> dict:
-    """Scaled-table stress: 16 x 4096 tokens, 184 routes, orders (2, 3), each route's order block
-    grown 64x (51,249,152 rows x 128 bf16 = 13.1 GB, HBM-resident), uniformly random codes; one
-    step = one gather + sum launch (one row per token, route and order; fp32 sums [16, 4096, 128])."""
+def scaled_gather(dev, steps: int, warmup: int):
+    """Set up, and return the timing run of, the scaled-table stress: 16 x 4096 tokens, 184 routes,
+    orders (2, 3), each route's order block grown 64x (51,249,152 rows x 128 bf16 = 13.1 GB,
+    HBM-resident), uniformly random codes; one step = one gather + sum launch (one row per token,
+    route and order; fp32 sums [16, 4096, 128])."""
     import torch
-
-    from lngram_hip import ops
 
     B, T, R, orders, sl, md = 16, 4096, 184, (2, 3), 6, 128
     n2, n3 = R << (sl + 8), R << (sl + 12)
@@ -339,6 +369,23 @@ def scaled_gather(dev, steps: int, warmup: int) -> dict:
         blk.normal_(0.0, 0.02, generator=g)
     tabs = [table[:n2], table[n2:]]
     codes = torch.randint(0, 16, (B, T, R), device=dev, dtype=torch.uint8)
+    state = {"tabs": tabs, "codes": codes}
+    del table, tabs, codes
+
+    def run() -> dict:
+        r = _scaled_run(state["tabs"], state["codes"], B, T, R, orders, sl, md, steps, warmup)
+        state.clear()
+        torch.cuda.empty_cache()
+        return r
+
+    return run
+
+
+def _scaled_run(tabs, codes, B, T, R, orders, sl, md, steps: int, warmup: int) -> dict:
+    import torch
+
+    from lngram_hip import ops
+
     for _ in range(warmup):
         ops.gather_sum_scaled(tabs, codes, orders, 4, sl, seed=2024)
     torch.cuda.synchronize()
@@ -350,8 +397,6 @@ def scaled_gather(dev, steps: int, warmup: int) -> dict:
     rows = B * R * ((T - 1) + (T - 2))                      # t >= n-1 reads a row
     alg = rows * md * 2 + B * T * md * 4 + B * T * R       # rows + fp32 out + codes
     gbs = alg / (ms * 1e-3) / 1e9
-    del table, tabs, codes
-    torch.cuda.empty_cache()
     return {"workload": "scaled-table gather + sum: B16 x T4096, R184, orders (2,3), 64x table "
                         "(51,249,152 x 128 bf16 = 13.1 GB), uniform random codes",
             "kernel": "k_gather_sum_scaled", "tokens_per_s": B * T / (ms * 1e-3), "avg_ms": ms,
@@ -442,22 +487,29 @@ def main() -> None:
         log(f"copy calibration: {n} bytes read, {n} bytes written")
         del src, dst
 
-    # The other GPU legs run first, so that the headline's timed forwards see the clocks a loaded GPU
-    # runs at (after a cold start the first tens of milliseconds of work run ~10 % slower); the CPU
-    # baselines run last, after every GPU measurement.
-    extra: dict = {}
-    if not args.no_draft:
-        log("draft step")
-        extra["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
+    # Every leg is set up first (host-side model builds take seconds, during which an idle GPU
+    # lowers its clocks); then the GPU legs run back to back and the headline's forwards follow at
+    # once.  The power-hungriest legs (the plain copy, the 13 GB random gather) go first and the
+    # SD-C layer forward, the load most like the headline's, last: after a change of load the GPU's
+    # clocks settle over a few milliseconds, and the headline's first forwards would otherwise run
+    # in that transient (up to ~7 % slower).  The CPU baselines run after every GPU measurement.
+    legs: dict = {}
     if not args.no_scaled:
-        log("scaled-table gather")
-        extra["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 5)
+        log("scaled-table gather: set-up")
+        legs["scaled_gather"] = scaled_gather(dev, max(3, args.steps // 2), 5)
+    if not args.no_draft:
+        log("draft step: set-up")
+        legs["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
     if not args.no_sdc:
-        log("SD-C forward")
-        extra["sdc_forward"] = sdc_forward(dev, max(3, args.steps // 2), 5)
-        log("tiny forward")
-        extra["tiny_forward"] = tiny_forward(dev, 50, 5)
+        log("tiny and SD-C forwards: set-up")
+        legs["tiny_forward"] = tiny_forward(dev, 50, 5)
+        legs["sdc_forward"] = sdc_forward(dev, max(3, args.steps // 2), 5)
+    torch.cuda.synchronize()
     copy_gbs = copy_bandwidth(dev)
+    extra: dict = {}
+    for name, run in legs.items():
+        log(name)
+        extra[name] = run()
 
     with torch.no_grad():
         for _ in range(args.warmup):

@@ -94,6 +94,7 @@ constexpr int WAITCNT_VM0 = 0x0F70;  // s_waitcnt vmcnt(0), expcnt and lgkmcnt l
 // 16-byte device-coherent hand-off through raw buffer operations with the sc1 cache policy (the
 // policy the agent-scope relaxed loads and stores above use), one instruction per 16 bytes.
 constexpr int BUF_DW3 = 0x00020000;  // raw buffer descriptor word 3 (gfx9 family)
+constexpr int CPOL_NT = 2;           // cache policy bit nt (non-temporal)
 constexpr int CPOL_SC1 = 16;         // cache policy bit sc1
 // base and bytes must be the same in every active lane: they are taken from the first one, so the
 // descriptor lives in scalar registers (a per-lane descriptor would serialise every access).

@@ -381,9 +381,21 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
   __shared__ float srow[ROWS];
   const int tid = threadIdx.x, lane = tid & 63;
   const int ngrp = static_cast<int>(blockDim.x >> 4);
-  const int t0 = static_cast<int>(blockIdx.x) * TT;
+  // XCD-aware order: blocks go to the 8 XCDs round-robin (block b to XCD b % 8); when the grid
+  // divides evenly, XCD x takes the x-th eighth of the (sequence, tile) order, so the 9-row causal
+  // halo of a tile was fetched into the same L2 by the tile before it (21.9 -> 20.7 us at
+  // B8 x T2048 x d1024)
+  int tile_t = static_cast<int>(blockIdx.x), tile_b = static_cast<int>(blockIdx.y);
+  const int64_t nb = static_cast<int64_t>(gridDim.x) * gridDim.y;
+  if ((nb & 7) == 0) {
+    const int64_t bid = tile_t + static_cast<int64_t>(gridDim.x) * tile_b;
+    const int64_t tile = (bid & 7) * (nb >> 3) + (bid >> 3);
+    tile_t = static_cast<int>(tile % gridDim.x);
+    tile_b = static_cast<int>(tile / gridDim.x);
+  }
+  const int t0 = tile_t * TT;
   const int T = static_cast<int>(T_len);
-  const size_t row0 = static_cast<size_t>(blockIdx.y) * T_len;
+  const size_t row0 = static_cast<size_t>(tile_b) * T_len;
   const uint32_t d = d4 * 4u;
   const bool active = static_cast<uint32_t>(tid) < d4;
   const uint32_t c = (active ? static_cast<uint32_t>(tid) : 0u) * 4u;

@@ -28,7 +28,7 @@ constexpr int FR_HD = 64;          // head dim
 constexpr int FR_DT = 256;         // route token dim (2 orders x 128)
 constexpr int FR_LD = FR_DT + 8;   // padded LDS row (bf16): 528 B, conflict-free 16-row access
 constexpr int FR_MAXR = 256;       // max routes (row-index slots per token)
-constexpr int FR_RB = FR_MAXR / 2;
+constexpr int FR_RQ = FR_MAXR / 4;
 // packed KV weight (bf16 elements): keys [h 4][ft 16][ks 2][lane 64][8] = Wk^T[h][16ft + lane%16][32ks + 8(lane/16) ..+8],
 // then values [h 4][dt 4][ks 8][lane 64][8] = Wv[h][16dt + lane%16][32ks + 8(lane/16) ..+8]
 constexpr int FR_PK_V = 4 * 16 * 2 * 64 * 8;
@@ -36,8 +36,21 @@ static_assert(2 * FR_PK_V == LNG_READOUT_PACK_ELEMS, "packed KV weight size");
 #ifndef LNG_READOUT_TOK
 #define LNG_READOUT_TOK 4
 #endif
+// Cache policies (measured on the SB-shape forward, 16384 tokens x 184 routes): the 3-gram rows
+// (a 193 MB table, each row met ~4 times per pass) load at device scope (sc1), which reads them
+// without pushing the 2-gram rows (12 MB, each met ~64 times) out of the XCD's L2; the query and
+// raw rows, read once, load non-temporal (nt).  Together 5 us of 244 off the launch; nt on the
+// 3-gram rows (which also gives up their reuse in the Infinity Cache) or on the head stores is slower.
+constexpr int FR_POL_T3 = CPOL_SC1;
+constexpr int FR_POL_STREAM = CPOL_NT;
 
 __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+// 16 bytes of a token-major activation (q, raw rows) at element offset e < 2^31, streamed (nt)
+__device__ __forceinline__ bf16x8 ldq(const bf16* base, int64_t e) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), 0, -1, BUF_DW3);
+  return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<uint32_t>(e) * 2u, 0,
+                                                                          FR_POL_STREAM));
+}
 __device__ __forceinline__ bf16x8 zero8() {
   bf16x8 z;
 #pragma unroll
@@ -71,7 +84,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
                                                           const bf16* __restrict__ w_mem, float eps, float scale,
                                                           float sink, bf16* __restrict__ head_out) {
   __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
-  __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][2][FR_RB];
+  __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][4][FR_RQ];
   __shared__ __attribute__((aligned(16))) bf16 wms[FR_DT];
   __shared__ float qscale[FR_TOK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -86,7 +99,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   if (q_rows) {
 #pragma unroll
     for (int k = 0; k < 2; ++k)
-      hq[k] = tq_own < ntok_all ? ld16(q_rows + tq_own * (FR_H * FR_HD) + 8 * (lane + 64 * k)) : zero8();
+      hq[k] = tq_own < ntok_all ? ldq(q_rows, tq_own * (FR_H * FR_HD) + 8 * (lane + 64 * k)) : zero8();
   }
 
   // phase-A operands first (no dependence on the codes), so their latency overlaps stage 0:
@@ -99,7 +112,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
     const int64_t tq = static_cast<int64_t>(blockIdx.x) * FR_TOK + 4 * tt + (li >> 2);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
-      bq[tt][ks] = tq < B * T ? ld16(q + tq * (FR_H * FR_HD) + a_hg * FR_HD + 32 * ks + 8 * lg) : zero8();
+      bq[tt][ks] = tq < B * T ? ldq(q, tq * (FR_H * FR_HD) + a_hg * FR_HD + 32 * ks + 8 * lg) : zero8();
   }
 #pragma unroll
   for (int ft = 0; ft < NFT; ++ft)
@@ -130,48 +143,57 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
         if (tpos >= 1) r2 = r * 256 + cv[1][k] + 16 * cv[0][k];
         if (tpos >= 2) r3 = r * 4096 + cv[2][k] + 16 * cv[1][k] + 256 * cv[0][k];
       }
-      rowsh[w][0][r & 1][r >> 1] = r2;
-      rowsh[w][1][r & 1][r >> 1] = r3;
+      rowsh[w][0][r & 3][r >> 2] = r2;
+      rowsh[w][1][r & 3][r >> 2] = r3;
     }
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
 
-  // chunk gather: instruction m, lane: route c0 + 2m + lane/32, order (lane/16)&1, 16-byte piece lane%16
-  const int g_ord = (lane >> 4) & 1, g_par = lane >> 5, g_piece = lane & 15;
-  const bf16* g_tab = g_ord ? table3 : table2;
+  // chunk gather: instruction m reads order m & 1 for routes c0 + 4 (m >> 1) + lane / 16, 16-byte
+  // piece lane % 16 (a quarter wave per 256-byte table row); one order per instruction, so that
+  // the 3-gram rows take their own cache policy (FR_POL_T3).
+  const int g_sub = lane >> 4, g_piece = lane & 15;
   // every row of a token at t >= 2 exists (both orders): its loads need no mask
   const bool all_rows = tpos >= 2;
+  // 3-gram rows through a raw buffer descriptor (the table, at most 256 routes x 4096 rows x 256 B,
+  // is < 4 GB, so row * 256 fits the 32-bit offset; every row index is in range, the descriptor's
+  // size is left at its maximum)
+  const __amdgpu_buffer_rsrc_t t3 = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(table3), 0, -1, BUF_DW3);
+  auto row_load = [&](int order, int32_t row) -> u32x4 {
+    if (order == 0) return *reinterpret_cast<const u32x4*>(table2 + static_cast<int64_t>(row) * 128 + 8 * g_piece);
+    return __builtin_amdgcn_raw_buffer_load_b128(t3, static_cast<uint32_t>(row) * 256u + 16u * g_piece, 0, FR_POL_T3);
+  };
   auto gather = [&](int c0, u32x4 (&g)[16]) {
-    const int32_t* rp = &rowsh[w][g_ord][g_par][c0 >> 1];
-    int32_t rows[16];
+    int32_t rows[2][8];  // [order][j]: route c0 + 4j + g_sub
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int32_t __attribute__((ext_vector_type(4))) r4 =
-          *reinterpret_cast<const int32_t __attribute__((ext_vector_type(4)))*>(rp + 4 * v);
-      rows[4 * v] = r4[0];
-      rows[4 * v + 1] = r4[1];
-      rows[4 * v + 2] = r4[2];
-      rows[4 * v + 3] = r4[3];
+    for (int o = 0; o < 2; ++o) {
+      const int32_t* rp = &rowsh[w][o][g_sub][c0 >> 2];
+#pragma unroll
+      for (int v = 0; v < 2; ++v) {
+        const int32_t __attribute__((ext_vector_type(4))) r4 =
+            *reinterpret_cast<const int32_t __attribute__((ext_vector_type(4)))*>(rp + 4 * v);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) rows[o][4 * v + e] = r4[e];
+      }
     }
     if (all_rows) {
       // routes past R hold row -1 too: clamp them to row 0 (their scores are masked below)
 #pragma unroll
-      for (int m = 0; m < 16; ++m)
-        g[m] = *reinterpret_cast<const u32x4*>(g_tab + static_cast<int64_t>(max(rows[m], 0)) * 128 + 8 * g_piece);
+      for (int m = 0; m < 16; ++m) g[m] = row_load(m & 1, max(rows[m & 1][m >> 1], 0));
     } else {
 #pragma unroll
       for (int m = 0; m < 16; ++m) {
         const u32x4 z = {0u, 0u, 0u, 0u};
-        g[m] = rows[m] >= 0 ? *reinterpret_cast<const u32x4*>(g_tab + static_cast<int64_t>(rows[m]) * 128 + 8 * g_piece)
-                            : z;
+        const int32_t row = rows[m & 1][m >> 1];
+        g[m] = row >= 0 ? row_load(m & 1, row) : z;
       }
     }
   };
   auto stash = [&](const u32x4 (&g)[16]) {
 #pragma unroll
     for (int m = 0; m < 16; ++m)
-      *reinterpret_cast<u32x4*>(&xs[w][2 * m + g_par][g_ord * 128 + 8 * g_piece]) = g[m];
+      *reinterpret_cast<u32x4*>(&xs[w][4 * (m >> 1) + g_sub][(m & 1) * 128 + 8 * g_piece]) = g[m];
   };
 
   u32x4 g[16];
@@ -379,6 +401,9 @@ extern "C" int lng_memory_readout_fused(const void* q, const void* q_rows, float
   if (ntok == 0) return LNG_OK;
   const int64_t blocks = cdiv(ntok, FR_TOK);
   if (blocks > 0x7fffffffLL) return fail(LNG_E_ARG, "memory_readout_fused: too many tokens");
+  // buffer offsets are 32-bit: the token-major activations (2 KB per token) stay under 4 GB; the
+  // 3-gram table (R <= 256 routes x 4096 rows x 256 B) always does
+  if (ntok > (int64_t{1} << 21)) return fail(LNG_E_ARG, "memory_readout_fused: more than 2^21 tokens per launch");
   hipLaunchKernelGGL(k_readout_fused<FR_TOK>, dim3(static_cast<unsigned>(blocks)), dim3(64 * FR_TOK), 0,
                      as_stream(stream), static_cast<const bf16*>(q), static_cast<const bf16*>(q_rows), q_eps, codes,
                      B, T, R, static_cast<const bf16*>(table2),

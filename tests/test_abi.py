@@ -72,6 +72,10 @@ def test_version_and_argument_errors(lib):
     rc = lib.lng_route_tokens(None, 3, 1, 4, 2, 0, 2, (ctypes.c_int32 * 1)(2), 1, 4, None, 1, 8, None, None, 9,
                               None, None)
     assert rc == -1 and b"target_length" in lib.lng_last_error()
+    # the fused readout's 32-bit buffer offsets bound a launch to 2^21 tokens
+    rc = lib.lng_memory_readout_fused(None, None, 0.0, None, 2, (1 << 20) + 1, 184, None, None, None, None, 1e-6,
+                                      0.125, 0.0, None, None)
+    assert rc == -1 and b"2^21 tokens" in lib.lng_last_error()
 
 
 def test_error_message_is_thread_local(lib):
