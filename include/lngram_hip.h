@@ -342,6 +342,32 @@ int lng_drafter_readout(const lng_drafter* D, const int32_t* windows, int32_t P,
  * (tree_route_tokens, drafting/tree.py:130-136; window_route_tokens, drafters.py:110-114). */
 int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, void* out, void* stream);
 
+/* Count sketches of the drafter's orders (drafting/sketches.py:1-12, bundle arrays sketch_ids_<n>,
+ * sketch_counts_<n>, fallback; export_drafter.py:33-34), on the device. */
+typedef struct lng_sketch {
+  const int32_t* ids[4];      /* per order index i (orders[i]): [R * 2^(bits*n), k] token ids, or null */
+  const int64_t* counts[4];   /* same shape: counts, 0 = empty slot (null with ids)                    */
+  int32_t k;                  /* slots per row                                                         */
+  int32_t cap;                /* shortlist length, 1 .. 256                                            */
+  const int32_t* fallback;    /* [n_fallback] padding tokens in order                                  */
+  int32_t n_fallback;         /* 0 .. 1024                                                             */
+} lng_sketch;
+
+/* Sketch-shortlist drafts (RefDrafter._shortlist + _readout + draft's top-k, cpu_drafter.py:179-206,
+ * :238-262; drafter.cpp:438-474) of P positions given their full-vocabulary logits [P, V] and
+ * full-vocabulary top-k (ids / scores [P, k], from lng_drafter_readout with the same k): the
+ * candidates are the tokens of the positions' sketch rows with counts summed per token, ordered
+ * by (total desc, id asc) and cut to cap, padded with fallback tokens not yet present (ids outside
+ * [0, V) are skipped); ids/scores [P, k] are their top-k logits, ties in candidate order; an empty
+ * list keeps the full-vocabulary top-k.  shortlist [P, cap] int32 / shortlist_logits [P, cap]
+ * (optional) receive the list (-1 / -inf pad; an empty list gives tokens 0 .. cap-1, as
+ * RefDrafter.trace).  Children as lng_drafter_readout.  Needs n_orders * R * k <= 8192, R <= 256. */
+int lng_drafter_shortlist(const lng_drafter* D, const lng_sketch* S, const int32_t* windows, int32_t P,
+                          const float* logits, const int64_t* full_ids, const float* full_scores, int32_t k,
+                          const int32_t* child_rows, const int32_t* child_parent, const int32_t* child_rank,
+                          int32_t n_children, int64_t* ids, float* scores, int32_t* shortlist,
+                          float* shortlist_logits, void* stream);
+
 /* One draft-tree step (draft_tree, drafting/tree.py:243-257, batched by depth): node 0 is the
  * last committed token, node i >= 1 lives at absolute row node_row0 + i; parent/rank (host, n
  * <= 64) as TreeSpec (tree.py:37-51).  Every parent's readout of one depth runs together;
@@ -352,6 +378,13 @@ int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, 
 int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n, int32_t node_row0,
                      int online, float kappa, void* work, size_t work_bytes, int32_t* counts, void* route_tokens,
                      void* stream);
+
+/* lng_drafter_tree with the sketch shortlist choosing every child (draft_tree over a RefDrafter
+ * whose draft() scores the shortlist, tree.py:243-257 with cpu_drafter.py:238-262); no online
+ * counts.  logits_work: device fp32 [16, V] scratch. */
+int lng_drafter_tree_shortlist(const lng_drafter* D, const lng_sketch* S, const int32_t* parent, const int32_t* rank,
+                               int32_t n, int32_t node_row0, void* work, size_t work_bytes, float* logits_work,
+                               void* route_tokens, void* stream);
 
 /* The whole draft tree of lng_drafter_tree in ONE cooperative launch (token-only drafters with
  * the per-token tables, bf16 tables, R <= 192, <= 2 orders, q_heads <= 8, q_heads*Dt <= 1024,

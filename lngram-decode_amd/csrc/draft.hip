@@ -702,6 +702,219 @@ __global__ __launch_bounds__(256) void k_draft_select(lng_drafter D, int32_t K, 
   }
 }
 
+// ------------------------------------------------------------------ sketch shortlist
+// RefDrafter._shortlist + _readout (cpu_drafter.py:179-206, :238-244; drafter.cpp:438-474): the
+// candidates of a position are the tokens of its rows' count-sketch slots (every order with a
+// sketch, every route), each with its counts summed over the slots that name it; ordered by
+// (total desc, id asc) and cut to `cap`, then padded with the fallback tokens not yet present, in
+// their order.  The drafts are the top-k of the candidates' logits, ties in candidate order (a
+// stable descending sort); an empty list scores the whole vocabulary.  One block per position:
+// the slots (n_orders * R * K <= 8192) are summed per token in an LDS hash table (open addressing
+// keyed by token id, 64-bit totals), then the list is taken one maximum at a time.
+constexpr int SL_SLOTS = 8192;
+constexpr int SL_MAXCAP = 256;
+constexpr int SL_MAXFB = 1024;
+constexpr int SL_MAXR = 256;
+constexpr int32_t SL_EMPTY = -1;
+constexpr int32_t SL_TAKEN = 0x40000000;  // flag on a slot's id once the token is in the list
+
+struct SlArgs {
+  const int32_t* ids[DR_MAXN];     // per order index: [R * 2^(bits*n), K] token ids (null: no sketch)
+  const int64_t* counts[DR_MAXN];  // same shape: counts (0 = empty slot)
+  const int32_t* fallback;
+  int32_t K, cap, n_fallback;
+};
+
+__device__ __forceinline__ uint32_t sl_hash(int32_t id) {
+  return (static_cast<uint32_t>(id) * 2654435761u) >> (32 - 13);  // 13 bits: SL_SLOTS
+}
+
+// (total, id) a beats (total b, id b): larger total, then smaller id
+__device__ __forceinline__ bool sl_better(unsigned long long ta, int32_t ia, unsigned long long tb, int32_t ib) {
+  return ta > tb || (ta == tb && ia < ib);
+}
+
+__global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W, SlArgs S,
+                                                         const float* __restrict__ logits,
+                                                         const int64_t* __restrict__ full_ids,
+                                                         const float* __restrict__ full_sc, int32_t K, DrChildren C,
+                                                         int64_t* __restrict__ ids, float* __restrict__ scores,
+                                                         int32_t* __restrict__ sl_out, float* __restrict__ sll_out) {
+  __shared__ int32_t hkey[SL_SLOTS];
+  __shared__ unsigned long long hval[SL_SLOTS];
+  __shared__ int64_t rowsh[DR_MAXN][SL_MAXR];
+  __shared__ int32_t fb[SL_MAXFB];
+  __shared__ int32_t sl[SL_MAXCAP];
+  __shared__ float sll[SL_MAXCAP];
+  __shared__ int32_t slot_rows[DR_MAXN];
+  __shared__ unsigned long long red_t[4];
+  __shared__ int32_t red_i[4], red_s[4];
+  __shared__ int64_t sel_id[DR_MAXK];
+  __shared__ float sel_sc[DR_MAXK];
+  const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int L = *D.length;
+  const int R = D.R, SK = S.K, cap = S.cap;
+  for (int e = tid; e < SL_SLOTS; e += 256) {
+    hkey[e] = SL_EMPTY;
+    hval[e] = 0ull;
+  }
+  for (int e = tid; e < S.n_fallback; e += 256) fb[e] = S.fallback[e];
+  if (tid < DR_MAXN) slot_rows[tid] = tid < D.maxn ? dr_resolve(W.slot[j][tid], L) : -1;
+  __syncthreads();
+  for (int e = tid; e < D.n_orders * R; e += 256) {
+    const int o = e / R, r = e % R;
+    rowsh[o][r] = S.ids[o] ? dr_row(D, slot_rows, o, r) : -1;
+  }
+  __syncthreads();
+  // sum the counts per token (at most SL_SLOTS distinct tokens: every probe sequence ends)
+  const int M = D.n_orders * R * SK;
+  for (int e = tid; e < M; e += 256) {
+    const int o = e / (R * SK), rem = e % (R * SK), r = rem / SK, q = rem % SK;
+    const int64_t row = rowsh[o][r];
+    if (row < 0) continue;
+    const int64_t cnt = S.counts[o][row * SK + q];
+    const int32_t id = S.ids[o][row * SK + q];
+    if (cnt <= 0 || id < 0 || id >= D.V) continue;
+    uint32_t h = sl_hash(id);
+    for (;;) {
+      const int32_t prev = atomicCAS(&hkey[h], SL_EMPTY, id);
+      if (prev == SL_EMPTY || prev == id) break;
+      h = (h + 1) & (SL_SLOTS - 1);
+    }
+    atomicAdd(&hval[h], static_cast<unsigned long long>(cnt));
+  }
+  __syncthreads();
+  // the list: one maximum of (total desc, id asc) at a time
+  int m = 0;
+  for (; m < cap; ++m) {
+    unsigned long long bt = 0ull;
+    int32_t bi = INT_MAX, bs = -1;
+    for (int e = tid; e < SL_SLOTS; e += 256) {
+      const int32_t k = hkey[e];
+      if (k < 0 || (k & SL_TAKEN)) continue;
+      if (sl_better(hval[e], k, bt, bi)) {
+        bt = hval[e];
+        bi = k;
+        bs = e;
+      }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      const unsigned long long ot = __shfl_xor(bt, off, 64);
+      const int32_t oi = __shfl_xor(bi, off, 64), os = __shfl_xor(bs, off, 64);
+      if (sl_better(ot, oi, bt, bi)) {
+        bt = ot;
+        bi = oi;
+        bs = os;
+      }
+    }
+    if (lane == 0) {
+      red_t[w] = bt;
+      red_i[w] = bi;
+      red_s[w] = bs;
+    }
+    __syncthreads();
+    bt = red_t[0];
+    bi = red_i[0];
+    bs = red_s[0];
+    for (int q = 1; q < 4; ++q)
+      if (sl_better(red_t[q], red_i[q], bt, bi)) {
+        bt = red_t[q];
+        bi = red_i[q];
+        bs = red_s[q];
+      }
+    __syncthreads();
+    if (bs < 0) break;  // no candidate left (uniform)
+    if (tid == 0) {
+      sl[m] = bi;
+      hkey[bs] = bi | SL_TAKEN;
+    }
+    __syncthreads();
+  }
+  // fallback padding: first occurrences not in the list, in order
+  int added = 0;
+  for (int f0 = 0; f0 < S.n_fallback && m + added < cap; f0 += 256) {
+    const int jf = f0 + tid;
+    bool ok = false;
+    int32_t f = -1;
+    if (jf < S.n_fallback) {
+      f = fb[jf];
+      ok = f >= 0 && f < D.V;
+      if (ok) {
+        uint32_t h = sl_hash(f);
+        for (;;) {
+          const int32_t k = hkey[h];
+          if (k == SL_EMPTY) break;
+          if ((k & ~SL_TAKEN) == f) {
+            ok = !(k & SL_TAKEN);
+            break;
+          }
+          h = (h + 1) & (SL_SLOTS - 1);
+        }
+      }
+      for (int i = 0; ok && i < jf; ++i) ok = fb[i] != f;
+    }
+    const unsigned long long bal = __ballot(ok);
+    const int before = __popcll(bal & ((1ull << lane) - 1ull));
+    if (lane == 0) red_s[w] = __popcll(bal);
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int q = 0; q < 4; ++q) {
+      base += q < w ? red_s[q] : 0;
+      tot += red_s[q];
+    }
+    if (ok) {
+      const int pos = m + added + base + before;
+      if (pos < cap) sl[pos] = f;
+    }
+    added += tot;
+    __syncthreads();
+  }
+  const int n_sl = min(cap, m + added);
+  const float* lg = logits + static_cast<int64_t>(j) * D.V;
+  for (int i = tid; i < cap; i += 256) {
+    int32_t id = -1;
+    if (n_sl > 0)
+      id = i < n_sl ? sl[i] : -1;
+    else
+      id = i < D.V ? i : -1;  // empty list: the whole vocabulary, cut to cap
+    const float v = id >= 0 ? lg[id] : -INFINITY;
+    sll[i] = v;
+    if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = id;
+    if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = v;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    if (n_sl == 0) {
+      for (int q = 0; q < K; ++q) {
+        sel_id[q] = full_ids[static_cast<int64_t>(j) * K + q];
+        sel_sc[q] = full_sc[static_cast<int64_t>(j) * K + q];
+      }
+    } else {
+      uint32_t used[SL_MAXCAP / 32] = {};
+      for (int q = 0; q < K; ++q) {
+        int best = -1;
+        for (int i = 0; i < n_sl; ++i) {
+          if ((used[i >> 5] >> (i & 31)) & 1u) continue;
+          if (best < 0 || sll[i] > sll[best]) best = i;  // strict: ties keep candidate order
+        }
+        if (best >= 0) used[best >> 5] |= 1u << (best & 31);
+        sel_id[q] = best >= 0 ? sl[best] : -1;
+        sel_sc[q] = best >= 0 ? sll[best] : -INFINITY;
+      }
+    }
+  }
+  __syncthreads();
+  if (tid < K) {
+    ids[static_cast<int64_t>(j) * K + tid] = sel_id[tid];
+    scores[static_cast<int64_t>(j) * K + tid] = sel_sc[tid];
+  }
+  for (int e = tid; e < C.n; e += 256) {
+    if (C.parent[e] != j) continue;
+    const int64_t t = sel_id[C.rank[e]];
+    D.tokens[C.row[e]] = t >= 0 ? t : sel_id[0];
+  }
+}
+
 // tokens[dst] = tokens[L - 1] (the root of a draft tree next to its nodes).
 __global__ void k_draft_root_copy(lng_drafter D, int32_t dst) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -2892,6 +3105,37 @@ int tp_plan(const lng_drafter& D, const int32_t* parent, const int32_t* rank, in
   return LNG_OK;
 }
 
+// Sketch arguments of the shortlist launches, checked against the drafter's shape.
+int sl_args(const lng_drafter& D, const lng_sketch* S, SlArgs& A) {
+  if (!S) return fail(LNG_E_ARG, "drafter_shortlist: null sketch");
+  if (S->cap < 1 || S->cap > SL_MAXCAP) return fail(LNG_E_ARG, "drafter_shortlist: 1 <= cap <= 256");
+  if (S->n_fallback < 0 || S->n_fallback > SL_MAXFB || (S->n_fallback && !S->fallback))
+    return fail(LNG_E_ARG, "drafter_shortlist: 0 <= n_fallback <= 1024");
+  if (S->k < 1 || D.R > SL_MAXR || static_cast<int64_t>(D.n_orders) * D.R * S->k > SL_SLOTS)
+    return fail(LNG_E_ARG, "drafter_shortlist: n_orders * R * k must be <= 8192 (R <= 256)");
+  if (D.V > SL_TAKEN) return fail(LNG_E_ARG, "drafter_shortlist: vocabulary must be below 2^30");
+  A = SlArgs{};
+  for (int o = 0; o < D.n_orders; ++o) {
+    if ((S->ids[o] == nullptr) != (S->counts[o] == nullptr))
+      return fail(LNG_E_ARG, "drafter_shortlist: an order's ids and counts come together");
+    A.ids[o] = S->ids[o];
+    A.counts[o] = S->counts[o];
+  }
+  A.fallback = S->fallback;
+  A.K = S->k;
+  A.cap = S->cap;
+  A.n_fallback = S->n_fallback;
+  return LNG_OK;
+}
+
+int dr_shortlist(const lng_drafter& D, const DrWin& W, const SlArgs& A, const float* logits, const int64_t* full_ids,
+                 const float* full_sc, int K, const DrChildren& C, int64_t* ids, float* scores, hipStream_t s,
+                 int32_t* sl = nullptr, float* sll = nullptr) {
+  hipLaunchKernelGGL(k_draft_shortlist, dim3(static_cast<unsigned>(W.n)), dim3(256), 0, s, D, W, A, logits, full_ids,
+                     full_sc, K, C, ids, scores, sl, sll);
+  return check_launch("drafter_shortlist");
+}
+
 }  // namespace
 
 }  // namespace lng
@@ -2966,6 +3210,34 @@ int lng_drafter_readout(const lng_drafter* D, const int32_t* windows, int32_t P,
                     as_stream(stream));
 }
 
+int lng_drafter_shortlist(const lng_drafter* D, const lng_sketch* S, const int32_t* windows, int32_t P,
+                          const float* logits, const int64_t* full_ids, const float* full_scores, int32_t k,
+                          const int32_t* child_rows, const int32_t* child_parent, const int32_t* child_rank,
+                          int32_t n_children, int64_t* ids, float* scores, int32_t* shortlist,
+                          float* shortlist_logits, void* stream) {
+  if (int rc = dr_check(D, "drafter_shortlist")) return rc;
+  if (!logits || !full_ids || !full_scores || !ids || !scores || !windows)
+    return fail(LNG_E_ARG, "drafter_shortlist: null argument");
+  if (k <= 0 || k > DR_MAXK) return fail(LNG_E_ARG, "drafter_shortlist: 1 <= k <= 8");
+  SlArgs A{};
+  if (int rc = sl_args(*D, S, A)) return rc;
+  DrWin W;
+  if (int rc = dr_windows(*D, windows, P, W)) return rc;
+  if (n_children < 0 || n_children > DR_MAXCH) return fail(LNG_E_ARG, "drafter_shortlist: at most 64 children");
+  DrChildren C{};
+  C.n = n_children;
+  for (int e = 0; e < n_children; ++e) {
+    if (child_rows[e] < 0 || child_rows[e] >= D->rows || child_parent[e] < 0 || child_parent[e] >= P ||
+        child_rank[e] < 0 || child_rank[e] >= k)
+      return fail(LNG_E_RANGE, "drafter_shortlist: bad child");
+    C.row[e] = child_rows[e];
+    C.parent[e] = static_cast<int8_t>(child_parent[e]);
+    C.rank[e] = static_cast<int8_t>(child_rank[e]);
+  }
+  return dr_shortlist(*D, W, A, logits, full_ids, full_scores, k, C, ids, scores, as_stream(stream), shortlist,
+                      shortlist_logits);
+}
+
 int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, void* out, void* stream) {
   if (int rc = dr_check(D, "drafter_gather")) return rc;
   if (!out || !windows) return fail(LNG_E_ARG, "drafter_gather: null pointer");
@@ -2974,10 +3246,12 @@ int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, 
   return dr_gather(*D, W, out, as_stream(stream));
 }
 
-int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n, int32_t node_row0,
-                     int online, float kappa, void* work, size_t work_bytes, int32_t* counts, void* route_tokens,
-                     void* stream) {
-  if (int rc = dr_check(D, "drafter_tree")) return rc;
+// Draft-tree driver of lng_drafter_tree and lng_drafter_tree_shortlist: with a sketch (sk), each
+// depth's readout leaves its full-vocabulary logits in sl_logits and the shortlist kernel picks
+// the children's tokens.
+static int dr_tree(const lng_drafter* D, const SlArgs* sk, float* sl_logits, const int32_t* parent,
+                   const int32_t* rank, int32_t n, int32_t node_row0, int online, float kappa, void* work,
+                   size_t work_bytes, int32_t* counts, void* route_tokens, void* stream) {
   if (!parent || !rank || n <= 0 || n > DR_MAXCH || parent[0] != -1)
     return fail(LNG_E_ARG, "drafter_tree: need 1 <= n <= 64 nodes with parent[0] == -1");
   if (node_row0 < 0 || static_cast<int64_t>(node_row0) + n > D->rows)
@@ -3044,9 +3318,16 @@ int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t*
           F.fresh[j] = coded[i] ? 0 : 1;
           coded[i] = 1;
         }
-        if (int rc = dr_readout_fast(*D, F, K, online, kappa, C, static_cast<char*>(work), need, counts, lvl_ids,
-                                     lvl_sc, nullptr, s))
+        if (int rc = dr_readout_fast(*D, F, K, online, kappa, sk ? DrChildren{} : C, static_cast<char*>(work), need,
+                                     counts, lvl_ids, lvl_sc, sk ? sl_logits : nullptr, s))
           return rc;
+        if (sk) {
+          DrWin W{};
+          W.n = P;
+          for (int j = 0; j < P; ++j)
+            for (int k = 0; k < DR_MAXN; ++k) W.slot[j][k] = F.slot[j][k];
+          if (int rc = dr_shortlist(*D, W, *sk, sl_logits, lvl_ids, lvl_sc, K, C, lvl_ids, lvl_sc, s)) return rc;
+        }
         continue;
       }
       // codes of the parents of this depth (their tokens were chosen one depth up)
@@ -3067,9 +3348,11 @@ int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t*
         window(parents[p0 + j], win.data());
         for (int k = 0; k < D->maxn; ++k) W.slot[j][k] = win[k];
       }
-      if (int rc = dr_readout(*D, W, K, online, kappa, C, static_cast<char*>(work), need, counts, lvl_ids, lvl_sc,
-                              nullptr, s))
+      if (int rc = dr_readout(*D, W, K, online, kappa, sk ? DrChildren{} : C, static_cast<char*>(work), need, counts,
+                              lvl_ids, lvl_sc, sk ? sl_logits : nullptr, s))
         return rc;
+      if (sk)
+        if (int rc = dr_shortlist(*D, W, *sk, sl_logits, lvl_ids, lvl_sc, K, C, lvl_ids, lvl_sc, s)) return rc;
     }
   }
   if (fast && route_tokens) {
@@ -3129,6 +3412,25 @@ int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t*
     }
   }
   return LNG_OK;
+}
+
+int lng_drafter_tree(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n, int32_t node_row0,
+                     int online, float kappa, void* work, size_t work_bytes, int32_t* counts, void* route_tokens,
+                     void* stream) {
+  if (int rc = dr_check(D, "drafter_tree")) return rc;
+  return dr_tree(D, nullptr, nullptr, parent, rank, n, node_row0, online, kappa, work, work_bytes, counts, route_tokens,
+                 stream);
+}
+
+int lng_drafter_tree_shortlist(const lng_drafter* D, const lng_sketch* S, const int32_t* parent, const int32_t* rank,
+                               int32_t n, int32_t node_row0, void* work, size_t work_bytes, float* logits_work,
+                               void* route_tokens, void* stream) {
+  if (int rc = dr_check(D, "drafter_tree_shortlist")) return rc;
+  SlArgs A{};
+  if (int rc = sl_args(*D, S, A)) return rc;
+  if (!logits_work) return fail(LNG_E_ARG, "drafter_tree_shortlist: logits_work [16, V] needed");
+  return dr_tree(D, &A, logits_work, parent, rank, n, node_row0, 0, 0.f, work, work_bytes, nullptr, route_tokens,
+                 stream);
 }
 
 size_t lng_drafter_tree_fused_workspace(const lng_drafter* D) {

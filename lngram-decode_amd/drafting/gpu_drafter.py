@@ -6,8 +6,10 @@ trace``, ``DraftOut``) with every per-token step on the GPU (``lng_drafter_*`` i
 Per token, as ``cpu_drafter.py:13-28`` describes: SSM step, router codes from
 ``concat(RMSNorm(E[x_{t-1}] or start), RMSNorm(E[x_t])[, s_t])``, the v2 n-gram rows, the draft
 readout over the shared table (memory norm, KV projection, sink softmax over routes, ``W_o``,
-RMSNorm) and logits against the tied embedding, top-k by (logit desc, id asc).  Scoring is over
-the full vocabulary (the sketch shortlist is not part of this drafter).  With ``online=True``
+RMSNorm) and logits against the tied embedding, top-k by (logit desc, id asc).  With count
+sketches in the bundle and a positive ``shortlist_cap`` the drafts are scored over the sketch
+shortlist instead (``cpu_drafter.py:179-206``: sketch tokens of the position's rows by summed
+count, padded with the fallback tokens; ``lng_drafter_shortlist``).  With ``online=True``
 the draft distribution is mixed with code-keyed online counts over the committed
 (row at t, token t+1) pairs (``drafting/drafters.py:117-142``); candidates are then ranked by,
 and ``topk_logits`` holds, the log of the mixed probability.
@@ -61,11 +63,12 @@ class GpuDrafter:
         c, t = _bundle_parts(bundle)
         self.cfg = c
         # RefDrafter scores a sketch shortlist when the cap is positive and the bundle carries
-        # sketches (cpu_drafter.py:105, :179-181); this drafter scores the full vocabulary only.
+        # sketches (cpu_drafter.py:102-105, :179-181)
         cap = int(c.get("shortlist_cap", 0) if shortlist_cap is None else shortlist_cap)
-        if cap > 0 and any(f"sketch_ids_{n}" in t for n in c["ngrams"]):
-            raise NotImplementedError("sketch shortlist scoring is not on this path: the GPU drafter scores the "
-                                      "full vocabulary; pass shortlist_cap=0 for full-vocabulary drafting")
+        self.cap = cap if cap > 0 and any(f"sketch_ids_{n}" in t for n in c["ngrams"]) else 0
+        if self.cap and online:
+            raise ValueError("the sketch shortlist and online counts do not combine (RefDrafter scores the "
+                             "shortlist without online counts)")
         self.topk = int(topk)
         self.online, self.kappa = bool(online), float(kappa)
         dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
@@ -99,6 +102,7 @@ class GpuDrafter:
                 x = x.float()
             return x.to(dev).contiguous()
 
+        self.sketch = self._load_sketch(t, dev) if self.cap else None
         self.emb = keep("embedding")
         self.tables = [keep(f"table_{n}") for n in self.ngrams]
         if len({x.dtype for x in self.tables}) != 1:
@@ -135,13 +139,56 @@ class GpuDrafter:
         self._tree_seq = 0
         self._fused_specs: dict = {}
         self._graphs: dict = {}          # (parent, rank, route_tokens) -> (captured tree step, out)
-        if fused and self.luts is not None:
+        if fused and self.luts is not None and self.sketch is None:
             fb = self.lib.lng_drafter_tree_fused_workspace(ctypes.byref(self.D))
             if fb:
                 self.tree_work = torch.zeros(int(fb), dtype=torch.uint8, device=dev)
         self.ids_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.int64, device=dev)
         self.sc_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.float32, device=dev)
+        if self.sketch is not None:
+            # full-vocabulary logits and top-k of up to 16 positions (the shortlist kernel's inputs)
+            self.sl_lg = torch.empty(16, self.V, dtype=torch.float32, device=dev)
+            self.sl_fid = torch.empty(16 * _MAX_K, dtype=torch.int64, device=dev)
+            self.sl_fsc = torch.empty(16 * _MAX_K, dtype=torch.float32, device=dev)
         self.reset()
+
+    def _load_sketch(self, t: dict, dev) -> _lib.Sketch:
+        """Device copies of the bundle's count sketches (ids int32, counts int64) and fallback list,
+        and their ``lng_sketch`` descriptor."""
+
+        def host(x) -> np.ndarray:
+            return np.asarray(x.cpu() if torch.is_tensor(x) else x)
+
+        S = _lib.Sketch()
+        keep = []
+        k = None
+        for i, n in enumerate(self.ngrams):
+            if f"sketch_ids_{n}" not in t:
+                continue
+            ids, cnt = host(t[f"sketch_ids_{n}"]), host(t[f"sketch_counts_{n}"])
+            rows = self.R * (1 << (self.bits * n))
+            if ids.ndim != 2 or ids.shape[0] != rows or cnt.shape != ids.shape:
+                raise ValueError(f"sketch of order {n} must be [{rows}, K] ids and counts")
+            if k is not None and ids.shape[1] != k:
+                raise ValueError("every order's sketch must have the same K")
+            k = ids.shape[1]
+            ids_d = torch.from_numpy(ids.astype(np.int32)).to(dev)
+            cnt_d = torch.from_numpy(cnt.astype(np.int64)).to(dev)
+            keep += [ids_d, cnt_d]
+            S.ids[i], S.counts[i] = ids_d.data_ptr(), cnt_d.data_ptr()
+        fb = t.get("fallback")
+        fb = np.zeros(0, np.int32) if fb is None else host(fb).ravel()
+        if len(fb) > 1024:
+            raise ValueError("at most 1024 fallback tokens")
+        fb_d = torch.from_numpy(fb.astype(np.int32)).to(dev) if len(fb) else torch.zeros(1, dtype=torch.int32,
+                                                                                          device=dev)
+        keep.append(fb_d)
+        S.k, S.cap, S.fallback, S.n_fallback = int(k), self.cap, fb_d.data_ptr(), len(fb)
+        if len(self.ngrams) * self.R * int(k) > 8192 or self.R > 256 or self.cap > 256:
+            raise NotImplementedError("the shortlist kernel takes n_orders * R * K <= 8192 sketch slots per "
+                                      "position, R <= 256 and a cap <= 256")
+        self._sketch_keep = keep
+        return S
 
     # ------------------------------------------------------------------ set-up
     def _compose(self, t: dict, dev) -> None:
@@ -338,9 +385,18 @@ class GpuDrafter:
                 child = i + 1 < gamma or last_codes
                 win = self._i32(self._window(seq))
                 cr, cp, ck = self._i32([nxt]), self._i32([0]), self._i32([0])
-                check(lib.lng_drafter_readout(Dp, win, 1, k, int(self.online), self.kappa, cr, cp, ck, int(child), wp,
-                                              wb, self.counts.data_ptr(), self.ids_d[i].data_ptr(),
-                                              self.sc_d[i].data_ptr(), None, st), "drafter readout")
+                if self.sketch is None:
+                    check(lib.lng_drafter_readout(Dp, win, 1, k, int(self.online), self.kappa, cr, cp, ck, int(child),
+                                                  wp, wb, self.counts.data_ptr(), self.ids_d[i].data_ptr(),
+                                                  self.sc_d[i].data_ptr(), None, st), "drafter readout")
+                else:
+                    check(lib.lng_drafter_readout(Dp, win, 1, k, 0, 0.0, None, None, None, 0, wp, wb, None,
+                                                  self.sl_fid.data_ptr(), self.sl_fsc.data_ptr(),
+                                                  self.sl_lg.data_ptr(), st), "drafter readout")
+                    check(lib.lng_drafter_shortlist(Dp, ctypes.byref(self.sketch), win, 1, self.sl_lg.data_ptr(),
+                                                    self.sl_fid.data_ptr(), self.sl_fsc.data_ptr(), k, cr, cp, ck,
+                                                    int(child), self.ids_d[i].data_ptr(), self.sc_d[i].data_ptr(),
+                                                    None, None, st), "drafter shortlist")
                 if child:
                     check(lib.lng_drafter_advance(Dp, self._i32([nxt]), self._i32([seq[-1]]), 1, 1, wp, wb, st),
                           "drafter advance")
@@ -401,6 +457,13 @@ class GpuDrafter:
                 self._fused_specs[key] = True
                 return self.tok_d[self.tree_row0: self.tree_row0 + n], out
             self._fused_specs[key] = False     # tree outside the one-launch limits: per-depth launches
+        if self.sketch is not None:
+            check(self.lib.lng_drafter_tree_shortlist(ctypes.byref(self.D), ctypes.byref(self.sketch), parent, rank, n,
+                                                      self.tree_row0, self.work.data_ptr(), self.work.numel(),
+                                                      self.sl_lg.data_ptr(),
+                                                      out.data_ptr() if out is not None else None, self._stream()),
+                  "drafter tree")
+            return self.tok_d[self.tree_row0: self.tree_row0 + n], out
         check(self.lib.lng_drafter_tree(ctypes.byref(self.D), parent, rank, n, self.tree_row0, int(self.online),
                                         self.kappa, self.work.data_ptr(), self.work.numel(), self.counts.data_ptr(),
                                         out.data_ptr() if out is not None else None, self._stream()),
@@ -419,8 +482,10 @@ class GpuDrafter:
         return 0
 
     def trace(self, tokens, codes=None, full: bool = False):
-        """Teacher-forced pass from an empty state: (codes [T, R] uint8, ids [T, V] int64,
-        logits [T, V] fp32) over the full vocabulary.  The committed state is untouched."""
+        """Teacher-forced pass from an empty state: (codes [T, R] uint8, ids [T, S] int64,
+        logits [T, S] fp32), S = the vocabulary, or the shortlist cap when the drafter scores a
+        sketch shortlist and ``full`` is off (``RefDrafter.trace``, ``cpu_drafter.py:272-289``:
+        candidate order, -1 / -inf pad).  The committed state is untouched."""
         toks = self._check_tokens(tokens)
         T = len(toks)
         dev = self.device
@@ -432,6 +497,12 @@ class GpuDrafter:
         logits = torch.empty(T, self.V, dtype=torch.float32, device=dev)
         ids = torch.empty(16, 1, dtype=torch.int64, device=dev)
         sc = torch.empty(16, 1, dtype=torch.float32, device=dev)
+        short = self.sketch is not None and not full
+        if short:
+            sl = torch.empty(max(T, 1), self.cap, dtype=torch.int32, device=dev)
+            sll = torch.empty(max(T, 1), self.cap, dtype=torch.float32, device=dev)
+            ids2 = torch.empty(16, 1, dtype=torch.int64, device=dev)
+            sc2 = torch.empty(16, 1, dtype=torch.float32, device=dev)
         nbytes = self.lib.lng_drafter_workspace_bytes(ctypes.byref(D), 16, 1, max(T, 1))
         work = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
         st = self._stream()
@@ -455,7 +526,14 @@ class GpuDrafter:
                 check(self.lib.lng_drafter_readout(ctypes.byref(D), self._i32(win), P, 1, 0, 0.0, None, None, None, 0,
                                                    work.data_ptr(), work.numel(), None, ids.data_ptr(), sc.data_ptr(),
                                                    logits[t0].data_ptr(), st), "drafter trace")
+                if short:
+                    check(self.lib.lng_drafter_shortlist(ctypes.byref(D), ctypes.byref(self.sketch), self._i32(win), P,
+                                                         logits[t0].data_ptr(), ids.data_ptr(), sc.data_ptr(), 1, None,
+                                                         None, None, 0, ids2.data_ptr(), sc2.data_ptr(),
+                                                         sl[t0].data_ptr(), sll[t0].data_ptr(), st), "drafter trace")
             out_c = cod[:T].cpu().numpy()
+            if short:
+                return out_c, sl[:T].long().cpu().numpy(), sll[:T].cpu().numpy()
             out_l = logits.cpu().numpy()
         out_i = np.broadcast_to(np.arange(self.V, dtype=np.int64), (T, self.V)).copy()
         return out_c, out_i, out_l

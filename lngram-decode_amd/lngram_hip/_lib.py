@@ -52,6 +52,16 @@ class Drafter(ctypes.Structure):
 
 _PD = ctypes.POINTER(Drafter)
 
+
+class Sketch(ctypes.Structure):
+    """``lng_sketch`` (include/lngram_hip.h): device count sketches of the drafter's orders."""
+
+    _fields_ = [("ids", ctypes.c_void_p * 4), ("counts", ctypes.c_void_p * 4), ("k", ctypes.c_int32),
+                ("cap", ctypes.c_int32), ("fallback", ctypes.c_void_p), ("n_fallback", ctypes.c_int32)]
+
+
+_PS = ctypes.POINTER(Sketch)
+
 # name -> (restype, argtypes); must cover every function declared in the header
 SIGNATURES = {
     "lng_abi_version": (_int, []),
@@ -94,7 +104,10 @@ SIGNATURES = {
     "lng_drafter_readout": (_int, [_PD, _P32, _i32, _i32, _int, _f, _P32, _P32, _P32, _i32, _p, ctypes.c_size_t,
                                    _p, _p, _p, _p, _p]),
     "lng_drafter_gather": (_int, [_PD, _P32, _i32, _p, _p]),
+    "lng_drafter_shortlist": (_int, [_PD, _PS, _P32, _i32, _p, _p, _p, _i32, _P32, _P32, _P32, _i32, _p, _p, _p, _p,
+                                     _p]),
     "lng_drafter_tree": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, _p, ctypes.c_size_t, _p, _p, _p]),
+    "lng_drafter_tree_shortlist": (_int, [_PD, _PS, _P32, _P32, _i32, _i32, _p, ctypes.c_size_t, _p, _p, _p]),
 }
 
 _lock = threading.Lock()

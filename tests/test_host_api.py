@@ -100,7 +100,7 @@ def test_no_cpu_compute_path():
         lngram_v2.pack_bits_to_route_codes(torch.zeros(1, 2, 8, dtype=torch.bool), 4)
 
 
-def test_drafter_refuses_sketch_shortlist_and_cpu():
+def test_drafter_shortlist_rules_and_no_cpu_path():
     from drafting.gpu_drafter import GpuDrafter
 
     cfg, t = workloads.build_draft_bundle(workloads.TINY_DRAFT, seed=0)
@@ -108,13 +108,13 @@ def test_drafter_refuses_sketch_shortlist_and_cpu():
     for n in cfg["ngrams"]:
         sk[f"sketch_ids_{n}"] = torch.zeros(4, 2, dtype=torch.int32)
         sk[f"sketch_counts_{n}"] = torch.ones(4, 2, dtype=torch.int32)
-    with pytest.raises(NotImplementedError, match="shortlist"):
-        GpuDrafter((cfg, sk), shortlist_cap=8, device="cpu")
-    # a zero cap (or no sketches) is full-vocabulary drafting; this host has no GPU path
-    with pytest.raises(RuntimeError, match="no CPU path"):
-        GpuDrafter((cfg, sk), shortlist_cap=0, device="cpu")
-    with pytest.raises(RuntimeError, match="no CPU path"):
-        GpuDrafter((cfg, t), shortlist_cap=8, device="cpu")
+    # the shortlist does not combine with online counts (RefDrafter scores it without them)
+    with pytest.raises(ValueError, match="online"):
+        GpuDrafter((cfg, sk), shortlist_cap=8, online=True, device="cpu")
+    # shortlist or full vocabulary, this host has no GPU path
+    for bundle, cap in (((cfg, sk), 8), ((cfg, sk), 0), ((cfg, t), 8)):
+        with pytest.raises(RuntimeError, match="no CPU path"):
+            GpuDrafter(bundle, shortlist_cap=cap, device="cpu")
 
 
 def test_storage_dtype_rule():
