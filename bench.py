@@ -303,6 +303,64 @@ def _tiny_result(w, ms: float) -> dict:
             "note": "launch-bound (512 tokens): the roofline fraction is not meaningful"}
 
 
+def decode_step(dev, iters: int, warmup: int):
+    """Set up, and return the timing run of, the cached decode step of the SB-shape memory layer:
+    8 sequences with 2048 cached positions each take one new token (router codes, fused readout
+    reading the code cache, output projection, conv over the cached window).  Eager launches and
+    the fixed-shape step replayed from a HIP graph, both timed with device synchronisation per
+    step; the state is rolled back after every step, so each reads 2048 cached positions."""
+    import numpy as np
+    import torch
+
+    from ffnmem.infer import DecodeState, memory_codes, memory_model, memory_step, static_memory_step
+    from lngram_hip import ops, workloads
+
+    w = workloads.SB
+    ctx = 2048
+    mem = workloads.build_memory(w, seed=0, device=dev)
+    model = memory_model(mem)
+    h = workloads.make_hidden(w.with_shape(w.batch, ctx + 1), seed=1, device=dev)
+    h_norm = ops.rmsnorm(h, torch.ones(w.d_model, dtype=w.dtype, device=dev), w.norm_eps)
+    st = DecodeState.empty(model, w.batch, ctx + 16)
+    with torch.no_grad():
+        memory_step(model, 0, st, h[:, :ctx], memory_codes(model, 0, st, h_norm=h_norm[:, :ctx]))
+    st.length = ctx
+    h1, hn1 = h[:, ctx:ctx + 1].contiguous(), h_norm[:, ctx:ctx + 1].contiguous()
+    L_t = torch.full((), ctx, dtype=torch.long, device=dev)
+
+    def eager():
+        return memory_step(model, 0, st, h1, memory_codes(model, 0, st, h_norm=hn1))
+
+    def static():
+        return static_memory_step(model, 0, st, h1, memory_codes(model, 0, st, h_norm=hn1), L_t)
+
+    def run() -> dict:
+        out = {}
+        with torch.no_grad():
+            static()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                static()
+            for name, fn in (("eager", eager), ("graph", g.replay)):
+                times = []
+                for i in range(warmup + iters):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    fn()
+                    torch.cuda.synchronize()
+                    if i >= warmup:
+                        times.append((time.perf_counter() - t0) * 1e6)
+                out[f"{name}_median_us"] = float(np.median(times))
+        med = out["graph_median_us"]
+        return {"workload": f"SB-shape memory layer cached decode step: {w.batch} sequences x 1 new token after {ctx} "
+                            "cached positions (router + fused readout on the code cache + o-proj + conv over the "
+                            "cached window)",
+                "unit": "us per step", "iters": iters, **out, "tokens_per_s": w.batch / (med * 1e-6)}
+
+    return run
+
+
 def sdc_forward(dev, steps: int, warmup: int):
     """Set up, and return the timing run of, the SD-C layer: 8 x 4096 tokens, 181 routes; one step =
     diagonal SSM scan of u [8, 4096, 256] fp32 (decays U[0.9, 0.999]) + router features concat(RMSNorm(E[x_{t-1}]), RMSNorm(E[x_t]), s_t) from
@@ -500,6 +558,9 @@ def main() -> None:
     if not args.no_draft:
         log("draft step: set-up")
         legs["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
+    if not args.no_draft:
+        log("cached decode step: set-up")
+        legs["decode_step"] = decode_step(dev, args.draft_iters, 20)
     if not args.no_sdc:
         log("tiny and SD-C forwards: set-up")
         legs["tiny_forward"] = tiny_forward(dev, 50, 5)

@@ -142,6 +142,17 @@ int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, i
                     int64_t T, int32_t d, int32_t K, int32_t dilation, float eps, int residual, void* out,
                     void* stream);
 
+/* The same convolution over a window of cached rows (the cached decode step: memory_step's
+ * conv over the cache, ffnmem/infer.py:176-182; DepthwiseCausalConv.forward_incremental,
+ * lngram_v2.py:288-311): rows [B, stride, d] hold `len` rows per sequence (pre-norm conv inputs,
+ * positions 0 .. len-1, zero left padding before 0); the outputs of positions p0 .. p0+n-1,
+ * p0 = pos0 + (*pos0_dev if pos0_dev, a device int32, e.g. the cached length), go to
+ * out [B, n, d].  Each row is normalised as lng_causal_conv does, so outputs equal the whole
+ * sequence's bit for bit.  Positions at or past len produce nothing (device p0 unchecked). */
+int lng_causal_conv_at(const void* rows, const void* norm_w, const void* conv_w, int dtype, int64_t B, int64_t stride,
+                       int64_t len, int64_t pos0, const int32_t* pos0_dev, int64_t n, int32_t d, int32_t K,
+                       int32_t dilation, float eps, int residual, void* out, void* stream);
+
 /* bf16 y[M,N] = x[M,K] . w[N,K]^T (K % 32 == 0) that also writes the RMSNorm
  * statistics of its bf16 output rows for the following short conv: rowsq[p*M + m]
  * holds partial sums of squares, p < lng_linear_rowsq_partials(N).  readout_o_proj
@@ -185,6 +196,18 @@ int lng_memory_readout_fused(const void* q, const void* q_rows, float q_eps, con
                              int64_t T, int32_t R, const void* table2, const void* table3, const void* kv_pack,
                              const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
                              void* stream);
+
+/* lng_memory_readout_fused for n new positions of B sequences after a cached prefix
+ * (memory_step, ffnmem/infer.py:152-176; static_verify's memory part, live_spec.py:100-114):
+ * q / q_rows / head_out [B*n, 16*64] hold the new positions; codes [B, codes_len, R] is the code
+ * cache (or a verification context, infer.py:163-165) and the new tokens sit at positions
+ * p0 .. p0+n-1 of it, p0 = pos0 + (*pos0_dev if pos0_dev, a device int32); their n-gram rows read
+ * the codes at t, t-1, t-2 (valid from position n-1 up).  Positions outside [0, codes_len) read
+ * no rows. */
+int lng_memory_readout_fused_at(const void* q, const void* q_rows, float q_eps, const uint8_t* codes, int64_t B,
+                                int64_t n, int32_t R, int64_t codes_len, int64_t pos0, const int32_t* pos0_dev,
+                                const void* table2, const void* table3, const void* kv_pack, const void* w_mem,
+                                float eps, float scale, float sink_logit, void* head_out, void* stream);
 
 /* out[N, K] = w[N, K] * s[K] (bf16, one rounding): a row RMSNorm's weight folded into the projection
  * that follows it (readout_query_norm.weight into readout_q_proj.weight, lngram_v2.py:1115-1118). */

@@ -73,20 +73,36 @@ __global__ __launch_bounds__(256) void k_rmsnorm_bf16_vec(const bf16* __restrict
 
 constexpr int CONV_TT = 16;  // positions per block
 
+// Rows the convolutions read: B sequences of `len` rows (positions 0 .. len-1, batch stride
+// `stride` rows, rows before position 0 are the zero left padding); outputs for positions
+// p0 .. p0+n-1 of each sequence, p0 = pos0 (+ *pos0_dev), written to out[b * n + (t - p0)].  A
+// whole sequence: stride = len = n, p0 = 0; a decode step: the cache, p0 = the cached length.
+// Positions at or past `len` produce nothing.
+struct ConvWin {
+  int64_t stride, len, pos0, n;
+  const int32_t* pos0_dev;
+};
+__device__ __forceinline__ int64_t conv_p0(const ConvWin& W) {
+  return W.pos0 + (W.pos0_dev ? static_cast<int64_t>(*W.pos0_dev) : 0);
+}
+
 // out[b,t,c] = [mixed +] SiLU(sum_j w[c,j] * xn[b, t - (K-1-j)*dil, c]), xn = RMSNorm(mixed).
 // Block: one (b, 16-position tile).  Row scales of the tile and its causal halo
 // are computed first (one wave per row), then threads sweep the channels.
 template <typename T>
 __global__ __launch_bounds__(256) void k_causal_conv(const T* __restrict__ mixed, const T* __restrict__ norm_w,
-                                                     const T* __restrict__ conv_w, int64_t T_len, int32_t d, int32_t K,
+                                                     const T* __restrict__ conv_w, ConvWin W, int32_t d, int32_t K,
                                                      int32_t dil, float eps, int residual, T* __restrict__ out) {
   extern __shared__ float scale[];  // [CONV_TT + (K-1)*dil]
   const int64_t b = blockIdx.y;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * CONV_TT;
+  const int64_t p0 = conv_p0(W);
+  const int64_t t0 = p0 + static_cast<int64_t>(blockIdx.x) * CONV_TT;
+  const int64_t T_len = min(W.len, p0 + W.n);  // rows read and outputs end here
   const int halo = (K - 1) * dil;
   const int nrow = CONV_TT + halo;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const T* base = mixed + b * T_len * d;
+  const T* base = mixed + b * W.stride * d;
+  if (p0 < 0) return;
   for (int i = wave; i < nrow; i += 4) {
     const int64_t t = t0 - halo + i;
     float r = 0.f;
@@ -117,7 +133,7 @@ __global__ __launch_bounds__(256) void k_causal_conv(const T* __restrict__ mixed
       }
       const float y = round_to<T>(acc);
       const float act = round_to<T>(y / (1.0f + expf(-y)));
-      out[(b * T_len + t) * d + c] = residual ? from_f32<T>(to_f32(base[t * d + c]) + act) : from_f32<T>(act);
+      out[(b * W.n + t - p0) * d + c] = residual ? from_f32<T>(to_f32(base[t * d + c]) + act) : from_f32<T>(act);
     }
   }
 }
@@ -155,13 +171,16 @@ __device__ __forceinline__ void store8(bf16* p, const float (&v)[8]) {
 
 template <typename T>
 __global__ __launch_bounds__(128) void k_causal_conv_k4d3(const T* __restrict__ mixed, const T* __restrict__ norm_w,
-                                                          const T* __restrict__ conv_w, int64_t T_len, int32_t d,
+                                                          const T* __restrict__ conv_w, ConvWin W, int32_t d,
                                                           float eps, int residual, T* __restrict__ out) {
   __shared__ float scale[C43_TT + C43_HALO];
   const int64_t b = blockIdx.y;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * C43_TT;
+  const int64_t p0 = conv_p0(W);
+  const int64_t t0 = p0 + static_cast<int64_t>(blockIdx.x) * C43_TT;
+  const int64_t T_len = min(W.len, p0 + W.n);  // rows read and outputs end here
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const T* base = mixed + b * T_len * d;
+  const T* base = mixed + b * W.stride * d;
+  if (p0 < 0) return;
   for (int i = wave; i < C43_TT + C43_HALO; i += 2) {
     const int64_t t = t0 - C43_HALO + i;
     float r = 0.f;
@@ -223,7 +242,7 @@ __global__ __launch_bounds__(128) void k_causal_conv_k4d3(const T* __restrict__ 
           const float act = round_to<T>(y / (1.0f + expf(-y)));
           o[j] = residual ? x[j] + act : act;
         }
-        store8(out + (b * T_len + t) * d + c, o);
+        store8(out + (b * W.n + t - p0) * d + c, o);
       }
     }
   }
@@ -373,7 +392,7 @@ __device__ __forceinline__ float hi_f(uint32_t u) { return __uint_as_float(u & 0
 template <int TT>
 __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __restrict__ mixed,
                                                                 const bf16* __restrict__ norm_w,
-                                                                const bf16* __restrict__ conv_w, uint32_t T_len,
+                                                                const bf16* __restrict__ conv_w, ConvWin W,
                                                                 uint32_t d4, float eps, int residual,
                                                                 bf16* __restrict__ out) {
   constexpr int ROWS = TT + CF_HALO;
@@ -393,9 +412,12 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
     tile_t = static_cast<int>(tile % gridDim.x);
     tile_b = static_cast<int>(tile / gridDim.x);
   }
-  const int t0 = tile_t * TT;
-  const int T = static_cast<int>(T_len);
-  const size_t row0 = static_cast<size_t>(tile_b) * T_len;
+  const int64_t p0 = conv_p0(W);
+  if (p0 < 0) return;
+  const int t0 = static_cast<int>(p0) + tile_t * TT;
+  const int T = static_cast<int>(min(W.len, p0 + W.n));  // rows read and outputs end here
+  const size_t row0 = static_cast<size_t>(tile_b) * W.stride;
+  const size_t orow0 = static_cast<size_t>(tile_b) * W.n - p0;  // output row of position t: orow0 + t
   const uint32_t d = d4 * 4u;
   const bool active = static_cast<uint32_t>(tid) < d4;
   const uint32_t c = (active ? static_cast<uint32_t>(tid) : 0u) * 4u;
@@ -479,7 +501,7 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
           o.x = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
           o.y = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
         }
-        *reinterpret_cast<uint2*>(out + (row0 + t) * d + c) = o;
+        *reinterpret_cast<uint2*>(out + (orow0 + t) * d + c) = o;
       }
     }
   }
@@ -564,51 +586,78 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
   return check_launch("causal_conv_rowsq");
 }
 
+}  // extern "C"
+
+namespace lng {
+
+// Launch of the causal conv over window W (see ConvWin) of B sequences.
+static int conv_launch(const void* mixed, const void* norm_w, const void* conv_w, int dtype, int64_t B, const ConvWin& W,
+                       int32_t d, int32_t K, int32_t dilation, float eps, int residual, void* out, hipStream_t s) {
+  const int64_t n = W.n;
+  const int halo = (K - 1) * dilation;
+  if (halo > 4096) return fail(LNG_E_ARG, "causal_conv: receptive field too large");
+  if (K == 4 && dilation == 3 && d % 4 == 0 && d <= 2048 && dtype == LNG_BF16 && B <= 65535 && W.len < INT32_MAX) {
+    // 16 positions (25 rows with the halo, 103 VGPRs): 4 waves per SIMD hide the load phase
+    // better than 32-position blocks, whose halo share is smaller (21.5 against 22.8 us at
+    // B8 x T2048 x d1024)
+    constexpr int TT = 16;
+    dim3 g43(static_cast<unsigned>(cdiv(n, TT)), static_cast<unsigned>(B));
+    const int threads = static_cast<int>(cdiv(d / 4, 64) * 64);
+    hipLaunchKernelGGL(k_causal_conv_k4d3_fused<TT>, g43, dim3(threads), 0, s, static_cast<const bf16*>(mixed),
+                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), W,
+                       static_cast<uint32_t>(d / 4), eps, residual, static_cast<bf16*>(out));
+    return check_launch("causal_conv_k4d3_bf16");
+  }
+  if (K == 4 && dilation == 3 && d % 8 == 0 && (dtype == LNG_F32 || dtype == LNG_BF16)) {
+    dim3 g43(static_cast<unsigned>(cdiv(n, C43_TT)), static_cast<unsigned>(B));
+    if (dtype == LNG_F32)
+      hipLaunchKernelGGL(k_causal_conv_k4d3<float>, g43, dim3(128), 0, s, static_cast<const float*>(mixed),
+                         static_cast<const float*>(norm_w), static_cast<const float*>(conv_w), W, d, eps, residual,
+                         static_cast<float*>(out));
+    else
+      hipLaunchKernelGGL(k_causal_conv_k4d3<bf16>, g43, dim3(128), 0, s, static_cast<const bf16*>(mixed),
+                         static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), W, d, eps, residual,
+                         static_cast<bf16*>(out));
+    return check_launch("causal_conv_k4d3");
+  }
+  dim3 grid(static_cast<unsigned>(cdiv(n, CONV_TT)), static_cast<unsigned>(B));
+  const size_t lds = sizeof(float) * (CONV_TT + halo);
+  if (dtype == LNG_F32)
+    hipLaunchKernelGGL(k_causal_conv<float>, grid, dim3(256), lds, s, static_cast<const float*>(mixed),
+                       static_cast<const float*>(norm_w), static_cast<const float*>(conv_w), W, d, K, dilation, eps,
+                       residual, static_cast<float*>(out));
+  else if (dtype == LNG_BF16)
+    hipLaunchKernelGGL(k_causal_conv<bf16>, grid, dim3(256), lds, s, static_cast<const bf16*>(mixed),
+                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), W, d, K, dilation, eps,
+                       residual, static_cast<bf16*>(out));
+  else
+    return fail(LNG_E_DTYPE, "causal_conv: dtype must be f32 or bf16");
+  return check_launch("causal_conv");
+}
+
+}  // namespace lng
+
+extern "C" {
+
 int lng_causal_conv(const void* mixed, const void* norm_w, const void* conv_w, int dtype, int64_t B, int64_t T,
                     int32_t d, int32_t K, int32_t dilation, float eps, int residual, void* out, void* stream) {
   if (B < 0 || T < 0 || d <= 0 || K <= 0 || dilation <= 0) return fail(LNG_E_ARG, "causal_conv: bad shape");
   if (mixed == out) return fail(LNG_E_ARG, "causal_conv: out must not alias mixed");
   if (B == 0 || T == 0) return LNG_OK;
-  const int halo = (K - 1) * dilation;
-  if (halo > 4096) return fail(LNG_E_ARG, "causal_conv: receptive field too large");
-  hipStream_t s = as_stream(stream);
-  if (K == 4 && dilation == 3 && d % 4 == 0 && d <= 2048 && dtype == LNG_BF16 && B <= 65535) {
-    // 16 positions (25 rows with the halo, 103 VGPRs): 4 waves per SIMD hide the load phase
-    // better than 32-position blocks, whose halo share is smaller (21.5 against 22.8 us at
-    // B8 x T2048 x d1024)
-    constexpr int TT = 16;
-    dim3 g43(static_cast<unsigned>(cdiv(T, TT)), static_cast<unsigned>(B));
-    const int threads = static_cast<int>(cdiv(d / 4, 64) * 64);
-    hipLaunchKernelGGL(k_causal_conv_k4d3_fused<TT>, g43, dim3(threads), 0, s, static_cast<const bf16*>(mixed),
-                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w),
-                       static_cast<uint32_t>(T), static_cast<uint32_t>(d / 4), eps, residual, static_cast<bf16*>(out));
-    return check_launch("causal_conv_k4d3_bf16");
-  }
-  if (K == 4 && dilation == 3 && d % 8 == 0 && (dtype == LNG_F32 || dtype == LNG_BF16)) {
-    dim3 g43(static_cast<unsigned>(cdiv(T, C43_TT)), static_cast<unsigned>(B));
-    if (dtype == LNG_F32)
-      hipLaunchKernelGGL(k_causal_conv_k4d3<float>, g43, dim3(128), 0, s, static_cast<const float*>(mixed),
-                         static_cast<const float*>(norm_w), static_cast<const float*>(conv_w), T, d, eps, residual,
-                         static_cast<float*>(out));
-    else
-      hipLaunchKernelGGL(k_causal_conv_k4d3<bf16>, g43, dim3(128), 0, s, static_cast<const bf16*>(mixed),
-                         static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), T, d, eps, residual,
-                         static_cast<bf16*>(out));
-    return check_launch("causal_conv_k4d3");
-  }
-  dim3 grid(static_cast<unsigned>(cdiv(T, CONV_TT)), static_cast<unsigned>(B));
-  const size_t lds = sizeof(float) * (CONV_TT + halo);
-  if (dtype == LNG_F32)
-    hipLaunchKernelGGL(k_causal_conv<float>, grid, dim3(256), lds, s, static_cast<const float*>(mixed),
-                       static_cast<const float*>(norm_w), static_cast<const float*>(conv_w), T, d, K, dilation, eps,
-                       residual, static_cast<float*>(out));
-  else if (dtype == LNG_BF16)
-    hipLaunchKernelGGL(k_causal_conv<bf16>, grid, dim3(256), lds, s, static_cast<const bf16*>(mixed),
-                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), T, d, K, dilation, eps,
-                       residual, static_cast<bf16*>(out));
-  else
-    return fail(LNG_E_DTYPE, "causal_conv: dtype must be f32 or bf16");
-  return check_launch("causal_conv");
+  const ConvWin W{T, T, 0, T, nullptr};
+  return conv_launch(mixed, norm_w, conv_w, dtype, B, W, d, K, dilation, eps, residual, out, as_stream(stream));
+}
+
+int lng_causal_conv_at(const void* rows, const void* norm_w, const void* conv_w, int dtype, int64_t B, int64_t stride,
+                       int64_t len, int64_t pos0, const int32_t* pos0_dev, int64_t n, int32_t d, int32_t K,
+                       int32_t dilation, float eps, int residual, void* out, void* stream) {
+  if (B < 0 || n < 0 || d <= 0 || K <= 0 || dilation <= 0 || len < 0 || stride < len || pos0 < 0)
+    return fail(LNG_E_ARG, "causal_conv_at: bad shape");
+  if (!pos0_dev && pos0 + n > len) return fail(LNG_E_RANGE, "causal_conv_at: outputs past the rows");
+  if (rows == out) return fail(LNG_E_ARG, "causal_conv_at: out must not alias the rows");
+  if (B == 0 || n == 0) return LNG_OK;
+  const ConvWin W{stride, len, pos0, n, pos0_dev};
+  return conv_launch(rows, norm_w, conv_w, dtype, B, W, d, K, dilation, eps, residual, out, as_stream(stream));
 }
 
 int lng_row_sumsq(const void* x, int64_t rows, int32_t d, float* rowsq, void* stream) {

@@ -77,7 +77,8 @@ template <int FR_TOK>
 __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const bf16* __restrict__ q,
                                                           const bf16* __restrict__ q_rows, float q_eps,
                                                           const uint8_t* __restrict__ codes,
-                                                          int64_t B, int64_t T, int32_t R,
+                                                          int64_t B, int64_t T, int32_t R, int64_t cstride,
+                                                          int64_t pos0, const int32_t* __restrict__ pos0_dev,
                                                           const bf16* __restrict__ table2,
                                                           const bf16* __restrict__ table3,
                                                           const bf16* __restrict__ kv_pack,
@@ -123,7 +124,14 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   const int64_t tok0 = static_cast<int64_t>(blockIdx.x) * FR_TOK;
   const int64_t tok = tok0 + w;
   const bool tok_ok = tok < ntok;
-  const int64_t tpos = tok_ok ? tok % T : 0;
+  // token (b, i) of the B x T outputs sits at position pos0 (+ *pos0_dev) + i of its sequence; its
+  // codes at position t are codes[(b * cstride + t) * R ..] (cstride = T, pos0 = 0: a whole
+  // sequence; cstride = the cache length, pos0 = L: new positions after a cached prefix)
+  const int64_t tb = tok_ok ? tok / T : 0;
+  const int64_t tpos = tok_ok ? tok % T + pos0 + (pos0_dev ? static_cast<int64_t>(*pos0_dev) : 0) : 0;
+  const int64_t crow = tb * cstride + tpos;  // codes row of the token
+  // a position outside [0, cstride) (a device position past the cache) reads no codes
+  const bool codes_ok = tok_ok && tpos >= 0 && tpos < cstride;
 
   // ---------------- stage 0: row indices of this wave's token (codes at t, t-1, t-2)
   {
@@ -133,13 +141,13 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
       const int r = lane + 64 * k;
 #pragma unroll
       for (int p = 0; p < 3; ++p)
-        cv[p][k] = (tok_ok && r < R && tpos >= p) ? static_cast<uint8_t>(codes[(tok - p) * R + r] & 15) : 0;
+        cv[p][k] = (codes_ok && r < R && tpos >= p) ? static_cast<uint8_t>(codes[(crow - p) * R + r] & 15) : 0;
     }
 #pragma unroll
     for (int k = 0; k < FR_MAXR / 64; ++k) {
       const int r = lane + 64 * k;
       int32_t r2 = -1, r3 = -1;
-      if (tok_ok && r < R) {
+      if (codes_ok && r < R) {
         if (tpos >= 1) r2 = r * 256 + cv[1][k] + 16 * cv[0][k];
         if (tpos >= 2) r3 = r * 4096 + cv[2][k] + 16 * cv[1][k] + 256 * cv[0][k];
       }
@@ -389,11 +397,10 @@ __global__ __launch_bounds__(256) void k_readout_pack(const bf16* __restrict__ k
 
 using namespace lng;
 
-extern "C" int lng_memory_readout_fused(const void* q, const void* q_rows, float q_eps, const uint8_t* codes,
-                                        int64_t B, int64_t T, int32_t R,
-                                        const void* table2, const void* table3, const void* kv_pack,
-                                        const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
-                                        void* stream) {
+static int readout_launch(const void* q, const void* q_rows, float q_eps, const uint8_t* codes, int64_t B, int64_t T,
+                          int32_t R, int64_t cstride, int64_t pos0, const int32_t* pos0_dev, const void* table2,
+                          const void* table3, const void* kv_pack, const void* w_mem, float eps, float scale,
+                          float sink_logit, void* head_out, void* stream) {
   constexpr int FR_TOK = LNG_READOUT_TOK;
   if (B < 0 || T < 0 || R <= 0) return fail(LNG_E_ARG, "memory_readout_fused: bad shape");
   if (R > FR_MAXR) return fail(LNG_E_ARG, "memory_readout_fused: at most 256 routes");
@@ -406,10 +413,31 @@ extern "C" int lng_memory_readout_fused(const void* q, const void* q_rows, float
   if (ntok > (int64_t{1} << 21)) return fail(LNG_E_ARG, "memory_readout_fused: more than 2^21 tokens per launch");
   hipLaunchKernelGGL(k_readout_fused<FR_TOK>, dim3(static_cast<unsigned>(blocks)), dim3(64 * FR_TOK), 0,
                      as_stream(stream), static_cast<const bf16*>(q), static_cast<const bf16*>(q_rows), q_eps, codes,
-                     B, T, R, static_cast<const bf16*>(table2),
+                     B, T, R, cstride, pos0, pos0_dev, static_cast<const bf16*>(table2),
                      static_cast<const bf16*>(table3), static_cast<const bf16*>(kv_pack),
                      static_cast<const bf16*>(w_mem), eps, scale, sink_logit, static_cast<bf16*>(head_out));
   return check_launch("memory_readout_fused");
+}
+
+extern "C" int lng_memory_readout_fused(const void* q, const void* q_rows, float q_eps, const uint8_t* codes,
+                                        int64_t B, int64_t T, int32_t R,
+                                        const void* table2, const void* table3, const void* kv_pack,
+                                        const void* w_mem, float eps, float scale, float sink_logit, void* head_out,
+                                        void* stream) {
+  return readout_launch(q, q_rows, q_eps, codes, B, T, R, T, 0, nullptr, table2, table3, kv_pack, w_mem, eps, scale,
+                        sink_logit, head_out, stream);
+}
+
+extern "C" int lng_memory_readout_fused_at(const void* q, const void* q_rows, float q_eps, const uint8_t* codes,
+                                           int64_t B, int64_t n, int32_t R, int64_t codes_len, int64_t pos0,
+                                           const int32_t* pos0_dev, const void* table2, const void* table3,
+                                           const void* kv_pack, const void* w_mem, float eps, float scale,
+                                           float sink_logit, void* head_out, void* stream) {
+  if (codes_len <= 0 || pos0 < 0) return fail(LNG_E_ARG, "memory_readout_fused_at: bad codes length or position");
+  if (!pos0_dev && pos0 + n > codes_len)
+    return fail(LNG_E_RANGE, "memory_readout_fused_at: positions pos0 .. pos0+n-1 past the codes");
+  return readout_launch(q, q_rows, q_eps, codes, B, n, R, codes_len, pos0, pos0_dev, table2, table3, kv_pack, w_mem,
+                        eps, scale, sink_logit, head_out, stream);
 }
 
 extern "C" int lng_memory_readout_pack(const void* kv, void* kv_pack, void* stream) {

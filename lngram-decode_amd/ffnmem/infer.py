@@ -1,0 +1,221 @@
+"""Cached decoding of the memory layers: drop-in for the memory half of the reference
+``ffnmem/infer.py`` (``DecodeState`` :65-112, ``ssm_continue`` :125-137, ``router_input_at``
+:140-149, ``memory_step`` :152-182) and for the memory part of ``static_verify``
+(``drafting/live_spec.py:68-139``).
+
+The caches hold, per memory layer, the route codes of every processed position (uint8,
+``[B, max_len, R]``) and the short conv's input rows (``[B, max_len, d]``), indexed by absolute
+position, so rolling back is moving ``length``.  A step of ``n`` new positions runs the same
+kernels as the whole-sequence forward, reading the cached history in place:
+
+- the fused readout (``lng_memory_readout_fused_at``) takes each new token's n-gram rows from the
+  code cache at positions ``t, t-1, t-2``; other shapes gather route tokens from the cached
+  context (``lng_route_tokens``) and run the materialised readout;
+- the short conv (``lng_causal_conv_at``) reads its causal window from the conv-input cache and
+  normalises each row as the whole-sequence conv does.
+
+So the cached outputs equal the full forward's up to the summation order of the projections
+(identical where the same GEMM kernel serves both shapes).  ``conv_in`` differs from the
+reference's in content, not in role: it keeps the conv's input rows before the conv's RMSNorm
+(the reference keeps them after it); rows move the same way under ``truncate`` and tree
+acceptance.
+
+The attention and FFN halves of the reference's ``decode_step`` belong to the transformer, which
+is not part of this path: ``DecodeState`` here caches the memory layers (``k`` / ``v`` stay empty).
+A "model" is anything with ``blocks`` (each with a ``memory`` attribute, an ``LngramMemory`` or
+None) and, for token-routed memories, ``tok_emb`` and ``ssm``; ``memory_model`` wraps a single
+memory layer.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from types import SimpleNamespace
+
+import torch
+from torch import Tensor
+
+from lngram_hip import ops
+
+
+# ------------------------------------------------------------------ state
+@dataclass
+class DecodeState:
+    batch: int
+    max_len: int
+    length: int = 0
+    tokens: Tensor | None = None                       # [B, max_len]
+    k: list = field(default_factory=list)              # attention caches: not on this path
+    v: list = field(default_factory=list)
+    codes: dict = field(default_factory=dict)          # block pos -> [B, max_len, R] uint8
+    conv_in: dict = field(default_factory=dict)        # block pos -> [B, max_len, d] conv input rows
+    ssm: Tensor | None = None                          # [B, max_len, N] fp32
+    epoch: int = 0                                     # bumped on truncate
+
+    @classmethod
+    def empty(cls, model, batch: int, max_len: int, dtype: torch.dtype | None = None) -> "DecodeState":
+        """``DecodeState.empty`` (``infer.py:78-97``) for the memory layers of ``model``."""
+        s = cls(batch=batch, max_len=max_len)
+        dev = None
+        for pos, block in enumerate(model.blocks):
+            mem = getattr(block, "memory", None)
+            if mem is None:
+                continue
+            m = mem.module
+            if m.execution_mode == "streaming":
+                raise NotImplementedError("cached decoding with streaming memory readout")
+            w = m.readout_o_proj.weight
+            dev = w.device
+            dt = dtype or w.dtype
+            s.codes[pos] = torch.zeros(batch, max_len, mem.routes, dtype=torch.uint8, device=dev)
+            s.conv_in[pos] = torch.zeros(batch, max_len, m.hidden_size, dtype=dt, device=dev)
+        if dev is None:
+            raise ValueError("the model has no memory layer")
+        s.tokens = torch.zeros(batch, max_len, dtype=torch.long, device=dev)
+        ssm = getattr(model, "ssm", None)
+        if ssm is not None:
+            s.ssm = torch.zeros(batch, max_len, ssm.state_dim, dtype=torch.float32, device=dev)
+        return s
+
+    def truncate(self, length: int) -> None:
+        if not 0 <= length <= self.length:
+            raise ValueError(f"cannot truncate to {length} (length {self.length})")
+        self.length = length
+        self.epoch += 1
+
+    def index_select(self, idx: Tensor) -> "DecodeState":
+        """Rows ``idx`` of every cache (``infer.py:105-111``)."""
+        def sel(t):
+            return t.index_select(0, idx.to(t.device))
+
+        return DecodeState(len(idx), self.max_len, self.length, sel(self.tokens), [], [],
+                           {p: sel(t) for p, t in self.codes.items()},
+                           {p: sel(t) for p, t in self.conv_in.items()},
+                           None if self.ssm is None else sel(self.ssm), self.epoch)
+
+
+def memory_model(mem, tok_emb=None, ssm=None):
+    """A one-block "model" around an ``LngramMemory`` for the functions below (block 0)."""
+    return SimpleNamespace(blocks=[SimpleNamespace(memory=mem)], tok_emb=tok_emb, ssm=ssm)
+
+
+# ------------------------------------------------------------------ pieces
+def ssm_continue(model, emb: Tensor, s_prev: Tensor | None) -> Tensor:
+    """SSM states of new positions from the state before them (``infer.py:125-137``):
+    ``lng_ssm_scan`` with the carried state as ``s0``."""
+    ssm = model.ssm
+    return ops.ssm_scan(ssm.decay(), ssm.inputs(emb), s_prev)
+
+
+def router_input_at(model, mem, state: DecodeState, emb: Tensor, s_new: Tensor | None) -> Tensor:
+    """Token-only router features of the new positions (``infer.py:140-149``): the previous
+    token's embedding comes from the cache."""
+    L = state.length
+    if L == 0:
+        return mem.router_features(emb, s_new)
+    prev = model.tok_emb(state.tokens[:, L - 1:L]).to(emb.dtype)
+    s_cat = None
+    if s_new is not None:
+        s_cat = torch.cat((state.ssm[:, L - 1:L], s_new), dim=1)
+    return mem.router_features(torch.cat((prev, emb), dim=1), s_cat)[:, 1:]
+
+
+def _readout_head(m, h: Tensor, codes: Tensor, pos0: int, pos0_dev: Tensor | None) -> Tensor:
+    """Fused readout of the new positions whose codes sit at ``pos0 (+ pos0_dev)`` of ``codes``."""
+    q_raw = ops.linear(h, m._folded_query_weight())
+    return ops.memory_readout_fused_at(q_raw, codes, pos0, m.tables["ngram_2"].weight, m.tables["ngram_3"].weight,
+                                       m._fused_weights(), m.readout_memory_norm.weight, m.readout_memory_norm.eps,
+                                       m.softmax_scale, m.readout_sink_logit, q_rows=h,
+                                       q_eps=m.readout_query_norm.eps, pos0_dev=pos0_dev)
+
+
+def _finish_cached(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tensor | None,
+                   pos_idx: Tensor | None) -> Tensor:
+    """``mixed = W_o head``, cached as conv input at positions L .. L+n-1, then
+    ``mixed + short_conv`` over the cached window (``infer.py:175-182``)."""
+    b = head.shape[0]
+    mixed = ops.linear(head.reshape(b, n, m.readout_inner_dim), m.readout_o_proj.weight)
+    if pos_idx is None:
+        conv_in[:, L:L + n] = mixed
+        length = L + n
+    else:
+        conv_in.index_copy_(1, pos_idx, mixed.to(conv_in.dtype))
+        length = conv_in.shape[1]
+    conv = m.short_conv
+    conv._check(mixed, None)
+    return ops.causal_conv_at(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps,
+                              pos0=L, n=n, length=length, pos0_dev=L_dev, residual=True)
+
+
+def memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tensor,
+                route_codes_ctx: Tensor | None = None, route_tokens: Tensor | None = None) -> Tensor:
+    """Memory output ``[B, n, d]`` of the new positions (``infer.py:152-182``); ``codes_new``
+    ``[B, n, R]`` are written into the cache.  ``route_codes_ctx [B, n + H, R]`` replaces the
+    cached history (tree verification: codes along each node's ancestor path); ``route_tokens
+    [B, n, R, len(ngrams) * mem_dim]`` are rows supplied by the caller (the gather is skipped)."""
+    mem = model.blocks[pos].memory
+    m = mem.module
+    L, n = state.length, h.shape[1]
+    if L + n > state.max_len:
+        raise ValueError(f"cache full: {L} + {n} > {state.max_len}")
+    cache = state.codes[pos]
+    cache[:, L:L + n] = codes_new.to(cache.dtype)
+    if route_tokens is None and m._fused_shape_ok(h):
+        if route_codes_ctx is None:
+            head = _readout_head(m, h, cache, L, None)
+        else:
+            ctx = route_codes_ctx.to(torch.uint8).contiguous()
+            head = _readout_head(m, h, ctx, ctx.shape[1] - n, None)
+    else:
+        if route_tokens is None:
+            ctx = route_codes_ctx
+            if ctx is None:
+                ctx = cache[:, max(0, L - m.route_history_length):L + n]
+            tokens = m._lookup_route_chunk(ctx, None, 0, m.num_routes, None, None, target_length=n)
+        else:
+            tokens = route_tokens.to(h.device, m.readout_kv_proj.weight.dtype)
+        key, value = m._project_memory(tokens)
+        head = m._manual_gqa(m._project_query(h), key, value)
+    return _finish_cached(m, head, state.conv_in[pos], L, n, None, None)
+
+
+def static_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tensor, L_t: Tensor) -> Tensor:
+    """``memory_step`` with shapes independent of the cached length (the memory part of
+    ``static_verify``, ``live_spec.py:100-114``): ``L_t`` is a 0-d device tensor holding the
+    length, the caches are written with ``index_copy_`` at ``L_t + arange(n)`` and the kernels read
+    the length on the device, so the launches can be captured in a HIP graph and replayed for any
+    length.  The caller advances ``state.length`` (and ``L_t``) afterwards."""
+    mem = model.blocks[pos].memory
+    m = mem.module
+    n = h.shape[1]
+    dev = h.device
+    L_long = L_t.to(torch.long)
+    pos_idx = L_long + torch.arange(n, device=dev)
+    cache = state.codes[pos]
+    cache.index_copy_(1, pos_idx, codes_new.to(cache.dtype))
+    L32 = L_t.to(torch.int32).reshape(1)
+    if m._fused_shape_ok(h):
+        head = _readout_head(m, h, cache, 0, L32)
+    else:
+        hist = m.route_history_length
+        hidx = L_long - hist + torch.arange(hist, device=dev)
+        hcodes = cache.index_select(1, hidx.clamp_min(0))
+        ctx = torch.cat((hcodes, codes_new.to(cache.dtype)), 1)
+        seg = torch.cat(((hidx >= 0).to(torch.int32), torch.ones(n, dtype=torch.int32, device=dev)))
+        tokens = m._lookup_route_chunk(ctx, None, 0, m.num_routes, seg[None].expand(h.shape[0], -1).contiguous(),
+                                       None, target_length=n)
+        key, value = m._project_memory(tokens)
+        head = m._manual_gqa(m._project_query(h), key, value)
+    return _finish_cached(m, head, state.conv_in[pos], 0, n, L32, pos_idx)
+
+
+# ------------------------------------------------------------------ one memory layer's step
+def memory_codes(model, pos: int, state: DecodeState, h_norm: Tensor | None = None,
+                 router_in: Tensor | None = None) -> Tensor:
+    """Route codes of the new positions (``infer.py:230-236``): the router reads ``h_norm``
+    (hidden router) or the token features ``router_in``."""
+    mem = model.blocks[pos].memory
+    x = h_norm if mem.router_input == "hidden" else router_in
+    if x is None:
+        raise ValueError(f"router_input={mem.router_input} needs {'h_norm' if mem.router_input == 'hidden' else 'router_in'}")
+    return mem.route_codes(x)[1]

@@ -133,6 +133,29 @@ class DepthwiseCausalConv(nn.Module):
         return ops.causal_conv(values, self.norm.weight, self.conv.weight, self.dilation, self.norm.eps,
                                residual=False)
 
+    def forward_incremental(self, values: Tensor, history: Optional[Tensor]) -> Tuple[Tensor, Tensor]:
+        """``forward_incremental`` (``lngram_v2.py:288-311``): the output for ``values [B, n, H]``
+        that follow ``history [B, H, left_padding]`` (None at the sequence start), and the history
+        of the next call.  Here the history holds the last ``left_padding`` input rows before their
+        RMSNorm: ``lng_causal_conv_at`` normalises every row it reads exactly as the whole-sequence
+        conv does, so chained calls give the whole sequence's output bit for bit (a zero row
+        normalises to zero, the left padding)."""
+        self._check(values, None)
+        b, n, d = values.shape
+        lp = self.left_padding
+        if lp == 0:
+            return self.forward(values), values.new_zeros(b, d, 0)
+        if history is None:
+            hist_rows = values.new_zeros(b, lp, d)
+        else:
+            if tuple(history.shape) != (b, d, lp):
+                raise ValueError(f"conv history shape={tuple(history.shape)}, expected {(b, d, lp)}")
+            hist_rows = history.transpose(1, 2).to(values.dtype)
+        window = torch.cat((hist_rows, values), dim=1).contiguous()
+        out = ops.causal_conv_at(window, self.norm.weight, self.conv.weight, self.dilation, self.norm.eps, pos0=lp,
+                                 n=n, residual=False)
+        return out, window[:, -lp:].transpose(1, 2).contiguous()
+
     def forward_residual(self, values: Tensor) -> Tensor:
         """``values + forward(values)`` in one kernel (the ``_finish`` residual)."""
         self._check(values, None)

@@ -81,11 +81,15 @@ SIGNATURES = {
                                           _f, _f, _p, _p]),
     "lng_sink_probabilities": (_int, [_p, _i64, _i32, _f, _p, _p]),
     "lng_causal_conv": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
+    "lng_causal_conv_at": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i32, _i32, _f, _int, _p,
+                                  _p]),
     "lng_linear_rowsq_partials": (_i32, [_i64]),
     "lng_linear_rowsq": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "lng_row_sumsq": (_int, [_p, _i64, _i32, _p, _p]),
     "lng_causal_conv_rowsq": (_int, [_p, _p, _i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
     "lng_memory_readout_fused": (_int, [_p, _p, _f, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f, _f, _f, _p, _p]),
+    "lng_memory_readout_fused_at": (_int, [_p, _p, _f, _p, _i64, _i64, _i32, _i64, _i64, _p, _p, _p, _p, _p, _f, _f,
+                                           _f, _p, _p]),
     "lng_fold_columns": (_int, [_p, _p, _i64, _i64, _p, _p]),
     "lng_memory_readout_pack": (_int, [_p, _p, _p]),
     "lng_gather_sum_scaled": (_int, [ctypes.POINTER(_p), _int, _i32, _p, _i64, _i64, _i32, _P32, _i32, _i32, _i32,

@@ -425,6 +425,32 @@ def causal_conv(mixed: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor,
     return out
 
 
+def causal_conv_at(rows: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor, dilation: int, eps: float,
+                   pos0: int, n: int, length: int | None = None, pos0_dev: torch.Tensor | None = None,
+                   residual: bool = True) -> torch.Tensor:
+    """``causal_conv`` for positions ``p0 .. p0+n-1`` of cached rows (``lng_causal_conv_at``):
+    ``rows [B, S, d]`` hold the conv's (pre-norm) inputs of positions ``0 .. length-1`` (default
+    ``length = S``); ``p0 = pos0 (+ pos0_dev)``, ``pos0_dev`` an int32 device scalar (the cached
+    length read on the device, for launches captured in a graph) -> ``[B, n, d]``."""
+    dev = _dev(rows, norm_w, conv_w, pos0_dev)
+    if rows.dim() != 3 or rows.stride(-1) != 1 or rows.stride(1) != rows.shape[-1]:
+        raise ValueError("causal_conv_at: rows must be [B, S, d] with contiguous rows")
+    b, s_len, d = rows.shape
+    length = s_len if length is None else int(length)
+    cw = _c(conv_w.reshape(d, -1).to(rows.dtype))
+    nw = _c(norm_w.to(rows.dtype))
+    pd = None
+    if pos0_dev is not None:
+        if pos0_dev.dtype != torch.int32 or pos0_dev.numel() != 1:
+            raise ValueError("causal_conv_at: pos0_dev must be one int32 on the device")
+        pd = pos0_dev
+    out = torch.empty(b, n, d, dtype=rows.dtype, device=dev)
+    check(lib().lng_causal_conv_at(_ptr(rows), _ptr(nw), _ptr(cw), dtype_code(rows.dtype), b, rows.stride(0) // d,
+                                   length, int(pos0), _ptr(pd), int(n), d, cw.shape[1], dilation, eps,
+                                   int(bool(residual)), _ptr(out), _stream(dev)), "causal_conv_at")
+    return out
+
+
 def memory_readout_pack(kv: torch.Tensor) -> torch.Tensor:
     """``readout_kv_proj.weight`` ``[512, 256]`` bf16 -> the fused readout's packed KV weight
     (``lng_memory_readout_pack``: a permutation into the kernel's operand order)."""
@@ -479,6 +505,40 @@ def memory_readout_fused(q: torch.Tensor, codes: torch.Tensor, table2: torch.Ten
         _ptr(qc), _ptr(qr), float(q_eps), _ptr(cc), b, t, r, _ptr(t2), _ptr(t3), _ptr(kp), _ptr(wmc), eps, scale,
         sink_logit, _ptr(out), _stream(dev)))
     check(rc, "memory_readout_fused")
+    return out
+
+
+def memory_readout_fused_at(q: torch.Tensor, codes: torch.Tensor, pos0: int, table2: torch.Tensor,
+                            table3: torch.Tensor, kv_pack: torch.Tensor, w_mem: torch.Tensor, eps: float,
+                            scale: float, sink_logit: float, q_rows: torch.Tensor | None = None, q_eps: float = 0.0,
+                            pos0_dev: torch.Tensor | None = None) -> torch.Tensor:
+    """``memory_readout_fused`` for ``n`` new positions (``lng_memory_readout_fused_at``): q
+    ``[B, n, 1024]``; codes ``[B, S, R]`` uint8 (a code cache or a verification context, row stride
+    ``S * R``) with the new tokens at positions ``p0 .. p0+n-1``, ``p0 = pos0 (+ pos0_dev)``."""
+    dev = _dev(q, codes, table2, table3, kv_pack, w_mem, q_rows, pos0_dev)
+    b, n = q.shape[0], q.shape[1]
+    if codes.dim() != 3 or codes.dtype != torch.uint8 or codes.shape[0] != b or not codes.is_contiguous():
+        raise ValueError("fused readout: codes must be a contiguous uint8 [B, S, R] cache")
+    r = codes.shape[2]
+    qc = _c(q)
+    if qc.dtype != torch.bfloat16 or qc.shape[-1] != 1024:
+        raise ValueError("fused readout expects a bf16 [B, n, 1024] query")
+    if table2.shape != (r * 256, 128) or table3.shape != (r * 4096, 128):
+        raise ValueError("fused readout expects tables [R*256,128] and [R*4096,128]")
+    if kv_pack.shape != (_lib.READOUT_PACK_ELEMS,) or kv_pack.dtype != torch.bfloat16 or w_mem.shape != (256,):
+        raise ValueError("fused readout weight shapes")
+    qr = None
+    if q_rows is not None:
+        qr = _c(q_rows)
+        if qr.dtype != torch.bfloat16 or qr.shape != qc.shape:
+            raise ValueError("fused readout: q_rows must be bf16 and shaped like q")
+    if pos0_dev is not None and (pos0_dev.dtype != torch.int32 or pos0_dev.numel() != 1):
+        raise ValueError("fused readout: pos0_dev must be one int32 on the device")
+    out = torch.empty(b, n, 1024, dtype=torch.bfloat16, device=dev)
+    t2, t3, kp, wmc = _c(table2), _c(table3), _c(kv_pack), _c(w_mem.to(torch.bfloat16))
+    check(lib().lng_memory_readout_fused_at(_ptr(qc), _ptr(qr), float(q_eps), _ptr(codes), b, n, r, codes.shape[1],
+                                            int(pos0), _ptr(pos0_dev), _ptr(t2), _ptr(t3), _ptr(kp), _ptr(wmc), eps,
+                                            scale, sink_logit, _ptr(out), _stream(dev)), "memory_readout_fused_at")
     return out
 
 
