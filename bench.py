@@ -326,13 +326,13 @@ def decode_step(dev, iters: int, warmup: int):
         memory_step(model, 0, st, h[:, :ctx], memory_codes(model, 0, st, h_norm=h_norm[:, :ctx]))
     st.length = ctx
     h1, hn1 = h[:, ctx:ctx + 1].contiguous(), h_norm[:, ctx:ctx + 1].contiguous()
-    L_t = torch.full((), ctx, dtype=torch.long, device=dev)
+    L_t = torch.full((), ctx, dtype=torch.int32, device=dev)
 
     def eager():
         return memory_step(model, 0, st, h1, memory_codes(model, 0, st, h_norm=hn1))
 
     def static():
-        return static_memory_step(model, 0, st, h1, memory_codes(model, 0, st, h_norm=hn1), L_t)
+        return static_memory_step(model, 0, st, h1, None, L_t, router_x=hn1)
 
     def run() -> dict:
         out = {}

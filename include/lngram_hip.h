@@ -108,6 +108,18 @@ enum { LNG_NORM_MODEL = 0, LNG_NORM_FUSED = 1 };
 int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps, int32_t mode,
                 void* out, void* stream);
 
+/* Decode-step projections written straight into caches (the cache writes of memory_step,
+ * ffnmem/infer.py:158, :177): row m = b * group + i (i < group) of x . w^T lands at row
+ * b * stride + p0 + i of the output, p0 = pos0 (+ *pos0_dev, a device int32).  bf16 operands,
+ * M <= 64 (a multiple of group), N % 16 == 0, K % 32 == 0.  lng_linear_at writes bf16 rows of N
+ * (the conv-input cache, from readout_o_proj); lng_router_codes_at writes the N/4 4-bit route codes
+ * (uint8) of LngramMemory.route_logits + quantize_route_logits (wrapper.py:98-101,
+ * lngram_v2.py:1012-1017) into the code cache.  Results equal lng_linear / lng_router_codes. */
+int lng_linear_at(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t group, int64_t stride,
+                  int64_t pos0, const int32_t* pos0_dev, void* y, void* stream);
+int lng_router_codes_at(const void* x, const void* w, int64_t M, int64_t K, int64_t N, int64_t group,
+                        int64_t stride, int64_t pos0, const int32_t* pos0_dev, uint8_t* codes, void* stream);
+
 /* y[M,N] = x[M,K] . w[N,K]^T in `dtype` (fp32 accumulation, output rounded to
  * dtype).  nn.Linear without bias as used by readout_q_proj / readout_kv_proj /
  * readout_o_proj (lngram_v2.py:1115-1131, :1354-1359) and the draft head. */

@@ -556,9 +556,85 @@ __global__ __launch_bounds__(256) void k_gemm_nt_f32(const TA* __restrict__ X, c
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Skinny GEMM for a few rows of X (decode steps, M <= 64): one wave per (16 columns of W, 16 rows
+// of X).  K is streamed in order in rounds of SK_CH MFMA steps whose operands go straight from
+// memory into registers (a 16-column tile of W at K = 1024 is 32 KB: one round trip), each step a
+// 16x16x32 MFMA accumulating in K order -- per output the same instruction sequence as the tiled
+// kernels above, so the results equal theirs.  The tiled kernels would run M = 8 rows on a handful
+// of 128-wide blocks.  Output rows may be scattered into a cache: row(m) = (m / group) * stride +
+// p0 + m % group, p0 = pos0 (+ *pos0_dev); the identity is group = M, stride = 0, p0 = 0.
+constexpr int SK_CH = 32;  // MFMA steps (32 K each) per load round
+constexpr int SK_MAXM = 64;
+
+struct RowMap {
+  int64_t group, stride, pos0;
+  const int32_t* pos0_dev;
+};
+
+template <int EPI>
+__global__ __launch_bounds__(64, 1) void k_gemm_skinny(const bf16* __restrict__ W, const bf16* __restrict__ X,
+                                                       int64_t N, int64_t M, int64_t K, RowMap map,
+                                                       void* __restrict__ out, float* __restrict__ logits,
+                                                       void* __restrict__ codes, int codes_dt, int64_t routes) {
+  const int lane = threadIdx.x;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * 16, m0 = static_cast<int64_t>(blockIdx.y) * 16;
+  const int rsel = lane & 15, psel = lane >> 4;
+  const int64_t wr = n0 + rsel < N ? n0 + rsel : N - 1;
+  const int64_t xr = m0 + rsel < M ? m0 + rsel : M - 1;
+  const bf16* wp = W + wr * K + 8 * psel;
+  const bf16* xp = X + xr * K + 8 * psel;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int nk = static_cast<int>(K / 32);
+  for (int k0 = 0; k0 < nk; k0 += SK_CH) {
+    const int cnt = nk - k0 < SK_CH ? nk - k0 : SK_CH;
+    bf16x8 a[SK_CH], b[SK_CH];
+#pragma unroll
+    for (int q = 0; q < SK_CH; ++q)
+      if (q < cnt) {
+        a[q] = *reinterpret_cast<const bf16x8*>(wp + static_cast<int64_t>(k0 + q) * 32);
+        b[q] = *reinterpret_cast<const bf16x8*>(xp + static_cast<int64_t>(k0 + q) * 32);
+      }
+#pragma unroll
+    for (int q = 0; q < SK_CH; ++q)
+      if (q < cnt) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[q], b[q], acc, 0, 0, 0);
+  }
+  const int64_t n = n0 + 4 * psel, m = m0 + rsel;
+  if (m >= M || n >= N) return;
+  const int64_t p0 = map.pos0 + (map.pos0_dev ? static_cast<int64_t>(*map.pos0_dev) : 0);
+  const int64_t row = (m / map.group) * map.stride + p0 + m % map.group;
+  if (EPI == EPI_BF16) {
+    bf16* o = static_cast<bf16*>(out) + row * N + n;
+    const bf16x4 pk = {static_cast<bf16>(acc[0]), static_cast<bf16>(acc[1]), static_cast<bf16>(acc[2]),
+                       static_cast<bf16>(acc[3])};
+    *reinterpret_cast<bf16x4*>(o) = pk;  // N % 16 == 0
+  } else if (EPI == EPI_F32) {
+    *reinterpret_cast<f32x4*>(static_cast<float*>(out) + row * N + n) = acc;
+  } else {
+    if (logits) *reinterpret_cast<f32x4*>(logits + m * N + n) = acc;
+    const int code = (acc[0] > 0.f ? 1 : 0) | (acc[1] > 0.f ? 2 : 0) | (acc[2] > 0.f ? 4 : 0) | (acc[3] > 0.f ? 8 : 0);
+    const int64_t r = n >> 2;
+    if (codes_dt == LNG_U8)
+      static_cast<uint8_t*>(codes)[row * routes + r] = static_cast<uint8_t>(code);
+    else
+      static_cast<int32_t*>(codes)[row * routes + r] = code;
+  }
+}
+
+template <int EPI>
+static int launch_skinny(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, const RowMap& map, void* out,
+                         float* logits, void* codes, int codes_dt, int64_t routes, hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(cdiv(N, 16)), static_cast<unsigned>(cdiv(M, 16)));
+  hipLaunchKernelGGL(k_gemm_skinny<EPI>, g, dim3(64), 0, s, w, x, N, M, K, map, out, logits, codes, codes_dt, routes);
+  return check_launch("gemm_bf16_skinny");
+}
+
 template <int EPI>
 static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, void* out, float* logits,
                        void* codes, int codes_dt, int64_t routes, hipStream_t s, float* rowsq = nullptr) {
+  if (!rowsq && M <= SK_MAXM && K % 32 == 0 && N % 16 == 0 && (EPI != EPI_ROUTER || N % 4 == 0))
+    return launch_skinny<EPI>(w, x, N, M, K, RowMap{M, 0, 0, nullptr}, out ? out : logits, logits, codes, codes_dt,
+                              routes, s);
   if constexpr (EPI != EPI_BF16) {
     if (K % WT_K == 0 && M >= 4096 && N > GB2 && N <= 2 * WT_N && (N & 3) == 0) {
       const int n_tiles = static_cast<int>(cdiv(N, WT_N));
@@ -690,6 +766,28 @@ int lng_router_codes(const void* x, int x_dtype, const void* w, int w_dtype, int
   }
   if (!codes) return LNG_OK;
   return lng_pack_route_codes(logits, M, N, bits, codes, codes_dtype, stream);
+}
+
+int lng_linear_at(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t group, int64_t stride,
+                  int64_t pos0, const int32_t* pos0_dev, void* y, void* stream) {
+  if (M < 0 || M > SK_MAXM || N <= 0 || N % 16 || K <= 0 || K % 32 || group <= 0 || M % group || pos0 < 0 ||
+      stride < 0)
+    return fail(LNG_E_ARG, "linear_at: bf16, M <= 64 (a multiple of group), N % 16 == 0, K % 32 == 0");
+  if (M == 0) return LNG_OK;
+  return launch_skinny<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K,
+                                 RowMap{group, stride, pos0, pos0_dev}, y, nullptr, nullptr, 0, 0, as_stream(stream));
+}
+
+int lng_router_codes_at(const void* x, const void* w, int64_t M, int64_t K, int64_t N, int64_t group,
+                        int64_t stride, int64_t pos0, const int32_t* pos0_dev, uint8_t* codes, void* stream) {
+  if (M < 0 || M > SK_MAXM || N <= 0 || N % 16 || K <= 0 || K % 32 || group <= 0 || M % group || pos0 < 0 ||
+      stride < 0 || !codes)
+    return fail(LNG_E_ARG, "router_codes_at: bf16, 4-bit codes, M <= 64 (a multiple of group), N % 16 == 0, "
+                           "K % 32 == 0");
+  if (M == 0) return LNG_OK;
+  return launch_skinny<EPI_ROUTER>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K,
+                                   RowMap{group, stride, pos0, pos0_dev}, nullptr, nullptr, codes, LNG_U8, N / 4,
+                                   as_stream(stream));
 }
 
 }  // extern "C"

@@ -129,20 +129,32 @@ def _readout_head(m, h: Tensor, codes: Tensor, pos0: int, pos0_dev: Tensor | Non
                                        q_eps=m.readout_query_norm.eps, pos0_dev=pos0_dev)
 
 
-def _finish_cached(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tensor | None,
-                   pos_idx: Tensor | None) -> Tensor:
-    """``mixed = W_o head``, cached as conv input at positions L .. L+n-1, then
+def _skinny_ok(x: Tensor, w: Tensor) -> bool:
+    """Whether ``lng_linear_at`` / ``lng_router_codes_at`` take ``x [B, n, K] . w^T`` (the decode
+    projections written straight into a cache)."""
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and x.shape[0] * x.shape[1] <= 64
+            and x.shape[-1] % 32 == 0 and w.shape[0] % 16 == 0)
+
+
+def _finish_cached(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tensor | None) -> Tensor:
+    """``mixed = W_o head``, cached as conv input at positions L .. L+n-1 (+ L_dev), then
     ``mixed + short_conv`` over the cached window (``infer.py:175-182``)."""
     b = head.shape[0]
-    mixed = ops.linear(head.reshape(b, n, m.readout_inner_dim), m.readout_o_proj.weight)
-    if pos_idx is None:
-        conv_in[:, L:L + n] = mixed
-        length = L + n
-    else:
-        conv_in.index_copy_(1, pos_idx, mixed.to(conv_in.dtype))
-        length = conv_in.shape[1]
+    x = head.reshape(b, n, m.readout_inner_dim)
+    w_o = m.readout_o_proj.weight
     conv = m.short_conv
-    conv._check(mixed, None)
+    if conv.conv.bias is not None:
+        raise NotImplementedError("conv bias is not supported by lng_causal_conv")
+    if _skinny_ok(x, w_o) and conv_in.dtype == torch.bfloat16:
+        ops.linear_at(x, w_o, conv_in, L, L_dev)     # the projection writes the cache rows
+    else:
+        mixed = ops.linear(x, w_o)
+        conv._check(mixed, None)
+        if L_dev is None:
+            conv_in[:, L:L + n] = mixed
+        else:
+            conv_in.index_copy_(1, L_dev.long() + torch.arange(n, device=x.device), mixed.to(conv_in.dtype))
+    length = L + n if L_dev is None else conv_in.shape[1]
     return ops.causal_conv_at(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps,
                               pos0=L, n=n, length=length, pos0_dev=L_dev, residual=True)
 
@@ -176,37 +188,45 @@ def memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tenso
             tokens = route_tokens.to(h.device, m.readout_kv_proj.weight.dtype)
         key, value = m._project_memory(tokens)
         head = m._manual_gqa(m._project_query(h), key, value)
-    return _finish_cached(m, head, state.conv_in[pos], L, n, None, None)
+    return _finish_cached(m, head, state.conv_in[pos], L, n, None)
 
 
-def static_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tensor, L_t: Tensor) -> Tensor:
+def static_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tensor | None, L_t: Tensor,
+                       router_x: Tensor | None = None) -> Tensor:
     """``memory_step`` with shapes independent of the cached length (the memory part of
     ``static_verify``, ``live_spec.py:100-114``): ``L_t`` is a 0-d device tensor holding the
-    length, the caches are written with ``index_copy_`` at ``L_t + arange(n)`` and the kernels read
-    the length on the device, so the launches can be captured in a HIP graph and replayed for any
-    length.  The caller advances ``state.length`` (and ``L_t``) afterwards."""
+    length (int32 saves a conversion), the kernels read it on the device and write the caches at
+    ``L_t .. L_t+n-1`` themselves (bf16, B*n <= 64; else ``index_copy_``), so the launches can be
+    captured in a HIP graph and replayed for any length.  ``codes_new`` None: the codes are
+    computed from ``router_x`` (``h_norm`` or the token features) straight into the code cache.
+    The caller advances ``state.length`` (and ``L_t``) afterwards."""
     mem = model.blocks[pos].memory
     m = mem.module
     n = h.shape[1]
     dev = h.device
-    L_long = L_t.to(torch.long)
-    pos_idx = L_long + torch.arange(n, device=dev)
+    L32 = (L_t if L_t.dtype == torch.int32 else L_t.to(torch.int32)).reshape(1)
     cache = state.codes[pos]
-    cache.index_copy_(1, pos_idx, codes_new.to(cache.dtype))
-    L32 = L_t.to(torch.int32).reshape(1)
+    if codes_new is None:
+        if router_x is None:
+            raise ValueError("static_memory_step needs codes_new or router_x")
+        if _skinny_ok(router_x, mem.router.weight) and mem.bits == 4:
+            ops.router_codes_at(router_x, mem.router.weight, cache, 0, L32)
+        else:
+            codes_new = mem.route_codes(router_x)[1]
+    if codes_new is not None:
+        cache.index_copy_(1, L32.long() + torch.arange(n, device=dev), codes_new.to(cache.dtype))
     if m._fused_shape_ok(h):
         head = _readout_head(m, h, cache, 0, L32)
     else:
         hist = m.route_history_length
-        hidx = L_long - hist + torch.arange(hist, device=dev)
-        hcodes = cache.index_select(1, hidx.clamp_min(0))
-        ctx = torch.cat((hcodes, codes_new.to(cache.dtype)), 1)
-        seg = torch.cat(((hidx >= 0).to(torch.int32), torch.ones(n, dtype=torch.int32, device=dev)))
+        hidx = L32.long() - hist + torch.arange(hist + n, device=dev)
+        ctx = cache.index_select(1, hidx.clamp_min(0))
+        seg = (hidx >= 0).to(torch.int32)
         tokens = m._lookup_route_chunk(ctx, None, 0, m.num_routes, seg[None].expand(h.shape[0], -1).contiguous(),
                                        None, target_length=n)
         key, value = m._project_memory(tokens)
         head = m._manual_gqa(m._project_query(h), key, value)
-    return _finish_cached(m, head, state.conv_in[pos], 0, n, L32, pos_idx)
+    return _finish_cached(m, head, state.conv_in[pos], 0, n, L32)
 
 
 # ------------------------------------------------------------------ one memory layer's step

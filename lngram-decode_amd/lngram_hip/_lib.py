@@ -76,6 +76,8 @@ SIGNATURES = {
                                 ctypes.POINTER(_p), _int, _i32, _p, _p, _i32, _p, _p]),
     "lng_rmsnorm": (_int, [_p, _p, _int, _i64, _i32, _f, _i32, _p, _p]),
     "lng_linear": (_int, [_p, _p, _int, _i64, _i64, _i64, _p, _p]),
+    "lng_linear_at": (_int, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
+    "lng_router_codes_at": (_int, [_p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _p]),
     "lng_sink_attention": (_int, [_p, _p, _p, _int, _i64, _i32, _i32, _i32, _i32, _f, _f, _p, _p]),
     "lng_sink_attention_strided": (_int, [_p, _p, _p, _int, _i64, _i32, _i32, _i32, _i32, _P64, _P64,
                                           _f, _f, _p, _p]),

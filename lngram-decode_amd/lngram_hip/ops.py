@@ -314,6 +314,42 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def _at_args(cache: torch.Tensor, pos0_dev: torch.Tensor | None):
+    if cache.dim() != 3 or not cache.is_contiguous():
+        raise ValueError("the cache must be a contiguous [B, S, N] tensor")
+    if pos0_dev is not None and (pos0_dev.dtype != torch.int32 or pos0_dev.numel() != 1):
+        raise ValueError("pos0_dev must be one int32 on the device")
+
+
+def linear_at(x: torch.Tensor, w: torch.Tensor, cache: torch.Tensor, pos0: int = 0,
+              pos0_dev: torch.Tensor | None = None) -> None:
+    """bf16 ``x [B, n, K] . w[N, K]^T`` written into ``cache [B, S, N]`` at positions
+    ``p0 .. p0+n-1``, ``p0 = pos0 (+ pos0_dev)`` (``lng_linear_at``; B*n <= 64)."""
+    dev = _dev(x, w, cache, pos0_dev)
+    _at_args(cache, pos0_dev)
+    b, n, k = x.shape
+    xc, wc = _c(x), _c(w.to(x.dtype))
+    if x.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16 or cache.shape[0] != b or cache.shape[2] != wc.shape[0]:
+        raise ValueError("linear_at: bf16 x [B, n, K] and cache [B, S, N]")
+    check(lib().lng_linear_at(_ptr(xc), _ptr(wc), b * n, wc.shape[0], k, n, cache.shape[1], int(pos0), _ptr(pos0_dev),
+                              _ptr(cache), _stream(dev)), "linear_at")
+
+
+def router_codes_at(x: torch.Tensor, w: torch.Tensor, cache: torch.Tensor, pos0: int = 0,
+                    pos0_dev: torch.Tensor | None = None) -> None:
+    """4-bit route codes of bf16 ``x [B, n, K] . w[4R, K]^T`` written into the uint8 code cache
+    ``[B, S, R]`` at positions ``p0 .. p0+n-1`` (``lng_router_codes_at``; B*n <= 64)."""
+    dev = _dev(x, w, cache, pos0_dev)
+    _at_args(cache, pos0_dev)
+    b, n, k = x.shape
+    xc, wc = _c(x), _c(w)
+    if (x.dtype != torch.bfloat16 or wc.dtype != torch.bfloat16 or cache.dtype != torch.uint8
+            or cache.shape[0] != b or 4 * cache.shape[2] != wc.shape[0]):
+        raise ValueError("router_codes_at: bf16 x [B, n, K], router [4R, K], uint8 cache [B, S, R]")
+    check(lib().lng_router_codes_at(_ptr(xc), _ptr(wc), b * n, k, wc.shape[0], n, cache.shape[1], int(pos0),
+                                    _ptr(pos0_dev), _ptr(cache), _stream(dev)), "router_codes_at")
+
+
 def linear_rowsq(x: torch.Tensor, w: torch.Tensor):
     """bf16 ``x [..., K] . w[N, K]^T`` plus the partial row sums of squares of the bf16 output
     (``[P, rows]`` fp32) that :func:`causal_conv_rowsq` consumes."""

@@ -109,10 +109,11 @@ def test_graph_captured_static_step_replays_eager(dev, shape):
         st.length = 16
         h_buf = torch.empty(1, n, w.d_model, dtype=w.dtype, device=dev)
         hn_buf = torch.empty_like(h_buf)
-        L_t = torch.full((), 16, dtype=torch.long, device=dev)
+        L_t = torch.full((), 16, dtype=torch.int32, device=dev)
 
         def step():
-            return static_memory_step(model, 0, st, h_buf, memory_codes(model, 0, st, h_norm=hn_buf), L_t)
+            # the codes go from the router straight into the code cache (bf16) or through index_copy_
+            return static_memory_step(model, 0, st, h_buf, None, L_t, router_x=hn_buf)
 
         # eager warm-up on a side stream writes past the cached length only, then capture
         h_buf.copy_(h[:, 16:20])
