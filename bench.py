@@ -35,6 +35,32 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def host_info() -> dict:
+    """The host cores a CPU baseline ran on: CPU model, the NUMA nodes holding the cores this
+    process may use, and their count."""
+    cpus = sorted(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), model)
+    except OSError:
+        pass
+    nodes = []
+    base = Path("/sys/devices/system/node")
+    for nd in sorted(base.glob("node[0-9]*")) if base.exists() else []:
+        try:
+            spec = (nd / "cpulist").read_text().strip()
+        except OSError:
+            continue
+        mine = set()
+        for part in filter(None, spec.split(",")):
+            a, _, b = part.partition("-")
+            mine.update(range(int(a), int(b or a) + 1))
+        if mine & set(cpus):
+            nodes.append(int(nd.name[4:]))
+    return {"cpu_model": model, "numa_nodes": nodes, "affinity_cpus": len(cpus)}
+
+
 def cpu_baseline(seconds: float) -> dict:
     """Oracle's PyTorch-CPU restatement of the reference SB forward (bf16, reference op order) on a
     bounded sample of the SB workload: 1 x 64-token windows, repeated for ~``seconds``."""
@@ -53,21 +79,29 @@ def cpu_baseline(seconds: float) -> dict:
     p["router.weight"] = sd["router.weight"]
     cfg = om.MemCfg(w.d_model, w.routes, w.mem_dim, w.q_heads, w.kv_heads, w.head_dim, eps=w.norm_eps)
     h = workloads.make_hidden(w, seed=1)
-    ones = torch.ones(w.d_model, dtype=w.dtype)
-    n_tok, t0 = 0, time.perf_counter()
-    while True:
-        h_norm = om.rms_norm(h, ones, w.norm_eps)
-        q = om.router_logits(h_norm, p["router.weight"], work=torch.float32)
-        codes = om.pack_route_codes(q.numpy(), 4)
-        om.memory_forward(p, cfg, h, codes)
-        n_tok += w.tokens
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+
+    def run(p, h, budget):
+        ones = torch.ones(w.d_model, dtype=h.dtype)
+        n_tok, t0 = 0, time.perf_counter()
+        while True:
+            h_norm = om.rms_norm(h, ones, w.norm_eps)
+            q = om.router_logits(h_norm, p["router.weight"], work=torch.float32)
+            codes = om.pack_route_codes(q.numpy(), 4)
+            om.memory_forward(p, cfg, h, codes)
+            n_tok += w.tokens
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return n_tok, el
+
+    n_tok, el = run(p, h, seconds)
+    n32, el32 = run({k: v.float() for k, v in p.items()}, h.float(), seconds / 2)
     del np
-    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port", **host_info(),
             "sample": f"SB shape (d1024, R184, bf16) 1x64-token windows, {n_tok} tokens in {el:.1f} s, "
-                      "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)"}
+                      "oracle PyTorch-CPU restatement of the reference forward (router fp32, module bf16)",
+            "fp32": {"value": n32 / el32, "unit": "tokens/s",
+                     "sample": f"the same forward with fp32 parameters and hidden states, {n32} tokens in "
+                               f"{el32:.1f} s"}}
 
 
 def sdc_cpu_baseline(seconds: float) -> dict:
@@ -104,7 +138,7 @@ def sdc_cpu_baseline(seconds: float) -> dict:
         el = time.perf_counter() - t0
         if el >= seconds:
             break
-    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": n_tok / el, "unit": "tokens/s", "cores": threads, "kind": "port", **host_info(),
             "sample": f"SD-C shape (d1024, R181, N256, bf16) 1x64-token windows, {n_tok} tokens in {el:.1f} s: "
                       "oracle SSM recurrence + router features + fp32 router + PyTorch-CPU module forward"}
 
@@ -138,7 +172,7 @@ def scaled_cpu_baseline(seconds: float) -> dict:
     rows = R * ((T - 1) + (T - 2))
     gbs = i * (rows * md * 2 + T * md * 4 + T * R) / el / 1e9
     del tabs
-    return {"value": n_tok / el, "unit": "tokens/s", "GBs": gbs, "cores": threads, "kind": "port",
+    return {"value": n_tok / el, "unit": "tokens/s", "GBs": gbs, "cores": threads, "kind": "port", **host_info(),
             "sample": f"184 routes, orders (2,3), table grown 4x ({(n2 + n3) * md * 2 / 1e9:.1f} GB bf16), "
                       f"{i} x 4096-token batches in {el:.1f} s: oracle row formula + PyTorch-CPU gather, fp32 sum"}
 
@@ -163,19 +197,27 @@ def draft_cpu_baseline(seconds: float) -> dict:
     c.commit(workloads.make_context(w, seed=0))
     commit_s = time.perf_counter() - t0
     spec = dtree.tree16()
-    steps = []
-    t_all = time.perf_counter()
-    while True:
-        t0 = time.perf_counter()
-        node = c.draft_tree(spec)
-        od.tree_accept(spec.parent, node, [node[i] for i in range(spec.n)])
-        steps.append((time.perf_counter() - t0) * 1e6)
-        if time.perf_counter() - t_all >= seconds:
-            break
+
+    def run(budget, least):
+        steps, t_all = [], time.perf_counter()
+        while True:
+            t0 = time.perf_counter()
+            node = c.draft_tree(spec)
+            od.tree_accept(spec.parent, node, [node[i] for i in range(spec.n)])
+            steps.append((time.perf_counter() - t0) * 1e6)
+            if time.perf_counter() - t_all >= budget and len(steps) >= least:
+                return steps
+
+    steps = run(seconds * 2 / 3, 1)
+    c.set_threads(1)
+    one = run(seconds / 3, 3)
     return {"value": float(np.median(steps)), "unit": "us per draft step", "cores": threads, "kind": "port",
+            **host_info(),
             "sample": f"{len(steps)} draft steps (16-node tree, 10 parent readouts over the full 32768 vocabulary, "
                       f"online counts) after committing the 2048-token context ({commit_s:.1f} s); C++ port of "
-                      "drafting/cpu/drafter.cpp with OpenMP"}
+                      "drafting/cpu/drafter.cpp with OpenMP",
+            "threads_1": {"value": float(np.median(one)), "unit": "us per draft step", "cores": 1,
+                          "sample": f"{len(one)} of the same steps on one thread"}}
 
 
 def draft_step(dev, iters: int, warmup: int):
@@ -461,7 +503,8 @@ def _scaled_run(tabs, codes, B, T, R, orders, sl, md, steps: int, warmup: int) -
                         "(51,249,152 x 128 bf16 = 13.1 GB), uniform random codes",
             "kernel": "k_gather_sum_scaled", "tokens_per_s": B * T / (ms * 1e-3), "avg_ms": ms,
             "algorithmic_bytes": alg, "achieved_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "steps": steps,
-            "traffic": measured_traffic("gather_sum_scaled_traffic.json")}
+            "traffic": measured_traffic("gather_sum_scaled_traffic.json"),
+            "traffic_source": "profiles/gather_sum_scaled_traffic.json (committed counter summary)"}
 
 
 def copy_bandwidth(dev, mib: int = 2048, reps: int = 10) -> float:
@@ -621,7 +664,10 @@ def main() -> None:
         "roofline": {"bound": "hbm", "kernel": "k_readout_fused", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes": fused_bytes, "avg_ms": fused_ms,
-                     "timed_launches": f"HIP events around every {EVENT_STRIDE}th launch of the timed loop"},
+                     "timed_launches": f"HIP events around every {EVENT_STRIDE}th launch of the timed loop",
+                     "traffic_source": "profiles/readout_fused_sb_traffic.json: rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                       "per dispatch of this kernel at this workload, copy-calibrated; read from "
+                                       "the committed summary, not measured in this run"},
         "layer_hbm_frac": layer_gbs / HBM_PEAK_GBS,
         "layer_algorithmic_bytes": layer_bytes,
         "copy_GBs": copy_gbs,

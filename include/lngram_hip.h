@@ -3,10 +3,19 @@
  *
  * Conventions (every entry point):
  *   - Tensors are caller-owned device buffers, row-major and contiguous.
- *   - Calls are ordered on `stream` (a hipStream_t passed as void*), allocate
- *     nothing, keep no pointer after return, and return 0 or a negative LNG_E_*.
+ *   - Calls are ordered on `stream` (a hipStream_t passed as void*), keep no
+ *     pointer to a caller's buffer after return, and return 0 or a negative LNG_E_*.
+ *   - Device memory is the caller's: scratch comes in as a workspace argument.
+ *     Three kinds of host-side state are kept per process, each made once and
+ *     guarded by a mutex, so calls stay reentrant from any host thread:
+ *       * the plain bf16 projections at M >= 1024 (lng_linear) run through
+ *         hipBLASLt, chosen by shape alone: one handle per device and one matmul
+ *         plan per (device, M, N, K), made on the first call of that shape (the
+ *         library allocates them); a shape with no plan runs the MFMA kernel;
+ *       * lng_drafter_tree_fused caches its cooperative grid size per device;
+ *       * lng_ssm_scan_static uses a static device array per GPU (its own
+ *         comment gives the limit), located once per device.
  *   - lng_last_error() returns a thread-local message for the last failure.
- *   - No mutable globals: calls are reentrant from any host thread.
  *   - dtype codes: LNG_F32, LNG_BF16, LNG_F16, LNG_U8, LNG_I32, LNG_I64.
  *
  * Each declaration names the reference interface (file:line in the reference
@@ -122,7 +131,10 @@ int lng_router_codes_at(const void* x, const void* w, int64_t M, int64_t K, int6
 
 /* y[M,N] = x[M,K] . w[N,K]^T in `dtype` (fp32 accumulation, output rounded to
  * dtype).  nn.Linear without bias as used by readout_q_proj / readout_kv_proj /
- * readout_o_proj (lngram_v2.py:1115-1131, :1354-1359) and the draft head. */
+ * readout_o_proj (lngram_v2.py:1115-1131, :1354-1359) and the draft head.
+ * bf16 at M >= 1024, N >= 256, K >= 256 runs on hipBLASLt (host-side plan, see the
+ * conventions above); M <= 64 on the skinny MFMA kernel; the rest on the tiled MFMA
+ * kernels.  fp32 runs in fp32 FMA. */
 int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, int64_t K, void* y,
                void* stream);
 

@@ -115,6 +115,7 @@ class CpuDrafter {
   std::vector<float> ssm;      // [n, N]
 
   int64_t length() const { return static_cast<int64_t>(tokens.size()); }
+  void set_threads(int t) { threads_ = std::max(1, t); }
 
   int commit(const int64_t* toks, int64_t n, const uint8_t* over) {
     Cursor cur = cursor();
@@ -436,6 +437,12 @@ void* cdr_create(const cdr_config* c, const cdr_weights* w, int threads, int onl
 void cdr_destroy(void* h) { delete static_cast<CpuDrafter*>(h); }
 
 int64_t cdr_length(void* h) { return static_cast<CpuDrafter*>(h)->length(); }
+
+void cdr_set_threads(void* h, int threads) {
+  auto* d = static_cast<CpuDrafter*>(h);
+  std::lock_guard<std::mutex> g(d->mu);
+  d->set_threads(threads);
+}
 
 void cdr_reset(void* h) {
   auto* d = static_cast<CpuDrafter*>(h);

@@ -51,6 +51,7 @@ def load():
                                ctypes.c_float]),
             "cdr_destroy": (None, [P]),
             "cdr_length": (i64, [P]),
+            "cdr_set_threads": (None, [P, ctypes.c_int]),
             "cdr_reset": (None, [P]),
             "cdr_truncate": (ctypes.c_int, [P, i64, i32, i32]),
             "cdr_commit": (ctypes.c_int, [P, P, i64, P]),
@@ -128,6 +129,11 @@ class CppDrafterPort:
     def reset(self) -> None:
         load().cdr_reset(self._h)
         self._tokens = []
+
+    def set_threads(self, threads: int) -> None:
+        """OpenMP threads for the later calls."""
+        self.threads = max(1, int(threads))
+        load().cdr_set_threads(self._h, self.threads)
 
     @property
     def length(self) -> int:
