@@ -507,6 +507,62 @@ def _scaled_run(tabs, codes, B, T, R, orders, sl, md, steps: int, warmup: int) -
             "traffic_source": "profiles/gather_sum_scaled_traffic.json (committed counter summary)"}
 
 
+def surrogate_backward(dev, steps: int, warmup: int):
+    """Set up, and return the timing run of, the lookup surrogate's backward at the SB shape: 8 x 2048
+    tokens, 184 routes, mem_dim 128, bf16 tables of orders 2 and 3, approximate mode; one step = the
+    route-logit gradient of both orders (one ``k_surrogate_grad`` launch per order) from resident
+    memory gradients, looked-up rows, logits and codes."""
+    import torch
+
+    from lngram_hip import ops
+
+    B, T, R, D, bits = 8, 2048, 184, 128, 4
+    g = torch.Generator(device=dev).manual_seed(11)
+    codes = torch.randint(0, 16, (B, T, R), device=dev, dtype=torch.uint8, generator=g)
+    q = torch.randn(B, T, R, bits, device=dev, generator=g)
+    legs = []
+    for order in (2, 3):
+        table = torch.empty(R << (bits * order), D, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=g)
+        grad = torch.empty(B, T, R, D, dtype=torch.bfloat16, device=dev).normal_(0.0, 1.0, generator=g)
+        valid = torch.ones(B, T, dtype=torch.bool, device=dev)
+        valid[:, :order - 1] = False
+        hard = ops.route_tokens(codes, [table], [order], bits)
+        legs.append((order, table, grad, valid, hard))
+
+    def step():
+        for order, table, grad, valid, hard in legs:
+            ops.surrogate_grad(grad, hard, q, codes, table, valid, order, bits, 0, 1.0, 1.0, False)
+
+    def run() -> dict:
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        with ops.KernelTimer("surrogate_grad") as kt:
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            el = time.perf_counter() - t0
+        d = kt.durations_ms()
+        per_order = {f"order_{o}_us": 1e3 * sum(d[i::2]) / len(d[i::2]) for i, o in enumerate((2, 3))}
+        ms = el / steps * 1e3
+        # per (token, route, order n): the memory-gradient row, the looked-up row and n*bits
+        # counterfactual rows (256 B each), 16 B of logits, 16 B of gradient, the code
+        alg = B * T * R * sum((2 + n * bits) * D * 2 + 2 * bits * 4 + 1 for n in (2, 3))
+        kern_ms = sum(d) / len(d) * 2
+        gbs = alg / (kern_ms * 1e-3) / 1e9
+        legs.clear()
+        torch.cuda.empty_cache()
+        return {"workload": "lookup surrogate backward (approximate) at the SB shape: B8 x T2048, R184, mem_dim 128, "
+                            "bf16 tables of orders 2 and 3; route-logit gradient of both orders",
+                "kernel": "k_surrogate_grad", "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), **per_order,
+                "algorithmic_bytes": alg, "achieved_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "steps": steps,
+                "note": "the counterfactual rows of a window lie in its route's block (1 MB of the 3-gram table), "
+                        "so most of these bytes come from L2 / the Infinity Cache"}
+
+    return run
+
+
 def copy_bandwidth(dev, mib: int = 2048, reps: int = 10) -> float:
     """Bytes read + written per second by a plain device-to-device copy of ``mib`` MiB (HIP
     events over ``reps`` copies): the bandwidth a streaming kernel reaches on this GPU, reported
@@ -556,6 +612,7 @@ def main() -> None:
     ap.add_argument("--no-draft", action="store_true")
     ap.add_argument("--no-scaled", action="store_true")
     ap.add_argument("--no-sdc", action="store_true")
+    ap.add_argument("--no-train", action="store_true", help="skip the surrogate-backward leg")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB before warmup (known-size kernel that scales "
                          "hardware byte counters)")
@@ -606,6 +663,9 @@ def main() -> None:
     if not args.no_draft:
         log("cached decode step: set-up")
         legs["decode_step"] = decode_step(dev, args.draft_iters, 20)
+    if not args.no_train:
+        log("surrogate backward: set-up")
+        legs["surrogate_backward"] = surrogate_backward(dev, max(3, args.steps // 4), 2)
     if not args.no_sdc:
         log("tiny and SD-C forwards: set-up")
         legs["tiny_forward"] = tiny_forward(dev, 50, 5)

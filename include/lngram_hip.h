@@ -257,6 +257,33 @@ int lng_gather_sum_scaled(const void* const* tables, int table_dtype, int32_t me
                           int64_t B, int64_t T, int32_t R, const int32_t* orders, int32_t n_orders, int32_t bits,
                           int32_t scale_log2, uint32_t seed, float* out, void* stream);
 
+/* Route-logit gradient of the lookup surrogate for one n-gram order: the backward of
+ * _LngramSurrogate (ffnmem/memory/lngram_v2.py:328-464; approximate mode :430-447, exact mode
+ * :394-429).  grad_memory, hard_memory [B, T, R, mem_dim] in mem_dtype (f32 or bf16, the table's
+ * dtype); q_logits [B, T, R, bits] (f32 or bf16); codes [B, T, R] (u8, i32 or i64) of routes
+ * route_start .. route_start + R - 1; table [table_rows, mem_dim] (the order's table, rows
+ * (route_start + r) * 2^(bits*order) + address); valid_mask [B, T] (the reference's _valid_mask,
+ * null = all valid).  Writes grad_q [B, T, R, bits] in out_dtype (f32 or bf16): the per-bit
+ * counterfactual scores times scale * temperature * p(1-p) (exact = 0), or the alphabet-wide
+ * expectation derivative (exact = 1), p = sigmoid(temperature * q).  Zero when T < order,
+ * temperature == 0 or scale == 0.  mem_dim in {32, 64, 128, 256}; 1 <= order <= 4, bits <= 8.
+ * Each output is a fixed sum in the reference's order (no atomics). */
+int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
+                       int q_dtype, const void* codes, int codes_dtype, const void* table, int64_t table_rows,
+                       const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start,
+                       int32_t mem_dim, int32_t order, int32_t bits, float temperature, float scale, int exact,
+                       void* grad_q, int out_dtype, void* stream);
+
+/* Table gradient of one order's lookup: the embedding backward behind _LngramSurrogate's
+ * pass-through of the memory gradient (lngram_v2.py:1084-1092, :454).  table_grad
+ * [table_rows, mem_dim] fp32 (the caller zeroes it) += grad_memory[b, t, r, :] at row
+ * (route_start + r) * 2^(bits*order) + address of the window ending at t, for t >= order-1 and
+ * valid_mask[b, t] (null = all valid).  fp32 atomics: rows met several times sum in a varying
+ * order.  mem_dim in {32, 64, 128, 256}. */
+int lng_table_grad(const void* grad_memory, int mem_dtype, const void* codes, int codes_dtype,
+                   const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start, int32_t mem_dim,
+                   int32_t order, int32_t bits, int64_t table_rows, float* table_grad, void* stream);
+
 /* ---------------------------------------------------------------- K4: SSM scan */
 /* s[B,T,N] (fp32): s_t = a*s_{t-1} + (1-a)*u_t, s_{-1} = s0[B,N] (zero if null).
  * chunked_scan / sequential_scan (ffnmem/memory/ssm.py:58-91) and the carried

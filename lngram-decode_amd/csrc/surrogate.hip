@@ -1,0 +1,373 @@
+// Route-logit gradient of the n-gram lookup's surrogate (training): the backward of
+// _LngramSurrogate (ffnmem/memory/lngram_v2.py:328-464) for one n-gram order.
+//
+// The forward is the identity on the looked-up memory; the backward passes the memory gradient
+// through and gives the route logits q [B, T, R, bits] a gradient from counterfactual rows.  With
+// window s = 0 .. VL-1 (VL = T - order + 1) ending at position p = s + order - 1, its row
+// idx_s = (route_start + r) * A^order + sum_k c[s+k] * A^k (A = 2^bits, oldest code least
+// significant), the masked memory gradient g_s = grad[b, p, r, :] * valid[b, p] and the current
+// row m_s = hard_memory[b, p, r, :]:
+//
+//   approximate:  G[t, bit] += sign * (table[idx_s ^ (1 << (e*bits + bit))] . g_s - m_s . g_s)
+//                 for every e = 0 .. order-1 with t = s + e, sign = +1 if that bit of idx_s is 0
+//                 else -1; then G *= scale * temperature * p (1 - p), p = sigmoid(temperature * q)
+//   exact:        G[t, bit] += scale * temperature * sum_{code < A} P(code) (bit(code) - p_bit)
+//                                                  * (table[idx_s + (code - c[t]) * A^e] . g_s)
+//                 P(code) = prod_b (bit_b(code) ? p_b : 1 - p_b) at position t
+//
+// A block owns one route r of one sequence b and a tile of P = 64 - (order - 1) consecutive
+// positions; its 16-lane groups take the 64 windows whose digits fall in the tile (the tile's
+// windows plus order - 1 before it), one window at a time: lane l holds elements [l*V, l*V + V)
+// of every row (D = 16 V), a dot product is a per-lane sum reduced over the 16 lanes.  A window's
+// memory-gradient and looked-up rows are read once (non-temporal: they are streamed), its
+// order * bits scores go to LDS, and each output sums its windows' scores in the reference's order
+// (e ascending), so the result is a fixed sum with no atomics.  Blocks are numbered so that the
+// blocks of one XCD work on one route at a time (the dispatcher deals blocks to the 8 XCDs in
+// turn): the route's block of the table (1 MB for order 3, mem_dim 128, bf16) stays in that
+// XCD's L2 while every counterfactual row is read from it.  Codes are read under the digit mask
+// A - 1, so every row stays inside its route's block of the table.
+#include "common.h"
+
+namespace lng {
+
+constexpr int SG_GROUPS = 16;  // 16-lane groups per 256-thread block
+constexpr int SG_MAXBITS = 8;
+constexpr int SG_MAXORDER = 4;
+
+struct SgArgs {
+  const void* grad;       // [B, T, R, D] memory gradient (TM)
+  const void* hard;       // [B, T, R, D] looked-up memory (TM)
+  const void* q;          // [B, T, R, bits] route logits
+  int q_dt;
+  const void* codes;      // [B, T, R] codes of these routes
+  int codes_dt;
+  const void* table;      // [rows, D] (TM)
+  const uint8_t* valid;   // [B, T] or null (all valid)
+  int64_t B, T;
+  int32_t R, route_start, order, bits;
+  float temperature, scale, alpha;   // alpha = scale * temperature (rounded as the reference's scalar)
+  void* out;              // [B, T, R, bits] in out_dt
+  int out_dt;
+  int64_t tiles;          // position tiles per sequence
+  int32_t nt;             // memory rows within 4 GB of their base: stream them with non-temporal loads
+};
+
+// V consecutive elements of a row to fp32 (V * sizeof(TM) bytes, aligned to that size)
+template <typename TM, int V>
+__device__ __forceinline__ void load_row(const TM* p, float (&v)[V]) {
+  if constexpr (sizeof(TM) * V == 16) {
+    const u32x4 w = *reinterpret_cast<const u32x4*>(p);
+    const TM* e = reinterpret_cast<const TM*>(&w);
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = to_f32(e[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < V; ++j) v[j] = to_f32(p[j]);
+  }
+}
+
+__device__ __forceinline__ float sum16(float v) {
+  // sum over the 16 lanes of this lane's row of the wave (DPP shifts within the row, then the
+  // row's last lane broadcast to the row)
+  v += dpp_row_shr<0x111>(v, 0.f);
+  v += dpp_row_shr<0x112>(v, 0.f);
+  v += dpp_row_shr<0x114>(v, 0.f);
+  v += dpp_row_shr<0x118>(v, 0.f);
+  return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(((threadIdx.x & 63) | 15) << 2,
+                                                                 __builtin_bit_cast(int, v)));
+}
+
+__device__ __forceinline__ int64_t sg_code(const void* p, int dt, int64_t i) {
+  if (dt == LNG_U8) return static_cast<const uint8_t*>(p)[i];
+  if (dt == LNG_I32) return static_cast<const int32_t*>(p)[i];
+  return static_cast<const int64_t*>(p)[i];
+}
+
+template <typename TM, int V>
+__device__ __forceinline__ void load_row_nt(const TM* base, int64_t e, bool nt, float (&v)[V]) {
+  // e: element offset from base; nt needs e * sizeof(TM) < 2^32 (checked by the host) and whole
+  // 16-byte pieces
+  if constexpr ((sizeof(TM) * V) % 16 == 0) {
+    if (nt) {
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<TM*>(base), 0, -1, BUF_DW3);
+#pragma unroll
+      for (int c = 0; c < static_cast<int>(sizeof(TM) * V / 16); ++c) {
+        const u32x4 w = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rs, static_cast<uint32_t>(e * sizeof(TM)) + 16u * c, 0, CPOL_NT));
+        const TM* x = reinterpret_cast<const TM*>(&w);
+#pragma unroll
+        for (int j = 0; j < static_cast<int>(16 / sizeof(TM)); ++j) v[c * (16 / sizeof(TM)) + j] = to_f32(x[j]);
+      }
+      return;
+    }
+  }
+  load_row<TM, V>(base + e, v);
+}
+
+constexpr int SG_WIN = 64;                       // windows per block (16 groups x 4)
+constexpr int SG_SC = SG_MAXORDER * SG_MAXBITS;  // scores per window in LDS: [e][bit]
+
+template <typename TM, int V, bool EXACT>
+__global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
+  __shared__ float sc[SG_WIN][SG_SC];
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  // block -> (route, sequence, tile): XCD x = block % 8 keeps to routes r = 8j + x, all of a route's
+  // (sequence, tile) blocks in a row
+  const int64_t xcd = blockIdx.x & 7;
+  const int64_t k8 = blockIdx.x >> 3;
+  const int64_t per_route = a.B * a.tiles;
+  const int64_t r64 = (k8 / per_route) * 8 + xcd;
+  if (r64 >= a.R) return;                        // the whole block: before any barrier
+  const int32_t r = static_cast<int32_t>(r64);
+  const int64_t rem = k8 % per_route;
+  const int64_t b = rem / a.tiles;
+  const int bits = a.bits, order = a.order;
+  const int P = SG_WIN - (order - 1);
+  const int64_t t0 = (rem % a.tiles) * P;
+  const int64_t s_lo = t0 - (order - 1);         // the window of local index 0
+  const int64_t VL = a.T - order + 1;
+  const int64_t A = int64_t(1) << bits;
+  const int64_t dmask = A - 1;
+  const int64_t D = 16 * V;
+  const int64_t RD = static_cast<int64_t>(a.R) * D;
+  const TM* grad = static_cast<const TM*>(a.grad);
+  const TM* hard = static_cast<const TM*>(a.hard);
+  const TM* table = static_cast<const TM*>(a.table);
+  const bool nt = a.nt != 0;
+  const int64_t block_base = static_cast<int64_t>(a.route_start + r) << (bits * order);
+  const bool active = VL > 0 && a.temperature != 0.f && a.scale != 0.f;
+
+  for (int w = grp; w < SG_WIN; w += 16) {
+    const int64_t s = s_lo + w;
+    float score[SG_MAXORDER][SG_MAXBITS];
+#pragma unroll
+    for (int e = 0; e < SG_MAXORDER; ++e)
+#pragma unroll
+      for (int k = 0; k < SG_MAXBITS; ++k) score[e][k] = 0.f;
+    if (active && s >= 0 && s < VL) {
+      const int64_t pos = s + order - 1;
+      const float vm = (a.valid == nullptr || a.valid[b * a.T + pos]) ? 1.f : 0.f;
+      int64_t addr = 0;
+      int64_t digit[SG_MAXORDER];
+#pragma unroll
+      for (int k = 0; k < SG_MAXORDER; ++k) {
+        digit[k] = 0;
+        if (k < order) {
+          digit[k] = sg_code(a.codes, a.codes_dt, (b * a.T + s + k) * a.R + r) & dmask;
+          addr |= digit[k] << (k * bits);
+        }
+      }
+      const int64_t idx = block_base + addr;
+      const int64_t mrow = (b * a.T + pos) * RD + static_cast<int64_t>(r) * D + l * V;
+      float g[V];
+      load_row_nt<TM, V>(grad, mrow, nt, g);
+#pragma unroll
+      for (int j = 0; j < V; ++j) g[j] *= vm;
+      if constexpr (!EXACT) {
+        float m[V];
+        load_row_nt<TM, V>(hard, mrow, nt, m);
+        float cd = 0.f;
+#pragma unroll
+        for (int j = 0; j < V; ++j) cd += m[j] * g[j];
+        cd = sum16(cd);
+#pragma unroll
+        for (int e = 0; e < SG_MAXORDER; ++e) {
+          if (e < order) {
+            // the counterfactual rows of digit e, four at a time, requested before any is reduced
+#pragma unroll
+            for (int k0 = 0; k0 < SG_MAXBITS; k0 += 4) {
+              if (k0 < bits) {
+                float f[4][V];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                  if (k0 + k < bits)
+                    load_row<TM, V>(table + (idx ^ (int64_t(1) << (e * bits + k0 + k))) * D + l * V, f[k]);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                  if (k0 + k < bits) {
+                    float fd = 0.f;
+#pragma unroll
+                    for (int j = 0; j < V; ++j) fd += f[k][j] * g[j];
+                    fd = sum16(fd);
+                    score[e][k0 + k] = (fd - cd) * (((idx >> (e * bits + k0 + k)) & 1) ? -1.f : 1.f);
+                  }
+                }
+              }
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < SG_MAXORDER; ++e) {
+          if (e < order) {
+            float p[SG_MAXBITS];
+#pragma unroll
+            for (int k = 0; k < SG_MAXBITS; ++k) {
+              p[k] = 0.f;
+              if (k < bits) {
+                const int64_t qi = ((b * a.T + s + e) * a.R + r) * bits + k;
+                const float qv = a.q_dt == LNG_BF16 ? to_f32(static_cast<const bf16*>(a.q)[qi])
+                                                    : static_cast<const float*>(a.q)[qi];
+                p[k] = 1.f / (1.f + expf(-(a.temperature * qv)));
+              }
+            }
+            const int64_t step = int64_t(1) << (e * bits);
+            const int64_t base = idx - digit[e] * step;
+#pragma unroll 1
+            for (int64_t code = 0; code < A; ++code) {
+              float v[V];
+              load_row<TM, V>(table + (base + code * step) * D + l * V, v);
+              float dot = 0.f;
+#pragma unroll
+              for (int j = 0; j < V; ++j) dot += v[j] * g[j];
+              dot = sum16(dot);
+              float cp = 1.f;
+#pragma unroll
+              for (int k = 0; k < SG_MAXBITS; ++k)
+                if (k < bits) cp *= ((code >> k) & 1) ? p[k] : 1.f - p[k];
+#pragma unroll
+              for (int k = 0; k < SG_MAXBITS; ++k) {
+                if (k < bits) {
+                  const float local = cp * (static_cast<float>((code >> k) & 1) - p[k]) * dot;
+                  score[e][k] = fmaf(a.alpha, local, score[e][k]);
+                }
+              }
+            }
+          }
+        }
+      }
+    }
+    if (l == 0) {
+#pragma unroll
+      for (int e = 0; e < SG_MAXORDER; ++e)
+#pragma unroll
+        for (int k = 0; k < SG_MAXBITS; ++k) sc[w][e * SG_MAXBITS + k] = score[e][k];
+    }
+  }
+  __syncthreads();
+  // output (t, bit): the windows t - e, e ascending
+  for (int i = threadIdx.x; i < P * bits; i += 256) {
+    const int tl = i / bits, k = i - (i / bits) * bits;
+    const int64_t t = t0 + tl;
+    if (t >= a.T) break;
+    float acc = 0.f;
+    for (int e = 0; e < order; ++e) acc += sc[tl + order - 1 - e][e * SG_MAXBITS + k];
+    const int64_t oi = ((b * a.T + t) * a.R + r) * bits + k;
+    if (!EXACT && active) {
+      const float qv = a.q_dt == LNG_BF16 ? to_f32(static_cast<const bf16*>(a.q)[oi]) : static_cast<const float*>(a.q)[oi];
+      const float p = 1.f / (1.f + expf(-(a.temperature * qv)));
+      acc *= a.alpha * p * (1.f - p);
+    }
+    if (a.out_dt == LNG_BF16)
+      static_cast<bf16*>(a.out)[oi] = static_cast<bf16>(acc);
+    else
+      static_cast<float*>(a.out)[oi] = acc;
+  }
+}
+
+// Table gradient of the lookup (the embedding backward behind the surrogate's pass-through,
+// lngram_v2.py:1084-1092 and :454): table_grad[row(b, t, r)] += grad[b, t, r, :] * valid[b, t] for
+// every position with an order-`order` window.  One 16-lane group per (b, t, r); fp32 atomics, so
+// rows met several times sum in an order that varies between calls.
+template <typename TM, int V>
+__global__ __launch_bounds__(256) void k_table_grad(SgArgs a, float* __restrict__ table_grad) {
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  const int64_t o = static_cast<int64_t>(blockIdx.x) * SG_GROUPS + grp;
+  if (o >= a.B * a.T * a.R) return;
+  const int32_t r = static_cast<int32_t>(o % a.R);
+  const int64_t bt = o / a.R;
+  const int64_t t = bt % a.T, b = bt / a.T;
+  const int bits = a.bits, order = a.order;
+  if (t < order - 1) return;
+  if (a.valid != nullptr && !a.valid[b * a.T + t]) return;
+  const int64_t dmask = (int64_t(1) << bits) - 1;
+  const int64_t s = t - order + 1;
+  int64_t addr = 0;
+  for (int k = 0; k < order; ++k)
+    addr |= (sg_code(a.codes, a.codes_dt, (b * a.T + s + k) * a.R + r) & dmask) << (k * bits);
+  const int64_t row = (static_cast<int64_t>(a.route_start + r) << (bits * order)) + addr;
+  const int64_t D = 16 * V;
+  float g[V];
+  load_row<TM, V>(static_cast<const TM*>(a.grad) + o * D + l * V, g);
+  float* dst = table_grad + row * D + l * V;
+#pragma unroll
+  for (int j = 0; j < V; ++j) atomicAdd(dst + j, g[j]);
+}
+
+template <typename TM, bool EXACT>
+static int sg_launch_v(const SgArgs& a, int64_t D, hipStream_t s) {
+  const int64_t blocks = 8 * cdiv(a.R, 8) * a.B * a.tiles;
+  if (blocks > 0x7FFFFFFF) return fail(LNG_E_ARG, "surrogate_grad: too many blocks");
+  switch (D) {
+    case 32: k_surrogate_grad<TM, 2, EXACT><<<blocks, 256, 0, s>>>(a); break;
+    case 64: k_surrogate_grad<TM, 4, EXACT><<<blocks, 256, 0, s>>>(a); break;
+    case 128: k_surrogate_grad<TM, 8, EXACT><<<blocks, 256, 0, s>>>(a); break;
+    case 256: k_surrogate_grad<TM, 16, EXACT><<<blocks, 256, 0, s>>>(a); break;
+    default: return fail(LNG_E_ARG, "surrogate_grad: mem_dim must be 32, 64, 128 or 256");
+  }
+  return check_launch("k_surrogate_grad");
+}
+
+}  // namespace lng
+
+using namespace lng;
+
+extern "C" int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
+                                  int q_dtype, const void* codes, int codes_dtype, const void* table,
+                                  int64_t table_rows, const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R,
+                                  int32_t route_start, int32_t mem_dim, int32_t order, int32_t bits,
+                                  float temperature, float scale, int exact, void* grad_q, int out_dtype,
+                                  void* stream) {
+  if (B < 0 || T < 0 || R <= 0 || route_start < 0 || order < 1 || order > SG_MAXORDER || bits < 1 ||
+      bits > SG_MAXBITS || bits * order > 40)
+    return fail(LNG_E_ARG, "surrogate_grad: bad shape (1 <= order <= 4, 1 <= bits <= 8)");
+  if (mem_dtype != LNG_F32 && mem_dtype != LNG_BF16) return fail(LNG_E_DTYPE, "surrogate_grad: memory f32 or bf16");
+  if ((q_dtype != LNG_F32 && q_dtype != LNG_BF16) || (out_dtype != LNG_F32 && out_dtype != LNG_BF16))
+    return fail(LNG_E_DTYPE, "surrogate_grad: logits and gradient f32 or bf16");
+  if (codes_dtype != LNG_U8 && codes_dtype != LNG_I32 && codes_dtype != LNG_I64)
+    return fail(LNG_E_DTYPE, "surrogate_grad: codes u8, i32 or i64");
+  if (!grad_memory || !hard_memory || !q_logits || !codes || !table || !grad_q)
+    return fail(LNG_E_ARG, "surrogate_grad: null buffer");
+  const int64_t need = (static_cast<int64_t>(route_start) + R) << (bits * order);
+  if (table_rows < need) return fail(LNG_E_ARG, "surrogate_grad: table has fewer rows than (route_start + R) * 2^(bits*order)");
+  if (B * T == 0) return LNG_OK;
+  const int64_t mem_bytes = B * T * R * static_cast<int64_t>(mem_dim) * (mem_dtype == LNG_BF16 ? 2 : 4);
+  SgArgs a{grad_memory, hard_memory, q_logits, q_dtype, codes, codes_dtype, table, valid_mask, B, T, R, route_start,
+           order, bits, temperature, scale, static_cast<float>(static_cast<double>(scale) * temperature), grad_q,
+           out_dtype, cdiv(T, SG_WIN - (order - 1)), mem_bytes < (int64_t(1) << 32) ? 1 : 0};
+  hipStream_t s = as_stream(stream);
+  if (mem_dtype == LNG_BF16)
+    return exact ? sg_launch_v<bf16, true>(a, mem_dim, s) : sg_launch_v<bf16, false>(a, mem_dim, s);
+  return exact ? sg_launch_v<float, true>(a, mem_dim, s) : sg_launch_v<float, false>(a, mem_dim, s);
+}
+
+extern "C" int lng_table_grad(const void* grad_memory, int mem_dtype, const void* codes, int codes_dtype,
+                              const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start,
+                              int32_t mem_dim, int32_t order, int32_t bits, int64_t table_rows, float* table_grad,
+                              void* stream) {
+  if (B < 0 || T < 0 || R <= 0 || route_start < 0 || order < 1 || order > SG_MAXORDER || bits < 1 ||
+      bits > SG_MAXBITS || bits * order > 40)
+    return fail(LNG_E_ARG, "table_grad: bad shape (1 <= order <= 4, 1 <= bits <= 8)");
+  if (mem_dtype != LNG_F32 && mem_dtype != LNG_BF16) return fail(LNG_E_DTYPE, "table_grad: memory f32 or bf16");
+  if (codes_dtype != LNG_U8 && codes_dtype != LNG_I32 && codes_dtype != LNG_I64)
+    return fail(LNG_E_DTYPE, "table_grad: codes u8, i32 or i64");
+  if (!grad_memory || !codes || !table_grad) return fail(LNG_E_ARG, "table_grad: null buffer");
+  if (table_rows < ((static_cast<int64_t>(route_start) + R) << (bits * order)))
+    return fail(LNG_E_ARG, "table_grad: table has fewer rows than (route_start + R) * 2^(bits*order)");
+  if (B * T == 0) return LNG_OK;
+  SgArgs a{grad_memory, nullptr, nullptr, LNG_F32, codes, codes_dtype, nullptr, valid_mask, B, T, R, route_start,
+           order, bits, 0.f, 0.f, 0.f, nullptr, LNG_F32, 0, 0};
+  hipStream_t s = as_stream(stream);
+  const int64_t blocks = cdiv(B * T * R, SG_GROUPS);
+#define TG_LAUNCH(TM, V) k_table_grad<TM, V><<<blocks, 256, 0, s>>>(a, table_grad)
+  const bool bf = mem_dtype == LNG_BF16;
+  switch (mem_dim) {
+    case 32: if (bf) TG_LAUNCH(bf16, 2); else TG_LAUNCH(float, 2); break;
+    case 64: if (bf) TG_LAUNCH(bf16, 4); else TG_LAUNCH(float, 4); break;
+    case 128: if (bf) TG_LAUNCH(bf16, 8); else TG_LAUNCH(float, 8); break;
+    case 256: if (bf) TG_LAUNCH(bf16, 16); else TG_LAUNCH(float, 16); break;
+    default: return fail(LNG_E_ARG, "table_grad: mem_dim must be 32, 64, 128 or 256");
+  }
+#undef TG_LAUNCH
+  return check_launch("k_table_grad");
+}

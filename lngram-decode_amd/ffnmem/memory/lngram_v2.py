@@ -7,11 +7,14 @@ methods that the reference's callers use (``quantize_route_logits``,
 ``:1354-1407``, ``:1887-1920``).  Every forward op is a gfx950 kernel from
 ``lngram_hip``; tensors must be on a ROCm device.
 
-Scope: eval-mode forward.  The surrogate route gradient, dropout and the
-context-parallel / streaming-state / packed-segment conv machinery of the
-reference (training and unused paths) raise ``NotImplementedError``.  The
-``streaming`` execution mode computes the same function as ``full``; both run
-the same kernels (the fused kernel is itself an online softmax over routes).
+Scope: the eval-mode forward, and the training-mode lookup with its surrogate route gradient
+(``_LngramSurrogate``, ``lngram_v2.py:328-464``: ``_lookup_route_chunk`` with route logits under
+autograd gives the route logits their counterfactual gradient and the tables their gather
+gradient, both on gfx950 kernels).  The readout after the lookup has no backward here, so the
+module's forward in training mode, dropout and the context-parallel / streaming-state /
+packed-segment conv machinery of the reference raise ``NotImplementedError``.  The ``streaming``
+execution mode computes the same function as ``full``; both run the same kernels (the fused
+kernel is itself an online softmax over routes).
 """
 
 from __future__ import annotations
@@ -39,6 +42,55 @@ def _normal_init(weight: Tensor, std: float) -> None:
     tmp = torch.empty_like(weight, dtype=torch.float32)
     nn.init.normal_(tmp, mean=0.0, std=std)
     weight.copy_(tmp.to(weight.dtype))
+
+
+class _LngramSurrogate(torch.autograd.Function):
+    """Identity on the looked-up memory of one order; the backward passes the memory gradient
+    through and gives the route logits the surrogate gradient (``lngram_v2.py:328-464``),
+    approximate (one-bit counterfactual rows) or exact (alphabet expectation), on
+    ``lng_surrogate_grad``.  Same arguments as the reference's."""
+
+    @staticmethod
+    def forward(ctx, hard_memory: Tensor, q_logits: Tensor, route_codes: Tensor, table_weight: Tensor,
+                valid_mask: Tensor, order: int, bits: int, route_start: int, alphabet_size: int,
+                temperature: float, scale: float, exact: bool) -> Tensor:
+        if int(alphabet_size) != 1 << int(bits):
+            raise ValueError("alphabet_size must be 2**bits")
+        ctx.save_for_backward(q_logits, route_codes, table_weight, valid_mask, hard_memory.detach())
+        ctx.cfg = (int(order), int(bits), int(route_start), float(temperature), float(scale), bool(exact))
+        return hard_memory
+
+    @staticmethod
+    def backward(ctx, grad_memory: Optional[Tensor]):
+        if grad_memory is None:
+            return (None,) * 12
+        q_logits, codes, table, valid_mask, hard = ctx.saved_tensors
+        order, bits, route_start, temperature, scale, exact = ctx.cfg
+        grad_q = ops.surrogate_grad(grad_memory, hard, q_logits.detach(), codes, table.detach(), valid_mask, order,
+                                    bits, route_start, temperature, scale, exact)
+        return (grad_memory, grad_q) + (None,) * 10
+
+
+class _TableRows(torch.autograd.Function):
+    """One order's looked-up rows ``[B, T, R, D]`` (zero where masked; ``lng_route_tokens``) with
+    the gather's table gradient (``lng_table_grad``), the embedding backward of
+    ``lngram_v2.py:1084-1092``."""
+
+    @staticmethod
+    def forward(ctx, table: Tensor, route_codes: Tensor, codes_chunk: Tensor, valid_mask: Tensor, order: int,
+                bits: int, route_start: int, route_end: int, segment_ids: Optional[Tensor],
+                valid_tokens: Optional[Tensor]) -> Tensor:
+        ctx.save_for_backward(codes_chunk, valid_mask)
+        ctx.cfg = (int(order), int(bits), int(route_start), table.shape[0], table.dtype)
+        return ops.route_tokens(route_codes, [table.detach()], [int(order)], int(bits), int(route_start),
+                                int(route_end), segment_ids, valid_tokens, None)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        codes_chunk, valid_mask = ctx.saved_tensors
+        order, bits, route_start, rows, dtype = ctx.cfg
+        g = ops.table_grad(grad, codes_chunk, valid_mask, order, bits, route_start, rows)
+        return (g.to(dtype),) + (None,) * 9
 
 
 class RMSNorm(nn.Module):
@@ -295,7 +347,11 @@ class _RouteNgramMemoryBase(nn.Module):
 
     def _check_inference(self, q_logits: Optional[Tensor] = None) -> None:
         if self._use_surrogate(q_logits):
-            raise NotImplementedError("the surrogate route gradient (training) is not part of the MI355X path")
+            raise NotImplementedError("the readout has no backward kernels: in training mode only "
+                                      "_lookup_route_chunk (route rows + surrogate route gradient) runs on the GPU")
+        self._check_dropout()
+
+    def _check_dropout(self) -> None:
         if self.training and (self.lookup_dropout.p > 0 or self.readout_attention_dropout > 0):
             raise NotImplementedError("dropout in training mode is not part of the MI355X path")
 
@@ -317,8 +373,17 @@ class _RouteNgramMemoryBase(nn.Module):
                             route_end: int, segment_ids: Optional[Tensor], valid_tokens: Optional[Tensor],
                             target_length: Optional[int] = None) -> Tensor:
         """Route tokens ``[B, T, route_end-route_start, len(ngrams)*mem_dim]`` (``lngram_v2.py:1047-1113``):
-        ``lng_route_tokens`` gathers every order's row (zero where masked) in one pass."""
-        self._check_inference(q_logits_btrm)
+        ``lng_route_tokens`` gathers every order's row (zero where masked) in one pass.
+
+        In training with route logits under autograd, each order's rows come from ``_TableRows``
+        (table gradient on the backward) through ``_LngramSurrogate`` (route-logit gradient), as in
+        the reference (``:1093-1109``)."""
+        self._check_dropout()
+        if self._use_surrogate(q_logits_btrm):
+            if target_length is not None:
+                raise RuntimeError("cached inference cannot use surrogate gradients")
+            return self._lookup_with_surrogate(route_codes, q_logits_btrm, int(route_start), int(route_end),
+                                               segment_ids, valid_tokens)
         tables = [self.tables[f"ngram_{n}"].weight for n in self.ngrams]
         tl = None if target_length is None else int(target_length)
         if tl is not None and not 0 < tl <= route_codes.shape[1]:
@@ -328,6 +393,22 @@ class _RouteNgramMemoryBase(nn.Module):
             return full[:, -tl:]
         return ops.route_tokens(route_codes, tables, self.ngrams, self.bits_per_route, int(route_start),
                                 int(route_end), segment_ids, valid_tokens, tl)
+
+    def _lookup_with_surrogate(self, route_codes: Tensor, q_logits_btrm: Tensor, route_start: int, route_end: int,
+                               segment_ids: Optional[Tensor], valid_tokens: Optional[Tensor]) -> Tensor:
+        b, t, _ = route_codes.shape
+        codes = route_codes[:, :, route_start:route_end].contiguous()
+        q_chunk = q_logits_btrm[:, :, route_start:route_end, :]
+        parts = []
+        for order in self.ngrams:
+            valid = self._valid_mask(order, b, t, route_codes.device, segment_ids, valid_tokens)
+            table = self.tables[f"ngram_{order}"].weight
+            rows = _TableRows.apply(table, route_codes, codes, valid, order, self.bits_per_route, route_start,
+                                    route_end, segment_ids, valid_tokens)
+            parts.append(_LngramSurrogate.apply(rows, q_chunk, codes, table, valid, order, self.bits_per_route,
+                                                route_start, self.alphabet_size, self.q_surrogate_temperature,
+                                                self.q_surrogate_scale, self.q_surrogate_mode == "exact"))
+        return torch.cat(parts, dim=-1)
 
     # ------------------------------------------------------------------ projections
     def _project_query(self, hidden_states: Tensor) -> Tensor:

@@ -96,6 +96,9 @@ SIGNATURES = {
     "lng_memory_readout_pack": (_int, [_p, _p, _p]),
     "lng_gather_sum_scaled": (_int, [ctypes.POINTER(_p), _int, _i32, _p, _i64, _i64, _i32, _P32, _i32, _i32, _i32,
                                      ctypes.c_uint32, _p, _p]),
+    "lng_surrogate_grad": (_int, [_p, _p, _int, _p, _int, _p, _int, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32,
+                                  _i32, _i32, _f, _f, _int, _p, _int, _p]),
+    "lng_table_grad": (_int, [_p, _int, _p, _int, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i64, _p, _p]),
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, ctypes.c_uint32, _p, _p]),
     "lng_ssm_scan_static": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p]),

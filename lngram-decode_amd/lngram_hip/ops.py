@@ -603,6 +603,57 @@ def gather_sum_scaled(tables, codes: torch.Tensor, orders, bits: int, scale_log2
     return out
 
 
+def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor, q_logits: torch.Tensor,
+                   codes: torch.Tensor, table: torch.Tensor, valid_mask: torch.Tensor | None, order: int, bits: int,
+                   route_start: int, temperature: float, scale: float, exact: bool) -> torch.Tensor:
+    """Route-logit gradient ``[B, T, R, bits]`` (``q_logits``' dtype) of the lookup surrogate of one
+    order (``lng_surrogate_grad``; ``_LngramSurrogate.backward``, ``lngram_v2.py:364-464``)."""
+    dev = _dev(grad_memory, hard_memory, q_logits, codes, table, valid_mask)
+    b, t, r, md = hard_memory.shape
+    if tuple(grad_memory.shape) != (b, t, r, md) or tuple(q_logits.shape) != (b, t, r, bits) or \
+            tuple(codes.shape) != (b, t, r) or table.dim() != 2 or table.shape[1] != md:
+        raise ValueError("surrogate_grad: memory [B,T,R,D], q_logits [B,T,R,bits], codes [B,T,R], table [rows, D]")
+    mdt = table.dtype
+    if hard_memory.dtype != mdt:
+        raise ValueError(f"surrogate_grad: memory dtype {hard_memory.dtype} != table dtype {mdt}")
+    g = _c(grad_memory.to(mdt))
+    hm, tab, q, cc = _c(hard_memory), _c(table), _c(q_logits), _c(codes)
+    if cc.dtype not in (torch.uint8, torch.int32, torch.int64):
+        cc = _c(cc.to(torch.int64))
+    vm = None if valid_mask is None else _c(valid_mask.to(torch.uint8))
+    if vm is not None and tuple(vm.shape) != (b, t):
+        raise ValueError("surrogate_grad: valid_mask must be [B, T]")
+    out = torch.empty(b, t, r, bits, dtype=q.dtype, device=dev)
+    rc = _timed("surrogate_grad", dev, lambda: lib().lng_surrogate_grad(
+        _ptr(g), _ptr(hm), dtype_code(mdt), _ptr(q), dtype_code(q.dtype), _ptr(cc), dtype_code(cc.dtype), _ptr(tab),
+        tab.shape[0], _ptr(vm), b, t, r, int(route_start), md, int(order), int(bits), float(temperature),
+        float(scale), int(bool(exact)), _ptr(out), dtype_code(out.dtype), _stream(dev)))
+    check(rc, "surrogate_grad")
+    return out
+
+
+def table_grad(grad_memory: torch.Tensor, codes: torch.Tensor, valid_mask: torch.Tensor | None, order: int,
+               bits: int, route_start: int, table_rows: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 ``[table_rows, D]`` table gradient of one order's lookup (``lng_table_grad``): the
+    embedding backward of ``_lookup_route_chunk``'s gather; adds into ``out`` when given."""
+    dev = _dev(grad_memory, codes, valid_mask, out)
+    b, t, r, md = grad_memory.shape
+    if tuple(codes.shape) != (b, t, r):
+        raise ValueError("table_grad: codes must be [B, T, R]")
+    g = _c(grad_memory if grad_memory.dtype in (torch.float32, torch.bfloat16) else grad_memory.float())
+    cc = _c(codes if codes.dtype in (torch.uint8, torch.int32, torch.int64) else codes.to(torch.int64))
+    vm = None if valid_mask is None else _c(valid_mask.to(torch.uint8))
+    if out is None:
+        out = torch.zeros(int(table_rows), md, dtype=torch.float32, device=dev)
+    elif out.dtype != torch.float32 or tuple(out.shape) != (int(table_rows), md) or not out.is_contiguous():
+        raise ValueError("table_grad: out must be a contiguous fp32 [table_rows, D]")
+    rc = _timed("table_grad", dev, lambda: lib().lng_table_grad(
+        _ptr(g), dtype_code(g.dtype), _ptr(cc), dtype_code(cc.dtype), _ptr(vm), b, t, r, int(route_start), md,
+        int(order), int(bits), int(table_rows), _ptr(out), _stream(dev)))
+    check(rc, "table_grad")
+    return out
+
+
 # ----------------------------------------------------------------------------- K4
 _ssm_ws: dict = {}
 _ssm_ws_lock = threading.Lock()

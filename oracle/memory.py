@@ -427,6 +427,97 @@ def ssm_scan_closed_form_constant(a, u_const, t: int, s0=None) -> np.ndarray:
     return u[None] + (a[None] ** k) * (s0 - u)[None]
 
 
+# ----------------------------------------------------------------------------- lookup surrogate (training)
+def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor, q_logits: torch.Tensor, codes, table,
+                   valid, order: int, bits: int, route_start: int, temperature: float, scale: float, exact: bool,
+                   work=torch.float64) -> torch.Tensor:
+    """Route-logit gradient of ``_LngramSurrogate.backward`` (``lngram_v2.py:364-464``) for one order.
+
+    Window ``w = 0 .. T-order`` ends at position ``w + order - 1`` and reads row ``idx_w``
+    (``route_rows``); its masked memory gradient is ``g_w`` and its looked-up row ``m_w``.
+    Digit ``e`` of the window is the code at position ``w + e``, so that position collects:
+
+    - approximate (``:430-447``): per bit k, ``sign * (table[idx_w ^ 2^(e*bits+k)] . g_w - m_w . g_w)``
+      (sign +1 when the bit is 0), the total scaled by ``scale * T * p (1-p)``;
+    - exact (``:394-429``): ``scale * T * sum_code P(code) (bit_k(code) - p_k) (table[row_w(e <- code)] . g_w)``
+      with ``P`` the product of the position's bit probabilities, ``p = sigmoid(T q)``.
+
+    ``valid`` is ``_valid_mask`` ``[B, T]``.  Returns ``[B, T, R, bits]`` in ``work``.
+    """
+    b, t, r, nb = q_logits.shape
+    A = 1 << bits
+    n_win = t - order + 1
+    out = torch.zeros(b, t, r, nb, dtype=work)
+    if n_win <= 0 or temperature == 0.0 or scale == 0.0:
+        return out
+    c = np.asarray(codes).astype(np.int64)
+    base = np.arange(route_start, route_start + r, dtype=np.int64)[None, None, :] * A ** order
+    idx = base + ngram_address(c, order, bits)                                  # [B, n_win, R]
+    keep = torch.as_tensor(np.asarray(valid, bool)[:, order - 1:]).to(work)
+    g = grad_memory[:, order - 1:].to(work) * keep[..., None, None]
+    tab = table.to(work)
+    p = torch.sigmoid(temperature * q_logits.to(work))
+    ts = scale * temperature
+
+    def dots(rows: np.ndarray) -> torch.Tensor:
+        return (tab[torch.from_numpy(rows)] * g).sum(-1)                       # [B, n_win, R]
+
+    for e in range(order):
+        at = slice(e, e + n_win)                                               # positions w + e
+        if exact:
+            digit = c[:, e:e + n_win] & (A - 1)
+            pe = p[:, at]
+            for code in range(A):
+                d = dots(idx + (code - digit) * A ** e)
+                bit = torch.tensor([(code >> k) & 1 for k in range(nb)], dtype=work)
+                prob = torch.where(bit.bool(), pe, 1.0 - pe).prod(-1)
+                out[:, at] += ts * prob[..., None] * (bit - pe) * d[..., None]
+        else:
+            here = (hard_memory[:, order - 1:].to(work) * g).sum(-1)
+            for k in range(nb):
+                flip = 1 << (e * bits + k)
+                sign = torch.from_numpy(1.0 - 2.0 * ((idx & flip) != 0)).to(work)
+                out[:, at, :, k] += (dots(idx ^ flip) - here) * sign
+    if not exact:
+        out *= ts * p * (1.0 - p)
+    return out
+
+
+def surrogate_expected_dot(q_logits: torch.Tensor, codes, table, grad_memory: torch.Tensor, valid, order: int,
+                           bits: int, route_start: int, temperature: float, scale: float) -> torch.Tensor:
+    """The objective whose exact derivative the exact surrogate mode is, computed by brute force
+    in fp64 (a check, not a restatement): ``scale * sum over windows w, digits e and codes c of
+    P(c | sigmoid(T q[w+e])) * (table[row of w with digit e replaced by c] . g_w)``, the other
+    digits held at their codes.  Differentiating it in ``q`` gives ``_LngramSurrogate``'s exact mode
+    (``lngram_v2.py:394-429``)."""
+    b, t, r, nb = q_logits.shape
+    A = 1 << bits
+    c = np.asarray(codes).astype(np.int64)
+    tab = table.double()
+    p = torch.sigmoid(temperature * q_logits.double())
+    total = torch.zeros((), dtype=torch.float64)
+    vm = np.asarray(valid, bool)
+    for bi in range(b):
+        for w in range(t - order + 1):
+            end = w + order - 1
+            if not vm[bi, end]:
+                continue
+            for ri in range(r):
+                g = grad_memory[bi, end, ri].double()
+                digits = [int(c[bi, w + k, ri]) for k in range(order)]
+                for e in range(order):
+                    pe = p[bi, w + e, ri]
+                    for code in range(A):
+                        dg = list(digits)
+                        dg[e] = code
+                        row = (route_start + ri) * A ** order + sum(v << (k * bits) for k, v in enumerate(dg))
+                        prob = torch.ones((), dtype=torch.float64)
+                        for k in range(nb):
+                            prob = prob * (pe[k] if (code >> k) & 1 else 1.0 - pe[k])
+                        total = total + prob * (tab[row] @ g)
+    return scale * total
+
+
 # ----------------------------------------------------------------------------- comparison metric
 def rel_err(got, want) -> float:
     """Norm-relative error ``||got - want|| / ||want||`` in fp64."""

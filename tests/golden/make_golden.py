@@ -13,6 +13,8 @@ from them, plus the torch version that computed it.  Fixtures:
 - ``memory_tiny_fp32.npz``: ``LngramMemory.forward`` (``wrapper.py:103-125``) at the C1 widths;
 - ``memory_sb_bf16.npz``: the same module cast to bf16 at the SB widths (32 routes), so the
   reference's bf16 rounding sequence (``lngram_v2.py:1361-1407``) is recorded;
+- ``surrogate.npz``: the route-logit and memory gradients of ``_LngramSurrogate``
+  (``lngram_v2.py:328-464``), approximate and exact, for the cases of ``recipe.SURROGATE_CASES``;
 - ``drafter_<kind>[_sketch].npz``: ``RefDrafter.trace`` (full vocabulary and shortlist) and
   ``RefDrafter.draft`` after a commit, with and without hypothetical tokens
   (``cpu_drafter.py:247-289``) on tiny SD-B / SD-C bundles, with and without count sketches.
@@ -146,18 +148,44 @@ def drafter(out: Path) -> None:
             np.savez_compressed(out / f"{name}.npz", **res)
 
 
+def surrogate(out: Path) -> None:
+    from ffnmem.memory.lngram_v2 import _LngramSurrogate, _aligned_ngram_address
+
+    res = {"torch": np.array(torch.__version__)}
+    for case in recipe.SURROGATE_CASES:
+        name, order, bits, R, rs, B, T, D, dt_name, temp, scale, exact = case
+        dt = torch.bfloat16 if dt_name == "bf16" else torch.float32
+        x = recipe.surrogate_inputs(case)
+        table = torch.from_numpy(x["table"]).to(dt)
+        codes = torch.from_numpy(x["codes"])
+        valid = torch.zeros(B, T, dtype=torch.bool)               # _valid_mask with valid_tokens
+        valid[:, order - 1:] = torch.from_numpy(x["valid_tokens"])[:, order - 1:]
+        A = 1 << bits
+        addr = _aligned_ngram_address(codes, order, bits)
+        rows = (torch.arange(rs, rs + R) * A ** order).view(1, 1, R) + addr
+        hard = torch.cat((table.new_zeros(B, order - 1, R, D), table[rows]), 1) * valid[..., None, None].to(dt)
+        q = torch.from_numpy(x["q"]).requires_grad_()
+        mem = hard.clone().requires_grad_()
+        y = _LngramSurrogate.apply(mem, q, codes, table, valid, order, bits, rs, A, temp, scale, exact)
+        y.backward(torch.from_numpy(x["grad"]).to(dt))
+        res[f"{name}_grad_q"] = q.grad.numpy()
+        res[f"{name}_grad_mem"] = (_bits if dt == torch.bfloat16 else (lambda v: v.numpy()))(mem.grad)
+    np.savez_compressed(out / "surrogate.npz", **res)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", required=True, help="the reference checkout")
     ap.add_argument("--out", default=str(HERE))
+    ap.add_argument("--only", nargs="*", help="fixture groups to write (default: all)")
     args = ap.parse_args()
     sys.path.insert(0, str(Path(args.ref).resolve()))
     torch.manual_seed(0)
     out = Path(args.out)
-    router_features(out)
-    ssm(out)
-    memory(out)
-    drafter(out)
+    groups = {"router_features": router_features, "ssm": ssm, "memory": memory, "drafter": drafter,
+              "surrogate": surrogate}
+    for name in args.only or groups:
+        groups[name](out)
     for p in sorted(out.glob("*.npz")):
         print(p.name, p.stat().st_size)
 

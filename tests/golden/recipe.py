@@ -112,3 +112,31 @@ def drafter_arrays(cfg: dict, base: int = 0) -> dict:
             out[f"sketch_counts_{n}"] = cnt.astype(np.uint32)   # count 0 = empty slot
         out["fallback"] = integers("fallback", (12,), 0, V, base).astype(np.int32)
     return out
+
+
+# ------------------------------------------------------------------ lookup surrogate (training)
+# (name, order, bits, routes, route_start, batch, time, mem_dim, dtype, temperature, scale, exact)
+SURROGATE_CASES = [
+    ("sg_o2_f32_approx", 2, 4, 3, 1, 2, 7, 32, "f32", 0.7, 1.3, False),
+    ("sg_o2_f32_exact", 2, 4, 3, 1, 2, 7, 32, "f32", 0.7, 1.3, True),
+    ("sg_o3_bf16_approx", 3, 4, 2, 0, 2, 9, 32, "bf16", 1.0, 1.0, False),
+    ("sg_o3_bf16_exact", 3, 4, 2, 0, 2, 9, 32, "bf16", 1.0, 1.0, True),
+    ("sg_o3_b2_f32_approx", 3, 2, 4, 2, 1, 11, 64, "f32", 1.5, 0.5, False),
+    ("sg_o3_b2_f32_exact", 3, 2, 4, 2, 1, 11, 64, "f32", 1.5, 0.5, True),
+]
+
+
+def surrogate_inputs(case) -> dict:
+    """Inputs of one surrogate case: the order's table (rows for routes 0 .. route_start + R - 1),
+    codes of the R routes, route logits, the memory gradient and the valid tokens (one position of
+    the first sequence invalid).  All fp32 / int64; the case's dtype is applied by the user."""
+    name, order, bits, R, rs, B, T, D = case[:8]
+    A = 1 << bits
+    rows = (rs + R) * A ** order
+    valid = np.ones((B, T), dtype=bool)
+    valid[0, min(T - 1, order + 1)] = False
+    return {"table": normal(f"{name}_table", (rows, D)),
+            "codes": integers(f"{name}_codes", (B, T, R), 0, A),
+            "q": normal(f"{name}_q", (B, T, R, bits)),
+            "grad": normal(f"{name}_grad", (B, T, R, D)),
+            "valid_tokens": valid}

@@ -1,0 +1,218 @@
+"""The lookup surrogate's backward on the GPU (``lng_surrogate_grad``, ``lng_table_grad`` and the
+mirror's ``_LngramSurrogate`` / training-mode ``_lookup_route_chunk``; reference
+``lngram_v2.py:328-464``, ``:1047-1113``).
+
+- The reference's own gradients (``tests/golden/surrogate.npz``): norm-relative < 1e-5.
+- The fp64 oracle at larger shapes (mem_dim 32..256, orders 1..3, 1..4-bit codes, fp32 and bf16
+  tables, bf16 logits and gradient outputs): < 1e-5 (bf16 outputs: the bf16 rounding).
+- At the full SB shape (8 x 2048 tokens, 184 routes, mem_dim 128, bf16, orders 2 and 3), a table
+  linear in the address bits with small-integer entries and gradients: every dot product is
+  exact in fp32, so the kernel must equal the closed form up to the fp32 slope (< 1e-6).
+- The table gradient against an fp64 scatter, and the training-mode lookup end to end.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from lngram_hip import ops
+from oracle import memory as om
+
+GOLD = Path(__file__).resolve().parent / "golden"
+sys.path.insert(0, str(GOLD))
+import recipe  # noqa: E402
+from .test_oracle_surrogate import case_inputs  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+def _gold() -> dict:
+    with np.load(GOLD / "surrogate.npz", allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+@pytest.mark.parametrize("case", recipe.SURROGATE_CASES, ids=[c[0] for c in recipe.SURROGATE_CASES])
+def test_kernel_matches_reference_gradients(dev, case):
+    name, order, bits, R, rs, B, T, D, dt_name, temp, scale, exact = case
+    x = case_inputs(case)
+    g = _gold()
+    got = ops.surrogate_grad(x["grad"].to(dev), x["hard"].to(dev), x["q"].to(dev),
+                             torch.from_numpy(x["codes"]).to(dev), x["table"].to(dev),
+                             torch.from_numpy(x["valid"]).to(dev), order, bits, rs, temp, scale, exact)
+    assert got.dtype == torch.float32 and got.shape == (B, T, R, bits)
+    want = torch.from_numpy(g[f"{name}_grad_q"])
+    assert om.rel_err(got.cpu(), want) < 1e-5
+    ora = om.surrogate_grad(x["grad"], x["hard"], x["q"], x["codes"], x["table"], x["valid"], order, bits, rs, temp,
+                            scale, exact)
+    assert om.rel_err(got.cpu(), ora) < 1e-5
+
+
+def _random_case(seed, B, T, R, rs, D, order, bits, dtype, q_dtype=torch.float32, invalid=True):
+    gen = torch.Generator().manual_seed(seed)
+    A = 1 << bits
+    table = (torch.randn((rs + R) * A ** order, D, generator=gen) * 0.5).to(dtype)
+    codes = torch.randint(0, A, (B, T, R), generator=gen)
+    q = torch.randn(B, T, R, bits, generator=gen).to(q_dtype)
+    grad = torch.randn(B, T, R, D, generator=gen).to(dtype)
+    vt = np.ones((B, T), bool)
+    if invalid and T > order + 2:
+        vt[B - 1, order + 1] = False
+    valid = om.valid_mask(order, B, T, valid_tokens=vt)
+    rows = om.route_rows(codes.numpy(), [order], bits, 0, R, valid_tokens=vt)[..., 0]
+    rows = np.where(rows >= 0, rows + rs * A ** order, -1)
+    hard = table[torch.from_numpy(rows).clamp_min(0)] * torch.from_numpy(rows >= 0)[..., None].to(dtype)
+    return dict(table=table, codes=codes, q=q, grad=grad, valid=valid, hard=hard)
+
+
+@pytest.mark.parametrize("D,order,bits,dtype", [(128, 3, 4, torch.bfloat16), (128, 2, 4, torch.bfloat16),
+                                                (256, 2, 3, torch.float32), (64, 1, 4, torch.float32),
+                                                (32, 3, 2, torch.bfloat16)])
+@pytest.mark.parametrize("exact", [False, True])
+def test_kernel_matches_oracle(dev, D, order, bits, dtype, exact):
+    B, T, R, rs = 2, 37, 6, 3
+    x = _random_case(D + order + bits, B, T, R, rs, D, order, bits, dtype)
+    temp, scale = 0.9, 1.1
+    got = ops.surrogate_grad(x["grad"].to(dev), x["hard"].to(dev), x["q"].to(dev), x["codes"].to(dev),
+                             x["table"].to(dev), torch.from_numpy(x["valid"]).to(dev), order, bits, rs, temp, scale,
+                             exact)
+    want = om.surrogate_grad(x["grad"], x["hard"], x["q"], x["codes"].numpy(), x["table"], x["valid"], order, bits,
+                             rs, temp, scale, exact)
+    assert want.abs().max() > 0
+    assert om.rel_err(got.cpu(), want) < 1e-5
+
+
+def test_bf16_logits_give_bf16_gradient_and_codes_any_int_dtype(dev):
+    B, T, R, rs, D, order, bits = 1, 20, 4, 0, 128, 3, 4
+    x = _random_case(5, B, T, R, rs, D, order, bits, torch.bfloat16, q_dtype=torch.bfloat16)
+    want = om.surrogate_grad(x["grad"], x["hard"], x["q"], x["codes"].numpy(), x["table"], x["valid"], order, bits,
+                             rs, 1.0, 1.0, False)
+    outs = []
+    for cdt in (torch.uint8, torch.int32, torch.int64):
+        got = ops.surrogate_grad(x["grad"].to(dev), x["hard"].to(dev), x["q"].to(dev), x["codes"].to(cdt).to(dev),
+                                 x["table"].to(dev), torch.from_numpy(x["valid"]).to(dev), order, bits, rs, 1.0, 1.0,
+                                 False)
+        assert got.dtype == torch.bfloat16
+        outs.append(got)
+        assert om.rel_err(got.float().cpu(), want) < 5e-3
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+
+
+def test_degenerate_and_errors(dev):
+    x = _random_case(9, 1, 2, 2, 0, 32, 3, 4, torch.float32)
+    args = [x["grad"].to(dev), x["hard"].to(dev), x["q"].to(dev), x["codes"].to(dev), x["table"].to(dev),
+            torch.from_numpy(x["valid"]).to(dev)]
+    assert ops.surrogate_grad(*args, 3, 4, 0, 1.0, 1.0, False).abs().max().item() == 0   # T < order
+    y = _random_case(9, 1, 9, 2, 0, 32, 2, 4, torch.float32)
+    args = [y["grad"].to(dev), y["hard"].to(dev), y["q"].to(dev), y["codes"].to(dev), y["table"].to(dev),
+            torch.from_numpy(y["valid"]).to(dev)]
+    assert ops.surrogate_grad(*args, 2, 4, 0, 0.0, 1.0, False).abs().max().item() == 0
+    assert ops.surrogate_grad(*args, 2, 4, 0, 1.0, 0.0, True).abs().max().item() == 0
+    with pytest.raises(RuntimeError, match="fewer rows"):
+        ops.surrogate_grad(*args, 2, 4, 1, 1.0, 1.0, False)              # routes 1..2 need 3 route blocks
+    z = _random_case(9, 1, 9, 2, 0, 48, 2, 4, torch.float32)
+    with pytest.raises(RuntimeError, match="mem_dim"):
+        ops.surrogate_grad(z["grad"].to(dev), z["hard"].to(dev), z["q"].to(dev), z["codes"].to(dev),
+                           z["table"].to(dev), None, 2, 4, 0, 1.0, 1.0, False)
+
+
+def _linear_table(gen, R, order, bits, D, dev):
+    """Rows w0[r] + sum_j bit_j(addr) v[r, j] with small integers: exact in bf16."""
+    nbit = order * bits
+    w0 = torch.randint(-3, 4, (R, D), generator=gen).float()
+    v = torch.randint(-2, 3, (R, nbit, D), generator=gen).float()
+    addr = torch.arange(1 << nbit)
+    ab = ((addr[:, None] >> torch.arange(nbit)) & 1).float()
+    table = (w0[:, None, :] + torch.einsum("aj,rjd->rad", ab, v)).reshape(-1, D)
+    return table.to(torch.bfloat16).to(dev), v.to(dev)
+
+
+def test_sb_shape_linear_table_closed_form(dev):
+    """Full SB shape: both orders' gradients against the closed form
+    G[t, k] = scale * T * p(1-p) * sum_e v[r, e*bits + k] . g[window t - e]."""
+    B, T, R, D, bits = 8, 2048, 184, 128, 4
+    gen = torch.Generator().manual_seed(2024)
+    codes = torch.randint(0, 16, (B, T, R), generator=gen, dtype=torch.uint8).to(dev)
+    q = torch.randn(B, T, R, bits, generator=gen).to(dev)
+    temp, scale = 1.0, 1.0
+    p = torch.sigmoid(temp * q.double())
+    for order in (2, 3):
+        table, v = _linear_table(gen, R, order, bits, D, dev)
+        grad = torch.randint(-2, 3, (B, T, R, D), generator=gen, dtype=torch.int8).to(dev).to(torch.bfloat16)
+        valid = torch.ones(B, T, dtype=torch.bool, device=dev)
+        valid[:, :order - 1] = False
+        hard = ops.route_tokens(codes, [table], [order], bits)
+        print(f"surrogate SB order {order}", flush=True)
+        got = ops.surrogate_grad(grad, hard, q, codes, table, valid, order, bits, 0, temp, scale, False)
+        torch.cuda.synchronize()
+        # closed form: window w (ending at w + order - 1) contributes v[r, e*bits+k] . g_w to position w + e
+        gw = grad[:, order - 1:].double()                                 # [B, VL, R, D]
+        vl = T - order + 1
+        want = torch.zeros(B, T, R, bits, dtype=torch.float64, device=dev)
+        for e in range(order):
+            for k in range(bits):
+                want[:, e:e + vl, :, k] += (gw * v[:, e * bits + k].double()[None, None]).sum(-1)
+        want *= scale * temp * p * (1 - p)
+        assert om.rel_err(got.cpu(), want.cpu()) < 1e-6, order
+        del hard, grad, table, got, want
+
+
+def test_table_grad_matches_scatter(dev):
+    B, T, R, rs, D, order, bits = 2, 30, 5, 1, 64, 3, 2
+    x = _random_case(17, B, T, R, rs, D, order, bits, torch.float32)
+    rows_n = x["table"].shape[0]
+    got = ops.table_grad(x["grad"].to(dev), x["codes"].to(dev), torch.from_numpy(x["valid"]).to(dev), order, bits,
+                         rs, rows_n)
+    rows = om.route_rows(x["codes"].numpy(), [order], bits, 0, R)[..., 0]
+    rows = np.where(rows >= 0, rows + rs * (1 << (bits * order)), -1)
+    keep = (rows >= 0) & x["valid"][..., None]
+    want = torch.zeros(rows_n, D, dtype=torch.float64)
+    want.index_add_(0, torch.from_numpy(rows[keep]), x["grad"].double()[torch.from_numpy(keep)])
+    assert om.rel_err(got.cpu(), want) < 1e-6
+
+
+def test_training_lookup_gradients(dev):
+    """Training-mode _lookup_route_chunk: route tokens equal the eval lookup; the route logits get
+    the sum over orders of the surrogate gradient and the tables the gather gradient."""
+    from ffnmem.memory.lngram_v2 import RouteNgramMemoryV2
+
+    torch.manual_seed(0)
+    m = RouteNgramMemoryV2(64, bits_per_route=4, num_routes=6, memory_dim=32, ngrams=(2, 3), readout_head_dim=16,
+                           readout_num_heads=4, readout_num_kv_heads=2, device=dev, dtype=torch.float32)
+    m.q_surrogate_temperature, m.q_surrogate_scale = 0.8, 1.2
+    b, t, R = 2, 11, 6
+    gen = torch.Generator().manual_seed(1)
+    with torch.no_grad():
+        for tab in m.tables.values():                   # the default init is zero tables
+            tab.weight.copy_(torch.randn(tab.weight.shape, generator=gen))
+    q = torch.randn(b, t, R, 4, generator=gen).to(dev).requires_grad_()
+    codes = m.quantize_route_logits(q.detach().reshape(b, t, R * 4))
+    vt = torch.ones(b, t, dtype=torch.bool, device=dev)
+    vt[1, 5] = False
+    with torch.no_grad():
+        m.eval()
+        ref_tokens = m._lookup_route_chunk(codes, None, 0, R, None, vt)
+    m.train()
+    tokens = m._lookup_route_chunk(codes, q, 0, R, None, vt)
+    assert torch.equal(tokens.detach(), ref_tokens)
+    w = torch.randn(tokens.shape, generator=gen).to(dev)
+    (tokens * w).sum().backward()
+    want_q = torch.zeros(b, t, R, 4, dtype=torch.float64)
+    for i, n in enumerate(m.ngrams):
+        tab = m.tables[f"ngram_{n}"].weight.detach().cpu()
+        valid = om.valid_mask(n, b, t, valid_tokens=vt.cpu().numpy())
+        g_n = w[..., i * 32:(i + 1) * 32].cpu()
+        want_q += om.surrogate_grad(g_n, ref_tokens[..., i * 32:(i + 1) * 32].cpu(), q.detach().cpu(),
+                                    codes.cpu().numpy(), tab, valid, n, 4, 0, 0.8, 1.2, False)
+        rows = om.route_rows(codes.cpu().numpy(), [n], 4, 0, R, valid_tokens=vt.cpu().numpy())[..., 0]
+        keep = rows >= 0
+        want_t = torch.zeros(tab.shape, dtype=torch.float64)
+        want_t.index_add_(0, torch.from_numpy(rows[keep]), g_n.double()[torch.from_numpy(keep)])
+        assert om.rel_err(m.tables[f"ngram_{n}"].weight.grad.cpu(), want_t) < 1e-6
+    assert om.rel_err(q.grad.cpu(), want_q) < 1e-5
+    with pytest.raises(NotImplementedError, match="backward"):
+        m(torch.randn(b, t, 64, device=dev), codes, q_logits=q.reshape(b, t, R * 4))
