@@ -403,6 +403,99 @@ def decode_step(dev, iters: int, warmup: int):
     return run
 
 
+def serving_step(dev, iters: int, warmup: int):
+    """Set up, and return the timing run of, decoding from host RAM at the SB shape: 8 sequences with
+    2048 cached positions each take one new token, the rows coming from a serving-layout copy of the
+    tables in pinned host memory that the GPU reads directly: B1 (the step's exact rows) and B4 (the
+    step's rows selected from candidate blocks prefetched by the previous step), against B0 (tables in
+    HBM).  Also the serving permutation of the 205 MB table (HBM-bound) and the host-link rate of the
+    candidate reads beside a plain pinned host-to-device copy."""
+    import numpy as np
+    import torch
+
+    from ffnmem.infer import DecodeState, memory_decode, memory_model
+    from lngram_hip import ops, workloads
+    from serving.prefetch import CandidatePrefetcher, HostGather, HostTables
+
+    w = workloads.SB
+    ctx = 2048
+    mem = workloads.build_memory(w, seed=0, device=dev)
+    model = memory_model(mem)
+    h = workloads.make_hidden(w.with_shape(w.batch, ctx + 1), seed=1, device=dev)
+    h_norm = ops.rmsnorm(h, torch.ones(w.d_model, dtype=w.dtype, device=dev), w.norm_eps)
+    st = DecodeState.empty(model, w.batch, ctx + warmup + iters + 1)
+    with torch.no_grad():
+        memory_decode(model, 0, st, h[:, :ctx], h_norm=h_norm[:, :ctx])
+    st.length = ctx
+    h1, hn1 = h[:, ctx:ctx + 1].contiguous(), h_norm[:, ctx:ctx + 1].contiguous()
+    host = HostTables.from_model(model)
+    lt = host[0]
+    m = mem.module
+    t3 = m.tables["ngram_3"].weight.detach()
+
+    def run() -> dict:
+        out = {}
+        b1, b4 = HostGather(host, dev), CandidatePrefetcher(host, dev)
+        with torch.no_grad():
+            for name, prov in (("b0", None), ("b1", b1), ("b4", b4)):
+                # a run of single-token steps from position 2048 on (each mode rewinds the state)
+                st.length = ctx
+                times = []
+                for i in range(warmup + iters):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    memory_decode(model, 0, st, h1, h_norm=hn1, row_provider=prov)
+                    torch.cuda.synchronize()
+                    st.length += 1
+                    if i >= warmup:
+                        times.append((time.perf_counter() - t0) * 1e6)
+                out[f"{name}_median_us"] = float(np.median(times))
+            out["b4_hit_rate"] = b4.stats.summary()["hit_rate"]
+            # serving permutation of the 3-gram table (193 MB read + written), HBM-bound
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            dst = torch.empty_like(t3)
+            ops.permute_table(t3, m.num_routes, 3, 4, dst)
+            e0.record()
+            for _ in range(5):
+                ops.permute_table(t3, m.num_routes, 3, 4, dst)
+            e1.record()
+            torch.cuda.synchronize()
+            perm_ms = e0.elapsed_time(e1) / 5
+            perm_bytes = 2 * t3.numel() * t3.element_size()
+            # host link: candidate blocks of 8 sequences read from host RAM by the GPU, beside a pinned copy
+            hist = st.codes[0][:, ctx - 2:ctx].contiguous()
+            cand = lt.candidates(hist, ctx)
+            e0.record()
+            for _ in range(10):
+                lt.candidates(hist, ctx, cand)
+            e1.record()
+            torch.cuda.synchronize()
+            cand_ms = e0.elapsed_time(e1) / 10
+            src = torch.empty(64 << 20, dtype=torch.uint8, pin_memory=True)
+            dst8 = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+            dst8.copy_(src, non_blocking=True)
+            e0.record()
+            for _ in range(10):
+                dst8.copy_(src, non_blocking=True)
+            e1.record()
+            torch.cuda.synchronize()
+            h2d_gbs = 10 * src.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        b4.close()
+        cand_bytes = cand.numel() * cand.element_size()
+        del dst, dst8, src, cand
+        return {"workload": f"SB-shape memory layer decode from host RAM: {w.batch} sequences x 1 new token after {ctx} "
+                            "cached positions; tables (205 MB, serving layout) in pinned host memory read by the GPU",
+                "unit": "us per step", "iters": iters, **out,
+                "permute_table": {"kernel": "k_permute_table", "table": "3-gram, 193 MB", "avg_ms": perm_ms,
+                                  "achieved_GBs": perm_bytes / (perm_ms * 1e-3) / 1e9,
+                                  "hbm_frac": perm_bytes / (perm_ms * 1e-3) / 1e9 / HBM_PEAK_GBS},
+                "candidate_read": {"kernel": "k_serving_candidates", "bytes": cand_bytes, "avg_us": cand_ms * 1e3,
+                                   "host_link_GBs": cand_bytes / (cand_ms * 1e-3) / 1e9,
+                                   "pinned_h2d_copy_GBs": h2d_gbs}}
+
+    return run
+
+
 def sdc_forward(dev, steps: int, warmup: int):
     """Set up, and return the timing run of, the SD-C layer: 8 x 4096 tokens, 181 routes; one step =
     diagonal SSM scan of u [8, 4096, 256] fp32 (decays U[0.9, 0.999]) + router features concat(RMSNorm(E[x_{t-1}]), RMSNorm(E[x_t]), s_t) from
@@ -663,6 +756,9 @@ def main() -> None:
     if not args.no_draft:
         log("cached decode step: set-up")
         legs["decode_step"] = decode_step(dev, args.draft_iters, 20)
+    if not args.no_draft:
+        log("host-RAM serving step: set-up")
+        legs["serving_step"] = serving_step(dev, args.draft_iters // 2, 10)
     if not args.no_train:
         log("surrogate backward: set-up")
         legs["surrogate_backward"] = surrogate_backward(dev, max(3, args.steps // 4), 2)

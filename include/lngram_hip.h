@@ -233,6 +233,16 @@ int lng_memory_readout_fused_at(const void* q, const void* q_rows, float q_eps, 
                                 const void* table2, const void* table3, const void* kv_pack, const void* w_mem,
                                 float eps, float scale, float sink_logit, void* head_out, void* stream);
 
+/* The fused readout over route tokens the caller supplies instead of codes and tables
+ * (memory_step with route_tokens, ffnmem/infer.py:167-171: rows from host-RAM serving or staged
+ * verify blocks).  route_tokens [B*n, R, 256] bf16 (the 2-gram row, then the 3-gram row; zeros
+ * where the lookup masks, as _lookup_route_chunk gives them); q / q_rows / head_out as in
+ * lng_memory_readout_fused.  Same arithmetic as the code path, so equal rows give equal outputs.
+ * B * n * R < 2^23. */
+int lng_memory_readout_fused_rows(const void* q, const void* q_rows, float q_eps, const void* route_tokens, int64_t B,
+                                  int64_t n, int32_t R, const void* kv_pack, const void* w_mem, float eps, float scale,
+                                  float sink_logit, void* head_out, void* stream);
+
 /* out[N, K] = w[N, K] * s[K] (bf16, one rounding): a row RMSNorm's weight folded into the projection
  * that follows it (readout_query_norm.weight into readout_q_proj.weight, lngram_v2.py:1115-1118). */
 int lng_fold_columns(const void* w, const void* s, int64_t N, int64_t K, void* out, void* stream);
@@ -283,6 +293,54 @@ int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem
 int lng_table_grad(const void* grad_memory, int mem_dtype, const void* codes, int codes_dtype,
                    const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start, int32_t mem_dim,
                    int32_t order, int32_t bits, int64_t table_rows, float* table_grad, void* stream);
+
+/* ---------------------------------------------------------------- serving layout and host-RAM rows */
+/* Device address of pinned host memory (hipHostGetDevicePointer): the serving movers below read
+ * host-RAM tables through it (zero-copy over the host link).  LNG_E_HIP for memory that is not
+ * pinned and mapped.  No reference counterpart: the reference stages rows through host copies
+ * (serving/prefetch.py:1-45, its transfer mode (ii) ZeroCopyGather is not implemented, :600-608). */
+int lng_host_device_pointer(const void* host_ptr, void** dev_ptr);
+
+/* Serving layout of one order's table (permute_table, serving/layout.py:38-43): dst row
+ * (r, j) = src row (r, rev(j)), rev reversing the `order` base-2^bits digits of j.  An involution:
+ * the same call maps back (restore_tables, prefetch.py:253-260).  [routes * 2^(bits*order),
+ * mem_dim] in dtype (f32, bf16, f16; rows a multiple of 16 bytes); src and dst distinct. */
+int lng_permute_table(const void* src, void* dst, int dtype, int32_t routes, int32_t order, int32_t bits,
+                      int32_t mem_dim, void* stream);
+
+/* out[B, T-order+1, R] int64 = sum_m codes[b, t'+order-1-m, r] << (m*bits): the address with the
+ * current code least significant (serving_address, serving/layout.py:52-63). */
+int lng_serving_address(const void* codes, int codes_dtype, int64_t B, int64_t T, int32_t R, int32_t order,
+                        int32_t bits, int64_t* out, void* stream);
+
+/* Exact route tokens of n new positions from serving-layout tables (LayerTable.exact_index +
+ * gather, serving/prefetch.py:184-199, :226-233; serving_route_tokens, layout.py:66-81):
+ * tables[k] = order orders[k]'s serving table (device or mapped host memory, table_rows[k] rows);
+ * ctx [B, h + n, R] = h history codes, then the n new positions' codes, the first new position being
+ * absolute position `start` (h <= start).  out [B, n, R, n_orders * mem_dim] in table_dtype,
+ * zeros where the n-gram does not fit (position < order - 1). */
+int lng_serving_gather(const void* const* tables, const int64_t* table_rows, int table_dtype, int32_t mem_dim,
+                       const int32_t* orders, int32_t n_orders, int32_t bits, const void* ctx, int codes_dtype,
+                       int64_t B, int64_t h, int64_t n, int32_t R, int64_t start, void* out, void* stream);
+
+/* Contiguous candidate blocks of position `position` (candidate_rows / candidate_base,
+ * serving/layout.py:84-108; LayerTable.candidate_index, prefetch.py:201-215): hist [B, h, R] =
+ * the codes ending at position - 1.  out [B, R, n_orders, 2^bits, mem_dim]: rows base .. base + 2^bits
+ * - 1 of each order's serving table; zeros where the n-gram does not fit. */
+int lng_serving_candidates(const void* const* tables, const int64_t* table_rows, int table_dtype, int32_t mem_dim,
+                           const int32_t* orders, int32_t n_orders, int32_t bits, const void* hist, int codes_dtype,
+                           int64_t B, int64_t h, int32_t R, int64_t position, void* out, void* stream);
+
+/* out[N, mem_dim] = table[idx[N]] (LayerTable.gather, serving/prefetch.py:226-233: one
+ * index_select of a serving table, here by the device from device or mapped host memory); an
+ * index outside [0, table_rows) gives a zero row. */
+int lng_gather_rows(const void* table, int64_t table_rows, int dtype, int32_t mem_dim, const int64_t* idx, int64_t N,
+                    void* out, void* stream);
+
+/* out[M, R, n_orders * mem_dim] = cand[M, R, k, codes[M, R], :] (select_candidates,
+ * serving/layout.py:111-116). */
+int lng_select_candidates(const void* cand, int dtype, int32_t mem_dim, const void* codes, int codes_dtype,
+                          int64_t M, int32_t R, int32_t n_orders, int32_t bits, void* out, void* stream);
 
 /* ---------------------------------------------------------------- K4: SSM scan */
 /* s[B,T,N] (fp32): s_t = a*s_{t-1} + (1-a)*u_t, s_{-1} = s0[B,N] (zero if null).

@@ -133,8 +133,20 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   // a position outside [0, cstride) (a device position past the cache) reads no codes
   const bool codes_ok = tok_ok && tpos >= 0 && tpos < cstride;
 
+  // route-token mode (codes == null): table2 / table3 are the caller's route tokens [ntok, R, 256]
+  // seen as 128-wide rows, the 2-gram row of (token, route) at 2 (token R + route) of table2 and
+  // its 3-gram row at the same index of table3 = table2 + 128 (zeros where the lookup masks)
+  const bool rows_mode = codes == nullptr;
   // ---------------- stage 0: row indices of this wave's token (codes at t, t-1, t-2)
-  {
+  if (rows_mode) {
+#pragma unroll
+    for (int k = 0; k < FR_MAXR / 64; ++k) {
+      const int r = lane + 64 * k;
+      const int32_t rr = (tok_ok && r < R) ? static_cast<int32_t>((tok * R + r) * 2) : -1;
+      rowsh[w][0][r & 3][r >> 2] = rr;
+      rowsh[w][1][r & 3][r >> 2] = rr;
+    }
+  } else {
     uint8_t cv[3][FR_MAXR / 64];
 #pragma unroll
     for (int k = 0; k < FR_MAXR / 64; ++k) {
@@ -162,8 +174,8 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   // piece lane % 16 (a quarter wave per 256-byte table row); one order per instruction, so that
   // the 3-gram rows take their own cache policy (FR_POL_T3).
   const int g_sub = lane >> 4, g_piece = lane & 15;
-  // every row of a token at t >= 2 exists (both orders): its loads need no mask
-  const bool all_rows = tpos >= 2;
+  // every row of a token at t >= 2 exists (both orders), as does every route token: no mask
+  const bool all_rows = rows_mode || tpos >= 2;
   // 3-gram rows through a raw buffer descriptor (the table, at most 256 routes x 4096 rows x 256 B,
   // is < 4 GB, so row * 256 fits the 32-bit offset; every row index is in range, the descriptor's
   // size is left at its maximum)
@@ -438,6 +450,17 @@ extern "C" int lng_memory_readout_fused_at(const void* q, const void* q_rows, fl
     return fail(LNG_E_RANGE, "memory_readout_fused_at: positions pos0 .. pos0+n-1 past the codes");
   return readout_launch(q, q_rows, q_eps, codes, B, n, R, codes_len, pos0, pos0_dev, table2, table3, kv_pack, w_mem,
                         eps, scale, sink_logit, head_out, stream);
+}
+
+extern "C" int lng_memory_readout_fused_rows(const void* q, const void* q_rows, float q_eps, const void* route_tokens,
+                                             int64_t B, int64_t n, int32_t R, const void* kv_pack, const void* w_mem,
+                                             float eps, float scale, float sink_logit, void* head_out, void* stream) {
+  if (!route_tokens) return fail(LNG_E_ARG, "memory_readout_fused_rows: null route tokens");
+  if (B * n * static_cast<int64_t>(R) >= (int64_t{1} << 23))
+    return fail(LNG_E_ARG, "memory_readout_fused_rows: route tokens must stay under 4 GB (B * n * R < 2^23)");
+  const bf16* tok = static_cast<const bf16*>(route_tokens);
+  return readout_launch(q, q_rows, q_eps, nullptr, B, n, R, n, 0, nullptr, tok, tok + 128, kv_pack, w_mem, eps, scale,
+                        sink_logit, head_out, stream);
 }
 
 extern "C" int lng_memory_readout_pack(const void* kv, void* kv_pack, void* stream) {

@@ -172,7 +172,13 @@ def memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tenso
         raise ValueError(f"cache full: {L} + {n} > {state.max_len}")
     cache = state.codes[pos]
     cache[:, L:L + n] = codes_new.to(cache.dtype)
-    if route_tokens is None and m._fused_shape_ok(h):
+    if route_tokens is not None and m._fused_shape_ok(h, tables=False):
+        # rows from the caller (host-RAM serving, staged verify blocks): the same fused readout
+        q_raw = ops.linear(h, m._folded_query_weight())
+        head = ops.memory_readout_fused_rows(q_raw, route_tokens.to(h.device, torch.bfloat16), m._fused_weights(),
+                                             m.readout_memory_norm.weight, m.readout_memory_norm.eps, m.softmax_scale,
+                                             m.readout_sink_logit, q_rows=h, q_eps=m.readout_query_norm.eps)
+    elif route_tokens is None and m._fused_shape_ok(h):
         if route_codes_ctx is None:
             head = _readout_head(m, h, cache, L, None)
         else:
@@ -227,6 +233,17 @@ def static_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new
         key, value = m._project_memory(tokens)
         head = m._manual_gqa(m._project_query(h), key, value)
     return _finish_cached(m, head, state.conv_in[pos], 0, n, L32)
+
+
+def memory_decode(model, pos: int, state: DecodeState, h: Tensor, h_norm: Tensor | None = None,
+                  router_in: Tensor | None = None, route_codes_ctx: Tensor | None = None, row_provider=None) -> Tensor:
+    """The memory block of the reference's ``decode_step`` (``infer.py:226-241``): the new positions'
+    route codes, then ``row_provider(pos, state, codes) -> route tokens [B, n, R, len*D] | None``
+    (host-RAM serving; called before the codes enter the cache, ``state.length`` still L), then
+    ``memory_step``.  The caller advances ``state.length`` after the step, as ``decode_step`` does."""
+    codes = memory_codes(model, pos, state, h_norm=h_norm, router_in=router_in)
+    rows = None if row_provider is None else row_provider(pos, state, codes)
+    return memory_step(model, pos, state, h, codes, route_codes_ctx, rows)
 
 
 # ------------------------------------------------------------------ one memory layer's step

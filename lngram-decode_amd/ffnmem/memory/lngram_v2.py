@@ -451,12 +451,17 @@ class _RouteNgramMemoryBase(nn.Module):
         return self.short_conv.forward_residual(mixed)
 
     # ------------------------------------------------------------------ fused path
-    def _fused_shape_ok(self, hidden_states: Tensor) -> bool:
-        return (hidden_states.dtype == torch.bfloat16 and self.ngrams == (2, 3) and self.memory_dim == 128
-                and self.bits_per_route == 4 and self.num_routes <= 256
-                and self.readout_num_heads == 16 and self.readout_head_dim == 64
-                and self.readout_num_kv_heads == 4 and self.readout_kv_proj.weight.dtype == torch.bfloat16
-                and all(t.weight.dtype == torch.bfloat16 for t in self.tables.values()))
+    def _fused_shape_ok(self, hidden_states: Tensor, tables: bool = True) -> bool:
+        """Whether the fused readout serves this layer (``tables``: reading its own tables, which
+        must then be on the device, not offloaded)."""
+        ok = (hidden_states.dtype == torch.bfloat16 and self.ngrams == (2, 3) and self.memory_dim == 128
+              and self.bits_per_route == 4 and self.num_routes <= 256
+              and self.readout_num_heads == 16 and self.readout_head_dim == 64
+              and self.readout_num_kv_heads == 4 and self.readout_kv_proj.weight.dtype == torch.bfloat16
+              and all(t.weight.dtype == torch.bfloat16 for t in self.tables.values()))
+        if ok and tables:
+            ok = all(t.weight.device.type == "cuda" for t in self.tables.values())
+        return ok
 
     def _folded_query_weight(self) -> Tensor:
         """``readout_q_proj.weight`` with ``readout_query_norm.weight`` folded into its columns

@@ -92,6 +92,7 @@ SIGNATURES = {
     "lng_memory_readout_fused": (_int, [_p, _p, _f, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f, _f, _f, _p, _p]),
     "lng_memory_readout_fused_at": (_int, [_p, _p, _f, _p, _i64, _i64, _i32, _i64, _i64, _p, _p, _p, _p, _p, _f, _f,
                                            _f, _p, _p]),
+    "lng_memory_readout_fused_rows": (_int, [_p, _p, _f, _p, _i64, _i64, _i32, _p, _p, _f, _f, _f, _p, _p]),
     "lng_fold_columns": (_int, [_p, _p, _i64, _i64, _p, _p]),
     "lng_memory_readout_pack": (_int, [_p, _p, _p]),
     "lng_gather_sum_scaled": (_int, [ctypes.POINTER(_p), _int, _i32, _p, _i64, _i64, _i32, _P32, _i32, _i32, _i32,
@@ -99,6 +100,15 @@ SIGNATURES = {
     "lng_surrogate_grad": (_int, [_p, _p, _int, _p, _int, _p, _int, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32,
                                   _i32, _i32, _f, _f, _int, _p, _int, _p]),
     "lng_table_grad": (_int, [_p, _int, _p, _int, _p, _i64, _i64, _i32, _i32, _i32, _i32, _i32, _i64, _p, _p]),
+    "lng_host_device_pointer": (_int, [_p, ctypes.POINTER(_p)]),
+    "lng_permute_table": (_int, [_p, _p, _int, _i32, _i32, _i32, _i32, _p]),
+    "lng_serving_address": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _p, _p]),
+    "lng_serving_gather": (_int, [ctypes.POINTER(_p), _P64, _int, _i32, _P32, _i32, _i32, _p, _int, _i64, _i64, _i64,
+                                  _i32, _i64, _p, _p]),
+    "lng_serving_candidates": (_int, [ctypes.POINTER(_p), _P64, _int, _i32, _P32, _i32, _i32, _p, _int, _i64, _i64,
+                                      _i32, _i64, _p, _p]),
+    "lng_gather_rows": (_int, [_p, _i64, _int, _i32, _p, _i64, _p, _p]),
+    "lng_select_candidates": (_int, [_p, _int, _i32, _p, _int, _i64, _i32, _i32, _i32, _p, _p]),
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, ctypes.c_uint32, _p, _p]),
     "lng_ssm_scan_static": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p]),

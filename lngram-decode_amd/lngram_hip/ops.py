@@ -578,6 +578,36 @@ def memory_readout_fused_at(q: torch.Tensor, codes: torch.Tensor, pos0: int, tab
     return out
 
 
+def memory_readout_fused_rows(q: torch.Tensor, route_tokens: torch.Tensor, kv_pack: torch.Tensor, w_mem: torch.Tensor,
+                              eps: float, scale: float, sink_logit: float, q_rows: torch.Tensor | None = None,
+                              q_eps: float = 0.0) -> torch.Tensor:
+    """The fused readout over supplied route tokens (``lng_memory_readout_fused_rows``): q ``[B, n,
+    1024]``, route_tokens ``[B, n, R, 256]`` bf16 -> head ``[B, n, 1024]``, equal to the code path's
+    output for the same rows."""
+    dev = _dev(q, route_tokens, kv_pack, w_mem, q_rows)
+    b, n = q.shape[0], q.shape[1]
+    if route_tokens.dim() != 4 or route_tokens.shape[:2] != (b, n) or route_tokens.shape[3] != 256 or \
+            route_tokens.dtype != torch.bfloat16:
+        raise ValueError("fused readout: route tokens must be bf16 [B, n, R, 256]")
+    r = route_tokens.shape[2]
+    qc, rt = _c(q), _c(route_tokens)
+    if qc.dtype != torch.bfloat16 or qc.shape[-1] != 1024:
+        raise ValueError("fused readout expects a bf16 [B, n, 1024] query")
+    if kv_pack.shape != (_lib.READOUT_PACK_ELEMS,) or kv_pack.dtype != torch.bfloat16 or w_mem.shape != (256,):
+        raise ValueError("fused readout weight shapes")
+    qr = None
+    if q_rows is not None:
+        qr = _c(q_rows)
+        if qr.dtype != torch.bfloat16 or qr.shape != qc.shape:
+            raise ValueError("fused readout: q_rows must be bf16 and shaped like q")
+    out = torch.empty(b, n, 1024, dtype=torch.bfloat16, device=dev)
+    kp, wmc = _c(kv_pack), _c(w_mem.to(torch.bfloat16))
+    check(lib().lng_memory_readout_fused_rows(_ptr(qc), _ptr(qr), float(q_eps), _ptr(rt), b, n, r, _ptr(kp), _ptr(wmc),
+                                              eps, scale, sink_logit, _ptr(out), _stream(dev)),
+          "memory_readout_fused_rows")
+    return out
+
+
 def gather_sum_scaled(tables, codes: torch.Tensor, orders, bits: int, scale_log2: int, seed: int) -> torch.Tensor:
     """fp32 ``[B, T, mem_dim]``: per token, the sum of one row per (route, order) of tables grown
     ``2**scale_log2`` times per route (``lng_gather_sum_scaled``); ``codes [B, T, R]`` uint8,
@@ -651,6 +681,133 @@ def table_grad(grad_memory: torch.Tensor, codes: torch.Tensor, valid_mask: torch
         _ptr(g), dtype_code(g.dtype), _ptr(cc), dtype_code(cc.dtype), _ptr(vm), b, t, r, int(route_start), md,
         int(order), int(bits), int(table_rows), _ptr(out), _stream(dev)))
     check(rc, "table_grad")
+    return out
+
+
+# ----------------------------------------------------------------------------- serving layout
+def table_address(t: torch.Tensor) -> int:
+    """Device-visible address of a table's first element: a GPU tensor's own, or the mapping of a
+    pinned host tensor into the device's address space (``lng_host_device_pointer``), through which
+    the serving kernels read host RAM directly."""
+    if t.device.type == "cuda":
+        return t.data_ptr()
+    if t.device.type != "cpu" or not t.is_pinned():
+        raise RuntimeError("a host table must be pinned host memory (allocate it with pin_memory=True)")
+    base = t.untyped_storage().data_ptr()
+    dp = ctypes.c_void_p()
+    check(lib().lng_host_device_pointer(ctypes.c_void_p(base), ctypes.byref(dp)), "host_device_pointer")
+    return dp.value + (t.data_ptr() - base)
+
+
+def _table_args(tables, orders, bits: int, routes: int):
+    ts = [t if t.is_contiguous() else None for t in tables]
+    if any(t is None for t in ts):
+        raise ValueError("serving tables must be contiguous")
+    dt, md = ts[0].dtype, ts[0].shape[1]
+    for t, o in zip(ts, orders):
+        if t.dtype != dt or t.dim() != 2 or t.shape[1] != md:
+            raise ValueError("serving tables: one dtype and row width")
+        if t.shape[0] < routes << (bits * int(o)):
+            raise ValueError(f"serving table of order {o} has {t.shape[0]} rows, needs {routes << (bits * int(o))}")
+    ptrs = (ctypes.c_void_p * len(ts))(*[table_address(t) for t in ts])
+    rows = (ctypes.c_int64 * len(ts))(*[t.shape[0] for t in ts])
+    return ptrs, rows, dt, md
+
+
+def permute_table(weight: torch.Tensor, routes: int, order: int, bits: int, out: torch.Tensor | None = None):
+    """Serving layout of a v2 table, or back (an involution): ``lng_permute_table``."""
+    dev = _dev(weight, out)
+    w = _c(weight)
+    if w.dim() != 2 or w.shape[0] != routes << (bits * order):
+        raise ValueError(f"table must be [routes * 2^(bits*order), D], got {tuple(w.shape)}")
+    out = torch.empty_like(w) if out is None else out
+    if out.shape != w.shape or out.dtype != w.dtype or not out.is_contiguous():
+        raise ValueError("permute_table: out must match the table")
+    check(lib().lng_permute_table(_ptr(w), _ptr(out), dtype_code(w.dtype), int(routes), int(order), int(bits),
+                                  w.shape[1], _stream(dev)), "permute_table")
+    return out
+
+
+def serving_address(codes: torch.Tensor, order: int, bits: int) -> torch.Tensor:
+    """int64 ``[B, T-order+1, R]``: window addresses with the current code least significant."""
+    dev = _dev(codes)
+    c = _c(codes if codes.dtype in (torch.uint8, torch.int32, torch.int64) else codes.to(torch.int64))
+    b, t, r = c.shape
+    out = torch.empty(b, max(0, t - order + 1), r, dtype=torch.int64, device=dev)
+    check(lib().lng_serving_address(_ptr(c), dtype_code(c.dtype), b, t, r, int(order), int(bits), _ptr(out),
+                                    _stream(dev)), "serving_address")
+    return out
+
+
+def serving_gather(tables, orders, bits: int, ctx: torch.Tensor, n: int, start: int,
+                   out: torch.Tensor | None = None) -> torch.Tensor:
+    """Route tokens ``[B, n, R, len(orders) * D]`` of the last ``n`` positions of ``ctx [B, h + n, R]``
+    (first new position = absolute ``start``) from serving-layout tables (device or pinned host
+    memory): ``lng_serving_gather``."""
+    dev = _dev(ctx, out)
+    c = _c(ctx if ctx.dtype in (torch.uint8, torch.int32, torch.int64) else ctx.to(torch.int64))
+    b, tc, r = c.shape
+    h = tc - n
+    ptrs, rows, dt, md = _table_args(tables, orders, bits, r)
+    if out is None:
+        out = torch.empty(b, n, r, len(orders) * md, dtype=dt, device=dev)
+    elif out.shape != (b, n, r, len(orders) * md) or out.dtype != dt or not out.is_contiguous():
+        raise ValueError("serving_gather: out must be a contiguous [B, n, R, len(orders) * D] of the tables' dtype")
+    rc = _timed("serving_gather", dev, lambda: lib().lng_serving_gather(
+        ptrs, rows, dtype_code(dt), md, _orders(orders), len(orders), int(bits), _ptr(c), dtype_code(c.dtype), b, h, n,
+        r, int(start), _ptr(out), _stream(dev)))
+    check(rc, "serving_gather")
+    return out
+
+
+def serving_candidates(tables, orders, bits: int, hist: torch.Tensor, position: int,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """Candidate blocks ``[B, R, len(orders), 2^bits, D]`` of ``position`` from the codes ``hist [B, h, R]``
+    ending at ``position - 1``: ``lng_serving_candidates``."""
+    dev = _dev(hist, out)
+    c = _c(hist if hist.dtype in (torch.uint8, torch.int32, torch.int64) else hist.to(torch.int64))
+    b, h, r = c.shape
+    ptrs, rows, dt, md = _table_args(tables, orders, bits, r)
+    shape = (b, r, len(orders), 1 << bits, md)
+    if out is None:
+        out = torch.empty(shape, dtype=dt, device=dev)
+    elif tuple(out.shape) != shape or out.dtype != dt or not out.is_contiguous():
+        raise ValueError(f"serving_candidates: out must be a contiguous {shape} of the tables' dtype")
+    rc = _timed("serving_candidates", dev, lambda: lib().lng_serving_candidates(
+        ptrs, rows, dtype_code(dt), md, _orders(orders), len(orders), int(bits), _ptr(c), dtype_code(c.dtype), b, h, r,
+        int(position), _ptr(out), _stream(dev)))
+    check(rc, "serving_candidates")
+    return out
+
+
+def gather_rows(table: torch.Tensor, idx: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``table[idx]`` (``[*idx.shape, D]``) by the device, from a device or pinned host table
+    (``lng_gather_rows``); an index outside the table gives a zero row."""
+    dev = _dev(idx, out)
+    if table.dim() != 2 or not table.is_contiguous():
+        raise ValueError("gather_rows: a contiguous [rows, D] table")
+    ii = _c(idx.reshape(-1).to(torch.int64))
+    md = table.shape[1]
+    if out is None:
+        out = torch.empty(ii.numel(), md, dtype=table.dtype, device=dev)
+    elif out.numel() != ii.numel() * md or out.dtype != table.dtype or not out.is_contiguous():
+        raise ValueError("gather_rows: out must be a contiguous buffer of idx.numel() rows")
+    check(lib().lng_gather_rows(ctypes.c_void_p(table_address(table)), table.shape[0], dtype_code(table.dtype), md,
+                                _ptr(ii), ii.numel(), _ptr(out), _stream(dev)), "gather_rows")
+    return out.view(*idx.shape, md)
+
+
+def select_candidates(cand: torch.Tensor, codes: torch.Tensor, bits: int) -> torch.Tensor:
+    """``[M, R, K * D]`` rows of ``cand [M, R, K, 2^bits, D]`` at ``codes [M, R]``: ``lng_select_candidates``."""
+    dev = _dev(cand, codes)
+    cd = _c(cand)
+    m, r, k, a, md = cd.shape
+    if a != 1 << bits or tuple(codes.shape) != (m, r):
+        raise ValueError("select_candidates: cand [M, R, K, 2^bits, D] and codes [M, R]")
+    cc = _c(codes if codes.dtype in (torch.uint8, torch.int32, torch.int64) else codes.to(torch.int64))
+    out = torch.empty(m, r, k * md, dtype=cd.dtype, device=dev)
+    check(lib().lng_select_candidates(_ptr(cd), dtype_code(cd.dtype), md, _ptr(cc), dtype_code(cc.dtype), m, r, k,
+                                      int(bits), _ptr(out), _stream(dev)), "select_candidates")
     return out
 
 

@@ -129,3 +129,25 @@ def test_workload_bytes_match_the_roofline_arithmetic():
     # SB: 2 KB h + 2 KB h_norm + 184*2*128*2 rows + 2 KB out = 100,352 B per token
     assert workloads.SB.algorithmic_bytes_per_token() == 100_352
     assert workloads.SB.tokens == 16384
+
+
+def test_serving_layout_index_helpers_and_no_cpu_path():
+    """The serving layout's index bookkeeping (``serving/layout.py:26-35``, ``:84-100``) on the CPU;
+    the row movers refuse CPU tensors."""
+    import pytest as _pytest
+    import torch as _torch
+
+    from serving import layout as sl
+    from serving.prefetch import HostGather, LayerTable
+
+    r = sl.reverse_digits(3, 4)
+    assert _torch.equal(r[r], _torch.arange(4096))
+    assert int(r[1]) == 256 and int(r[16]) == 16 and int(r[0x123]) == 0x321
+    hist = _torch.tensor([[[3, 1], [5, 2]]])                     # [B 1, 2 codes, R 2], oldest first
+    base = sl.candidate_base(hist, 3, 4)
+    assert base.tolist() == [[16 * (5 + 16 * 3), 4096 + 16 * (2 + 16 * 1)]]
+    assert LayerTable.num_rows(2, (2, 3), 4) == 2 * (256 + 4096) + 1
+    with _pytest.raises(RuntimeError, match="CPU path|ROCm"):
+        sl.serving_address(_torch.zeros(1, 4, 2, dtype=_torch.uint8), 2, 4)
+    with _pytest.raises(RuntimeError, match="CPU path"):
+        HostGather({0: None}, "cpu")
