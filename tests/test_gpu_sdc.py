@@ -84,3 +84,42 @@ def test_sdc_shape_forward(dev):
     assert om.rel_err(out, ref) < 2e-2
     ref64 = om.memory_forward(p, cfg_of(w), h.double(), codes)
     assert om.rel_err(out, ref64) < 2e-2
+
+
+def test_sdc_full_size_sampled(dev):
+    """The full SD-C shape (8 x 4096 tokens, R181, 256-channel SSM): the scan and the router features
+    against the oracle, every code against the fp64 router (outside the near-tie band), and the
+    layer output at sampled positions against the bf16 and fp64 oracles of their 12-position
+    causal windows (the conv's halo is 9 positions, the n-grams reach 2 back)."""
+    from .test_gpu_memory import _window_oracle
+
+    w = workloads.SDC
+    mem, E, tok, a, u, h = _sdc_pipeline(w, dev, seed=3)
+    feats = mem.router_features
+    s = ops.ssm_scan(a.to(dev), u.to(dev))
+    x = feats.from_ids(tok.to(dev), E.to(dev), s)
+    out = mem(h.to(dev), None, router_in=x)
+    assert out.shape == (8, 4096, 1024) and bool(torch.isfinite(out).all())
+    _, codes_gpu = mem.route_codes(x)
+    s_ref = torch.from_numpy(om.ssm_scan(a.numpy(), u.numpy()))
+    assert om.rel_err(s.cpu().double(), s_ref) < 1e-5
+    p = oracle_params(mem)
+    fsd = {k: v.detach().cpu() for k, v in feats.state_dict().items()}
+    for b in (0, 5):                                          # whole sequences of two batch rows
+        want = om.router_features(E[tok[b]][None], fsd["start"], fsd["prev_norm.weight"], fsd["cur_norm.weight"],
+                                  w.norm_eps, s.cpu()[b][None])
+        assert om.rel_err(x[b].cpu().double(), want[0].double()) < 4e-3, b
+    rng = np.random.default_rng(1)
+    q64 = om.router_logits(x.reshape(-1, x.shape[-1]).cpu(), p["router.weight"]).numpy().reshape(8, 4096, -1)
+    codes, near = codes_check(codes_gpu.cpu().numpy().astype(np.int32), q64)
+    print(f"near-tie routes at SD-C size: {near} of {codes.size}")
+    out_given = mem.module(h.to(dev), torch.as_tensor(codes, device=dev)).cpu()
+    picks = [(0, 0), (0, 1), (0, 2), (4, 9), (7, 4095)] + [(int(rng.integers(0, 8)), int(rng.integers(0, 4096)))
+                                                          for _ in range(11)]
+    cfg = cfg_of(w)
+    got = torch.stack([out_given[b, t] for b, t in picks])
+    want = torch.stack([_window_oracle(p, cfg, h, codes, b, t) for b, t in picks])
+    want64 = torch.stack([om.memory_forward(p, cfg, h[b:b + 1, max(0, t - 11):t + 1].double(),
+                                            codes[b:b + 1, max(0, t - 11):t + 1])[0, -1] for b, t in picks])
+    assert om.rel_err(got, want) < 2e-2
+    assert om.rel_err(got, want64) < 2e-2
