@@ -644,14 +644,19 @@ def surrogate_backward(dev, steps: int, warmup: int):
         alg = B * T * R * sum((2 + n * bits) * D * 2 + 2 * bits * 4 + 1 for n in (2, 3))
         kern_ms = sum(d) / len(d) * 2
         gbs = alg / (kern_ms * 1e-3) / 1e9
+        # distinct bytes: the memory-gradient and looked-up streams, logits, gradient and codes once, plus
+        # each order's table once
+        distinct = sum(B * T * R * (2 * D * 2 + 2 * bits * 4 + 1) + (R << (bits * n)) * D * 2 for n in (2, 3))
         legs.clear()
         torch.cuda.empty_cache()
         return {"workload": "lookup surrogate backward (approximate) at the SB shape: B8 x T2048, R184, mem_dim 128, "
                             "bf16 tables of orders 2 and 3; route-logit gradient of both orders",
                 "kernel": "k_surrogate_grad", "ms_per_step": ms, "tokens_per_s": B * T / (ms * 1e-3), **per_order,
-                "algorithmic_bytes": alg, "achieved_GBs": gbs, "hbm_frac": gbs / HBM_PEAK_GBS, "steps": steps,
-                "note": "the counterfactual rows of a window lie in its route's block (1 MB of the 3-gram table), "
-                        "so most of these bytes come from L2 / the Infinity Cache"}
+                "gathered_bytes": alg, "gathered_GBs": gbs, "distinct_bytes": distinct,
+                "distinct_GBs": distinct / (kern_ms * 1e-3) / 1e9,
+                "distinct_hbm_frac": distinct / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "steps": steps,
+                "note": "gathered bytes: the rows the reference algorithm reads (the counterfactual rows of a window "
+                        "lie in its route's block, so most come from L2); distinct bytes: what has to cross HBM"}
 
     return run
 

@@ -28,7 +28,10 @@ namespace lng {
 
 constexpr int SSM_WAVES = 8;          // waves per block
 constexpr int SSM_GC = 256;           // channels per group (64 lanes x 4)
-constexpr int SSM_LW = 16;            // steps per wave
+#ifndef LNG_SSM_LW
+#define LNG_SSM_LW 16
+#endif
+constexpr int SSM_LW = LNG_SSM_LW;    // steps per wave
 constexpr int SSM_SPAN = SSM_WAVES * SSM_LW;
 constexpr int SSM_WIN = 32;           // aggregates folded per look-back; the record before comes inclusive
 constexpr int SSM_PER_WAVE = (SSM_WIN + 1 + SSM_WAVES - 1) / SSM_WAVES;

@@ -104,6 +104,26 @@ __device__ __forceinline__ void load_row_nt(const TM* base, int64_t e, bool nt, 
   load_row<TM, V>(base + e, v);
 }
 
+typedef __bf16 sg_bf16x2 __attribute__((ext_vector_type(2)));
+
+// bf16 rows of 128 (16 bytes per lane) stay packed: a lane's share of a dot product is four
+// v_dot2_f32_bf16 (each bf16 product is exact in fp32) instead of eight conversions and FMAs
+__device__ __forceinline__ u32x4 ld_raw16(const void* base, int64_t byte_off, bool nt) {
+  if (nt) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, -1, BUF_DW3);
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<uint32_t>(byte_off), 0,
+                                                                           CPOL_NT));
+  }
+  return *reinterpret_cast<const u32x4*>(static_cast<const char*>(base) + byte_off);
+}
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(sg_bf16x2, a), __builtin_bit_cast(sg_bf16x2, b), acc,
+                                         false);
+}
+__device__ __forceinline__ float dot8_bf16(u32x4 a, u32x4 b) {
+  return dot2_bf16(a.w, b.w, dot2_bf16(a.z, b.z, dot2_bf16(a.y, b.y, dot2_bf16(a.x, b.x, 0.f))));
+}
+
 constexpr int SG_WIN = 64;                       // windows per block (16 groups x 4)
 constexpr int SG_SC = SG_MAXORDER * SG_MAXBITS;  // scores per window in LDS: [e][bit]
 
@@ -144,9 +164,10 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
     for (int e = 0; e < SG_MAXORDER; ++e)
 #pragma unroll
       for (int k = 0; k < SG_MAXBITS; ++k) score[e][k] = 0.f;
-    if (active && s >= 0 && s < VL) {
+    // a window whose memory position is masked has a zero gradient row: its scores stay zero
+    const bool win = active && s >= 0 && s < VL && (a.valid == nullptr || a.valid[b * a.T + s + order - 1]);
+    if (win) {
       const int64_t pos = s + order - 1;
-      const float vm = (a.valid == nullptr || a.valid[b * a.T + pos]) ? 1.f : 0.f;
       int64_t addr = 0;
       int64_t digit[SG_MAXORDER];
 #pragma unroll
@@ -159,10 +180,35 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
       }
       const int64_t idx = block_base + addr;
       const int64_t mrow = (b * a.T + pos) * RD + static_cast<int64_t>(r) * D + l * V;
+      constexpr bool PACKED = sizeof(TM) == 2 && V == 8;
+      if constexpr (PACKED && !EXACT) {
+        const u32x4 gr = ld_raw16(grad, mrow * 2, nt);
+        const float cd = sum16(dot8_bf16(ld_raw16(hard, mrow * 2, nt), gr));
+#pragma unroll
+        for (int e = 0; e < SG_MAXORDER; ++e) {
+          if (e < order) {
+#pragma unroll
+            for (int k0 = 0; k0 < SG_MAXBITS; k0 += 4) {
+              if (k0 < bits) {
+                u32x4 f[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                  if (k0 + k < bits) f[k] = ld_raw16(table, ((idx ^ (int64_t(1) << (e * bits + k0 + k))) * D + l * V) * 2,
+                                                     false);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                  if (k0 + k < bits) {
+                    const float fd = sum16(dot8_bf16(f[k], gr));
+                    score[e][k0 + k] = (fd - cd) * (((idx >> (e * bits + k0 + k)) & 1) ? -1.f : 1.f);
+                  }
+                }
+              }
+            }
+          }
+        }
+      } else {
       float g[V];
       load_row_nt<TM, V>(grad, mrow, nt, g);
-#pragma unroll
-      for (int j = 0; j < V; ++j) g[j] *= vm;
       if constexpr (!EXACT) {
         float m[V];
         load_row_nt<TM, V>(hard, mrow, nt, m);
@@ -235,6 +281,7 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
             }
           }
         }
+      }
       }
     }
     if (l == 0) {
