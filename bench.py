@@ -345,6 +345,60 @@ def _tiny_result(w, ms: float) -> dict:
             "note": "launch-bound (512 tokens): the roofline fraction is not meaningful"}
 
 
+def chain_draft(dev, iters: int, warmup: int):
+    """Set up, and return the timing run of, the reference's own drafter benchmark
+    (``drafting/cpu_drafter.py:409-423``) on its published configuration's shapes (the SD-C bundle:
+    R181, V32768, d1024, 256-channel SSM router and query term, count sketches K 16 per row and order,
+    shortlist 64; ``results/evaluation/drafter/cpu_bench_sdc.json``): commit a 256-token random
+    prompt, then per iteration time ``draft(4)`` (results on the host), divide by gamma, and commit
+    the first drafted token."""
+    import numpy as np
+    import torch
+
+    from drafting.gpu_drafter import GpuDrafter
+    from lngram_hip import workloads
+
+    w = workloads.SDC_DRAFT
+    cfg, t = workloads.build_draft_bundle(w, seed=0)
+    rng = np.random.default_rng(3)
+    V, R, bits = cfg["vocab"], cfg["routes"], cfg["bits"]
+    for n in cfg["ngrams"]:
+        rows = R * (1 << (bits * n))
+        t[f"sketch_ids_{n}"] = torch.from_numpy(rng.integers(0, V, (rows, 16)).astype(np.int32))
+        t[f"sketch_counts_{n}"] = torch.from_numpy(rng.integers(0, 4, (rows, 16)).astype(np.int64))
+    t["fallback"] = torch.from_numpy(rng.choice(V, size=64, replace=False).astype(np.int32))
+    cfg = dict(cfg, sketch_k=16, shortlist_cap=64)
+    gamma, plen = 4, 256
+    g = GpuDrafter((cfg, t), device=dev, max_len=plen + warmup + iters + 16)
+    prompt = [int(x) for x in np.random.default_rng(0).integers(0, V, plen)]
+
+    def run() -> dict:
+        g.reset()
+        g.commit(prompt)
+        per_tok = []
+        for i in range(warmup + iters):
+            t0 = time.perf_counter()
+            out = g.draft(gamma)
+            dt = time.perf_counter() - t0
+            if i >= warmup:
+                per_tok.append(dt / gamma * 1e6)
+            g.commit(out.tokens[:1])
+        a = np.asarray(per_tok)
+        med = float(np.median(a))
+        return {"workload": "the reference's drafter benchmark: SD-C bundle shapes (R181, V32768, d1024, N256, bf16 "
+                            "tables), sketch K 16, shortlist 64, gamma 4, 256-token random prompt, one token committed "
+                            "per draft",
+                "unit": "us per drafted token", "iters": iters, "median_us": med,
+                "p99_us": float(np.percentile(a, 99)), "mean_us": float(a.mean()),
+                "reference_published": {"cpp_1_thread_us": 10312.791913747787, "cpp_4_threads_us": 3603.148739784956,
+                                        "pytorch_us": 1317.1385508030653,
+                                        "source": "results/evaluation/drafter/cpu_bench_sdc.json, cpu_bench_sdc_ref.json "
+                                                  "(host CPU of the reference's evaluation box, fp16 tables)"},
+                "vs_reference_cpp_1_thread": 10312.791913747787 / med}
+
+    return run
+
+
 def decode_step(dev, iters: int, warmup: int):
     """Set up, and return the timing run of, the cached decode step of the SB-shape memory layer:
     8 sequences with 2048 cached positions each take one new token (router codes, fused readout
@@ -758,6 +812,9 @@ def main() -> None:
     if not args.no_draft:
         log("draft step: set-up")
         legs["draft_step_us"] = draft_step(dev, args.draft_iters, 20)
+    if not args.no_draft:
+        log("chain draft (the reference's drafter benchmark): set-up")
+        legs["chain_draft"] = chain_draft(dev, args.draft_iters, 20)
     if not args.no_draft:
         log("cached decode step: set-up")
         legs["decode_step"] = decode_step(dev, args.draft_iters, 20)

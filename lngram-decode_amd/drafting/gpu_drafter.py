@@ -145,6 +145,11 @@ class GpuDrafter:
                 self.tree_work = torch.zeros(int(fb), dtype=torch.uint8, device=dev)
         self.ids_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.int64, device=dev)
         self.sc_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.float32, device=dev)
+        # a draft's results (top-k ids, scores, codes of the drafted rows) leave the device in one
+        # copy: packed into a device staging buffer, then copied to pinned host memory
+        self._out_bytes = _HYP_ROWS * _MAX_K * 12 + _HYP_ROWS * self.R
+        self._out_d = torch.empty(self._out_bytes, dtype=torch.uint8, device=dev)
+        self._out_h = torch.empty(self._out_bytes, dtype=torch.uint8, pin_memory=True)
         if self.sketch is not None:
             # full-vocabulary logits and top-k of up to 16 positions (the shortlist kernel's inputs)
             self.sl_lg = torch.empty(16, self.V, dtype=torch.float32, device=dev)
@@ -402,13 +407,29 @@ class GpuDrafter:
                           "drafter advance")
                     seq.append(nxt)
                     advanced += 1
-            ids = self.ids_d[:gamma, :k].cpu().numpy().copy()
-            lg = self.sc_d[:gamma, :k].cpu().numpy().copy()
-            codes = self.codes_d[base: base + nh + advanced].cpu().numpy().copy()
+            ids, lg, codes = self._fetch(gamma, k, base, nh + advanced)
         if gamma and (ids[:, 0] == -2).any():
             raise RuntimeError("drafter select: candidate buffer overflow (context too long for online counts)")
         lg[ids < 0] = -np.inf
         return DraftOut([int(x) for x in ids[:, 0]], ids, lg.astype(np.float32), codes)
+
+    def _fetch(self, gamma: int, k: int, row0: int, nrows: int):
+        """Top-k ids [gamma, k], scores [gamma, k] and the codes of rows row0 .. row0+nrows-1 on the
+        host, through one device-to-host copy."""
+        n_ids, n_sc, n_c = gamma * k * 8, gamma * k * 4, nrows * self.R
+        total = n_ids + n_sc + n_c
+        d = self._out_d
+        d[:n_ids].view(torch.int64).view(gamma, k).copy_(self.ids_d[:gamma, :k])
+        d[n_ids:n_ids + n_sc].view(torch.float32).view(gamma, k).copy_(self.sc_d[:gamma, :k])
+        d[n_ids + n_sc:total].view(nrows, self.R).copy_(self.codes_d[row0: row0 + nrows])
+        h = self._out_h
+        h[:total].copy_(d[:total], non_blocking=True)
+        torch.cuda.current_stream(self.device).synchronize()
+        a = h[:total].numpy()
+        ids = a[:n_ids].view(np.int64).reshape(gamma, k).copy()
+        lg = a[n_ids:n_ids + n_sc].view(np.float32).reshape(gamma, k).copy()
+        codes = a[n_ids + n_sc:total].reshape(nrows, self.R).copy()
+        return ids, lg, codes
 
     def draft_tree(self, spec) -> list:
         """``draft_tree`` (``drafting/tree.py:243-257``) with every parent of one depth in one readout;
