@@ -420,7 +420,9 @@ typedef struct lng_drafter {
    *   wv_t      [kv_heads, Dt, hd] (wv_dtype)   Wv[h]^T, the value rows of kv_proj transposed
    *   mem_norm  [Dt] fp32   readout_memory_norm weight
    *   sync      int32 [LNG_DR_SYNC_INTS], zero before the first call; every call leaves it
-   *             zero (block counters, online totals and per-block candidate counts). */
+   *             zero (block counters, online totals and per-block candidate counts).  Any
+   *             drafter may set it: readouts of at most 4 positions then run the small-batch
+   *             kernels (one weight row per wave, route chunks merged by the last block). */
   const float* lut_prev;
   const float* lut_cur;
   const float* lut_start;
@@ -499,6 +501,18 @@ int lng_drafter_shortlist(const lng_drafter* D, const lng_sketch* S, const int32
                           const int32_t* child_rows, const int32_t* child_parent, const int32_t* child_rank,
                           int32_t n_children, int64_t* ids, float* scores, int32_t* shortlist,
                           float* shortlist_logits, void* stream);
+
+/* The readout and the sketch shortlist of P positions in one call (RefDrafter.draft's per-token
+ * step with a shortlist: _readout of the shortlist tokens only, cpu_drafter.py:238-262;
+ * drafter.cpp:438-474): the candidates are scored from the readout's hidden state, and only a
+ * position whose list is empty scores the whole vocabulary.  Results as lng_drafter_readout
+ * followed by lng_drafter_shortlist (same list, ids, scores and children; logits within fp32
+ * rounding).  work: lng_drafter_workspace_bytes(D, P, k, .) bytes.  No online counts. */
+int lng_drafter_readout_shortlist(const lng_drafter* D, const lng_sketch* S, const int32_t* windows, int32_t P,
+                                  int32_t k, const int32_t* child_rows, const int32_t* child_parent,
+                                  const int32_t* child_rank, int32_t n_children, void* work, size_t work_bytes,
+                                  int64_t* ids, float* scores, int32_t* shortlist, float* shortlist_logits,
+                                  void* stream);
 
 /* One draft-tree step (draft_tree, drafting/tree.py:243-257, batched by depth): node 0 is the
  * last committed token, node i >= 1 lives at absolute row node_row0 + i; parent/rank (host, n

@@ -71,6 +71,49 @@ __device__ __forceinline__ float ld_any(const void* p, int dt, int64_t i) {
   return dt == LNG_BF16 ? ldf<bf16>(p, i) : (dt == LNG_F16 ? ldf<_Float16>(p, i) : ldf<float>(p, i));
 }
 
+// Four / eight consecutive elements of a float, bf16 or fp16 row as fp32 (8- / 16-byte aligned for
+// the 2-byte types, 16- / 32-byte for fp32).
+__device__ __forceinline__ f32x4 bf2f4(uint32_t a, uint32_t b) {
+  return f32x4{__uint_as_float(a << 16), __uint_as_float(a & 0xffff0000u), __uint_as_float(b << 16),
+               __uint_as_float(b & 0xffff0000u)};
+}
+__device__ __forceinline__ f32x4 h2f4(uint32_t a, uint32_t b) {
+  return f32x4{static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a & 0xffffu))),
+               static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(a >> 16))),
+               static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b & 0xffffu))),
+               static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(b >> 16)))};
+}
+__device__ __forceinline__ f32x4 ld4_any(const void* p, int dt, int64_t i) {
+  if (dt == LNG_F32) return *reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + i);
+  const uint2 v = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p) + i);
+  return dt == LNG_BF16 ? bf2f4(v.x, v.y) : h2f4(v.x, v.y);
+}
+template <typename T>
+__device__ __forceinline__ void ld8f(const T* p, f32x4& a, f32x4& b);
+template <>
+__device__ __forceinline__ void ld8f<float>(const float* p, f32x4& a, f32x4& b) {
+  a = reinterpret_cast<const f32x4*>(p)[0];
+  b = reinterpret_cast<const f32x4*>(p)[1];
+}
+template <>
+__device__ __forceinline__ void ld8f<bf16>(const bf16* p, f32x4& a, f32x4& b) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  a = bf2f4(v.x, v.y);
+  b = bf2f4(v.z, v.w);
+}
+template <>
+__device__ __forceinline__ void ld8f<_Float16>(const _Float16* p, f32x4& a, f32x4& b) {
+  const u32x4 v = *reinterpret_cast<const u32x4*>(p);
+  a = h2f4(v.x, v.y);
+  b = h2f4(v.z, v.w);
+}
+__device__ __forceinline__ float dot4(f32x4 a, f32x4 b, float acc) {
+  acc = fmaf(a.x, b.x, acc);
+  acc = fmaf(a.y, b.y, acc);
+  acc = fmaf(a.z, b.z, acc);
+  return fmaf(a.w, b.w, acc);
+}
+
 // Sum over a block of 256 threads (4 waves); `red` holds >= 4 floats.
 __device__ __forceinline__ float block_sum256(float v, float* red) {
   v = wave_sum(v);
@@ -410,14 +453,22 @@ __global__ __launch_bounds__(256) void k_draft_hidden(lng_drafter D, int32_t P, 
 // logits[j, v] = E[v] . (RMSNorm(hid_j) * out_norm); per block and position: max, sum of
 // exponentials and the block's top-k by (logit desc, index asc):
 // lpart[(j * nblk + b) * (2 + 2K)] = {max, sumexp, K logits, K indices (as float bits)}
+// Each wave scores four vocabulary rows at a time with 16-byte loads (d % 8 == 0; else one
+// element per lane and load).  need (optional, [P]): the launch is skipped unless a position has
+// need[j] != 0 (the shortlist left it to the whole vocabulary).
 //                                                                   grid (cdiv(V, 64))
-template <typename TE>
+template <typename TE, int PM>
 __global__ __launch_bounds__(256) void k_draft_logits(lng_drafter D, int32_t P, int32_t K,
                                                       const float* __restrict__ hid, float* __restrict__ logits,
-                                                      float* __restrict__ lpart) {
-  extern __shared__ float hs[];  // [P][d]
+                                                      float* __restrict__ lpart, const int32_t* __restrict__ need) {
+  extern __shared__ __attribute__((aligned(16))) float hs[];  // [P][d]
   __shared__ float red[4];
   __shared__ float lt[DR_MAXP][DR_VB];
+  if (need) {
+    bool any = false;
+    for (int j = 0; j < P; ++j) any = any || need[j] != 0;
+    if (!any) return;
+  }
   const int d = D.d;
   const int64_t V = D.V;
   for (int j = 0; j < P; ++j) {
@@ -434,29 +485,76 @@ __global__ __launch_bounds__(256) void k_draft_logits(lng_drafter D, int32_t P, 
   __syncthreads();
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const TE* E = static_cast<const TE*>(D.emb);
-  for (int q = 0; q < DR_VB / 4; ++q) {
-    const int vl = w * (DR_VB / 4) + q;
-    const int64_t v = static_cast<int64_t>(blockIdx.x) * DR_VB + vl;
-    if (v >= V) {
-      if (lane < DR_MAXP) lt[lane][vl] = -INFINITY;
-      continue;
+  if (d % 8 == 0) {
+    for (int q0 = 0; q0 < DR_VB / 4; q0 += 4) {
+      const int vl0 = w * (DR_VB / 4) + q0;
+      const int64_t v0 = static_cast<int64_t>(blockIdx.x) * DR_VB + vl0;
+      float acc[4][PM];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int jj = 0; jj < PM; ++jj) acc[u][jj] = 0.f;
+      for (int c8 = lane; c8 < d / 8; c8 += 64) {
+        f32x4 ea[4], eb[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (v0 + u < V) {
+            ld8f<TE>(E + (v0 + u) * d + 8 * c8, ea[u], eb[u]);
+          } else {
+            ea[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            eb[u] = ea[u];
+          }
+        }
+#pragma unroll
+        for (int jj = 0; jj < PM; ++jj) {
+          if (jj < P) {
+            const f32x4 h0 = *reinterpret_cast<const f32x4*>(hs + jj * d + 8 * c8);
+            const f32x4 h1 = *reinterpret_cast<const f32x4*>(hs + jj * d + 8 * c8 + 4);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc[u][jj] = dot4(eb[u], h1, dot4(ea[u], h0, acc[u][jj]));
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int vl = vl0 + u;
+        const int64_t v = v0 + u;
+#pragma unroll
+        for (int jj = 0; jj < PM; ++jj) {
+          if (jj >= P) continue;
+          const float a = wave_sum(acc[u][jj]);
+          if (lane == 0) {
+            lt[jj][vl] = v < V ? a : -INFINITY;
+            if (v < V) logits[static_cast<int64_t>(jj) * V + v] = a;
+          }
+        }
+      }
     }
-    float acc[DR_MAXP];
+  } else {
+    for (int q = 0; q < DR_VB / 4; ++q) {
+      const int vl = w * (DR_VB / 4) + q;
+      const int64_t v = static_cast<int64_t>(blockIdx.x) * DR_VB + vl;
+      if (v >= V) {
+        if (lane < DR_MAXP) lt[lane][vl] = -INFINITY;
+        continue;
+      }
+      float acc[PM];
 #pragma unroll
-    for (int j = 0; j < DR_MAXP; ++j) acc[j] = 0.f;
-    for (int c = lane; c < d; c += 64) {
-      const float ev = to_f32(E[v * d + c]);
+      for (int jj = 0; jj < PM; ++jj) acc[jj] = 0.f;
+      for (int c = lane; c < d; c += 64) {
+        const float ev = to_f32(E[v * d + c]);
 #pragma unroll
-      for (int j = 0; j < DR_MAXP; ++j)
-        if (j < P) acc[j] = fmaf(ev, hs[j * d + c], acc[j]);
-    }
+        for (int jj = 0; jj < PM; ++jj)
+          if (jj < P) acc[jj] = fmaf(ev, hs[jj * d + c], acc[jj]);
+      }
 #pragma unroll
-    for (int j = 0; j < DR_MAXP; ++j) {
-      if (j < P) {
-        const float a = wave_sum(acc[j]);
-        if (lane == 0) {
-          lt[j][vl] = a;
-          logits[static_cast<int64_t>(j) * V + v] = a;
+      for (int jj = 0; jj < PM; ++jj) {
+        if (jj < P) {
+          const float a = wave_sum(acc[jj]);
+          if (lane == 0) {
+            lt[jj][vl] = a;
+            logits[static_cast<int64_t>(jj) * V + v] = a;
+          }
         }
       }
     }
@@ -563,13 +661,15 @@ __global__ __launch_bounds__(256) void k_draft_select(lng_drafter D, int32_t K, 
                                                       float kappa, const float* __restrict__ logits,
                                                       const float* __restrict__ lpart, const int32_t* __restrict__ w,
                                                       int32_t ld_w, int32_t* __restrict__ sc, DrChildren C,
-                                                      int64_t* __restrict__ ids, float* __restrict__ scores) {
+                                                      int64_t* __restrict__ ids, float* __restrict__ scores,
+                                                      const int32_t* __restrict__ need) {
   __shared__ float redf[4];
   __shared__ float bvs[4];
   __shared__ int bis[4];
   __shared__ int64_t sel_id[DR_MAXK];
   __shared__ float sel_sc[DR_MAXK];
   const int j = blockIdx.x;
+  if (need && !need[j]) return;  // the shortlist drafted this position
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const float* lp = lpart + static_cast<int64_t>(j) * nblk * (2 + 2 * K);
   // global max and sum of exponentials
@@ -619,7 +719,7 @@ __global__ __launch_bounds__(256) void k_draft_select(lng_drafter D, int32_t K, 
       overflow = 1;
       break;
     }
-    a_val[na] = score_of(id, 0.f);
+    a_val[na] = mix ? score_of(id, 0.f) : lp[b * (2 + 2 * K) + 2 + k];
     a_id[na] = id;
     ++na;
   }
@@ -710,11 +810,16 @@ __global__ __launch_bounds__(256) void k_draft_select(lng_drafter D, int32_t K, 
 // their order.  The drafts are the top-k of the candidates' logits, ties in candidate order (a
 // stable descending sort); an empty list scores the whole vocabulary.  One block per position:
 // the slots (n_orders * R * K <= 8192) are summed per token in an LDS hash table (open addressing
-// keyed by token id, 64-bit totals), then the list is taken one maximum at a time.
+// keyed by token id, 64-bit totals, 2^tbits >= n_orders * R * K slots).  The list is cut by an
+// exact radix select, 8 bits per pass from the top, on the key total << idbits | (2^idbits - 1 -
+// id): it orders like (total desc, id asc) and is unique per token, so the keys at or above the
+// selected threshold are exactly the list, which is then ranked.  Totals too wide for that key
+// (above 2^(64 - idbits)) take the list one maximum at a time instead.
 constexpr int SL_SLOTS = 8192;
 constexpr int SL_MAXCAP = 256;
 constexpr int SL_MAXFB = 1024;
 constexpr int SL_MAXR = 256;
+constexpr int SL_LOADS = 8;  // sketch slots each thread has in flight
 constexpr int32_t SL_EMPTY = -1;
 constexpr int32_t SL_TAKEN = 0x40000000;  // flag on a slot's id once the token is in the list
 
@@ -723,10 +828,11 @@ struct SlArgs {
   const int64_t* counts[DR_MAXN];  // same shape: counts (0 = empty slot)
   const int32_t* fallback;
   int32_t K, cap, n_fallback;
+  int32_t tbits;                   // log2 of the hash table's slots (8 .. 13)
 };
 
-__device__ __forceinline__ uint32_t sl_hash(int32_t id) {
-  return (static_cast<uint32_t>(id) * 2654435761u) >> (32 - 13);  // 13 bits: SL_SLOTS
+__device__ __forceinline__ uint32_t sl_hash(int32_t id, int tbits) {
+  return (static_cast<uint32_t>(id) * 2654435761u) >> (32 - tbits);
 }
 
 // (total, id) a beats (total b, id b): larger total, then smaller id
@@ -734,102 +840,291 @@ __device__ __forceinline__ bool sl_better(unsigned long long ta, int32_t ia, uns
   return ta > tb || (ta == tb && ia < ib);
 }
 
+// Logits of candidates ids[0 .. n) against the normalised hidden state hn (LDS, d floats, d % 8
+// == 0): wave w scores candidates 4w .. 4w+3, 4w+16 .., four rows in flight per lane.
+template <typename TE>
+__device__ void sl_score(const lng_drafter& D, const int32_t* ids, int n, const float* hn, float* out) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int d = D.d, d8 = d >> 3;
+  const TE* E = static_cast<const TE*>(D.emb);
+  for (int i0 = 4 * w; i0 < n; i0 += 16) {
+    int32_t id[4];
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) id[u] = i0 + u < n ? ids[i0 + u] : -1;
+    for (int c8 = lane; c8 < d8; c8 += 64) {
+      const f32x4 h0 = *reinterpret_cast<const f32x4*>(hn + 8 * c8);
+      const f32x4 h1 = *reinterpret_cast<const f32x4*>(hn + 8 * c8 + 4);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (id[u] < 0) continue;
+        f32x4 a, b;
+        ld8f<TE>(E + static_cast<int64_t>(id[u]) * d + 8 * c8, a, b);
+        acc[u] = dot4(b, h1, dot4(a, h0, acc[u]));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float s = wave_sum(acc[u]);
+      if (lane == 0 && i0 + u < n) out[i0 + u] = id[u] >= 0 ? s : -INFINITY;
+    }
+  }
+}
+
+// FROM_HID = false: the candidates' logits are read from the full-vocabulary logits [P, V] and an
+// empty list keeps the full-vocabulary top-k (full_ids / full_sc).  FROM_HID = true: the
+// candidates are scored here from the readout's hidden state hid [P, d] (RMSNorm * out_norm, then
+// E[id] . h); a position whose list is empty gets need_full[j] = 1 and no outputs (the
+// full-vocabulary kernels that follow write them), every other position need_full[j] = 0.
+template <typename TE, bool FROM_HID>
 __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W, SlArgs S,
                                                          const float* __restrict__ logits,
                                                          const int64_t* __restrict__ full_ids,
-                                                         const float* __restrict__ full_sc, int32_t K, DrChildren C,
+                                                         const float* __restrict__ full_sc,
+                                                         const float* __restrict__ hid, int32_t K, DrChildren C,
                                                          int64_t* __restrict__ ids, float* __restrict__ scores,
-                                                         int32_t* __restrict__ sl_out, float* __restrict__ sll_out) {
+                                                         int32_t* __restrict__ sl_out, float* __restrict__ sll_out,
+                                                         int32_t* __restrict__ need_full) {
   __shared__ int32_t hkey[SL_SLOTS];
   __shared__ unsigned long long hval[SL_SLOTS];
   __shared__ int64_t rowsh[DR_MAXN][SL_MAXR];
   __shared__ int32_t fb[SL_MAXFB];
   __shared__ int32_t sl[SL_MAXCAP];
   __shared__ float sll[SL_MAXCAP];
+  __shared__ unsigned long long selk[SL_MAXCAP];
+  __shared__ int32_t hist[256];
   __shared__ int32_t slot_rows[DR_MAXN];
+  __shared__ const int32_t* idp[DR_MAXN];
+  __shared__ const int64_t* cnp[DR_MAXN];
   __shared__ unsigned long long red_t[4];
   __shared__ int32_t red_i[4], red_s[4];
+  __shared__ int32_t rad[4];  // selected digit, keys above it, keys in it; list length
+  __shared__ float red_f[4];
   __shared__ int64_t sel_id[DR_MAXK];
   __shared__ float sel_sc[DR_MAXK];
+  __shared__ __attribute__((aligned(16))) float hn[FROM_HID ? LNG_DR_MAX_D : 4];
   const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int L = *D.length;
-  const int R = D.R, SK = S.K, cap = S.cap;
-  for (int e = tid; e < SL_SLOTS; e += 256) {
+  const int R = D.R, SK = S.K, cap = S.cap, tb = S.tbits, TS = 1 << tb, TM = TS - 1;
+  for (int e = tid; e < TS; e += 256) {
     hkey[e] = SL_EMPTY;
     hval[e] = 0ull;
   }
   for (int e = tid; e < S.n_fallback; e += 256) fb[e] = S.fallback[e];
   if (tid < DR_MAXN) slot_rows[tid] = tid < D.maxn ? dr_resolve(W.slot[j][tid], L) : -1;
+  if (tid == 0) {
+#pragma unroll
+    for (int o = 0; o < DR_MAXN; ++o) {
+      idp[o] = S.ids[o];
+      cnp[o] = S.counts[o];
+    }
+  }
   __syncthreads();
   for (int e = tid; e < D.n_orders * R; e += 256) {
     const int o = e / R, r = e % R;
-    rowsh[o][r] = S.ids[o] ? dr_row(D, slot_rows, o, r) : -1;
+    rowsh[o][r] = idp[o] ? dr_row(D, slot_rows, o, r) : -1;
   }
   __syncthreads();
-  // sum the counts per token (at most SL_SLOTS distinct tokens: every probe sequence ends)
-  const int M = D.n_orders * R * SK;
-  for (int e = tid; e < M; e += 256) {
-    const int o = e / (R * SK), rem = e % (R * SK), r = rem / SK, q = rem % SK;
-    const int64_t row = rowsh[o][r];
-    if (row < 0) continue;
-    const int64_t cnt = S.counts[o][row * SK + q];
-    const int32_t id = S.ids[o][row * SK + q];
-    if (cnt <= 0 || id < 0 || id >= D.V) continue;
-    uint32_t h = sl_hash(id);
-    for (;;) {
-      const int32_t prev = atomicCAS(&hkey[h], SL_EMPTY, id);
-      if (prev == SL_EMPTY || prev == id) break;
-      h = (h + 1) & (SL_SLOTS - 1);
+  // sum the counts per token, SL_LOADS slots in flight per thread (at most TS distinct tokens:
+  // every probe sequence ends)
+  const int RS = R * SK, M = D.n_orders * RS;
+  for (int e0 = 0; e0 < M; e0 += 256 * SL_LOADS) {
+    int32_t idv[SL_LOADS];
+    int64_t cv[SL_LOADS];
+#pragma unroll
+    for (int u = 0; u < SL_LOADS; ++u) {
+      const int e = e0 + u * 256 + tid;
+      idv[u] = -1;
+      cv[u] = 0;
+      if (e < M) {
+        const int o = e / RS, rem = e - o * RS, r = rem / SK, q = rem - r * SK;
+        const int64_t row = rowsh[o][r];
+        if (row >= 0) {
+          cv[u] = cnp[o][row * SK + q];
+          idv[u] = idp[o][row * SK + q];
+        }
+      }
     }
-    atomicAdd(&hval[h], static_cast<unsigned long long>(cnt));
+#pragma unroll
+    for (int u = 0; u < SL_LOADS; ++u) {
+      const int32_t id = idv[u];
+      if (cv[u] <= 0 || id < 0 || id >= D.V) continue;
+      uint32_t h = sl_hash(id, tb);
+      for (;;) {
+        const int32_t prev = atomicCAS(&hkey[h], SL_EMPTY, id);
+        if (prev == SL_EMPTY || prev == id) break;
+        h = (h + 1) & TM;
+      }
+      atomicAdd(&hval[h], static_cast<unsigned long long>(cv[u]));
+    }
   }
   __syncthreads();
-  // the list: one maximum of (total desc, id asc) at a time
+  // the list: distinct tokens and their largest total
+  const int SPT = TS >> 8;  // slots per thread, 1 .. 32
+  unsigned long long tmax = 0ull;
+  int cnt = 0;
+  for (int q = 0; q < SPT; ++q) {
+    const int e = tid + (q << 8);
+    if (hkey[e] >= 0) {
+      tmax = hval[e] > tmax ? hval[e] : tmax;
+      ++cnt;
+    }
+  }
+  for (int off = 32; off >= 1; off >>= 1) {
+    const unsigned long long ot = __shfl_xor(tmax, off, 64);
+    tmax = ot > tmax ? ot : tmax;
+    cnt += __shfl_xor(cnt, off, 64);
+  }
+  if (lane == 0) {
+    red_t[w] = tmax;
+    red_i[w] = cnt;
+  }
+  __syncthreads();
+  tmax = red_t[0];
+  cnt = red_i[0];
+  for (int q = 1; q < 4; ++q) {
+    tmax = red_t[q] > tmax ? red_t[q] : tmax;
+    cnt += red_i[q];
+  }
+  const int ib = D.V > 1 ? 32 - __clz(D.V - 1) : 1;  // bits of a token id
+  const int nb = (tmax ? 64 - __clzll(static_cast<long long>(tmax)) : 0) + ib;
   int m = 0;
-  for (; m < cap; ++m) {
-    unsigned long long bt = 0ull;
-    int32_t bi = INT_MAX, bs = -1;
-    for (int e = tid; e < SL_SLOTS; e += 256) {
-      const int32_t k = hkey[e];
-      if (k < 0 || (k & SL_TAKEN)) continue;
-      if (sl_better(hval[e], k, bt, bi)) {
-        bt = hval[e];
-        bi = k;
-        bs = e;
+  if (nb <= 64) {
+    const unsigned long long vmask = (1ull << ib) - 1ull;
+    unsigned long long key[SL_SLOTS / 256];
+#pragma unroll
+    for (int q = 0; q < SL_SLOTS / 256; ++q) {
+      const int e = tid + (q << 8);
+      key[q] = 0ull;
+      if (q < SPT && hkey[e] >= 0)
+        key[q] = (hval[e] << ib) | (vmask - static_cast<unsigned long long>(hkey[e]));
+    }
+    const int want = min(cap, cnt);
+    unsigned long long thr = ~0ull;
+    if (want > 0) {
+      int shift = ((nb + 7) >> 3) * 8 - 8;
+      unsigned long long prefix = 0ull, pmask = 0ull;
+      int rem = want;  // keys still to take among those matching prefix
+      for (;;) {
+        hist[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < SL_SLOTS / 256; ++q) {
+          const unsigned long long k = key[q];
+          if (k && (k & pmask) == prefix) atomicAdd(&hist[static_cast<int>((k >> shift) & 255ull)], 1);
+        }
+        __syncthreads();
+        if (w == 0) {
+          // lane l holds bins 4l .. 4l+3; suf = keys in bins >= 4l (non-increasing in l)
+          const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
+          const int s = (h0 + h1) + (h2 + h3);
+          int suf = s;
+          for (int off = 1; off < 64; off <<= 1) {
+            const int t = __shfl_down(suf, off, 64);
+            if (lane + off < 64) suf += t;
+          }
+          const unsigned long long bal = __ballot(suf >= rem);
+          const int ls = 63 - __clzll(static_cast<long long>(bal));
+          if (lane == ls) {
+            int above = suf - s, b = 4 * lane + 3, hb = h3;
+            if (above + h3 < rem) {
+              above += h3;
+              b = 4 * lane + 2;
+              hb = h2;
+              if (above + h2 < rem) {
+                above += h2;
+                b = 4 * lane + 1;
+                hb = h1;
+                if (above + h1 < rem) {
+                  above += h1;
+                  b = 4 * lane;
+                  hb = h0;
+                }
+              }
+            }
+            rad[0] = b;
+            rad[1] = above;
+            rad[2] = hb;
+          }
+        }
+        __syncthreads();
+        rem -= rad[1];
+        prefix |= static_cast<unsigned long long>(rad[0]) << shift;
+        pmask |= 255ull << shift;
+        if (rad[2] == rem || shift == 0) {  // every key in the digit's bin is taken
+          thr = prefix;
+          break;
+        }
+        shift -= 8;
       }
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-      const unsigned long long ot = __shfl_xor(bt, off, 64);
-      const int32_t oi = __shfl_xor(bi, off, 64), os = __shfl_xor(bs, off, 64);
-      if (sl_better(ot, oi, bt, bi)) {
-        bt = ot;
-        bi = oi;
-        bs = os;
+    if (tid == 0) rad[3] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < SL_SLOTS / 256; ++q) {
+      const unsigned long long k = key[q];
+      if (k && k >= thr) {
+        const int pos = atomicAdd(&rad[3], 1);  // keys are unique: exactly `want` pass
+        if (pos < SL_MAXCAP) selk[pos] = k;
+        hkey[tid + (q << 8)] |= SL_TAKEN;
       }
     }
-    if (lane == 0) {
-      red_t[w] = bt;
-      red_i[w] = bi;
-      red_s[w] = bs;
-    }
     __syncthreads();
-    bt = red_t[0];
-    bi = red_i[0];
-    bs = red_s[0];
-    for (int q = 1; q < 4; ++q)
-      if (sl_better(red_t[q], red_i[q], bt, bi)) {
-        bt = red_t[q];
-        bi = red_i[q];
-        bs = red_s[q];
+    m = min(rad[3], cap);
+    for (int i = tid; i < m; i += 256) {
+      const unsigned long long k = selk[i];
+      int rank = 0;
+      for (int i2 = 0; i2 < m; ++i2) rank += selk[i2] > k ? 1 : 0;
+      sl[rank] = static_cast<int32_t>(vmask - (k & vmask));
+    }
+  } else {
+    // one maximum of (total desc, id asc) at a time
+    for (; m < cap; ++m) {
+      unsigned long long bt = 0ull;
+      int32_t bi = INT_MAX, bs = -1;
+      for (int e = tid; e < TS; e += 256) {
+        const int32_t k = hkey[e];
+        if (k < 0 || (k & SL_TAKEN)) continue;
+        if (sl_better(hval[e], k, bt, bi)) {
+          bt = hval[e];
+          bi = k;
+          bs = e;
+        }
       }
-    __syncthreads();
-    if (bs < 0) break;  // no candidate left (uniform)
-    if (tid == 0) {
-      sl[m] = bi;
-      hkey[bs] = bi | SL_TAKEN;
+      for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned long long ot = __shfl_xor(bt, off, 64);
+        const int32_t oi = __shfl_xor(bi, off, 64), os = __shfl_xor(bs, off, 64);
+        if (sl_better(ot, oi, bt, bi)) {
+          bt = ot;
+          bi = oi;
+          bs = os;
+        }
+      }
+      if (lane == 0) {
+        red_t[w] = bt;
+        red_i[w] = bi;
+        red_s[w] = bs;
+      }
+      __syncthreads();
+      bt = red_t[0];
+      bi = red_i[0];
+      bs = red_s[0];
+      for (int q = 1; q < 4; ++q)
+        if (sl_better(red_t[q], red_i[q], bt, bi)) {
+          bt = red_t[q];
+          bi = red_i[q];
+          bs = red_s[q];
+        }
+      __syncthreads();
+      if (bs < 0) break;  // no candidate left (uniform)
+      if (tid == 0) {
+        sl[m] = bi;
+        hkey[bs] = bi | SL_TAKEN;
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
+  __syncthreads();
   // fallback padding: first occurrences not in the list, in order
   int added = 0;
   for (int f0 = 0; f0 < S.n_fallback && m + added < cap; f0 += 256) {
@@ -840,7 +1135,7 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
       f = fb[jf];
       ok = f >= 0 && f < D.V;
       if (ok) {
-        uint32_t h = sl_hash(f);
+        uint32_t h = sl_hash(f, tb);
         for (;;) {
           const int32_t k = hkey[h];
           if (k == SL_EMPTY) break;
@@ -848,7 +1143,7 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
             ok = !(k & SL_TAKEN);
             break;
           }
-          h = (h + 1) & (SL_SLOTS - 1);
+          h = (h + 1) & TM;
         }
       }
       for (int i = 0; ok && i < jf; ++i) ok = fb[i] != f;
@@ -870,36 +1165,81 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
     __syncthreads();
   }
   const int n_sl = min(cap, m + added);
-  const float* lg = logits + static_cast<int64_t>(j) * D.V;
-  for (int i = tid; i < cap; i += 256) {
-    int32_t id = -1;
-    if (n_sl > 0)
-      id = i < n_sl ? sl[i] : -1;
-    else
-      id = i < D.V ? i : -1;  // empty list: the whole vocabulary, cut to cap
-    const float v = id >= 0 ? lg[id] : -INFINITY;
-    sll[i] = v;
-    if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = id;
-    if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = v;
+  if constexpr (FROM_HID) {
+    const int d = D.d;
+    float ss = 0.f;
+    for (int c = tid; c < d; c += 256) {
+      const float v = hid[static_cast<int64_t>(j) * d + c];
+      hn[c] = v;
+      ss = fmaf(v, v, ss);
+    }
+    ss = block_sum256(ss, red_f);
+    const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + D.draft_eps);
+    for (int c = tid; c < d; c += 256) hn[c] = hn[c] * r * D.out_norm[c];
+    // an empty list reports tokens 0 .. cap-1 with their logits
+    const int nsc = n_sl > 0 ? n_sl : ((sl_out || sll_out) ? min(cap, D.V) : 0);
+    if (n_sl == 0)
+      for (int i = tid; i < nsc; i += 256) sl[i] = i;
+    __syncthreads();
+    sl_score<TE>(D, sl, nsc, hn, sll);
+    __syncthreads();
+    for (int i = tid; i < cap; i += 256) {
+      if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sl[i] : -1;
+      if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sll[i] : -INFINITY;
+    }
+    if (tid == 0) need_full[j] = n_sl == 0 ? 1 : 0;
+    if (n_sl == 0) return;  // the full-vocabulary kernels write this position's drafts (uniform)
+  } else {
+    const float* lg = logits + static_cast<int64_t>(j) * D.V;
+    for (int i = tid; i < cap; i += 256) {
+      int32_t id = -1;
+      if (n_sl > 0)
+        id = i < n_sl ? sl[i] : -1;
+      else
+        id = i < D.V ? i : -1;  // empty list: the whole vocabulary, cut to cap
+      const float v = id >= 0 ? lg[id] : -INFINITY;
+      sll[i] = v;
+      if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = id;
+      if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = v;
+    }
   }
   __syncthreads();
-  if (tid == 0) {
-    if (n_sl == 0) {
-      for (int q = 0; q < K; ++q) {
-        sel_id[q] = full_ids[static_cast<int64_t>(j) * K + q];
-        sel_sc[q] = full_sc[static_cast<int64_t>(j) * K + q];
-      }
-    } else {
-      uint32_t used[SL_MAXCAP / 32] = {};
-      for (int q = 0; q < K; ++q) {
-        int best = -1;
-        for (int i = 0; i < n_sl; ++i) {
-          if ((used[i >> 5] >> (i & 31)) & 1u) continue;
-          if (best < 0 || sll[i] > sll[best]) best = i;  // strict: ties keep candidate order
+  if (n_sl == 0) {
+    if (tid < K) {
+      sel_id[tid] = full_ids[static_cast<int64_t>(j) * K + tid];
+      sel_sc[tid] = full_sc[static_cast<int64_t>(j) * K + tid];
+    }
+  } else if (w == 0) {
+    // top-K of sll[0 .. n_sl) by (logit desc, candidate index asc): lane l holds l, l+64, ..
+    constexpr int NQ = SL_MAXCAP / 64;
+    float v[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) v[q] = lane + 64 * q < n_sl ? sll[lane + 64 * q] : 0.f;
+    unsigned used = 0u;
+    for (int k = 0; k < K; ++k) {
+      float bv = -INFINITY;
+      int bi = INT_MAX;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        const int i = lane + 64 * q;
+        if (i >= n_sl || ((used >> q) & 1u)) continue;
+        if (v[q] > bv || (v[q] == bv && i < bi)) {
+          bv = v[q];
+          bi = i;
         }
-        if (best >= 0) used[best >> 5] |= 1u << (best & 31);
-        sel_id[q] = best >= 0 ? sl[best] : -1;
-        sel_sc[q] = best >= 0 ? sll[best] : -INFINITY;
+      }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (ov > bv || (ov == bv && oi < bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (bi != INT_MAX && (bi & 63) == lane) used |= 1u << (bi >> 6);
+      if (lane == 0) {
+        sel_id[k] = bi == INT_MAX ? -1 : sl[bi];
+        sel_sc[k] = bi == INT_MAX ? -INFINITY : bv;
       }
     }
   }
@@ -2781,9 +3121,398 @@ __global__ __launch_bounds__(TP_THREADS) void k_tree_persist(lng_drafter D, Tree
 // ------------------------------------------------------------------ host side
 namespace {
 
+// ------------------------------------------------------------------ small-batch readout and advance
+// The per-token launches of a chain draft (at most SM_P positions): one weight row per wave, its
+// 16-byte loads issued before the block stages the inputs, so each launch has hundreds of blocks
+// with their row loads in flight (the general kernels above amortise rows over 16 positions).
+constexpr int SM_P = 4;       // positions
+constexpr int SM_RC = 8;      // routes per attention block
+constexpr int SM_MAXCH = 32;  // attention blocks per position (R <= 256)
+
+__device__ __forceinline__ const void* dr_table(const lng_drafter& D, int oi) {
+  return oi == 0 ? D.tables[0] : (oi == 1 ? D.tables[1] : (oi == 2 ? D.tables[2] : D.tables[3]));
+}
+
+// qkw[j, o] = r_j * QK[o] . e_j (+ QKS[o] . s_j); wave w of block b computes row o = 4b + w, wave j
+// stages position j's embedding row and RMS factor.              grid (cdiv(QH*Dt, 4))
+__global__ __launch_bounds__(256) void k_sm_qkw(lng_drafter D, DrWin W, float* __restrict__ qkw) {
+  __shared__ __attribute__((aligned(16))) float es[SM_P][LNG_DR_MAX_D];
+  __shared__ __attribute__((aligned(16))) float ss[SM_P][LNG_DR_MAX_N];
+  __shared__ float rj[SM_P];
+  constexpr int NQ = LNG_DR_MAX_D / 256;
+  const int d = D.d, d4 = d >> 2, P = W.n, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int N = D.query_ssm ? D.ssm_dim : 0, QD = D.q_heads * D.dt;
+  const int o = blockIdx.x * 4 + w;
+  const bool live = o < QD;
+  f32x4 wq[NQ];
+  const f32x4* qr = reinterpret_cast<const f32x4*>(D.qk + static_cast<int64_t>(live ? o : 0) * d);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+    wq[q] = (live && lane + 64 * q < d4) ? qr[lane + 64 * q] : f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 wsq = {0.f, 0.f, 0.f, 0.f};
+  if (live && lane < (N >> 2)) wsq = reinterpret_cast<const f32x4*>(D.qks + static_cast<int64_t>(o) * N)[lane];
+  const int L = *D.length;
+  if (w < P) {
+    const int32_t row = dr_resolve(W.slot[w][D.maxn - 1], L);
+    const int64_t tok = row >= 0 ? D.tokens[row] : -1;
+    const bool ok = dr_tok_ok(D, tok);
+    float sq = 0.f;
+    for (int c4 = lane; c4 < d4; c4 += 64) {
+      const f32x4 v = ok ? ld4_any(D.emb, D.emb_dtype, tok * d + 4 * c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<f32x4*>(&es[w][4 * c4]) = v;
+      sq = dot4(v, v, sq);
+    }
+    sq = wave_sum(sq);
+    if (lane == 0) rj[w] = 1.0f / sqrtf(sq / static_cast<float>(d) + D.draft_eps);
+    for (int c = lane; c < N; c += 64) ss[w][c] = row >= 0 ? D.ssm[static_cast<int64_t>(row) * D.ssm_dim + c] : 0.f;
+  }
+  __syncthreads();
+  if (!live) return;
+  float acc[SM_P] = {0.f, 0.f, 0.f, 0.f}, accs[SM_P] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int c4 = lane + 64 * q;
+    if (c4 < d4) {
+#pragma unroll
+      for (int jj = 0; jj < SM_P; ++jj)
+        if (jj < P) acc[jj] = dot4(wq[q], *reinterpret_cast<const f32x4*>(&es[jj][4 * c4]), acc[jj]);
+    }
+  }
+  if (lane < (N >> 2)) {
+#pragma unroll
+    for (int jj = 0; jj < SM_P; ++jj)
+      if (jj < P) accs[jj] = dot4(wsq, *reinterpret_cast<const f32x4*>(&ss[jj][4 * lane]), accs[jj]);
+  }
+#pragma unroll
+  for (int jj = 0; jj < SM_P; ++jj) {
+    if (jj >= P) break;
+    const float a = wave_sum(acc[jj]);
+    const float b = wave_sum(accs[jj]);
+    if (lane == 0) qkw[static_cast<int64_t>(jj) * QD + o] = rj[jj] * a + b;
+  }
+}
+
+// Partial sink-free softmax of position j over SM_RC routes for every query head, then the last
+// block of the position merges the chunks with the sink into u[j] [QH * Dt]:
+//   part_u [((j * nch + c) * QH + qh) * Dt + i], part_ml [((j * nch + c) * QH + qh) * 2 + {0, 1}] = (m, l)
+// (device-coherent hand-off; sync[SY_ATT + j] counts the blocks).       grid (nch, P)
+__global__ __launch_bounds__(256) void k_sm_attend(lng_drafter D, DrWin W, const float* __restrict__ qkw,
+                                                   float* __restrict__ part_u, float* __restrict__ part_ml,
+                                                   float* __restrict__ u) {
+  __shared__ __attribute__((aligned(16))) float xs[SM_RC][LNG_DR_MAX_DT];
+  __shared__ __attribute__((aligned(16))) float qs[LNG_DR_MAX_QH * LNG_DR_MAX_DT];
+  __shared__ float sxs[SM_RC];
+  __shared__ float sc[LNG_DR_MAX_QH][SM_RC];
+  __shared__ int64_t rowsh[SM_RC][DR_MAXN];
+  __shared__ int32_t slot_rows[DR_MAXN];
+  __shared__ float mls[LNG_DR_MAX_QH][SM_MAXCH][2];
+  __shared__ float scl[LNG_DR_MAX_QH][SM_MAXCH];
+  __shared__ int last_flag;
+  const int j = blockIdx.y, c = blockIdx.x, nch = gridDim.x;
+  const int L = *D.length;
+  const int Dt = D.dt, D4 = Dt >> 2, QH = D.q_heads, md = D.mem_dim, QD = QH * Dt;
+  const int r0 = c * SM_RC, nr = min(SM_RC, D.R - r0);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  if (threadIdx.x < DR_MAXN) slot_rows[threadIdx.x] = threadIdx.x < D.maxn ? dr_resolve(W.slot[j][threadIdx.x], L) : -1;
+  const float* qv = qkw + static_cast<int64_t>(j) * QD;
+  for (int e = threadIdx.x; e < (QD >> 2); e += 256)
+    reinterpret_cast<f32x4*>(qs)[e] = reinterpret_cast<const f32x4*>(qv)[e];
+  __syncthreads();
+  if (threadIdx.x < nr * D.n_orders) {
+    const int rr = threadIdx.x / D.n_orders, oi = threadIdx.x % D.n_orders;
+    rowsh[rr][oi] = dr_row(D, slot_rows, oi, r0 + rr);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < nr * D4; e += 256) {
+    const int rr = e / D4, i = 4 * (e % D4), oi = i / md;
+    const int64_t row = rowsh[rr][oi];
+    *reinterpret_cast<f32x4*>(&xs[rr][i]) =
+        row >= 0 ? ld4_any(dr_table(D, oi), D.table_dtype, row * md + (i % md)) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  for (int rr = w; rr < nr; rr += 4) {
+    float ss = 0.f;
+    for (int i = lane; i < Dt; i += 64) ss = fmaf(xs[rr][i], xs[rr][i], ss);
+    ss = wave_sum(ss);
+    const float s = 1.0f / sqrtf(ss / static_cast<float>(Dt) + D.mem_eps);
+    if (lane == 0) sxs[rr] = s;
+    for (int qh = 0; qh < QH; ++qh) {
+      float a = 0.f;
+      for (int i = lane; i < Dt; i += 64) a = fmaf(qs[qh * Dt + i], xs[rr][i], a);
+      a = wave_sum(a);
+      if (lane == 0) sc[qh][rr] = s * a;
+    }
+  }
+  __syncthreads();
+  const uint32_t nrec = gridDim.y * static_cast<uint32_t>(nch) * QH;
+  const __amdgpu_buffer_rsrc_t ru = dev_buf(part_u, nrec * static_cast<uint32_t>(Dt) * 4u);
+  for (int e = threadIdx.x; e < QH * D4; e += 256) {
+    const int qh = e / D4, i = 4 * (e % D4);
+    float m = -INFINITY;
+    for (int rr = 0; rr < nr; ++rr) m = fmaxf(m, sc[qh][rr]);
+    float l = 0.f;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int rr = 0; rr < nr; ++rr) {
+      const float p = expf(sc[qh][rr] - m);
+      l += p;
+      const float ps = p * sxs[rr];
+      const f32x4 x = *reinterpret_cast<const f32x4*>(&xs[rr][i]);
+      acc.x = fmaf(ps, x.x, acc.x);
+      acc.y = fmaf(ps, x.y, acc.y);
+      acc.z = fmaf(ps, x.z, acc.z);
+      acc.w = fmaf(ps, x.w, acc.w);
+    }
+    const uint32_t rec = (static_cast<uint32_t>(j) * nch + c) * QH + qh;
+    st_dev4(ru, 4u * (rec * Dt + i), acc);
+    if (i == 0) {
+      st_dev(&part_ml[2 * rec], m);
+      st_dev(&part_ml[2 * rec + 1], l);
+    }
+  }
+  if (!dr_last_block(&D.sync[SY_ATT + j], nch, &last_flag)) return;
+  // merge: per head the sink-seeded normaliser and each chunk's weight
+  for (int e = threadIdx.x; e < QH * nch; e += 256) {
+    const int qh = e / nch, cc = e % nch;
+    const uint32_t rec = (static_cast<uint32_t>(j) * nch + cc) * QH + qh;
+    mls[qh][cc][0] = ld_dev(&part_ml[2 * rec]);
+    mls[qh][cc][1] = ld_dev(&part_ml[2 * rec + 1]);
+  }
+  __syncthreads();
+  if (threadIdx.x < QH) {
+    const int qh = threadIdx.x;
+    const float b0 = D.sink_logit;
+    float M = b0;
+    for (int cc = 0; cc < nch; ++cc) M = fmaxf(M, mls[qh][cc][0]);
+    float l = expf(b0 - M);
+    for (int cc = 0; cc < nch; ++cc) {
+      const float f = expf(mls[qh][cc][0] - M);
+      l = fmaf(mls[qh][cc][1], f, l);
+      scl[qh][cc] = f;
+    }
+    for (int cc = 0; cc < nch; ++cc) scl[qh][cc] /= l;
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < QH * D4; e += 256) {
+    const int qh = e / D4, i = 4 * (e % D4);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int c0 = 0; c0 < nch; c0 += 8) {
+      f32x4 v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const uint32_t rec = (static_cast<uint32_t>(j) * nch + c0 + q) * QH + qh;
+        v[q] = c0 + q < nch ? ld_dev4(ru, 4u * (rec * Dt + i)) : f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        if (c0 + q >= nch) break;
+        const float f = scl[qh][c0 + q];
+        acc.x = fmaf(v[q].x, f, acc.x);
+        acc.y = fmaf(v[q].y, f, acc.y);
+        acc.z = fmaf(v[q].z, f, acc.z);
+        acc.w = fmaf(v[q].w, f, acc.w);
+      }
+    }
+    *reinterpret_cast<f32x4*>(u + static_cast<int64_t>(j) * QD + qh * Dt + i) = acc;
+  }
+}
+
+// hid[j, o] = OV[o] . u_j, one row per wave.                          grid (cdiv(d, 4))
+__global__ __launch_bounds__(256) void k_sm_hidden(lng_drafter D, int32_t P, const float* __restrict__ u,
+                                                   float* __restrict__ hid) {
+  extern __shared__ __attribute__((aligned(16))) float us[];  // [P][QD]
+  constexpr int NQ = LNG_DR_MAX_QH * LNG_DR_MAX_DT / 256;
+  const int QD = D.q_heads * D.dt, Q4 = QD >> 2, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int o = blockIdx.x * 4 + w;
+  const bool live = o < D.d;
+  f32x4 wv[NQ];
+  const f32x4* wr = reinterpret_cast<const f32x4*>(D.ov + static_cast<int64_t>(live ? o : 0) * QD);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) wv[q] = (live && lane + 64 * q < Q4) ? wr[lane + 64 * q] : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int e = threadIdx.x; e < P * Q4; e += 256) reinterpret_cast<f32x4*>(us)[e] = reinterpret_cast<const f32x4*>(u)[e];
+  __syncthreads();
+  if (!live) return;
+  float acc[SM_P] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int c4 = lane + 64 * q;
+    if (c4 < Q4) {
+#pragma unroll
+      for (int jj = 0; jj < SM_P; ++jj)
+        if (jj < P) acc[jj] = dot4(wv[q], reinterpret_cast<const f32x4*>(us)[jj * Q4 + c4], acc[jj]);
+    }
+  }
+#pragma unroll
+  for (int jj = 0; jj < SM_P; ++jj) {
+    if (jj >= P) break;
+    const float a = wave_sum(acc[jj]);
+    if (lane == 0) hid[static_cast<int64_t>(jj) * D.d + o] = a;
+  }
+}
+
+// SSM step of up to SM_P positions in one launch: u_j[n] = W_in[n] . (RMSNorm(E[tok_j]) *
+// ssm_norm), then s[row_j][n] = a_n s[prev_j][n] + (1 - a_n) u_j[n] in position order (a chain in
+// the batch reads the state the same lane wrote for the earlier position).  One channel per wave.
+//                                                                   grid (cdiv(N, 4))
+__global__ __launch_bounds__(256) void k_sm_ssm(lng_drafter D, DrAdv A) {
+  __shared__ __attribute__((aligned(16))) float xs[SM_P][LNG_DR_MAX_D];
+  constexpr int NQ = LNG_DR_MAX_D / 256;
+  const int d = D.d, d4 = d >> 2, N = D.ssm_dim, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int n = blockIdx.x * 4 + w;
+  const bool live = n < N;
+  f32x4 wq[NQ];
+  const f32x4* wr = reinterpret_cast<const f32x4*>(D.ssm_w_in + static_cast<int64_t>(live ? n : 0) * d);
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+    wq[q] = (live && lane + 64 * q < d4) ? wr[lane + 64 * q] : f32x4{0.f, 0.f, 0.f, 0.f};
+  const int L = *D.length;
+  if (w < A.n) {
+    const int32_t row = A.range ? A.base + w : dr_resolve(A.row[w], L);
+    const int64_t tok = row >= 0 ? D.tokens[row] : -1;
+    const bool ok = dr_tok_ok(D, tok);
+    float sq = 0.f;
+    for (int c4 = lane; c4 < d4; c4 += 64) {
+      const f32x4 v = ok ? ld4_any(D.emb, D.emb_dtype, tok * d + 4 * c4) : f32x4{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<f32x4*>(&xs[w][4 * c4]) = v;
+      sq = dot4(v, v, sq);
+    }
+    sq = wave_sum(sq);
+    const float r = 1.0f / sqrtf(sq / static_cast<float>(d) + D.ssm_eps);
+    for (int c4 = lane; c4 < d4; c4 += 64) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(&xs[w][4 * c4]);
+      const f32x4 g = reinterpret_cast<const f32x4*>(D.ssm_norm)[c4];
+      v.x = v.x * r * g.x;
+      v.y = v.y * r * g.y;
+      v.z = v.z * r * g.z;
+      v.w = v.w * r * g.w;
+      *reinterpret_cast<f32x4*>(&xs[w][4 * c4]) = v;
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  float acc[SM_P] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int c4 = lane + 64 * q;
+    if (c4 < d4) {
+#pragma unroll
+      for (int jj = 0; jj < SM_P; ++jj)
+        if (jj < A.n) acc[jj] = dot4(wq[q], *reinterpret_cast<const f32x4*>(&xs[jj][4 * c4]), acc[jj]);
+    }
+  }
+  float uj[SM_P];
+#pragma unroll
+  for (int jj = 0; jj < SM_P; ++jj) uj[jj] = jj < A.n ? wave_sum(acc[jj]) : 0.f;
+  if (lane == 0) {
+    const float a = D.ssm_decay[n];
+#pragma unroll
+    for (int jj = 0; jj < SM_P; ++jj) {
+      if (jj >= A.n) break;
+      const int32_t row = A.range ? A.base + jj : dr_resolve(A.row[jj], L);
+      const int32_t pv = A.range ? (jj == 0 ? dr_resolve(A.prev0, L) : A.base + jj - 1) : dr_resolve(A.prev[jj], L);
+      if (row < 0) continue;
+      const float sp = pv >= 0 ? D.ssm[static_cast<int64_t>(pv) * N + n] : 0.f;
+      D.ssm[static_cast<int64_t>(row) * N + n] = a * sp + (1.f - a) * uj[jj];
+    }
+  }
+}
+
+// Router codes of up to SM_P positions, one route per block: wave b < bits computes bit b's logit
+// router[r*bits + b] . f_j, f_j = concat(RMSNorm(E[prev_j] or start) * prev_norm,
+// RMSNorm(E[tok_j]) * cur_norm [, s[row_j]]) (F = 2d (+N) floats per position in LDS).  grid (R)
+template <typename TR>
+__global__ __launch_bounds__(256) void k_sm_codes(lng_drafter D, DrAdv A) {
+  extern __shared__ __attribute__((aligned(16))) float fs[];  // [n][F]
+  __shared__ float lg[SM_P][4];
+  __shared__ int32_t rows[SM_P];
+  constexpr int NQ = (2 * LNG_DR_MAX_D + LNG_DR_MAX_N + 511) / 512;
+  const int d = D.d, d4 = d >> 2, N = D.router_ssm ? D.ssm_dim : 0, F = 2 * d + N, F8 = F >> 3;
+  const int r = blockIdx.x, bits = D.bits, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const bool live = w < bits;
+  const TR* wrow = static_cast<const TR*>(D.router) + (static_cast<int64_t>(r) * bits + (live ? w : 0)) * F;
+  f32x4 wa[NQ], wb[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (live && lane + 64 * q < F8) {
+      ld8f<TR>(wrow + 8 * (lane + 64 * q), wa[q], wb[q]);
+    } else {
+      wa[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+      wb[q] = wa[q];
+    }
+  }
+  const int L = *D.length;
+  if (threadIdx.x < A.n) {
+    const int jj = threadIdx.x;
+    rows[jj] = A.range ? A.base + jj : dr_resolve(A.row[jj], L);
+  }
+  for (int t = w; t < 2 * A.n; t += 4) {
+    const int jj = t >> 1, half = t & 1;
+    const int32_t row = A.range ? A.base + jj : dr_resolve(A.row[jj], L);
+    const int32_t pv = A.range ? (jj == 0 ? dr_resolve(A.prev0, L) : A.base + jj - 1) : dr_resolve(A.prev[jj], L);
+    if (row < 0) continue;
+    const bool use_start = half == 0 && pv < 0;
+    const int64_t tk = half == 0 ? (pv >= 0 ? D.tokens[pv] : 0) : D.tokens[row];
+    const bool ok = dr_tok_ok(D, tk);
+    const float* nw = half == 0 ? D.router_prev_norm : D.router_cur_norm;
+    float* f = fs + jj * F + half * d;
+    float sq = 0.f;
+    for (int c4 = lane; c4 < d4; c4 += 64) {
+      const f32x4 v = use_start ? reinterpret_cast<const f32x4*>(D.router_start)[c4]
+                                : (ok ? ld4_any(D.emb, D.emb_dtype, tk * d + 4 * c4) : f32x4{0.f, 0.f, 0.f, 0.f});
+      *reinterpret_cast<f32x4*>(f + 4 * c4) = v;
+      sq = dot4(v, v, sq);
+    }
+    sq = wave_sum(sq);
+    const float rs = 1.0f / sqrtf(sq / static_cast<float>(d) + D.router_eps);
+    for (int c4 = lane; c4 < d4; c4 += 64) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(f + 4 * c4);
+      const f32x4 g = reinterpret_cast<const f32x4*>(nw)[c4];
+      v.x = v.x * rs * g.x;
+      v.y = v.y * rs * g.y;
+      v.z = v.z * rs * g.z;
+      v.w = v.w * rs * g.w;
+      *reinterpret_cast<f32x4*>(f + 4 * c4) = v;
+    }
+  }
+  for (int e = threadIdx.x; e < A.n * N; e += 256) {
+    const int jj = e / N, c = e % N;
+    const int32_t row = A.range ? A.base + jj : dr_resolve(A.row[jj], L);
+    fs[jj * F + 2 * d + c] = row >= 0 ? D.ssm[static_cast<int64_t>(row) * D.ssm_dim + c] : 0.f;
+  }
+  __syncthreads();
+  if (live) {
+    float acc[SM_P] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int c8 = lane + 64 * q;
+      if (c8 < F8) {
+#pragma unroll
+        for (int jj = 0; jj < SM_P; ++jj) {
+          if (jj >= A.n) break;
+          const float* f = fs + jj * F + 8 * c8;
+          acc[jj] = dot4(wb[q], *reinterpret_cast<const f32x4*>(f + 4),
+                         dot4(wa[q], *reinterpret_cast<const f32x4*>(f), acc[jj]));
+        }
+      }
+    }
+#pragma unroll
+    for (int jj = 0; jj < SM_P; ++jj) {
+      if (jj >= A.n) break;
+      const float s = wave_sum(acc[jj]);
+      if (lane == 0) lg[jj][w] = s;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x < A.n && rows[threadIdx.x] >= 0) {
+    const int jj = threadIdx.x;
+    int code = 0;
+    for (int b = 0; b < bits; ++b) code |= (lg[jj][b] > 0.f ? 1 : 0) << b;
+    D.codes[static_cast<int64_t>(rows[jj]) * D.R + r] = static_cast<uint8_t>(code);
+  }
+}
+
 struct DrLayout {
-  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, total;
-  int nch, nblk, fnch, fnblk;
+  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, smu, smml, smout, need, total;
+  int nch, nblk, fnch, fnblk, smch;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -2814,8 +3543,25 @@ DrLayout dr_layout(const lng_drafter& D, int P, int K, int max_pairs) {
   l.tot = 0;
   l.flpart = take(sizeof(float) * static_cast<size_t>(P) * l.fnblk * fl_rs<DR_MAXK>());
   l.cand = take(sizeof(int4) * static_cast<size_t>(P) * l.fnblk * FL_VB);
+  l.smch = static_cast<int>(cdiv(D.R, SM_RC));
+  l.smu = take(sizeof(float) * static_cast<size_t>(std::min(P, SM_P)) * l.smch * QD);
+  l.smml = take(sizeof(float) * static_cast<size_t>(std::min(P, SM_P)) * l.smch * D.q_heads * 2);
+  l.smout = take(sizeof(float) * static_cast<size_t>(std::min(P, SM_P)) * QD);
+  l.need = take(sizeof(int32_t) * DR_MAXP);
   l.total = off;
   return l;
+}
+
+// The small-batch kernels apply: at most SM_P positions, 16-byte row loads (d % 8, Dt % 4, mem_dim
+// % 4, N % 8), the block counters of sync, and the codes kernel's features within 64 KB of LDS.
+bool sm_ok(const lng_drafter& D, int P) {
+  return P >= 1 && P <= SM_P && D.sync && D.d % 8 == 0 && D.dt % 4 == 0 && D.mem_dim % 4 == 0 &&
+         D.ssm_dim % 8 == 0 && cdiv(D.R, SM_RC) <= SM_MAXCH;
+}
+bool sm_adv_ok(const lng_drafter& D, int n) {
+  const int F = 2 * D.d + (D.router_ssm ? D.ssm_dim : 0);
+  return n >= 1 && n <= SM_P && D.d % 8 == 0 && D.ssm_dim % 8 == 0 && D.bits <= 4 &&
+         static_cast<size_t>(n) * F * sizeof(float) <= 65536;
 }
 
 bool dr_fast(const lng_drafter& D) {
@@ -2857,6 +3603,24 @@ int dr_advance(const lng_drafter& D, const DrAdv& A, int from_router, float* u, 
     return check_launch("drafter_advance(fast codes)");
   }
   const bool has_ssm = D.ssm_dim > 0 && D.ssm && D.ssm_w_in;
+  if (sm_adv_ok(D, A.n)) {
+    if (has_ssm) {
+      hipLaunchKernelGGL(k_sm_ssm, dim3(static_cast<unsigned>(cdiv(D.ssm_dim, 4))), dim3(256), 0, s, D, A);
+      if (int rc = check_launch("drafter_advance(ssm)")) return rc;
+    }
+    if (from_router) {
+      const size_t lds = sizeof(float) * A.n * (2 * D.d + (D.router_ssm ? D.ssm_dim : 0));
+      const dim3 g(static_cast<unsigned>(D.R));
+      if (D.router_dtype == LNG_BF16)
+        hipLaunchKernelGGL(k_sm_codes<bf16>, g, dim3(256), lds, s, D, A);
+      else if (D.router_dtype == LNG_F16)
+        hipLaunchKernelGGL(k_sm_codes<_Float16>, g, dim3(256), lds, s, D, A);
+      else
+        hipLaunchKernelGGL(k_sm_codes<float>, g, dim3(256), lds, s, D, A);
+      if (int rc = check_launch("drafter_advance(codes)")) return rc;
+    }
+    return LNG_OK;
+  }
   if (has_ssm) {
     hipLaunchKernelGGL(k_draft_ssm_u, dim3(static_cast<unsigned>(cdiv(D.ssm_dim, 16)), static_cast<unsigned>(cdiv(A.n, 4))),
                        dim3(256), 0, s, D, A, u);
@@ -2923,6 +3687,72 @@ int dr_readout_fast(const lng_drafter& D, const FastLevel& F, int K, int online,
   return check_launch("drafter_readout(fast logits)");
 }
 
+// LDS of the general readout kernels (positions x width) within their 60 KB budget.
+bool dr_lds_ok(const lng_drafter& D, int P) {
+  const int QD = D.q_heads * D.dt;
+  const int Nq = D.query_ssm ? D.ssm_dim : 0;
+  const size_t lim = 60 * 1024;
+  return sizeof(float) * P * (D.d + Nq) <= lim && sizeof(float) * P * QD <= lim && sizeof(float) * P * D.d <= lim;
+}
+
+// The readout of P positions up to the hidden states hid [P, d] (work + l.hid): query-key weights,
+// attention over the routes, output projection.
+int dr_front(const lng_drafter& D, const DrWin& W, const DrLayout& l, char* work, hipStream_t s) {
+  const int P = W.n, QD = D.q_heads * D.dt;
+  const int Nq = D.query_ssm ? D.ssm_dim : 0;
+  float* qkw = reinterpret_cast<float*>(work + l.qkw);
+  float* hid = reinterpret_cast<float*>(work + l.hid);
+  if (sm_ok(D, P)) {
+    float* pu = reinterpret_cast<float*>(work + l.smu);
+    float* pml = reinterpret_cast<float*>(work + l.smml);
+    float* uo = reinterpret_cast<float*>(work + l.smout);
+    hipLaunchKernelGGL(k_sm_qkw, dim3(static_cast<unsigned>(cdiv(QD, 4))), dim3(256), 0, s, D, W, qkw);
+    if (int rc = check_launch("drafter_readout(qkw)")) return rc;
+    hipLaunchKernelGGL(k_sm_attend, dim3(static_cast<unsigned>(l.smch), static_cast<unsigned>(P)), dim3(256), 0, s, D,
+                       W, qkw, pu, pml, uo);
+    if (int rc = check_launch("drafter_readout(attend)")) return rc;
+    hipLaunchKernelGGL(k_sm_hidden, dim3(static_cast<unsigned>(cdiv(D.d, 4))), dim3(256), sizeof(float) * P * QD, s, D,
+                       P, uo, hid);
+    return check_launch("drafter_readout(hidden)");
+  }
+  float* part = reinterpret_cast<float*>(work + l.part);
+  const size_t lds_q = sizeof(float) * P * (D.d + Nq);
+  const size_t lds_h = sizeof(float) * P * QD;
+  hipLaunchKernelGGL(k_draft_qkw, dim3(static_cast<unsigned>(cdiv(QD, 32))), dim3(256), lds_q, s, D, W, qkw);
+  if (int rc = check_launch("drafter_readout(qkw)")) return rc;
+  hipLaunchKernelGGL(k_draft_attend, dim3(static_cast<unsigned>(l.nch), static_cast<unsigned>(P)), dim3(256), 0, s, D,
+                     W, qkw, part);
+  if (int rc = check_launch("drafter_readout(attend)")) return rc;
+  hipLaunchKernelGGL(k_draft_hidden, dim3(static_cast<unsigned>(cdiv(D.d, 16))), dim3(256), lds_h, s, D, P, l.nch, part,
+                     hid);
+  return check_launch("drafter_readout(hidden)");
+}
+
+// Full-vocabulary logits (logits_out, else the workspace) and the top-k of P positions from their
+// hidden states; need (optional, [P]): only the positions with need[j] != 0 are drafted.
+int dr_vocab(const lng_drafter& D, int P, int K, int online, float kappa, const DrChildren& C, const DrLayout& l,
+             char* work, int max_pairs, int32_t* counts, int64_t* ids, float* scores, float* logits_out,
+             const int32_t* need, hipStream_t s) {
+  const float* hid = reinterpret_cast<const float*>(work + l.hid);
+  float* logits = logits_out ? logits_out : reinterpret_cast<float*>(work + l.logits);
+  float* lpart = reinterpret_cast<float*>(work + l.lpart);
+  const int32_t* wbuf = reinterpret_cast<const int32_t*>(work + l.w);
+  const size_t lds_l = sizeof(float) * P * D.d;
+  const dim3 g(static_cast<unsigned>(l.nblk));
+  auto launch = [&](auto kern) { hipLaunchKernelGGL(kern, g, dim3(256), lds_l, s, D, P, K, hid, logits, lpart, need); };
+  const bool small = P <= SM_P;
+  if (D.emb_dtype == LNG_BF16)
+    small ? launch(k_draft_logits<bf16, SM_P>) : launch(k_draft_logits<bf16, DR_MAXP>);
+  else if (D.emb_dtype == LNG_F16)
+    small ? launch(k_draft_logits<_Float16, SM_P>) : launch(k_draft_logits<_Float16, DR_MAXP>);
+  else
+    small ? launch(k_draft_logits<float, SM_P>) : launch(k_draft_logits<float, DR_MAXP>);
+  if (int rc = check_launch("drafter_readout(logits)")) return rc;
+  hipLaunchKernelGGL(k_draft_select, dim3(static_cast<unsigned>(P)), dim3(256), 0, s, D, K, l.nblk, online, kappa, logits,
+                     lpart, wbuf, max_pairs, counts, C, ids, scores, need);
+  return check_launch("drafter_readout(select)");
+}
+
 int dr_readout(const lng_drafter& D, const DrWin& W, int K, int online, float kappa, const DrChildren& C,
                char* work, size_t work_bytes, int32_t* counts, int64_t* ids, float* scores, float* logits_out,
                hipStream_t s) {
@@ -2941,45 +3771,15 @@ int dr_readout(const lng_drafter& D, const DrWin& W, int K, int online, float ka
   const DrLayout l = dr_layout(D, P, K, online ? max_pairs : 1);
   if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter: workspace too small");
   if (online && !counts) return fail(LNG_E_ARG, "drafter: online counts need the counts buffer");
-  float* qkw = reinterpret_cast<float*>(work + l.qkw);
-  float* part = reinterpret_cast<float*>(work + l.part);
-  float* hid = reinterpret_cast<float*>(work + l.hid);
-  float* logits = logits_out ? logits_out : reinterpret_cast<float*>(work + l.logits);
-  float* lpart = reinterpret_cast<float*>(work + l.lpart);
-  int32_t* wbuf = reinterpret_cast<int32_t*>(work + l.w);
-  const int QD = D.q_heads * D.dt;
-  const int Nq = D.query_ssm ? D.ssm_dim : 0;
-  const size_t lds_q = sizeof(float) * P * (D.d + Nq);
-  const size_t lds_h = sizeof(float) * P * QD;
-  const size_t lds_l = sizeof(float) * P * D.d;
-  if (lds_q > 60 * 1024 || lds_h > 60 * 1024 || lds_l > 60 * 1024)
-    return fail(LNG_E_ARG, "drafter: too many positions for this width");
-  hipLaunchKernelGGL(k_draft_qkw, dim3(static_cast<unsigned>(cdiv(QD, 32))), dim3(256), lds_q, s, D, W, qkw);
-  if (int rc = check_launch("drafter_readout(qkw)")) return rc;
+  if (!dr_lds_ok(D, P)) return fail(LNG_E_ARG, "drafter: too many positions for this width");
+  if (int rc = dr_front(D, W, l, work, s)) return rc;
   if (online) {
+    int32_t* wbuf = reinterpret_cast<int32_t*>(work + l.w);
     hipLaunchKernelGGL(k_draft_online_match, dim3(static_cast<unsigned>(cdiv(max_pairs, DR_TB)), static_cast<unsigned>(P)),
                        dim3(256), 0, s, D, W, wbuf, counts, max_pairs);
     if (int rc = check_launch("drafter_readout(online)")) return rc;
   }
-  hipLaunchKernelGGL(k_draft_attend, dim3(static_cast<unsigned>(l.nch), static_cast<unsigned>(P)), dim3(256), 0, s, D,
-                     W, qkw, part);
-  if (int rc = check_launch("drafter_readout(attend)")) return rc;
-  hipLaunchKernelGGL(k_draft_hidden, dim3(static_cast<unsigned>(cdiv(D.d, 16))), dim3(256), lds_h, s, D, P, l.nch, part,
-                     hid);
-  if (int rc = check_launch("drafter_readout(hidden)")) return rc;
-  if (D.emb_dtype == LNG_BF16)
-    hipLaunchKernelGGL(k_draft_logits<bf16>, dim3(static_cast<unsigned>(l.nblk)), dim3(256), lds_l, s, D, P, K, hid,
-                       logits, lpart);
-  else if (D.emb_dtype == LNG_F16)
-    hipLaunchKernelGGL(k_draft_logits<_Float16>, dim3(static_cast<unsigned>(l.nblk)), dim3(256), lds_l, s, D, P, K, hid,
-                       logits, lpart);
-  else
-    hipLaunchKernelGGL(k_draft_logits<float>, dim3(static_cast<unsigned>(l.nblk)), dim3(256), lds_l, s, D, P, K, hid,
-                       logits, lpart);
-  if (int rc = check_launch("drafter_readout(logits)")) return rc;
-  hipLaunchKernelGGL(k_draft_select, dim3(static_cast<unsigned>(P)), dim3(256), 0, s, D, K, l.nblk, online, kappa, logits,
-                     lpart, wbuf, max_pairs, counts, C, ids, scores);
-  return check_launch("drafter_readout(select)");
+  return dr_vocab(D, P, K, online, kappa, C, l, work, max_pairs, counts, ids, scores, logits_out, nullptr, s);
 }
 
 int dr_gather(const lng_drafter& D, const DrWin& W, void* out, hipStream_t s) {
@@ -3125,15 +3925,37 @@ int sl_args(const lng_drafter& D, const lng_sketch* S, SlArgs& A) {
   A.K = S->k;
   A.cap = S->cap;
   A.n_fallback = S->n_fallback;
+  // hash slots: a power of two >= 2 * slots read (at most 8192, never below the slots read)
+  const int64_t M = static_cast<int64_t>(D.n_orders) * D.R * S->k;
+  A.tbits = 8;
+  while ((int64_t{1} << A.tbits) < 2 * M && (1 << A.tbits) < SL_SLOTS) ++A.tbits;
   return LNG_OK;
 }
 
 int dr_shortlist(const lng_drafter& D, const DrWin& W, const SlArgs& A, const float* logits, const int64_t* full_ids,
                  const float* full_sc, int K, const DrChildren& C, int64_t* ids, float* scores, hipStream_t s,
                  int32_t* sl = nullptr, float* sll = nullptr) {
-  hipLaunchKernelGGL(k_draft_shortlist, dim3(static_cast<unsigned>(W.n)), dim3(256), 0, s, D, W, A, logits, full_ids,
-                     full_sc, K, C, ids, scores, sl, sll);
+  hipLaunchKernelGGL((k_draft_shortlist<float, false>), dim3(static_cast<unsigned>(W.n)), dim3(256), 0, s, D, W, A,
+                     logits, full_ids, full_sc, nullptr, K, C, ids, scores, sl, sll, nullptr);
   return check_launch("drafter_shortlist");
+}
+
+// The shortlist scored from the readout's hidden states (need_full [P]: positions left to the
+// full-vocabulary kernels).
+int dr_shortlist_hid(const lng_drafter& D, const DrWin& W, const SlArgs& A, const float* hid, int K,
+                     const DrChildren& C, int64_t* ids, float* scores, int32_t* sl, float* sll, int32_t* need_full,
+                     hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(W.n));
+  if (D.emb_dtype == LNG_BF16)
+    hipLaunchKernelGGL((k_draft_shortlist<bf16, true>), g, dim3(256), 0, s, D, W, A, nullptr, nullptr, nullptr, hid,
+                       K, C, ids, scores, sl, sll, need_full);
+  else if (D.emb_dtype == LNG_F16)
+    hipLaunchKernelGGL((k_draft_shortlist<_Float16, true>), g, dim3(256), 0, s, D, W, A, nullptr, nullptr, nullptr,
+                       hid, K, C, ids, scores, sl, sll, need_full);
+  else
+    hipLaunchKernelGGL((k_draft_shortlist<float, true>), g, dim3(256), 0, s, D, W, A, nullptr, nullptr, nullptr, hid,
+                       K, C, ids, scores, sl, sll, need_full);
+  return check_launch("drafter_readout_shortlist(shortlist)");
 }
 
 }  // namespace
@@ -3236,6 +4058,55 @@ int lng_drafter_shortlist(const lng_drafter* D, const lng_sketch* S, const int32
   }
   return dr_shortlist(*D, W, A, logits, full_ids, full_scores, k, C, ids, scores, as_stream(stream), shortlist,
                       shortlist_logits);
+}
+
+int lng_drafter_readout_shortlist(const lng_drafter* D, const lng_sketch* S, const int32_t* windows, int32_t P,
+                                  int32_t k, const int32_t* child_rows, const int32_t* child_parent,
+                                  const int32_t* child_rank, int32_t n_children, void* work, size_t work_bytes,
+                                  int64_t* ids, float* scores, int32_t* shortlist, float* shortlist_logits,
+                                  void* stream) {
+  if (int rc = dr_check(D, "drafter_readout_shortlist")) return rc;
+  if (k <= 0 || k > DR_MAXK || !ids || !scores || !windows || !work)
+    return fail(LNG_E_ARG, "drafter_readout_shortlist: 1 <= k <= 8, non-null windows, ids, scores, work");
+  SlArgs A{};
+  if (int rc = sl_args(*D, S, A)) return rc;
+  DrWin W;
+  if (int rc = dr_windows(*D, windows, P, W)) return rc;
+  if (n_children < 0 || n_children > DR_MAXCH)
+    return fail(LNG_E_ARG, "drafter_readout_shortlist: at most 64 children");
+  DrChildren C{};
+  C.n = n_children;
+  for (int e = 0; e < n_children; ++e) {
+    if (child_rows[e] < 0 || child_rows[e] >= D->rows || child_parent[e] < 0 || child_parent[e] >= P ||
+        child_rank[e] < 0 || child_rank[e] >= k)
+      return fail(LNG_E_RANGE, "drafter_readout_shortlist: bad child");
+    C.row[e] = child_rows[e];
+    C.parent[e] = static_cast<int8_t>(child_parent[e]);
+    C.rank[e] = static_cast<int8_t>(child_rank[e]);
+  }
+  hipStream_t s = as_stream(stream);
+  char* wk = static_cast<char*>(work);
+  const DrLayout l = dr_layout(*D, P, k, 1);
+  if (!dr_lds_ok(*D, P)) return fail(LNG_E_ARG, "drafter_readout_shortlist: too many positions for this width");
+  if (dr_fast(*D) || D->d % 8 != 0) {
+    // the full-vocabulary logits and top-k in the workspace, then the shortlist reads them
+    const size_t o_sc = l.total + align256(sizeof(int64_t) * DR_MAXP * k);
+    if (work_bytes < o_sc + align256(sizeof(float) * DR_MAXP * k))
+      return fail(LNG_E_ARG, "drafter_readout_shortlist: workspace too small");
+    float* lg = reinterpret_cast<float*>(wk + l.logits);
+    int64_t* fid = reinterpret_cast<int64_t*>(wk + l.total);
+    float* fsc = reinterpret_cast<float*>(wk + o_sc);
+    const DrChildren none{};
+    if (int rc = dr_readout(*D, W, k, 0, 0.f, none, wk, work_bytes, nullptr, fid, fsc, lg, s)) return rc;
+    return dr_shortlist(*D, W, A, lg, fid, fsc, k, C, ids, scores, s, shortlist, shortlist_logits);
+  }
+  if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter_readout_shortlist: workspace too small");
+  if (int rc = dr_front(*D, W, l, wk, s)) return rc;
+  int32_t* need = reinterpret_cast<int32_t*>(wk + l.need);
+  if (int rc = dr_shortlist_hid(*D, W, A, reinterpret_cast<const float*>(wk + l.hid), k, C, ids, scores, shortlist,
+                                shortlist_logits, need, s))
+    return rc;
+  return dr_vocab(*D, P, k, 0, 0.f, C, l, wk, 1, nullptr, ids, scores, nullptr, need, s);
 }
 
 int lng_drafter_gather(const lng_drafter* D, const int32_t* windows, int32_t P, void* out, void* stream) {

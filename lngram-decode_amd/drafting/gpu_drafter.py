@@ -124,6 +124,8 @@ class GpuDrafter:
         self.codes_d = torch.zeros(rows, self.R, dtype=torch.uint8, device=dev)
         self.ssm_d = torch.zeros(rows, max(self.N, 1), dtype=torch.float32, device=dev)
         self.len_d = torch.zeros(1, dtype=torch.int32, device=dev)
+        # block counters of the kernels that hand partial results to a last block (zero between calls)
+        self.sync = torch.zeros(_lib.DR_SYNC_INTS, dtype=torch.int32, device=dev)
         self.D = self._descriptor(self.tok_d, self.codes_d, self.ssm_d, self.len_d, rows)
         self.lib = _lib.load()
         if self.lib.lng_drafter_size() != ctypes.sizeof(_lib.Drafter):
@@ -151,7 +153,8 @@ class GpuDrafter:
         self._out_d = torch.empty(self._out_bytes, dtype=torch.uint8, device=dev)
         self._out_h = torch.empty(self._out_bytes, dtype=torch.uint8, pin_memory=True)
         if self.sketch is not None:
-            # full-vocabulary logits and top-k of up to 16 positions (the shortlist kernel's inputs)
+            # full-vocabulary logits and top-k of up to 16 positions (the inputs of lng_drafter_shortlist
+            # in trace and of the tree shortlist; chain drafts score only the shortlist)
             self.sl_lg = torch.empty(16, self.V, dtype=torch.float32, device=dev)
             self.sl_fid = torch.empty(16 * _MAX_K, dtype=torch.int64, device=dev)
             self.sl_fsc = torch.empty(16 * _MAX_K, dtype=torch.float32, device=dev)
@@ -249,7 +252,6 @@ class GpuDrafter:
         lut["mem_norm"] = t["mem_norm"].to(dev, torch.float32).contiguous()
         self.wv_dtype = ops.dtype_code(wdt)
         self.luts = lut
-        self.sync = torch.zeros(_lib.DR_SYNC_INTS, dtype=torch.int32, device=dev)
         del ef
 
     @staticmethod
@@ -287,10 +289,10 @@ class GpuDrafter:
         D.qks = self.qks.data_ptr() if self.qks is not None else None
         D.tokens, D.codes, D.ssm, D.length = tok.data_ptr(), codes.data_ptr(), ssm.data_ptr(), length.data_ptr()
         D.rows = rows
+        D.sync = self.sync.data_ptr()
         if self.luts is not None:
             for k, v in self.luts.items():
                 setattr(D, k, v.data_ptr())
-            D.sync = self.sync.data_ptr()
             D.wv_dtype = self.wv_dtype
         return D
 
@@ -395,13 +397,10 @@ class GpuDrafter:
                                                   wp, wb, self.counts.data_ptr(), self.ids_d[i].data_ptr(),
                                                   self.sc_d[i].data_ptr(), None, st), "drafter readout")
                 else:
-                    check(lib.lng_drafter_readout(Dp, win, 1, k, 0, 0.0, None, None, None, 0, wp, wb, None,
-                                                  self.sl_fid.data_ptr(), self.sl_fsc.data_ptr(),
-                                                  self.sl_lg.data_ptr(), st), "drafter readout")
-                    check(lib.lng_drafter_shortlist(Dp, ctypes.byref(self.sketch), win, 1, self.sl_lg.data_ptr(),
-                                                    self.sl_fid.data_ptr(), self.sl_fsc.data_ptr(), k, cr, cp, ck,
-                                                    int(child), self.ids_d[i].data_ptr(), self.sc_d[i].data_ptr(),
-                                                    None, None, st), "drafter shortlist")
+                    check(lib.lng_drafter_readout_shortlist(Dp, ctypes.byref(self.sketch), win, 1, k, cr, cp, ck,
+                                                            int(child), wp, wb, self.ids_d[i].data_ptr(),
+                                                            self.sc_d[i].data_ptr(), None, None, st),
+                          "drafter readout + shortlist")
                 if child:
                     check(lib.lng_drafter_advance(Dp, self._i32([nxt]), self._i32([seq[-1]]), 1, 1, wp, wb, st),
                           "drafter advance")

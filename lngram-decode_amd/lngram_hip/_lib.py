@@ -125,6 +125,8 @@ SIGNATURES = {
     "lng_drafter_gather": (_int, [_PD, _P32, _i32, _p, _p]),
     "lng_drafter_shortlist": (_int, [_PD, _PS, _P32, _i32, _p, _p, _p, _i32, _P32, _P32, _P32, _i32, _p, _p, _p, _p,
                                      _p]),
+    "lng_drafter_readout_shortlist": (_int, [_PD, _PS, _P32, _i32, _i32, _P32, _P32, _P32, _i32, _p, ctypes.c_size_t,
+                                             _p, _p, _p, _p, _p]),
     "lng_drafter_tree": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, _p, ctypes.c_size_t, _p, _p, _p]),
     "lng_drafter_tree_shortlist": (_int, [_PD, _PS, _P32, _P32, _i32, _i32, _p, ctypes.c_size_t, _p, _p, _p]),
 }

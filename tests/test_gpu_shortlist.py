@@ -126,6 +126,36 @@ def test_shortlist_matches_oracle_with_repeats_and_fallback(dev, kind):
         assert node_tok.cpu().tolist() == want and rt.shape == (spec.n, cfg["routes"], d.dt)
 
 
+@pytest.mark.parametrize("scale", [0, 40, 57])
+def test_shortlist_totals_of_any_width(dev, scale):
+    """Totals of a few bits (ties broken by id), near 2^45 (the radix select walks every byte of
+    the key) and above 2^(64 - id bits) (the one-maximum-at-a-time path): the lists, drafts and
+    logits equal the oracle's, through the trace (full-vocabulary logits) and through draft (the
+    candidates scored from the hidden state)."""
+    cfg, t = _sketch_bundle("sdb", k=8, cap=24, seed=17)
+    gen = np.random.default_rng(23)
+    for n in cfg["ngrams"]:
+        c = t[f"sketch_counts_{n}"].numpy()
+        wide = c * (np.int64(1) << scale) + (c > 0) * gen.integers(0, 4, c.shape)
+        t[f"sketch_counts_{n}"] = torch.from_numpy(wide.astype(np.int64))
+    toks = torch.randint(0, cfg["vocab"], (24,), generator=torch.Generator().manual_seed(8)).tolist()
+    o = od.DrafterOracle(cfg, t, topk=3)
+    oc, oi, ol = o.trace_readout(toks)
+    d = GpuDrafter((cfg, t), device=dev, max_len=64)
+    _, ids, lg = d.trace(toks, codes=oc)
+    np.testing.assert_array_equal(ids, oi)
+    assert _rel(lg, ol) < 1e-5
+    o.reset()
+    o.commit(toks, codes=oc)
+    d.commit(toks, codes=oc)
+    for hyp, gamma in (((), 4), (tuple(toks[3:5]), 2)):
+        want = o.draft(gamma, hyp=hyp, topk=3)
+        got = d.draft(gamma, hyp=hyp, topk=3)
+        assert got.tokens == want.tokens
+        np.testing.assert_array_equal(got.topk_ids, want.topk_ids)
+        assert _rel(got.topk_logits, want.topk_logits) < 1e-5
+
+
 def test_shortlist_edge_cases(dev):
     cfg, t = _sketch_bundle("sdb", cap=8, fallback=20)
     V = cfg["vocab"]
