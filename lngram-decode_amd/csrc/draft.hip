@@ -819,7 +819,7 @@ constexpr int SL_SLOTS = 8192;
 constexpr int SL_MAXCAP = 256;
 constexpr int SL_MAXFB = 1024;
 constexpr int SL_MAXR = 256;
-constexpr int SL_LOADS = 8;  // sketch slots each thread has in flight
+constexpr int SL_LOADS = 24;  // sketch slots each thread has in flight
 constexpr int32_t SL_EMPTY = -1;
 constexpr int32_t SL_TAKEN = 0x40000000;  // flag on a slot's id once the token is in the list
 
@@ -831,8 +831,13 @@ struct SlArgs {
   int32_t tbits;                   // log2 of the hash table's slots (8 .. 13)
 };
 
+// Probe sequence of a token: start sl_hash, step sl_step (odd, so it visits every slot of the
+// power-of-two table); double hashing keeps the probe chains short at load factors near 0.7.
 __device__ __forceinline__ uint32_t sl_hash(int32_t id, int tbits) {
   return (static_cast<uint32_t>(id) * 2654435761u) >> (32 - tbits);
+}
+__device__ __forceinline__ uint32_t sl_step(int32_t id, int tbits) {
+  return ((static_cast<uint32_t>(id) * 0x85EBCA6Bu) >> (32 - tbits)) | 1u;
 }
 
 // (total, id) a beats (total b, id b): larger total, then smaller id
@@ -840,33 +845,89 @@ __device__ __forceinline__ bool sl_better(unsigned long long ta, int32_t ia, uns
   return ta > tb || (ta == tb && ia < ib);
 }
 
+// Eight consecutive row elements in their storage form (one or two 16-byte loads), converted
+// when used.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<bf16> {
+  u32x4 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ void zero() { v = u32x4{0u, 0u, 0u, 0u}; }
+  __device__ __forceinline__ void get(f32x4& a, f32x4& b) const {
+    a = bf2f4(v.x, v.y);
+    b = bf2f4(v.z, v.w);
+  }
+};
+template <>
+struct Raw8<_Float16> {
+  u32x4 v;
+  __device__ __forceinline__ void load(const _Float16* p) { v = *reinterpret_cast<const u32x4*>(p); }
+  __device__ __forceinline__ void zero() { v = u32x4{0u, 0u, 0u, 0u}; }
+  __device__ __forceinline__ void get(f32x4& a, f32x4& b) const {
+    a = h2f4(v.x, v.y);
+    b = h2f4(v.z, v.w);
+  }
+};
+template <>
+struct Raw8<float> {
+  f32x4 x, y;
+  __device__ __forceinline__ void load(const float* p) {
+    x = reinterpret_cast<const f32x4*>(p)[0];
+    y = reinterpret_cast<const f32x4*>(p)[1];
+  }
+  __device__ __forceinline__ void zero() {
+    x = f32x4{0.f, 0.f, 0.f, 0.f};
+    y = x;
+  }
+  __device__ __forceinline__ void get(f32x4& a, f32x4& b) const {
+    a = x;
+    b = y;
+  }
+};
+
 // Logits of candidates ids[0 .. n) against the normalised hidden state hn (LDS, d floats, d % 8
-// == 0): wave w scores candidates 4w .. 4w+3, 4w+16 .., four rows in flight per lane.
-template <typename TE>
+// == 0, d / 8 <= 64 * CPL): wave w scores rows w*G .. w*G+G-1 (then 4G further on) with every
+// row's loads (CPL 16-byte pieces per lane) issued before the first product, so a group of
+// candidates costs one memory round trip.
+template <typename TE, int CPL>
 __device__ void sl_score(const lng_drafter& D, const int32_t* ids, int n, const float* hn, float* out) {
+  constexpr int G = (sizeof(TE) == 4 ? 16 : 32) / CPL;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int d = D.d, d8 = d >> 3;
   const TE* E = static_cast<const TE*>(D.emb);
-  for (int i0 = 4 * w; i0 < n; i0 += 16) {
-    int32_t id[4];
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  f32x4 h0[CPL], h1[CPL];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) id[u] = i0 + u < n ? ids[i0 + u] : -1;
-    for (int c8 = lane; c8 < d8; c8 += 64) {
-      const f32x4 h0 = *reinterpret_cast<const f32x4*>(hn + 8 * c8);
-      const f32x4 h1 = *reinterpret_cast<const f32x4*>(hn + 8 * c8 + 4);
+  for (int c = 0; c < CPL; ++c) {
+    const int c8 = lane + 64 * c;
+    h0[c] = c8 < d8 ? *reinterpret_cast<const f32x4*>(hn + 8 * c8) : f32x4{0.f, 0.f, 0.f, 0.f};
+    h1[c] = c8 < d8 ? *reinterpret_cast<const f32x4*>(hn + 8 * c8 + 4) : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int i0 = w * G; i0 < n; i0 += 4 * G) {
+    Raw8<TE> raw[G][CPL];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        if (id[u] < 0) continue;
-        f32x4 a, b;
-        ld8f<TE>(E + static_cast<int64_t>(id[u]) * d + 8 * c8, a, b);
-        acc[u] = dot4(b, h1, dot4(a, h0, acc[u]));
+    for (int g = 0; g < G; ++g) {
+      const int32_t id = i0 + g < n ? ids[i0 + g] : -1;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int c8 = lane + 64 * c;
+        if (id >= 0 && c8 < d8)
+          raw[g][c].load(E + static_cast<int64_t>(id) * d + 8 * c8);
+        else
+          raw[g][c].zero();
       }
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float s = wave_sum(acc[u]);
-      if (lane == 0 && i0 + u < n) out[i0 + u] = id[u] >= 0 ? s : -INFINITY;
+    for (int g = 0; g < G; ++g) {
+      float acc = 0.f;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        f32x4 a, b;
+        raw[g][c].get(a, b);
+        acc = dot4(b, h1[c], dot4(a, h0[c], acc));
+      }
+      const float sum = wave_sum(acc);
+      if (lane == 0 && i0 + g < n) out[i0 + g] = ids[i0 + g] >= 0 ? sum : -INFINITY;
     }
   }
 }
@@ -885,9 +946,9 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
                                                          int64_t* __restrict__ ids, float* __restrict__ scores,
                                                          int32_t* __restrict__ sl_out, float* __restrict__ sll_out,
                                                          int32_t* __restrict__ need_full) {
-  __shared__ int32_t hkey[SL_SLOTS];
-  __shared__ unsigned long long hval[SL_SLOTS];
-  __shared__ int64_t rowsh[DR_MAXN][SL_MAXR];
+  __shared__ __attribute__((aligned(16))) int32_t hkey[SL_SLOTS];
+  __shared__ __attribute__((aligned(16))) unsigned long long hval[SL_SLOTS];
+  __shared__ int64_t rowsh[DR_MAXN * SL_MAXR];  // per (order, route): first element of the sketch row
   __shared__ int32_t fb[SL_MAXFB];
   __shared__ int32_t sl[SL_MAXCAP];
   __shared__ float sll[SL_MAXCAP];
@@ -906,9 +967,21 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
   const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int L = *D.length;
   const int R = D.R, SK = S.K, cap = S.cap, tb = S.tbits, TS = 1 << tb, TM = TS - 1;
-  for (int e = tid; e < TS; e += 256) {
-    hkey[e] = SL_EMPTY;
-    hval[e] = 0ull;
+  // the hidden state and the output norm are loaded now and used at the end
+  constexpr int HQ = FROM_HID ? LNG_DR_MAX_D / 256 : 1;
+  float hv[HQ], gv[HQ];
+  if constexpr (FROM_HID) {
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int c = tid + 256 * q;
+      hv[q] = c < D.d ? hid[static_cast<int64_t>(j) * D.d + c] : 0.f;
+      gv[q] = c < D.d ? D.out_norm[c] : 0.f;
+    }
+  }
+  for (int e = 4 * tid; e < TS; e += 1024) {
+    *reinterpret_cast<int4*>(&hkey[e]) = int4{SL_EMPTY, SL_EMPTY, SL_EMPTY, SL_EMPTY};
+    *reinterpret_cast<ulonglong2*>(&hval[e]) = ulonglong2{0ull, 0ull};
+    *reinterpret_cast<ulonglong2*>(&hval[e + 2]) = ulonglong2{0ull, 0ull};
   }
   for (int e = tid; e < S.n_fallback; e += 256) fb[e] = S.fallback[e];
   if (tid < DR_MAXN) slot_rows[tid] = tid < D.maxn ? dr_resolve(W.slot[j][tid], L) : -1;
@@ -922,12 +995,15 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
   __syncthreads();
   for (int e = tid; e < D.n_orders * R; e += 256) {
     const int o = e / R, r = e % R;
-    rowsh[o][r] = idp[o] ? dr_row(D, slot_rows, o, r) : -1;
+    const int64_t row = idp[o] ? dr_row(D, slot_rows, o, r) : -1;
+    rowsh[e] = row >= 0 ? row * SK : -1;
   }
   __syncthreads();
   // sum the counts per token, SL_LOADS slots in flight per thread (at most TS distinct tokens:
-  // every probe sequence ends)
-  const int RS = R * SK, M = D.n_orders * RS;
+  // every probe sequence ends); slot e is element e % K of sketch row e / K (order, route)
+  const int M = D.n_orders * R * SK;
+  const bool k_pow2 = (SK & (SK - 1)) == 0;
+  const int k_shift = __ffs(SK) - 1;
   for (int e0 = 0; e0 < M; e0 += 256 * SL_LOADS) {
     int32_t idv[SL_LOADS];
     int64_t cv[SL_LOADS];
@@ -937,11 +1013,13 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
       idv[u] = -1;
       cv[u] = 0;
       if (e < M) {
-        const int o = e / RS, rem = e - o * RS, r = rem / SK, q = rem - r * SK;
-        const int64_t row = rowsh[o][r];
-        if (row >= 0) {
-          cv[u] = cnp[o][row * SK + q];
-          idv[u] = idp[o][row * SK + q];
+        const int rr = k_pow2 ? e >> k_shift : e / SK;
+        const int q = e - rr * SK;
+        const int o = (rr >= R) + (rr >= 2 * R) + (rr >= 3 * R);
+        const int64_t base = rowsh[rr];
+        if (base >= 0) {
+          cv[u] = cnp[o][base + q];
+          idv[u] = idp[o][base + q];
         }
       }
     }
@@ -950,25 +1028,48 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
       const int32_t id = idv[u];
       if (cv[u] <= 0 || id < 0 || id >= D.V) continue;
       uint32_t h = sl_hash(id, tb);
-      for (;;) {
+      const uint32_t st = sl_step(id, tb);
+      bool placed = false;
+      for (int p = 0; p < TS && !placed; ++p) {  // a free or matching slot always exists (TS >= M)
         const int32_t prev = atomicCAS(&hkey[h], SL_EMPTY, id);
-        if (prev == SL_EMPTY || prev == id) break;
-        h = (h + 1) & TM;
+        placed = prev == SL_EMPTY || prev == id;
+        if (!placed) h = (h + st) & TM;
       }
-      atomicAdd(&hval[h], static_cast<unsigned long long>(cv[u]));
+      if (placed) atomicAdd(&hval[h], static_cast<unsigned long long>(cv[u]));
     }
   }
   __syncthreads();
-  // the list: distinct tokens and their largest total
-  const int SPT = TS >> 8;  // slots per thread, 1 .. 32
+  // the list: every slot's (id, total) into registers once (thread tid owns slots 1024 g + 4 tid
+  // .. +3, read 16 bytes at a time); distinct tokens and largest total
+  constexpr int KQ = SL_SLOTS / 256;
+  int32_t kid[KQ];
+  unsigned long long key[KQ];
   unsigned long long tmax = 0ull;
   int cnt = 0;
-  for (int q = 0; q < SPT; ++q) {
-    const int e = tid + (q << 8);
-    if (hkey[e] >= 0) {
-      tmax = hval[e] > tmax ? hval[e] : tmax;
-      ++cnt;
+#pragma unroll
+  for (int g = 0; g < KQ / 4; ++g) {
+    const int e = (g << 10) + 4 * tid;
+    int4 k4 = int4{SL_EMPTY, SL_EMPTY, SL_EMPTY, SL_EMPTY};
+    ulonglong2 t01 = ulonglong2{0ull, 0ull}, t23 = t01;
+    if (e < TS) {
+      k4 = *reinterpret_cast<const int4*>(&hkey[e]);
+      t01 = *reinterpret_cast<const ulonglong2*>(&hval[e]);
+      t23 = *reinterpret_cast<const ulonglong2*>(&hval[e + 2]);
     }
+    kid[4 * g] = k4.x;
+    kid[4 * g + 1] = k4.y;
+    kid[4 * g + 2] = k4.z;
+    kid[4 * g + 3] = k4.w;
+    key[4 * g] = t01.x;
+    key[4 * g + 1] = t01.y;
+    key[4 * g + 2] = t23.x;
+    key[4 * g + 3] = t23.y;
+  }
+#pragma unroll
+  for (int q = 0; q < KQ; ++q) {
+    if (kid[q] < 0) key[q] = 0ull;
+    tmax = key[q] > tmax ? key[q] : tmax;
+    cnt += kid[q] >= 0 ? 1 : 0;
   }
   for (int off = 32; off >= 1; off >>= 1) {
     const unsigned long long ot = __shfl_xor(tmax, off, 64);
@@ -991,34 +1092,51 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
   int m = 0;
   if (nb <= 64) {
     const unsigned long long vmask = (1ull << ib) - 1ull;
-    unsigned long long key[SL_SLOTS / 256];
 #pragma unroll
-    for (int q = 0; q < SL_SLOTS / 256; ++q) {
-      const int e = tid + (q << 8);
-      key[q] = 0ull;
-      if (q < SPT && hkey[e] >= 0)
-        key[q] = (hval[e] << ib) | (vmask - static_cast<unsigned long long>(hkey[e]));
-    }
+    for (int q = 0; q < KQ; ++q)
+      key[q] = kid[q] >= 0 ? (key[q] << ib) | (vmask - static_cast<unsigned long long>(kid[q])) : 0ull;
     const int want = min(cap, cnt);
     unsigned long long thr = ~0ull;
     if (want > 0) {
-      int shift = ((nb + 7) >> 3) * 8 - 8;
+      // passes of at most 8 bits from the top, none straddling the total / id boundary: the total
+      // passes see few distinct digits (one atomic per distinct digit and wave), the id passes
+      // spread over the bins
       unsigned long long prefix = 0ull, pmask = 0ull;
       int rem = want;  // keys still to take among those matching prefix
+      int hi = nb;
       for (;;) {
+        const int lo = hi > ib ? ib : 0;
+        const int width = min(8, hi - lo), shift = hi - width;
+        const unsigned long long dm = (1ull << width) - 1ull;
         hist[tid] = 0;
         __syncthreads();
+        if (shift >= ib && width <= 3) {
+          // a pass over the totals sees few distinct digits: counted per wave with ballots
+          int c8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
-        for (int q = 0; q < SL_SLOTS / 256; ++q) {
-          const unsigned long long k = key[q];
-          if (k && (k & pmask) == prefix) atomicAdd(&hist[static_cast<int>((k >> shift) & 255ull)], 1);
+          for (int q = 0; q < KQ; ++q) {
+            const unsigned long long k = key[q];
+            const int dg = (k && (k & pmask) == prefix) ? static_cast<int>((k >> shift) & dm) : -1;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) c8[t] += __popcll(__ballot(dg == t));
+          }
+          int mine = 0;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) mine = lane == t ? c8[t] : mine;
+          if (lane < 8 && mine) atomicAdd(&hist[lane], mine);
+        } else {
+#pragma unroll
+          for (int q = 0; q < KQ; ++q) {
+            const unsigned long long k = key[q];
+            if (k && (k & pmask) == prefix) atomicAdd(&hist[static_cast<int>((k >> shift) & dm)], 1);
+          }
         }
         __syncthreads();
         if (w == 0) {
           // lane l holds bins 4l .. 4l+3; suf = keys in bins >= 4l (non-increasing in l)
           const int h0 = hist[4 * lane], h1 = hist[4 * lane + 1], h2 = hist[4 * lane + 2], h3 = hist[4 * lane + 3];
-          const int s = (h0 + h1) + (h2 + h3);
-          int suf = s;
+          const int s4 = (h0 + h1) + (h2 + h3);
+          int suf = s4;
           for (int off = 1; off < 64; off <<= 1) {
             const int t = __shfl_down(suf, off, 64);
             if (lane + off < 64) suf += t;
@@ -1026,7 +1144,7 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
           const unsigned long long bal = __ballot(suf >= rem);
           const int ls = 63 - __clzll(static_cast<long long>(bal));
           if (lane == ls) {
-            int above = suf - s, b = 4 * lane + 3, hb = h3;
+            int above = suf - s4, b = 4 * lane + 3, hb = h3;
             if (above + h3 < rem) {
               above += h3;
               b = 4 * lane + 2;
@@ -1050,23 +1168,23 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
         __syncthreads();
         rem -= rad[1];
         prefix |= static_cast<unsigned long long>(rad[0]) << shift;
-        pmask |= 255ull << shift;
+        pmask |= dm << shift;
         if (rad[2] == rem || shift == 0) {  // every key in the digit's bin is taken
           thr = prefix;
           break;
         }
-        shift -= 8;
+        hi = shift;
       }
     }
     if (tid == 0) rad[3] = 0;
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < SL_SLOTS / 256; ++q) {
+    for (int q = 0; q < KQ; ++q) {
       const unsigned long long k = key[q];
       if (k && k >= thr) {
         const int pos = atomicAdd(&rad[3], 1);  // keys are unique: exactly `want` pass
         if (pos < SL_MAXCAP) selk[pos] = k;
-        hkey[tid + (q << 8)] |= SL_TAKEN;
+        hkey[((q >> 2) << 10) + 4 * tid + (q & 3)] |= SL_TAKEN;
       }
     }
     __syncthreads();
@@ -1136,14 +1254,15 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
       ok = f >= 0 && f < D.V;
       if (ok) {
         uint32_t h = sl_hash(f, tb);
-        for (;;) {
+        const uint32_t st = sl_step(f, tb);
+        for (int p = 0; p < TS; ++p) {  // a full table has no empty slot to end on
           const int32_t k = hkey[h];
           if (k == SL_EMPTY) break;
           if ((k & ~SL_TAKEN) == f) {
             ok = !(k & SL_TAKEN);
             break;
           }
-          h = (h + 1) & TM;
+          h = (h + st) & TM;
         }
       }
       for (int i = 0; ok && i < jf; ++i) ok = fb[i] != f;
@@ -1168,20 +1287,27 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
   if constexpr (FROM_HID) {
     const int d = D.d;
     float ss = 0.f;
-    for (int c = tid; c < d; c += 256) {
-      const float v = hid[static_cast<int64_t>(j) * d + c];
-      hn[c] = v;
-      ss = fmaf(v, v, ss);
-    }
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) ss = fmaf(hv[q], hv[q], ss);
     ss = block_sum256(ss, red_f);
     const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + D.draft_eps);
-    for (int c = tid; c < d; c += 256) hn[c] = hn[c] * r * D.out_norm[c];
+#pragma unroll
+    for (int q = 0; q < HQ; ++q) {
+      const int c = tid + 256 * q;
+      if (c < d) hn[c] = hv[q] * r * gv[q];
+    }
     // an empty list reports tokens 0 .. cap-1 with their logits
     const int nsc = n_sl > 0 ? n_sl : ((sl_out || sll_out) ? min(cap, D.V) : 0);
     if (n_sl == 0)
       for (int i = tid; i < nsc; i += 256) sl[i] = i;
     __syncthreads();
-    sl_score<TE>(D, sl, nsc, hn, sll);
+    const int cpl = ((d >> 3) + 63) >> 6;
+    if (cpl <= 1)
+      sl_score<TE, 1>(D, sl, nsc, hn, sll);
+    else if (cpl <= 2)
+      sl_score<TE, 2>(D, sl, nsc, hn, sll);
+    else
+      sl_score<TE, 4>(D, sl, nsc, hn, sll);
     __syncthreads();
     for (int i = tid; i < cap; i += 256) {
       if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sl[i] : -1;
