@@ -932,26 +932,14 @@ __device__ void sl_score(const lng_drafter& D, const int32_t* ids, int n, const 
   }
 }
 
-// FROM_HID = false: the candidates' logits are read from the full-vocabulary logits [P, V] and an
-// empty list keeps the full-vocabulary top-k (full_ids / full_sc).  FROM_HID = true: the
-// candidates are scored here from the readout's hidden state hid [P, d] (RMSNorm * out_norm, then
-// E[id] . h); a position whose list is empty gets need_full[j] = 1 and no outputs (the
-// full-vocabulary kernels that follow write them), every other position need_full[j] = 0.
-template <typename TE, bool FROM_HID>
-__global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W, SlArgs S,
-                                                         const float* __restrict__ logits,
-                                                         const int64_t* __restrict__ full_ids,
-                                                         const float* __restrict__ full_sc,
-                                                         const float* __restrict__ hid, int32_t K, DrChildren C,
-                                                         int64_t* __restrict__ ids, float* __restrict__ scores,
-                                                         int32_t* __restrict__ sl_out, float* __restrict__ sll_out,
-                                                         int32_t* __restrict__ need_full) {
+// The candidate list of position j (RefDrafter._shortlist): sl[0 .. n) in LDS, n returned (0: empty
+// list).  Called by every thread of a 256-thread block; the hash table and selection state are
+// this function's own LDS.
+__device__ int sl_build(const lng_drafter& D, const DrWin& W, const SlArgs& S, int j, int32_t* sl) {
   __shared__ __attribute__((aligned(16))) int32_t hkey[SL_SLOTS];
   __shared__ __attribute__((aligned(16))) unsigned long long hval[SL_SLOTS];
   __shared__ int64_t rowsh[DR_MAXN * SL_MAXR];  // per (order, route): first element of the sketch row
   __shared__ int32_t fb[SL_MAXFB];
-  __shared__ int32_t sl[SL_MAXCAP];
-  __shared__ float sll[SL_MAXCAP];
   __shared__ unsigned long long selk[SL_MAXCAP];
   __shared__ int32_t hist[256];
   __shared__ int32_t slot_rows[DR_MAXN];
@@ -960,24 +948,9 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
   __shared__ unsigned long long red_t[4];
   __shared__ int32_t red_i[4], red_s[4];
   __shared__ int32_t rad[4];  // selected digit, keys above it, keys in it; list length
-  __shared__ float red_f[4];
-  __shared__ int64_t sel_id[DR_MAXK];
-  __shared__ float sel_sc[DR_MAXK];
-  __shared__ __attribute__((aligned(16))) float hn[FROM_HID ? LNG_DR_MAX_D : 4];
-  const int j = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int L = *D.length;
   const int R = D.R, SK = S.K, cap = S.cap, tb = S.tbits, TS = 1 << tb, TM = TS - 1;
-  // the hidden state and the output norm are loaded now and used at the end
-  constexpr int HQ = FROM_HID ? LNG_DR_MAX_D / 256 : 1;
-  float hv[HQ], gv[HQ];
-  if constexpr (FROM_HID) {
-#pragma unroll
-    for (int q = 0; q < HQ; ++q) {
-      const int c = tid + 256 * q;
-      hv[q] = c < D.d ? hid[static_cast<int64_t>(j) * D.d + c] : 0.f;
-      gv[q] = c < D.d ? D.out_norm[c] : 0.f;
-    }
-  }
   for (int e = 4 * tid; e < TS; e += 1024) {
     *reinterpret_cast<int4*>(&hkey[e]) = int4{SL_EMPTY, SL_EMPTY, SL_EMPTY, SL_EMPTY};
     *reinterpret_cast<ulonglong2*>(&hval[e]) = ulonglong2{0ull, 0ull};
@@ -1283,93 +1256,51 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
     added += tot;
     __syncthreads();
   }
-  const int n_sl = min(cap, m + added);
-  if constexpr (FROM_HID) {
-    const int d = D.d;
-    float ss = 0.f;
+  return min(cap, m + added);
+}
+
+// top-K of the candidates sl[0 .. n) by (logit sll desc, candidate index asc), by wave 0, into
+// sel_id / sel_sc (-1 / -inf past the list)
+__device__ void sl_topk(const int32_t* sl, const float* sll, int n, int K, int64_t* sel_id, float* sel_sc) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x >= 64) return;
+  constexpr int NQ = SL_MAXCAP / 64;
+  float v[NQ];
 #pragma unroll
-    for (int q = 0; q < HQ; ++q) ss = fmaf(hv[q], hv[q], ss);
-    ss = block_sum256(ss, red_f);
-    const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + D.draft_eps);
+  for (int q = 0; q < NQ; ++q) v[q] = lane + 64 * q < n ? sll[lane + 64 * q] : 0.f;
+  unsigned used = 0u;
+  for (int k = 0; k < K; ++k) {
+    float bv = -INFINITY;
+    int bi = INT_MAX;
 #pragma unroll
-    for (int q = 0; q < HQ; ++q) {
-      const int c = tid + 256 * q;
-      if (c < d) hn[c] = hv[q] * r * gv[q];
+    for (int q = 0; q < NQ; ++q) {
+      const int i = lane + 64 * q;
+      if (i >= n || ((used >> q) & 1u)) continue;
+      if (v[q] > bv || (v[q] == bv && i < bi)) {
+        bv = v[q];
+        bi = i;
+      }
     }
-    // an empty list reports tokens 0 .. cap-1 with their logits
-    const int nsc = n_sl > 0 ? n_sl : ((sl_out || sll_out) ? min(cap, D.V) : 0);
-    if (n_sl == 0)
-      for (int i = tid; i < nsc; i += 256) sl[i] = i;
-    __syncthreads();
-    const int cpl = ((d >> 3) + 63) >> 6;
-    if (cpl <= 1)
-      sl_score<TE, 1>(D, sl, nsc, hn, sll);
-    else if (cpl <= 2)
-      sl_score<TE, 2>(D, sl, nsc, hn, sll);
-    else
-      sl_score<TE, 4>(D, sl, nsc, hn, sll);
-    __syncthreads();
-    for (int i = tid; i < cap; i += 256) {
-      if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sl[i] : -1;
-      if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sll[i] : -INFINITY;
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
+      }
     }
-    if (tid == 0) need_full[j] = n_sl == 0 ? 1 : 0;
-    if (n_sl == 0) return;  // the full-vocabulary kernels write this position's drafts (uniform)
-  } else {
-    const float* lg = logits + static_cast<int64_t>(j) * D.V;
-    for (int i = tid; i < cap; i += 256) {
-      int32_t id = -1;
-      if (n_sl > 0)
-        id = i < n_sl ? sl[i] : -1;
-      else
-        id = i < D.V ? i : -1;  // empty list: the whole vocabulary, cut to cap
-      const float v = id >= 0 ? lg[id] : -INFINITY;
-      sll[i] = v;
-      if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = id;
-      if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = v;
+    if (bi != INT_MAX && (bi & 63) == lane) used |= 1u << (bi >> 6);
+    if (lane == 0) {
+      sel_id[k] = bi == INT_MAX ? -1 : sl[bi];
+      sel_sc[k] = bi == INT_MAX ? -INFINITY : bv;
     }
   }
-  __syncthreads();
-  if (n_sl == 0) {
-    if (tid < K) {
-      sel_id[tid] = full_ids[static_cast<int64_t>(j) * K + tid];
-      sel_sc[tid] = full_sc[static_cast<int64_t>(j) * K + tid];
-    }
-  } else if (w == 0) {
-    // top-K of sll[0 .. n_sl) by (logit desc, candidate index asc): lane l holds l, l+64, ..
-    constexpr int NQ = SL_MAXCAP / 64;
-    float v[NQ];
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) v[q] = lane + 64 * q < n_sl ? sll[lane + 64 * q] : 0.f;
-    unsigned used = 0u;
-    for (int k = 0; k < K; ++k) {
-      float bv = -INFINITY;
-      int bi = INT_MAX;
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) {
-        const int i = lane + 64 * q;
-        if (i >= n_sl || ((used >> q) & 1u)) continue;
-        if (v[q] > bv || (v[q] == bv && i < bi)) {
-          bv = v[q];
-          bi = i;
-        }
-      }
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      if (bi != INT_MAX && (bi & 63) == lane) used |= 1u << (bi >> 6);
-      if (lane == 0) {
-        sel_id[k] = bi == INT_MAX ? -1 : sl[bi];
-        sel_sc[k] = bi == INT_MAX ? -INFINITY : bv;
-      }
-    }
-  }
-  __syncthreads();
+}
+
+// ids / scores [P, K] and the children's tokens from the selected drafts of position j
+__device__ void sl_write(const lng_drafter& D, int j, int K, const DrChildren& C, const int64_t* sel_id,
+                         const float* sel_sc, int64_t* ids, float* scores) {
+  const int tid = threadIdx.x;
   if (tid < K) {
     ids[static_cast<int64_t>(j) * K + tid] = sel_id[tid];
     scores[static_cast<int64_t>(j) * K + tid] = sel_sc[tid];
@@ -1379,6 +1310,108 @@ __global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W,
     const int64_t t = sel_id[C.rank[e]];
     D.tokens[C.row[e]] = t >= 0 ? t : sel_id[0];
   }
+}
+
+// The shortlist drafts of P positions given their full-vocabulary logits [P, V] and top-k: the
+// candidates' logits are read from the logits; an empty list keeps the full-vocabulary top-k
+// (full_ids / full_sc).                                            grid (P)
+__global__ __launch_bounds__(256) void k_draft_shortlist(lng_drafter D, DrWin W, SlArgs S,
+                                                         const float* __restrict__ logits,
+                                                         const int64_t* __restrict__ full_ids,
+                                                         const float* __restrict__ full_sc, int32_t K, DrChildren C,
+                                                         int64_t* __restrict__ ids, float* __restrict__ scores,
+                                                         int32_t* __restrict__ sl_out, float* __restrict__ sll_out) {
+  __shared__ int32_t sl[SL_MAXCAP];
+  __shared__ float sll[SL_MAXCAP];
+  __shared__ int64_t sel_id[DR_MAXK];
+  __shared__ float sel_sc[DR_MAXK];
+  const int j = blockIdx.x, tid = threadIdx.x, cap = S.cap;
+  const int n_sl = sl_build(D, W, S, j, sl);
+  const float* lg = logits + static_cast<int64_t>(j) * D.V;
+  for (int i = tid; i < cap; i += 256) {
+    int32_t id = -1;
+    if (n_sl > 0)
+      id = i < n_sl ? sl[i] : -1;
+    else
+      id = i < D.V ? i : -1;  // empty list: the whole vocabulary, cut to cap
+    const float v = id >= 0 ? lg[id] : -INFINITY;
+    sll[i] = v;
+    if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = id;
+    if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = v;
+  }
+  __syncthreads();
+  if (n_sl == 0) {
+    if (tid < K) {
+      sel_id[tid] = full_ids[static_cast<int64_t>(j) * K + tid];
+      sel_sc[tid] = full_sc[static_cast<int64_t>(j) * K + tid];
+    }
+  } else {
+    sl_topk(sl, sll, n_sl, K, sel_id, sel_sc);
+  }
+  __syncthreads();
+  sl_write(D, j, K, C, sel_id, sel_sc, ids, scores);
+}
+
+// The drafts of P positions scored over their candidate lists from the readout's hidden states:
+// lists [P][1 + cap] (length, then the ids, as the attention launch's list blocks wrote them),
+// hid [P, d] (RMSNorm * out_norm, then E[id] . h).  A position with an empty list gets
+// need_full[j] = 1 and no drafts (the full-vocabulary kernels that follow write them), every other
+// position need_full[j] = 0.  shortlist / shortlist_logits (optional): as lng_drafter_shortlist
+// (an empty list reports tokens 0 .. cap-1 with their logits).          grid (P)
+template <typename TE>
+__global__ __launch_bounds__(256) void k_sl_score(lng_drafter D, int32_t cap, const int32_t* __restrict__ lists,
+                                                  const float* __restrict__ hid, int32_t K, DrChildren C,
+                                                  int64_t* __restrict__ ids, float* __restrict__ scores,
+                                                  int32_t* __restrict__ sl_out, float* __restrict__ sll_out,
+                                                  int32_t* __restrict__ need_full) {
+  __shared__ int32_t sl[SL_MAXCAP];
+  __shared__ float sll[SL_MAXCAP];
+  __shared__ int64_t sel_id[DR_MAXK];
+  __shared__ float sel_sc[DR_MAXK];
+  __shared__ float red_f[4];
+  __shared__ __attribute__((aligned(16))) float hn[LNG_DR_MAX_D];
+  const int j = blockIdx.x, tid = threadIdx.x, d = D.d;
+  constexpr int HQ = LNG_DR_MAX_D / 256;
+  float hv[HQ], gv[HQ];
+#pragma unroll
+  for (int q = 0; q < HQ; ++q) {
+    const int c = tid + 256 * q;
+    hv[q] = c < d ? hid[static_cast<int64_t>(j) * d + c] : 0.f;
+    gv[q] = c < d ? D.out_norm[c] : 0.f;
+  }
+  const int32_t* lj = lists + static_cast<int64_t>(j) * (cap + 1);
+  const int n_sl = min(cap, max(0, lj[0]));
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < HQ; ++q) ss = fmaf(hv[q], hv[q], ss);
+  ss = block_sum256(ss, red_f);
+  const float r = 1.0f / sqrtf(ss / static_cast<float>(d) + D.draft_eps);
+#pragma unroll
+  for (int q = 0; q < HQ; ++q) {
+    const int c = tid + 256 * q;
+    if (c < d) hn[c] = hv[q] * r * gv[q];
+  }
+  // an empty list reports tokens 0 .. cap-1 with their logits
+  const int nsc = n_sl > 0 ? n_sl : ((sl_out || sll_out) ? min(cap, D.V) : 0);
+  for (int i = tid; i < nsc; i += 256) sl[i] = n_sl > 0 ? lj[1 + i] : i;
+  __syncthreads();
+  const int cpl = ((d >> 3) + 63) >> 6;
+  if (cpl <= 1)
+    sl_score<TE, 1>(D, sl, nsc, hn, sll);
+  else if (cpl <= 2)
+    sl_score<TE, 2>(D, sl, nsc, hn, sll);
+  else
+    sl_score<TE, 4>(D, sl, nsc, hn, sll);
+  __syncthreads();
+  for (int i = tid; i < cap; i += 256) {
+    if (sl_out) sl_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sl[i] : -1;
+    if (sll_out) sll_out[static_cast<int64_t>(j) * cap + i] = i < nsc ? sll[i] : -INFINITY;
+  }
+  if (tid == 0) need_full[j] = n_sl == 0 ? 1 : 0;
+  if (n_sl == 0) return;  // the full-vocabulary kernels write this position's drafts (uniform)
+  sl_topk(sl, sll, n_sl, K, sel_id, sel_sc);
+  __syncthreads();
+  sl_write(D, j, K, C, sel_id, sel_sc, ids, scores);
 }
 
 // tokens[dst] = tokens[L - 1] (the root of a draft tree next to its nodes).
@@ -3321,10 +3354,24 @@ __global__ __launch_bounds__(256) void k_sm_qkw(lng_drafter D, DrWin W, float* _
 // Partial sink-free softmax of position j over SM_RC routes for every query head, then the last
 // block of the position merges the chunks with the sink into u[j] [QH * Dt]:
 //   part_u [((j * nch + c) * QH + qh) * Dt + i], part_ml [((j * nch + c) * QH + qh) * 2 + {0, 1}] = (m, l)
-// (device-coherent hand-off; sync[SY_ATT + j] counts the blocks).       grid (nch, P)
+// (device-coherent hand-off; sync[SY_ATT + j] counts the blocks).       grid (nch (+1), P)
+// With LIST, block nch of each position builds its sketch shortlist meanwhile (it needs only the
+// window's codes) into lists [P][1 + cap]: the length, then the ids.
+template <bool LIST>
 __global__ __launch_bounds__(256) void k_sm_attend(lng_drafter D, DrWin W, const float* __restrict__ qkw,
                                                    float* __restrict__ part_u, float* __restrict__ part_ml,
-                                                   float* __restrict__ u) {
+                                                   float* __restrict__ u, SlArgs S, int32_t* __restrict__ lists) {
+  if constexpr (LIST) {
+    if (blockIdx.x == gridDim.x - 1) {
+      __shared__ int32_t sl[SL_MAXCAP];
+      const int j = blockIdx.y;
+      const int n = sl_build(D, W, S, j, sl);
+      int32_t* lj = lists + static_cast<int64_t>(j) * (S.cap + 1);
+      if (threadIdx.x == 0) lj[0] = n;
+      for (int i = threadIdx.x; i < n; i += 256) lj[1 + i] = sl[i];
+      return;
+    }
+  }
   __shared__ __attribute__((aligned(16))) float xs[SM_RC][LNG_DR_MAX_DT];
   __shared__ __attribute__((aligned(16))) float qs[LNG_DR_MAX_QH * LNG_DR_MAX_DT];
   __shared__ float sxs[SM_RC];
@@ -3334,7 +3381,7 @@ __global__ __launch_bounds__(256) void k_sm_attend(lng_drafter D, DrWin W, const
   __shared__ float mls[LNG_DR_MAX_QH][SM_MAXCH][2];
   __shared__ float scl[LNG_DR_MAX_QH][SM_MAXCH];
   __shared__ int last_flag;
-  const int j = blockIdx.y, c = blockIdx.x, nch = gridDim.x;
+  const int j = blockIdx.y, c = blockIdx.x, nch = gridDim.x - (LIST ? 1 : 0);
   const int L = *D.length;
   const int Dt = D.dt, D4 = Dt >> 2, QH = D.q_heads, md = D.mem_dim, QD = QH * Dt;
   const int r0 = c * SM_RC, nr = min(SM_RC, D.R - r0);
@@ -3637,7 +3684,7 @@ __global__ __launch_bounds__(256) void k_sm_codes(lng_drafter D, DrAdv A) {
 }
 
 struct DrLayout {
-  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, smu, smml, smout, need, total;
+  size_t u, qkw, part, hid, logits, lpart, w, fpart, ro, tot, flpart, cand, smu, smml, smout, need, lists, total;
   int nch, nblk, fnch, fnblk, smch;
 };
 
@@ -3674,6 +3721,7 @@ DrLayout dr_layout(const lng_drafter& D, int P, int K, int max_pairs) {
   l.smml = take(sizeof(float) * static_cast<size_t>(std::min(P, SM_P)) * l.smch * D.q_heads * 2);
   l.smout = take(sizeof(float) * static_cast<size_t>(std::min(P, SM_P)) * QD);
   l.need = take(sizeof(int32_t) * DR_MAXP);
+  l.lists = take(sizeof(int32_t) * static_cast<size_t>(std::min(P, SM_P)) * (SL_MAXCAP + 1));
   l.total = off;
   return l;
 }
@@ -3822,8 +3870,10 @@ bool dr_lds_ok(const lng_drafter& D, int P) {
 }
 
 // The readout of P positions up to the hidden states hid [P, d] (work + l.hid): query-key weights,
-// attention over the routes, output projection.
-int dr_front(const lng_drafter& D, const DrWin& W, const DrLayout& l, char* work, hipStream_t s) {
+// attention over the routes, output projection.  sk (small-batch kernels only): the attention
+// launch also builds each position's sketch shortlist into work + l.lists.
+int dr_front(const lng_drafter& D, const DrWin& W, const DrLayout& l, char* work, hipStream_t s,
+             const SlArgs* sk = nullptr) {
   const int P = W.n, QD = D.q_heads * D.dt;
   const int Nq = D.query_ssm ? D.ssm_dim : 0;
   float* qkw = reinterpret_cast<float*>(work + l.qkw);
@@ -3834,8 +3884,12 @@ int dr_front(const lng_drafter& D, const DrWin& W, const DrLayout& l, char* work
     float* uo = reinterpret_cast<float*>(work + l.smout);
     hipLaunchKernelGGL(k_sm_qkw, dim3(static_cast<unsigned>(cdiv(QD, 4))), dim3(256), 0, s, D, W, qkw);
     if (int rc = check_launch("drafter_readout(qkw)")) return rc;
-    hipLaunchKernelGGL(k_sm_attend, dim3(static_cast<unsigned>(l.smch), static_cast<unsigned>(P)), dim3(256), 0, s, D,
-                       W, qkw, pu, pml, uo);
+    if (sk)
+      hipLaunchKernelGGL(k_sm_attend<true>, dim3(static_cast<unsigned>(l.smch + 1), static_cast<unsigned>(P)),
+                         dim3(256), 0, s, D, W, qkw, pu, pml, uo, *sk, reinterpret_cast<int32_t*>(work + l.lists));
+    else
+      hipLaunchKernelGGL(k_sm_attend<false>, dim3(static_cast<unsigned>(l.smch), static_cast<unsigned>(P)),
+                         dim3(256), 0, s, D, W, qkw, pu, pml, uo, SlArgs{}, nullptr);
     if (int rc = check_launch("drafter_readout(attend)")) return rc;
     hipLaunchKernelGGL(k_sm_hidden, dim3(static_cast<unsigned>(cdiv(D.d, 4))), dim3(256), sizeof(float) * P * QD, s, D,
                        P, uo, hid);
@@ -4061,27 +4115,25 @@ int sl_args(const lng_drafter& D, const lng_sketch* S, SlArgs& A) {
 int dr_shortlist(const lng_drafter& D, const DrWin& W, const SlArgs& A, const float* logits, const int64_t* full_ids,
                  const float* full_sc, int K, const DrChildren& C, int64_t* ids, float* scores, hipStream_t s,
                  int32_t* sl = nullptr, float* sll = nullptr) {
-  hipLaunchKernelGGL((k_draft_shortlist<float, false>), dim3(static_cast<unsigned>(W.n)), dim3(256), 0, s, D, W, A,
-                     logits, full_ids, full_sc, nullptr, K, C, ids, scores, sl, sll, nullptr);
+  hipLaunchKernelGGL(k_draft_shortlist, dim3(static_cast<unsigned>(W.n)), dim3(256), 0, s, D, W, A, logits, full_ids,
+                     full_sc, K, C, ids, scores, sl, sll);
   return check_launch("drafter_shortlist");
 }
 
-// The shortlist scored from the readout's hidden states (need_full [P]: positions left to the
-// full-vocabulary kernels).
-int dr_shortlist_hid(const lng_drafter& D, const DrWin& W, const SlArgs& A, const float* hid, int K,
-                     const DrChildren& C, int64_t* ids, float* scores, int32_t* sl, float* sll, int32_t* need_full,
-                     hipStream_t s) {
-  const dim3 g(static_cast<unsigned>(W.n));
+// The drafts of P positions scored over the lists the attention launch built (need_full [P]:
+// positions left to the full-vocabulary kernels).
+int dr_sl_score(const lng_drafter& D, int P, int cap, const int32_t* lists, const float* hid, int K,
+                const DrChildren& C, int64_t* ids, float* scores, int32_t* sl, float* sll, int32_t* need_full,
+                hipStream_t s) {
+  const dim3 g(static_cast<unsigned>(P));
   if (D.emb_dtype == LNG_BF16)
-    hipLaunchKernelGGL((k_draft_shortlist<bf16, true>), g, dim3(256), 0, s, D, W, A, nullptr, nullptr, nullptr, hid,
-                       K, C, ids, scores, sl, sll, need_full);
+    hipLaunchKernelGGL(k_sl_score<bf16>, g, dim3(256), 0, s, D, cap, lists, hid, K, C, ids, scores, sl, sll, need_full);
   else if (D.emb_dtype == LNG_F16)
-    hipLaunchKernelGGL((k_draft_shortlist<_Float16, true>), g, dim3(256), 0, s, D, W, A, nullptr, nullptr, nullptr,
-                       hid, K, C, ids, scores, sl, sll, need_full);
+    hipLaunchKernelGGL(k_sl_score<_Float16>, g, dim3(256), 0, s, D, cap, lists, hid, K, C, ids, scores, sl, sll,
+                       need_full);
   else
-    hipLaunchKernelGGL((k_draft_shortlist<float, true>), g, dim3(256), 0, s, D, W, A, nullptr, nullptr, nullptr, hid,
-                       K, C, ids, scores, sl, sll, need_full);
-  return check_launch("drafter_readout_shortlist(shortlist)");
+    hipLaunchKernelGGL(k_sl_score<float>, g, dim3(256), 0, s, D, cap, lists, hid, K, C, ids, scores, sl, sll, need_full);
+  return check_launch("drafter_readout_shortlist(score)");
 }
 
 }  // namespace
@@ -4214,7 +4266,7 @@ int lng_drafter_readout_shortlist(const lng_drafter* D, const lng_sketch* S, con
   char* wk = static_cast<char*>(work);
   const DrLayout l = dr_layout(*D, P, k, 1);
   if (!dr_lds_ok(*D, P)) return fail(LNG_E_ARG, "drafter_readout_shortlist: too many positions for this width");
-  if (dr_fast(*D) || D->d % 8 != 0) {
+  if (dr_fast(*D) || !sm_ok(*D, P)) {
     // the full-vocabulary logits and top-k in the workspace, then the shortlist reads them
     const size_t o_sc = l.total + align256(sizeof(int64_t) * DR_MAXP * k);
     if (work_bytes < o_sc + align256(sizeof(float) * DR_MAXP * k))
@@ -4227,10 +4279,11 @@ int lng_drafter_readout_shortlist(const lng_drafter* D, const lng_sketch* S, con
     return dr_shortlist(*D, W, A, lg, fid, fsc, k, C, ids, scores, s, shortlist, shortlist_logits);
   }
   if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter_readout_shortlist: workspace too small");
-  if (int rc = dr_front(*D, W, l, wk, s)) return rc;
+  if (int rc = dr_front(*D, W, l, wk, s, &A)) return rc;
   int32_t* need = reinterpret_cast<int32_t*>(wk + l.need);
-  if (int rc = dr_shortlist_hid(*D, W, A, reinterpret_cast<const float*>(wk + l.hid), k, C, ids, scores, shortlist,
-                                shortlist_logits, need, s))
+  if (int rc = dr_sl_score(*D, P, A.cap, reinterpret_cast<const int32_t*>(wk + l.lists),
+                           reinterpret_cast<const float*>(wk + l.hid), k, C, ids, scores, shortlist, shortlist_logits,
+                           need, s))
     return rc;
   return dr_vocab(*D, P, k, 0, 0.f, C, l, wk, 1, nullptr, ids, scores, nullptr, need, s);
 }
