@@ -553,6 +553,27 @@ int lng_drafter_tree_fused(const lng_drafter* D, const int32_t* parent, const in
                            int32_t node_row0, int online, float kappa, uint32_t seq, void* work, size_t work_bytes,
                            void* route_tokens, long long* stamps, void* stream);
 
+/* Draft tree with verification gather, one launch per depth (drafting/tree.py:243-257 draft_tree
+ * over cpu_drafter.py:208-270 readouts and drafters.py:117-142 online counts; tree.py:96-136
+ * tree_route_tokens), for token-only drafters with the per-token tables at the SD drafters' shape:
+ * q_heads 4, head_dim 64, orders (2, 3) with mem_dim 128, bits 4, R <= 192, bf16 tables and value
+ * weight, V <= 32832; trees of at most 32 nodes, 8 depths, 4 parents per depth and rank < 4.
+ * Same outputs as lng_drafter_tree (node tokens and codes in rows node_row0 + i, the root token in
+ * row node_row0, route_tokens [n, R, 256] bf16 when not null).  Launch d: the parents of depth d
+ * select their own tokens from the previous launch's vocabulary records, gather their windows and
+ * attend per query head; vocabulary blocks hold their lut_out slice from launch entry, count the
+ * online matches of the pairs whose next token they own, and score it once the parents' outputs
+ * arrive through device-coherent (value, tag) pairs (bounded waits).  `work` holds
+ * lng_drafter_tree_levels_workspace(D) bytes, zero before the first call and kept between calls
+ * (its first word counts the calls; the int32 at byte offset 4 is a sticky error word: non-zero =
+ * a wait timed out; zero the workspace after an error).  The workspace size is 0, and the call
+ * returns LNG_E_ARG without launching, for a drafter or tree outside the limits above
+ * (lng_drafter_tree runs those). */
+size_t lng_drafter_tree_levels_workspace(const lng_drafter* D);
+int lng_drafter_tree_levels(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n,
+                            int32_t node_row0, int online, float kappa, void* work, size_t work_bytes,
+                            void* route_tokens, void* stream);
+
 
 /* Tree acceptance (drafting/tree.py:205-220): from the root take the first child
  * (index order) whose token equals argmax[cur]; repeat.  path[n] receives the

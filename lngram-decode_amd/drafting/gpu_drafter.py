@@ -59,7 +59,8 @@ class GpuDrafter:
     name = "gpu"
 
     def __init__(self, bundle, topk: int = 3, shortlist_cap: int | None = None, device=None, max_len: int = 4096,
-                 online: bool = False, kappa: float = 1.0, tables: bool = True, fused: bool = False):
+                 online: bool = False, kappa: float = 1.0, tables: bool = True, fused: bool = False,
+                 levels: bool = True):
         c, t = _bundle_parts(bundle)
         self.cfg = c
         # RefDrafter scores a sketch shortlist when the cap is positive and the bundle carries
@@ -145,6 +146,15 @@ class GpuDrafter:
             fb = self.lib.lng_drafter_tree_fused_workspace(ctypes.byref(self.D))
             if fb:
                 self.tree_work = torch.zeros(int(fb), dtype=torch.uint8, device=dev)
+        # draft trees of token-only drafters at the SD drafters' shape: one launch per depth
+        # (lng_drafter_tree_levels); trees outside its limits take the per-depth readouts of
+        # lng_drafter_tree.  Its workspace keeps a call counter, so it is zeroed once here.
+        self.level_work = None
+        self._level_specs: dict = {}
+        if levels and self.tree_work is None and self.luts is not None and self.sketch is None:
+            lb = self.lib.lng_drafter_tree_levels_workspace(ctypes.byref(self.D))
+            if lb:
+                self.level_work = torch.zeros(int(lb), dtype=torch.uint8, device=dev)
         self.ids_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.int64, device=dev)
         self.sc_d = torch.empty(_HYP_ROWS, _MAX_K, dtype=torch.float32, device=dev)
         # a draft's results (top-k ids, scores, codes of the drafted rows) leave the device in one
@@ -477,6 +487,17 @@ class GpuDrafter:
                 self._fused_specs[key] = True
                 return self.tok_d[self.tree_row0: self.tree_row0 + n], out
             self._fused_specs[key] = False     # tree outside the one-launch limits: per-depth launches
+        if self.level_work is not None and self._level_specs.get(key, True):
+            rc = self.lib.lng_drafter_tree_levels(ctypes.byref(self.D), parent, rank, n, self.tree_row0,
+                                                  int(self.online), self.kappa, self.level_work.data_ptr(),
+                                                  self.level_work.numel(),
+                                                  out.data_ptr() if out is not None else None, self._stream())
+            if rc == 0:
+                self._level_specs[key] = True
+                return self.tok_d[self.tree_row0: self.tree_row0 + n], out
+            if rc != _lib.E_ARG:
+                check(rc, "drafter tree (one launch per depth)")
+            self._level_specs[key] = False     # tree outside the per-depth kernel's limits
         if self.sketch is not None:
             check(self.lib.lng_drafter_tree_shortlist(ctypes.byref(self.D), ctypes.byref(self.sketch), parent, rank, n,
                                                       self.tree_row0, self.work.data_ptr(), self.work.numel(),
@@ -491,7 +512,13 @@ class GpuDrafter:
         return self.tok_d[self.tree_row0: self.tree_row0 + n], out
 
     def tree_error(self) -> int:
-        """Error word of the one-launch tree (synchronises): 0 = ok; non-zero clears it and raises."""
+        """Error word of the one-launch tree or of the launch-per-depth tree (synchronises): 0 = ok;
+        non-zero clears it and raises."""
+        if self.level_work is not None:
+            err = int(self.level_work[4:8].view(torch.int32).item())
+            if err:
+                self.level_work.zero_()
+                raise RuntimeError(f"drafter tree (one launch per depth): a device wait failed (error word {err})")
         if self.tree_work is None:
             return 0
         err = int(self.tree_work[:4].view(torch.int32).item())

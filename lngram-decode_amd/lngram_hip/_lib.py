@@ -26,6 +26,7 @@ _int = ctypes.c_int
 _P64 = ctypes.POINTER(ctypes.c_int64)
 _P32 = ctypes.POINTER(ctypes.c_int32)
 
+E_ARG = -1  # LNG_E_ARG
 ROW_NONE = -2147483648  # LNG_ROW_NONE
 NORM_MODEL, NORM_FUSED = 0, 1  # LNG_NORM_MODEL / LNG_NORM_FUSED
 DR_SYNC_INTS = 4160  # LNG_DR_SYNC_INTS
@@ -115,6 +116,8 @@ SIGNATURES = {
     "lng_drafter_tree_fused_workspace": (ctypes.c_size_t, [_PD]),
     "lng_drafter_tree_fused": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, ctypes.c_uint32, _p, ctypes.c_size_t, _p,
                                       _p, _p]),
+    "lng_drafter_tree_levels_workspace": (ctypes.c_size_t, [_PD]),
+    "lng_drafter_tree_levels": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, _p, ctypes.c_size_t, _p, _p]),
     "lng_tree_accept": (_int, [_p, _p, _p, _i32, _p, _p, _p, _p]),
     "lng_drafter_size": (ctypes.c_size_t, []),
     "lng_drafter_workspace_bytes": (ctypes.c_size_t, [_PD, _i32, _i32, _i32]),

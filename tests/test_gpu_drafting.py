@@ -276,3 +276,45 @@ def test_sdb_shape_graph_tree_step_replays_match_eager(dev):
     node_g = g.tree_step(SPEC16, route_tokens=False, graph=True)[0]
     torch.cuda.synchronize()
     assert torch.equal(node_g, node_e)
+
+
+@pytest.mark.parametrize("online", [False, True])
+def test_sdb_shape_launch_per_step_tree_matches_oracle(dev, online):
+    """SD-B drafter shape, a context with repeated tokens: the one-launch tree (lng_drafter_tree_levels:
+    selection by every block that needs a pick, vocabulary slices held across depths, device-coherent
+    hand-offs) equals the oracle's draft tree over repeated steps with commits between them, for the
+    16-node, default and chain trees (eager and graph-replayed); without online counts it also equals
+    the per-depth readouts of lng_drafter_tree bit for bit (node tokens, node codes, verification
+    gather)."""
+    w = wl.SDB_DRAFT
+    cfg, t = wl.build_draft_bundle(w, seed=0)
+    ctx = wl.make_context(w, seed=1)
+    g1 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 16, online=online)
+    g0 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 16, online=online, levels=False)
+    assert g1.level_work is not None and g0.level_work is None
+    g1.commit(ctx[:-8])
+    g0.commit(ctx[:-8], codes=g1.committed_codes())
+    o = od.DrafterOracle(cfg, t, online=online)
+    o.commit(ctx[:-8], codes=g1.committed_codes())
+    k = 0
+    for spec in (SPEC16, dtree.default_tree(), dtree.chain_tree(5)):
+        for rep in range(2):
+            print(f"[sdb levels tree] online={online} n={spec.n} step {rep}", flush=True)
+            n1, r1 = g1.tree_step(spec, route_tokens=True, graph=rep == 1)
+            n1, r1 = n1.clone(), r1.clone()
+            torch.cuda.synchronize()
+            assert g1.tree_error() == 0
+            assert g1._level_specs[(tuple(spec.parent), tuple(spec.rank))]
+            assert n1.cpu().tolist() == od.draft_tree(o, od.TreeSpec(spec.parent, spec.rank))
+            if not online:
+                n0, r0 = g0.tree_step(spec, route_tokens=True)
+                torch.cuda.synchronize()
+                assert n1.cpu().tolist() == n0.cpu().tolist()
+                assert torch.equal(r1, r0)
+                rows = slice(g1.tree_row0 + 1, g1.tree_row0 + spec.n)
+                assert torch.equal(g1.codes_d[rows], g0.codes_d[rows])
+            nxt = ctx[-8 + k: -7 + k]
+            g1.commit(nxt)
+            g0.commit(nxt, codes=g1.committed_codes()[-1:])
+            o.commit(nxt, codes=g1.committed_codes()[-1:])
+            k += 1
