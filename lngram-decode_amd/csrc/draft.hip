@@ -1918,7 +1918,9 @@ __global__ __launch_bounds__(256) void k_fast_attend(lng_drafter D, FastLevel F,
         sho[oi] = static_cast<uint32_t>(8 * (maxn - n));
       }
       const int sh = 8 * (maxn - 1);
-      uint32_t amax = 0xFFFFFFFFu;
+      // window bytes 0 .. maxn-1 start at the invalid digit; the bytes above the window stay zero so
+      // that each shift leaves room for the newest code in byte maxn-1
+      uint32_t amax = maxn >= 4 ? 0xFFFFFFFFu : ((1u << (8 * maxn)) - 1u);
 #pragma unroll
       for (int k = 0; k < DR_MAXN - 1; ++k)
         if (k < maxn - 1) amax = (amax >> 8) | (pre[k] << sh);

@@ -283,9 +283,9 @@ def test_sdb_shape_launch_per_step_tree_matches_oracle(dev, online):
     """SD-B drafter shape, a context with repeated tokens: the one-launch tree (lng_drafter_tree_levels:
     selection by every block that needs a pick, vocabulary slices held across depths, device-coherent
     hand-offs) equals the oracle's draft tree over repeated steps with commits between them, for the
-    16-node, default and chain trees (eager and graph-replayed); without online counts it also equals
-    the per-depth readouts of lng_drafter_tree bit for bit (node tokens, node codes, verification
-    gather)."""
+    16-node, default and chain trees (eager and graph-replayed), and the per-depth readouts of
+    lng_drafter_tree bit for bit (node tokens, node codes, verification gather); the per-depth chain
+    draft's top-k equals the oracle's."""
     w = wl.SDB_DRAFT
     cfg, t = wl.build_draft_bundle(w, seed=0)
     ctx = wl.make_context(w, seed=1)
@@ -306,13 +306,17 @@ def test_sdb_shape_launch_per_step_tree_matches_oracle(dev, online):
             assert g1.tree_error() == 0
             assert g1._level_specs[(tuple(spec.parent), tuple(spec.rank))]
             assert n1.cpu().tolist() == od.draft_tree(o, od.TreeSpec(spec.parent, spec.rank))
-            if not online:
-                n0, r0 = g0.tree_step(spec, route_tokens=True)
-                torch.cuda.synchronize()
-                assert n1.cpu().tolist() == n0.cpu().tolist()
-                assert torch.equal(r1, r0)
-                rows = slice(g1.tree_row0 + 1, g1.tree_row0 + spec.n)
-                assert torch.equal(g1.codes_d[rows], g0.codes_d[rows])
+            # the per-depth readouts, bit for bit (online counts included: the match window of the
+            # first pair of each counting block once dropped its oldest code)
+            n0, r0 = g0.tree_step(spec, route_tokens=True)
+            torch.cuda.synchronize()
+            assert n1.cpu().tolist() == n0.cpu().tolist()
+            assert torch.equal(r1, r0)
+            rows = slice(g1.tree_row0 + 1, g1.tree_row0 + spec.n)
+            assert torch.equal(g1.codes_d[rows], g0.codes_d[rows])
+            if rep == 0:
+                d0, do = g0.draft(1, topk=4), o.draft(1, topk=4)
+                assert d0.topk_ids.tolist() == do.topk_ids.tolist()
             nxt = ctx[-8 + k: -7 + k]
             g1.commit(nxt)
             g0.commit(nxt, codes=g1.committed_codes()[-1:])
