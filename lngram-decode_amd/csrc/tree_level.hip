@@ -46,8 +46,9 @@ constexpr int TL_NA = TL_MAXP * TL_QH;  // A blocks
 constexpr int TL_MAXN = 32;       // tree nodes
 constexpr int TL_MAXL = 8;        // depths with parents
 constexpr int TL_NLB = TL_MAXL + 1;  // depth buffers
-constexpr int TL_NJ = 5;          // vocabulary rows per lane group (32 lane groups per block)
-constexpr int TL_VS = 32 * TL_NJ; // vocabulary rows per V block
+constexpr int TL_VS = 160;        // vocabulary rows per V block (64-row MFMA groups: 64, 64, 32)
+constexpr int TL_VG = 3;          // 64-row groups of a V block
+constexpr int TL_VK = TL_I / TL_WAVES;  // features per wave in the vocabulary product
 constexpr int TL_MAXVB = 224;     // V blocks: V <= 224 * 160
 constexpr int TL_MINGB = 8;       // G blocks at least
 constexpr int TL_MAXGRID = 256;
@@ -56,6 +57,7 @@ constexpr int TL_NI = 16;         // count-bearing tokens inline in a record
 constexpr int TL_RW = 64;         // words per record
 constexpr int TL_AP = TL_DT + TL_HD;  // pairs per A record: Y[256], then o[64]
 constexpr int TL_PL = 4096;       // listed pairs of a V block (more: re-listed per depth in rounds)
+constexpr int TL_KL = 48;         // listed pairs whose match keys a V block keeps in LDS
 constexpr long long TL_SPIN_TICKS = 2000000;  // 20 ms
 constexpr int TL_XS = TL_DT + 8;  // LDS row of one route token (bf16, padded)
 constexpr int TL_NST = 16;        // phase stamps per block and depth
@@ -256,9 +258,13 @@ __device__ bool tl_wait_ready(int nvb, const uint32_t* rdy, int lev, uint32_t ta
 // The wave's top-KM over every lane's sorted list (value desc, id asc): KM rounds of (wave max, the
 // smallest id holding it, its removal).  sv/si receive it in order, identical in every lane
 // ((-inf, INT_MAX) past the candidates).  Ids are distinct across the wave.  Call from converged code.
-__device__ __forceinline__ void tl_wave_topk(TlTop& tk, float* sv, int* si) {
+__device__ __forceinline__ void tl_wave_topk(TlTop& tk, float* sv, int* si, int kn = TL_KM) {
 #pragma unroll
   for (int k = 0; k < TL_KM; ++k) {
+    if (k >= kn) {  // (kn is wave-uniform)
+      sv[k] = -INFINITY, si[k] = INT_MAX;
+      continue;
+    }
     const float wm = wave_max(tk.v[0]);
     const int wid = tl_wave_min_i(tk.v[0] == wm ? tk.i[0] : INT_MAX);
     sv[k] = wid == INT_MAX ? -INFINITY : wm;
@@ -267,71 +273,76 @@ __device__ __forceinline__ void tl_wave_topk(TlTop& tk, float* sv, int* si) {
   }
 }
 
-// Top-KM of parent `slot` of depth `lev` from the V records, ranked as k_fast_logits' selection
-// ranks them: logits, or the online mixture (1 - lam) softmax + lam count / total.  Whole block;
-// ids land in S.sel (-1 past the candidates).  Thread t takes V block t's record: its top-KM of
-// the tokens without counts (already in order) and its count-bearing tokens; each wave ranks its
-// lanes' lists, and wave 0 ranks the waves' lists.
+// Top-K (K <= KM) of parent `slot` of depth `lev` from the V records, ranked as k_fast_logits'
+// selection ranks them: logits, or the online mixture (1 - lam) softmax + lam count / total.  Whole
+// block; ids land in S.sel (-1 past the candidates).  Two threads per V block's record: the even one
+// takes the record's header, its top-KM of the tokens without counts and the even count-bearing
+// entries, the odd one the odd entries; each wave ranks its lanes' lists, wave 0 the waves' lists.
 __device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t* spill, float denom, int lev,
                           int slot, TlSelLds& S, long long* stp = nullptr) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  const int nvb = T.nvb;
-  const bool ok = t < nvb;
+  const int rec = t >> 1, h = t & 1;
+  const bool ok = rec < T.nvb;
   const bool online = T.online != 0;
   // one descriptor for the slot's records (a buffer descriptor is taken from the first lane), the
-  // record of V block t at a per-lane offset; the count-bearing entries only with online counts
+  // record at a per-lane offset; the count-bearing entries only with online counts
   const size_t r0 = (static_cast<size_t>(lev) * TL_MAXP + slot) * TL_MAXVB;
   const __amdgpu_buffer_rsrc_t rb = dev_buf(vrec + r0 * TL_RW, TL_MAXVB * TL_RW * 4u);
   const __amdgpu_buffer_rsrc_t sb = dev_buf(spill + r0 * (TL_VS * 3), TL_MAXVB * TL_VS * 12u);
-  const uint32_t roff = 4u * TL_RW * static_cast<uint32_t>(ok ? t : 0);
+  const uint32_t roff = 4u * TL_RW * static_cast<uint32_t>(ok ? rec : 0);
   u32x4 q[TL_RW / 4];
 #pragma unroll
   for (int k = 0; k < TL_RW / 4; ++k)
     q[k] = (ok && (k < 3 || online)) ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, roff + 16u * k, 0, CPOL_SC1))
                                      : u32x4{0u, 0u, 0u, 0u};
   auto word = [&](int k) { return q[k >> 2][k & 3]; };  // constant k: a register
-  if (stp && t == 0) stp[8] = wall_clock64();
-  const float m = ok ? __uint_as_float(word(0)) : -INFINITY;
-  const float s = ok ? __uint_as_float(word(1)) : 0.f;
-  const int tot = ok ? static_cast<int>(word(2)) : 0;
-  const int nc = ok && online ? min(static_cast<int>(word(3)), TL_VS) : 0;
-  const float wm0 = wave_max(m);
-  const int totw = tl_wave_sum_i(tot);
-  if (lane == 0) S.rv[w] = wm0, S.rt[w] = totw;
+  // max, sum of exponentials and online total over the records (even lanes), merged per wave and
+  // then across the waves in a fixed order
+  const bool head = ok && h == 0;
+  const float m = head ? __uint_as_float(word(0)) : -INFINITY;
+  const float mw = wave_max(m);
+  const float sw = wave_sum(m == -INFINITY ? 0.f : __uint_as_float(word(1)) * expf(m - mw));
+  const int totw = tl_wave_sum_i(head ? static_cast<int>(word(2)) : 0);
+  if (lane == 0) S.rv[w] = mw, S.rs[w] = sw, S.rt[w] = totw;
   __syncthreads();
+  if (stp && t == 0) stp[8] = wall_clock64();
   float M = S.rv[0];
   int totb = S.rt[0];
 #pragma unroll
   for (int k = 1; k < TL_WAVES; ++k) M = fmaxf(M, S.rv[k]), totb += S.rt[k];
-  const float sw_ = wave_sum(m == -INFINITY ? 0.f : s * expf(m - M));
-  if (lane == 0) S.rs[w] = sw_;
-  __syncthreads();
   float Ssum = 0.f;
 #pragma unroll
-  for (int k = 0; k < TL_WAVES; ++k) Ssum += S.rs[k];
+  for (int k = 0; k < TL_WAVES; ++k) Ssum += S.rv[k] == -INFINITY ? 0.f : S.rs[k] * expf(S.rv[k] - M);
   const float tj = online ? static_cast<float>(totb) : 0.f;
   const float n_eff = tj / denom;
   const float lam = tj > 0.f ? n_eff / (n_eff + T.kappa) : 0.f;
   const float mix_a = (1.f - lam) / Ssum, mix_b = tj > 0.f ? lam / tj : 0.f;
   // the record's top-KM (inserted: values that round equal after the mixture rank by id), then the
-  // count-bearing tokens: inline entries (as far as the wave's largest count reaches) and the spill area
+  // count-bearing entries of this lane's parity (as far as the wave's largest share reaches), then
+  // the spill area
   TlTop tk;
   tk.clear();
+  if (head)
 #pragma unroll
-  for (int k = 0; k < TL_KM; ++k) {
-    const int id = static_cast<int>(word(4 + TL_KM + k));
-    if (ok && id >= 0) tk.insert(online ? mix_a * expf(__uint_as_float(word(4 + k)) - M) : __uint_as_float(word(4 + k)), id);
-  }
-  const int ncw = online ? static_cast<int>(wave_max(static_cast<float>(nc))) : 0;
+    for (int k = 0; k < TL_KM; ++k) {
+      const int id = static_cast<int>(word(4 + TL_KM + k));
+      if (id >= 0) tk.insert(online ? mix_a * expf(__uint_as_float(word(4 + k)) - M) : __uint_as_float(word(4 + k)), id);
+    }
+  const int nc = ok && online ? min(static_cast<int>(word(3)), TL_VS) : 0;
+  const int mine = (min(nc, TL_NI) + 1 - h) >> 1;  // entries h, h + 2, ... below min(nc, NI)
+  const int mw_n = online ? static_cast<int>(wave_max(static_cast<float>(mine))) : 0;
 #pragma unroll
-  for (int e = 0; e < TL_NI; ++e) {
-    if (e < ncw && e < nc)
-      tk.insert(fmaf(mix_b, static_cast<float>(static_cast<int>(word(14 + 3 * e))),
-                     mix_a * expf(__uint_as_float(word(13 + 3 * e)) - M)),
-                static_cast<int>(word(12 + 3 * e)));
+  for (int u = 0; u < TL_NI / 2; ++u) {
+    if (u < mw_n && u < mine) {
+      const uint32_t id = h ? word(15 + 6 * u) : word(12 + 6 * u);
+      const uint32_t lb = h ? word(16 + 6 * u) : word(13 + 6 * u);
+      const uint32_t c = h ? word(17 + 6 * u) : word(14 + 6 * u);
+      tk.insert(fmaf(mix_b, static_cast<float>(static_cast<int>(c)), mix_a * expf(__uint_as_float(lb) - M)),
+                static_cast<int>(id));
+    }
   }
-  const uint32_t soff = 12u * TL_VS * static_cast<uint32_t>(ok ? t : 0);
-  for (int e = TL_NI; e < nc; ++e) {
+  const uint32_t soff = 12u * TL_VS * static_cast<uint32_t>(ok ? rec : 0);
+  for (int e = TL_NI + h; e < nc; e += 2) {
     const int id = static_cast<int>(tl_ld_w(sb, soff + 12u * e));
     const float l = __uint_as_float(tl_ld_w(sb, soff + 12u * e + 4u));
     const int c = static_cast<int>(tl_ld_w(sb, soff + 12u * e + 8u));
@@ -341,7 +352,7 @@ __device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t*
   // each wave's top-KM, then wave 0 ranks the waves' lists (lane l holds wave l / KM's l % KM-th)
   float sv[TL_KM];
   int si[TL_KM];
-  tl_wave_topk(tk, sv, si);
+  tl_wave_topk(tk, sv, si, T.K);
   if (lane < TL_KM) {
     float vv = sv[0];
     int ii = si[0];
@@ -356,7 +367,7 @@ __device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t*
     TlTop tw;
     tw.clear();
     if (lane < TL_WAVES * TL_KM) tw.v[0] = S.cv[lane], tw.i[0] = S.ci[lane];
-    tl_wave_topk(tw, sv, si);
+    tl_wave_topk(tw, sv, si, T.K);
     if (lane < TL_KM) {
       int ii = si[0];
 #pragma unroll
@@ -387,8 +398,12 @@ struct TlALds {
 struct TlVLds {
   float ro[TL_MAXP][TL_DT];
   float lt[TL_MAXP][TL_VS];
+  f32x4 lpart[TL_WAVES][TL_VG * 64];  // per wave: (row, 4 parents) partial logits over its features
   int32_t sc[TL_MAXP][TL_VS];
   uint32_t qry[TL_MAXP][TL_MAXR];
+  uint16_t keys[TL_KL][TL_MAXR];  // match keys of the first listed pairs: 12-bit order-3 key, bit 12 order 2
+                                  // usable (pair >= 1), bit 13 order 3 usable (pair >= 2)
+  uint8_t knt[TL_KL];             // their next tokens, relative to the slice
   int32_t list[TL_PL];
   int32_t nmatch;
   int32_t tot[TL_MAXP][TL_WAVES];
@@ -721,16 +736,17 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
     const int vb = b - TL_NA;
     const int64_t v0 = static_cast<int64_t>(vb) * TL_VS;
     const int64_t V = D.V;
-    const int kg = t & 15, rg = t >> 4;
-    // lut_out rows v0 + rg + 32 jj, features 16 kg .. 16 kg + 15: held for every depth
-    f32x4 av[TL_NJ][4];
+    // lut_out rows v0 + 64 g + lane (g < 3), features TL_VK w .. + TL_VK: the A operands of the
+    // wave's 4x4x1 MFMAs (lane 4b + i holds row 4b + i of block b), held for every depth
+    f32x4 av[TL_VG][TL_VK / 4];
 #pragma unroll
-    for (int jj = 0; jj < TL_NJ; ++jj) {
-      const int64_t v = v0 + rg + 32 * jj;
+    for (int g = 0; g < TL_VG; ++g) {
+      const int i = 64 * g + lane;
+      const int64_t v = v0 + i;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        av[jj][q] = v < V ? *reinterpret_cast<const f32x4*>(D.lut_out + v * TL_I + 16 * kg + 4 * q)
-                          : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int q = 0; q < TL_VK / 4; ++q)
+        av[g][q] = (i < TL_VS && v < V) ? *reinterpret_cast<const f32x4*>(D.lut_out + v * TL_I + TL_VK * w + 4 * q)
+                                       : f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const bool online = T.online != 0;
     const int npairs = L - 1;
@@ -753,6 +769,18 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
     __syncthreads();
     const bool overflow = S.nmatch > TL_PL;
     const int nlist = min(S.nmatch, TL_PL);
+    const int nkey = min(nlist, TL_KL);
+    // match keys of the first listed pairs, formed once for every depth (committed codes only)
+    for (int e = t; e < nkey * R; e += TL_THREADS) {
+      const int li = e / R, r = e % R;
+      const int q = S.list[li];
+      const int c0 = codes_d[static_cast<int64_t>(q) * R + r] & 15;
+      const int c1 = q >= 1 ? codes_d[static_cast<int64_t>(q - 1) * R + r] & 15 : 0;
+      const int c2 = q >= 2 ? codes_d[static_cast<int64_t>(q - 2) * R + r] & 15 : 0;
+      S.keys[li][r] = static_cast<uint16_t>(c2 | (c1 << 4) | (c0 << 8) | (q >= 1 ? 1 << 12 : 0) | (q >= 2 ? 1 << 13 : 0));
+    }
+    for (int li = t; li < nkey; li += TL_THREADS) S.knt[li] = static_cast<uint8_t>(toks_d[S.list[li] + 1] - v0);
+    __syncthreads();
     const __amdgpu_buffer_rsrc_t rdb = dev_buf(W.rdy, TL_NLB * TL_MAXVB * 4u);
     for (int lev = 0; lev < T.nlev; ++lev) {
       const int P = T.lev_np[lev];
@@ -782,30 +810,38 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
         __syncthreads();
         stamp(lev, 1);
         // matches of the listed pairs: item (listed pair, route r); the keys of the window ending at pair q
-        auto count = [&](int nl) {
+        // items (listed pair, route); pairs li < k0 take their keys from LDS
+        auto count = [&](int nl, int k0) {
           for (int e = t; e < nl * R; e += TL_THREADS) {
             const int li = e / R, r = e % R;
-            const int q = S.list[li];
-            const int c0 = codes_d[static_cast<int64_t>(q) * R + r] & 15;
-            const int c1 = q >= 1 ? codes_d[static_cast<int64_t>(q - 1) * R + r] & 15 : 0;
-            const int c2 = q >= 2 ? codes_d[static_cast<int64_t>(q - 2) * R + r] & 15 : 0;
-            const uint32_t k3 = static_cast<uint32_t>(c2 | (c1 << 4) | (c0 << 8));
-            const int64_t nt = toks_d[q + 1];
+            uint32_t k3, nt;
+            if (li < k0) {
+              k3 = S.keys[li][r];
+              nt = S.knt[li];
+            } else {
+              const int q = S.list[li];
+              const int c0 = codes_d[static_cast<int64_t>(q) * R + r] & 15;
+              const int c1 = q >= 1 ? codes_d[static_cast<int64_t>(q - 1) * R + r] & 15 : 0;
+              const int c2 = q >= 2 ? codes_d[static_cast<int64_t>(q - 2) * R + r] & 15 : 0;
+              k3 = static_cast<uint32_t>(c2 | (c1 << 4) | (c0 << 8) | (q >= 1 ? 1 << 12 : 0) | (q >= 2 ? 1 << 13 : 0));
+              nt = static_cast<uint32_t>(toks_d[q + 1] - v0);
+            }
 #pragma unroll
             for (int p = 0; p < TL_MAXP; ++p) {
               if (p >= P) break;
               const uint32_t qv = S.qry[p][r];
-              const int mt = (((qv >> 12) & 1u) && q >= 1 && (k3 >> 4) == ((qv >> 4) & 0xffu) ? 1 : 0) +
-                             (((qv >> 13) & 1u) && q >= 2 && k3 == (qv & 0xfffu) ? 1 : 0);
+              // order 2: key (t - 1, t) against query slots (1, 2); order 3: all three
+              const int mt = ((qv & k3 & (1u << 12)) && ((k3 >> 4) & 0xffu) == ((qv >> 4) & 0xffu) ? 1 : 0) +
+                             ((qv & k3 & (1u << 13)) && (k3 & 0xfffu) == (qv & 0xfffu) ? 1 : 0);
               if (mt) {
-                atomicAdd(&S.sc[p][static_cast<int>(nt - v0)], mt);
+                atomicAdd(&S.sc[p][nt], mt);
                 tot_p[p] += mt;
               }
             }
           }
         };
         if (!overflow) {
-          count(nlist);
+          count(nlist, nkey);
         } else {
           // more listed pairs than the list holds: list and count them in rounds
           for (int base = 0; base < npairs; base += TL_PL) {
@@ -814,7 +850,7 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
             __syncthreads();
             list_pairs(base, TL_PL);
             __syncthreads();
-            count(min(S.nmatch, TL_PL));
+            count(min(S.nmatch, TL_PL), 0);
           }
         }
       }
@@ -822,6 +858,18 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
       // A records of every (parent, head); re-read what is still stale
       const __amdgpu_buffer_rsrc_t ab =
           dev_buf(W.arec + static_cast<size_t>(lev) * TL_MAXP * TL_QH * TL_AP, TL_MAXP * TL_QH * TL_AP * 8u);
+      // a light probe first (one pair per record: the last value its head's block writes), then the
+      // bulk read of every (parent, head) record
+      if (w == 0 && !failed) {
+        const long long t0 = wall_clock64();
+        for (;;) {
+          const bool okp =
+              lane >= TL_QH * P || static_cast<uint32_t>(tl_ld_pair(ab, 8u * (lane * TL_AP + TL_AP - 1)) >> 32) == tag;
+          if (__ballot(!okp) == 0 || wall_clock64() - t0 > TL_SPIN_TICKS) break;
+          __builtin_amdgcn_s_sleep(1);
+        }
+      }
+      __syncthreads();
       // thread t < 256 = feature e: o[e] (head e / 64) and Y[e] of every head, per parent
       float ov[TL_MAXP], yv[TL_MAXP];
       {
@@ -885,30 +933,36 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
       __syncthreads();
       if (t < TL_DT)
 #pragma unroll
-        for (int p = 0; p < TL_MAXP; ++p)
-          if (p < P) S.ro[p][t] = S.rn[p] * ov[p];
+        for (int p = 0; p < TL_MAXP; ++p) S.ro[p][t] = p < P ? S.rn[p] * ov[p] : 0.f;
       __syncthreads();
-      // logits of rows rg + 32 jj for each parent: 16-feature partial dot, summed over the lane group
-      for (int p = 0; p < P; ++p) {
-        float rv[16];
+      // logits: D[row][parent] over the wave's features with 4x4x1 MFMAs (16 blocks of 4 rows x 4
+      // parents; B = ro[lane % 4][k]), then the waves' partials summed in wave order
+      {
+        f32x4 acc[TL_VG];
 #pragma unroll
-        for (int k = 0; k < 16; k += 4) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(&S.ro[p][16 * kg + k]);
-          rv[k] = x[0], rv[k + 1] = x[1], rv[k + 2] = x[2], rv[k + 3] = x[3];
+        for (int g = 0; g < TL_VG; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const float* rop = &S.ro[lane & 3][TL_VK * w];
+#pragma unroll
+        for (int q = 0; q < TL_VK / 4; ++q) {
+          const f32x4 bq = *reinterpret_cast<const f32x4*>(rop + 4 * q);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int g = 0; g < TL_VG; ++g) acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(av[g][q][e], bq[e], acc[g], 0, 0, 0);
         }
+        // lane 4b + n, register i: row 64 g + 4b + i, parent n
 #pragma unroll
-        for (int jj = 0; jj < TL_NJ; ++jj) {
-          float a = 0.f;
+        for (int g = 0; g < TL_VG; ++g) S.lpart[w][64 * g + lane] = acc[g];
+      }
+      __syncthreads();
+      for (int e = t; e < TL_MAXP * TL_VS; e += TL_THREADS) {
+        const int p = e / TL_VS, i = e % TL_VS;
+        const int blk = i >> 2, ii = i & 3;  // row i = 64 g + 4 b + ii sits in lane 4 b + p of group g
+        const int g = blk >> 4, bb = blk & 15;
+        float a = 0.f;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            a = fmaf(av[jj][q][0], rv[4 * q], a);
-            a = fmaf(av[jj][q][1], rv[4 * q + 1], a);
-            a = fmaf(av[jj][q][2], rv[4 * q + 2], a);
-            a = fmaf(av[jj][q][3], rv[4 * q + 3], a);
-          }
-          a = tl_row16_sum(a);
-          if (kg == 15) S.lt[p][rg + 32 * jj] = a;
-        }
+        for (int ww = 0; ww < TL_WAVES; ++ww) a += S.lpart[ww][64 * g + 4 * bb + p][ii];
+        S.lt[p][i] = a;
       }
       __syncthreads();
       stamp(lev, 4);
