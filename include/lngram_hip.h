@@ -12,7 +12,8 @@
  *         hipBLASLt, chosen by shape alone: one handle per device and one matmul
  *         plan per (device, M, N, K), made on the first call of that shape (the
  *         library allocates them); a shape with no plan runs the MFMA kernel;
- *       * lng_drafter_tree_fused caches its cooperative grid size per device;
+ *       * lng_drafter_tree_fused caches its cooperative grid size per device, and
+ *         lng_drafter_tree_levels its resident grid size;
  *       * lng_ssm_scan_static uses a static device array per GPU (its own
  *         comment gives the limit), located once per device.
  *   - lng_last_error() returns a thread-local message for the last failure.
@@ -566,7 +567,8 @@ int lng_drafter_tree_fused(const lng_drafter* D, const int32_t* parent, const in
  * arrive through device-coherent (value, tag) pairs (bounded waits).  `work` holds
  * lng_drafter_tree_levels_workspace(D) bytes, zero before the first call and kept between calls
  * (its first word counts the calls; the int32 at byte offset 4 is a sticky error word: non-zero =
- * a wait timed out; zero the workspace after an error).  The workspace size is 0, and the call
+ * a wait timed out; zero the workspace after an error; a non-zero int32 at byte offset 8 asks for
+ * per-block phase times of the 100 MHz clock in the workspace's last section).  The workspace size is 0, and the call
  * returns LNG_E_ARG without launching, for a drafter or tree outside the limits above
  * (lng_drafter_tree runs those). */
 size_t lng_drafter_tree_levels_workspace(const lng_drafter* D);
