@@ -59,7 +59,6 @@ constexpr int TL_AP = TL_DT + TL_HD;  // pairs per A record: Y[256], then o[64]
 constexpr int TL_PL = 4096;       // listed pairs of a V block (more: re-listed per depth in rounds)
 constexpr int TL_KL = 48;         // listed pairs whose match keys a V block keeps in LDS
 constexpr long long TL_SPIN_TICKS = 2000000;  // 20 ms
-constexpr int TL_XS = TL_DT + 8;  // LDS row of one route token (bf16, padded)
 constexpr int TL_NST = 16;        // phase stamps per block and depth
 
 struct TlPlan {
@@ -148,11 +147,19 @@ __device__ __forceinline__ int tl_wave_sum_i(int v) {
 }
 
 // Block-wide sum / max of one value per thread through red[TL_WAVES] (every thread receives it).
+// Block barrier that orders the block's LDS accesses only: global stores still in flight are not
+// waited for (a hand-off to other blocks is tagged, so no block reads its own global stores back)
+__device__ __forceinline__ void tl_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float tl_block_sum(float v, float* red) {
   v = wave_sum(v);
-  __syncthreads();
+  tl_sync();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  tl_sync();
   float s = 0.f;
 #pragma unroll
   for (int k = 0; k < TL_WAVES; ++k) s += red[k];
@@ -160,9 +167,9 @@ __device__ __forceinline__ float tl_block_sum(float v, float* red) {
 }
 __device__ __forceinline__ float tl_block_max(float v, float* red) {
   v = wave_max(v);
-  __syncthreads();
+  tl_sync();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
+  tl_sync();
   float m = red[0];
 #pragma unroll
   for (int k = 1; k < TL_WAVES; ++k) m = fmaxf(m, red[k]);
@@ -381,11 +388,11 @@ __device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t*
 
 // ------------------------------------------------------------------ LDS of the three roles
 struct TlALds {
-  bf16 xs[TL_MAXR][TL_XS];
+  alignas(16) float gram[TL_HD][TL_I];  // Gram rows qh*64 .. qh*64 + 63 of the block's head
   float qk[TL_DT];
   float sc[TL_MAXR], sx[TL_MAXR], wr[TL_MAXR];
-  float red[TL_WAVES][TL_DT];  // U partials per route eighth; then Y partials per eighth of o
-  float opart[64][TL_HD];      // o' partials per input group
+  float red[TL_THREADS / 16][TL_DT];  // U partials per route row; then Y partials per eighth of o
+  float opart[TL_WAVES][TL_HD];  // o' partials per input run
   float un[TL_DT];
   float o[TL_HD];
   int32_t rows[TL_MAXR][2];
@@ -520,18 +527,19 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
     TlALds& A = lds.a;
     const int slot = b % TL_MAXP, qh = b / TL_MAXP;
     const int h = qh / (TL_QH / D.kv_heads);
-    // the head's value weight (bf16 Wv[h]^T rows 4 ig .. 4 ig + 3, outputs 8 og .. 8 og + 7) and
-    // Gram rows (qh*64 + 8 cq .. + 7, features 4 eq .. 4 eq + 3), once for every depth
-    const int og = t & 7, ig = t >> 3, eq = t & 63, cq = t >> 6;
-    bf16x8 wv8[4];
+    // the head's value weight (bf16 Wv[h][oc][32 iq .. 32 iq + 31], packed in pairs) and Gram rows
+    // (qh*64 + 8 cq .. + 7, features 4 eq .. 4 eq + 3), once for every depth
+    const int oc = t & 63, iq = t >> 6, eq = t & 63, cq = t >> 6;
+    uint32_t wvp[16];
+    {
+      const uint16_t* wsrc = static_cast<const uint16_t*>(D.wv_t) + (static_cast<int64_t>(h) * TL_DT + 32 * iq) * TL_HD + oc;
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      wv8[q] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(D.wv_t) +
-                                                (static_cast<int64_t>(h) * TL_DT + 4 * ig + q) * TL_HD + 8 * og);
-    f32x4 gv[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q)
-      gv[q] = *reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(qh * TL_HD + 8 * cq + q) * TL_I + 4 * eq);
+      for (int k = 0; k < 16; ++k)
+        wvp[k] = static_cast<uint32_t>(wsrc[(2 * k) * TL_HD]) | (static_cast<uint32_t>(wsrc[(2 * k + 1) * TL_HD]) << 16);
+    }
+    for (int e = t; e < TL_HD * TL_I / 4; e += TL_THREADS)
+      reinterpret_cast<f32x4*>(&A.gram[0][0])[e] =
+          reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(qh * TL_HD) * TL_I)[e];
     const float mnorm = t < TL_DT ? D.mem_norm[t] : 0.f;
     for (int lev = 0; lev < T.nlev; ++lev) {
       const int P = T.lev_np[lev];
@@ -584,60 +592,66 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
         }
       }
       stamp(lev, 3);
-      // gather the window's rows: route r, order oi, 16-byte piece c (R <= 192: 12 pieces per thread)
-      {
-        u32x4 pv[12];
+      // the window's rows straight into registers: thread t holds features fo .. fo + 15 (fo = 128 oi +
+      // 16 pc: order oi, 16-byte pieces 2 pc and 2 pc + 1) of routes rs + 32 u (R <= 192: 6 routes),
+      // so the 16 lanes of a DPP row hold one route
+      const int pc = t & 7, oi = (t >> 3) & 1, rs = t >> 4;
+      const int fo = oi * TL_MD + 16 * pc;
+      // the thread's routes rs + 32 u < R are u < nu; per-route LDS entries at constant offsets from
+      // one address (no per-route address registers)
+      const int nu = R > rs ? (R - rs + 31) >> 5 : 0;
+      const int32_t* const rowp = &A.rows[rs][oi];
+      float* const sxp = &A.sx[rs];
+      float* const scp = &A.sc[rs];
+      const float* const wrp = &A.wr[rs];
+      u32x4 pv[6][2];
 #pragma unroll
-        for (int u = 0; u < 12; ++u) {
-          const int e = t + TL_THREADS * u;
-          const int r = e >> 5, oi = (e >> 4) & 1, c = e & 15;
-          const int32_t rw = r < R ? A.rows[r][oi] : -1;
-          pv[u] = rw >= 0 ? *reinterpret_cast<const u32x4*>((oi ? tab3 : tab2) + static_cast<int64_t>(rw) * TL_MD + 8 * c)
-                          : u32x4{0u, 0u, 0u, 0u};
-        }
+      for (int u = 0; u < 6; ++u) {
+        const int32_t rw = u < nu ? rowp[64 * u] : -1;
+        const bf16* src = (oi ? tab3 : tab2) + static_cast<int64_t>(rw < 0 ? 0 : rw) * TL_MD + 16 * pc;
 #pragma unroll
-        for (int u = 0; u < 12; ++u) {
-          const int e = t + TL_THREADS * u;
-          const int r = e >> 5, oi = (e >> 4) & 1, c = e & 15;
-          if (r < R) *reinterpret_cast<u32x4*>(&A.xs[r][oi * TL_MD + 8 * c]) = pv[u];
-        }
+        for (int k = 0; k < 2; ++k)
+          pv[u][k] = rw >= 0 ? *reinterpret_cast<const u32x4*>(src + 8 * k) : u32x4{0u, 0u, 0u, 0u};
       }
-      __syncthreads();
       stamp(lev, 4);
-      // scores: 16 lanes per route, lane part p covers features 16 p .. 16 p + 15
+      // scores: each route's sum of squares and query-key dot, summed over its DPP row
       {
-        const int p = t & 15, rg = t >> 4;
         float qv[16];
 #pragma unroll
         for (int k = 0; k < 16; k += 4) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(&A.qk[16 * p + k]);
+          const f32x4 v = *reinterpret_cast<const f32x4*>(&A.qk[fo + k]);
           qv[k] = v[0], qv[k + 1] = v[1], qv[k + 2] = v[2], qv[k + 3] = v[3];
         }
-        for (int r0 = 0; r0 < R; r0 += TL_THREADS / 16) {
-          const int r = r0 + rg;
-          const int rr = r < R ? r : R - 1;
-          const u32x4 a = *reinterpret_cast<const u32x4*>(&A.xs[rr][16 * p]);
-          const u32x4 c = *reinterpret_cast<const u32x4*>(&A.xs[rr][16 * p + 8]);
-          const uint32_t wd[8] = {a[0], a[1], a[2], a[3], c[0], c[1], c[2], c[3]};
-          float ss = 0.f, dot = 0.f;
+        float s2[6], d2[6];
+#pragma unroll
+        for (int u = 0; u < 6; ++u) {
+          float sa = 0.f, da = 0.f;
 #pragma unroll
           for (int k = 0; k < 8; ++k) {
-            const float x0 = __uint_as_float(wd[k] << 16), x1 = __uint_as_float(wd[k] & 0xffff0000u);
-            ss = fmaf(x0, x0, ss);
-            ss = fmaf(x1, x1, ss);
-            dot = fmaf(qv[2 * k], x0, dot);
-            dot = fmaf(qv[2 * k + 1], x1, dot);
+            const uint32_t wd = pv[u][k >> 2][k & 3];
+            const float x0 = __uint_as_float(wd << 16), x1 = __uint_as_float(wd & 0xffff0000u);
+            sa = fmaf(x0, x0, sa);
+            sa = fmaf(x1, x1, sa);
+            da = fmaf(qv[2 * k], x0, da);
+            da = fmaf(qv[2 * k + 1], x1, da);
           }
-          ss = tl_row16_sum(ss);
-          dot = tl_row16_sum(dot);
-          if (p == 15 && r < R) {
-            const float sv = 1.0f / sqrtf(ss / static_cast<float>(TL_DT) + D.mem_eps);
-            A.sx[r] = sv;
-            A.sc[r] = sv * dot;
+          s2[u] = sa, d2[u] = da;
+          __builtin_amdgcn_sched_barrier(0);  // one route at a time: the unpacked words stay few
+        }
+#pragma unroll
+        for (int u = 0; u < 6; ++u) s2[u] = tl_row16_sum(s2[u]), d2[u] = tl_row16_sum(d2[u]);
+        if ((t & 15) == 15) {
+#pragma unroll
+          for (int u = 0; u < 6; ++u) {
+            if (u < nu) {
+              const float sv = 1.0f / sqrtf(s2[u] / static_cast<float>(TL_DT) + D.mem_eps);
+              sxp[32 * u] = sv;
+              scp[32 * u] = sv * d2[u];
+            }
           }
         }
       }
-      __syncthreads();
+      tl_sync();
       stamp(lev, 5);
       // softmax over the routes (the sink enters through the weight below)
       const float scv = t < R ? A.sc[t] : -INFINITY;
@@ -649,63 +663,73 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
       const float Mx = fmaxf(b0, m);
       const float fex = expf(m - Mx);
       const float wgt = fex / fmaf(l, fex, expf(b0 - Mx));
-      // U[i] = sum_r wr[r] x_r[i]: thread (features 4 fq .. 4 fq + 3, route eighth rq)
+      // U[i] = sum_r wr[r] x_r[i]: the thread's routes, then the 32 route rows of the block
       {
-        const int fq = t & 63, rq = t >> 6;
-        const int rn = (R + TL_WAVES - 1) / TL_WAVES, rb = rq * rn, re = min(R, rb + rn);
-        float u0 = 0.f, u1 = 0.f, u2 = 0.f, u3 = 0.f;
-        for (int r = rb; r < re; ++r) {
-          const uint2 xv = *reinterpret_cast<const uint2*>(&A.xs[r][4 * fq]);
-          const float wv = A.wr[r];
-          u0 = fmaf(wv, __uint_as_float(xv.x << 16), u0);
-          u1 = fmaf(wv, __uint_as_float(xv.x & 0xffff0000u), u1);
-          u2 = fmaf(wv, __uint_as_float(xv.y << 16), u2);
-          u3 = fmaf(wv, __uint_as_float(xv.y & 0xffff0000u), u3);
+        float ua[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) ua[k] = 0.f;
+#pragma unroll
+        for (int u = 0; u < 6; ++u) {
+          const float wv = u < nu ? wrp[32 * u] : 0.f;
+#pragma unroll
+          for (int k = 0; k < 8; ++k) {
+            const uint32_t wd = pv[u][k >> 2][k & 3];
+            ua[2 * k] = fmaf(wv, __uint_as_float(wd << 16), ua[2 * k]);
+            ua[2 * k + 1] = fmaf(wv, __uint_as_float(wd & 0xffff0000u), ua[2 * k + 1]);
+          }
         }
-        *reinterpret_cast<f32x4*>(&A.red[rq][4 * fq]) = f32x4{u0, u1, u2, u3};
+#pragma unroll
+        for (int k = 0; k < 16; k += 4)
+          *reinterpret_cast<f32x4*>(&A.red[rs][fo + k]) = f32x4{ua[k], ua[k + 1], ua[k + 2], ua[k + 3]};
       }
-      __syncthreads();
+      tl_sync();
       if (t < TL_DT) {
         float u = 0.f;
 #pragma unroll
-        for (int k = 0; k < TL_WAVES; ++k) u += A.red[k][t];
+        for (int k = 0; k < TL_THREADS / 16; ++k) u += A.red[k][t];
         A.un[t] = u * mnorm;  // mem_norm . U
       }
-      __syncthreads();
+      tl_sync();
       stamp(lev, 6);
-      // o'[c] = sum_i Wv[h][c][i] un[i]: thread (outputs 8 og .., inputs 4 ig ..)
+      // o'[c] = sum_i Wv[h][c][i] un[i]: thread (output oc, inputs 32 iq .. 32 iq + 31), then the
+      // eight input runs
       {
-        float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        float acc = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float uq = A.un[4 * ig + q];
+        for (int k = 0; k < 32; k += 4) {
+          const f32x4 uq = *reinterpret_cast<const f32x4*>(&A.un[32 * iq + k]);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] = fmaf(static_cast<float>(wv8[q][e]), uq, acc[e]);
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t pr = wvp[(k + e) >> 1];
+            const float wf = ((k + e) & 1) ? __uint_as_float(pr & 0xffff0000u) : __uint_as_float(pr << 16);
+            acc = fmaf(wf, uq[e], acc);
+          }
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) A.opart[ig][8 * og + e] = acc[e];
+        A.opart[iq][oc] = acc;
       }
-      __syncthreads();
+      tl_sync();
       if (t < TL_HD) {
         float a = 0.f;
-        for (int g = 0; g < 64; ++g) a += A.opart[g][t];
+#pragma unroll
+        for (int g = 0; g < TL_WAVES; ++g) a += A.opart[g][t];
         A.o[t] = wgt * a;
       }
-      __syncthreads();
+      tl_sync();
       // Y[e] = sum_c Gram[qh*64 + c][e] o[c]: thread (features 4 eq .., rows 8 cq ..)
       {
         f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
-          const float oc = A.o[8 * cq + q];
-          y[0] = fmaf(gv[q][0], oc, y[0]);
-          y[1] = fmaf(gv[q][1], oc, y[1]);
-          y[2] = fmaf(gv[q][2], oc, y[2]);
-          y[3] = fmaf(gv[q][3], oc, y[3]);
+          const float ov = A.o[8 * cq + q];
+          const f32x4 gq = *reinterpret_cast<const f32x4*>(&A.gram[8 * cq + q][4 * eq]);
+          y[0] = fmaf(gq[0], ov, y[0]);
+          y[1] = fmaf(gq[1], ov, y[1]);
+          y[2] = fmaf(gq[2], ov, y[2]);
+          y[3] = fmaf(gq[3], ov, y[3]);
         }
         *reinterpret_cast<f32x4*>(&A.red[cq][4 * eq]) = y;
       }
-      __syncthreads();
+      tl_sync();
       {
         const __amdgpu_buffer_rsrc_t ab =
             dev_buf(W.arec + ((static_cast<size_t>(lev) * TL_MAXP + slot) * TL_QH + qh) * TL_AP, TL_AP * 8u);
@@ -719,14 +743,17 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
         }
       }
       stamp(lev, 7);
-      // head 0: the node's verification route tokens, from LDS
+      // head 0: the node's verification route tokens, from the registers (after the record: the
+      // barriers wait for the block's global stores)
       if (qh == 0 && rt_out) {
-        bf16* out = rt_out + static_cast<int64_t>(j) * R * TL_DT;
-        for (int e = t; e < R * 32; e += TL_THREADS) {
-          const int r = e >> 5, pc = e & 31;
-          *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(r) * TL_DT + 8 * pc) =
-              *reinterpret_cast<const u32x4*>(&A.xs[r][8 * pc]);
-        }
+        // the node's [R, 256] block at a uniform base; route step 32 u as the constant offset
+        const __amdgpu_buffer_rsrc_t ob = dev_buf(rt_out + static_cast<int64_t>(j) * R * TL_DT, 2u * R * TL_DT);
+        const uint32_t vo = 2u * static_cast<uint32_t>(rs * TL_DT + fo);
+#pragma unroll
+        for (int u = 0; u < 6; ++u)
+          if (u < nu)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) __builtin_amdgcn_raw_buffer_store_b128(pv[u][k], ob, vo + 16u * k, 2 * 32 * TL_DT * u, 0);
       }
       __syncthreads();  // LDS is reused by the next depth
     }
