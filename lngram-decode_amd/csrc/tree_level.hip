@@ -146,6 +146,39 @@ __device__ __forceinline__ int tl_wave_sum_i(int v) {
          (__builtin_amdgcn_readlane(v, 47) + __builtin_amdgcn_readlane(v, 63));
 }
 
+// Ranking key of a candidate (value desc, then id asc): the value's bits in an order-preserving
+// unsigned form (-0 taken as +0, so equal values compare equal) above 2^31 - 1 - id.  A larger key
+// ranks first; 0 is below every candidate's key.
+__device__ __forceinline__ uint64_t tl_key(float v, int id) {
+  uint32_t b = __float_as_uint(v + 0.0f);
+  b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (static_cast<uint64_t>(b) << 32) | static_cast<uint32_t>(0x7FFFFFFF - id);
+}
+__device__ __forceinline__ int tl_key_id(uint64_t k) { return 0x7FFFFFFF - static_cast<int>(static_cast<uint32_t>(k)); }
+
+// The wave's largest 64-bit key (row maxima by DPP row_shr, then the four rows), in every lane.
+template <int CTRL>
+__device__ __forceinline__ uint64_t tl_dpp_u64(uint64_t k) {
+  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(k >> 32), CTRL, 0xf, 0xf, false));
+  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(static_cast<uint32_t>(k)), CTRL, 0xf, 0xf, false));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+__device__ __forceinline__ uint64_t tl_wave_max_u64(uint64_t k) {
+  uint64_t o;
+  o = tl_dpp_u64<0x111>(k), k = o > k ? o : k;
+  o = tl_dpp_u64<0x112>(k), k = o > k ? o : k;
+  o = tl_dpp_u64<0x114>(k), k = o > k ? o : k;
+  o = tl_dpp_u64<0x118>(k), k = o > k ? o : k;
+  uint64_t m = 0;
+#pragma unroll
+  for (int r = 15; r < 64; r += 16) {
+    const uint64_t x = (static_cast<uint64_t>(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(k >> 32), r))) << 32) |
+                       static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(k)), r));
+    m = x > m ? x : m;
+  }
+  return m;
+}
+
 // Block-wide sum / max of one value per thread through red[TL_WAVES] (every thread receives it).
 // Block barrier that orders the block's LDS accesses only: global stores still in flight are not
 // waited for (a hand-off to other blocks is tagged, so no block reads its own global stores back)
@@ -243,14 +276,13 @@ struct TlSelLds {
   float rv[TL_WAVES];
   float rs[TL_WAVES];
   int rt[TL_WAVES];
-  float cv[TL_WAVES * TL_KM];
-  int ci[TL_WAVES * TL_KM];
+  uint64_t wk[2][TL_WAVES];  // each wave's largest key of a ranking round (two rounds in flight)
   int sel[TL_KM];
 };
 
 // Bounded wait until every V block's ready word of depth `lev` holds `tag` (whole block; returns
 // false after a timeout).
-__device__ bool tl_wait_ready(int nvb, const uint32_t* rdy, int lev, uint32_t tag) {
+__device__ __forceinline__ bool tl_wait_ready(int nvb, const uint32_t* rdy, int lev, uint32_t tag) {
   const __amdgpu_buffer_rsrc_t rb = dev_buf(rdy + static_cast<size_t>(lev) * TL_MAXVB, TL_MAXVB * 4u);
   const int t = threadIdx.x;
   const long long t0 = wall_clock64();
@@ -262,30 +294,13 @@ __device__ bool tl_wait_ready(int nvb, const uint32_t* rdy, int lev, uint32_t ta
   }
 }
 
-// The wave's top-KM over every lane's sorted list (value desc, id asc): KM rounds of (wave max, the
-// smallest id holding it, its removal).  sv/si receive it in order, identical in every lane
-// ((-inf, INT_MAX) past the candidates).  Ids are distinct across the wave.  Call from converged code.
-__device__ __forceinline__ void tl_wave_topk(TlTop& tk, float* sv, int* si, int kn = TL_KM) {
-#pragma unroll
-  for (int k = 0; k < TL_KM; ++k) {
-    if (k >= kn) {  // (kn is wave-uniform)
-      sv[k] = -INFINITY, si[k] = INT_MAX;
-      continue;
-    }
-    const float wm = wave_max(tk.v[0]);
-    const int wid = tl_wave_min_i(tk.v[0] == wm ? tk.i[0] : INT_MAX);
-    sv[k] = wid == INT_MAX ? -INFINITY : wm;
-    si[k] = wid;
-    if (wid != INT_MAX && tk.i[0] == wid) tk.pop();
-  }
-}
-
 // Top-K (K <= KM) of parent `slot` of depth `lev` from the V records, ranked as k_fast_logits'
 // selection ranks them: logits, or the online mixture (1 - lam) softmax + lam count / total.  Whole
 // block; ids land in S.sel (-1 past the candidates).  Two threads per V block's record: the even one
 // takes the record's header, its top-KM of the tokens without counts and the even count-bearing
-// entries, the odd one the odd entries; each wave ranks its lanes' lists, wave 0 the waves' lists.
-__device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t* spill, float denom, int lev,
+// entries, the odd one the odd entries; then K rounds of (each wave's best, the block's best of the
+// waves' bests, the holder's next best).
+__device__ __forceinline__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t* spill, float denom, int lev,
                           int slot, TlSelLds& S, long long* stp = nullptr) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int rec = t >> 1, h = t & 1;
@@ -324,16 +339,18 @@ __device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t*
   const float n_eff = tj / denom;
   const float lam = tj > 0.f ? n_eff / (n_eff + T.kappa) : 0.f;
   const float mix_a = (1.f - lam) / Ssum, mix_b = tj > 0.f ? lam / tj : 0.f;
-  // the record's top-KM (inserted: values that round equal after the mixture rank by id), then the
-  // count-bearing entries of this lane's parity (as far as the wave's largest share reaches), then
-  // the spill area
-  TlTop tk;
-  tk.clear();
+  // the thread's candidates as ranking keys: slots 0-3 the record's top-KM (even thread), 4-11 its
+  // inline count-bearing entries (this lane's parity, as far as the wave's largest share reaches),
+  // 12-15 the best four of its spill entries; key 0: none
+  uint64_t ck[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) ck[k] = 0;
   if (head)
 #pragma unroll
     for (int k = 0; k < TL_KM; ++k) {
       const int id = static_cast<int>(word(4 + TL_KM + k));
-      if (id >= 0) tk.insert(online ? mix_a * expf(__uint_as_float(word(4 + k)) - M) : __uint_as_float(word(4 + k)), id);
+      if (id >= 0)
+        ck[k] = tl_key(online ? mix_a * expf(__uint_as_float(word(4 + k)) - M) : __uint_as_float(word(4 + k)), id);
     }
   const int nc = ok && online ? min(static_cast<int>(word(3)), TL_VS) : 0;
   const int mine = (min(nc, TL_NI) + 1 - h) >> 1;  // entries h, h + 2, ... below min(nc, NI)
@@ -344,51 +361,68 @@ __device__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t*
       const uint32_t id = h ? word(15 + 6 * u) : word(12 + 6 * u);
       const uint32_t lb = h ? word(16 + 6 * u) : word(13 + 6 * u);
       const uint32_t c = h ? word(17 + 6 * u) : word(14 + 6 * u);
-      tk.insert(fmaf(mix_b, static_cast<float>(static_cast<int>(c)), mix_a * expf(__uint_as_float(lb) - M)),
-                static_cast<int>(id));
+      ck[4 + u] = tl_key(fmaf(mix_b, static_cast<float>(static_cast<int>(c)), mix_a * expf(__uint_as_float(lb) - M)),
+                         static_cast<int>(id));
     }
   }
-  const uint32_t soff = 12u * TL_VS * static_cast<uint32_t>(ok ? rec : 0);
-  for (int e = TL_NI + h; e < nc; e += 2) {
-    const int id = static_cast<int>(tl_ld_w(sb, soff + 12u * e));
-    const float l = __uint_as_float(tl_ld_w(sb, soff + 12u * e + 4u));
-    const int c = static_cast<int>(tl_ld_w(sb, soff + 12u * e + 8u));
-    tk.insert(fmaf(mix_b, static_cast<float>(c), mix_a * expf(l - M)), id);
+  if (nc > TL_NI + h) {
+    TlTop tk;
+    tk.clear();
+    const uint32_t soff = 12u * TL_VS * static_cast<uint32_t>(ok ? rec : 0);
+    for (int e = TL_NI + h; e < nc; e += 2) {
+      const int id = static_cast<int>(tl_ld_w(sb, soff + 12u * e));
+      const float l = __uint_as_float(tl_ld_w(sb, soff + 12u * e + 4u));
+      const int c = static_cast<int>(tl_ld_w(sb, soff + 12u * e + 8u));
+      tk.insert(fmaf(mix_b, static_cast<float>(c), mix_a * expf(l - M)), id);
+    }
+#pragma unroll
+    for (int k = 0; k < TL_KM; ++k)
+      if (tk.i[k] != INT_MAX) ck[12 + k] = tl_key(tk.v[k], tk.i[k]);
   }
   if (stp && t == 0) stp[9] = wall_clock64();
-  // each wave's top-KM, then wave 0 ranks the waves' lists (lane l holds wave l / KM's l % KM-th)
-  float sv[TL_KM];
-  int si[TL_KM];
-  tl_wave_topk(tk, sv, si, T.K);
-  if (lane < TL_KM) {
-    float vv = sv[0];
-    int ii = si[0];
+  // K rounds: each wave's largest key, the block's largest of the eight, and the thread that held it
+  // (ids are unique among the candidates) moves on to its next largest
+  uint64_t bk;
+  int bs;
+  auto best = [&]() {
+    bk = ck[0], bs = 0;
 #pragma unroll
-    for (int k = 1; k < TL_KM; ++k)
-      if (lane == k) vv = sv[k], ii = si[k];
-    S.cv[w * TL_KM + lane] = vv;
-    S.ci[w * TL_KM + lane] = ii;
-  }
-  __syncthreads();
-  if (w == 0) {
-    TlTop tw;
-    tw.clear();
-    if (lane < TL_WAVES * TL_KM) tw.v[0] = S.cv[lane], tw.i[0] = S.ci[lane];
-    tl_wave_topk(tw, sv, si, T.K);
-    if (lane < TL_KM) {
-      int ii = si[0];
+    for (int q = 1; q < 16; ++q) {
+      const bool bt = ck[q] > bk;
+      bk = bt ? ck[q] : bk;
+      bs = bt ? q : bs;
+    }
+  };
+  best();
 #pragma unroll
-      for (int k = 1; k < TL_KM; ++k)
-        if (lane == k) ii = si[k];
-      S.sel[lane] = ii == INT_MAX ? -1 : ii;
+  for (int k = 0; k < TL_KM; ++k) {
+    if (k >= T.K) {
+      if (t == 0) S.sel[k] = -1;
+      continue;
+    }
+    const uint64_t wk = tl_wave_max_u64(bk);
+    if (lane == 0) S.wk[k & 1][w] = wk;
+    tl_sync();
+    uint64_t gk = S.wk[k & 1][0];
+#pragma unroll
+    for (int ww = 1; ww < TL_WAVES; ++ww) {
+      const uint64_t x = S.wk[k & 1][ww];
+      gk = x > gk ? x : gk;
+    }
+    if (t == 0) S.sel[k] = gk == 0 ? -1 : tl_key_id(gk);
+    if (gk != 0 && bk == gk) {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) ck[q] = q == bs ? 0 : ck[q];
+      best();
     }
   }
-  __syncthreads();
+  tl_sync();
 }
 
 // ------------------------------------------------------------------ LDS of the three roles
 struct TlALds {
   alignas(16) float gram[TL_HD][TL_I];  // Gram rows qh*64 .. qh*64 + 63 of the block's head
+  alignas(16) uint16_t wv[TL_HD][TL_DT + 8];  // the head's value weight Wv[h] (bf16 bits, padded rows)
   float qk[TL_DT];
   float sc[TL_MAXR], sx[TL_MAXR], wr[TL_MAXR];
   float red[TL_THREADS / 16][TL_DT];  // U partials per route row; then Y partials per eighth of o
@@ -447,7 +481,7 @@ __device__ __forceinline__ uint32_t tl_root_window(const lng_drafter& D, const T
 // Slots 0 and 1 of node i's window from its parent's published window (depth lev - 1: the parent's
 // slots 1 and 2) into wc, the parent's token into *ptok and node i's validity bits into *vfl
 // (LDS).  Whole block; false after a timeout.
-__device__ bool tl_parent_window(int R, const TlPlan& T, const uint64_t* crec, uint32_t epoch, int lev, int i,
+__device__ __forceinline__ bool tl_parent_window(int R, const TlPlan& T, const uint64_t* crec, uint32_t epoch, int lev, int i,
                                  uint8_t (*wc)[TL_MAXR], int64_t* ptok, uint32_t* vfl) {
   const int pp = T.parent[i], ps = T.pslot[pp];
   const uint32_t tag = tl_tag(epoch, lev - 1);
@@ -527,15 +561,13 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
     TlALds& A = lds.a;
     const int slot = b % TL_MAXP, qh = b / TL_MAXP;
     const int h = qh / (TL_QH / D.kv_heads);
-    // the head's value weight (bf16 Wv[h][oc][32 iq .. 32 iq + 31], packed in pairs) and Gram rows
-    // (qh*64 + 8 cq .. + 7, features 4 eq .. 4 eq + 3), once for every depth
+    // the head's value weight (bf16 Wv[h], rows oc) and Gram rows (qh*64 ..) into LDS, once for every
+    // depth; the o' product's thread takes output oc and inputs 32 iq .., the Gram product's
+    // features 4 eq .. and rows 8 cq ..
     const int oc = t & 63, iq = t >> 6, eq = t & 63, cq = t >> 6;
-    uint32_t wvp[16];
     {
-      const uint16_t* wsrc = static_cast<const uint16_t*>(D.wv_t) + (static_cast<int64_t>(h) * TL_DT + 32 * iq) * TL_HD + oc;
-#pragma unroll
-      for (int k = 0; k < 16; ++k)
-        wvp[k] = static_cast<uint32_t>(wsrc[(2 * k) * TL_HD]) | (static_cast<uint32_t>(wsrc[(2 * k + 1) * TL_HD]) << 16);
+      const uint16_t* wsrc = static_cast<const uint16_t*>(D.wv_t) + static_cast<int64_t>(h) * TL_DT * TL_HD;
+      for (int e = t; e < TL_DT * TL_HD; e += TL_THREADS) A.wv[e % TL_HD][e / TL_HD] = wsrc[e];
     }
     for (int e = t; e < TL_HD * TL_I / 4; e += TL_THREADS)
       reinterpret_cast<f32x4*>(&A.gram[0][0])[e] =
@@ -696,12 +728,15 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
       {
         float acc = 0.f;
 #pragma unroll
-        for (int k = 0; k < 32; k += 4) {
-          const f32x4 uq = *reinterpret_cast<const f32x4*>(&A.un[32 * iq + k]);
+        for (int k = 0; k < 32; k += 8) {
+          const u32x4 wq = *reinterpret_cast<const u32x4*>(&A.wv[oc][32 * iq + k]);
+          const f32x4 ua = *reinterpret_cast<const f32x4*>(&A.un[32 * iq + k]);
+          const f32x4 ub = *reinterpret_cast<const f32x4*>(&A.un[32 * iq + k + 4]);
+          const float uq[8] = {ua[0], ua[1], ua[2], ua[3], ub[0], ub[1], ub[2], ub[3]};
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const uint32_t pr = wvp[(k + e) >> 1];
-            const float wf = ((k + e) & 1) ? __uint_as_float(pr & 0xffff0000u) : __uint_as_float(pr << 16);
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t pr = wq[e >> 1];
+            const float wf = (e & 1) ? __uint_as_float(pr & 0xffff0000u) : __uint_as_float(pr << 16);
             acc = fmaf(wf, uq[e], acc);
           }
         }
