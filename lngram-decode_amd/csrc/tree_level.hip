@@ -384,14 +384,24 @@ __device__ __forceinline__ void tl_select(const TlPlan& T, const uint32_t* vrec,
   // (ids are unique among the candidates) moves on to its next largest
   uint64_t bk;
   int bs;
-  auto best = [&]() {
-    bk = ck[0], bs = 0;
+  auto best = [&]() {  // a 4-level tree of pairwise maxima (short dependency chain)
+    uint64_t m[8];
+    int ms[8];
 #pragma unroll
-    for (int q = 1; q < 16; ++q) {
-      const bool bt = ck[q] > bk;
-      bk = bt ? ck[q] : bk;
-      bs = bt ? q : bs;
+    for (int q = 0; q < 8; ++q) {
+      const bool bt = ck[2 * q + 1] > ck[2 * q];
+      m[q] = bt ? ck[2 * q + 1] : ck[2 * q];
+      ms[q] = bt ? 2 * q + 1 : 2 * q;
     }
+#pragma unroll
+    for (int n = 4; n >= 1; n >>= 1)
+#pragma unroll
+      for (int q = 0; q < n; ++q) {
+        const bool bt = m[q + n] > m[q];
+        m[q] = bt ? m[q + n] : m[q];
+        ms[q] = bt ? ms[q + n] : ms[q];
+      }
+    bk = m[0], bs = ms[0];
   };
   best();
 #pragma unroll
@@ -403,12 +413,14 @@ __device__ __forceinline__ void tl_select(const TlPlan& T, const uint32_t* vrec,
     const uint64_t wk = tl_wave_max_u64(bk);
     if (lane == 0) S.wk[k & 1][w] = wk;
     tl_sync();
-    uint64_t gk = S.wk[k & 1][0];
+    uint64_t g8[TL_WAVES];
 #pragma unroll
-    for (int ww = 1; ww < TL_WAVES; ++ww) {
-      const uint64_t x = S.wk[k & 1][ww];
-      gk = x > gk ? x : gk;
-    }
+    for (int ww = 0; ww < TL_WAVES; ++ww) g8[ww] = S.wk[k & 1][ww];
+#pragma unroll
+    for (int n = TL_WAVES / 2; n >= 1; n >>= 1)
+#pragma unroll
+      for (int q = 0; q < n; ++q) g8[q] = g8[q + n] > g8[q] ? g8[q + n] : g8[q];
+    const uint64_t gk = g8[0];
     if (t == 0) S.sel[k] = gk == 0 ? -1 : tl_key_id(gk);
     if (gk != 0 && bk == gk) {
 #pragma unroll
