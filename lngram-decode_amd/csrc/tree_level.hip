@@ -441,7 +441,6 @@ struct TlALds {
   float opart[TL_WAVES][TL_HD];  // o' partials per input run
   float un[TL_DT];
   float o[TL_HD];
-  int32_t rows[TL_MAXR][2];
   uint8_t wc[3][TL_MAXR];
   float stat[TL_WAVES];
   TlSelLds S;
@@ -609,18 +608,18 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
         tok = a >= 0 ? a : A.S.sel[0];
         tl_fresh_codes(D, A.ptok, tok, A.wc);
       }
+      // the query-key row of head qh, by the last wave (idle in the codes above: R <= 192), so its load
+      // overlaps the code lookups
+      if (t >= TL_THREADS - TL_DT / 4) {
+        const int q = t - (TL_THREADS - TL_DT / 4);
+        const f32x4 v = tl_tok_ok(D, tok)
+                            ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * (TL_QH * TL_DT) + qh * TL_DT + 4 * q)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f32x4*>(&A.qk[4 * q]) = v;
+      }
       stamp(lev, 2);
       __syncthreads();
       const uint32_t vfl = A.vfl;
-      tl_rows(D, vfl, A.wc, A.rows);
-      // the query-key row of head qh
-      const bool tok_ok = tl_tok_ok(D, tok);
-      if (t < TL_DT / 4) {
-        const f32x4 v = tok_ok ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * (TL_QH * TL_DT) + qh * TL_DT + 4 * t)
-                               : f32x4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<f32x4*>(&A.qk[4 * t]) = v;
-      }
-      __syncthreads();
       if (qh == 0) {
         // the window codes (the V blocks' online query, the children's windows) and the token;
         // the node's token and codes into its row
@@ -644,14 +643,22 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
       // the thread's routes rs + 32 u < R are u < nu; per-route LDS entries at constant offsets from
       // one address (no per-route address registers)
       const int nu = R > rs ? (R - rs + 31) >> 5 : 0;
-      const int32_t* const rowp = &A.rows[rs][oi];
+      const uint8_t* const wc0 = &A.wc[0][rs];
+      const uint8_t* const wc1 = &A.wc[1][rs];
+      const uint8_t* const wc2 = &A.wc[2][rs];
+      const bool vo2 = (vfl >> 1) & 1u, vo3 = (vfl >> 2) & 1u;
       float* const sxp = &A.sx[rs];
       float* const scp = &A.sc[rs];
       const float* const wrp = &A.wr[rs];
       u32x4 pv[6][2];
 #pragma unroll
       for (int u = 0; u < 6; ++u) {
-        const int32_t rw = u < nu ? rowp[64 * u] : -1;
+        // the route's row of order oi (as tl_rows forms it), -1 outside the sequence
+        const int r = rs + 32 * u;
+        const int32_t c0 = wc0[32 * u], c1 = wc1[32 * u], c2 = wc2[32 * u];
+        const int32_t rw = u >= nu ? -1
+                           : oi  ? (vo3 ? r * 4096 + (c0 | (c1 << 4) | (c2 << 8)) : -1)
+                                 : (vo2 ? r * 256 + (c1 | (c2 << 4)) : -1);
         const bf16* src = (oi ? tab3 : tab2) + static_cast<int64_t>(rw < 0 ? 0 : rw) * TL_MD + 16 * pc;
 #pragma unroll
         for (int k = 0; k < 2; ++k)
