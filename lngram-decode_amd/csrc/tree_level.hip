@@ -463,7 +463,6 @@ struct TlVLds {
   float rn[TL_MAXP];
 };
 struct TlGLds {
-  int32_t rows[TL_MAXR][2];
   uint8_t wc[3][TL_MAXR];
   TlSelLds S;
   int64_t ptok;
@@ -525,17 +524,6 @@ __device__ __forceinline__ bool tl_parent_window(int R, const TlPlan& T, const u
 // Slot 2 of a window from the router tables: the codes of (previous token, token).  Whole block.
 __device__ __forceinline__ void tl_fresh_codes(const lng_drafter& D, int64_t ptok, int64_t tok, uint8_t (*wc)[TL_MAXR]) {
   for (int r = threadIdx.x; r < D.R; r += TL_THREADS) wc[2][r] = static_cast<uint8_t>(tl_lut_code(D, ptok, tok, r));
-}
-
-// Rows of the window's two n-grams (orders 2 and 3) per route, -1 when a slot is outside the sequence.
-__device__ __forceinline__ void tl_rows(const lng_drafter& D, uint32_t vfl, const uint8_t (*wc)[TL_MAXR],
-                                        int32_t (*rows)[2]) {
-  const bool v2 = (vfl >> 1) & 1u, v3 = (vfl >> 2) & 1u;
-  for (int r = threadIdx.x; r < D.R; r += TL_THREADS) {
-    const int32_t c0 = wc[0][r], c1 = wc[1][r], c2 = wc[2][r];
-    rows[r][0] = v2 ? r * 256 + (c1 | (c2 << 4)) : -1;
-    rows[r][1] = v3 ? r * 4096 + (c0 | (c1 << 4) | (c2 << 8)) : -1;
-  }
 }
 
 // ------------------------------------------------------------------ the tree kernel
@@ -653,7 +641,8 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
       u32x4 pv[6][2];
 #pragma unroll
       for (int u = 0; u < 6; ++u) {
-        // the route's row of order oi (as tl_rows forms it), -1 outside the sequence
+        // the route's row of order oi (order 2: 256 r + the two newest codes, order 3: 4096 r + all
+        // three), -1 when a window slot is outside the sequence
         const int r = rs + 32 * u;
         const int32_t c0 = wc0[32 * u], c1 = wc1[32 * u], c2 = wc2[32 * u];
         const int32_t rw = u >= nu ? -1
@@ -1150,17 +1139,33 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
           if (t == 0) D.tokens[nr] = tok;
         }
         if (rt_out) {
-          tl_rows(D, G.vfl, G.wc, G.rows);
-          __syncthreads();
-          bf16* out = rt_out + static_cast<int64_t>(i) * R * TL_DT;
-          for (int e = t; e < R * 32; e += TL_THREADS) {
-            const int r = e >> 5, oi = (e >> 4) & 1, c = e & 15;
-            const int32_t rw = G.rows[r][oi];
-            u32x4 v = {0u, 0u, 0u, 0u};
-            if (rw >= 0)
-              v = *reinterpret_cast<const u32x4*>((oi ? tab3 : tab2) + static_cast<int64_t>(rw) * TL_MD + 8 * c);
-            *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(r) * TL_DT + oi * TL_MD + 8 * c) = v;
+          // the leaf's route tokens: every row load in flight before the stores (thread t: features
+          // fo .. fo + 15 of routes rs + 32 u, row indices formed from the window codes)
+          const uint32_t vfl = G.vfl;
+          const bool vo2 = (vfl >> 1) & 1u, vo3 = (vfl >> 2) & 1u;
+          const int pc = t & 7, oi = (t >> 3) & 1, rs = t >> 4;
+          const int fo = oi * TL_MD + 16 * pc;
+          const int nu = R > rs ? (R - rs + 31) >> 5 : 0;
+          u32x4 pv[6][2];
+#pragma unroll
+          for (int u = 0; u < 6; ++u) {
+            const int r = rs + 32 * u;
+            const int32_t c0 = u < nu ? G.wc[0][r] : 0, c1 = u < nu ? G.wc[1][r] : 0, c2 = u < nu ? G.wc[2][r] : 0;
+            const int32_t rw = u >= nu ? -1
+                               : oi  ? (vo3 ? r * 4096 + (c0 | (c1 << 4) | (c2 << 8)) : -1)
+                                     : (vo2 ? r * 256 + (c1 | (c2 << 4)) : -1);
+            const bf16* src = (oi ? tab3 : tab2) + static_cast<int64_t>(rw < 0 ? 0 : rw) * TL_MD + 16 * pc;
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+              pv[u][k] = rw >= 0 ? *reinterpret_cast<const u32x4*>(src + 8 * k) : u32x4{0u, 0u, 0u, 0u};
           }
+          const __amdgpu_buffer_rsrc_t ob = dev_buf(rt_out + static_cast<int64_t>(i) * R * TL_DT, 2u * R * TL_DT);
+          const uint32_t vo = 2u * static_cast<uint32_t>(rs * TL_DT + fo);
+#pragma unroll
+          for (int u = 0; u < 6; ++u)
+            if (u < nu)
+#pragma unroll
+              for (int k = 0; k < 2; ++k) __builtin_amdgcn_raw_buffer_store_b128(pv[u][k], ob, vo + 16u * k, 2 * 32 * TL_DT * u, 0);
         }
         __syncthreads();  // LDS is reused by the next leaf
       }
