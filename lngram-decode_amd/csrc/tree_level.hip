@@ -155,6 +155,11 @@ __device__ __forceinline__ uint64_t tl_key(float v, int id) {
   return (static_cast<uint64_t>(b) << 32) | static_cast<uint32_t>(0x7FFFFFFF - id);
 }
 __device__ __forceinline__ int tl_key_id(uint64_t k) { return 0x7FFFFFFF - static_cast<int>(static_cast<uint32_t>(k)); }
+__device__ __forceinline__ float tl_key_value(uint64_t k) {
+  uint32_t b = static_cast<uint32_t>(k >> 32);
+  b = (b & 0x80000000u) ? (b & 0x7FFFFFFFu) : ~b;
+  return __uint_as_float(b);
+}
 
 // The wave's largest 64-bit key (row maxima by DPP row_shr, then the four rows), in every lane.
 template <int CTRL>
@@ -1055,20 +1060,21 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
 #pragma unroll
         for (int u = 0; u < 3; ++u) se += x[u] == -INFINITY ? 0.f : expf(x[u] - m);
         const float s = wave_sum(se);
-        TlTop tk;
-        tk.clear();
+        // top-KM of the tokens without counts: KM rounds of the wave's largest ranking key (value
+        // desc, id asc), each taken out of its lane
+        uint64_t ck[3];
 #pragma unroll
-        for (int u = 0; u < 3; ++u)
-          if (x[u] != -INFINITY && c[u] == 0) tk.insert(x[u], static_cast<int>(id[u]));
+        for (int u = 0; u < 3; ++u) ck[u] = (x[u] != -INFINITY && c[u] == 0) ? tl_key(x[u], static_cast<int>(id[u])) : 0;
         float sv[TL_KM];
         int si[TL_KM];
 #pragma unroll
         for (int k = 0; k < TL_KM; ++k) {
-          const float wm = wave_max(tk.v[0]);
-          const int wid = tl_wave_min_i(tk.v[0] == wm ? tk.i[0] : INT_MAX);
-          sv[k] = wid == INT_MAX ? -INFINITY : wm;
-          si[k] = wid == INT_MAX ? -1 : wid;
-          if (wid != INT_MAX && tk.i[0] == wid) tk.pop();
+          const uint64_t b01 = ck[1] > ck[0] ? ck[1] : ck[0];
+          const uint64_t wk = tl_wave_max_u64(ck[2] > b01 ? ck[2] : b01);
+          sv[k] = wk == 0 ? -INFINITY : tl_key_value(wk);
+          si[k] = wk == 0 ? -1 : tl_key_id(wk);
+#pragma unroll
+          for (int u = 0; u < 3; ++u) ck[u] = (wk != 0 && ck[u] == wk) ? 0 : ck[u];
         }
         const size_t ri = (static_cast<size_t>(lev) * TL_MAXP + p) * TL_MAXVB + vb;
         const __amdgpu_buffer_rsrc_t rb = dev_buf(W.vrec + ri * TL_RW, TL_RW * 4u);
