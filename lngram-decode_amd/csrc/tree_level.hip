@@ -281,7 +281,7 @@ struct TlSelLds {
   float rv[TL_WAVES];
   float rs[TL_WAVES];
   int rt[TL_WAVES];
-  uint64_t wk[2][TL_WAVES];  // each wave's largest key of a ranking round (two rounds in flight)
+  uint64_t wk[TL_WAVES * TL_KM];  // each wave's top-KM ranking keys
   int sel[TL_KM];
 };
 
@@ -303,8 +303,8 @@ __device__ __forceinline__ bool tl_wait_ready(int nvb, const uint32_t* rdy, int 
 // selection ranks them: logits, or the online mixture (1 - lam) softmax + lam count / total.  Whole
 // block; ids land in S.sel (-1 past the candidates).  Two threads per V block's record: the even one
 // takes the record's header, its top-KM of the tokens without counts and the even count-bearing
-// entries, the odd one the odd entries; then K rounds of (each wave's best, the block's best of the
-// waves' bests, the holder's next best).
+// entries, the odd one the odd entries; each wave ranks its candidates' keys, then the block ranks the
+// waves' lists.
 __device__ __forceinline__ void tl_select(const TlPlan& T, const uint32_t* vrec, const uint32_t* spill, float denom, int lev,
                           int slot, TlSelLds& S, long long* stp = nullptr) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
@@ -385,8 +385,9 @@ __device__ __forceinline__ void tl_select(const TlPlan& T, const uint32_t* vrec,
       if (tk.i[k] != INT_MAX) ck[12 + k] = tl_key(tk.v[k], tk.i[k]);
   }
   if (stp && t == 0) stp[9] = wall_clock64();
-  // K rounds: each wave's largest key, the block's largest of the eight, and the thread that held it
-  // (ids are unique among the candidates) moves on to its next largest
+  // each wave's top-K by K rounds of (the wave's largest key, taken out of its thread: ids are unique
+  // among the candidates), then the block's top-K of the waves' lists by counting, for each listed
+  // key, the keys above it
   uint64_t bk;
   int bs;
   auto best = [&]() {  // a 4-level tree of pairwise maxima (short dependency chain)
@@ -409,29 +410,27 @@ __device__ __forceinline__ void tl_select(const TlPlan& T, const uint32_t* vrec,
     bk = m[0], bs = ms[0];
   };
   best();
+  uint64_t wl = 0;  // lane k < KM: the wave's k-th key
 #pragma unroll
   for (int k = 0; k < TL_KM; ++k) {
-    if (k >= T.K) {
-      if (t == 0) S.sel[k] = -1;
-      continue;
-    }
+    if (k >= T.K) break;  // (K is block-uniform)
     const uint64_t wk = tl_wave_max_u64(bk);
-    if (lane == 0) S.wk[k & 1][w] = wk;
-    tl_sync();
-    uint64_t g8[TL_WAVES];
-#pragma unroll
-    for (int ww = 0; ww < TL_WAVES; ++ww) g8[ww] = S.wk[k & 1][ww];
-#pragma unroll
-    for (int n = TL_WAVES / 2; n >= 1; n >>= 1)
-#pragma unroll
-      for (int q = 0; q < n; ++q) g8[q] = g8[q + n] > g8[q] ? g8[q + n] : g8[q];
-    const uint64_t gk = g8[0];
-    if (t == 0) S.sel[k] = gk == 0 ? -1 : tl_key_id(gk);
-    if (gk != 0 && bk == gk) {
+    if (lane == k) wl = wk;
+    if (wk != 0 && bk == wk) {
 #pragma unroll
       for (int q = 0; q < 16; ++q) ck[q] = q == bs ? 0 : ck[q];
       best();
     }
+  }
+  if (lane < TL_KM) S.wk[w * TL_KM + lane] = wl;
+  if (t < TL_KM) S.sel[t] = -1;
+  tl_sync();
+  if (t < TL_WAVES * TL_KM) {
+    const uint64_t kj = S.wk[t];
+    int above = 0;
+#pragma unroll
+    for (int q = 0; q < TL_WAVES * TL_KM; ++q) above += S.wk[q] > kj ? 1 : 0;
+    if (kj != 0 && above < T.K) S.sel[above] = tl_key_id(kj);
   }
   tl_sync();
 }
