@@ -464,7 +464,6 @@ struct TlVLds {
   int32_t nmatch;
   int32_t tot[TL_MAXP][TL_WAVES];
   float part[TL_MAXP][TL_WAVES];
-  float rn[TL_MAXP];
 };
 struct TlGLds {
   uint8_t wc[3][TL_MAXR];
@@ -990,27 +989,28 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
         }
       }
       stamp(lev, 3);
-      // hidden-state scale per parent: r = rsqrt(o . (Gram o) / d + eps)
+      // hidden-state scale per parent: r = rsqrt(o . (Gram o) / d + eps); the waves' partial dots and
+      // o itself through LDS, then every lane forms the four scales (the same sums in the same order)
 #pragma unroll
       for (int p = 0; p < TL_MAXP; ++p) {
         const float sp = wave_sum(t < TL_DT ? ov[p] * yv[p] : 0.f);
         const int tp = tl_wave_sum_i(tot_p[p]);
         if (lane == 0) S.part[p][w] = sp, S.tot[p][w] = tp;
       }
-      __syncthreads();
-      if (t < TL_MAXP) {
-        float ss = 0.f;
-#pragma unroll
-        for (int k = 0; k < TL_WAVES; ++k) ss += S.part[t][k];
-        S.rn[t] = 1.0f / sqrtf(ss / static_cast<float>(D.d) + D.draft_eps);
-      }
-      __syncthreads();
       if (t < TL_DT)
 #pragma unroll
-        for (int p = 0; p < TL_MAXP; ++p) S.ro[p][t] = p < P ? S.rn[p] * ov[p] : 0.f;
-      __syncthreads();
+        for (int p = 0; p < TL_MAXP; ++p) S.ro[p][t] = ov[p];
+      tl_sync();
+      float rl;  // the scale of parent lane % 4, the column of the MFMAs' B operand (0 past the parents)
+      {
+        const int pl = lane & 3;
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < TL_WAVES; ++k) ss += S.part[pl][k];
+        rl = pl < P ? 1.0f / sqrtf(ss / static_cast<float>(D.d) + D.draft_eps) : 0.f;
+      }
       // logits: D[row][parent] over the wave's features with 4x4x1 MFMAs (16 blocks of 4 rows x 4
-      // parents; B = ro[lane % 4][k]), then the waves' partials summed in wave order
+      // parents; B = r o[lane % 4][k]), then the waves' partials summed in wave order
       {
         f32x4 acc[TL_VG];
 #pragma unroll
@@ -1022,7 +1022,7 @@ __global__ __launch_bounds__(TL_THREADS) void k_tree_step(lng_drafter D, TlPlan 
 #pragma unroll
           for (int e = 0; e < 4; ++e)
 #pragma unroll
-            for (int g = 0; g < TL_VG; ++g) acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(av[g][q][e], bq[e], acc[g], 0, 0, 0);
+            for (int g = 0; g < TL_VG; ++g) acc[g] = __builtin_amdgcn_mfma_f32_4x4x1f32(av[g][q][e], rl * bq[e], acc[g], 0, 0, 0);
         }
         // lane 4b + n, register i: row 64 g + 4b + i, parent n
 #pragma unroll
