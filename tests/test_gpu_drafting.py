@@ -322,3 +322,39 @@ def test_sdb_shape_launch_per_step_tree_matches_oracle(dev, online):
             g0.commit(nxt, codes=g1.committed_codes()[-1:])
             o.commit(nxt, codes=g1.committed_codes()[-1:])
             k += 1
+
+
+def test_levels_tree_many_count_bearing_tokens_in_one_slice(dev):
+    """Forty distinct next tokens of one vocabulary slice after the same three-token window, and a
+    context that ends in that window: the slice's record carries more count-bearing tokens than its
+    inline entries, so the one-launch tree's selection also reads the record's spill area.  Node
+    tokens, node codes and the verification gather equal the per-depth readouts bit for bit, and the
+    node tokens equal the oracle's draft tree (16-node and chain trees)."""
+    w = wl.SDB_DRAFT
+    cfg, t = wl.build_draft_bundle(w, seed=0)
+    gen = torch.Generator().manual_seed(5)
+    fill = torch.randint(4000, w.vocab, (256,), generator=gen).tolist()
+    ctx = list(fill)
+    for i in range(40):
+        ctx += [1000, 2000, 3000, 10 + i]
+    ctx += fill[:64] + [1000, 2000, 3000]
+    g1 = GpuDrafter((cfg, t), device=dev, max_len=len(ctx) + 16, online=True)
+    g0 = GpuDrafter((cfg, t), device=dev, max_len=len(ctx) + 16, online=True, levels=False)
+    g1.commit(ctx)
+    g0.commit(ctx, codes=g1.committed_codes())
+    o = od.DrafterOracle(cfg, t, online=True)
+    o.commit(ctx, codes=g1.committed_codes())
+    for spec in (SPEC16, dtree.chain_tree(5)):
+        print(f"[levels tree, many counts in one slice] n={spec.n}", flush=True)
+        n1, r1 = g1.tree_step(spec, route_tokens=True)
+        n1, r1 = n1.clone(), r1.clone()
+        torch.cuda.synchronize()
+        assert g1.tree_error() == 0
+        assert g1._level_specs[(tuple(spec.parent), tuple(spec.rank))]
+        n0, r0 = g0.tree_step(spec, route_tokens=True)
+        torch.cuda.synchronize()
+        assert n1.cpu().tolist() == n0.cpu().tolist()
+        assert torch.equal(r1, r0)
+        rows = slice(g1.tree_row0 + 1, g1.tree_row0 + spec.n)
+        assert torch.equal(g1.codes_d[rows], g0.codes_d[rows])
+        assert n1.cpu().tolist() == od.draft_tree(o, od.TreeSpec(spec.parent, spec.rank))
