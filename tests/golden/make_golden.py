@@ -15,6 +15,8 @@ from them, plus the torch version that computed it.  Fixtures:
   reference's bf16 rounding sequence (``lngram_v2.py:1361-1407``) is recorded;
 - ``surrogate.npz``: the route-logit and memory gradients of ``_LngramSurrogate``
   (``lngram_v2.py:328-464``), approximate and exact, for the cases of ``recipe.SURROGATE_CASES``;
+- ``online_counts.npz``: ``OnlineCounts(codes, x, orders, 4, V, kappa).mix(p, win, real, deadline)``
+  (``drafters.py:117-142``) for the cases of ``recipe.ONLINE_CASES``;
 - ``drafter_<kind>[_sketch].npz``: ``RefDrafter.trace`` (full vocabulary and shortlist) and
   ``RefDrafter.draft`` after a commit, with and without hypothetical tokens
   (``cpu_drafter.py:247-289``) on tiny SD-B / SD-C bundles, with and without count sketches.
@@ -173,6 +175,21 @@ def surrogate(out: Path) -> None:
     np.savez_compressed(out / "surrogate.npz", **res)
 
 
+def online(out: Path) -> None:
+    from drafting.drafters import OnlineCounts
+
+    res = {"torch": np.array(torch.__version__)}
+    for case in recipe.ONLINE_CASES:
+        name, T, R, V, orders, kappa = case
+        x = recipe.online_inputs(case)
+        oc = OnlineCounts(torch.from_numpy(x["codes"]), torch.from_numpy(x["x"]), orders, 4, V, kappa)
+        with torch.no_grad():
+            mixed = oc.mix(torch.from_numpy(x["p"]), torch.from_numpy(x["win"]), torch.from_numpy(x["real"]),
+                           torch.from_numpy(x["deadline"]))
+        res[f"{name}_mix"] = mixed.numpy()
+    np.savez_compressed(out / "online_counts.npz", **res)
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--ref", required=True, help="the reference checkout")
@@ -183,7 +200,7 @@ def main() -> None:
     torch.manual_seed(0)
     out = Path(args.out)
     groups = {"router_features": router_features, "ssm": ssm, "memory": memory, "drafter": drafter,
-              "surrogate": surrogate}
+              "surrogate": surrogate, "online": online}
     for name in args.only or groups:
         groups[name](out)
     for p in sorted(out.glob("*.npz")):

@@ -140,3 +140,51 @@ def surrogate_inputs(case) -> dict:
             "q": normal(f"{name}_q", (B, T, R, bits)),
             "grad": normal(f"{name}_grad", (B, T, R, D)),
             "valid_tokens": valid}
+
+
+# ------------------------------------------------------------------ online counts (drafting)
+# (name, time, routes, vocab, orders, kappa)
+ONLINE_CASES = [
+    ("oc_o23_k1", 48, 4, 20, (2, 3), 1.0),
+    ("oc_o23_k05", 48, 4, 20, (2, 3), 0.5),
+    ("oc_o3_k1", 40, 3, 12, (3,), 1.0),
+    ("oc_o2_r1_k05", 36, 1, 9, (2,), 0.5),
+]
+
+
+def online_inputs(case) -> dict:
+    """Inputs of one online-count case (``OnlineCounts(codes, x, orders, 4, V, kappa).mix``).
+
+    The committed codes ``[T, R]`` use the values 0..11: their first half is random, the second
+    half repeats a 4-step pattern, so windows taken there match many earlier pairs.  Eight query
+    windows ``[8, 3, R]`` with their real masks and deadlines:
+
+    0. a window of the repeating half (many matches, every pair verified);
+    1. the same window with a deadline that cuts the later matches;
+    2. a window of the random half (at least its own pair matches);
+    3. codes 12..15 only, which no committed code has (no match);
+    4. window 0 with its oldest position before the sequence start (order 3 invalid, order 2 counts);
+    5. only the newest position real (no order is valid: the distribution is unchanged);
+    6. window 0 with nothing verified yet (deadline -1);
+    7. window 2's newest two codes after a changed oldest code (order 2 matches, order 3 not).
+
+    ``p`` is a softmax of random logits (fp32)."""
+    name, T, R, V = case[:4]
+    half = T // 2
+    codes = integers(f"{name}_codes", (T, R), 0, 12)
+    pat = integers(f"{name}_pat", (4, R), 0, 12)
+    codes[half:] = pat[np.arange(T - half) % 4]
+    x = integers(f"{name}_x", (T,), 0, V)
+    ta, tb = T - 6, half - 5                  # window ends: repeating half, random half
+    w0, w2 = codes[ta - 2: ta + 1], codes[tb - 2: tb + 1]
+    w7 = w2.copy()
+    w7[0] = (w7[0] + 1) % 12
+    win = np.stack([w0, w0, w2, integers(f"{name}_none", (3, R), 12, 16), w0, w0, w0, w7])
+    real = np.ones((8, 3), dtype=bool)
+    real[4, 0] = False
+    real[5, :2] = False
+    deadline = np.array([T - 2, half + 6, T - 2, T - 2, T - 2, T - 2, -1, T - 2], dtype=np.int64)
+    logits = normal(f"{name}_logits", (8, V))
+    p = np.exp(logits - logits.max(1, keepdims=True))
+    p = (p / p.sum(1, keepdims=True)).astype(np.float32)
+    return {"codes": codes, "x": x, "win": win, "real": real, "deadline": deadline, "p": p}

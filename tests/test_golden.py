@@ -10,7 +10,9 @@ through the oracle:
 - the memory layer forward (``wrapper.py:103-125``): the tiny fp32 layer within 1e-5 and the
   bf16 layer at the SB widths against the reference's bf16 rounding sequence;
 - the drafter (``cpu_drafter.py:147-289``): codes bit-exact, logits within 1e-5 norm-relative
-  (fp64 oracle) of the reference's fp32, top-k ids equal, and the sketch shortlist identical.
+  (fp64 oracle) of the reference's fp32, top-k ids equal, and the sketch shortlist identical;
+- the online-count mix (``drafters.py:117-142``) within 2e-7 of the reference's fp32, plus a
+  hand-computed mix weight.
 """
 
 from __future__ import annotations
@@ -189,3 +191,64 @@ def test_drafter_draft_matches_reference(name):
     assert out.tokens == g["hyp_tokens"].tolist()
     assert (out.topk_ids == g["hyp_ids"]).all() and (out.codes == g["hyp_codes"]).all()
     assert _logit_err(out.topk_logits.astype(np.float64), g["hyp_logits"]) < 1e-5
+
+
+# ------------------------------------------------------------------ online counts
+@pytest.mark.parametrize("case", recipe.ONLINE_CASES, ids=[c[0] for c in recipe.ONLINE_CASES])
+def test_online_counts_mix_matches_reference(case):
+    # OnlineCounts(codes, x, orders, 4, V, kappa).mix (drafters.py:117-142), computed by the
+    # reference in fp32; the oracle runs in fp64
+    name, T, R, V, orders, kappa = case
+    x = recipe.online_inputs(case)
+    want = load("online_counts")[f"{name}_mix"].astype(np.float64)
+    got = od.online_counts_mix(x["p"], x["codes"], x["x"], orders, 4, x["win"], x["real"], x["deadline"], kappa)
+    got = got.numpy()
+    assert np.abs(got - want).max() < 2e-7
+    # the cases do what their windows say: unchanged rows (no match, no valid order, nothing
+    # verified), and rows whose mix moved mass
+    p = x["p"].astype(np.float64)
+    for j in (3, 5, 6):
+        assert np.abs(want[j] - p[j]).max() < 1e-7
+    for j in (0, 1, 2):
+        assert np.abs(want[j] - p[j]).max() > 1e-3
+
+
+def test_online_mix_weight_hand_computed():
+    # one route, orders 2 and 3, one matching pair: the 2-gram of the window (codes 1, 2) is the
+    # row of pair t = 1, whose next token is x[2] = 12; the 3-gram (0, 1, 2) matches nothing.
+    # n_eff = 1 / (1 route * 2 orders) = 1/2, lambda = n_eff / (n_eff + 1) = 1/3:
+    # p' = 2/3 * p + 1/3 * onehot(12)
+    codes = np.array([[1], [2], [3], [4]])
+    x = np.array([10, 11, 12, 13])
+    p = torch.full((1, 16), 1.0 / 16, dtype=torch.float64)
+    win = np.array([[[0], [1], [2]]])
+    real = np.ones((1, 3), bool)
+    got = od.online_counts_mix(p, codes, x, (2, 3), 4, win, real, [2], kappa=1.0)
+    want = torch.full((1, 16), (2.0 / 3.0) / 16, dtype=torch.float64)
+    want[0, 12] += 1.0 / 3.0
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-15)
+    # kappa 0.5: lambda = 0.5 / (0.5 + 0.5) = 1/2
+    got = od.online_counts_mix(p, codes, x, (2, 3), 4, win, real, [2], kappa=0.5)
+    want = torch.full((1, 16), 0.5 / 16, dtype=torch.float64)
+    want[0, 12] += 0.5
+    torch.testing.assert_close(got, want, rtol=0, atol=1e-15)
+
+
+@pytest.mark.parametrize("name", ["drafter_sdb", "drafter_sdc"])
+def test_drafter_online_mix_equals_counts_mix(name):
+    # the drafter's per-cursor mix (keys = the first n_pairs committed pairs) is OnlineCounts.mix
+    # at the cursor's window with deadline n_pairs - 1, which the fixture above pins
+    g = load(name)
+    o = _drafter(name)
+    toks = np.concatenate([g["tokens"], g["tokens"][:12]])
+    o.commit(toks)
+    cur = o._cursor()
+    codes = o.committed_codes()
+    v = o.V
+    p = torch.softmax(torch.from_numpy(recipe.normal(f"{name}_online_p", (v,))).double(), -1)
+    win = codes[-3:][None]
+    real = np.ones((1, 3), bool)
+    for n_pairs in (5, 30, len(toks) - 1):
+        got = o.online_mix(p, cur, n_pairs)
+        want = od.online_counts_mix(p[None], codes, toks, o.ngrams, o.bits, win, real, [n_pairs - 1], o.kappa)[0]
+        torch.testing.assert_close(got, want, rtol=0, atol=1e-14)
