@@ -193,7 +193,7 @@ int lng_row_sumsq(const void* x, int64_t rows, int32_t d, float* rowsq, void* st
 
 /* lng_causal_conv for bf16, kernel 4, dilation 3, taking the row statistics from
  * lng_linear_rowsq instead of recomputing them (same rounding as lng_causal_conv).
- * n_partials <= 16, i.e. d <= 2048. */
+ * d % 4 == 0, n_partials <= 16 (lng_linear_rowsq makes 2 per 256 output channels). */
 int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_partials, const void* norm_w,
                           const void* conv_w, int64_t B, int64_t T, int32_t d, int32_t K, int32_t dilation,
                           float eps, int residual, void* out, void* stream);

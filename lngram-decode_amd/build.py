@@ -25,9 +25,6 @@ FLAGS = [f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
 
-# hipBLASLt runs the plain bf16 projections (csrc/gemm_lt.hip)
-LIBS = ["-L/opt/rocm/lib", "-lhipblaslt", "-Wl,-rpath,/opt/rocm/lib"]
-
 
 def _run(cmd: list) -> None:
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -46,7 +43,7 @@ def build(verbose: bool = True) -> Path:
     with ThreadPoolExecutor(jobs) as ex:
         list(ex.map(lambda so: _run([HIPCC, *FLAGS, "-c", str(so[0]), "-o", str(so[1])]), zip(srcs, objs)))
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, *FLAGS, "-shared", *map(str, objs), "-o", str(tmp), *LIBS])
+    _run([HIPCC, *FLAGS, "-shared", *map(str, objs), "-o", str(tmp)])
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB} from {len(srcs)} sources")

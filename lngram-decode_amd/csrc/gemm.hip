@@ -510,6 +510,172 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Projection GEMM for large M (the memory readout's query and output projections, 16384 x 1024 x
+// 1024 at SB): 256 (W rows) x 256 (X rows) tiles, 8 waves in a 2 x 4 grid, each 128 x 64 of
+// v_mfma_f32_32x32x16_bf16 (a lane holds 4 consecutive channels of one token per 4 registers).
+//
+// - K advances 64 per stage, so every tile row of a stage is one whole 128 B line; a 2-slot ring
+//   (2 x 64 KB of LDS) holds stage k + 1 in flight while stage k is multiplied.  The loads are raw
+//   buffer loads straight into LDS over the tile's rows (rows past N or M lie outside the buffer
+//   and read as zero, so ragged edges need no clamping); piece p of row r sits at slot p ^ (r & 7).
+// - A stage is four k16 slices; the fragments of slice s + 1 are read from LDS under the MFMAs of
+//   slice s (two register sets), and the scheduling hints interleave one LDS read (or two buffer
+//   loads) with each MFMA.
+// - Epilogue: the accumulators go through LDS (the ring, free once every wave has left the K
+//   loop) as each wave's [64 tokens][128 channels] bf16 tile, so every store instruction writes
+//   four whole 256 B row pieces instead of 32 scattered 8 B pieces.  Optionally the same pass forms
+//   each token's sum of squares of its bf16-rounded outputs over the wave's 128 channels: partial
+//   p = 2 * (column tile) + (wave column) of row m lands at rowsq[p * M + m] (a following RMSNorm's
+//   statistics, summed in that fixed order by its consumer).
+// - Blocks go to the 8 XCDs round-robin; with the M tiles a multiple of 8, the N tiles of one M
+//   tile run on one XCD, so that token slice is fetched into one L2.
+constexpr int PT = 256, PK = 64, P_ROWS = 2 * PT, P_STAGE = P_ROWS * PK;
+constexpr int P_FN = 4, P_FM = 2;      // 32 x 32 fragments per wave: 4 (W rows) x 2 (X rows)
+constexpr int P_DPW = P_ROWS / 8 / 8;  // buffer loads (8 rows each) per wave per stage
+
+__global__ __launch_bounds__(512, 1) void k_gemm_proj_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
+                                                           int64_t N, int64_t M, int64_t K, int n_tiles,
+                                                           int xcd_local, bf16* __restrict__ out,
+                                                           float* __restrict__ rowsq) {
+  __shared__ __attribute__((aligned(16))) bf16 ring[2 * P_STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1, wm = wave >> 1;  // wave tile: W rows wn*128 .. +128, X rows wm*64 .. +64
+  const int b = static_cast<int>(blockIdx.x);
+  const int slot = xcd_local ? b >> 3 : b;
+  const int nt = slot % n_tiles;
+  const int64_t n0 = static_cast<int64_t>(nt) * PT;
+  const int64_t m0 = (static_cast<int64_t>(xcd_local ? (b & 7) * xcd_local : 0) + slot / n_tiles) * PT;
+  const int nk = static_cast<int>(K / PK);
+
+  // loads: waves 0-3 fill the W rows of a stage, waves 4-7 the X rows, 8 rows per instruction
+  const bool is_w = wave < 4;
+  const int row0 = (wave & 3) * P_DPW * 8 + (lane >> 3);
+  const int64_t rows_left = is_w ? N - n0 : M - m0;
+  const uint64_t bytes = static_cast<uint64_t>(rows_left) * K * 2;
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(is_w ? W + n0 * K : X + m0 * K), 0,
+      static_cast<int>(bytes < 0x7fffffffull ? bytes : 0x7fffffffull), BUF_DW3);
+  const uint32_t voff0 = static_cast<uint32_t>((row0 * K + 8 * ((lane & 7) ^ (row0 & 7))) * 2);
+  const uint32_t dstep = static_cast<uint32_t>(8 * K * 2);
+  auto issue = [&](int stage, int c) {
+    bf16* dst = ring + c * P_STAGE + wave * P_DPW * 8 * PK;
+#pragma unroll
+    for (int d = 0; d < P_DPW; ++d)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + d * 8 * PK), 16,
+                                               voff0 + d * dstep + static_cast<uint32_t>(stage) * PK * 2, 0, 0, 0);
+  };
+  // fragment of 32 rows x 16 k: lane (r31, hi) reads row r31 at k piece 2 ks + hi
+  const int r31 = lane & 31, hi = lane >> 5;
+  const int a_base = (wn * 128 + r31) * PK, b_base = (PT + wm * 64 + r31) * PK;
+  auto frags = [&](bf16x8* a, bf16x8* bb, int c, int ks) {
+    const int off = c * P_STAGE + 8 * ((2 * ks + hi) ^ (lane & 7));
+#pragma unroll
+    for (int i = 0; i < P_FN; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&ring[off + a_base + i * 32 * PK]);
+#pragma unroll
+    for (int j = 0; j < P_FM; ++j) bb[j] = *reinterpret_cast<const bf16x8*>(&ring[off + b_base + j * 32 * PK]);
+  };
+  f32x16 acc[P_FN][P_FM];
+#pragma unroll
+  for (int i = 0; i < P_FN; ++i)
+#pragma unroll
+    for (int j = 0; j < P_FM; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  auto mm = [&](const bf16x8* a, const bf16x8* bb) {
+#pragma unroll
+    for (int i = 0; i < P_FN; ++i)
+#pragma unroll
+      for (int j = 0; j < P_FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bb[j], acc[i][j], 0, 0, 0);
+  };
+  constexpr int NR = P_FN + P_FM, NMF = P_FN * P_FM;
+  auto interleave_reads = [&]() {  // one LDS read after each of the first NR MFMAs
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, NMF - NR, 0);
+  };
+  bf16x8 a0[P_FN], b0[P_FM], a1[P_FN], b1[P_FM];
+  issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  issue(nk > 1 ? 1 : 0, 1);
+  frags(a0, b0, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int c = kt & 1;
+    frags(a1, b1, c, 1);
+    mm(a0, b0);
+    interleave_reads();
+    frags(a0, b0, c, 2);
+    mm(a1, b1);
+    interleave_reads();
+    frags(a1, b1, c, 3);
+    mm(a0, b0);
+    interleave_reads();
+    // every wave's reads of slot c are complete and stage kt + 1 has landed in slot c ^ 1
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    // stage kt + 2 into the freed slot (past the end: a reload of the last stage, never read)
+    issue(kt + 2 < nk ? kt + 2 : nk - 1, c);
+    frags(a0, b0, c ^ 1, 0);
+    mm(a1, b1);
+#pragma unroll
+    for (int q = 0; q < P_DPW; ++q) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();  // every wave has left the ring
+
+  // lane (r31, hi) holds token t = 32 j + r31 of the wave's 64 and channels 32 i + 8 g + 4 hi + e of
+  // its 128; the wave's tile goes to LDS as [64][128] bf16 rows, 16 B unit u of row t at u ^ (t & 15)
+  bf16* tl = ring + wave * 64 * 128;
+  float ps[P_FM] = {0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < P_FN; ++i)
+#pragma unroll
+    for (int j = 0; j < P_FM; ++j) {
+      const int t = j * 32 + r31;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const bf16x4 pk = {static_cast<bf16>(acc[i][j][4 * g]), static_cast<bf16>(acc[i][j][4 * g + 1]),
+                           static_cast<bf16>(acc[i][j][4 * g + 2]), static_cast<bf16>(acc[i][j][4 * g + 3])};
+        if (rowsq) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float r = static_cast<float>(pk[e]);
+            ps[j] = fmaf(r, r, ps[j]);
+          }
+        }
+        const int u = (i * 4 + g) ^ (t & 15);
+        *reinterpret_cast<bf16x4*>(tl + t * 128 + u * 8 + 4 * hi) = pk;
+      }
+    }
+  if (rowsq) {
+#pragma unroll
+    for (int j = 0; j < P_FM; ++j) {
+      const float v = ps[j] + __shfl_xor(ps[j], 32, 64);
+      const int64_t m = m0 + wm * 64 + j * 32 + r31;
+      if (hi == 0 && m < M) rowsq[(static_cast<int64_t>(nt) * 2 + wn) * M + m] = v;
+    }
+  }
+  const int u = lane & 15;
+  const int64_t n = n0 + wn * 128 + 8 * u;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    const int t = 4 * q + (lane >> 4);
+    const bf16x8 v = *reinterpret_cast<const bf16x8*>(tl + t * 128 + 8 * (u ^ (t & 15)));
+    const int64_t m = m0 + wm * 64 + t;
+    if (m < M && n < N) *reinterpret_cast<bf16x8*>(out + m * N + n) = v;  // N % 8 == 0
+  }
+}
+
 // fp32 VALU tile GEMM: 64x64 tile per 256-thread block, 4x4 outputs per thread,
 // K staged through LDS 16 at a time.  A/B element types may be float or bf16.
 template <typename TA, typename TB, typename TO>
@@ -663,6 +829,19 @@ static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64
   return check_launch("gemm_bf16");
 }
 
+// The projection kernel takes M >= 1024 (at least 4 tiles of rows), K % 64 == 0 and N % 8 == 0.
+static bool proj_shape(int64_t N, int64_t M, int64_t K) { return M >= 1024 && N >= 64 && K % PK == 0 && N % 8 == 0; }
+
+static int launch_proj(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, bf16* out, float* rowsq,
+                       hipStream_t s) {
+  const int n_tiles = static_cast<int>(cdiv(N, PT));
+  const int64_t m_tiles = cdiv(M, PT);
+  const int xcd_local = m_tiles % 8 == 0 ? static_cast<int>(m_tiles / 8) : 0;
+  hipLaunchKernelGGL(k_gemm_proj_bf16, dim3(static_cast<unsigned>(n_tiles * m_tiles)), dim3(512), 0, s, w, x, N, M,
+                     K, n_tiles, xcd_local, out, rowsq);
+  return check_launch("gemm_bf16_proj");
+}
+
 template <typename TA, typename TB, typename TO>
 static int launch_f32(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(cdiv(N, 64)), static_cast<unsigned>(cdiv(M, 64)));
@@ -679,10 +858,11 @@ __global__ void k_fold_columns(const bf16* __restrict__ w, const bf16* __restric
   out[i] = static_cast<bf16>(static_cast<float>(w[i]) * static_cast<float>(s[i % K]));
 }
 
-int linear_bf16_lt(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s);
-
 // Shared entry for bf16 MFMA linears (used by other translation units).
 int linear_bf16(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, hipStream_t s) {
+  if (proj_shape(N, M, K))
+    return launch_proj(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, static_cast<bf16*>(y),
+                       nullptr, s);
   return launch_mfma<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, y, nullptr,
                                nullptr, 0, 0, s);
 }
@@ -709,6 +889,9 @@ int lng_linear_rowsq(const void* x, const void* w, int64_t M, int64_t N, int64_t
   if (K % DK) return fail(LNG_E_ARG, "linear_rowsq: needs K % 32 == 0");
   if (!rowsq) return fail(LNG_E_ARG, "linear_rowsq: rowsq buffer required");
   if (M == 0) return LNG_OK;
+  if (proj_shape(N, M, K))
+    return launch_proj(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, static_cast<bf16*>(y),
+                       rowsq, as_stream(stream));
   return launch_mfma<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, y, nullptr,
                                nullptr, 0, 0, as_stream(stream), rowsq);
 }
@@ -719,13 +902,6 @@ int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, in
   hipStream_t s = as_stream(stream);
   if (dtype == LNG_BF16) {
     if (K % 8) return fail(LNG_E_ARG, "linear: bf16 needs K % 8 == 0");
-    // large plain projections (no epilogue to fuse) run on hipBLASLt, the library GEMM, which is
-    // faster on them than the kernels here; shapes it has no algorithm for, and the rest, run the
-    // MFMA kernels of this file.  The choice depends on the shape alone.
-    if (M >= 1024 && N >= 256 && K >= 256) {
-      const int rc = linear_bf16_lt(x, w, M, N, K, y, s);
-      if (rc != LNG_E_ARG) return rc;
-    }
     return linear_bf16(x, w, M, N, K, y, s);
   }
   if (dtype == LNG_F32) return launch_f32<float, float, float>(x, w, M, N, K, y, s);

@@ -248,92 +248,8 @@ __global__ __launch_bounds__(128) void k_causal_conv_k4d3(const T* __restrict__ 
   }
 }
 
-// bf16, kernel 4, dilation 3, with the row sums of squares already reduced by the
-// producing GEMM (rowsq[p][m], P <= MAXP partials per row m = b*T + t, summed in fixed
-// order; slots p >= P add an exact zero).  Block = (b, RSQ_TT positions), thread = 8
-// channels: the thread loads the RSQ_TT + 9 rows its outputs depend on (all loads issued
-// before the block barrier), the first RSQ_ROWS threads turn the partials into the row
-// scales in LDS, then each row is normalised once and scattered into the (up to) four
-// outputs whose taps read it.  SiLU uses the hardware exp2 and reciprocal.
-constexpr int RSQ_MAXP = 16;
-constexpr int RSQ_TT = 8;
-constexpr int RSQ_ROWS = RSQ_TT + 9;
-
-template <int MAXP>
-__global__ __launch_bounds__(256) void k_causal_conv_k4d3_rowsq(const bf16* __restrict__ mixed,
-                                                               const float* __restrict__ rowsq, int32_t P,
-                                                               const bf16* __restrict__ norm_w,
-                                                               const bf16* __restrict__ conv_w, uint32_t M,
-                                                               uint32_t T_len, uint32_t d8, float eps, int residual,
-                                                               bf16* __restrict__ out) {
-  __shared__ float srow[RSQ_ROWS];
-  const uint32_t tid = threadIdx.x;
-  const int t0 = static_cast<int>(blockIdx.x) * RSQ_TT;
-  const int T = static_cast<int>(T_len);
-  const size_t row0 = static_cast<size_t>(blockIdx.y) * T_len;
-  const uint32_t d = d8 * 8u;
-  auto clamp_t = [&](int tp) { return tp < 0 ? 0 : (tp >= T ? T - 1 : tp); };
-  if (tid < RSQ_ROWS) {
-    const size_t m = row0 + clamp_t(t0 - 9 + static_cast<int>(tid));
-    float ss = 0.f;
-#pragma unroll
-    for (int p = 0; p < MAXP; ++p) {
-      const float v = rowsq[static_cast<size_t>(p < P ? p : 0) * M + m];
-      ss += p < P ? v : 0.f;
-    }
-    srow[tid] = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
-  }
-  const bool active = tid < d8;
-  const uint32_t c = (active ? tid : 0u) * 8u;
-  bf16x8 x[RSQ_ROWS];
-#pragma unroll
-  for (int r = 0; r < RSQ_ROWS; ++r)
-    x[r] = *reinterpret_cast<const bf16x8*>(mixed + (row0 + clamp_t(t0 - 9 + r)) * d + c);
-  const bf16x8 nwv = *reinterpret_cast<const bf16x8*>(norm_w + c);
-  bf16x8 cw[4];  // taps of channels c .. c+7: cw[q][4*i + k] = conv_w[c + 2q + i][k]
-#pragma unroll
-  for (int q = 0; q < 4; ++q) cw[q] = *reinterpret_cast<const bf16x8*>(conv_w + static_cast<size_t>(c) * 4 + 8 * q);
-  __syncthreads();
-  if (!active) return;
-  float acc[RSQ_TT][8];
-#pragma unroll
-  for (int i = 0; i < RSQ_TT; ++i)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
-#pragma unroll
-  for (int r = 0; r < RSQ_ROWS; ++r) {
-    const int tp = t0 - 9 + r;
-    if (tp < 0 || tp >= T) continue;  // zero left padding; rows past T feed no stored output
-    const float s = srow[r];
-    float xn[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      xn[j] = norm_elem<bf16, true>(static_cast<float>(x[r][j]), s, static_cast<float>(nwv[j]));
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = r - 3 * k;  // output t0 + i reads this row with tap k
-      if (i < 0 || i >= RSQ_TT) continue;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(static_cast<float>(cw[j >> 1][4 * (j & 1) + k]), xn[j], acc[i][j]);
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < RSQ_TT; ++i) {
-    if (t0 + i >= T) break;
-    bf16x8 o;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float y = round_to<bf16>(acc[i][j]);
-      const float e = __builtin_amdgcn_exp2f(-y * 1.4426950408889634f);
-      const float act = round_to<bf16>(y * __builtin_amdgcn_rcpf(1.0f + e));
-      o[j] = static_cast<bf16>(residual ? static_cast<float>(x[i + 9][j]) + act : act);
-    }
-    *reinterpret_cast<bf16x8*>(out + (row0 + t0 + i) * d + c) = o;
-  }
-}
-
 // rowsq[m] = sum_c x[m, c]^2 of bf16 rows (the RMSNorm statistic of the short conv, in the one-
-// partial layout k_causal_conv_k4d3_rowsq reads).  One wave per row, 16-byte loads.
+// partial layout k_causal_conv_k4d3_stream reads).  One wave per row, 16-byte loads.
 __global__ __launch_bounds__(256) void k_row_sumsq_bf16(const bf16* __restrict__ x, int64_t rows, int32_t d,
                                                         float* __restrict__ rowsq) {
   const int lane = threadIdx.x & 63;
@@ -358,7 +274,7 @@ __global__ __launch_bounds__(256) void k_row_sumsq_bf16(const bf16* __restrict__
 // halo included) once; a row's sum of squares is a bf16 dot product per lane, summed over 16
 // lanes with DPP and over the block's 16-lane groups in LDS in a fixed order.  Then the rows are
 // normalised in order and the outputs formed as soon as their last tap is ready.  The rounding
-// sequence is the one of k_causal_conv_k4d3_rowsq: normalise and scale by the weight in fp32,
+// sequence is F.rms_norm's then the reference conv's: normalise and scale by the weight in fp32,
 // round once, taps in order with fp32 accumulation (v_dot2_f32_bf16 adds a tap pair's exact
 // bf16 products with one rounding), round, SiLU (hardware exp2 and reciprocal), round, add the
 // residual.  A normalised row r is rounded straight into the pairs (r - 3, r) and (r, r + 3),
@@ -507,6 +423,114 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
   }
 }
 
+// bf16, kernel 4, dilation 3, with the row sums of squares formed by the producing GEMM
+// (rowsq[p][m], P <= MAXP partials per row m = b*T + t, summed in the fixed order p = 0, 1, ...).
+// One wave streams one (sequence, 256-channel group, SL-position range): lane l owns channels
+// 4l .. 4l+3 of the group.  All SL + 9 rows (the range and its causal halo) are requested at
+// kernel entry; each output is formed as soon as its four rows have arrived, so the arithmetic of
+// the early rows overlaps the loads of the later ones, with no block barrier and no reduction in
+// the kernel.  Lane r (< SL + 9) turns the partials of row t0 - 9 + r into that row's scale,
+// which the wave reads back as a scalar.  The rounding sequence is k_causal_conv_k4d3_fused's.
+// Ranges are numbered so that consecutive ranges of a sequence land on one XCD (blocks go to the
+// 8 XCDs round-robin), where a range's halo rows were fetched by the range before it.
+constexpr int CS_SL = 32;
+constexpr int CS_MAXP = 16;
+
+template <int SL, int MAXP>
+__global__ __launch_bounds__(64) void k_causal_conv_k4d3_stream(const bf16* __restrict__ mixed,
+                                                                const float* __restrict__ rowsq, int32_t P,
+                                                                const bf16* __restrict__ norm_w,
+                                                                const bf16* __restrict__ conv_w, int32_t T,
+                                                                int32_t d, int32_t G, int32_t R, int64_t M, float eps,
+                                                                int residual, bf16* __restrict__ out) {
+  constexpr int ROWS = SL + CF_HALO;
+  const int lane = threadIdx.x;
+  // the host keeps the tile count below 2^31
+  uint32_t tile = blockIdx.x;
+  const uint32_t nb = gridDim.x;
+  if ((nb & 7) == 0) tile = (tile & 7) * (nb >> 3) + (tile >> 3);
+  const uint32_t gr = tile / static_cast<uint32_t>(G);
+  const int cg = static_cast<int>(tile - gr * static_cast<uint32_t>(G));
+  const uint32_t bb = gr / static_cast<uint32_t>(R);
+  const int rg = static_cast<int>(gr - bb * static_cast<uint32_t>(R));
+  const int64_t b = bb;
+  const int t0 = rg * SL;
+  const int64_t row0 = b * T;
+  const int c = cg * 256 + 4 * lane;
+  const bool active = c < d;
+  const int cc = active ? c : 0;
+  auto clamp_t = [&](int tp) { return tp < 0 ? 0 : (tp >= T ? T - 1 : tp); };
+  // the partials first (every lane loads, unconditionally, so the row loads are not held back
+  // behind them), then the rows
+  const int tl = t0 - CF_HALO + (lane < ROWS ? lane : 0);
+  const int64_t ml = row0 + clamp_t(tl);
+  float pv[MAXP];
+#pragma unroll
+  for (int q = 0; q < MAXP; ++q) pv[q] = rowsq[static_cast<int64_t>(q < P ? q : 0) * M + ml];
+  uint2 x[ROWS];  // channels cc .. cc+3 of row t0 - 9 + r
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r)
+    x[r] = *reinterpret_cast<const uint2*>(mixed + (row0 + clamp_t(t0 - CF_HALO + r)) * d + cc);
+  const uint2 nwv = *reinterpret_cast<const uint2*>(norm_w + cc);
+  const uint4 cw01 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(cc) * 4);      // channels c, c+1
+  const uint4 cw23 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(cc) * 4 + 8);  // channels c+2, c+3
+  const float nw[4] = {lo_f(nwv.x), hi_f(nwv.x), lo_f(nwv.y), hi_f(nwv.y)};
+  const uint32_t wa[4] = {cw01.x, cw01.z, cw23.x, cw23.z};
+  const uint32_t wb[4] = {cw01.y, cw01.w, cw23.y, cw23.w};
+  // lane r's scale is row t0 - 9 + r's; rows before the sequence start are the zero left padding
+  float ss = 0.f;
+#pragma unroll
+  for (int q = 0; q < MAXP; ++q) ss += q < P ? pv[q] : 0.f;
+  const float s = tl < 0 ? 0.f : 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+  float yn[ROWS][4];
+  bf16x2 q[ROWS][4];  // q[r][j] = (yn[r][j], yn[r + 3][j]) rounded to bf16
+#pragma unroll
+  for (int r = 0; r < ROWS; ++r) {
+    const float sr = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s), r));
+    const float xf[4] = {lo_f(x[r].x), hi_f(x[r].x), lo_f(x[r].y), hi_f(x[r].y)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) yn[r][j] = xf[j] * sr * nw[j];
+    if (r >= 3) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) q[r - 3][j] = pk2(yn[r - 3][j], yn[r][j]);
+    }
+    if (r >= CF_HALO) {
+      // every lane forms the output (no divergent branch, so no load is sunk into one); rows past
+      // the sequence end and lanes past d only skip the store
+      const int i = r - CF_HALO;
+      const int t = t0 + i;
+      {
+        float y[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float a = __builtin_amdgcn_fdot2_f32_bf16(q[i][j], __builtin_bit_cast(bf16x2, wa[j]), 0.f, false);
+          y[j] = __builtin_amdgcn_fdot2_f32_bf16(q[i + 6][j], __builtin_bit_cast(bf16x2, wb[j]), a, false);
+        }
+        const uint32_t yp0 = __builtin_bit_cast(uint32_t, pk2(y[0], y[1]));
+        const uint32_t yp1 = __builtin_bit_cast(uint32_t, pk2(y[2], y[3]));
+        const float yr[4] = {lo_f(yp0), hi_f(yp0), lo_f(yp1), hi_f(yp1)};
+        float act[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = __builtin_amdgcn_exp2f(-yr[j] * 1.4426950408889634f);
+          act[j] = yr[j] * __builtin_amdgcn_rcpf(1.0f + e);
+        }
+        uint2 o;
+        if (residual) {
+          const uint32_t ap0 = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+          const uint32_t ap1 = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+          o.x = __builtin_bit_cast(uint32_t, pk2(xf[0] + lo_f(ap0), xf[1] + hi_f(ap0)));
+          o.y = __builtin_bit_cast(uint32_t, pk2(xf[2] + lo_f(ap1), xf[3] + hi_f(ap1)));
+        } else {
+          o.x = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+          o.y = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+        }
+        if (t < T && active) *reinterpret_cast<uint2*>(out + (row0 + t) * d + c) = o;
+      }
+    }
+  }
+}
+
 template <bool FUSED>
 int rmsnorm_launch(const void* x, const void* w, int dtype, int64_t rows, int32_t dim, float eps, void* out,
                           hipStream_t s) {
@@ -554,35 +578,33 @@ int lng_rmsnorm(const void* x, const void* w, int dtype, int64_t rows, int32_t d
 int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_partials, const void* norm_w,
                           const void* conv_w, int64_t B, int64_t T, int32_t d, int32_t K, int32_t dilation, float eps,
                           int residual, void* out, void* stream) {
-  if (B < 0 || T < 0 || d <= 0 || d % 8 || n_partials <= 0) return fail(LNG_E_ARG, "causal_conv_rowsq: bad shape");
+  if (B < 0 || T < 0 || d <= 0 || d % 4 || n_partials <= 0) return fail(LNG_E_ARG, "causal_conv_rowsq: bad shape");
   if (K != 4 || dilation != 3) return fail(LNG_E_ARG, "causal_conv_rowsq: kernel 4 / dilation 3 only");
   if (mixed == out) return fail(LNG_E_ARG, "causal_conv_rowsq: out must not alias mixed");
-  if (n_partials > RSQ_MAXP || d > 2048 || B > 65535)
-    return fail(LNG_E_ARG, "causal_conv_rowsq: needs d <= 2048 (at most 16 partials) and B <= 65535");
-  const int64_t n = B * T * (d / 8);
-  if (n == 0) return LNG_OK;
-  if (n >= (int64_t{1} << 31) || B * T * d >= (int64_t{1} << 32))
-    return fail(LNG_E_ARG, "causal_conv_rowsq: tensor too large for 32-bit indexing");
-  const dim3 grid(static_cast<unsigned>(cdiv(T, RSQ_TT)), static_cast<unsigned>(B));
-  const dim3 block(static_cast<unsigned>(cdiv(d / 8, 64) * 64));
-  const uint32_t M = static_cast<uint32_t>(B * T), Tl = static_cast<uint32_t>(T), d8 = static_cast<uint32_t>(d / 8);
+  if (n_partials > CS_MAXP) return fail(LNG_E_ARG, "causal_conv_rowsq: at most 16 partials");
+  if (B * T == 0) return LNG_OK;
+  if (T >= (int64_t{1} << 30) || B * T * d >= (int64_t{1} << 40))
+    return fail(LNG_E_ARG, "causal_conv_rowsq: tensor too large");
+  const int32_t G = static_cast<int32_t>(cdiv(d, 256)), R = static_cast<int32_t>(cdiv(T, CS_SL));
+  const int64_t nb = B * G * R;
+  if (nb >= (int64_t{1} << 31)) return fail(LNG_E_ARG, "causal_conv_rowsq: too many tiles");
   const bf16* mx = static_cast<const bf16*>(mixed);
   const bf16* nw = static_cast<const bf16*>(norm_w);
   const bf16* cw = static_cast<const bf16*>(conv_w);
   bf16* o = static_cast<bf16*>(out);
+  const int64_t M = B * T;
+  const int32_t Ti = static_cast<int32_t>(T);
   hipStream_t s = as_stream(stream);
+  const dim3 grid(static_cast<unsigned>(nb));
   if (n_partials <= 2)
-    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<2>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M, Tl, d8,
-                       eps, residual, o);
-  else if (n_partials <= 4)
-    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<4>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M, Tl, d8,
-                       eps, residual, o);
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 2>), grid, dim3(64), 0, s, mx, rowsq, n_partials, nw, cw, Ti,
+                       d, G, R, M, eps, residual, o);
   else if (n_partials <= 8)
-    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<8>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M, Tl, d8,
-                       eps, residual, o);
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 8>), grid, dim3(64), 0, s, mx, rowsq, n_partials, nw, cw, Ti,
+                       d, G, R, M, eps, residual, o);
   else
-    hipLaunchKernelGGL(k_causal_conv_k4d3_rowsq<RSQ_MAXP>, grid, block, 0, s, mx, rowsq, n_partials, nw, cw, M,
-                       Tl, d8, eps, residual, o);
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, CS_MAXP>), grid, dim3(64), 0, s, mx, rowsq, n_partials, nw,
+                       cw, Ti, d, G, R, M, eps, residual, o);
   return check_launch("causal_conv_rowsq");
 }
 

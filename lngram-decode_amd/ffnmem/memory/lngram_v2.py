@@ -441,12 +441,12 @@ class _RouteNgramMemoryBase(nn.Module):
         if segment_ids is not None:
             raise NotImplementedError("packed-segment causal conv is not part of the MI355X path")
         flat = head_output.reshape(b, t, self.readout_inner_dim)
-        if self.short_conv.takes_row_stats(flat.dtype) and self.readout_inner_dim % 32 == 0 and b * t < 1024:
-            # small batches: the projection kernel also writes the conv's RMSNorm row statistics
+        if self.short_conv.takes_row_stats(flat.dtype) and self.readout_inner_dim % 32 == 0:
+            # the projection kernel also writes the conv's RMSNorm row statistics
             mixed, rowsq = ops.linear_rowsq(flat, self.readout_o_proj.weight)
             return self.short_conv.forward_residual_stats(mixed, rowsq)
-        # large batches: the projection on hipBLASLt, then the single-pass conv (row statistics
-        # formed inside its blocks)
+        # other dtypes and widths: the projection, then the single-pass conv (row statistics formed
+        # inside its blocks)
         mixed = ops.linear(flat, self.readout_o_proj.weight)
         return self.short_conv.forward_residual(mixed)
 
