@@ -186,6 +186,16 @@ int32_t lng_linear_rowsq_partials(int64_t N);
 int lng_linear_rowsq(const void* x, const void* w, int64_t M, int64_t N, int64_t K, void* y, float* rowsq,
                      void* stream);
 
+/* bf16 y[M,N] = (x[M,K] . w[N,K]^T) * rsqrt(mean_k(x[m,k]^2) + eps): a projection of RMSNorm(x),
+ * the norm's weight folded into w's columns (lng_fold_columns), with each row's RMS scale formed
+ * inside the GEMM from the x rows it streams.  The query projection of the fused memory readout,
+ * q = W_q RMSNorm(h) (_project_query, lngram_v2.py:1115-1118), which then needs no q_rows.
+ * Shapes: lng_linear_rowscale_ok(M, N, K) != 0 (M >= 1024, N >= 64, N % 8 == 0, K % 64 == 0);
+ * other shapes return LNG_E_ARG. */
+int32_t lng_linear_rowscale_ok(int64_t M, int64_t N, int64_t K);
+int lng_linear_rowscale(const void* x, const void* w, int64_t M, int64_t N, int64_t K, float eps, void* y,
+                        void* stream);
+
 /* rowsq[m] (fp32) = sum_c x[m, c]^2 over bf16 rows [rows, d]: the RMSNorm statistic of the short
  * conv's input (DepthwiseCausalConv, lngram_v2.py:273-286) as one partial for lng_causal_conv_rowsq,
  * for output projections that do not produce it in their epilogue. */

@@ -530,14 +530,20 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
 //   statistics, summed in that fixed order by its consumer).
 // - Blocks go to the 8 XCDs round-robin; with the M tiles a multiple of 8, the N tiles of one M
 //   tile run on one XCD, so that token slice is fetched into one L2.
+// - XRMS (the query projection of the memory readout): every block streams its X rows over the
+//   whole of K, so it also forms each row's sum of squares from the B fragments it reads
+//   (v_dot2_f32_bf16 beside the MFMAs) and scales the row's outputs by rsqrt(mean(x^2) + x_eps)
+//   before rounding: y = (x . w^T) / rms(x), a row RMSNorm (its weight folded into w) applied
+//   without a pass over x of its own.
 constexpr int PT = 256, PK = 64, P_ROWS = 2 * PT, P_STAGE = P_ROWS * PK;
 constexpr int P_FN = 4, P_FM = 2;      // 32 x 32 fragments per wave: 4 (W rows) x 2 (X rows)
 constexpr int P_DPW = P_ROWS / 8 / 8;  // buffer loads (8 rows each) per wave per stage
 
+template <bool XRMS>
 __global__ __launch_bounds__(512, 1) void k_gemm_proj_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
                                                            int64_t N, int64_t M, int64_t K, int n_tiles,
                                                            int xcd_local, bf16* __restrict__ out,
-                                                           float* __restrict__ rowsq) {
+                                                           float* __restrict__ rowsq, float x_eps) {
   __shared__ __attribute__((aligned(16))) bf16 ring[2 * P_STAGE];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -583,11 +589,23 @@ __global__ __launch_bounds__(512, 1) void k_gemm_proj_bf16(const bf16* __restric
     for (int j = 0; j < P_FM; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  float xss[P_FM] = {0.f, 0.f};  // XRMS: sum of squares of this lane's k pieces of X row 32 j + r31
   auto mm = [&](const bf16x8* a, const bf16x8* bb) {
 #pragma unroll
     for (int i = 0; i < P_FN; ++i)
 #pragma unroll
       for (int j = 0; j < P_FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], bb[j], acc[i][j], 0, 0, 0);
+    if (XRMS) {
+#pragma unroll
+      for (int j = 0; j < P_FM; ++j) {
+        const bf16x2 p0 = __builtin_shufflevector(bb[j], bb[j], 0, 1), p1 = __builtin_shufflevector(bb[j], bb[j], 2, 3);
+        const bf16x2 p2 = __builtin_shufflevector(bb[j], bb[j], 4, 5), p3 = __builtin_shufflevector(bb[j], bb[j], 6, 7);
+        xss[j] = __builtin_amdgcn_fdot2_f32_bf16(p0, p0, xss[j], false);
+        xss[j] = __builtin_amdgcn_fdot2_f32_bf16(p1, p1, xss[j], false);
+        xss[j] = __builtin_amdgcn_fdot2_f32_bf16(p2, p2, xss[j], false);
+        xss[j] = __builtin_amdgcn_fdot2_f32_bf16(p3, p3, xss[j], false);
+      }
+    }
   };
   constexpr int NR = P_FN + P_FM, NMF = P_FN * P_FM;
   auto interleave_reads = [&]() {  // one LDS read after each of the first NR MFMAs
@@ -636,6 +654,17 @@ __global__ __launch_bounds__(512, 1) void k_gemm_proj_bf16(const bf16* __restric
   // lane (r31, hi) holds token t = 32 j + r31 of the wave's 64 and channels 32 i + 8 g + 4 hi + e of
   // its 128; the wave's tile goes to LDS as [64][128] bf16 rows, 16 B unit u of row t at u ^ (t & 15)
   bf16* tl = ring + wave * 64 * 128;
+  if (XRMS) {
+#pragma unroll
+    for (int j = 0; j < P_FM; ++j) {
+      const float ss = xss[j] + __shfl_xor(xss[j], 32, 64);  // the other half of the row's k pieces
+      const float rs = __builtin_amdgcn_rsqf(ss / static_cast<float>(K) + x_eps);
+#pragma unroll
+      for (int i = 0; i < P_FN; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] *= rs;
+    }
+  }
   float ps[P_FM] = {0.f, 0.f};
 #pragma unroll
   for (int i = 0; i < P_FN; ++i)
@@ -833,12 +862,17 @@ static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64
 static bool proj_shape(int64_t N, int64_t M, int64_t K) { return M >= 1024 && N >= 64 && K % PK == 0 && N % 8 == 0; }
 
 static int launch_proj(const bf16* w, const bf16* x, int64_t N, int64_t M, int64_t K, bf16* out, float* rowsq,
-                       hipStream_t s) {
+                       hipStream_t s, bool x_rms = false, float x_eps = 0.f) {
   const int n_tiles = static_cast<int>(cdiv(N, PT));
   const int64_t m_tiles = cdiv(M, PT);
   const int xcd_local = m_tiles % 8 == 0 ? static_cast<int>(m_tiles / 8) : 0;
-  hipLaunchKernelGGL(k_gemm_proj_bf16, dim3(static_cast<unsigned>(n_tiles * m_tiles)), dim3(512), 0, s, w, x, N, M,
-                     K, n_tiles, xcd_local, out, rowsq);
+  const dim3 grid(static_cast<unsigned>(n_tiles * m_tiles));
+  if (x_rms)
+    hipLaunchKernelGGL(k_gemm_proj_bf16<true>, grid, dim3(512), 0, s, w, x, N, M, K, n_tiles, xcd_local, out, rowsq,
+                       x_eps);
+  else
+    hipLaunchKernelGGL(k_gemm_proj_bf16<false>, grid, dim3(512), 0, s, w, x, N, M, K, n_tiles, xcd_local, out, rowsq,
+                       x_eps);
   return check_launch("gemm_bf16_proj");
 }
 
@@ -894,6 +928,18 @@ int lng_linear_rowsq(const void* x, const void* w, int64_t M, int64_t N, int64_t
                        rowsq, as_stream(stream));
   return launch_mfma<EPI_BF16>(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, y, nullptr,
                                nullptr, 0, 0, as_stream(stream), rowsq);
+}
+
+int32_t lng_linear_rowscale_ok(int64_t M, int64_t N, int64_t K) { return proj_shape(N, M, K) ? 1 : 0; }
+
+int lng_linear_rowscale(const void* x, const void* w, int64_t M, int64_t N, int64_t K, float eps, void* y,
+                        void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(LNG_E_ARG, "linear_rowscale: bad shape");
+  if (M == 0) return LNG_OK;
+  if (!proj_shape(N, M, K))
+    return fail(LNG_E_ARG, "linear_rowscale: needs M >= 1024, N >= 64, N % 8 == 0 and K % 64 == 0");
+  return launch_proj(static_cast<const bf16*>(w), static_cast<const bf16*>(x), N, M, K, static_cast<bf16*>(y), nullptr,
+                     as_stream(stream), true, eps);
 }
 
 int lng_linear(const void* x, const void* w, int dtype, int64_t M, int64_t N, int64_t K, void* y, void* stream) {

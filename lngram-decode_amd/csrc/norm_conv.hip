@@ -282,7 +282,6 @@ __global__ __launch_bounds__(256) void k_row_sumsq_bf16(const bf16* __restrict__
 constexpr int CF_HALO = 9;
 constexpr int CF_MAXG = 32;  // 16-lane groups per block: d <= 2048
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 // v[k] summed over each 16-lane row of the wave, returned in every lane of the row (fixed
@@ -426,29 +425,33 @@ __global__ __launch_bounds__(512) void k_causal_conv_k4d3_fused(const bf16* __re
 // bf16, kernel 4, dilation 3, with the row sums of squares formed by the producing GEMM
 // (rowsq[p][m], P <= MAXP partials per row m = b*T + t, summed in the fixed order p = 0, 1, ...).
 // One wave streams one (sequence, 256-channel group, SL-position range): lane l owns channels
-// 4l .. 4l+3 of the group.  All SL + 9 rows (the range and its causal halo) are requested at
+// 4l .. 4l+3 of the group; a block holds WPB consecutive such tiles.  All SL + 9 rows (the range and its causal halo) are requested at
 // kernel entry; each output is formed as soon as its four rows have arrived, so the arithmetic of
 // the early rows overlaps the loads of the later ones, with no block barrier and no reduction in
 // the kernel.  Lane r (< SL + 9) turns the partials of row t0 - 9 + r into that row's scale,
 // which the wave reads back as a scalar.  The rounding sequence is k_causal_conv_k4d3_fused's.
 // Ranges are numbered so that consecutive ranges of a sequence land on one XCD (blocks go to the
 // 8 XCDs round-robin), where a range's halo rows were fetched by the range before it.
-constexpr int CS_SL = 32;
+constexpr int CS_SL = 16;   // 16 positions + 9 halo rows, 4 waves a block: 18.7 us at B8 x T2048 x d1024
+constexpr int CS_WPB = 4;  // (32 positions: 20.6 us; one-wave blocks: 21.2 us; 64 positions: 24.3 us)
 constexpr int CS_MAXP = 16;
 
 template <int SL, int MAXP>
-__global__ __launch_bounds__(64) void k_causal_conv_k4d3_stream(const bf16* __restrict__ mixed,
+__global__ __launch_bounds__(64 * CS_WPB) void k_causal_conv_k4d3_stream(const bf16* __restrict__ mixed,
                                                                 const float* __restrict__ rowsq, int32_t P,
                                                                 const bf16* __restrict__ norm_w,
                                                                 const bf16* __restrict__ conv_w, int32_t T,
-                                                                int32_t d, int32_t G, int32_t R, int64_t M, float eps,
-                                                                int residual, bf16* __restrict__ out) {
+                                                                int32_t d, int32_t G, int32_t R, int64_t B_tiles,
+                                                                int64_t M, float eps, int residual,
+                                                                bf16* __restrict__ out) {
   constexpr int ROWS = SL + CF_HALO;
-  const int lane = threadIdx.x;
-  // the host keeps the tile count below 2^31
-  uint32_t tile = blockIdx.x;
-  const uint32_t nb = gridDim.x;
+  const int lane = threadIdx.x & 63;
+  // the host keeps the tile count below 2^31 (and pads it to whole blocks: tiles past the end exit)
+  const uint32_t ntiles = static_cast<uint32_t>(B_tiles);
+  uint32_t tile = blockIdx.x * CS_WPB + (threadIdx.x >> 6);
+  const uint32_t nb = gridDim.x * CS_WPB;
   if ((nb & 7) == 0) tile = (tile & 7) * (nb >> 3) + (tile >> 3);
+  if (tile >= ntiles) return;  // no barrier follows
   const uint32_t gr = tile / static_cast<uint32_t>(G);
   const int cg = static_cast<int>(tile - gr * static_cast<uint32_t>(G));
   const uint32_t bb = gr / static_cast<uint32_t>(R);
@@ -595,16 +598,16 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
   const int64_t M = B * T;
   const int32_t Ti = static_cast<int32_t>(T);
   hipStream_t s = as_stream(stream);
-  const dim3 grid(static_cast<unsigned>(nb));
+  const dim3 grid(static_cast<unsigned>(cdiv(nb, CS_WPB))), block(64 * CS_WPB);
   if (n_partials <= 2)
-    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 2>), grid, dim3(64), 0, s, mx, rowsq, n_partials, nw, cw, Ti,
-                       d, G, R, M, eps, residual, o);
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 2>), grid, block, 0, s, mx, rowsq, n_partials, nw, cw, Ti,
+                       d, G, R, nb, M, eps, residual, o);
   else if (n_partials <= 8)
-    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 8>), grid, dim3(64), 0, s, mx, rowsq, n_partials, nw, cw, Ti,
-                       d, G, R, M, eps, residual, o);
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 8>), grid, block, 0, s, mx, rowsq, n_partials, nw, cw, Ti,
+                       d, G, R, nb, M, eps, residual, o);
   else
-    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, CS_MAXP>), grid, dim3(64), 0, s, mx, rowsq, n_partials, nw,
-                       cw, Ti, d, G, R, M, eps, residual, o);
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, CS_MAXP>), grid, block, 0, s, mx, rowsq, n_partials, nw,
+                       cw, Ti, d, G, R, nb, M, eps, residual, o);
   return check_launch("causal_conv_rowsq");
 }
 

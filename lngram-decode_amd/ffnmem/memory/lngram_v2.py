@@ -506,11 +506,17 @@ class _RouteNgramMemoryBase(nn.Module):
             # the query RMSNorm's weight is folded into the projection and its row scale applied in
             # the readout kernel, so the normalised hidden states are never written out
             kv_pack = self._fused_weights()
-            q_raw = ops.linear(hidden_states, self._folded_query_weight())
-            head = ops.memory_readout_fused(q_raw, route_codes_btr, self.tables["ngram_2"].weight,
+            wq = self._folded_query_weight()
+            if ops.linear_rowscale_ok(hidden_states, wq):
+                # large batches: the projection kernel forms each row's RMS scale from the rows it
+                # streams, so the readout reads no hidden rows
+                q, q_rows = ops.linear_rowscale(hidden_states, wq, self.readout_query_norm.eps), None
+            else:
+                q, q_rows = ops.linear(hidden_states, wq), hidden_states
+            head = ops.memory_readout_fused(q, route_codes_btr, self.tables["ngram_2"].weight,
                                             self.tables["ngram_3"].weight, kv_pack, self.readout_memory_norm.weight,
                                             self.readout_memory_norm.eps, self.softmax_scale,
-                                            self.readout_sink_logit, q_rows=hidden_states,
+                                            self.readout_sink_logit, q_rows=q_rows,
                                             q_eps=self.readout_query_norm.eps)
             head_output = head.view(b, t, self.readout_num_heads, self.readout_head_dim)
         else:

@@ -88,6 +88,8 @@ SIGNATURES = {
                                   _p]),
     "lng_linear_rowsq_partials": (_i32, [_i64]),
     "lng_linear_rowsq": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
+    "lng_linear_rowscale_ok": (_i32, [_i64, _i64, _i64]),
+    "lng_linear_rowscale": (_int, [_p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "lng_row_sumsq": (_int, [_p, _i64, _i32, _p, _p]),
     "lng_causal_conv_rowsq": (_int, [_p, _p, _i32, _p, _p, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
     "lng_memory_readout_fused": (_int, [_p, _p, _f, _p, _i64, _i64, _i32, _p, _p, _p, _p, _f, _f, _f, _p, _p]),

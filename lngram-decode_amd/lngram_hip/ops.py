@@ -314,6 +314,29 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def linear_rowscale_ok(x: torch.Tensor, w: torch.Tensor) -> bool:
+    """Whether :func:`linear_rowscale` serves this bf16 shape (``lng_linear_rowscale_ok``)."""
+    k = x.shape[-1]
+    return (x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16 and w.dim() == 2 and w.shape[1] == k
+            and bool(lib().lng_linear_rowscale_ok(x.numel() // k, w.shape[0], k)))
+
+
+def linear_rowscale(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """bf16 ``(x . w^T) * rsqrt(mean(x^2, -1) + eps)`` per row (``lng_linear_rowscale``): the projection
+    of ``RMSNorm(x)`` with the norm's weight folded into ``w``, the row scale formed inside the GEMM."""
+    dev = _dev(x, w)
+    k = x.shape[-1]
+    x2 = _c(x.reshape(-1, k))
+    wc = _c(w)
+    if x.dtype != torch.bfloat16 or wc.dtype != torch.bfloat16 or wc.shape[1] != k:
+        raise ValueError("linear_rowscale needs bf16 x [..., K] and w [N, K]")
+    n = wc.shape[0]
+    out = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=dev)
+    check(lib().lng_linear_rowscale(_ptr(x2), _ptr(wc), x2.shape[0], n, k, float(eps), _ptr(out), _stream(dev)),
+          "linear_rowscale")
+    return out
+
+
 def _at_args(cache: torch.Tensor, pos0_dev: torch.Tensor | None):
     if cache.dim() != 3 or not cache.is_contiguous():
         raise ValueError("the cache must be a contiguous [B, S, N] tensor")

@@ -238,6 +238,30 @@ def test_linear_rowsq_and_conv_from_row_stats(dev, b, t, d, k):
         ops.causal_conv_rowsq(y.to(dev), rowsq.to(dev), nw, cw, 2, cfg.eps)
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 1024, 1024), (1280, 200, 128)])
+def test_linear_rowscale(dev, m, n, k):
+    # the query projection with the RMSNorm row scale formed inside the GEMM
+    # (_project_query, lngram_v2.py:1115-1118, the norm weight folded into w): against fp64, and
+    # against the plain projection scaled afterwards
+    g = torch.Generator().manual_seed(m + n)
+    x = (torch.randn(m, k, generator=g) * 0.7).bfloat16()
+    x[3] = 0                                   # a zero row: scale rsqrt(eps)
+    w = (torch.randn(n, k, generator=g) * 0.03).bfloat16()
+    eps = 1e-5
+    assert ops.linear_rowscale_ok(x.to(dev), w.to(dev))
+    got = ops.linear_rowscale(x.to(dev), w.to(dev), eps).cpu()
+    xd = x.double()
+    ref = (xd @ w.double().T) * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + eps)
+    assert om.rel_err(got, ref) < 1e-2
+    assert float((got.double() - ref).abs().max()) <= float(ref.abs().max()) * 2 ** -7
+    plain = ops.linear(x.to(dev), w.to(dev)).cpu().float()
+    scaled = plain * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps)
+    assert float((got.float() - scaled).abs().max()) <= float(scaled.abs().max()) * 2 ** -6
+    assert not ops.linear_rowscale_ok(x[:512].to(dev), w.to(dev))
+    with pytest.raises(RuntimeError):
+        ops.linear_rowscale(x[:512].to(dev), w.to(dev), eps)
+
+
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
 def test_causal_conv_generic_shape(dev, dtype, tol):
     # kernel 3, dilation 2, odd width: the general (non-specialised) conv kernel
