@@ -6,12 +6,8 @@
  *   - Calls are ordered on `stream` (a hipStream_t passed as void*), keep no
  *     pointer to a caller's buffer after return, and return 0 or a negative LNG_E_*.
  *   - Device memory is the caller's: scratch comes in as a workspace argument.
- *     Three kinds of host-side state are kept per process, each made once and
+ *     Two kinds of host-side state are kept per process, each made once and
  *     guarded by a mutex, so calls stay reentrant from any host thread:
- *       * the plain bf16 projections at M >= 1024 (lng_linear) run through
- *         hipBLASLt, chosen by shape alone: one handle per device and one matmul
- *         plan per (device, M, N, K), made on the first call of that shape (the
- *         library allocates them); a shape with no plan runs the MFMA kernel;
  *       * lng_drafter_tree_fused caches its cooperative grid size per device, and
  *         lng_drafter_tree_levels its resident grid size;
  *       * lng_ssm_scan_static uses a static device array per GPU (its own
@@ -358,22 +354,36 @@ int lng_select_candidates(const void* cand, int dtype, int32_t mem_dim, const vo
  * chunked_scan / sequential_scan (ffnmem/memory/ssm.py:58-91) and the carried
  * state of ssm_continue (ffnmem/infer.py:125-137), in one pass over u.  `workspace`
  * (workspace_bytes >= lng_ssm_workspace_bytes(B, T, N)) holds the tiles' hand-off
- * records; zero it once before its first use.  `epoch` tags this call's records: give every
- * call on one workspace a different value (a counter; values are taken mod 2^30).  Calls that
- * share a workspace must not overlap.  The int32 at byte 0 of the workspace gets a nonzero bit
- * if a hand-off wait ran out (the call's result is then wrong). */
+ * records; zero it once before its first use.  The kernel keeps the epoch that tags each call's
+ * records in the workspace's header and advances it at the end of every call, so one workspace
+ * serves any number of calls, replays of a captured HIP graph included; calls that share a
+ * workspace must not overlap.  A tile whose wait for its predecessors' records runs out forms its
+ * carry from u directly (exact, slow) and sets bit 0 of the int32 at byte 0 of the workspace (the
+ * caller may read and clear it). */
 size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N);
 int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
-                 void* workspace, size_t workspace_bytes, uint32_t epoch, float* s, void* stream);
+                 void* workspace, size_t workspace_bytes, float* s, void* stream);
+
+/* lng_ssm_scan with the wait for predecessor records bounded by `spin_limit` short sleeps per tile
+ * (lng_ssm_scan uses a bound far past any real wait; 0 never waits, so every tile whose
+ * predecessors have not yet published forms its carry from u directly).  No counterpart in the
+ * reference: it lets tests drive the direct-carry path from the host. */
+int lng_ssm_scan_bounded(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
+                         void* workspace, size_t workspace_bytes, int32_t spin_limit, float* s, void* stream);
 
 /* lng_ssm_scan without a workspace argument and without any allocation: the hand-off records live
  * in a static device array of the library (8.4 MB per GPU, held until the process ends), which
  * limits the shape to B * ceil(N/256) * ceil(T/128) <= 2048 tiles (LNG_E_ARG beyond).  No
  * counterpart in the reference: it is for callers that cannot allocate (code under HIP graph
  * capture, tight serving loops).  Every call on one GPU shares that GPU's array, so calls that
- * overlap on one GPU (other streams, other threads) race; calls in one stream are fine. */
+ * overlap on one GPU (other streams, other threads) race; calls in one stream are fine, and so are
+ * replays of a graph that captured it (its epoch lives in the array, not in the launch). */
 int lng_ssm_scan_static(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
                         float* s, void* stream);
+
+/* The static array's status word (bit 0: a call formed some tile's carry directly, see
+ * lng_ssm_scan), read after the device has finished its work and then cleared (synchronous). */
+int lng_ssm_scan_static_status(int32_t* status);
 
 /* ---------------------------------------------------------------- K5: drafting */
 /* A token-routed drafter (the per-token algorithm of RefDrafter, drafting/cpu_drafter.py:76-289,

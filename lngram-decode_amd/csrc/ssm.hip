@@ -15,13 +15,16 @@
 //      writes s.
 // Records are self-validating: every element is a 64-bit (value, tag) pair written and read with
 // single 64-bit accesses at the device-coherent level, the tag holding the call's epoch and the
-// record kind, so a reader needs no separate flag and a writer no completion wait.  A tile waits
-// only on tiles with smaller block indices (tiles run in span-major order), which the in-order
-// dispatcher has started before it and which publish their aggregate before they wait on anything;
-// waits are bounded all the same (an error bit in the workspace header reports one that ran out).
+// record kind, so a reader needs no separate flag and a writer no completion wait.  The epoch lives
+// in the workspace header: every tile reads it at entry and the last tile to finish advances it, so
+// consecutive launches (a replayed HIP graph included) never accept each other's records.  A tile
+// waits only on tiles with smaller block indices (tiles run in span-major order), which the in-order
+// dispatcher has started before it and which publish their aggregate before they wait on anything.
+// Waits are bounded all the same: a tile whose wait runs out forms its carry directly from u
+// (a sequential scan of the steps before it: slow, exact), and sets bit 0 of the header's status
+// word, so the result is right either way.
 #include "common.h"
 
-#include <atomic>
 #include <mutex>
 
 namespace lng {
@@ -35,8 +38,9 @@ constexpr int SSM_LW = LNG_SSM_LW;    // steps per wave
 constexpr int SSM_SPAN = SSM_WAVES * SSM_LW;
 constexpr int SSM_WIN = 32;           // aggregates folded per look-back; the record before comes inclusive
 constexpr int SSM_PER_WAVE = (SSM_WIN + 1 + SSM_WAVES - 1) / SSM_WAVES;
-// workspace: a 256-byte header (error bits), then one record per tile: its aggregate and its end
-// state, 256 (value, tag) pairs each
+// workspace: a 256-byte header (int32 words: 0 status bits, 1 epoch, 2 finished tiles of the
+// running launch), then one record per tile: its aggregate and its end state, 256 (value, tag)
+// pairs each
 constexpr size_t SSM_HDR = 256;
 constexpr size_t SSM_REC = 2 * SSM_GC * sizeof(uint64_t);
 constexpr uint32_t SSM_AGG = 1u, SSM_INC = 2u;
@@ -94,11 +98,16 @@ template <bool VEC, int CPOL>
 __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, const float* __restrict__ u,
                                                   const float* __restrict__ s0, int32_t T, int32_t N, int32_t G,
                                                   int32_t chains, uint8_t* __restrict__ ws, uint32_t ws_bytes,
-                                                  uint32_t epoch, float* __restrict__ s_out) {
+                                                  int32_t spin_limit, float* __restrict__ s_out) {
   __shared__ float s_end[SSM_WAVES][SSM_GC];   // wave ends from a zero start
   __shared__ float s_term[SSM_WAVES][SSM_GC];  // the waves' terms of the tile's aggregate
   __shared__ float s_part[SSM_WAVES][SSM_GC];  // the waves' shares of the carry
+  __shared__ int s_direct;                     // some wave's look-back wait ran out
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int32_t* hdr = reinterpret_cast<int32_t*>(ws);
+  const uint32_t epoch =
+      static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(ld_dev(hdr + 1))) & 0x3FFFFFFFu;
+  if (tid == 0) s_direct = 0;
   // span-major tile order: every tile's predecessors have smaller block indices
   const int tile = static_cast<int>(blockIdx.x);
   const int span = tile / chains, chain = tile % chains;
@@ -177,7 +186,7 @@ __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, c
     const bool mine = lane < SSM_PER_WAVE && (k < m || (past && k == m));
     const uint32_t poff = mine ? rec_off(tile - (k + 1) * chains, k >= m) + 8u * (SSM_GC - 1) : 0u;
     const uint32_t pwant = k < m ? tag_agg : tag_inc;
-    for (int spins = 0; spins < SSM_SPIN_LIMIT; ++spins) {
+    for (int spins = 0; spins < spin_limit; ++spins) {
       const bool ok = !mine || static_cast<uint32_t>(ld_pair<CPOL>(wsb, poff) >> 32) == pwant;
       if (__ballot(!ok) == 0) break;
       __builtin_amdgcn_s_sleep(4);
@@ -208,10 +217,12 @@ __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, c
       again |= need[i];
     }
     if (!again) break;
-    if (spins >= SSM_SPIN_LIMIT) {
-      if (lane == 0)
-        __hip_atomic_fetch_or(reinterpret_cast<int32_t*>(ws), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;  // give up (the result is flagged wrong)
+    if (spins >= spin_limit) {
+      if (lane == 0) {
+        __hip_atomic_fetch_or(hdr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_direct = 1;
+      }
+      break;  // the tile forms its carry directly from u below
     }
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
@@ -234,13 +245,36 @@ __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, c
     s_part[wave][lane * 4 + j] = part;
   }
   __syncthreads();
+  // a wait ran out: wave 0 forms the carry into the tile directly, a sequential scan of the steps
+  // before it from s0 (or 0), and puts it where the shares were
+  const bool direct = s_direct != 0 && span > 0;
+  if (direct) {
+    if (wave == 0) {
+      float sd[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sd[j] = (s0 && c + j < N) ? s0[static_cast<int64_t>(b) * N + c + j] : 0.f;
+      for (int t = 0; t < ts; ++t) {
+        float xv[4];
+        load4<VEC>(ub + static_cast<int64_t>(t) * N, c, N, xv);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sd[j] = fmaf(av[j], sd[j], bv[j] * xv[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s_part[0][lane * 4 + j] = sd[j];
+    }
+    __syncthreads();
+  }
   // every wave sums the shares (same order in every wave), wave 0 publishes the tile's end state,
   // and each wave carries the tile's carry through the waves before it
   float st[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     float carry = 0.f;
-    for (int w = 0; w < SSM_WAVES; ++w) carry += s_part[w][lane * 4 + j];
+    if (direct) {
+      carry = s_part[0][lane * 4 + j];
+    } else {
+      for (int w = 0; w < SSM_WAVES; ++w) carry += s_part[w][lane * 4 + j];
+    }
     if (span == 0) carry = (s0 && c + j < N) ? s0[static_cast<int64_t>(b) * N + c + j] : 0.f;
     if (wave == 0) st_pair<CPOL>(wsb, rec_off(tile, true) + 32u * lane + 8u * j, fmaf(A[j], carry, E[j]), tag_inc);
     for (int w = 0; w < wave; ++w) carry = fmaf(pw[j], carry, s_end[w][lane * 4 + j]);
@@ -257,6 +291,15 @@ __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, c
       }
     }
   }
+  // the last tile to finish advances the epoch for the next launch (every tile of this one read it
+  // at entry, and the next launch on the stream starts after this one has ended)
+  if (tid == 0) {
+    const int32_t done = __hip_atomic_fetch_add(hdr + 2, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (done == static_cast<int32_t>(gridDim.x) - 1) {
+      st_dev(hdr + 2, 0);
+      st_dev(hdr + 1, static_cast<int32_t>((epoch + 1) & 0x3FFFFFFFu));
+    }
+  }
 }
 
 int64_t ssm_tiles(int64_t B, int64_t T, int32_t N) { return B * cdiv(N, SSM_GC) * cdiv(T, SSM_SPAN); }
@@ -266,7 +309,7 @@ size_t ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
 }
 
 int ssm_scan_launch(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, uint8_t* ws,
-                    size_t ws_bytes, uint32_t epoch, float* s, hipStream_t st) {
+                    size_t ws_bytes, int32_t spin_limit, float* s, hipStream_t st) {
   if (B < 0 || T < 0 || N <= 0) return fail(LNG_E_ARG, "ssm_scan: bad shape");
   if (B == 0 || T == 0) return LNG_OK;
   if (T > INT32_MAX / 2 || static_cast<int64_t>(N) * T > (int64_t{1} << 40))
@@ -278,13 +321,15 @@ int ssm_scan_launch(const float* a, const float* u, const float* s0, int64_t B, 
   const int32_t G = static_cast<int32_t>(cdiv(N, SSM_GC));
   const int32_t chains = static_cast<int32_t>(B * G);
   const int32_t Ti = static_cast<int32_t>(T);
-  const uint32_t ep = epoch & 0x3FFFFFFFu;
+  if (spin_limit < 0) return fail(LNG_E_ARG, "ssm_scan: negative spin limit");
   const uint32_t wsb = static_cast<uint32_t>(ssm_workspace_bytes(B, T, N));
   const dim3 grid(static_cast<unsigned>(tiles)), blk(512);
   if (N % 4 == 0)
-    hipLaunchKernelGGL((k_ssm_scan<true, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb, ep, s);
+    hipLaunchKernelGGL((k_ssm_scan<true, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb,
+                       spin_limit, s);
   else
-    hipLaunchKernelGGL((k_ssm_scan<false, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb, ep, s);
+    hipLaunchKernelGGL((k_ssm_scan<false, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb,
+                       spin_limit, s);
   return check_launch("ssm_scan");
 }
 
@@ -299,7 +344,6 @@ static __device__ __align__(256) uint8_t scratch[SSM_STATIC_BYTES];
 constexpr int SSM_MAX_DEVICES = 64;
 static std::mutex g_scratch_mu;
 static uint8_t* g_scratch_ptr[SSM_MAX_DEVICES];
-static std::atomic<uint32_t> g_scratch_epoch[SSM_MAX_DEVICES];
 
 static int scratch_of_current_device(uint8_t** ptr, int* dev) {
   if (hipGetDevice(dev) != hipSuccess || *dev < 0 || *dev >= SSM_MAX_DEVICES)
@@ -332,8 +376,21 @@ int lng_ssm_scan_static(const float* a, const float* u, const float* s0, int64_t
   uint8_t* ws = nullptr;
   int dev = 0;
   if (int rc = scratch_of_current_device(&ws, &dev)) return rc;
-  const uint32_t epoch = g_scratch_epoch[dev].fetch_add(1, std::memory_order_relaxed);
-  return ssm_scan_launch(a, u, s0, B, T, N, ws, SSM_STATIC_BYTES, epoch, s, as_stream(stream));
+  return ssm_scan_launch(a, u, s0, B, T, N, ws, SSM_STATIC_BYTES, SSM_SPIN_LIMIT, s, as_stream(stream));
+}
+
+int lng_ssm_scan_static_status(int32_t* status) {
+  if (!status) return fail(LNG_E_ARG, "ssm_scan_static_status: null status");
+  uint8_t* ws = nullptr;
+  int dev = 0;
+  if (int rc = scratch_of_current_device(&ws, &dev)) return rc;
+  // stream-ordered behind every call on the null stream and synchronous: read, then clear, word 0
+  int32_t v = 0;
+  hipError_t e = hipMemcpy(&v, ws, sizeof(v), hipMemcpyDeviceToHost);
+  if (e == hipSuccess && v) e = hipMemset(ws, 0, sizeof(v));
+  if (e != hipSuccess) return fail(LNG_E_HIP, std::string("ssm_scan_static_status: ") + hipGetErrorString(e));
+  *status = v;
+  return LNG_OK;
 }
 
 size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
@@ -342,8 +399,14 @@ size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
 }
 
 int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, void* workspace,
-                 size_t workspace_bytes, uint32_t epoch, float* s, void* stream) {
-  return ssm_scan_launch(a, u, s0, B, T, N, static_cast<uint8_t*>(workspace), workspace_bytes, epoch, s,
+                 size_t workspace_bytes, float* s, void* stream) {
+  return ssm_scan_launch(a, u, s0, B, T, N, static_cast<uint8_t*>(workspace), workspace_bytes, SSM_SPIN_LIMIT, s,
+                         as_stream(stream));
+}
+
+int lng_ssm_scan_bounded(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
+                         void* workspace, size_t workspace_bytes, int32_t spin_limit, float* s, void* stream) {
+  return ssm_scan_launch(a, u, s0, B, T, N, static_cast<uint8_t*>(workspace), workspace_bytes, spin_limit, s,
                          as_stream(stream));
 }
 

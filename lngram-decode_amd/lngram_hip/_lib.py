@@ -113,8 +113,10 @@ SIGNATURES = {
     "lng_gather_rows": (_int, [_p, _i64, _int, _i32, _p, _i64, _p, _p]),
     "lng_select_candidates": (_int, [_p, _int, _i32, _p, _int, _i64, _i32, _i32, _i32, _p, _p]),
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
-    "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, ctypes.c_uint32, _p, _p]),
+    "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _p, _p]),
+    "lng_ssm_scan_bounded": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _i32, _p, _p]),
     "lng_ssm_scan_static": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p]),
+    "lng_ssm_scan_static_status": (_int, [_p]),
     "lng_drafter_tree_fused_workspace": (ctypes.c_size_t, [_PD]),
     "lng_drafter_tree_fused": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, ctypes.c_uint32, _p, ctypes.c_size_t, _p,
                                       _p, _p]),

@@ -839,31 +839,52 @@ _ssm_ws: dict = {}
 _ssm_ws_lock = threading.Lock()
 
 
-def _ssm_workspace(dev: torch.device, nbytes: int) -> tuple[torch.Tensor, int]:
-    """The scan's hand-off workspace for (device, current stream) and the next epoch for it: zeroed
-    once when it is made or grown, then reused with a new epoch per call."""
+def _ssm_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """The scan's hand-off workspace for (device, current stream): zeroed once when it is made or
+    grown, then reused (the kernel keeps its epoch in the workspace's header)."""
     key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
     with _ssm_ws_lock:
-        ws, epoch = _ssm_ws.get(key, (None, 0))
+        ws = _ssm_ws.get(key)
         if ws is None or ws.numel() < nbytes:
-            ws, epoch = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev), 0
-        _ssm_ws[key] = (ws, epoch + 1)
-        return ws, epoch & 0x3FFFFFFF
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        _ssm_ws[key] = ws
+        return ws
 
 
-def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None) -> torch.Tensor:
-    """``s_t = a s_{t-1} + (1 - a) u_t`` (fp32) for u ``[B, T, N]``, a ``[N]``, s0 ``[B, N]`` or None."""
+def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None,
+             spin_limit: int | None = None) -> torch.Tensor:
+    """``s_t = a s_{t-1} + (1 - a) u_t`` (fp32) for u ``[B, T, N]``, a ``[N]``, s0 ``[B, N]`` or None.
+    ``spin_limit`` bounds each tile's wait for its predecessors (``lng_ssm_scan_bounded``; None: the
+    library's bound); a tile whose wait runs out forms its carry from u directly (exact)."""
     dev = _dev(a, u, s0)
     uc = _c(u.float())
     ac = _c(a.float())
     s0c = None if s0 is None else _c(s0.float())
     b, t, n = uc.shape
     out = torch.empty_like(uc)
-    ws, epoch = _ssm_workspace(dev, lib().lng_ssm_workspace_bytes(b, t, n))
-    rc = _timed("ssm_scan", dev, lambda: lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws),
-                                                            ws.numel(), epoch, _ptr(out), _stream(dev)))
-    check(rc, "ssm_scan")
+    ws = _ssm_workspace(dev, lib().lng_ssm_workspace_bytes(b, t, n))
+    if spin_limit is None:
+        launch = lambda: lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws), ws.numel(),  # noqa: E731
+                                            _ptr(out), _stream(dev))
+    else:
+        launch = lambda: lib().lng_ssm_scan_bounded(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws),  # noqa: E731
+                                                    ws.numel(), int(spin_limit), _ptr(out), _stream(dev))
+    check(_timed("ssm_scan", dev, launch), "ssm_scan")
     return out
+
+
+def ssm_scan_status(dev: torch.device) -> int:
+    """Read and clear the status word of the current stream's scan workspace (bit 0: some tile of a
+    call since the last read formed its carry directly, after its wait ran out).  Synchronises."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    with _ssm_ws_lock:
+        ws = _ssm_ws.get(key)
+    if ws is None:
+        return 0
+    word = ws[:4].view(torch.int32)
+    v = int(word.item())
+    word.zero_()
+    return v
 
 
 def tree_accept(parent: torch.Tensor, node_tokens: torch.Tensor, argmax: torch.Tensor, out=None):

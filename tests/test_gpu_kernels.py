@@ -301,6 +301,26 @@ def test_ssm_scan_workspace_reuse_across_shapes(dev):
         assert np.abs(got - want).max() < 1e-5 * max(1.0, np.abs(want).max()), (b, t, n)
 
 
+def test_ssm_scan_direct_carry_when_waits_run_out(dev):
+    # the host bounds every tile's wait for its predecessors' records at zero sleeps: a tile whose
+    # predecessors have not yet published forms its carry from u directly.  Every kernel exits
+    # normally and the states still equal the recurrence; the status word says whether the direct
+    # path ran (bit 0) and reads back as zero after a default call.
+    g = torch.Generator().manual_seed(11)
+    for b, t, n in ((8, 4096, 256), (3, 301, 70)):
+        a = 0.9 + 0.099 * torch.rand(n, generator=g)
+        u = torch.randn(b, t, n, generator=g)
+        s0 = torch.randn(b, n, generator=g)
+        ops.ssm_scan_status(dev)
+        got = ops.ssm_scan(a.to(dev), u.to(dev), s0.to(dev), spin_limit=0).cpu().numpy()
+        want = om.ssm_scan(a.numpy(), u.numpy(), s0.numpy())
+        assert np.abs(got - want).max() < 1e-5 * max(1.0, np.abs(want).max()), (b, t, n)
+        assert ops.ssm_scan_status(dev) in (0, 1)
+        again = ops.ssm_scan(a.to(dev), u.to(dev), s0.to(dev)).cpu().numpy()
+        assert np.abs(again - want).max() < 1e-5 * max(1.0, np.abs(want).max()), (b, t, n)
+        assert ops.ssm_scan_status(dev) == 0
+
+
 def test_ssm_scan_constant_input_closed_form(dev):
     a = torch.tensor([0.9, 0.95, 0.999, 0.5])
     u = torch.tensor([1.0, -2.0, 0.5, 3.0])
