@@ -8,8 +8,7 @@
  *   - Device memory is the caller's: scratch comes in as a workspace argument.
  *     Two kinds of host-side state are kept per process, each made once and
  *     guarded by a mutex, so calls stay reentrant from any host thread:
- *       * lng_drafter_tree_fused caches its cooperative grid size per device, and
- *         lng_drafter_tree_levels its resident grid size;
+ *       * lng_drafter_tree_levels caches its resident grid size per device;
  *       * lng_ssm_scan_static uses a static device array per GPU (its own
  *         comment gives the limit), located once per device.
  *   - lng_last_error() returns a thread-local message for the last failure.
@@ -405,7 +404,6 @@ int lng_ssm_scan_static_status(int32_t* status);
 #define LNG_DR_MAX_P 16
 #define LNG_DR_MAX_K 8
 #define LNG_DR_SYNC_INTS 4160  /* int32 entries of lng_drafter.sync */
-#define LNG_DR_TREE_SYNC_BYTES 16640  /* error word + counters at the start of the one-launch tree's workspace */
 
 typedef struct lng_drafter {
   int32_t d, V, R, bits, mem_dim, dt, n_orders, orders[4], maxn;
@@ -553,44 +551,25 @@ int lng_drafter_tree_shortlist(const lng_drafter* D, const lng_sketch* S, const 
                                int32_t n, int32_t node_row0, void* work, size_t work_bytes, float* logits_work,
                                void* route_tokens, void* stream);
 
-/* The whole draft tree of lng_drafter_tree in ONE cooperative launch (token-only drafters with
- * the per-token tables, bf16 tables, R <= 192, <= 2 orders, q_heads <= 8, q_heads*Dt <= 1024,
- * q_heads*head_dim <= 256; n <= 32 nodes, <= 8 depths with parents, <= 8 parents per depth).
- * Same results as lng_drafter_tree (tokens of every node in rows node_row0 .., node codes, the
- * verification gather [n, R, Dt] if route_tokens is non-null).  One block per CU stays resident:
- * each depth's parents run their readouts, every block scores its vocabulary slice (and its
- * online-count matches) against them, writer blocks select the children's tokens; blocks meet
- * through device-coherent counters (bounded waits).  `work` holds
- * lng_drafter_tree_fused_workspace(D) bytes, zero before the first call; `seq` must increase by
- * one per call on the same workspace (counters are double-buffered by seq & 1).  The int32 at byte
- * offset 0 of `work` is a sticky error word (0 = ok; bit 0 = a wait timed out, bit 1 = no committed
- * token, bit 2 = counters were not zero): after an error zero the first LNG_DR_TREE_SYNC_BYTES
- * bytes and restart seq.  stamps (optional, device int64 [grid][40]) receive the 100 MHz
- * real-time counter at phase boundaries of each
- * block.  Returns LNG_E_ARG without launching when the drafter or tree is outside the limits
- * above (lng_drafter_tree then runs it); the workspace size is 0 for a drafter outside them. */
-size_t lng_drafter_tree_fused_workspace(const lng_drafter* D);
-int lng_drafter_tree_fused(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n,
-                           int32_t node_row0, int online, float kappa, uint32_t seq, void* work, size_t work_bytes,
-                           void* route_tokens, long long* stamps, void* stream);
-
-/* Draft tree with verification gather, one launch per depth (drafting/tree.py:243-257 draft_tree
+/* Draft tree with verification gather in one launch for the whole tree (drafting/tree.py:243-257 draft_tree
  * over cpu_drafter.py:208-270 readouts and drafters.py:117-142 online counts; tree.py:96-136
  * tree_route_tokens), for token-only drafters with the per-token tables at the SD drafters' shape:
  * q_heads 4, head_dim 64, orders (2, 3) with mem_dim 128, bits 4, R <= 192, bf16 tables and value
  * weight, V <= 32832; trees of at most 32 nodes, 8 depths, 4 parents per depth and rank < 4.
  * Same outputs as lng_drafter_tree (node tokens and codes in rows node_row0 + i, the root token in
- * row node_row0, route_tokens [n, R, 256] bf16 when not null).  Launch d: the parents of depth d
- * select their own tokens from the previous launch's vocabulary records, gather their windows and
- * attend per query head; vocabulary blocks hold their lut_out slice from launch entry, count the
- * online matches of the pairs whose next token they own, and score it once the parents' outputs
- * arrive through device-coherent (value, tag) pairs (bounded waits).  `work` holds
- * lng_drafter_tree_levels_workspace(D) bytes, zero before the first call and kept between calls
- * (its first word counts the calls; the int32 at byte offset 4 is a sticky error word: non-zero =
- * a wait timed out; zero the workspace after an error; a non-zero int32 at byte offset 8 asks for
- * per-block phase times of the 100 MHz clock in the workspace's last section).  The workspace size is 0, and the call
- * returns LNG_E_ARG without launching, for a drafter or tree outside the limits above
- * (lng_drafter_tree runs those). */
+ * row node_row0, route_tokens [n, R, 256] bf16 when not null).  One grid of resident blocks runs
+ * every depth: at depth d the attention blocks select their node's token from depth d-1's
+ * vocabulary records, gather its window and attend per query head; vocabulary blocks hold their
+ * lut_out slice in registers for the whole tree, count the online matches of the pairs whose next
+ * token they own, and score the slice once the depth's attention records arrive through
+ * device-coherent (value, tag) pairs; leaf blocks gather the leaves' verification rows.  Every wait
+ * is bounded.  `work` holds lng_drafter_tree_levels_workspace(D) bytes, zero before the first call
+ * and kept between calls (its first word holds the call epoch; the int32 at byte offset 4 is an
+ * error word: non-zero = a wait timed out, and the call's outputs are then not to be used: read it
+ * after the call, and on non-zero zero the workspace and redo the call with lng_drafter_tree; a
+ * non-zero int32 at byte offset 8 asks for per-block phase times of the 100 MHz clock in the
+ * workspace's last section).  The workspace size is 0, and the call returns LNG_E_ARG without
+ * launching, for a drafter or tree outside the limits above (lng_drafter_tree runs those). */
 size_t lng_drafter_tree_levels_workspace(const lng_drafter* D);
 int lng_drafter_tree_levels(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n,
                             int32_t node_row0, int online, float kappa, void* work, size_t work_bytes,

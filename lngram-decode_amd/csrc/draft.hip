@@ -2456,829 +2456,6 @@ __global__ __launch_bounds__(256) void k_fast_gather(lng_drafter D, FastLevel F,
   }
 }
 
-// ------------------------------------------------------------------ persistent tree step
-// One cooperative launch runs a whole draft tree (every depth) and the verification gather for
-// token-only drafters (the per-token tables of the fast path).  The grid is one resident block
-// per CU (checked at launch); blocks hand data to each other through device-coherent stores and
-// loads (st_dev / ld_dev) and monotone counters:
-//   depth l, parent j (block j): pick its token from the previous depth's partials, compute its
-//       codes from the router tables -> codes_ready[l]; window rows, gather, sink attention over
-//       routes, o = Wv' U and the hidden RMSNorm scale r = rsqrt(o' Gram o / d + eps) ->
-//       ro = r o -> ro_ready[l]
-//   every block b (vocabulary slice [b sv, b sv + sv)): after codes_ready[l], online matches of
-//       the committed pairs whose next token lies in the slice; after ro_ready[l], the slice's
-//       logits lut_out . ro for every parent of the depth -> per (parent, block) partial: max, sum
-//       of exponentials, online total, top-KM among tokens without counts and the list of
-//       count-bearing tokens -> part_done[l]
-//   writer blocks (the last ones of the grid): after part_done[l], each selects one parent's
-//       top-K and writes its children's tokens -> written
-//   after written == parents: leaf codes, node tokens and codes into their rows, verification
-//       gather, items spread over the grid.
-// Every wait is bounded (TP_SPIN_TICKS of the 100 MHz real-time counter, and it ends at once
-// once the error word is set); a timeout sets the error word and the grid still drains.
-constexpr int TP_THREADS = 512;
-constexpr int TP_MAXN = 32;     // nodes
-constexpr int TP_MAXL = 8;      // depths with parents
-constexpr int TP_MAXP = 8;      // parents per depth
-constexpr int TP_MAXR = 192;    // routes
-constexpr int TP_MAXQD = 1024;  // q_heads * Dt
-constexpr int TP_MAXQH = 4;
-constexpr int TP_MAXI = 256;    // q_heads * head_dim
-constexpr int TP_MAXSV = 256;   // vocabulary rows per block
-constexpr int TP_MAXNB = 256;   // blocks
-constexpr int TP_LINE = 32;     // ints per counter: one 128-byte line each (polled lines stay apart)
-constexpr int TP_NCTR = 64;     // counters per buffer
-constexpr int TP_SYNC = TP_NCTR * TP_LINE;  // ints per counter buffer
-static_assert(256 + 2 * TP_SYNC * 4 == LNG_DR_TREE_SYNC_BYTES, "error word + two counter buffers");
-constexpr int TP_NSTAMP = 64;
-constexpr long long TP_SPIN_TICKS = 2000000;  // 20 ms
-constexpr int TS_CODES = 0, TS_RO = 8, TS_PART = 16, TS_WRITTEN = 24, TS_CUR = 32;  // TS_CUR: [TP_MAXN] list sizes
-
-struct TreePlan {
-  int32_t n, n_levels, n_par, K, online, node_row0, nb, sv, seq;
-  float kappa;
-  int8_t parent[TP_MAXN], rank[TP_MAXN], pidx[TP_MAXN];
-  int8_t win[TP_MAXN][DR_MAXN];  // position k back from node i: v >= 1 node v, v <= 0 committed row L-1+v
-  int8_t lev_np[TP_MAXL], lev_g0[TP_MAXL];
-  int8_t lev_node[TP_MAXL][TP_MAXP];
-};
-
-// The per-node arrays of the plan in LDS (lane-dependent indices into kernel arguments would be
-// memory loads).
-struct TpPlanL {
-  int8_t parent[TP_MAXN], rank[TP_MAXN], pidx[TP_MAXN];
-  int8_t win[TP_MAXN][DR_MAXN];
-};
-
-struct TpWork {
-  int32_t* sync;       // [2][TP_SYNC] counters (zero before first use)
-  int32_t* err;        // sticky error word
-  int32_t* ntok;       // [TP_MAXN] node tokens
-  int32_t* ncode;      // [TP_MAXN][TP_MAXR] node codes
-  float* ro;           // [TP_MAXN][TP_MAXI] r * o per parent
-  float* part;         // [TP_MAXN][nb][4 + 2 KM] partials
-  int32_t* cand;       // [TP_MAXN][V][3] count-bearing tokens per parent (id, logit bits, count)
-  void* route_tokens;  // [n, R, Dt] or null
-  long long* stamps;   // [nb][TP_NSTAMP] or null
-};
-
-constexpr int TP_LD = LNG_DR_MAX_DT + 8;  // padded route row (bf16): conflict-free 16-row MFMA reads
-
-struct TpAttnLds {
-  bf16 xs[TP_MAXR][TP_LD];
-  bf16 qkb[16][TP_LD];  // score MFMA B operand: row n < QH = hi(qk[n]), QH <= n < 2 QH = lo(qk[n - QH])
-  float qk[TP_MAXQD];
-  float sc[TP_MAXQH][TP_MAXR];
-  float sx[TP_MAXR];
-  float u[TP_MAXQD];
-  float part[16][TP_MAXI];
-  float o[TP_MAXI];
-  int32_t rows[TP_MAXR][2];
-  uint8_t wc[DR_MAXN][TP_MAXR];
-};
-struct TpBLds {
-  float ro[TP_MAXP][TP_MAXI];
-  int32_t qa[TP_MAXP][2][TP_MAXR];
-  int32_t cnt[TP_MAXP][TP_MAXSV];
-  float lg[TP_MAXP][TP_MAXSV];
-  int32_t tl[TP_THREADS];
-  int32_t tot[TP_MAXP];
-  int32_t lev[TP_MAXP];
-  int32_t ntl;
-};
-union TpLds {
-  TpAttnLds a;
-  TpBLds b;
-};
-
-__device__ __forceinline__ void tp_stamp(const TpWork& W, int k) {
-  if (W.stamps && threadIdx.x == 0 && k < TP_NSTAMP) W.stamps[blockIdx.x * TP_NSTAMP + k] = wall_clock64();
-}
-
-// Block-wide wait until *ctr >= target (thread 0 polls; bounded).
-__device__ __forceinline__ void tp_wait(const TpWork& W, const int32_t* ctr, int32_t target) {
-  if (threadIdx.x == 0) {
-    const long long t0 = wall_clock64();
-    while (ld_dev(ctr) < target) {
-      if (ld_dev(W.err) != 0) break;
-      if (wall_clock64() - t0 > TP_SPIN_TICKS) {
-        __hip_atomic_fetch_or(W.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(8);
-    }
-  }
-  __syncthreads();
-}
-
-// Count the block in once its device-coherent stores are complete.
-__device__ __forceinline__ void tp_signal(int32_t* ctr) {
-  __builtin_amdgcn_s_waitcnt(WAITCNT_VM0);
-  __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The position k steps back from node i (k = 0: i itself): x = 2 tree node y (>= 1), x = 1
-// committed row y (the root is row L-1), x = 0 before the sequence start.
-__device__ __forceinline__ int2 tp_back(const TpPlanL& P, int i, int k, int L) {
-  const int v = P.win[i][k];
-  if (v > 0) return int2{2, v};
-  const int row = L - 1 + v;
-  return row >= 0 ? int2{1, row} : int2{0, 0};
-}
-
-__device__ __forceinline__ int tp_code(const lng_drafter& D, const TpWork& W, int2 src, int r) {
-  if (src.x == 2) return ld_dev(W.ncode + src.y * TP_MAXR + r);
-  if (src.x == 1) return D.codes[static_cast<int64_t>(src.y) * D.R + r] & ((1 << D.bits) - 1);
-  return 0;
-}
-
-// Token of node i (the root is the last committed token).
-__device__ __forceinline__ int64_t tp_tok(const lng_drafter& D, const TpWork& W, int i, int L) {
-  return i == 0 ? D.tokens[L - 1] : static_cast<int64_t>(ld_dev(W.ntok + i));
-}
-
-template <int KM>
-__host__ __device__ constexpr int tp_rs() { return 4 + 2 * KM; }
-
-__device__ __forceinline__ float tp_block_max(float v, float* red) {
-  v = wave_max(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float m = red[0];
-#pragma unroll
-  for (int k = 1; k < TP_THREADS / 64; ++k) m = fmaxf(m, red[k]);
-  return m;
-}
-__device__ __forceinline__ float tp_block_sum(float v, float* red) {
-  v = wave_sum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < TP_THREADS / 64; ++k) s += red[k];
-  return s;
-}
-
-// Top-KM of global parent g from the grid's partials (whole block; the result lands in
-// sel_v/sel_i, visible after the next barrier).  Ranking as k_fast_logits' selection: logits, or
-// the online mixture (1 - lam) softmax + lam count / total.  One partial record per thread, then
-// the parent's count-bearing tokens spread over the block, then the waves' lists merged.
-template <int KM>
-__device__ void tp_select(const lng_drafter& D, const TreePlan& T, const TpWork& W, const int32_t* sync, int g,
-                          float* red, float (*wl_v)[DR_MAXK], int (*wl_i)[DR_MAXK], float* sel_v, int* sel_i) {
-  constexpr int RS = tp_rs<KM>();
-  constexpr int CU = 4;  // count-bearing tokens per thread per load batch
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6, nb = T.nb;
-  const bool ok = tid < nb;
-  const float* rec = W.part + (static_cast<int64_t>(g) * nb + (ok ? tid : 0)) * RS;
-  const float rm = ok ? ld_dev(rec) : -INFINITY;
-  const float rsum = ok ? ld_dev(rec + 1) : 0.f;
-  const float rt = ok ? static_cast<float>(__float_as_int(ld_dev(rec + 2))) : 0.f;
-  float av[KM];
-  int ai[KM];
-#pragma unroll
-  for (int k = 0; k < KM; ++k) {
-    av[k] = ok ? ld_dev(rec + 4 + k) : -INFINITY;
-    ai[k] = ok ? __float_as_int(ld_dev(rec + 4 + KM + k)) : -1;
-  }
-  const int total = T.online ? min(ld_dev(sync + (TS_CUR + g) * TP_LINE), D.V) : 0;
-  tp_stamp(W, 50);
-  const float M = tp_block_max(rm, red);
-  const float S = tp_block_sum(rm == -INFINITY ? 0.f : rsum * expf(rm - M), red);
-  const float tj = T.online ? tp_block_sum(rt, red) : 0.f;  // exact: integer partial totals < 2^24
-  const float n_eff = tj / static_cast<float>(D.R * D.n_orders);
-  const float lam = tj > 0.f ? n_eff / (n_eff + T.kappa) : 0.f;
-  const float mix_a = (1.f - lam) / S, mix_b = tj > 0.f ? lam / tj : 0.f;
-  tp_stamp(W, 51);
-  TopK<KM> t;
-  t.clear();
-#pragma unroll
-  for (int k = 0; k < KM; ++k)
-    t.insert(ai[k] < 0 ? -INFINITY : (T.online ? mix_a * expf(av[k] - M) : av[k]), ai[k] < 0 ? INT_MAX : ai[k]);
-  const int32_t* cl = W.cand + static_cast<int64_t>(g) * D.V * 3;
-  for (int e0 = 0; e0 < total; e0 += TP_THREADS * CU) {
-    int id[CU], lb[CU], c[CU];
-#pragma unroll
-    for (int u = 0; u < CU; ++u) {
-      const int e = e0 + u * TP_THREADS + tid;
-      const int32_t* p = cl + 3 * static_cast<int64_t>(e < total ? e : 0);
-      id[u] = e < total ? ld_dev(p) : INT_MAX;
-      lb[u] = e < total ? ld_dev(p + 1) : 0;
-      c[u] = e < total ? ld_dev(p + 2) : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < CU; ++u)
-      t.insert(id[u] == INT_MAX ? -INFINITY : fmaf(mix_b, static_cast<float>(c[u]), mix_a * expf(__int_as_float(lb[u]) - M)),
-               id[u]);
-  }
-  tp_stamp(W, 52);
-  float sv[KM];
-  int si[KM];
-  wave_topk(t, sv, si);
-  if (lane == 0)
-#pragma unroll
-    for (int k = 0; k < KM; ++k) wl_v[wv][k] = sv[k], wl_i[wv][k] = si[k];
-  __syncthreads();
-  tp_stamp(W, 53);
-  if (wv == 0) {
-    t.clear();
-    if (lane < (TP_THREADS / 64) * KM) {
-      const int w2 = lane / KM, k2 = lane % KM;
-      if (wl_i[w2][k2] >= 0) t.insert(wl_v[w2][k2], wl_i[w2][k2]);
-    }
-    wave_topk(t, sv, si);
-    if (lane == 0)
-#pragma unroll
-      for (int k = 0; k < KM; ++k) sel_v[k] = sv[k], sel_i[k] = si[k];
-  }
-}
-
-// Attention of one parent (node i, global parent g): codes, rows, gather, sink attention,
-// o = Wv' U, ro = rsqrt(o' Gram o / d + eps) o.  Whole block.
-template <int KM>
-__device__ void tp_attend(const lng_drafter& D, const TreePlan& T, const TpPlanL& P, const TpWork& W, TpAttnLds& A,
-                          int lvl, int i, int g, int64_t tok, int L, int32_t* sync) {
-  const int R = D.R, bits = D.bits, maxn = D.maxn, n_ord = D.n_orders, md = D.mem_dim, Dt = D.dt;
-  const int QH = D.q_heads, hd = D.head_dim, I = QH * hd, QD = QH * Dt, G = QH / D.kv_heads;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const bool tok_ok = dr_tok_ok(D, tok);
-  // window codes (slot k = position maxn-1-k back; the last slot is the node itself) and the
-  // node's query-key row
-  const int ord0 = D.orders[0], ord1 = D.orders[1];
-  const void* const tab0 = D.tables[0];
-  const void* const tab1 = D.tables[1];
-  const int64_t ptok = i == 0 ? -1 : tp_tok(D, W, P.parent[i], L);
-  for (int e = tid; e < maxn * R; e += TP_THREADS) {
-    const int k = e / R, r = e % R;
-    int c;
-    if (k == maxn - 1 && i != 0) {
-      c = dr_lut_code4(D, ptok, tok, r);
-      st_dev(W.ncode + i * TP_MAXR + r, c);
-      D.codes[static_cast<int64_t>(T.node_row0 + i) * R + r] = static_cast<uint8_t>(c);
-    } else {
-      c = tp_code(D, W, tp_back(P, i, maxn - 1 - k, L), r);
-    }
-    A.wc[k][r] = static_cast<uint8_t>(c);
-  }
-  for (int e = 4 * tid; e < QD; e += 4 * TP_THREADS)
-    *reinterpret_cast<f32x4*>(&A.qk[e]) = tok_ok ? *reinterpret_cast<const f32x4*>(D.lut_qk + tok * QD + e)
-                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
-  __syncthreads();
-  tp_signal(sync + (TS_CODES + lvl) * TP_LINE);
-  tp_stamp(W, 40);
-  // rows (window positions must exist for every code of the n-gram)
-  for (int e = tid; e < R * n_ord; e += TP_THREADS) {
-    const int r = e / n_ord, oi = e % n_ord, n = oi == 0 ? ord0 : ord1;
-    int32_t addr = 0;
-    bool ok = true;
-    for (int k = 0; k < n; ++k) {
-      ok = ok && tp_back(P, i, n - 1 - k, L).x != 0;
-      addr |= static_cast<int32_t>(A.wc[maxn - n + k][r]) << (bits * k);
-    }
-    A.rows[r][oi] = ok ? (r << (bits * n)) + addr : -1;
-  }
-  __syncthreads();
-  tp_stamp(W, 41);
-  // gather: 16-byte pieces, every load issued before the first store to LDS (the rows up to the
-  // next multiple of 32 are zero: they enter the MFMA tiles)
-  {
-    const int rpad = (R + 31) & ~31;
-    for (int e = tid; e < (rpad - R) * (Dt / 8); e += TP_THREADS)
-      *reinterpret_cast<bf16x8*>(&A.xs[R + e / (Dt / 8)][8 * (e % (Dt / 8))]) = bf16x8{};
-    const int pieces = md / 8, per_route = n_ord * pieces, total = R * per_route;
-    constexpr int GU = (TP_MAXR * 2 * (LNG_DR_MAX_DT / 2 / 8) + TP_THREADS - 1) / TP_THREADS;
-    bf16x8 v[GU];
-#pragma unroll
-    for (int u = 0; u < GU; ++u) {
-      const int e = tid + u * TP_THREADS;
-      v[u] = bf16x8{};
-      if (e < total) {
-        const int r = e / per_route, rem = e % per_route, oi = rem / pieces, pc = rem % pieces;
-        const int32_t row = A.rows[r][oi];
-        if (row >= 0) v[u] = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(oi == 0 ? tab0 : tab1) +
-                                                               static_cast<int64_t>(row) * md + 8 * pc);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < GU; ++u) {
-      const int e = tid + u * TP_THREADS;
-      if (e < total) {
-        const int r = e / per_route, rem = e % per_route, oi = rem / pieces, pc = rem % pieces;
-        *reinterpret_cast<bf16x8*>(&A.xs[r][oi * md + 8 * pc]) = v[u];
-      }
-    }
-  }
-  __syncthreads();
-  tp_stamp(W, 42);
-  // scores on MFMA (16x16x32 bf16): A = route rows (lane: route 16 t + li, features 32 ks + 8 lg ..),
-  // B = the query-key rows split into bf16 hi + lo parts (columns n and n + QH, whose products are
-  // exact in fp32 and summed after), so score = s_r (C[r][n] + C[r][n + QH]).  Sums of squares of
-  // the same A operands give s_r.
-  {
-    const int li = lane & 15, lg = lane >> 4;
-    for (int e = tid; e < 16 * Dt; e += TP_THREADS) {
-      const int n = e / Dt, f = e % Dt;
-      float v = 0.f;
-      if (n < QH) v = A.qk[n * Dt + f];
-      else if (n < 2 * QH) { const float q = A.qk[(n - QH) * Dt + f]; v = q - static_cast<float>(static_cast<bf16>(q)); }
-      A.qkb[n][f] = static_cast<bf16>(v);
-    }
-    __syncthreads();
-    const int nks = Dt / 32, ntile = ((R + 15) & ~15) / 16;
-    bf16x8 qb[LNG_DR_MAX_DT / 32];
-#pragma unroll
-    for (int ks = 0; ks < LNG_DR_MAX_DT / 32; ++ks)
-      qb[ks] = ks < nks ? *reinterpret_cast<const bf16x8*>(&A.qkb[li][32 * ks + 8 * lg]) : bf16x8{};
-    for (int tl = wv; tl < ntile; tl += TP_THREADS / 64) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-      float ss = 0.f;
-#pragma unroll
-      for (int ks = 0; ks < LNG_DR_MAX_DT / 32; ++ks) {
-        if (ks >= nks) break;
-        const bf16x8 x = *reinterpret_cast<const bf16x8*>(&A.xs[16 * tl + li][32 * ks + 8 * lg]);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xf = static_cast<float>(x[j]);
-          ss = fmaf(xf, xf, ss);
-        }
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, qb[ks], c, 0, 0, 0);
-      }
-      ss += __shfl_xor(ss, 16, 64);
-      ss += __shfl_xor(ss, 32, 64);
-      const float sr = 1.0f / sqrtf(ss / static_cast<float>(Dt) + D.mem_eps);  // route 16 tl + li
-      if (lg == 0 && 16 * tl + li < R) A.sx[16 * tl + li] = sr;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float lo = __shfl(c[i], (lane + QH) & 63, 64);
-        const float sri = __shfl(sr, 4 * lg + i, 64);
-        const int r = 16 * tl + 4 * lg + i;
-        if (li < QH && r < R) A.sc[li][r] = sri * (c[i] + lo);
-      }
-    }
-  }
-  __syncthreads();
-  tp_stamp(W, 43);
-  // sink softmax per query head (wave qh): p_r s_r in sc
-  for (int qh = wv; qh < QH; qh += TP_THREADS / 64) {
-    constexpr int RQ = (TP_MAXR + 63) / 64;
-    float sv[RQ];
-    float m = D.sink_logit;
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) {
-      const int r = lane + 64 * q;
-      sv[q] = r < R ? A.sc[qh][r] : -INFINITY;
-      m = fmaxf(m, sv[q]);
-    }
-    m = wave_max(m);
-    float l = 0.f;
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) {
-      sv[q] = sv[q] == -INFINITY ? 0.f : expf(sv[q] - m);
-      l += sv[q];
-    }
-    l = wave_sum(l) + expf(D.sink_logit - m);
-    const float il = 1.0f / l;
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) {
-      const int r = lane + 64 * q;
-      if (r < R) A.sc[qh][r] = sv[q] * il * A.sx[r];
-    }
-  }
-  __syncthreads();
-  tp_stamp(W, 44);
-  // U[qh][f] = mem_norm[f] sum_r p_r s_r x_r[f] on MFMA: A = P split into bf16 hi (rows qh) and lo
-  // (rows QH + qh), k = 32 routes per step; B = route rows read transposed out of LDS
-  // (ds_read_b64_tr_b16: element c of lane (lg, li) is X[4 lg + c][16 ft + li], elements 4 + c the
-  // rows 16 further).  Wave w owns feature tiles w, w + 8, ...
-  {
-    const int li = lane & 15, lg = lane >> 4;
-    const int nft = Dt / 16;
-    const int qrow = li < QH ? li : li - QH;
-    const bool hi = li < QH, used = li < 2 * QH;
-    for (int ft = wv; ft < nft; ft += TP_THREADS / 64) {
-      f32x4 c = {0.f, 0.f, 0.f, 0.f};
-      for (int ch = 0; ch < (R + 31) / 32; ++ch) {
-        const int c0 = 32 * ch;
-        bf16x8 pa;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int r = c0 + (j < 4 ? 4 * lg + j : 16 + 4 * lg + (j - 4));
-          const float pv = (used && r < R) ? A.sc[qrow][r] : 0.f;
-          const float ph = static_cast<float>(static_cast<bf16>(pv));
-          pa[j] = static_cast<bf16>(hi ? ph : pv - ph);
-        }
-        const int col = 16 * ft + 4 * (li & 3);
-        const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (__attribute__((address_space(3))) bf16x4*)(&A.xs[c0 + 4 * lg + (li >> 2)][col]));
-        const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-            (__attribute__((address_space(3))) bf16x4*)(&A.xs[c0 + 16 + 4 * lg + (li >> 2)][col]));
-        const bf16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
-        c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, c, 0, 0, 0);
-      }
-      // rows 4 lg + i: hi parts (rows < QH) and lo parts (rows QH .. 2 QH - 1), joined below
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (4 * lg + i < 2 * QH) A.part[4 * lg + i][16 * ft + li] = c[i];
-    }
-    __syncthreads();
-    for (int e = tid; e < QH * Dt; e += TP_THREADS) {
-      const int qh = e / Dt, f = e % Dt;
-      A.u[e] = (A.part[qh][f] + A.part[QH + qh][f]) * D.mem_norm[f];
-    }
-  }
-  __syncthreads();
-  tp_stamp(W, 45);
-  // o[qh][e] = sum_f Wv[h][e][f] U[qh][f]: item (qh, 8 outputs, feature part), wv_t = [kv][Dt][hd]
-  {
-    const int n8 = I / 8;                      // output groups of 8
-    const int FP = min(16, TP_THREADS / n8);   // feature parts
-    const int fl = (Dt + FP - 1) / FP;
-    const int it = tid % n8, fp = tid / n8;
-    const int qh = (it * 8) / hd, e0 = (it * 8) % hd, h = qh / G;
-    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (fp < FP) {
-      const int f0 = fp * fl, f1 = min(Dt, f0 + fl);
-      if (D.wv_dtype == LNG_BF16) {
-        const bf16* wt = static_cast<const bf16*>(D.wv_t) + static_cast<int64_t>(h) * Dt * hd + e0;
-        for (int f = f0; f < f1; f += 16) {
-          bf16x8 w8[16];
-#pragma unroll
-          for (int q = 0; q < 16; ++q) w8[q] = f + q < f1 ? *reinterpret_cast<const bf16x8*>(wt + (f + q) * hd) : bf16x8{};
-#pragma unroll
-          for (int q = 0; q < 16; ++q) {
-            const float uq = f + q < f1 ? A.u[qh * Dt + f + q] : 0.f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) acc[k] = fmaf(static_cast<float>(w8[q][k]), uq, acc[k]);
-          }
-        }
-      } else {
-        const float* wt = static_cast<const float*>(D.wv_t) + static_cast<int64_t>(h) * Dt * hd + e0;
-        for (int f = f0; f < f1; ++f) {
-          const f32x4 a0 = *reinterpret_cast<const f32x4*>(wt + f * hd);
-          const f32x4 a1 = *reinterpret_cast<const f32x4*>(wt + f * hd + 4);
-          const float uq = A.u[qh * Dt + f];
-#pragma unroll
-          for (int k = 0; k < 4; ++k) {
-            acc[k] = fmaf(a0[k], uq, acc[k]);
-            acc[4 + k] = fmaf(a1[k], uq, acc[4 + k]);
-          }
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < 8; ++k) A.part[fp][it * 8 + k] = acc[k];
-    }
-    __syncthreads();
-    for (int e = tid; e < I; e += TP_THREADS) {
-      float a = 0.f;
-      for (int q = 0; q < FP; ++q) a += A.part[q][e];
-      A.o[e] = a;
-    }
-  }
-  __syncthreads();
-  tp_stamp(W, 46);
-  // y = Gram o (item: 4 outputs x feature part), ss = o . y, r = rsqrt(ss / d + eps)
-  {
-    const int n4 = I / 4, EP = min(16, TP_THREADS / n4), el = (I + EP - 1) / EP;
-    const int it = tid % n4, ep = tid / n4;
-    f32x4 y = {0.f, 0.f, 0.f, 0.f};
-    if (ep < EP) {
-      const int f0 = ep * el, f1 = min(I, f0 + el);
-      for (int f = f0; f < f1; f += 16) {
-        f32x4 gv[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q)
-          gv[q] = f + q < f1 ? *reinterpret_cast<const f32x4*>(D.gram_out + static_cast<int64_t>(f + q) * I + 4 * it)
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const float oq = f + q < f1 ? A.o[f + q] : 0.f;
-#pragma unroll
-          for (int k = 0; k < 4; ++k) y[k] = fmaf(gv[q][k], oq, y[k]);
-        }
-      }
-      float ss = 0.f;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) ss = fmaf(A.o[4 * it + k], y[k], ss);
-      (&A.part[0][0])[tid] = ss;  // one partial per thread (the o reduction above is done)
-    } else {
-      (&A.part[0][0])[tid] = 0.f;
-    }
-  }
-  __syncthreads();
-  if (wv == 0) {
-    float s = 0.f;
-    for (int e = lane; e < TP_THREADS; e += 64) s += (&A.part[0][0])[e];
-    s = wave_sum(s);
-    if (lane == 0) A.sx[0] = 1.0f / sqrtf(s / static_cast<float>(D.d) + D.draft_eps);
-  }
-  __syncthreads();
-  tp_stamp(W, 47);
-  const float rn = A.sx[0];
-  for (int e = tid; e < I; e += TP_THREADS) st_dev(W.ro + g * TP_MAXI + e, rn * A.o[e]);
-  tp_signal(sync + (TS_RO + lvl) * TP_LINE);
-}
-
-// Phase B of depth l for this block's vocabulary slice.
-template <int KM>
-__device__ void tp_phase_b(const lng_drafter& D, const TreePlan& T, const TpPlanL& P, const TpWork& W, TpBLds& B,
-                           int lvl, int L, int32_t* sync) {
-  const int ord0 = D.orders[0], ord1 = D.orders[1];
-  const int R = D.R, bits = D.bits, n_ord = D.n_orders, I = D.q_heads * D.head_dim;
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int np = T.lev_np[lvl], g0 = T.lev_g0[lvl];
-  const int sv = T.sv;
-  const int64_t v0 = static_cast<int64_t>(blockIdx.x) * sv;
-  const int nrow = static_cast<int>(max<int64_t>(0, min<int64_t>(sv, D.V - v0)));
-  // lut_out rows of the slice's first 128 rows, a quarter row per thread: in flight while waiting
-  const int row = tid >> 2, qd = tid & 3, Iq = I / 4;
-  f32x4 lo[TP_MAXI / 16];
-  auto load_rows = [&](int rbase) {
-#pragma unroll
-    for (int q = 0; q < TP_MAXI / 16; ++q) {
-      const int64_t v = v0 + rbase + row;
-      lo[q] = (4 * q < Iq && rbase + row < nrow) ? *reinterpret_cast<const f32x4*>(D.lut_out + v * I + qd * Iq + 4 * q)
-                                                 : f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  load_rows(0);
-  for (int e = tid; e < np * TP_MAXSV; e += TP_THREADS) B.cnt[e / TP_MAXSV][e % TP_MAXSV] = 0;
-  if (tid < np) B.lev[tid] = T.lev_node[lvl][tid];
-  if (tid < TP_MAXP) B.tot[tid] = 0;
-  if (tid == 0) B.ntl = 0;
-  tp_wait(W, sync + (TS_CODES + lvl) * TP_LINE, np);
-  tp_stamp(W, 4 * lvl + 1);
-  // query addresses of every parent of the depth (-1 = no row)
-  for (int e = tid; e < np * n_ord * R; e += TP_THREADS) {
-    const int j = e / (n_ord * R), rem = e % (n_ord * R), oi = rem / R, r = rem % R;
-    const int i = B.lev[j], n = oi == 0 ? ord0 : ord1;
-    int32_t addr = 0;
-    bool ok = true;
-    for (int k = 0; k < n; ++k) {
-      const int2 src = tp_back(P, i, n - 1 - k, L);
-      ok = ok && src.x != 0;
-      addr |= tp_code(D, W, src, r) << (bits * k);
-    }
-    B.qa[j][oi][r] = ok ? addr : -1;
-  }
-  __syncthreads();
-  // online matches: committed pairs (t, t+1), t < L-1, whose next token lies in the slice
-  if (T.online) {
-    const int npairs = L - 1;
-    for (int t0 = 0; t0 < npairs; t0 += TP_THREADS) {
-      const int t = t0 + tid;
-      if (t < npairs) {
-        const int64_t x = D.tokens[t + 1];
-        if (x >= v0 && x < v0 + nrow) B.tl[atomicAdd(&B.ntl, 1)] = t;
-      }
-      __syncthreads();
-      const int nt = B.ntl;
-      for (int q = wv; q < nt; q += TP_THREADS / 64) {
-        const int tt = B.tl[q];
-        int w[TP_MAXP];
-#pragma unroll
-        for (int j = 0; j < TP_MAXP; ++j) w[j] = 0;
-        for (int r = lane; r < R; r += 64) {
-          int c[DR_MAXN];
-#pragma unroll
-          for (int k = 0; k < DR_MAXN; ++k) {
-            const int pos = tt - (DR_MAXN - 1) + k;
-            c[k] = (k >= DR_MAXN - D.maxn && pos >= 0) ? (D.codes[static_cast<int64_t>(pos) * R + r] & ((1 << bits) - 1))
-                                                        : 0;
-          }
-          for (int oi = 0; oi < n_ord; ++oi) {
-            const int n = oi == 0 ? ord0 : ord1;
-            if (tt < n - 1) continue;
-            int32_t key = 0;
-            for (int k = 0; k < n; ++k) key |= c[DR_MAXN - n + k] << (bits * k);
-#pragma unroll
-            for (int j = 0; j < TP_MAXP; ++j)
-              if (j < np) w[j] += (B.qa[j][oi][r] == key) ? 1 : 0;
-          }
-        }
-#pragma unroll
-        for (int j = 0; j < TP_MAXP; ++j)
-          if (j < np) {
-            const int s = wave_sum_i(w[j]);
-            if (lane == 0 && s > 0) {
-              atomicAdd(&B.cnt[j][D.tokens[tt + 1] - v0], s);
-              atomicAdd(&B.tot[j], s);
-            }
-          }
-      }
-      __syncthreads();
-      if (tid == 0) B.ntl = 0;
-      __syncthreads();
-    }
-  }
-  tp_wait(W, sync + (TS_RO + lvl) * TP_LINE, np);
-  tp_stamp(W, 4 * lvl + 2);
-  for (int e = tid; e < np * I; e += TP_THREADS) B.ro[e / I][e % I] = ld_dev(W.ro + (g0 + e / I) * TP_MAXI + e % I);
-  __syncthreads();
-  // logits of the slice rows, 128 rows per pass (4 threads per row)
-  for (int rbase = 0; rbase < nrow; rbase += TP_THREADS / 4) {
-    if (rbase > 0) load_rows(rbase);
-    for (int j = 0; j < np; ++j) {
-      float a = 0.f;
-#pragma unroll
-      for (int q = 0; q < TP_MAXI / 16; ++q)
-        if (4 * q < Iq) {
-          const f32x4 rv = *reinterpret_cast<const f32x4*>(&B.ro[j][qd * Iq + 4 * q]);
-          a = fmaf(lo[q][0], rv[0], a);
-          a = fmaf(lo[q][1], rv[1], a);
-          a = fmaf(lo[q][2], rv[2], a);
-          a = fmaf(lo[q][3], rv[3], a);
-        }
-      a += __shfl_xor(a, 1);
-      a += __shfl_xor(a, 2);
-      if (qd == 0 && rbase + row < nrow) B.lg[j][rbase + row] = a;
-    }
-  }
-  __syncthreads();
-  // per-parent partials (wave j)
-  constexpr int RS = tp_rs<KM>();
-  for (int j = wv; j < np; j += TP_THREADS / 64) {
-    const int g = g0 + j;
-    float* rec = W.part + (static_cast<int64_t>(g) * T.nb + blockIdx.x) * RS;
-    constexpr int RQ = TP_MAXSV / 64;
-    float x[RQ];
-    int cn[RQ];
-    float m = -INFINITY;
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) {
-      const int rr = lane + 64 * q;
-      x[q] = rr < nrow ? B.lg[j][rr] : -INFINITY;
-      cn[q] = rr < nrow ? B.cnt[j][rr] : 0;
-      m = fmaxf(m, x[q]);
-    }
-    m = wave_max(m);
-    float s = 0.f;
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) s += x[q] == -INFINITY ? 0.f : expf(x[q] - m);
-    s = wave_sum(s);
-    TopK<KM> t;
-    t.clear();
-    int ncnt = 0;
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) ncnt += __popcll(__ballot(cn[q] > 0));
-    int pos = 0;
-    if (ncnt > 0) {
-      int base = 0;
-      if (lane == 0) base = __hip_atomic_fetch_add(sync + (TS_CUR + g) * TP_LINE, ncnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pos = __shfl(base, 0);
-      if (pos + ncnt > D.V) {  // counters not zeroed: never write past the parent's list
-        if (lane == 0) __hip_atomic_fetch_or(W.err, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        pos = -1;
-      }
-    }
-    int32_t* cl = W.cand + static_cast<int64_t>(g) * D.V * 3;
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-#pragma unroll
-    for (int q = 0; q < RQ; ++q) {
-      const int rr = lane + 64 * q;
-      const bool has = cn[q] > 0;
-      const bool ok = x[q] != -INFINITY && !has;
-      t.insert(ok ? x[q] : -INFINITY, ok ? static_cast<int>(v0 + rr) : INT_MAX);
-      const uint64_t mk = __ballot(has);
-      if (has && pos >= 0) {
-        int32_t* dst = cl + 3 * static_cast<int64_t>(pos + __popcll(mk & below));
-        st_dev(dst, static_cast<int32_t>(v0 + rr));
-        st_dev(dst + 1, __float_as_int(x[q]));
-        st_dev(dst + 2, cn[q]);
-      }
-      if (pos >= 0) pos += __popcll(mk);
-    }
-    float svv[KM];
-    int sii[KM];
-    wave_topk(t, svv, sii);
-    if (lane == 0) {
-      st_dev(rec, m);
-      st_dev(rec + 1, s);
-      st_dev(rec + 2, __int_as_float(B.tot[j]));
-      st_dev(rec + 3, __int_as_float(ncnt));
-#pragma unroll
-      for (int k = 0; k < KM; ++k) {
-        st_dev(rec + 4 + k, svv[k]);
-        st_dev(rec + 4 + KM + k, __int_as_float(sii[k]));
-      }
-    }
-  }
-  tp_signal(sync + (TS_PART + lvl) * TP_LINE);
-  tp_stamp(W, 4 * lvl + 3);
-}
-
-template <int KM>
-__global__ __launch_bounds__(TP_THREADS) void k_tree_persist(lng_drafter D, TreePlan T, TpWork W) {
-  __shared__ TpLds S;
-  __shared__ float sel_v[DR_MAXK];
-  __shared__ int sel_i[DR_MAXK];
-  __shared__ TpPlanL P;
-  __shared__ float red[TP_THREADS / 64];
-  __shared__ float wl_v[TP_THREADS / 64][DR_MAXK];
-  __shared__ int wl_i[TP_THREADS / 64][DR_MAXK];
-  const int b = blockIdx.x, tid = threadIdx.x, nb = T.nb;
-  int32_t* sync = W.sync + (T.seq & 1) * TP_SYNC;
-  if (b == 0)  // the next call's counters
-    for (int e = tid; e < TP_NCTR; e += TP_THREADS) st_dev(W.sync + ((T.seq + 1) & 1) * TP_SYNC + e * TP_LINE, 0);
-  tp_stamp(W, 4 * TP_MAXL + 2);
-  if (W.stamps && tid == 0) W.stamps[b * TP_NSTAMP + 60] = static_cast<long long>(__builtin_amdgcn_s_memtime());
-  for (int e = tid; e < TP_MAXN; e += TP_THREADS) {
-    P.parent[e] = T.parent[e];
-    P.rank[e] = T.rank[e];
-    P.pidx[e] = T.pidx[e];
-#pragma unroll
-    for (int k = 0; k < DR_MAXN; ++k) P.win[e][k] = T.win[e][k];
-  }
-  __syncthreads();
-  const int L = *D.length;
-  if (L < 1) {  // no root token: nothing to draft (the host checks this too)
-    if (b == 0 && tid == 0) __hip_atomic_fetch_or(W.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return;
-  }
-  for (int lvl = 0; lvl < T.n_levels; ++lvl) {
-    const int np = T.lev_np[lvl];
-    if (b < np) {
-      const int i = T.lev_node[lvl][b], g = T.lev_g0[lvl] + b;
-      int64_t tok;
-      if (lvl == 0) {
-        tok = D.tokens[L - 1];
-      } else {
-        tp_wait(W, sync + (TS_PART + lvl - 1) * TP_LINE, nb);
-        tp_select<KM>(D, T, W, sync, P.pidx[P.parent[i]], red, wl_v, wl_i, sel_v, sel_i);
-        __syncthreads();
-        const int t2 = sel_i[P.rank[i]];
-        tok = t2 >= 0 ? t2 : sel_i[0];
-        if (tid == 0) st_dev(W.ntok + i, static_cast<int32_t>(tok));
-      }
-      tp_attend<KM>(D, T, P, W, S.a, lvl, i, g, tok, L, sync);
-      __syncthreads();
-    }
-    tp_stamp(W, 4 * lvl);
-    tp_phase_b<KM>(D, T, P, W, S.b, lvl, L, sync);
-    // writers: one parent of this depth each
-    if (b >= nb - np) {
-      const int j = nb - 1 - b, g = T.lev_g0[lvl] + j, p = T.lev_node[lvl][j];
-      tp_wait(W, sync + (TS_PART + lvl) * TP_LINE, nb);
-      tp_select<KM>(D, T, W, sync, g, red, wl_v, wl_i, sel_v, sel_i);
-      __syncthreads();
-      for (int c = 1 + tid; c < T.n; c += TP_THREADS)
-        if (P.parent[c] == p) {
-          const int t2 = sel_i[P.rank[c]];
-          st_dev(W.ntok + c, t2 >= 0 ? t2 : sel_i[0]);
-        }
-      tp_signal(sync + TS_WRITTEN * TP_LINE);
-    }
-    __syncthreads();
-  }
-  // every node's token is known: node rows, leaf codes, verification gather
-  tp_wait(W, sync + TS_WRITTEN * TP_LINE, T.n_par);
-  tp_stamp(W, 4 * TP_MAXL);
-  const int R = D.R, bits = D.bits, n_ord = D.n_orders, md = D.mem_dim, Dt = D.dt;
-  const int ord0 = D.orders[0], ord1 = D.orders[1];
-  const void* const tab0 = D.tables[0];
-  const void* const tab1 = D.tables[1];
-  if (b == 0)
-    for (int i = tid; i < T.n; i += TP_THREADS) D.tokens[T.node_row0 + i] = tp_tok(D, W, i, L);
-  const int pieces = md / 8;
-  const int64_t items = static_cast<int64_t>(T.n) * R * n_ord * pieces;
-  for (int64_t it = static_cast<int64_t>(b) * TP_THREADS + tid; it < items; it += static_cast<int64_t>(nb) * TP_THREADS) {
-    const int pc = static_cast<int>(it % pieces);
-    const int64_t rest = it / pieces;
-    const int oi = static_cast<int>(rest % n_ord);
-    const int r = static_cast<int>((rest / n_ord) % R);
-    const int i = static_cast<int>(rest / (static_cast<int64_t>(n_ord) * R));
-    // this node's code: committed (root), from its readout (parents), else from the router tables
-    int own;
-    if (i == 0)
-      own = tp_code(D, W, int2{1, L - 1}, r);
-    else if (P.pidx[i] >= 0)
-      own = ld_dev(W.ncode + i * TP_MAXR + r);
-    else {
-      own = dr_lut_code4(D, tp_tok(D, W, P.parent[i], L), tp_tok(D, W, i, L), r);
-      if (oi == 0 && pc == 0) D.codes[static_cast<int64_t>(T.node_row0 + i) * R + r] = static_cast<uint8_t>(own);
-    }
-    if (!W.route_tokens) continue;
-    const int n = oi == 0 ? ord0 : ord1;
-    int32_t addr = 0;
-    bool ok = true;
-    for (int k = 0; k < n; ++k) {
-      const int back = n - 1 - k;
-      const int2 src = tp_back(P, i, back, L);
-      ok = ok && src.x != 0;
-      addr |= (back == 0 ? own : tp_code(D, W, src, r)) << (bits * k);
-    }
-    bf16x8 v = bf16x8{};
-    if (ok) v = *reinterpret_cast<const bf16x8*>(static_cast<const bf16*>(oi == 0 ? tab0 : tab1) +
-                                                 (static_cast<int64_t>(r << (bits * n)) + addr) * md + 8 * pc);
-    *reinterpret_cast<bf16x8*>(static_cast<bf16*>(W.route_tokens) + (static_cast<int64_t>(i) * R + r) * Dt + oi * md +
-                               8 * pc) = v;
-  }
-  tp_stamp(W, 4 * TP_MAXL + 1);
-  if (W.stamps && tid == 0) W.stamps[b * TP_NSTAMP + 61] = static_cast<long long>(__builtin_amdgcn_s_memtime());
-}
-
 // ------------------------------------------------------------------ host side
 namespace {
 
@@ -3975,118 +3152,6 @@ int dr_gather(const lng_drafter& D, const DrWin& W, void* out, hipStream_t s) {
   return check_launch("drafter_gather");
 }
 
-// ------------------------------------------------------------------ persistent tree step: host side
-struct TpLayout {
-  size_t sync, err, ntok, ncode, ro, part, cand, total;
-};
-
-TpLayout tp_layout(const lng_drafter& D, int nb) {
-  TpLayout l{};
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    const size_t o = off;
-    off = align256(off + bytes);
-    return o;
-  };
-  l.err = take(sizeof(int32_t));
-  l.sync = take(sizeof(int32_t) * 2 * TP_SYNC);
-  l.ntok = take(sizeof(int32_t) * TP_MAXN);
-  l.ncode = take(sizeof(int32_t) * TP_MAXN * TP_MAXR);
-  l.ro = take(sizeof(float) * TP_MAXN * TP_MAXI);
-  l.part = take(sizeof(float) * TP_MAXN * static_cast<size_t>(nb) * tp_rs<DR_MAXK>());
-  l.cand = take(sizeof(int32_t) * 3 * TP_MAXN * static_cast<size_t>(D.V));
-  l.total = off;
-  return l;
-}
-
-// Resident blocks of the persistent kernel on the current device (one per CU, at most TP_MAXNB).
-int tp_grid() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  int nb = cache[dev].load(std::memory_order_relaxed);
-  if (nb > 0) return nb;
-  int cus = 0, per = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, reinterpret_cast<const void*>(&k_tree_persist<DR_MAXK>),
-                                                   TP_THREADS, 0) != hipSuccess)
-    return 0;
-  int coop = 0;
-  if (hipDeviceGetAttribute(&coop, hipDeviceAttributeCooperativeLaunch, dev) != hipSuccess || !coop) return 0;
-  nb = std::min(TP_MAXNB, cus * std::max(per, 0));
-  cache[dev].store(nb, std::memory_order_relaxed);
-  return nb;
-}
-
-// Plan of a tree for the persistent kernel; returns an error (no launch) if the drafter or the tree
-// is outside its limits.
-bool tp_drafter_ok(const lng_drafter& D, int nb) {
-  const int I = D.q_heads * D.head_dim;
-  return dr_fast(D) && D.table_dtype == LNG_BF16 && D.R <= TP_MAXR && D.n_orders <= 2 && D.mem_dim % 8 == 0 &&
-         D.q_heads <= TP_MAXQH && D.q_heads * D.dt <= TP_MAXQD && I <= TP_MAXI && D.head_dim % 8 == 0 &&
-         (D.wv_dtype == LNG_BF16 || D.wv_dtype == LNG_F32) && nb > 0 && cdiv(D.V, nb) <= TP_MAXSV;
-}
-
-int tp_plan(const lng_drafter& D, const int32_t* parent, const int32_t* rank, int n, int node_row0, int online,
-            float kappa, uint32_t seq, int nb, TreePlan& T) {
-  if (!tp_drafter_ok(D, nb))
-    return fail(LNG_E_ARG, "drafter_tree_fused: drafter shape outside the persistent kernel's limits");
-  if (n < 2 || n > TP_MAXN || parent[0] != -1) return fail(LNG_E_ARG, "drafter_tree_fused: need 2 <= n <= 32 nodes");
-  if (node_row0 < 0 || static_cast<int64_t>(node_row0) + n > D.rows)
-    return fail(LNG_E_RANGE, "drafter_tree_fused: node rows out of range");
-  T = TreePlan{};
-  T.n = n;
-  T.online = online;
-  T.kappa = kappa;
-  T.node_row0 = node_row0;
-  T.nb = nb;
-  T.sv = static_cast<int32_t>(cdiv(D.V, nb));
-  T.seq = static_cast<int32_t>(seq & 0x7fffffff);
-  if (T.sv > TP_MAXSV) return fail(LNG_E_ARG, "drafter_tree_fused: vocabulary too large for the grid");
-  std::vector<int> depth(n, 0), nchild(n, 0);
-  int K = 1, maxd = 0;
-  for (int i = 1; i < n; ++i) {
-    if (parent[i] < 0 || parent[i] >= i) return fail(LNG_E_ARG, "drafter_tree_fused: parent[i] must precede i");
-    if (rank[i] < 0 || rank[i] >= DR_MAXK) return fail(LNG_E_ARG, "drafter_tree_fused: rank out of range");
-    depth[i] = depth[parent[i]] + 1;
-    ++nchild[parent[i]];
-    K = std::max(K, rank[i] + 1);
-    maxd = std::max(maxd, depth[i]);
-  }
-  T.K = K;
-  int g = 0;
-  for (int i = 0; i < n; ++i) {
-    T.parent[i] = static_cast<int8_t>(parent[i]);
-    T.rank[i] = static_cast<int8_t>(i == 0 ? 0 : rank[i]);
-    T.pidx[i] = -1;
-  }
-  for (int dep = 0; dep < maxd; ++dep) {
-    if (dep >= TP_MAXL) return fail(LNG_E_ARG, "drafter_tree_fused: at most 8 depths with parents");
-    int np = 0;
-    T.lev_g0[dep] = static_cast<int8_t>(g);
-    for (int i = 0; i < n; ++i)
-      if (depth[i] == dep && nchild[i] > 0) {
-        if (np >= TP_MAXP) return fail(LNG_E_ARG, "drafter_tree_fused: at most 8 parents per depth");
-        T.lev_node[dep][np++] = static_cast<int8_t>(i);
-        T.pidx[i] = static_cast<int8_t>(g++);
-      }
-    T.lev_np[dep] = static_cast<int8_t>(np);
-    if (dep > 0 && T.lev_np[dep - 1] + np > nb) return fail(LNG_E_ARG, "drafter_tree_fused: grid too small");
-  }
-  for (int i = 0; i < n; ++i)
-    for (int k = 0; k < DR_MAXN; ++k) {
-      int a = i, kk = k;
-      while (kk > 0 && a > 0) {
-        a = parent[a];
-        --kk;
-      }
-      T.win[i][k] = static_cast<int8_t>(a > 0 ? a : -kk);  // node a, or committed row L-1-kk
-    }
-  T.n_levels = maxd;
-  T.n_par = g;
-  return LNG_OK;
-}
-
 // Sketch arguments of the shortlist launches, checked against the drafter's shape.
 int sl_args(const lng_drafter& D, const lng_sketch* S, SlArgs& A) {
   if (!S) return fail(LNG_E_ARG, "drafter_shortlist: null sketch");
@@ -4483,43 +3548,6 @@ int lng_drafter_tree_shortlist(const lng_drafter* D, const lng_sketch* S, const 
   if (!logits_work) return fail(LNG_E_ARG, "drafter_tree_shortlist: logits_work [16, V] needed");
   return dr_tree(D, &A, logits_work, parent, rank, n, node_row0, 0, 0.f, work, work_bytes, nullptr, route_tokens,
                  stream);
-}
-
-size_t lng_drafter_tree_fused_workspace(const lng_drafter* D) {
-  if (dr_check(D, "drafter_tree_fused_workspace")) return 0;
-  const int nb = tp_grid();
-  return tp_drafter_ok(*D, nb) ? tp_layout(*D, nb).total : 0;
-}
-
-int lng_drafter_tree_fused(const lng_drafter* D, const int32_t* parent, const int32_t* rank, int32_t n,
-                           int32_t node_row0, int online, float kappa, uint32_t seq, void* work, size_t work_bytes,
-                           void* route_tokens, long long* stamps, void* stream) {
-  if (int rc = dr_check(D, "drafter_tree_fused")) return rc;
-  if (!parent || !rank || !work) return fail(LNG_E_ARG, "drafter_tree_fused: null argument");
-  const int nb = tp_grid();
-  TreePlan T;
-  if (int rc = tp_plan(*D, parent, rank, n, node_row0, online, kappa, seq, nb, T)) return rc;
-  const TpLayout l = tp_layout(*D, nb);
-  if (work_bytes < l.total) return fail(LNG_E_ARG, "drafter_tree_fused: workspace too small");
-  char* w = static_cast<char*>(work);
-  TpWork Wk{reinterpret_cast<int32_t*>(w + l.sync), reinterpret_cast<int32_t*>(w + l.err),
-            reinterpret_cast<int32_t*>(w + l.ntok),  reinterpret_cast<int32_t*>(w + l.ncode),
-            reinterpret_cast<float*>(w + l.ro),      reinterpret_cast<float*>(w + l.part),
-            reinterpret_cast<int32_t*>(w + l.cand),  route_tokens, stamps};
-  lng_drafter Dc = *D;
-  void* args[] = {&Dc, &T, &Wk};
-  const void* kern;
-  switch (T.K) {
-    case 1: kern = reinterpret_cast<const void*>(&k_tree_persist<1>); break;
-    case 2: kern = reinterpret_cast<const void*>(&k_tree_persist<2>); break;
-    case 3: kern = reinterpret_cast<const void*>(&k_tree_persist<3>); break;
-    case 4: kern = reinterpret_cast<const void*>(&k_tree_persist<4>); break;
-    default: kern = reinterpret_cast<const void*>(&k_tree_persist<DR_MAXK>); break;
-  }
-  const hipError_t e = hipLaunchCooperativeKernel(kern, dim3(static_cast<unsigned>(nb)), dim3(TP_THREADS), args, 0,
-                                                  as_stream(stream));
-  if (e != hipSuccess) return fail(LNG_E_HIP, std::string("drafter_tree_fused: ") + hipGetErrorString(e));
-  return LNG_OK;
 }
 
 }  // extern "C"

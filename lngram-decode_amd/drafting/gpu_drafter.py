@@ -59,8 +59,7 @@ class GpuDrafter:
     name = "gpu"
 
     def __init__(self, bundle, topk: int = 3, shortlist_cap: int | None = None, device=None, max_len: int = 4096,
-                 online: bool = False, kappa: float = 1.0, tables: bool = True, fused: bool = False,
-                 levels: bool = True):
+                 online: bool = False, kappa: float = 1.0, tables: bool = True, levels: bool = True):
         c, t = _bundle_parts(bundle)
         self.cfg = c
         # RefDrafter scores a sketch shortlist when the cap is positive and the bundle carries
@@ -136,22 +135,13 @@ class GpuDrafter:
             raise ValueError("drafter shape outside the kernels' limits")
         self.work = torch.empty(int(nbytes), dtype=torch.uint8, device=dev)
         self.counts = torch.zeros(16, self.V, dtype=torch.int32, device=dev)
-        # one-launch draft tree (lng_drafter_tree_fused) for token-only drafters with tables: opt-in;
-        # at the SD-B shape it measures about the same as the per-depth launches, which stay the default
-        self.tree_work = None
-        self._tree_seq = 0
-        self._fused_specs: dict = {}
         self._graphs: dict = {}          # (parent, rank, route_tokens) -> (captured tree step, out)
-        if fused and self.luts is not None and self.sketch is None:
-            fb = self.lib.lng_drafter_tree_fused_workspace(ctypes.byref(self.D))
-            if fb:
-                self.tree_work = torch.zeros(int(fb), dtype=torch.uint8, device=dev)
-        # draft trees of token-only drafters at the SD drafters' shape: one launch per depth
+        # draft trees of token-only drafters at the SD drafters' shape: the one-launch tree
         # (lng_drafter_tree_levels); trees outside its limits take the per-depth readouts of
-        # lng_drafter_tree.  Its workspace keeps a call counter, so it is zeroed once here.
+        # lng_drafter_tree.  Its workspace keeps a call epoch, so it is zeroed once here.
         self.level_work = None
         self._level_specs: dict = {}
-        if levels and self.tree_work is None and self.luts is not None and self.sketch is None:
+        if levels and self.luts is not None and self.sketch is None:
             lb = self.lib.lng_drafter_tree_levels_workspace(ctypes.byref(self.D))
             if lb:
                 self.level_work = torch.zeros(int(lb), dtype=torch.uint8, device=dev)
@@ -442,20 +432,39 @@ class GpuDrafter:
 
     def draft_tree(self, spec) -> list:
         """``draft_tree`` (``drafting/tree.py:243-257``) with every parent of one depth in one readout;
-        returns the node tokens (root = the last committed token)."""
+        returns the node tokens (root = the last committed token).  The node tokens and the
+        one-launch tree's error word leave the device in one copy; if a wait of the one-launch tree
+        ran out, its workspace is cleared and the tree is drafted again by the per-depth readouts."""
         self.tree_step(spec, route_tokens=False)
-        return self.tok_d[self.tree_row0: self.tree_row0 + spec.n].cpu().tolist()
+        rows = slice(self.tree_row0, self.tree_row0 + spec.n)
+        if self.level_work is None or not self._level_specs.get((tuple(spec.parent), tuple(spec.rank)), False):
+            return self.tok_d[rows].cpu().tolist()
+        both = torch.cat((self.tok_d[rows], self.tree_status().to(torch.int64))).cpu().tolist()
+        if both[-1] == 0:
+            return both[:-1]
+        self.level_work.zero_()
+        self._redo_per_depth(spec, None)
+        return self.tok_d[rows].cpu().tolist()
+
+    def tree_status(self) -> torch.Tensor:
+        """The one-launch tree's error word as a device int32 ``[1]`` view (no synchronisation): a
+        caller of :meth:`tree_step` copies it to the host with its own results; non-zero means a wait
+        of that call ran out and its outputs are not to be used (clear it with :meth:`tree_error` and
+        redo the step).  Zero for drafters without the one-launch tree."""
+        if self.level_work is None:
+            return torch.zeros(1, dtype=torch.int32, device=self.device)
+        return self.level_work[4:8].view(torch.int32)
 
     def tree_step(self, spec, route_tokens: bool = True, graph: bool = False):
         """Draft the tree on the device and (optionally) gather its verification route tokens
         ``[n, R, Dt]``; returns (node tokens int64 [n] (device view), route tokens or None).
-        No host synchronisation.
+        No host synchronisation: the one-launch tree's error word is :meth:`tree_status`.
 
         ``graph=True`` replays the step's launches from a HIP graph captured on the first call for
         this tree shape (the launches read the drafter state from device memory, so one capture
         serves every later step).  The route tokens then live in a buffer owned by the capture:
         each replay overwrites the previous step's."""
-        if graph and self.tree_work is None:
+        if graph:
             key = (tuple(spec.parent), tuple(spec.rank), bool(route_tokens))
             ent = self._graphs.get(key)
             if ent is None:
@@ -477,16 +486,6 @@ class GpuDrafter:
             out = torch.empty(n, self.R, self.dt, dtype=self.tables[0].dtype, device=self.device)
         parent, rank = self._i32(spec.parent), self._i32(spec.rank)
         key = (tuple(spec.parent), tuple(spec.rank))
-        if self.tree_work is not None and self._fused_specs.get(key, True):
-            rc = self.lib.lng_drafter_tree_fused(ctypes.byref(self.D), parent, rank, n, self.tree_row0,
-                                                 int(self.online), self.kappa, self._tree_seq,
-                                                 self.tree_work.data_ptr(), self.tree_work.numel(),
-                                                 out.data_ptr() if out is not None else None, None, self._stream())
-            if rc == 0:
-                self._tree_seq += 1
-                self._fused_specs[key] = True
-                return self.tok_d[self.tree_row0: self.tree_row0 + n], out
-            self._fused_specs[key] = False     # tree outside the one-launch limits: per-depth launches
         if self.level_work is not None and self._level_specs.get(key, True):
             rc = self.lib.lng_drafter_tree_levels(ctypes.byref(self.D), parent, rank, n, self.tree_row0,
                                                   int(self.online), self.kappa, self.level_work.data_ptr(),
@@ -496,36 +495,36 @@ class GpuDrafter:
                 self._level_specs[key] = True
                 return self.tok_d[self.tree_row0: self.tree_row0 + n], out
             if rc != _lib.E_ARG:
-                check(rc, "drafter tree (one launch per depth)")
-            self._level_specs[key] = False     # tree outside the per-depth kernel's limits
+                check(rc, "drafter tree (one-launch tree, lng_drafter_tree_levels)")
+            self._level_specs[key] = False     # tree outside the one-launch kernel's limits
+        self._redo_per_depth(spec, out)
+        return self.tok_d[self.tree_row0: self.tree_row0 + n], out
+
+    def _redo_per_depth(self, spec, out) -> None:
+        """The tree by the per-depth readouts (``lng_drafter_tree``, or its shortlist form)."""
+        parent, rank = self._i32(spec.parent), self._i32(spec.rank)
+        n = spec.n
         if self.sketch is not None:
             check(self.lib.lng_drafter_tree_shortlist(ctypes.byref(self.D), ctypes.byref(self.sketch), parent, rank, n,
                                                       self.tree_row0, self.work.data_ptr(), self.work.numel(),
                                                       self.sl_lg.data_ptr(),
                                                       out.data_ptr() if out is not None else None, self._stream()),
                   "drafter tree")
-            return self.tok_d[self.tree_row0: self.tree_row0 + n], out
+            return
         check(self.lib.lng_drafter_tree(ctypes.byref(self.D), parent, rank, n, self.tree_row0, int(self.online),
                                         self.kappa, self.work.data_ptr(), self.work.numel(), self.counts.data_ptr(),
                                         out.data_ptr() if out is not None else None, self._stream()),
               "drafter tree")
-        return self.tok_d[self.tree_row0: self.tree_row0 + n], out
 
     def tree_error(self) -> int:
-        """Error word of the one-launch tree or of the launch-per-depth tree (synchronises): 0 = ok;
-        non-zero clears it and raises."""
+        """Error word of the one-launch tree (synchronises): 0 = ok; non-zero clears the workspace
+        and raises."""
         if self.level_work is not None:
-            err = int(self.level_work[4:8].view(torch.int32).item())
+            err = int(self.tree_status().item())
             if err:
                 self.level_work.zero_()
-                raise RuntimeError(f"drafter tree (one launch per depth): a device wait failed (error word {err})")
-        if self.tree_work is None:
-            return 0
-        err = int(self.tree_work[:4].view(torch.int32).item())
-        if err:
-            self.tree_work[:_lib.TREE_SYNC_BYTES].zero_()
-            self._tree_seq = 0
-            raise RuntimeError(f"drafter tree (one launch): a device wait failed (error word {err})")
+                raise RuntimeError(f"drafter tree (one-launch tree, lng_drafter_tree_levels): a device wait ran "
+                                   f"out (error word {err})")
         return 0
 
     def trace(self, tokens, codes=None, full: bool = False):

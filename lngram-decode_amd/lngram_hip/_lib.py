@@ -30,7 +30,6 @@ E_ARG = -1  # LNG_E_ARG
 ROW_NONE = -2147483648  # LNG_ROW_NONE
 NORM_MODEL, NORM_FUSED = 0, 1  # LNG_NORM_MODEL / LNG_NORM_FUSED
 DR_SYNC_INTS = 4160  # LNG_DR_SYNC_INTS
-TREE_SYNC_BYTES = 16640  # LNG_DR_TREE_SYNC_BYTES: error word (offset 0) + counters of the one-launch tree
 READOUT_PACK_ELEMS = 131072  # LNG_READOUT_PACK_ELEMS: bf16 elements of the fused readout's packed KV weight
 
 
@@ -117,9 +116,6 @@ SIGNATURES = {
     "lng_ssm_scan_bounded": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _i32, _p, _p]),
     "lng_ssm_scan_static": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p]),
     "lng_ssm_scan_static_status": (_int, [_p]),
-    "lng_drafter_tree_fused_workspace": (ctypes.c_size_t, [_PD]),
-    "lng_drafter_tree_fused": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, ctypes.c_uint32, _p, ctypes.c_size_t, _p,
-                                      _p, _p]),
     "lng_drafter_tree_levels_workspace": (ctypes.c_size_t, [_PD]),
     "lng_drafter_tree_levels": (_int, [_PD, _P32, _P32, _i32, _i32, _int, _f, _p, ctypes.c_size_t, _p, _p]),
     "lng_tree_accept": (_int, [_p, _p, _p, _i32, _p, _p, _p, _p]),

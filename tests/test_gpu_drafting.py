@@ -48,12 +48,11 @@ def _assert_logits(got: np.ndarray, want: np.ndarray, rel: float = 1e-5) -> None
 
 
 def _gpu(kind, cfg, t, dev, **kw) -> GpuDrafter:
-    """sdb / sdb_fast: per-token tables (two launches per readout; sdb_fast has Dt = 64, so its
-    trees run in one launch); sdb_generic / sdc: the general kernels."""
-    kw.setdefault("fused", kind == "sdb_fast")
+    """sdb / sdb_fast: per-token tables (two launches per readout; sdb_fast has Dt = 64);
+    sdb_generic / sdc: the general kernels.  At these tiny shapes trees take the per-depth
+    readouts (the one-launch tree serves the SD drafters' shape)."""
     g = GpuDrafter((cfg, t), device=dev, tables=kind in ("sdb", "sdb_fast"), **kw)
     assert (g.luts is not None) == (kind in ("sdb", "sdb_fast"))
-    assert (g.tree_work is not None) == (kind == "sdb_fast")
     return g
 
 
@@ -225,30 +224,54 @@ def test_sdb_shape_tree_step_matches_oracle(dev):
 
 
 def test_sdb_shape_one_launch_tree_matches_per_depth_launches_and_oracle(dev):
-    """SD-B drafter shape with online counts: the one-launch tree equals the per-depth launches
-    (node tokens, node codes, verification gather, bit for bit) and the oracle's draft tree."""
+    """SD-B drafter shape with online counts: the one-launch tree (lng_drafter_tree_levels) equals
+    the per-depth readouts (node tokens, node codes, verification gather, bit for bit) and the
+    oracle: the oracle's draft tree, its router codes of every node outside the near-tie band, and
+    its verification gather ``tree_route_tokens`` [16, 182, 256] (tree.py:96-136) of the nodes'
+    windows, bit for bit."""
     w = wl.SDB_DRAFT
     cfg, t = wl.build_draft_bundle(w, seed=0)
     ctx = wl.make_context(w, seed=0)
-    g1 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8, online=True, fused=True)
-    g0 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8, online=True, fused=False)
-    assert g1.tree_work is not None and g0.tree_work is None
+    g1 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8, online=True)
+    g0 = GpuDrafter((cfg, t), device=dev, max_len=w.context + 8, online=True, levels=False)
+    assert g1.level_work is not None and g0.level_work is None
     g1.commit(ctx)
-    g0.commit(ctx, codes=g1.committed_codes())
+    committed = g1.committed_codes()
+    g0.commit(ctx, codes=committed)
     o = od.DrafterOracle(cfg, t, online=True)
-    o.commit(ctx, codes=g1.committed_codes())
+    o.commit(ctx, codes=committed)
     want = od.draft_tree(o, od.TreeSpec(SPEC16.parent, SPEC16.rank))
-    for rep in range(3):                                     # repeated calls reuse the counters
+    rows = slice(g1.tree_row0, g1.tree_row0 + SPEC16.n)
+    for rep in range(3):                                     # repeated calls reuse the workspace
         print(f"[sdb one-launch tree] call {rep}", flush=True)
         n1, r1 = g1.tree_step(SPEC16, route_tokens=True)
         n0, r0 = g0.tree_step(SPEC16, route_tokens=True)
         torch.cuda.synchronize()
         assert g1.tree_error() == 0
-        assert g1._fused_specs[(tuple(SPEC16.parent), tuple(SPEC16.rank))]
+        assert g1._level_specs[(tuple(SPEC16.parent), tuple(SPEC16.rank))]
         assert n1.cpu().tolist() == n0.cpu().tolist() == want
         assert torch.equal(r1, r0)
-        rows = slice(g1.tree_row0, g1.tree_row0 + SPEC16.n)
         assert torch.equal(g1.codes_d[rows][1:], g0.codes_d[rows][1:])
+    # node codes against the oracle's router (root = the last committed token)
+    node_codes = g1.codes_d[rows].cpu().numpy().astype(np.int64)
+    node_codes[0] = committed[-1]
+    n_bad = 0
+    for i in range(1, SPEC16.n):
+        lg = o.router_logits(want[SPEC16.parent[i]], want[i], None)
+        tie = (lg.abs() < TAU).view(o.R, o.bits).any(-1).numpy()
+        bits = (lg > 0).view(o.R, o.bits).to(torch.int64).numpy()
+        oc = (bits << np.arange(o.bits)).sum(-1)
+        n_bad += int((node_codes[i] != oc)[~tie].sum())
+    assert n_bad == 0
+    # the verification gather against the oracle's, from the nodes' codes along their ancestors
+    hist = committed[None, -3:-1].astype(np.int64)
+    octx, ok = od.tree_ngram_codes(SPEC16.parent, node_codes[None], hist, 2)
+    tables = {n: t[f"table_{n}"] for n in cfg["ngrams"]}
+    rt_want = od.tree_route_tokens(tables, cfg["ngrams"], cfg["bits"], octx, ok)[0]
+    assert tuple(rt_want.shape) == (16, 182, 256)
+    assert torch.equal(r1.cpu(), rt_want.to(r1.dtype))
+    # draft_tree reads the error word in its one copy and agrees
+    assert g1.draft_tree(SPEC16) == want
 
 
 def test_sdb_shape_graph_tree_step_replays_match_eager(dev):
