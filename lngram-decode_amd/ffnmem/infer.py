@@ -163,8 +163,11 @@ def memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tenso
                 route_codes_ctx: Tensor | None = None, route_tokens: Tensor | None = None) -> Tensor:
     """Memory output ``[B, n, d]`` of the new positions (``infer.py:152-182``); ``codes_new``
     ``[B, n, R]`` are written into the cache.  ``route_codes_ctx [B, n + H, R]`` replaces the
-    cached history (tree verification: codes along each node's ancestor path); ``route_tokens
-    [B, n, R, len(ngrams) * mem_dim]`` are rows supplied by the caller (the gather is skipped)."""
+    cached codes for the lookup only (the n-grams ending at the new positions are read from it);
+    as in the reference, the short conv still reads the cached rows in position order, so a
+    draft tree's verification (whose conv follows each node's ancestors, ``tree.py:186-194``) is
+    not this function's.  ``route_tokens [B, n, R, len(ngrams) * mem_dim]`` are rows supplied by
+    the caller (the gather is skipped)."""
     mem = model.blocks[pos].memory
     m = mem.module
     L, n = state.length, h.shape[1]

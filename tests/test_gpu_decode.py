@@ -75,6 +75,47 @@ def test_bf16_sb_shape_steps_match_full_forward(dev):
     assert om.rel_err(got.float().cpu(), ref) < 2e-2
 
 
+def test_step_with_route_codes_context_matches_oracle(dev):
+    # memory_step(route_codes_ctx=...) (infer.py:152-182): the lookup of the new positions reads the
+    # given code context [B, n + H, R] (here a history that differs from the cache) instead of the
+    # cached codes, and the conv reads the cached rows in position order, as the reference's does.
+    # The oracle: heads of the first L positions from the cached codes, heads of the new positions
+    # from the context's n-grams, then one finish (o-proj + conv) over the whole sequence.
+    w = wl.TINY.with_shape(2, 24)
+    mem, h, h_norm = _layer(w, dev)
+    model = memory_model(mem)
+    L, n, hist = 20, 4, 2
+    gen = torch.Generator().manual_seed(8)
+    with torch.no_grad():
+        st = DecodeState.empty(model, 2, 24)
+        codes_a = memory_codes(model, 0, st, h_norm=h_norm[:, :L])
+        memory_step(model, 0, st, h[:, :L], codes_a)
+        st.length = L
+        codes_new = torch.randint(0, 16, (2, n, w.routes), generator=gen, dtype=torch.uint8).to(dev)
+        ctx_hist = torch.randint(0, 16, (2, hist, w.routes), generator=gen, dtype=torch.uint8).to(dev)
+        ctx = torch.cat((ctx_hist, codes_new), 1)
+        got = memory_step(model, 0, st, h[:, L:], codes_new, route_codes_ctx=ctx)
+    assert torch.equal(st.codes[0][:, L:L + n], codes_new)
+    sd = {k: v.detach().cpu() for k, v in mem.state_dict().items()}
+    prm = {k[len("module."):]: v for k, v in sd.items() if k.startswith("module.")}
+    cfg = om.MemCfg(w.d_model, w.routes, w.mem_dim, w.q_heads, w.kv_heads, w.head_dim, eps=w.norm_eps)
+    h64 = h.cpu().double()
+    p64 = {k: v.double() for k, v in prm.items()}
+    tables = {o: p64[f"tables.ngram_{o}.weight"] for o in cfg.orders}
+    q = om.project_query(p64, cfg, h64)
+    tok_a = om.route_tokens(tables, codes_a.cpu().numpy(), cfg.orders, cfg.bits)
+    tok_b = om.route_tokens(tables, ctx.cpu().numpy(), cfg.orders, cfg.bits, target_length=n)
+    head_a = om.manual_gqa(cfg, q[:, :L], *om.project_memory(p64, cfg, tok_a))
+    head_b = om.manual_gqa(cfg, q[:, L:], *om.project_memory(p64, cfg, tok_b))
+    want = om.finish(p64, cfg, torch.cat((head_a, head_b), 1))[:, L:]
+    assert om.rel_err(got.cpu().double(), want) < 1e-5
+    # and the context matters: the cached history gives another output
+    with torch.no_grad():
+        st.length = L
+        other = memory_step(model, 0, st, h[:, L:], codes_new)
+    assert not torch.equal(other, got)
+
+
 @pytest.mark.parametrize("shape", ["tiny", "sb"])
 def test_truncate_then_recompute(dev, shape):
     w = (wl.TINY if shape == "tiny" else wl.SB).with_shape(1, 24)

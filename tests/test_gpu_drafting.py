@@ -381,3 +381,38 @@ def test_levels_tree_many_count_bearing_tokens_in_one_slice(dev):
         rows = slice(g1.tree_row0 + 1, g1.tree_row0 + spec.n)
         assert torch.equal(g1.codes_d[rows], g0.codes_d[rows])
         assert n1.cpu().tolist() == od.draft_tree(o, od.TreeSpec(spec.parent, spec.rank))
+
+
+@pytest.mark.parametrize("n_ctx", [2048, 4200])
+def test_levels_tree_pairs_past_the_key_cache_and_the_list(dev, n_ctx):
+    """A context whose tokens all lie in the first vocabulary slice (160 tokens), so one block lists
+    every committed pair: 2047 pairs pass the 48 whose match keys sit in LDS (the rest recompute
+    their keys from the committed codes), and 4199 pairs pass the 4096-entry list (the pairs are
+    then listed and counted per depth in rounds).  Node tokens, node codes and the verification
+    gather equal the per-depth readouts bit for bit, and the node tokens equal the oracle's draft
+    tree with online counts."""
+    w = wl.SDB_DRAFT
+    cfg, t = wl.build_draft_bundle(w, seed=0)
+    gen = torch.Generator().manual_seed(n_ctx)
+    ctx = torch.randint(0, 160, (n_ctx,), generator=gen).tolist()
+    g1 = GpuDrafter((cfg, t), device=dev, max_len=n_ctx + 16, online=True)
+    g0 = GpuDrafter((cfg, t), device=dev, max_len=n_ctx + 16, online=True, levels=False)
+    assert g1.level_work is not None
+    g1.commit(ctx)
+    g0.commit(ctx, codes=g1.committed_codes())
+    o = od.DrafterOracle(cfg, t, online=True)
+    o.commit(ctx, codes=g1.committed_codes())
+    for spec in (SPEC16, dtree.chain_tree(5)):
+        print(f"[levels tree, {n_ctx - 1} pairs in one slice] n={spec.n}", flush=True)
+        n1, r1 = g1.tree_step(spec, route_tokens=True)
+        n1, r1 = n1.clone(), r1.clone()
+        torch.cuda.synchronize()
+        assert g1.tree_error() == 0
+        assert g1._level_specs[(tuple(spec.parent), tuple(spec.rank))]
+        n0, r0 = g0.tree_step(spec, route_tokens=True)
+        torch.cuda.synchronize()
+        assert n1.cpu().tolist() == n0.cpu().tolist()
+        assert torch.equal(r1, r0)
+        rows = slice(g1.tree_row0 + 1, g1.tree_row0 + spec.n)
+        assert torch.equal(g1.codes_d[rows], g0.codes_d[rows])
+        assert n1.cpu().tolist() == od.draft_tree(o, od.TreeSpec(spec.parent, spec.rank))

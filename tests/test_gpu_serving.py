@@ -21,6 +21,8 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import memory as om
+
 from ffnmem.infer import DecodeState, memory_decode
 from lngram_hip import ops
 from lngram_hip import workloads as wl
@@ -87,12 +89,19 @@ def test_serving_layout_route_tokens_candidates_and_involution(dev, variant):
     codes = torch.randint(0, 16, (3, 20, R), device=dev, dtype=torch.uint8, generator=gen)
     with torch.no_grad():
         want = m._lookup_route_chunk(codes, None, 0, R, None, None)
-    assert torch.equal(sl.serving_route_tokens(tables, codes, m.ngrams, bits), want)
+    got = sl.serving_route_tokens(tables, codes, m.ngrams, bits)
+    assert torch.equal(got, want)
+    # the oracle's route tokens (lngram_v2.py:1047-1113) from the module's own tables, bit for bit
+    otab = {o: m.tables[f"ngram_{o}"].weight.detach().cpu() for o in m.ngrams}
+    assert torch.equal(got.cpu(), om.route_tokens(otab, codes.cpu().numpy(), m.ngrams, bits).to(got.dtype))
+    # reverse_digits' known answers (reference tests/test_index_layout.py:40-43), and the serving
+    # address = the oracle's aligned address (oldest code least significant) with its digits reversed
+    r = sl.reverse_digits(3, 4, dev)
+    assert torch.equal(r[r], torch.arange(4096, device=dev)) and int(r[1]) == 256 and int(r[16]) == 16
     for o in m.ngrams:
         addr = sl.serving_address(codes, o, bits)
-        c = codes.long()
-        ref = sum(c[:, o - 1 - k: c.shape[1] - k] << (k * bits) for k in range(o))
-        assert torch.equal(addr, ref)
+        aligned = torch.from_numpy(om.ngram_address(codes.cpu().numpy(), o, bits)).to(dev)
+        assert torch.equal(addr, sl.reverse_digits(o, bits, dev)[aligned])
     for t in range(2, 19):                                   # codes up to t known; rows of t + 1
         cands = sl.candidate_rows(tables, codes[:, t - 1:t + 1], m.ngrams, bits)
         for o, blk in cands.items():
