@@ -602,9 +602,9 @@ def _sdc_result(w, ms: float, kms: dict) -> dict:
     n = w.tokens
     scan_bytes = 2 * n * w.ssm_dim * 4
     layer_bytes = n * w.algorithmic_bytes_per_token() + w.weight_bytes() + scan_bytes
-    # rows (R x 2 orders x 256 B) + query + raw rows (the query RMSNorm's statistics) + codes read,
-    # head output written
-    fused_bytes = n * (w.routes * 2 * w.mem_dim * 2 + 3 * w.d_model * 2 + w.routes)
+    # rows (R x 2 orders x 256 B) + query + codes read, head output written (the query's RMSNorm
+    # scale comes with the query: the projection forms it)
+    fused_bytes = n * (w.routes * 2 * w.mem_dim * 2 + 2 * w.d_model * 2 + w.routes)
     return {"workload": "SD-C layer: 8 x 4096 tokens, R181, d1024 bf16, 256-channel SSM scan (fp32) + embed2_ssm "
                         "router features + memory forward",
             "tokens_per_s": n / (ms * 1e-3), "ms_per_step": ms, "algorithmic_bytes": layer_bytes,
@@ -867,10 +867,10 @@ def main() -> None:
         fused_ms = kt.mean_ms()
     ms = el / args.steps * 1e3
     tok_s = w.tokens / (el / args.steps)
-    # fused kernel algorithmic bytes per launch: rows (R x 2 orders x 256 B) + query + raw rows (the
-    # query RMSNorm's statistics, formed in the kernel) + codes read, head output written
+    # fused kernel algorithmic bytes per launch: rows (R x 2 orders x 256 B) + query + codes read,
+    # head output written (the query arrives scaled by its RMSNorm: the projection forms the scale)
     es = 2
-    fused_bytes = w.tokens * (w.routes * 2 * w.mem_dim * es + 3 * w.d_model * es + w.routes)
+    fused_bytes = w.tokens * (w.routes * 2 * w.mem_dim * es + 2 * w.d_model * es + w.routes)
     achieved = fused_bytes / (fused_ms * 1e-3) / 1e9
     layer_bytes = w.tokens * w.algorithmic_bytes_per_token() + w.weight_bytes()
     layer_gbs = layer_bytes / (el / args.steps) / 1e9
