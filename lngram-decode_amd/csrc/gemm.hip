@@ -518,7 +518,7 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
 // - K advances 64 per stage, so every tile row of a stage is one whole 128 B line; a 2-slot ring
 //   (2 x 64 KB of LDS) holds stage k + 1 in flight while stage k is multiplied.  The loads are raw
 //   buffer loads straight into LDS over the tile's rows (rows past N or M lie outside the buffer
-//   and read as zero, so ragged edges need no clamping); piece p of row r sits at slot p ^ (r & 7).
+//   and read as zero, so ragged edges need no clamping); piece p of row r sits at slot pswz(r, p).
 // - A stage is four k16 slices; the fragments of slice s + 1 are read from LDS under the MFMAs of
 //   slice s (two register sets), and the scheduling hints interleave one LDS read (or two buffer
 //   loads) with each MFMA.
@@ -538,6 +538,12 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
 constexpr int PT = 256, PK = 64, P_ROWS = 2 * PT, P_STAGE = P_ROWS * PK;
 constexpr int P_FN = 4, P_FM = 2;      // 32 x 32 fragments per wave: 4 (W rows) x 2 (X rows)
 constexpr int P_DPW = P_ROWS / 8 / 8;  // buffer loads (8 rows each) per wave per stage
+// Piece p of tile row r sits at 16 B slot p ^ (r & 7) ^ (bit 4 of r).  A ds_read_b128 is served
+// in passes of 16 lanes, lanes 0-7 with 16-23 (and so on), over 256 B of banks; the 32 x 32
+// fragment puts rows r and r + 16 in one pass at the same piece, which the r & 7 term alone maps to
+// the same bank group (rocprofv3: 3.46 M bank-conflict cycles per launch at 16384 x 1024 x 1024,
+// 0.26 M with the bit-4 term).
+__device__ __forceinline__ int pswz(int r, int p) { return p ^ (r & 7) ^ ((r >> 4) & 1); }
 
 template <bool XRMS>
 __global__ __launch_bounds__(512, 1) void k_gemm_proj_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
@@ -563,20 +569,26 @@ __global__ __launch_bounds__(512, 1) void k_gemm_proj_bf16(const bf16* __restric
   const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<bf16*>(is_w ? W + n0 * K : X + m0 * K), 0,
       static_cast<int>(bytes < 0x7fffffffull ? bytes : 0x7fffffffull), BUF_DW3);
-  const uint32_t voff0 = static_cast<uint32_t>((row0 * K + 8 * ((lane & 7) ^ (row0 & 7))) * 2);
-  const uint32_t dstep = static_cast<uint32_t>(8 * K * 2);
+  // instruction d covers rows row0 + 8 d (row bit 4 changes with d, so the swizzle does too)
+  uint32_t voff[P_DPW];
+#pragma unroll
+  for (int d = 0; d < P_DPW; ++d) {
+    const int r = row0 + 8 * d;
+    voff[d] = static_cast<uint32_t>((r * K + 8 * pswz(r, lane & 7)) * 2);
+  }
   auto issue = [&](int stage, int c) {
     bf16* dst = ring + c * P_STAGE + wave * P_DPW * 8 * PK;
 #pragma unroll
     for (int d = 0; d < P_DPW; ++d)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)(dst + d * 8 * PK), 16,
-                                               voff0 + d * dstep + static_cast<uint32_t>(stage) * PK * 2, 0, 0, 0);
+                                               voff[d] + static_cast<uint32_t>(stage) * PK * 2, 0, 0, 0);
   };
-  // fragment of 32 rows x 16 k: lane (r31, hi) reads row r31 at k piece 2 ks + hi
+  // fragment of 32 rows x 16 k: lane (r31, hi) reads row r31 at k piece 2 ks + hi (rows of one
+  // fragment differ from r31 by multiples of 32, so their swizzle is r31's)
   const int r31 = lane & 31, hi = lane >> 5;
   const int a_base = (wn * 128 + r31) * PK, b_base = (PT + wm * 64 + r31) * PK;
   auto frags = [&](bf16x8* a, bf16x8* bb, int c, int ks) {
-    const int off = c * P_STAGE + 8 * ((2 * ks + hi) ^ (lane & 7));
+    const int off = c * P_STAGE + 8 * pswz(r31, 2 * ks + hi);
 #pragma unroll
     for (int i = 0; i < P_FN; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&ring[off + a_base + i * 32 * PK]);
 #pragma unroll

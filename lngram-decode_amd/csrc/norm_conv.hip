@@ -436,14 +436,13 @@ constexpr int CS_SL = 16;   // 16 positions + 9 halo rows, 4 waves a block: 18.7
 constexpr int CS_WPB = 4;  // (32 positions: 20.6 us; one-wave blocks: 21.2 us; 64 positions: 24.3 us)
 constexpr int CS_MAXP = 16;
 
-template <int SL, int MAXP>
+template <int SL, int MAXP, bool RESIDUAL>
 __global__ __launch_bounds__(64 * CS_WPB) void k_causal_conv_k4d3_stream(const bf16* __restrict__ mixed,
                                                                 const float* __restrict__ rowsq, int32_t P,
                                                                 const bf16* __restrict__ norm_w,
                                                                 const bf16* __restrict__ conv_w, int32_t T,
                                                                 int32_t d, int32_t G, int32_t R, int64_t B_tiles,
-                                                                int64_t M, float eps, int residual,
-                                                                bf16* __restrict__ out) {
+                                                                int64_t M, float eps, bf16* __restrict__ out) {
   constexpr int ROWS = SL + CF_HALO;
   const int lane = threadIdx.x & 63;
   // the host keeps the tile count below 2^31 (and pads it to whole blocks: tiles past the end exit)
@@ -451,29 +450,50 @@ __global__ __launch_bounds__(64 * CS_WPB) void k_causal_conv_k4d3_stream(const b
   uint32_t tile = blockIdx.x * CS_WPB + (threadIdx.x >> 6);
   const uint32_t nb = gridDim.x * CS_WPB;
   if ((nb & 7) == 0) tile = (tile & 7) * (nb >> 3) + (tile >> 3);
+  tile = __builtin_amdgcn_readfirstlane(tile);
   if (tile >= ntiles) return;  // no barrier follows
   const uint32_t gr = tile / static_cast<uint32_t>(G);
   const int cg = static_cast<int>(tile - gr * static_cast<uint32_t>(G));
   const uint32_t bb = gr / static_cast<uint32_t>(R);
   const int rg = static_cast<int>(gr - bb * static_cast<uint32_t>(R));
-  const int64_t b = bb;
   const int t0 = rg * SL;
-  const int64_t row0 = b * T;
   const int c = cg * 256 + 4 * lane;
   const bool active = c < d;
   const int cc = active ? c : 0;
-  auto clamp_t = [&](int tp) { return tp < 0 ? 0 : (tp >= T ? T - 1 : tp); };
+  // Rows are addressed through one buffer resource per sequence (T * d * 2 < 2^31 bytes, checked
+  // by the host) and 32-bit byte offsets: a row before the sequence start (negative offset) or at
+  // or past its end lies outside the resource, so its loads read zero and its stores are dropped
+  // by the hardware -- no clamping, 64-bit address arithmetic or store branches per row.  Rows past
+  // the end feed only outputs past the end; rows before the start are the zero left padding.
+  const uint32_t seq_bytes = static_cast<uint32_t>(T) * static_cast<uint32_t>(d) * 2u;
+  const size_t seq0 = static_cast<size_t>(bb) * static_cast<size_t>(T) * static_cast<size_t>(d);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(mixed + seq0), 0, static_cast<int>(seq_bytes), BUF_DW3);
+  const __amdgpu_buffer_rsrc_t yr_out =
+      __builtin_amdgcn_make_buffer_rsrc(out + seq0, 0, static_cast<int>(seq_bytes), BUF_DW3);
+  const uint32_t rstride = static_cast<uint32_t>(d) * 2u;
+  // unsigned offsets: a row before the start wraps above 2^31; lanes past d start at 2^31, which no
+  // row step (ROWS * d * 2 < 2^30, checked by the host) brings back below T * d * 2
+  const uint32_t voff = active ? static_cast<uint32_t>(t0 - CF_HALO) * rstride + 2u * static_cast<uint32_t>(c)
+                               : 0x80000000u;
   // the partials first (every lane loads, unconditionally, so the row loads are not held back
-  // behind them), then the rows
+  // behind them), then the rows; lane r's partials are row t0 - 9 + r's (clamped into the sequence)
   const int tl = t0 - CF_HALO + (lane < ROWS ? lane : 0);
-  const int64_t ml = row0 + clamp_t(tl);
+  const int tlc = tl < 0 ? 0 : (tl >= T ? T - 1 : tl);
+  const __amdgpu_buffer_rsrc_t pr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(rowsq), 0, static_cast<int>(static_cast<uint32_t>(P) * static_cast<uint32_t>(M) * 4u), BUF_DW3);
+  const int32_t poff = (static_cast<int32_t>(bb) * T + tlc) * 4;
+  const int32_t pstep = static_cast<int32_t>(M) * 4;
   float pv[MAXP];
 #pragma unroll
-  for (int q = 0; q < MAXP; ++q) pv[q] = rowsq[static_cast<int64_t>(q < P ? q : 0) * M + ml];
-  uint2 x[ROWS];  // channels cc .. cc+3 of row t0 - 9 + r
+  for (int q = 0; q < MAXP; ++q)
+    pv[q] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(pr, poff + (q < P ? q : 0) * pstep, 0, 0));
+  uint2 x[ROWS];  // channels cc .. cc+3 of row t0 - 9 + r (zero outside the sequence)
 #pragma unroll
-  for (int r = 0; r < ROWS; ++r)
-    x[r] = *reinterpret_cast<const uint2*>(mixed + (row0 + clamp_t(t0 - CF_HALO + r)) * d + cc);
+  for (int r = 0; r < ROWS; ++r) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(xr, static_cast<int>(voff + r * rstride), 0, 0);
+    x[r] = uint2{static_cast<uint32_t>(v[0]), static_cast<uint32_t>(v[1])};
+  }
   const uint2 nwv = *reinterpret_cast<const uint2*>(norm_w + cc);
   const uint4 cw01 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(cc) * 4);      // channels c, c+1
   const uint4 cw23 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(cc) * 4 + 8);  // channels c+2, c+3
@@ -498,40 +518,71 @@ __global__ __launch_bounds__(64 * CS_WPB) void k_causal_conv_k4d3_stream(const b
       for (int j = 0; j < 4; ++j) q[r - 3][j] = pk2(yn[r - 3][j], yn[r][j]);
     }
     if (r >= CF_HALO) {
-      // every lane forms the output (no divergent branch, so no load is sunk into one); rows past
-      // the sequence end and lanes past d only skip the store
+      // output t0 + i reads rows i, i+3 (taps 0, 1) and i+6, i+9 (taps 2, 3); every lane forms it
+      // and the resource drops the stores past the sequence end and past d
       const int i = r - CF_HALO;
-      const int t = t0 + i;
-      {
-        float y[4];
+      float y[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float a = __builtin_amdgcn_fdot2_f32_bf16(q[i][j], __builtin_bit_cast(bf16x2, wa[j]), 0.f, false);
-          y[j] = __builtin_amdgcn_fdot2_f32_bf16(q[i + 6][j], __builtin_bit_cast(bf16x2, wb[j]), a, false);
-        }
-        const uint32_t yp0 = __builtin_bit_cast(uint32_t, pk2(y[0], y[1]));
-        const uint32_t yp1 = __builtin_bit_cast(uint32_t, pk2(y[2], y[3]));
-        const float yr[4] = {lo_f(yp0), hi_f(yp0), lo_f(yp1), hi_f(yp1)};
-        float act[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e = __builtin_amdgcn_exp2f(-yr[j] * 1.4426950408889634f);
-          act[j] = yr[j] * __builtin_amdgcn_rcpf(1.0f + e);
-        }
-        uint2 o;
-        if (residual) {
-          const uint32_t ap0 = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
-          const uint32_t ap1 = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
-          o.x = __builtin_bit_cast(uint32_t, pk2(xf[0] + lo_f(ap0), xf[1] + hi_f(ap0)));
-          o.y = __builtin_bit_cast(uint32_t, pk2(xf[2] + lo_f(ap1), xf[3] + hi_f(ap1)));
-        } else {
-          o.x = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
-          o.y = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
-        }
-        if (t < T && active) *reinterpret_cast<uint2*>(out + (row0 + t) * d + c) = o;
+      for (int j = 0; j < 4; ++j) {
+        const float a = __builtin_amdgcn_fdot2_f32_bf16(q[i][j], __builtin_bit_cast(bf16x2, wa[j]), 0.f, false);
+        y[j] = __builtin_amdgcn_fdot2_f32_bf16(q[i + 6][j], __builtin_bit_cast(bf16x2, wb[j]), a, false);
       }
+      const uint32_t yp0 = __builtin_bit_cast(uint32_t, pk2(y[0], y[1]));
+      const uint32_t yp1 = __builtin_bit_cast(uint32_t, pk2(y[2], y[3]));
+      const float yr[4] = {lo_f(yp0), hi_f(yp0), lo_f(yp1), hi_f(yp1)};
+      float act[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = __builtin_amdgcn_exp2f(-yr[j] * 1.4426950408889634f);
+        act[j] = yr[j] * __builtin_amdgcn_rcpf(1.0f + e);
+      }
+      uint32_t o0, o1;
+      if (RESIDUAL) {
+        const uint32_t ap0 = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+        const uint32_t ap1 = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+        o0 = __builtin_bit_cast(uint32_t, pk2(xf[0] + lo_f(ap0), xf[1] + hi_f(ap0)));
+        o1 = __builtin_bit_cast(uint32_t, pk2(xf[2] + lo_f(ap1), xf[3] + hi_f(ap1)));
+      } else {
+        o0 = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+        o1 = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+      }
+      typedef int i32x2 __attribute__((ext_vector_type(2)));
+      __builtin_amdgcn_raw_buffer_store_b64(i32x2{static_cast<int>(o0), static_cast<int>(o1)}, yr_out,
+                                            static_cast<int>(voff + r * rstride), 0, 0);
     }
   }
+}
+
+template <int SL, int MAXP>
+static void conv_stream_kernel(dim3 grid, dim3 block, hipStream_t s, bool residual, const bf16* mx, const float* rowsq,
+                               int32_t P, const bf16* nw, const bf16* cw, int32_t T, int32_t d, int32_t G, int32_t R,
+                               int64_t nb, int64_t M, float eps, bf16* o) {
+  if (residual)
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<SL, MAXP, true>), grid, block, 0, s, mx, rowsq, P, nw, cw, T, d, G, R,
+                       nb, M, eps, o);
+  else
+    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<SL, MAXP, false>), grid, block, 0, s, mx, rowsq, P, nw, cw, T, d, G,
+                       R, nb, M, eps, o);
+}
+
+// the short conv over whole sequences with the row statistics of the producing GEMM
+template <int SL>
+static int launch_conv_stream(const bf16* mx, const float* rowsq, int32_t n_partials, const bf16* nw, const bf16* cw,
+                              int64_t B, int64_t T, int32_t d, float eps, bool residual, bf16* o, hipStream_t s) {
+  const int32_t G = static_cast<int32_t>(cdiv(d, 256)), R = static_cast<int32_t>(cdiv(T, SL));
+  const int64_t nb = B * G * R;
+  if (nb >= (int64_t{1} << 31)) return fail(LNG_E_ARG, "causal_conv_rowsq: too many tiles");
+  const int64_t M = B * T;
+  const int32_t Ti = static_cast<int32_t>(T);
+  const dim3 grid(static_cast<unsigned>(cdiv(nb, CS_WPB))), block(64 * CS_WPB);
+  if (n_partials <= 2)
+    conv_stream_kernel<SL, 2>(grid, block, s, residual, mx, rowsq, n_partials, nw, cw, Ti, d, G, R, nb, M, eps, o);
+  else if (n_partials <= 8)
+    conv_stream_kernel<SL, 8>(grid, block, s, residual, mx, rowsq, n_partials, nw, cw, Ti, d, G, R, nb, M, eps, o);
+  else
+    conv_stream_kernel<SL, CS_MAXP>(grid, block, s, residual, mx, rowsq, n_partials, nw, cw, Ti, d, G, R, nb, M, eps,
+                                    o);
+  return LNG_OK;
 }
 
 template <bool FUSED>
@@ -586,28 +637,23 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
   if (mixed == out) return fail(LNG_E_ARG, "causal_conv_rowsq: out must not alias mixed");
   if (n_partials > CS_MAXP) return fail(LNG_E_ARG, "causal_conv_rowsq: at most 16 partials");
   if (B * T == 0) return LNG_OK;
-  if (T >= (int64_t{1} << 30) || B * T * d >= (int64_t{1} << 40))
+  // one sequence and the partials fit one buffer resource each (byte offsets below 2^31), and a
+  // wave's row steps stay below 2^30 bytes
+  if (T * d >= (int64_t{1} << 30) || d > 65536 || static_cast<int64_t>(n_partials) * B * T >= (int64_t{1} << 29))
     return fail(LNG_E_ARG, "causal_conv_rowsq: tensor too large");
-  const int32_t G = static_cast<int32_t>(cdiv(d, 256)), R = static_cast<int32_t>(cdiv(T, CS_SL));
-  const int64_t nb = B * G * R;
-  if (nb >= (int64_t{1} << 31)) return fail(LNG_E_ARG, "causal_conv_rowsq: too many tiles");
   const bf16* mx = static_cast<const bf16*>(mixed);
   const bf16* nw = static_cast<const bf16*>(norm_w);
   const bf16* cw = static_cast<const bf16*>(conv_w);
   bf16* o = static_cast<bf16*>(out);
-  const int64_t M = B * T;
-  const int32_t Ti = static_cast<int32_t>(T);
-  hipStream_t s = as_stream(stream);
-  const dim3 grid(static_cast<unsigned>(cdiv(nb, CS_WPB))), block(64 * CS_WPB);
-  if (n_partials <= 2)
-    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 2>), grid, block, 0, s, mx, rowsq, n_partials, nw, cw, Ti,
-                       d, G, R, nb, M, eps, residual, o);
-  else if (n_partials <= 8)
-    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, 8>), grid, block, 0, s, mx, rowsq, n_partials, nw, cw, Ti,
-                       d, G, R, nb, M, eps, residual, o);
+  static const int sl = getenv("LNG_CONV_SL") ? atoi(getenv("LNG_CONV_SL")) : 16;  // EXPERIMENT
+  int rc;
+  if (sl == 32)
+    rc = launch_conv_stream<32>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
+  else if (sl == 24)
+    rc = launch_conv_stream<24>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
   else
-    hipLaunchKernelGGL((k_causal_conv_k4d3_stream<CS_SL, CS_MAXP>), grid, block, 0, s, mx, rowsq, n_partials, nw,
-                       cw, Ti, d, G, R, nb, M, eps, residual, o);
+    rc = launch_conv_stream<CS_SL>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
+  if (rc) return rc;
   return check_launch("causal_conv_rowsq");
 }
 

@@ -26,7 +26,12 @@ namespace lng {
 constexpr int FR_H = 16;           // query heads
 constexpr int FR_HD = 64;          // head dim
 constexpr int FR_DT = 256;         // route token dim (2 orders x 128)
-constexpr int FR_LD = FR_DT + 8;   // padded LDS row (bf16): 528 B, conflict-free 16-row access
+// LDS row (bf16): 544 B, so row r starts 32 r bytes (mod 256) into the banks.  A 16-lane pass
+// of a 16-byte LDS access (lanes 0-7 with 16-23, and so on) covers 256 B of banks; with this skew,
+// a chunk row stored by one such pass (the gather's lane map), the score operands (rows 0-7 at
+// pieces of opposite parity in the two halves of a pass, fr_col) and the transposed 8-byte reads
+// (rows 0-7, 32 B each) all land on distinct bank groups.
+constexpr int FR_LD = FR_DT + 16;
 constexpr int FR_MAXR = 256;       // max routes (row-index slots per token)
 constexpr int FR_RQ = FR_MAXR / 4;
 // packed KV weight (bf16 elements): keys [h 4][ft 16][ks 2][lane 64][8] = Wk^T[h][16ft + lane%16][32ks + 8(lane/16) ..+8],
@@ -45,6 +50,10 @@ constexpr int FR_POL_T3 = CPOL_SC1;
 constexpr int FR_POL_STREAM = CPOL_NT;
 
 __device__ __forceinline__ bf16x8 ld16(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+// route-token column of the score operands' 8-feature piece kk of lane group lg: the pieces of lane
+// groups 0 and 1 (2 and 3) alternate in parity, so the two halves of an LDS pass never share a
+// bank group (the score is a dot product over all 256 features; their grouping is free)
+__device__ __forceinline__ int fr_col(int lg, int kk) { return 16 * kk + 8 * (lg & 1) + 128 * (lg >> 1); }
 // 16 bytes of a token-major activation (q, raw rows) at element offset e < 2^31, streamed (nt)
 __device__ __forceinline__ bf16x8 ldq(const bf16* base, int64_t e) {
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16*>(base), 0, -1, BUF_DW3);
@@ -69,7 +78,7 @@ __device__ __forceinline__ float sumsq8(const bf16x8 v, float acc) {
   return acc;
 }
 
-// LDS (TOK = 8: 148.5 KB, one block per CU; TOK = 4: 74.3 KB, two blocks per CU): per wave a
+// LDS (TOK = 8: 152.5 KB, one block per CU; TOK = 4: 76.3 KB, two blocks per CU): per wave a
 // 32-row region reused as qkw (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B)
 // and u (rows 0..15, phase B -> C); per wave the token's row indices [order][route parity]
 // [route / 2] (-1 = zero row); the memory-norm weight.
@@ -170,10 +179,11 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   __builtin_amdgcn_wave_barrier();
 
-  // chunk gather: instruction m reads order m & 1 for routes c0 + 4 (m >> 1) + lane / 16, 16-byte
-  // piece lane % 16 (a quarter wave per 256-byte table row); one order per instruction, so that
-  // the 3-gram rows take their own cache policy (FR_POL_T3).
-  const int g_sub = lane >> 4, g_piece = lane & 15;
+  // chunk gather: instruction m reads order m & 1 for routes c0 + 4 (m >> 1) + g_sub, 16-byte
+  // piece g_piece (16 lanes per 256-byte table row); one order per instruction, so that the 3-gram
+  // rows take their own cache policy (FR_POL_T3).  Lanes 0-7 and 16-23 (8-15 and 24-31, ...)
+  // fetch the two halves of one row, so the LDS pass that stores them writes 256 contiguous bytes.
+  const int g_sub = ((lane >> 3) & 1) | ((lane >> 4) & 2), g_piece = (lane & 7) | ((lane >> 1) & 8);
   // every row of a token at t >= 2 exists (both orders), as does every route token: no mask
   const bool all_rows = rows_mode || tpos >= 2;
   // 3-gram rows through a raw buffer descriptor (the table, at most 256 routes x 4096 rows x 256 B,
@@ -249,7 +259,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   // ---------------- phase B: one token per wave
   bf16x8 qb[8];
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][li][64 * lg + 8 * kk]);
+  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][li][fr_col(lg, kk)]);
 
   float m_run = sink, l_part = 0.f;
   f32x4 acc[16];
@@ -262,14 +272,14 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
     __builtin_amdgcn_wave_barrier();
     if (c0 + 32 < R) gather(c0 + 32, g);
 
-    // scores: A = route rows (lane: route 16tt + li, features 64lg + 8kk..), B = qkw
+    // scores: A = route rows (lane: route 16tt + li, features fr_col(lg, kk) ..+8), B = qkw
     float sr[2];
     f32x4 sc[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
       bf16x8 x[8];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) x[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][16 * tt + li][64 * lg + 8 * kk]);
+      for (int kk = 0; kk < 8; ++kk) x[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][16 * tt + li][fr_col(lg, kk)]);
       float ss = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) ss = sumsq8(x[kk], ss);
