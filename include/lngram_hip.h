@@ -65,6 +65,29 @@ int lng_router_features(const void* emb, int dtype, const int64_t* token_ids, in
                         int32_t d, const void* start, const void* prev_w, const void* cur_w, float eps,
                         const float* ssm_state, int32_t N, void* out, void* stream);
 
+/* The token router's tables (bf16): fprev [vocab+2, d] = RMSNorm(E[v]; prev_w) for every row v,
+ * then RMSNorm(start; prev_w) (row vocab), then a zero row; fcur [vocab+1, d] = RMSNorm(E[v];
+ * cur_w), then a zero row.  The per-row halves of TokenRouterFeatures.forward
+ * (ffnmem/memory/router.py:50-59, model.RMSNorm rounding ffnmem/model.py:39-48), which depend on
+ * the token id only: formed once per weight version, read by lng_router_codes_ids. */
+int lng_router_feature_tables(const void* emb, int64_t vocab, int32_t d, const void* start, const void* prev_w,
+                              const void* cur_w, float eps, void* fprev, void* fcur, void* stream);
+
+/* Route codes of the token router straight from token ids: the router GEMM + sign-pack of
+ * lng_router_codes over x[p] = concat(fprev[x_{t-1}] (fprev[vocab] = start at t = 0),
+ * fcur[x_t], ssm_bf16[p]) with the rows gathered inside the GEMM, so the [B*T, 2d+N] features of
+ * lng_router_features are never written.  Replaces TokenRouterFeatures.forward
+ * (ffnmem/memory/router.py:50-59) + LngramMemory.route_logits and its quantisation
+ * (ffnmem/memory/wrapper.py:98-109; lngram_v2.py:1012-1017); the codes equal those of
+ * lng_router_features + lng_router_codes bit for bit.  An id outside [0, vocab) reads a zero row.
+ * token_ids int64 [B*T]; ssm_bf16 [B*T, N] bf16 (lng_ssm_scan_with_bf16) or null with N = 0;
+ * w [n_out, 2d+N] bf16; codes uint8 [B*T, n_out/4] (4-bit codes); logits fp32 or null.
+ * Shapes: lng_router_codes_ids_ok. */
+int32_t lng_router_codes_ids_ok(int64_t M, int32_t d, int32_t N, int64_t n_out);
+int lng_router_codes_ids(const int64_t* token_ids, int64_t vocab, int64_t B, int64_t T, const void* fprev,
+                         const void* fcur, int32_t d, const void* ssm_bf16, int32_t N, const void* w, int64_t n_out,
+                         float* logits, uint8_t* codes, void* stream);
+
 /* ---------------------------------------------------------------- K2: addresses / rows */
 /* addr[B, T-order+1, R] = sum_k codes[b, t'+k, r] << (k*bits).
  * _aligned_ngram_address (lngram_v2.py:314-325).  out_dtype LNG_I32 or LNG_I64. */
@@ -362,6 +385,12 @@ int lng_select_candidates(const void* cand, int dtype, int32_t mem_dim, const vo
 size_t lng_ssm_workspace_bytes(int64_t B, int64_t T, int32_t N);
 int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
                  void* workspace, size_t workspace_bytes, float* s, void* stream);
+
+/* lng_ssm_scan that also writes the states rounded to bf16 (s_bf16 [B, T, N]): the SSM columns
+ * of the token router's features, which TokenRouterFeatures casts to the feature dtype
+ * (ffnmem/memory/router.py:58), for lng_router_codes_ids. */
+int lng_ssm_scan_with_bf16(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
+                           void* workspace, size_t workspace_bytes, float* s, void* s_bf16, void* stream);
 
 /* lng_ssm_scan with the wait for predecessor records bounded by `spin_limit` short sleeps per tile
  * (lng_ssm_scan uses a bound far past any real wait; 0 never waits, so every tile whose

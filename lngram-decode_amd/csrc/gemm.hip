@@ -409,11 +409,25 @@ constexpr int WT_DPW = WT_ROWS / 8 / (WT_WN * WT_WM);  // DMA instructions (8 ro
 
 __device__ __forceinline__ int wswz(int row, int piece) { return piece ^ (row & 7); }
 
-template <int EPI>
+// Gathered X rows (the token router of SD-B / SD-C): row m of X is
+//   concat(fprev[id(m - 1), or `start` at a sequence start], fcur[id(m)], xs[m])
+// over K = 2 dm + ns columns, with fprev / fcur the tabled RMSNorms of the embedding rows
+// (lng_router_feature_tables: row vocab of fprev is `start`, the last row of each table is zero
+// and takes every id outside [0, vocab)) and xs the bf16 SSM states [M, ns] (ns = 0: none).
+// dm and ns are multiples of the 64-column K stage, so every stage reads one source.
+struct XGather {
+  const bf16* fprev;
+  const bf16* fcur;
+  const int64_t* ids;  // [M] token ids, sequences of T
+  int64_t T, vocab;
+  int32_t dm, ns;
+};
+
+template <int EPI, bool GATHER>
 __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restrict__ W, const bf16* __restrict__ X,
                                                            int64_t N, int64_t M, int64_t K, int n_tiles,
                                                            int xcd_local, float* __restrict__ y, void* __restrict__ codes,
-                                                           int codes_dt, int64_t routes) {
+                                                           int codes_dt, int64_t routes, XGather xg) {
   static_assert(EPI == EPI_F32 || EPI == EPI_ROUTER, "fp32 outputs and router codes only");
   constexpr int TN = WT_N / WT_WN, TM = WT_M / WT_WM, FI = TN / 16, FJ = TM / 16;
   __shared__ __attribute__((aligned(16))) bf16 ring[2][WT_ROWS * WT_K];
@@ -429,26 +443,56 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
   const int nk = static_cast<int>(K / WT_K);
   // DMA: tile rows 0 .. WT_N-1 are W rows, the rest X rows; wave w fills rows
   // 8 * (w * WT_DPW + d) .. +8, 8 lanes (16 B pieces) per row
-  const bf16* src[WT_DPW];
+  // src[d]: address of the lane's piece at column 0 of its row's current source (a gathered X row:
+  // of the source's first column, less that column's K offset), as an integer
+  uint64_t src[WT_DPW];
+  int32_t idp[WT_DPW], idc[WT_DPW];  // GATHER: table rows of the previous and the current token
+  const bool x_wave = wave * WT_DPW * 8 >= WT_N;  // waves that fill X rows (uniform per wave)
 #pragma unroll
   for (int d = 0; d < WT_DPW; ++d) {
     const int row = (wave * WT_DPW + d) * 8 + (lane >> 3);
     const int piece = wswz(row, lane & 7);
     if (row < WT_N) {
       const int64_t r = n0 + row < N ? n0 + row : N - 1;
-      src[d] = W + r * K + 8 * piece;
+      src[d] = reinterpret_cast<uint64_t>(W + r * K + 8 * piece);
     } else {
       const int64_t r = m0 + row - WT_N < M ? m0 + row - WT_N : M - 1;
-      src[d] = X + r * K + 8 * piece;
+      if constexpr (GATHER) {
+        // a sequence start reads `start` (fprev row vocab); an id outside [0, vocab) the zero row
+        const bool seq_start = r % xg.T == 0;
+        const int64_t cur = xg.ids[r], prev = seq_start ? 0 : xg.ids[r - 1];
+        idc[d] = static_cast<int32_t>(cur >= 0 && cur < xg.vocab ? cur : xg.vocab);
+        idp[d] = static_cast<int32_t>(seq_start ? xg.vocab : (prev >= 0 && prev < xg.vocab ? prev : xg.vocab + 1));
+        src[d] = reinterpret_cast<uint64_t>(xg.fprev + static_cast<int64_t>(idp[d]) * xg.dm + 8 * piece);
+      } else {
+        src[d] = reinterpret_cast<uint64_t>(X + r * K + 8 * piece);
+      }
     }
   }
+  // GATHER: at the first stage of the fcur and of the state columns, X rows switch source
+  auto x_section = [&](int kt) {
+    if constexpr (GATHER) {
+      const int64_t kb = static_cast<int64_t>(kt) * WT_K;
+      if (!x_wave || (kb != xg.dm && kb != 2 * static_cast<int64_t>(xg.dm))) return;
+#pragma unroll
+      for (int d = 0; d < WT_DPW; ++d) {
+        const int row = (wave * WT_DPW + d) * 8 + (lane >> 3);
+        const int piece = wswz(row, lane & 7);
+        const int64_t r = m0 + row - WT_N < M ? m0 + row - WT_N : M - 1;
+        const bf16* p = kb == xg.dm ? xg.fcur + static_cast<int64_t>(idc[d]) * xg.dm + 8 * piece
+                                    : X + r * xg.ns + 8 * piece;
+        src[d] = reinterpret_cast<uint64_t>(p) - static_cast<uint64_t>(kb) * sizeof(bf16);
+      }
+    }
+  };
   auto issue = [&](int kt) {
     bf16* base = &ring[kt & 1][wave * WT_DPW * 8 * WT_K];
-    const int64_t kb = static_cast<int64_t>(kt) * WT_K;
+    const uint64_t kb = static_cast<uint64_t>(kt) * WT_K * sizeof(bf16);
 #pragma unroll
     for (int d = 0; d < WT_DPW; ++d) {
       bf16* dst = base + d * 8 * WT_K;
-      __builtin_amdgcn_global_load_lds(src[d] + kb, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const bf16*>(src[d] + kb),
+                                       (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
     }
   };
 
@@ -466,7 +510,10 @@ __global__ __launch_bounds__(512, 1) void k_gemm_wide_bf16(const bf16* __restric
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + 1 < nk) issue(kt + 1);
+    if (kt + 1 < nk) {
+      x_section(kt + 1);
+      issue(kt + 1);
+    }
     const bf16* st = &ring[kt & 1][0];
 #pragma unroll
     for (int kk = 0; kk < WT_K / 32; ++kk) {
@@ -849,8 +896,8 @@ static int launch_mfma(const bf16* w, const bf16* x, int64_t N, int64_t M, int64
       // X tiles per XCD when the grid divides evenly over the 8 XCDs, else 0 (plain order)
       const int xcd_local = m_tiles % 8 == 0 ? static_cast<int>(m_tiles / 8) : 0;
       const dim3 g(static_cast<unsigned>(n_tiles * m_tiles));
-      hipLaunchKernelGGL(k_gemm_wide_bf16<EPI>, g, dim3(512), 0, s, w, x, N, M, K, n_tiles, xcd_local,
-                         logits ? logits : static_cast<float*>(out), codes, codes_dt, routes);
+      hipLaunchKernelGGL((k_gemm_wide_bf16<EPI, false>), g, dim3(512), 0, s, w, x, N, M, K, n_tiles, xcd_local,
+                         logits ? logits : static_cast<float*>(out), codes, codes_dt, routes, XGather{});
       return check_launch("gemm_bf16_wide");
     }
   }
@@ -1000,6 +1047,37 @@ int lng_router_codes(const void* x, int x_dtype, const void* w, int w_dtype, int
   }
   if (!codes) return LNG_OK;
   return lng_pack_route_codes(logits, M, N, bits, codes, codes_dtype, stream);
+}
+
+int32_t lng_router_codes_ids_ok(int64_t M, int32_t d, int32_t N, int64_t n_out) {
+  const int64_t K = 2 * static_cast<int64_t>(d) + N;
+  return M >= 4096 && d > 0 && d % WT_K == 0 && N >= 0 && N % WT_K == 0 && n_out > GB2 && n_out <= 2 * WT_N &&
+                 n_out % 4 == 0 && K <= (int64_t{1} << 20)
+             ? 1
+             : 0;
+}
+
+int lng_router_codes_ids(const int64_t* token_ids, int64_t vocab, int64_t B, int64_t T, const void* fprev,
+                         const void* fcur, int32_t d, const void* ssm_bf16, int32_t N, const void* w, int64_t n_out,
+                         float* logits, uint8_t* codes, void* stream) {
+  if (!token_ids || !fprev || !fcur || !w || !codes || (N > 0) != (ssm_bf16 != nullptr))
+    return fail(LNG_E_ARG, "router_codes_ids: null pointer (ssm_bf16 and N > 0 go together)");
+  if (B < 0 || T <= 0 || vocab <= 0 || vocab > (int64_t{1} << 30)) return fail(LNG_E_ARG, "router_codes_ids: bad shape");
+  const int64_t M = B * T;
+  if (M == 0) return LNG_OK;
+  if (!lng_router_codes_ids_ok(M, d, N, n_out))
+    return fail(LNG_E_ARG, "router_codes_ids: needs B*T >= 4096, d and N multiples of 64, 256 < n_out <= 768, "
+                           "n_out % 4 == 0 (lng_router_codes_ids_ok)");
+  const int64_t K = 2 * static_cast<int64_t>(d) + N;
+  const int n_tiles = static_cast<int>(cdiv(n_out, WT_N));
+  const int64_t m_tiles = cdiv(M, WT_M);
+  const int xcd_local = m_tiles % 8 == 0 ? static_cast<int>(m_tiles / 8) : 0;
+  const dim3 g(static_cast<unsigned>(n_tiles * m_tiles));
+  const XGather xg{static_cast<const bf16*>(fprev), static_cast<const bf16*>(fcur), token_ids, T, vocab, d, N};
+  hipLaunchKernelGGL((k_gemm_wide_bf16<EPI_ROUTER, true>), g, dim3(512), 0, as_stream(stream),
+                     static_cast<const bf16*>(w), static_cast<const bf16*>(ssm_bf16), n_out, M, K, n_tiles, xcd_local,
+                     logits, codes, LNG_U8, n_out / 4, xg);
+  return check_launch("router_codes_ids");
 }
 
 int lng_linear_at(const void* x, const void* w, int64_t M, int64_t N, int64_t K, int64_t group, int64_t stride,

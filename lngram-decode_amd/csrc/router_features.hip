@@ -112,9 +112,54 @@ __global__ __launch_bounds__(256) void k_router_features(FeArgs A, TT* __restric
   }
 }
 
+// The router's normalised embedding tables (bf16): fprev [V+2, d] = RMSNorm_prev of E's rows,
+// then of `start` (row V), then a zero row (V+1); fcur [V+1, d] = RMSNorm_cur of E's rows, then a
+// zero row (V).  Rows are normalised exactly as k_router_features normalises a gathered row, so a
+// feature row assembled from the tables equals the one that kernel writes.  One wave per row index.
+template <int PPL>
+__global__ __launch_bounds__(256) void k_router_feature_tables(const bf16* __restrict__ E, int64_t V,
+                                                               const bf16* __restrict__ start,
+                                                               const bf16* __restrict__ prev_w,
+                                                               const bf16* __restrict__ cur_w, int32_t d, float eps,
+                                                               bf16* __restrict__ fprev, bf16* __restrict__ fcur) {
+  const int lane = threadIdx.x & 63;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (v > V + 1) return;
+  const int np = d / 8;
+  const bf16* row = v < V ? E + v * d : nullptr;
+  fe_piece_t vp[PPL], vc[PPL];
+  fe_load_row<bf16, PPL>(v < V ? row : (v == V ? start : nullptr), np, lane, vp);
+  fe_load_row<bf16, PPL>(row, np, lane, vc);
+  fe_norm_store<bf16, PPL>(vp, prev_w, d, np, eps, fprev + v * d, lane);
+  if (v <= V) fe_norm_store<bf16, PPL>(vc, cur_w, d, np, eps, fcur + v * d, lane);
+}
+
 }  // namespace lng
 
 using namespace lng;
+
+extern "C" int lng_router_feature_tables(const void* emb, int64_t vocab, int32_t d, const void* start,
+                                         const void* prev_w, const void* cur_w, float eps, void* fprev, void* fcur,
+                                         void* stream) {
+  if (!emb || !start || !prev_w || !cur_w || !fprev || !fcur) return fail(LNG_E_ARG, "router_feature_tables: null pointer");
+  if (vocab <= 0 || vocab > (int64_t{1} << 30) || d <= 0 || d % 8 || d / 8 > FE_MAXP * 64)
+    return fail(LNG_E_ARG, "router_feature_tables: bf16 rows of d % 8 == 0, d <= 4096, 0 < vocab <= 2^30");
+  const dim3 grid(static_cast<unsigned>(cdiv(vocab + 2, 4)));
+  hipStream_t s = as_stream(stream);
+  const bf16 *e = static_cast<const bf16*>(emb), *st = static_cast<const bf16*>(start);
+  const bf16 *pw = static_cast<const bf16*>(prev_w), *cw = static_cast<const bf16*>(cur_w);
+  bf16 *fp = static_cast<bf16*>(fprev), *fc = static_cast<bf16*>(fcur);
+  switch (static_cast<int>(cdiv(d / 8, 64))) {
+    case 1: hipLaunchKernelGGL((k_router_feature_tables<1>), grid, dim3(256), 0, s, e, vocab, st, pw, cw, d, eps, fp, fc); break;
+    case 2: hipLaunchKernelGGL((k_router_feature_tables<2>), grid, dim3(256), 0, s, e, vocab, st, pw, cw, d, eps, fp, fc); break;
+    case 3:
+    case 4: hipLaunchKernelGGL((k_router_feature_tables<4>), grid, dim3(256), 0, s, e, vocab, st, pw, cw, d, eps, fp, fc); break;
+    default:
+      hipLaunchKernelGGL((k_router_feature_tables<FE_MAXP>), grid, dim3(256), 0, s, e, vocab, st, pw, cw, d, eps, fp, fc);
+      break;
+  }
+  return check_launch("router_feature_tables");
+}
 
 extern "C" int lng_router_features(const void* emb, int dtype, const int64_t* token_ids, int64_t vocab, int64_t B,
                                    int64_t T, int32_t d, const void* start, const void* prev_w, const void* cur_w,

@@ -98,7 +98,8 @@ template <bool VEC, int CPOL>
 __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, const float* __restrict__ u,
                                                   const float* __restrict__ s0, int32_t T, int32_t N, int32_t G,
                                                   int32_t chains, uint8_t* __restrict__ ws, uint32_t ws_bytes,
-                                                  int32_t spin_limit, float* __restrict__ s_out) {
+                                                  int32_t spin_limit, float* __restrict__ s_out,
+                                                  bf16* __restrict__ sb_out) {
   __shared__ float s_end[SSM_WAVES][SSM_GC];   // wave ends from a zero start
   __shared__ float s_term[SSM_WAVES][SSM_GC];  // the waves' terms of the tile's aggregate
   __shared__ float s_part[SSM_WAVES][SSM_GC];  // the waves' shares of the carry
@@ -288,6 +289,13 @@ __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, c
 #pragma unroll
         for (int j = 0; j < 4; ++j) st[j] = fmaf(av[j], st[j], bv[j] * x[i][j]);
         store4<VEC>(sb + static_cast<int64_t>(t0 + i) * N, c, N, st);
+        if (sb_out) {
+          // the states rounded to bf16 as well (the token router's feature columns)
+          bf16* q = sb_out + static_cast<int64_t>(b) * T * N + static_cast<int64_t>(t0 + i) * N;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (c + j < N) q[c + j] = static_cast<bf16>(st[j]);
+        }
       }
     }
   }
@@ -309,7 +317,7 @@ size_t ssm_workspace_bytes(int64_t B, int64_t T, int32_t N) {
 }
 
 int ssm_scan_launch(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, uint8_t* ws,
-                    size_t ws_bytes, int32_t spin_limit, float* s, hipStream_t st) {
+                    size_t ws_bytes, int32_t spin_limit, float* s, hipStream_t st, bf16* sb = nullptr) {
   if (B < 0 || T < 0 || N <= 0) return fail(LNG_E_ARG, "ssm_scan: bad shape");
   if (B == 0 || T == 0) return LNG_OK;
   if (T > INT32_MAX / 2 || static_cast<int64_t>(N) * T > (int64_t{1} << 40))
@@ -326,10 +334,10 @@ int ssm_scan_launch(const float* a, const float* u, const float* s0, int64_t B, 
   const dim3 grid(static_cast<unsigned>(tiles)), blk(512);
   if (N % 4 == 0)
     hipLaunchKernelGGL((k_ssm_scan<true, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb,
-                       spin_limit, s);
+                       spin_limit, s, sb);
   else
     hipLaunchKernelGGL((k_ssm_scan<false, CPOL_SC1>), grid, blk, 0, st, a, u, s0, Ti, N, G, chains, ws, wsb,
-                       spin_limit, s);
+                       spin_limit, s, sb);
   return check_launch("ssm_scan");
 }
 
@@ -402,6 +410,13 @@ int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int
                  size_t workspace_bytes, float* s, void* stream) {
   return ssm_scan_launch(a, u, s0, B, T, N, static_cast<uint8_t*>(workspace), workspace_bytes, SSM_SPIN_LIMIT, s,
                          as_stream(stream));
+}
+
+int lng_ssm_scan_with_bf16(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
+                           void* workspace, size_t workspace_bytes, float* s, void* s_bf16, void* stream) {
+  if (!s_bf16) return fail(LNG_E_ARG, "ssm_scan_with_bf16: null bf16 output");
+  return ssm_scan_launch(a, u, s0, B, T, N, static_cast<uint8_t*>(workspace), workspace_bytes, SSM_SPIN_LIMIT, s,
+                         as_stream(stream), static_cast<bf16*>(s_bf16));
 }
 
 int lng_ssm_scan_bounded(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,

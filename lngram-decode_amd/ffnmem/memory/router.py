@@ -43,6 +43,7 @@ class TokenRouterFeatures(nn.Module):
         self.cur_norm = RMSNorm(d_model, eps)
         self.start = nn.Parameter(torch.empty(d_model))
         nn.init.normal_(self.start, mean=0.0, std=init_std)
+        self._tables_cache = None
 
     def _features(self, emb: Tensor, ssm_state: Tensor | None, token_ids: Tensor | None = None) -> Tensor:
         if self.kind == "embed2_ssm" and ssm_state is None:
@@ -64,6 +65,20 @@ class TokenRouterFeatures(nn.Module):
         """``forward(table[token_ids], ssm_state)`` with the embedding gather fused into the kernel
         (not in the reference module: the model gathers ``emb`` itself)."""
         return self._features(table, ssm_state, token_ids)
+
+    def tables(self, table: Tensor) -> tuple:
+        """``(fprev, fcur)``: the normalised rows of the embedding table for the previous-token and the
+        current-token halves (``fprev[V]`` the normalised ``start``, a zero row last in each;
+        ``ops.router_feature_tables``), cached per version of the table and of this module's
+        parameters.  Not in the reference module: the gathered router GEMM reads them."""
+        ps = (table, self.start, self.prev_norm.weight, self.cur_norm.weight)
+        key = tuple((p.data_ptr(), p._version) for p in ps) + (table.shape, table.device)
+        if self._tables_cache is None or self._tables_cache[0] != key:
+            with torch.no_grad():
+                t = ops.router_feature_tables(table.detach(), self.start.detach(), self.prev_norm.weight.detach(),
+                                              self.cur_norm.weight.detach(), self.prev_norm.eps)
+            self._tables_cache = (key, t)
+        return self._tables_cache[1]
 
     def step(self, emb_prev: Tensor | None, emb_cur: Tensor, ssm_state: Tensor | None = None) -> Tensor:
         """One position (decode / drafter), ``[B, d]`` inputs; ``emb_prev`` None at t = 0.  The kernel

@@ -104,6 +104,35 @@ class LngramMemory(nn.Module):
         if self.training and torch.is_grad_enabled():
             raise NotImplementedError("training (surrogate route gradient) is not part of the MI355X path")
         q_logits, codes = self.route_codes(x, want_logits=keep)
+        return self._forward_codes(h, q_logits, codes, keep)
+
+    def forward_ids(self, h: Tensor, token_ids: Tensor, emb_table: Tensor, ssm_state: Tensor | None = None) -> Tensor:
+        """``forward(h, None, router_features.from_ids(token_ids, emb_table, ssm_state))`` for a
+        token-routed memory (``router.py:50-59`` + ``wrapper.py:103-125``), with the router's
+        feature rows gathered inside the router GEMM from tables of the normalised embedding rows
+        (``lng_router_codes_ids``), so the ``[B, T, 2d + N]`` features are never materialised.
+        ``ssm_state`` ``[B, T, N]`` (``embed2_ssm``), bf16 (``ops.ssm_scan(..., want_bf16=True)``)
+        or fp32.  Shapes the gathered GEMM does not take run the materialised features."""
+        if self.router_input == "hidden":
+            raise ValueError("forward_ids is for token-routed memories (router_input embed2 / embed2_ssm)")
+        if self.training and torch.is_grad_enabled():
+            raise NotImplementedError("training (surrogate route gradient) is not part of the MI355X path")
+        s_in = ssm_state if self.router_input == "embed2_ssm" else None
+        if self.router_input == "embed2_ssm" and s_in is None:
+            raise ValueError("embed2_ssm router needs the SSM state")
+        b, t = token_ids.shape
+        n = 0 if s_in is None else s_in.shape[-1]
+        w = self.router.weight
+        if not (emb_table.dtype == w.dtype == torch.bfloat16 and self.bits == 4
+                and ops.router_codes_ids_ok(b * t, emb_table.shape[1], n, w.shape[0])):
+            return self.forward(h, None, self.router_features.from_ids(token_ids, emb_table, s_in))
+        keep = self.token_router is not None or self.capture_route_logits
+        fprev, fcur = self.router_features.tables(emb_table)
+        sb = None if s_in is None else (s_in if s_in.dtype == torch.bfloat16 else s_in.to(torch.bfloat16))
+        q_logits, codes = ops.router_codes_ids(token_ids, fprev, fcur, sb, w, want_logits=keep)
+        return self._forward_codes(h, q_logits, codes, keep)
+
+    def _forward_codes(self, h: Tensor, q_logits: Tensor | None, codes: Tensor, keep: bool) -> Tensor:
         if keep:
             self.last_route_logits = q_logits.detach()
         if self.collect_diagnostics and not self.training:

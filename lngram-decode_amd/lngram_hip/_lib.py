@@ -69,6 +69,9 @@ SIGNATURES = {
     "lng_router_codes": (_int, [_p, _int, _p, _int, _i64, _i64, _i64, _i32, _p, _p, _int, _p]),
     "lng_pack_route_codes": (_int, [_p, _i64, _i64, _i32, _p, _int, _p]),
     "lng_router_features": (_int, [_p, _int, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _f, _p, _i32, _p, _p]),
+    "lng_router_feature_tables": (_int, [_p, _i64, _i32, _p, _p, _p, _f, _p, _p, _p]),
+    "lng_router_codes_ids_ok": (_i32, [_i64, _i32, _i32, _i64]),
+    "lng_router_codes_ids": (_int, [_p, _i64, _i64, _i64, _p, _p, _i32, _p, _i32, _p, _i64, _p, _p, _p]),
     "lng_ngram_address": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _p, _int, _p]),
     "lng_ngram_rows": (_int, [_p, _int, _i64, _i64, _i32, _i32, _i32, _P32, _i32, _i32, _p, _p, _p, _int, _p]),
     "lng_online_mix": (_int, [_p, _p, _i32, _p, _p, _i32, _i32, _i32, _p, _i64, _f, _p, _p, _p]),
@@ -114,6 +117,7 @@ SIGNATURES = {
     "lng_ssm_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32]),
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _p, _p]),
     "lng_ssm_scan_bounded": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _i32, _p, _p]),
+    "lng_ssm_scan_with_bf16": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _p, _p, _p]),
     "lng_ssm_scan_static": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p]),
     "lng_ssm_scan_static_status": (_int, [_p]),
     "lng_drafter_tree_levels_workspace": (ctypes.c_size_t, [_PD]),

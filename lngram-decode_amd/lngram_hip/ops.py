@@ -185,6 +185,53 @@ def router_features(emb: torch.Tensor, start: torch.Tensor, prev_w: torch.Tensor
     return out
 
 
+def router_feature_tables(emb: torch.Tensor, start: torch.Tensor, prev_w: torch.Tensor, cur_w: torch.Tensor,
+                          eps: float) -> tuple:
+    """``(fprev [V+2, d], fcur [V+1, d])`` bf16 (``lng_router_feature_tables``): the normalised
+    embedding rows of the token router, ``fprev[V]`` the normalised ``start``, the last row of
+    each a zero row."""
+    dev = _dev(emb, start, prev_w, cur_w)
+    if emb.dtype != torch.bfloat16 or emb.dim() != 2:
+        raise ValueError("router_feature_tables takes a bf16 [V, d] embedding table")
+    v, d = emb.shape
+    fprev = torch.empty(v + 2, d, dtype=torch.bfloat16, device=dev)
+    fcur = torch.empty(v + 1, d, dtype=torch.bfloat16, device=dev)
+    bf = torch.bfloat16
+    check(lib().lng_router_feature_tables(_ptr(_c(emb)), v, d, _ptr(_c(start.to(bf))), _ptr(_c(prev_w.to(bf))),
+                                          _ptr(_c(cur_w.to(bf))), eps, _ptr(fprev), _ptr(fcur), _stream(dev)),
+          "router_feature_tables")
+    return fprev, fcur
+
+
+def router_codes_ids_ok(m: int, d: int, n: int, n_out: int) -> bool:
+    """Shapes ``lng_router_codes_ids`` takes (``m`` tokens, ``d``-wide embeddings, ``n`` SSM columns)."""
+    return bool(lib().lng_router_codes_ids_ok(m, d, n, n_out))
+
+
+def router_codes_ids(token_ids: torch.Tensor, fprev: torch.Tensor, fcur: torch.Tensor, ssm_bf16: torch.Tensor | None,
+                     w: torch.Tensor, want_logits: bool = False):
+    """``(fp32 logits or None, uint8 codes [B, T, n_out/4])`` of the token router over the features
+    gathered from the tables inside the GEMM (``lng_router_codes_ids``): equal to
+    ``router_codes(router_features(...), w, 4)``."""
+    dev = _dev(token_ids, fprev, fcur, ssm_bf16, w)
+    b, t = token_ids.shape
+    v = fcur.shape[0] - 1
+    d = fcur.shape[1]
+    n = 0 if ssm_bf16 is None else ssm_bf16.shape[-1]
+    if w.dtype != torch.bfloat16 or w.shape[1] != 2 * d + n:
+        raise ValueError(f"router weight {tuple(w.shape)} does not take [2d + N] = [{2 * d + n}] bf16 features")
+    if ssm_bf16 is not None and (ssm_bf16.dtype != torch.bfloat16 or tuple(ssm_bf16.shape[:2]) != (b, t)):
+        raise ValueError("ssm_bf16 must be bf16 [B, T, N]")
+    n_out = w.shape[0]
+    ids = _c(token_ids.to(torch.int64))
+    codes = torch.empty(b, t, n_out // 4, dtype=torch.uint8, device=dev)
+    logits = torch.empty(b, t, n_out, dtype=torch.float32, device=dev) if want_logits else None
+    check(lib().lng_router_codes_ids(_ptr(ids), v, b, t, _ptr(_c(fprev)), _ptr(_c(fcur)), d,
+                                     _ptr(None if ssm_bf16 is None else _c(ssm_bf16)), n, _ptr(_c(w)), n_out,
+                                     _ptr(logits), _ptr(codes), _stream(dev)), "router_codes_ids")
+    return logits, codes
+
+
 def router_features_ok(d: int, n: int, dtype: torch.dtype) -> bool:
     """Shapes ``lng_router_features`` takes."""
     es = torch.finfo(dtype).bits // 8 if dtype.is_floating_point else 0
@@ -852,10 +899,11 @@ def _ssm_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
 
 
 def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None,
-             spin_limit: int | None = None) -> torch.Tensor:
+             spin_limit: int | None = None, want_bf16: bool = False):
     """``s_t = a s_{t-1} + (1 - a) u_t`` (fp32) for u ``[B, T, N]``, a ``[N]``, s0 ``[B, N]`` or None.
     ``spin_limit`` bounds each tile's wait for its predecessors (``lng_ssm_scan_bounded``; None: the
-    library's bound); a tile whose wait runs out forms its carry from u directly (exact)."""
+    library's bound); a tile whose wait runs out forms its carry from u directly (exact).
+    ``want_bf16``: returns ``(s, s rounded to bf16)`` from the same launch (``lng_ssm_scan_with_bf16``)."""
     dev = _dev(a, u, s0)
     uc = _c(u.float())
     ac = _c(a.float())
@@ -863,14 +911,21 @@ def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None,
     b, t, n = uc.shape
     out = torch.empty_like(uc)
     ws = _ssm_workspace(dev, lib().lng_ssm_workspace_bytes(b, t, n))
-    if spin_limit is None:
+    sb = None
+    if want_bf16:
+        if spin_limit is not None:
+            raise ValueError("want_bf16 takes the library's wait bound")
+        sb = torch.empty(b, t, n, dtype=torch.bfloat16, device=dev)
+        launch = lambda: lib().lng_ssm_scan_with_bf16(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws),  # noqa: E731
+                                                      ws.numel(), _ptr(out), _ptr(sb), _stream(dev))
+    elif spin_limit is None:
         launch = lambda: lib().lng_ssm_scan(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws), ws.numel(),  # noqa: E731
                                             _ptr(out), _stream(dev))
     else:
         launch = lambda: lib().lng_ssm_scan_bounded(_ptr(ac), _ptr(uc), _ptr(s0c), b, t, n, _ptr(ws),  # noqa: E731
                                                     ws.numel(), int(spin_limit), _ptr(out), _stream(dev))
     check(_timed("ssm_scan", dev, launch), "ssm_scan")
-    return out
+    return (out, sb) if want_bf16 else out
 
 
 def ssm_scan_status(dev: torch.device) -> int:

@@ -123,3 +123,43 @@ def test_sdc_full_size_sampled(dev):
                                             codes[b:b + 1, max(0, t - 11):t + 1])[0, -1] for b, t in picks])
     assert om.rel_err(got, want) < 2e-2
     assert om.rel_err(got, want64) < 2e-2
+
+
+@pytest.mark.parametrize("which", ["sdc", "sdb"])
+def test_router_codes_from_ids_equal_materialised_features(dev, which):
+    """The router GEMM over rows gathered from the tabled embedding norms (lng_router_codes_ids) against
+    the materialised features + router GEMM (lng_router_features + lng_router_codes, pinned to the
+    oracle above): the tables equal the features' halves, and codes, logits and the layer output are
+    bit-identical, with ids outside the vocabulary and sequence starts in the batch."""
+    base = workloads.SDC if which == "sdc" else workloads.SDB
+    w = base.with_shape(2, 2048)                              # 4096 tokens: the gathered GEMM's smallest M
+    mem, E, tok, a, u, h = _sdc_pipeline(w, dev, seed=5)
+    V, d = w.vocab, w.d_model
+    tok[0, 7] = -1
+    tok[1, 100] = V
+    tok[1, 5] = V + 9
+    E, tok, h = E.to(dev), tok.to(dev), h.to(dev)
+    feats = mem.router_features
+    s = sb = None
+    if which == "sdc":
+        s, sb = ops.ssm_scan(a.to(dev), u.to(dev), want_bf16=True)
+        assert torch.equal(s, ops.ssm_scan(a.to(dev), u.to(dev)))
+        assert torch.equal(sb, s.to(torch.bfloat16))
+    x = feats.from_ids(tok, E, s)
+    fprev, fcur = feats.tables(E)
+    assert fprev.shape == (V + 2, d) and fcur.shape == (V + 1, d)
+    valid = (tok >= 0) & (tok < V)
+    idc = torch.where(valid, tok, V)
+    idp = torch.cat((torch.full_like(idc[:, :1], V), torch.where(valid, tok, V + 1)[:, :-1]), 1)
+    assert torch.equal(x[..., :d], fprev[idp]) and torch.equal(x[..., d:2 * d], fcur[idc])
+    assert not bool(fprev[V + 1].any()) and not bool(fcur[V].any())
+    n = 0 if sb is None else sb.shape[-1]
+    assert ops.router_codes_ids_ok(tok.numel(), d, n, mem.router.weight.shape[0])
+    lg_ref, codes_ref = mem.route_codes(x, want_logits=True)
+    lg, codes = ops.router_codes_ids(tok, fprev, fcur, sb, mem.router.weight, want_logits=True)
+    assert torch.equal(codes, codes_ref) and torch.equal(lg, lg_ref)
+    with torch.no_grad():
+        out_ref = mem(h, None, router_in=x)
+        out = mem.forward_ids(h, tok, E, sb)
+        out32 = mem.forward_ids(h, tok, E, s)                 # fp32 states are rounded the same way
+    assert torch.equal(out, out_ref) and torch.equal(out32, out_ref)
