@@ -312,6 +312,151 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
   }
 }
 
+// The approximate mode for bf16 rows of 128 and 4-bit codes (the SB layer's lookup), orders 2 and
+// 3: the same windows, scores and output sums as k_surrogate_grad over tiles of 128 windows (8 per
+// 16-lane group, halving the blocks and their fixed staging and output phases), with the tile's digits and
+// window validity staged in LDS once per block (one coalesced load each, instead of order
+// scattered code loads per window on each window's critical path) and the windows of a 16-lane
+// group pipelined two deep: window i + 1's memory-gradient, looked-up and counterfactual rows are
+// requested before window i's dot products are reduced.
+// SP_WIN windows per block: RG consecutive routes x SP_WIN / RG windows each.
+template <int ORDER, int RG, int SP_WIN>
+__global__ __launch_bounds__(256) void k_surrogate_grad_pk(SgArgs a) {
+  constexpr int BITS = 4, NF = ORDER * BITS, NW = SP_WIN / 16, WR = SP_WIN / RG;
+  constexpr int64_t D = 128;
+  __shared__ float sc[SP_WIN][SG_SC];                 // window rr * WR + lw
+  __shared__ uint8_t cds[RG][WR + SG_MAXORDER];       // digit of route r0 + rr at position s_lo + i
+  __shared__ uint8_t vld[WR];                         // window s_lo + lw has a gradient row
+  const int grp = threadIdx.x >> 4, l = threadIdx.x & 15;
+  // block -> (route group, sequence, tile): XCD x = block % 8 keeps to groups 8j + x, all of a group's
+  // (sequence, tile) blocks in a row, so the group's blocks of the table stay in that XCD's L2
+  const int64_t xcd = blockIdx.x & 7;
+  const int64_t k8 = blockIdx.x >> 3;
+  const int64_t per_group = a.B * a.tiles;
+  const int64_t g = (k8 / per_group) * 8 + xcd;
+  const int64_t r0 = g * RG;
+  if (r0 >= a.R) return;                              // the whole block: before any barrier
+  const int64_t rem = k8 % per_group;
+  const int64_t b = rem / a.tiles;
+  constexpr int P = WR - (ORDER - 1);
+  const int64_t t0 = (rem % a.tiles) * P;
+  const int64_t s_lo = t0 - (ORDER - 1);
+  const int64_t VL = a.T - ORDER + 1;
+  const int64_t RD = static_cast<int64_t>(a.R) * D;
+  const bf16* grad = static_cast<const bf16*>(a.grad);
+  const bf16* hard = static_cast<const bf16*>(a.hard);
+  const bf16* table = static_cast<const bf16*>(a.table);
+  const bool nt = a.nt != 0;
+  const bool active = VL > 0 && a.temperature != 0.f && a.scale != 0.f;
+  // the codes of RG consecutive routes at one position are consecutive bytes: rr runs fastest
+  for (int i = threadIdx.x; i < RG * (WR + ORDER - 1); i += 256) {
+    const int rr = i % RG, pi = i / RG;
+    const int64_t pos = s_lo + pi;
+    cds[rr][pi] = (pos >= 0 && pos < a.T && r0 + rr < a.R)
+                      ? static_cast<uint8_t>(sg_code(a.codes, a.codes_dt, (b * a.T + pos) * a.R + r0 + rr) & 15)
+                      : 0;
+  }
+  for (int i = threadIdx.x; i < WR; i += 256) {
+    const int64_t sw = s_lo + i;
+    vld[i] = active && sw >= 0 && sw < VL && (a.valid == nullptr || a.valid[b * a.T + sw + ORDER - 1]);
+  }
+  __syncthreads();
+  // Window w = rr * WR + lw reads its memory-gradient and looked-up rows (streamed from HBM) and
+  // the rows of its route's block of the table (2^(4 ORDER) rows of 256 B) with bit f of its
+  // address flipped (mostly L2 hits): offsets (row << 8) | (lane << 4) in a buffer resource over the
+  // block, so the row with bit f flipped is the offset with bit f + 8 flipped.  A group's windows
+  // are pipelined two deep.
+  auto live = [&](int w) { return vld[w % WR] && r0 + w / WR < a.R; };
+  auto addr_of = [&](int w) -> uint32_t {
+    const int rr = w / WR, lw = w % WR;
+    uint32_t addr = 0;
+#pragma unroll
+    for (int k = 0; k < ORDER; ++k) addr |= static_cast<uint32_t>(cds[rr][lw + k]) << (k * BITS);
+    return addr;
+  };
+  auto load_gh = [&](int w, u32x4 (&v)[2]) {
+    if (!live(w)) return;
+    const int64_t mrow = (b * a.T + s_lo + w % WR + ORDER - 1) * RD + (r0 + w / WR) * D + l * 8;
+    v[0] = ld_raw16(grad, mrow * 2, nt);
+    v[1] = ld_raw16(hard, mrow * 2, nt);
+  };
+  auto load_cf = [&](int w, uint32_t addr, u32x4 (&v)[NF]) {
+    if (!live(w)) return;
+    const __amdgpu_buffer_rsrc_t tb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16*>(table + ((static_cast<int64_t>(a.route_start) + r0 + w / WR) << (BITS * ORDER)) * D), 0,
+        static_cast<int>((int64_t(1) << (BITS * ORDER)) * D * 2), BUF_DW3);
+    const uint32_t off = (addr << 8) | (static_cast<uint32_t>(l) << 4);
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      v[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tb, off ^ (1u << (f + 8)), 0, 0));
+  };
+  // a dot product's 16-lane partials summed along the row (inclusive prefix by DPP shifts, the order
+  // of sum16): the total is in the row's last lane, which alone forms and stores the scores
+  auto sum_last = [](float x) {
+    x += dpp_row_shr<0x111>(x, 0.f);
+    x += dpp_row_shr<0x112>(x, 0.f);
+    x += dpp_row_shr<0x114>(x, 0.f);
+    x += dpp_row_shr<0x118>(x, 0.f);
+    return x;
+  };
+  auto reduce = [&](int w, uint32_t addr, const u32x4 (&gh)[2], const u32x4 (&cf)[NF]) {
+    float score[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) score[f] = 0.f;
+    if (live(w)) {
+      const float cd = sum_last(dot8_bf16(gh[1], gh[0]));
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const float fd = sum_last(dot8_bf16(cf[f], gh[0]));
+        score[f] = (fd - cd) * (((addr >> f) & 1) ? -1.f : 1.f);
+      }
+    }
+    if (l == 15) {
+#pragma unroll
+      for (int e = 0; e < SG_MAXORDER; ++e)
+#pragma unroll
+        for (int k = 0; k < SG_MAXBITS; ++k)
+          sc[w][e * SG_MAXBITS + k] = (e < ORDER && k < BITS) ? score[e * BITS + k] : 0.f;
+    }
+  };
+  // two windows in flight per group: window j + 1's rows are requested before window j is reduced
+  u32x4 gh[2][2], cf[2][NF];
+  uint32_t ad[2];
+  ad[0] = addr_of(grp);
+  load_gh(grp, gh[0]);
+  load_cf(grp, ad[0], cf[0]);
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    if (j + 1 < NW) {
+      ad[(j + 1) & 1] = addr_of(grp + 16 * (j + 1));
+      load_gh(grp + 16 * (j + 1), gh[(j + 1) & 1]);
+      load_cf(grp + 16 * (j + 1), ad[(j + 1) & 1], cf[(j + 1) & 1]);
+    }
+    reduce(grp + 16 * j, ad[j & 1], gh[j & 1], cf[j & 1]);
+  }
+  __syncthreads();
+  // output (t, route, bit), bits then routes fastest (whole lines of the [B, T, R, bits] arrays):
+  // the windows t - e, e ascending
+  for (int i = threadIdx.x; i < P * RG * BITS; i += 256) {
+    const int k = i % BITS, rr = (i / BITS) % RG, tl = i / (BITS * RG);
+    const int64_t t = t0 + tl;
+    if (t >= a.T) break;
+    if (r0 + rr >= a.R) continue;
+    float acc = 0.f;
+    for (int e = 0; e < ORDER; ++e) acc += sc[rr * WR + tl + ORDER - 1 - e][e * SG_MAXBITS + k];
+    const int64_t oi = ((b * a.T + t) * a.R + r0 + rr) * BITS + k;
+    if (active) {
+      const float qv = a.q_dt == LNG_BF16 ? to_f32(static_cast<const bf16*>(a.q)[oi]) : static_cast<const float*>(a.q)[oi];
+      const float p = 1.f / (1.f + expf(-(a.temperature * qv)));
+      acc *= a.alpha * p * (1.f - p);
+    }
+    if (a.out_dt == LNG_BF16)
+      static_cast<bf16*>(a.out)[oi] = static_cast<bf16>(acc);
+    else
+      static_cast<float*>(a.out)[oi] = acc;
+  }
+}
+
 // Table gradient of the lookup (the embedding backward behind the surrogate's pass-through,
 // lngram_v2.py:1084-1092 and :454): table_grad[row(b, t, r)] += grad[b, t, r, :] * valid[b, t] for
 // every position with an order-`order` window.  One 16-lane group per (b, t, r); fp32 atomics, so
@@ -345,6 +490,24 @@ template <typename TM, bool EXACT>
 static int sg_launch_v(const SgArgs& a, int64_t D, hipStream_t s) {
   const int64_t blocks = 8 * cdiv(a.R, 8) * a.B * a.tiles;
   if (blocks > 0x7FFFFFFF) return fail(LNG_E_ARG, "surrogate_grad: too many blocks");
+  if constexpr (sizeof(TM) == 2 && !EXACT) {
+    if (D == 128 && a.bits == 4 && (a.order == 2 || a.order == 3)) {
+      // 8 routes a block at order 2 (their table blocks: 512 KB), 4 at order 3 (4 MB, one XCD's L2)
+      // order 2: 8 routes x 32 windows a block (their table blocks: 512 KB; the logits and gradients
+      // of 8 routes fill whole 128 B lines); order 3: one route x 128 windows (its 1 MB block of
+      // the table stays in the XCD's L2, where four routes' blocks were evicted by the streams)
+      const int rg = a.order == 2 ? 8 : 1, win = a.order == 2 ? 256 : 128;
+      SgArgs ap = a;
+      ap.tiles = cdiv(a.T, win / rg - (a.order - 1));
+      const int64_t pblocks = 8 * cdiv(cdiv(a.R, rg), 8) * a.B * ap.tiles;
+      if (pblocks > 0x7FFFFFFF) return fail(LNG_E_ARG, "surrogate_grad: too many blocks");
+      if (a.order == 2)
+        k_surrogate_grad_pk<2, 8, 256><<<pblocks, 256, 0, s>>>(ap);
+      else
+        k_surrogate_grad_pk<3, 1, 128><<<pblocks, 256, 0, s>>>(ap);
+      return check_launch("k_surrogate_grad_pk");
+    }
+  }
   switch (D) {
     case 32: k_surrogate_grad<TM, 2, EXACT><<<blocks, 256, 0, s>>>(a); break;
     case 64: k_surrogate_grad<TM, 4, EXACT><<<blocks, 256, 0, s>>>(a); break;
