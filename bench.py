@@ -300,6 +300,46 @@ def _draft_run(g, spec, fc, parent, res, res_new, res_path, res_len, host, w, it
         out[case] = {"median_us": float(np.median(wall)), "p99_us": float(np.percentile(wall, 99)),
                      "gpu_median_us": float(np.median(gpu)), "accepted": k - 1}
         g.tree_error()            # the one-launch tree's error word is sticky: raises if any step's wait ran out
+    # the draft + verify-gather step on its own (the tree with its verification route tokens, left on
+    # the device for the verifier): the tree launch replayed from its graph, GPU and wall time
+    g.tree_step(spec, route_tokens=True, graph=True)
+    torch.cuda.synchronize()
+    wall, gpu = [], []
+    for i in range(warmup + iters):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        g.tree_step(spec, route_tokens=True, graph=True)
+        e1.record(stream)
+        stream.synchronize()
+        el = time.perf_counter() - t0
+        if i >= warmup:
+            wall.append(el * 1e6)
+            gpu.append(e0.elapsed_time(e1) * 1e3)
+    g.tree_error()
+    wall_e, gpu_e = [], []
+    for i in range(warmup + iters):   # the same launch issued directly (no graph)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        e0.record(stream)
+        g.tree_step(spec, route_tokens=True)
+        e1.record(stream)
+        stream.synchronize()
+        el = time.perf_counter() - t0
+        if i >= warmup:
+            wall_e.append(el * 1e6)
+            gpu_e.append(e0.elapsed_time(e1) * 1e3)
+    g.tree_error()
+    out["draft_verify_gather"] = {"median_us": float(np.median(wall)), "p99_us": float(np.percentile(wall, 99)),
+                                  "gpu_median_us": float(np.median(gpu)),
+                                  "direct_launch": {"median_us": float(np.median(wall_e)),
+                                                    "p99_us": float(np.percentile(wall_e, 99)),
+                                                    "gpu_median_us": float(np.median(gpu_e))},
+                                  "note": "the 16-node tree and its verification route tokens [16, 182, 256] on the "
+                                          "device (one launch, replayed from a graph), without the verifier stand-in, "
+                                          "the acceptance and the host copy of the all_accept / reject_at_root steps"}
     e_bytes = w.vocab * w.d_model * 2
     alg = 4 * e_bytes + n * w.routes * 2 * w.mem_dim * 2 * 2 + 10 * w.routes * 2 * w.mem_dim * 2
     med = out["all_accept"]["gpu_median_us"]

@@ -34,6 +34,12 @@ constexpr int FR_DT = 256;         // route token dim (2 orders x 128)
 constexpr int FR_LD = FR_DT + 16;
 constexpr int FR_MAXR = 256;       // max routes (row-index slots per token)
 constexpr int FR_RQ = FR_MAXR / 4;
+// Token t's 32-row LDS region starts at fr_tok(t) elements: regions 256 B apart beyond their
+// size, skewed by 128 (t & 1) + 16 ((t >> 1) & 1) bytes, so the phases that touch several tokens'
+// regions in one LDS pass (the query-key products, 8-byte stores of 4 tokens x 4 heads; the value
+// operands, 16-byte reads of 2 tokens x 4 heads) spread over distinct bank groups.
+constexpr int FR_TS = 32 * (FR_DT + 16) + 128;  // elements per token region (row length 544 B)
+__device__ __forceinline__ int fr_tok(int t) { return t * FR_TS + 64 * (t & 1) + 8 * ((t >> 1) & 1); }
 // packed KV weight (bf16 elements): keys [h 4][ft 16][ks 2][lane 64][8] = Wk^T[h][16ft + lane%16][32ks + 8(lane/16) ..+8],
 // then values [h 4][dt 4][ks 8][lane 64][8] = Wv[h][16dt + lane%16][32ks + 8(lane/16) ..+8]
 constexpr int FR_PK_V = 4 * 16 * 2 * 64 * 8;
@@ -93,8 +99,10 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
                                                           const bf16* __restrict__ kv_pack,
                                                           const bf16* __restrict__ w_mem, float eps, float scale,
                                                           float sink, bf16* __restrict__ head_out) {
-  __shared__ __attribute__((aligned(16))) bf16 xs[FR_TOK][32][FR_LD];
-  __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][4][FR_RQ];
+  __shared__ __attribute__((aligned(16))) bf16 xs_lds[FR_TOK * FR_TS];
+  __shared__ __attribute__((aligned(16))) int32_t rowsh[FR_TOK][2][4][FR_RQ + 4];  // rows 272 B apart
+  // element (row, c) of token t's region (see fr_tok)
+  auto XS = [&](int t, int row, int c) -> bf16& { return xs_lds[fr_tok(t) + row * FR_LD + c]; };
   __shared__ __attribute__((aligned(16))) bf16 wms[FR_DT];
   __shared__ float qscale[FR_TOK];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -223,7 +231,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   auto stash = [&](const u32x4 (&g)[16]) {
 #pragma unroll
     for (int m = 0; m < 16; ++m)
-      *reinterpret_cast<u32x4*>(&xs[w][4 * (m >> 1) + g_sub][(m & 1) * 128 + 8 * g_piece]) = g[m];
+      *reinterpret_cast<u32x4*>(&XS(w, 4 * (m >> 1) + g_sub, (m & 1) * 128 + 8 * g_piece)) = g[m];
   };
 
   u32x4 g[16];
@@ -251,7 +259,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
       bf16x4 o;
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = static_cast<bf16>(d[i] * to_f32(wm4[i]) * sc_t);
-      *reinterpret_cast<bf16x4*>(&xs[4 * tt + (li >> 2)][a_hg][f]) = o;
+      *reinterpret_cast<bf16x4*>(&XS(4 * tt + (li >> 2), a_hg, f)) = o;
     }
   }
   __syncthreads();
@@ -259,7 +267,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
   // ---------------- phase B: one token per wave
   bf16x8 qb[8];
 #pragma unroll
-  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][li][fr_col(lg, kk)]);
+  for (int kk = 0; kk < 8; ++kk) qb[kk] = *reinterpret_cast<const bf16x8*>(&XS(w, li, fr_col(lg, kk)));
 
   float m_run = sink, l_part = 0.f;
   f32x4 acc[16];
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
     for (int tt = 0; tt < 2; ++tt) {
       bf16x8 x[8];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) x[kk] = *reinterpret_cast<const bf16x8*>(&xs[w][16 * tt + li][fr_col(lg, kk)]);
+      for (int kk = 0; kk < 8; ++kk) x[kk] = *reinterpret_cast<const bf16x8*>(&XS(w, 16 * tt + li, fr_col(lg, kk)));
       float ss = 0.f;
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) ss = sumsq8(x[kk], ss);
@@ -336,9 +344,9 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
     for (int ft = 0; ft < 16; ++ft) {
       const int col = 16 * ft + 4 * (li & 3);
       const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-          (__attribute__((address_space(3))) bf16x4*)(&xs[w][4 * lg + (li >> 2)][col]));
+          (__attribute__((address_space(3))) bf16x4*)(&XS(w, 4 * lg + (li >> 2), col)));
       const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-          (__attribute__((address_space(3))) bf16x4*)(&xs[w][16 + 4 * lg + (li >> 2)][col]));
+          (__attribute__((address_space(3))) bf16x4*)(&XS(w, 16 + 4 * lg + (li >> 2), col)));
       const bf16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
       acc[ft] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b, acc[ft], 0, 0, 0);
     }
@@ -369,7 +377,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
     const int f = 16 * ft + li;
     const float wm = to_f32(wms[f]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) xs[w][4 * lg + i][f] = static_cast<bf16>(acc[ft][i] * iD[i] * wm);
+    for (int i = 0; i < 4; ++i) XS(w, 4 * lg + i, f) = static_cast<bf16>(acc[ft][i] * iD[i] * wm);
   }
   __syncthreads();
 
@@ -380,7 +388,7 @@ __global__ __launch_bounds__(64 * FR_TOK, 8 / FR_TOK) void k_readout_fused(const
     bf16x8 ub[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      ub[ks] = *reinterpret_cast<const bf16x8*>(&xs[4 * tt + (li >> 2)][c_hg][32 * ks + 8 * lg]);
+      ub[ks] = *reinterpret_cast<const bf16x8*>(&XS(4 * tt + (li >> 2), c_hg, 32 * ks + 8 * lg));
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       f32x4 d = {0.f, 0.f, 0.f, 0.f};
