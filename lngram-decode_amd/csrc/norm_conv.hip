@@ -645,14 +645,8 @@ int lng_causal_conv_rowsq(const void* mixed, const float* rowsq, int32_t n_parti
   const bf16* nw = static_cast<const bf16*>(norm_w);
   const bf16* cw = static_cast<const bf16*>(conv_w);
   bf16* o = static_cast<bf16*>(out);
-  static const int sl = getenv("LNG_CONV_SL") ? atoi(getenv("LNG_CONV_SL")) : 16;  // EXPERIMENT
-  int rc;
-  if (sl == 32)
-    rc = launch_conv_stream<32>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
-  else if (sl == 24)
-    rc = launch_conv_stream<24>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
-  else
-    rc = launch_conv_stream<CS_SL>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
+  const int rc =
+      launch_conv_stream<CS_SL>(mx, rowsq, n_partials, nw, cw, B, T, d, eps, residual != 0, o, as_stream(stream));
   if (rc) return rc;
   return check_launch("causal_conv_rowsq");
 }
