@@ -84,7 +84,7 @@ __device__ __forceinline__ float sumsq8(const bf16x8 v, float acc) {
   return acc;
 }
 
-// LDS (TOK = 8: 152.5 KB, one block per CU; TOK = 4: 76.3 KB, two blocks per CU): per wave a
+// LDS (TOK = 8: 159,264 B, one block per CU; TOK = 4: 79,888 B, two blocks per CU): per wave a
 // 32-row region reused as qkw (rows 0..15, phase A -> B), the route chunk (rows 0..31, phase B)
 // and u (rows 0..15, phase B -> C); per wave the token's row indices [order][route parity]
 // [route / 2] (-1 = zero row); the memory-norm weight.

@@ -313,9 +313,9 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
 }
 
 // The approximate mode for bf16 rows of 128 and 4-bit codes (the SB layer's lookup), orders 2 and
-// 3: the same windows, scores and output sums as k_surrogate_grad over tiles of 128 windows (8 per
-// 16-lane group, halving the blocks and their fixed staging and output phases), with the tile's digits and
-// window validity staged in LDS once per block (one coalesced load each, instead of order
+// 3: the same windows, scores and output sums as k_surrogate_grad over blocks of SP_WIN windows
+// (SP_WIN / 16 per 16-lane group, fewer blocks and fewer fixed staging and output phases than
+// 64-window tiles), with the tile's digits and window validity staged in LDS once per block (one coalesced load each, instead of order
 // scattered code loads per window on each window's critical path) and the windows of a 16-lane
 // group pipelined two deep: window i + 1's memory-gradient, looked-up and counterfactual rows are
 // requested before window i's dot products are reduced.
@@ -492,7 +492,6 @@ static int sg_launch_v(const SgArgs& a, int64_t D, hipStream_t s) {
   if (blocks > 0x7FFFFFFF) return fail(LNG_E_ARG, "surrogate_grad: too many blocks");
   if constexpr (sizeof(TM) == 2 && !EXACT) {
     if (D == 128 && a.bits == 4 && (a.order == 2 || a.order == 3)) {
-      // 8 routes a block at order 2 (their table blocks: 512 KB), 4 at order 3 (4 MB, one XCD's L2)
       // order 2: 8 routes x 32 windows a block (their table blocks: 512 KB; the logits and gradients
       // of 8 routes fill whole 128 B lines); order 3: one route x 128 windows (its 1 MB block of
       // the table stays in the XCD's L2, where four routes' blocks were evicted by the streams)
