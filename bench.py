@@ -512,6 +512,54 @@ def decode_step(dev, iters: int, warmup: int):
     return run
 
 
+def tree_verify_step(dev, iters: int, warmup: int):
+    """Set up, and return the timing run of, the memory block of draft-tree verification at the SB
+    layer shape: one sequence with 2048 cached positions takes the 16 nodes of a draft tree (the
+    nodes' router codes, their n-gram rows along their ancestors, the fused readout over those rows,
+    the output projection into the conv cache and the conv over each node's ancestor window).  Eager
+    launches, device synchronisation per step; the cached length stays 2048."""
+    import numpy as np
+    import torch
+
+    from drafting.tree import tree16
+    from ffnmem.infer import DecodeState, memory_codes, memory_model, memory_step, tree_memory_step
+    from lngram_hip import ops, workloads
+
+    w = workloads.SB.with_shape(1, 2048)
+    ctx, parent = 2048, tree16().parent
+    n = len(parent)
+    mem = workloads.build_memory(w, seed=0, device=dev)
+    model = memory_model(mem)
+    h = workloads.make_hidden(w.with_shape(1, ctx + n), seed=1, device=dev)
+    h_norm = ops.rmsnorm(h, torch.ones(w.d_model, dtype=w.dtype, device=dev), w.norm_eps)
+    st = DecodeState.empty(model, 1, ctx + n)
+    with torch.no_grad():
+        memory_step(model, 0, st, h[:, :ctx], memory_codes(model, 0, st, h_norm=h_norm[:, :ctx]))
+    st.length = ctx
+    hn, hnn = h[:, ctx:].contiguous(), h_norm[:, ctx:].contiguous()
+
+    def step():
+        return tree_memory_step(model, 0, st, hn, memory_codes(model, 0, st, h_norm=hnn), parent)
+
+    def run() -> dict:
+        times = []
+        with torch.no_grad():
+            for i in range(warmup + iters):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                step()
+                torch.cuda.synchronize()
+                if i >= warmup:
+                    times.append((time.perf_counter() - t0) * 1e6)
+        return {"workload": f"SB-shape memory layer, draft-tree verification: 1 sequence, {n}-node tree after {ctx} "
+                            "cached positions (node codes, ancestor-window rows, fused readout over them, o-proj "
+                            "into the conv cache, conv over ancestor windows)",
+                "unit": "us per tree", "iters": iters, "eager_median_us": float(np.median(times)),
+                "p99_us": float(np.percentile(times, 99))}
+
+    return run
+
+
 def serving_step(dev, iters: int, warmup: int):
     """Set up, and return the timing run of, decoding from host RAM at the SB shape: 8 sequences with
     2048 cached positions each take one new token, the rows coming from a serving-layout copy of the
@@ -877,6 +925,9 @@ def main() -> None:
     if not args.no_draft:
         log("cached decode step: set-up")
         legs["decode_step"] = decode_step(dev, args.draft_iters, 20)
+    if not args.no_draft:
+        log("draft-tree verification memory block: set-up")
+        legs["tree_verify_step"] = tree_verify_step(dev, args.draft_iters // 2, 10)
     if not args.no_draft:
         log("host-RAM serving step: set-up")
         legs["serving_step"] = serving_step(dev, args.draft_iters // 2, 10)

@@ -196,6 +196,17 @@ int lng_causal_conv_at(const void* rows, const void* norm_w, const void* conv_w,
                        int64_t len, int64_t pos0, const int32_t* pos0_dev, int64_t n, int32_t d, int32_t K,
                        int32_t dilation, float eps, int residual, void* out, void* stream);
 
+/* The same convolution with each output's window given as rows of the cache: the ancestor-window
+ * conv of a draft tree's verification (drafting/tree.py:186-194, over the slots of tree_slots
+ * :96-111).  slots [n, back + 1] (device int32, back = (K - 1) * dilation, oldest first): output
+ * (b, i) reads tap j from row slots[i][j * dilation] of sequence b of rows [B, stride, d] and its
+ * residual from row slots[i][back]; a slot outside [0, len) is a zero row (the left padding).
+ * out [B, n, d].  Each shape runs the arithmetic of the kernel lng_causal_conv_at runs for it, so an
+ * output equals the sequence conv's at a position whose window holds the same rows. */
+int lng_causal_conv_slots(const void* rows, const void* norm_w, const void* conv_w, int dtype, int64_t B,
+                          int64_t stride, int64_t len, const int32_t* slots, int64_t n, int32_t back, int32_t d,
+                          int32_t K, int32_t dilation, float eps, int residual, void* out, void* stream);
+
 /* bf16 y[M,N] = x[M,K] . w[N,K]^T (K % 32 == 0) that also writes the RMSNorm
  * statistics of its bf16 output rows for the following short conv: rowsq[p*M + m]
  * holds partial sums of squares, p < lng_linear_rowsq_partials(N).  readout_o_proj
@@ -391,6 +402,14 @@ int lng_ssm_scan(const float* a, const float* u, const float* s0, int64_t B, int
  * (ffnmem/memory/router.py:58), for lng_router_codes_ids. */
 int lng_ssm_scan_with_bf16(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N,
                            void* workspace, size_t workspace_bytes, float* s, void* s_bf16, void* stream);
+
+/* The SSM states of a draft tree's nodes (the parent-ordered recurrence of tree_verify_step,
+ * drafting/tree.py:153-161): s[b, i] = a * s[b, parent[i]] + (1 - a) * u[b, i] for the n nodes in
+ * index order, with lng_ssm_scan's step, so a node's state equals the scan's along its root path.
+ * parent [n] (device int32); a parent outside [0, i) -- the root's -1 -- continues from
+ * s_root [B, N] (the state before the tree), or from zero when s_root is null.  u, s [B, n, N]. */
+int lng_ssm_tree(const float* a, const float* u, const float* s_root, const int32_t* parent, int64_t B, int32_t n,
+                 int32_t N, float* s, void* stream);
 
 /* lng_ssm_scan with the wait for predecessor records bounded by `spin_limit` short sleeps per tile
  * (lng_ssm_scan uses a bound far past any real wait; 0 never waits, so every tile whose

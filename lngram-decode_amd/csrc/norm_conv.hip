@@ -700,6 +700,203 @@ static int conv_launch(const void* mixed, const void* norm_w, const void* conv_w
   return check_launch("causal_conv");
 }
 
+// ---------------------------------------------------------------- the conv over listed rows
+// The short conv with each output's window given as row indices instead of a position range:
+// output (b, i) reads tap j from row slots[i * (back + 1) + j * dil] of sequence b and its
+// residual from row slots[i * (back + 1) + back], back = (K - 1) * dil, oldest first (a draft
+// tree's ancestor windows, drafting/tree.py:186-194).  A slot outside [0, len) is a zero row (the
+// left padding).  Each shape runs the arithmetic of the sequence kernel that conv_launch picks for
+// it, so an output equals the sequence conv's at a position whose window holds the same rows.
+
+__device__ __forceinline__ int64_t slot_row(const int32_t* slots, int64_t i, int back, int k, int64_t len) {
+  const int32_t s = slots[i * (back + 1) + k];
+  return (s >= 0 && s < len) ? s : -1;
+}
+
+// bf16, kernel 4, dilation 3: k_causal_conv_k4d3_fused's thread layout, row sums (dot products per
+// lane, 16-lane DPP sums, 16-lane groups in LDS in order) and tap pairs.  Block (i, b), d/4
+// threads of 4 channels (rounded up to whole waves).
+__global__ __launch_bounds__(512) void k_conv_k4d3_slots_bf16(const bf16* __restrict__ rows,
+                                                              const bf16* __restrict__ norm_w,
+                                                              const bf16* __restrict__ conv_w,
+                                                              const int32_t* __restrict__ slots, int64_t stride,
+                                                              int64_t len, int64_t n, uint32_t d4, float eps,
+                                                              int residual, bf16* __restrict__ out) {
+  __shared__ float part[CF_MAXG][4];
+  __shared__ float srow[4];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int ngrp = static_cast<int>(blockDim.x >> 4);
+  const int64_t i = blockIdx.x, b = blockIdx.y;
+  const uint32_t d = d4 * 4u;
+  const bool active = static_cast<uint32_t>(tid) < d4;
+  const uint32_t c = (active ? static_cast<uint32_t>(tid) : 0u) * 4u;
+  int64_t rw[4];
+  uint2 x[4];  // channels c .. c+3 of the rows of taps 0..3 (zero for a padding slot)
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    rw[k] = slot_row(slots, i, CF_HALO, 3 * k, len);
+    x[k] = rw[k] >= 0 ? *reinterpret_cast<const uint2*>(rows + (b * stride + rw[k]) * d + c) : uint2{0u, 0u};
+  }
+  const uint2 nwv = *reinterpret_cast<const uint2*>(norm_w + c);
+  const uint4 cw01 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(c) * 4);
+  const uint4 cw23 = *reinterpret_cast<const uint4*>(conv_w + static_cast<size_t>(c) * 4 + 8);
+  const float live = active ? 1.f : 0.f;
+  float ss[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float a = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x[k].x),
+                                                    __builtin_bit_cast(bf16x2, x[k].x), 0.f, false);
+    ss[k] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x[k].y), __builtin_bit_cast(bf16x2, x[k].y), a,
+                                            false) * live;
+  }
+  row16_sums(ss);
+  if ((lane & 15) == 0) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) part[tid >> 4][k] = ss[k];
+  }
+  __syncthreads();
+  if (tid < 4) {
+    float s = 0.f;
+    for (int g = 0; g < ngrp; ++g) s += part[g][tid];
+    srow[tid] = rw[tid] < 0 ? 0.f : 1.0f / sqrtf(s / static_cast<float>(d) + eps);
+  }
+  __syncthreads();
+  if (!active) return;
+  const float nw[4] = {lo_f(nwv.x), hi_f(nwv.x), lo_f(nwv.y), hi_f(nwv.y)};
+  const uint32_t wa[4] = {cw01.x, cw01.z, cw23.x, cw23.z};
+  const uint32_t wb[4] = {cw01.y, cw01.w, cw23.y, cw23.w};
+  float yn[4][4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float s = srow[k];
+    const float xf[4] = {lo_f(x[k].x), hi_f(x[k].x), lo_f(x[k].y), hi_f(x[k].y)};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) yn[k][j] = xf[j] * s * nw[j];
+  }
+  float y[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a = __builtin_amdgcn_fdot2_f32_bf16(pk2(yn[0][j], yn[1][j]), __builtin_bit_cast(bf16x2, wa[j]), 0.f,
+                                                    false);
+    y[j] = __builtin_amdgcn_fdot2_f32_bf16(pk2(yn[2][j], yn[3][j]), __builtin_bit_cast(bf16x2, wb[j]), a, false);
+  }
+  const uint32_t yp0 = __builtin_bit_cast(uint32_t, pk2(y[0], y[1]));
+  const uint32_t yp1 = __builtin_bit_cast(uint32_t, pk2(y[2], y[3]));
+  const float yr[4] = {lo_f(yp0), hi_f(yp0), lo_f(yp1), hi_f(yp1)};
+  float act[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float e = __builtin_amdgcn_exp2f(-yr[j] * 1.4426950408889634f);
+    act[j] = yr[j] * __builtin_amdgcn_rcpf(1.0f + e);
+  }
+  uint2 o;
+  if (residual) {
+    const float xs[4] = {lo_f(x[3].x), hi_f(x[3].x), lo_f(x[3].y), hi_f(x[3].y)};
+    const uint32_t ap0 = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+    const uint32_t ap1 = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+    o.x = __builtin_bit_cast(uint32_t, pk2(xs[0] + lo_f(ap0), xs[1] + hi_f(ap0)));
+    o.y = __builtin_bit_cast(uint32_t, pk2(xs[2] + lo_f(ap1), xs[3] + hi_f(ap1)));
+  } else {
+    o.x = __builtin_bit_cast(uint32_t, pk2(act[0], act[1]));
+    o.y = __builtin_bit_cast(uint32_t, pk2(act[2], act[3]));
+  }
+  *reinterpret_cast<uint2*>(out + (b * n + i) * d + c) = o;
+}
+
+// Other shapes: K4D3 = k_causal_conv_k4d3<T>'s row sums (8 consecutive elements a lane, 512 apart)
+// and tap order; otherwise k_causal_conv<T>'s (one element a lane, 64 apart).  Block (i, b) of 256
+// threads; a wave per tap row for the row scales, then the threads sweep the channels.
+template <typename T, bool K4D3>
+__global__ __launch_bounds__(256) void k_conv_slots(const T* __restrict__ rows, const T* __restrict__ norm_w,
+                                                    const T* __restrict__ conv_w, const int32_t* __restrict__ slots,
+                                                    int64_t stride, int64_t len, int64_t n, int32_t d, int32_t K,
+                                                    int32_t dil, float eps, int residual, T* __restrict__ out) {
+  extern __shared__ float tap_scale[];  // [K]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t i = blockIdx.x, b = blockIdx.y;
+  const int back = (K - 1) * dil;
+  const T* base = rows + b * stride * d;
+  for (int k = wave; k < K; k += 4) {
+    const int64_t r = slot_row(slots, i, back, k * dil, len);
+    float sc = 0.f;
+    if (r >= 0) {
+      float ss = 0.f;
+      if (K4D3) {
+        for (int c = lane * 8; c < d; c += 64 * 8) {
+          float v[8];
+          load8(base + r * d + c, v);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) ss = fmaf(v[j], v[j], ss);
+        }
+      } else {
+        for (int c = lane; c < d; c += 64) {
+          const float v = to_f32(base[r * d + c]);
+          ss = fmaf(v, v, ss);
+        }
+      }
+      ss = wave_sum(ss);
+      sc = 1.0f / sqrtf(ss / static_cast<float>(d) + eps);
+    }
+    if (lane == 0) tap_scale[k] = sc;
+  }
+  __syncthreads();
+  const int64_t self = slot_row(slots, i, back, back, len);
+  for (int c = threadIdx.x; c < d; c += blockDim.x) {
+    const float nw = to_f32(norm_w[c]);
+    float acc = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int64_t r = slot_row(slots, i, back, k * dil, len);
+      const float xn = r >= 0 ? norm_elem<T, true>(to_f32(base[r * d + c]), tap_scale[k], nw) : 0.f;
+      if (K4D3)
+        acc = k == 0 ? to_f32(conv_w[c * K]) * xn : fmaf(to_f32(conv_w[c * K + k]), xn, acc);
+      else if (r >= 0)
+        acc = fmaf(to_f32(conv_w[c * K + k]), xn, acc);
+    }
+    const float y = round_to<T>(acc);
+    const float act = round_to<T>(y / (1.0f + expf(-y)));
+    const float xs = self >= 0 ? to_f32(base[self * d + c]) : 0.f;
+    out[(b * n + i) * d + c] = residual ? from_f32<T>(xs + act) : from_f32<T>(act);
+  }
+}
+
+static int conv_slots_launch(const void* rows, const void* norm_w, const void* conv_w, int dtype, int64_t B,
+                             int64_t stride, int64_t len, const int32_t* slots, int64_t n, int32_t d, int32_t K,
+                             int32_t dil, float eps, int residual, void* out, hipStream_t s) {
+  const dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>(B));
+  // the same shape tests as conv_launch, in the same order
+  if (K == 4 && dil == 3 && d % 4 == 0 && d <= 2048 && dtype == LNG_BF16 && len < INT32_MAX) {
+    const int threads = static_cast<int>(cdiv(d / 4, 64) * 64);
+    hipLaunchKernelGGL(k_conv_k4d3_slots_bf16, grid, dim3(threads), 0, s, static_cast<const bf16*>(rows),
+                       static_cast<const bf16*>(norm_w), static_cast<const bf16*>(conv_w), slots, stride, len, n,
+                       static_cast<uint32_t>(d / 4), eps, residual, static_cast<bf16*>(out));
+    return check_launch("causal_conv_slots_k4d3_bf16");
+  }
+  const bool k4d3 = K == 4 && dil == 3 && d % 8 == 0;
+  const size_t lds = sizeof(float) * K;
+  if (dtype == LNG_F32) {
+    const float *x = static_cast<const float*>(rows), *nw = static_cast<const float*>(norm_w),
+                *cw = static_cast<const float*>(conv_w);
+    if (k4d3)
+      hipLaunchKernelGGL((k_conv_slots<float, true>), grid, dim3(256), lds, s, x, nw, cw, slots, stride, len, n, d, K,
+                         dil, eps, residual, static_cast<float*>(out));
+    else
+      hipLaunchKernelGGL((k_conv_slots<float, false>), grid, dim3(256), lds, s, x, nw, cw, slots, stride, len, n, d, K,
+                         dil, eps, residual, static_cast<float*>(out));
+  } else if (dtype == LNG_BF16) {
+    const bf16 *x = static_cast<const bf16*>(rows), *nw = static_cast<const bf16*>(norm_w),
+               *cw = static_cast<const bf16*>(conv_w);
+    if (k4d3)
+      hipLaunchKernelGGL((k_conv_slots<bf16, true>), grid, dim3(256), lds, s, x, nw, cw, slots, stride, len, n, d, K,
+                         dil, eps, residual, static_cast<bf16*>(out));
+    else
+      hipLaunchKernelGGL((k_conv_slots<bf16, false>), grid, dim3(256), lds, s, x, nw, cw, slots, stride, len, n, d, K,
+                         dil, eps, residual, static_cast<bf16*>(out));
+  } else {
+    return fail(LNG_E_DTYPE, "causal_conv_slots: dtype must be f32 or bf16");
+  }
+  return check_launch("causal_conv_slots");
+}
+
 }  // namespace lng
 
 extern "C" {
@@ -723,6 +920,21 @@ int lng_causal_conv_at(const void* rows, const void* norm_w, const void* conv_w,
   if (B == 0 || n == 0) return LNG_OK;
   const ConvWin W{stride, len, pos0, n, pos0_dev};
   return conv_launch(rows, norm_w, conv_w, dtype, B, W, d, K, dilation, eps, residual, out, as_stream(stream));
+}
+
+int lng_causal_conv_slots(const void* rows, const void* norm_w, const void* conv_w, int dtype, int64_t B,
+                          int64_t stride, int64_t len, const int32_t* slots, int64_t n, int32_t back, int32_t d,
+                          int32_t K, int32_t dilation, float eps, int residual, void* out, void* stream) {
+  if (B < 0 || n < 0 || d <= 0 || K <= 0 || dilation <= 0 || len < 0 || stride < len)
+    return fail(LNG_E_ARG, "causal_conv_slots: bad shape");
+  if (back != (K - 1) * dilation) return fail(LNG_E_ARG, "causal_conv_slots: back must be (K - 1) * dilation");
+  if (B > 65535 || n > 0x7FFFFFFF) return fail(LNG_E_ARG, "causal_conv_slots: B <= 65535 sequences");
+  if (K > 64) return fail(LNG_E_ARG, "causal_conv_slots: kernel size at most 64");
+  if (rows == out) return fail(LNG_E_ARG, "causal_conv_slots: out must not alias the rows");
+  if (B == 0 || n == 0) return LNG_OK;
+  if (!slots) return fail(LNG_E_ARG, "causal_conv_slots: null slots");
+  return conv_slots_launch(rows, norm_w, conv_w, dtype, B, stride, len, slots, n, d, K, dilation, eps, residual, out,
+                           as_stream(stream));
 }
 
 int lng_row_sumsq(const void* x, int64_t rows, int32_t d, float* rowsq, void* stream) {

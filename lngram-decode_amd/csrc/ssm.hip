@@ -368,11 +368,47 @@ static int scratch_of_current_device(uint8_t** ptr, int* dev) {
   return LNG_OK;
 }
 
+// The states of a draft tree's nodes (drafting/tree.py:153-161): node i continues from its parent's
+// state, s[b, i] = a * s[b, parent[i]] + (1 - a) * u[b, i] with k_ssm_scan's step (one fmaf over
+// a and (1 - a) * u), so a node's state equals the scan's along its root path.  A parent outside
+// [0, i) (the root's -1) continues from s_root[b] (the state before the tree), or from zero when
+// s_root is null.  One thread per (sequence, channel); the nodes run in index order, each reading
+// back the parent state it wrote itself.
+__global__ __launch_bounds__(256) void k_ssm_tree(const float* __restrict__ a, const float* __restrict__ u,
+                                                  const float* __restrict__ s_root, const int32_t* __restrict__ parent,
+                                                  int64_t B, int32_t n, int32_t N, float* __restrict__ s) {
+  const int64_t g = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (g >= B * N) return;
+  const int64_t b = g / N;
+  const int c = static_cast<int>(g - b * N);
+  const float av = a[c], bv = 1.0f - av;
+  const float s0 = s_root ? s_root[b * N + c] : 0.f;
+  const float* ub = u + b * n * N + c;
+  float* sb = s + b * n * N + c;
+  for (int32_t i = 0; i < n; ++i) {
+    const int32_t p = parent[i];
+    const float sp = (p >= 0 && p < i) ? sb[static_cast<int64_t>(p) * N] : s0;
+    sb[static_cast<int64_t>(i) * N] = fmaf(av, sp, bv * ub[static_cast<int64_t>(i) * N]);
+  }
+}
+
 }  // namespace lng
 
 using namespace lng;
 
 extern "C" {
+
+int lng_ssm_tree(const float* a, const float* u, const float* s_root, const int32_t* parent, int64_t B, int32_t n,
+                 int32_t N, float* s, void* stream) {
+  if (B < 0 || n < 0 || N <= 0) return fail(LNG_E_ARG, "ssm_tree: bad shape");
+  if (B * n == 0) return LNG_OK;
+  if (!a || !u || !parent || !s) return fail(LNG_E_ARG, "ssm_tree: null pointer");
+  if (s == u) return fail(LNG_E_ARG, "ssm_tree: s must not alias u");
+  const int64_t threads = B * N;
+  hipLaunchKernelGGL(k_ssm_tree, dim3(static_cast<unsigned>(cdiv(threads, 256))), dim3(256), 0, as_stream(stream), a,
+                     u, s_root, parent, B, n, N, s);
+  return check_launch("ssm_tree");
+}
 
 int lng_ssm_scan_static(const float* a, const float* u, const float* s0, int64_t B, int64_t T, int32_t N, float* s,
                         void* stream) {

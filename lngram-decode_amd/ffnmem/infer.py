@@ -1,7 +1,9 @@
 """Cached decoding of the memory layers: drop-in for the memory half of the reference
 ``ffnmem/infer.py`` (``DecodeState`` :65-112, ``ssm_continue`` :125-137, ``router_input_at``
-:140-149, ``memory_step`` :152-182) and for the memory part of ``static_verify``
-(``drafting/live_spec.py:68-139``).
+:140-149, ``memory_step`` :152-182), for the memory part of ``static_verify``
+(``drafting/live_spec.py:68-139``) and for the memory block of draft-tree verification
+(``tree_verify_step``, ``drafting/tree.py:141-202``: ``tree_ssm_states``, ``tree_router_input``,
+``tree_memory_step``).
 
 The caches hold, per memory layer, the route codes of every processed position (uint8,
 ``[B, max_len, R]``) and the short conv's input rows (``[B, max_len, d]``), indexed by absolute
@@ -136,9 +138,8 @@ def _skinny_ok(x: Tensor, w: Tensor) -> bool:
             and x.shape[-1] % 32 == 0 and w.shape[0] % 16 == 0)
 
 
-def _finish_cached(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tensor | None) -> Tensor:
-    """``mixed = W_o head``, cached as conv input at positions L .. L+n-1 (+ L_dev), then
-    ``mixed + short_conv`` over the cached window (``infer.py:175-182``)."""
+def _oproj_to_cache(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tensor | None) -> None:
+    """``mixed = W_o head``, cached as conv input at positions L .. L+n-1 (+ L_dev)."""
     b = head.shape[0]
     x = head.reshape(b, n, m.readout_inner_dim)
     w_o = m.readout_o_proj.weight
@@ -154,6 +155,13 @@ def _finish_cached(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tens
             conv_in[:, L:L + n] = mixed
         else:
             conv_in.index_copy_(1, L_dev.long() + torch.arange(n, device=x.device), mixed.to(conv_in.dtype))
+
+
+def _finish_cached(m, head: Tensor, conv_in: Tensor, L: int, n: int, L_dev: Tensor | None) -> Tensor:
+    """``mixed = W_o head``, cached as conv input at positions L .. L+n-1 (+ L_dev), then
+    ``mixed + short_conv`` over the cached window (``infer.py:175-182``)."""
+    _oproj_to_cache(m, head, conv_in, L, n, L_dev)
+    conv = m.short_conv
     length = L + n if L_dev is None else conv_in.shape[1]
     return ops.causal_conv_at(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps,
                               pos0=L, n=n, length=length, pos0_dev=L_dev, residual=True)
@@ -164,9 +172,9 @@ def memory_step(model, pos: int, state: DecodeState, h: Tensor, codes_new: Tenso
     """Memory output ``[B, n, d]`` of the new positions (``infer.py:152-182``); ``codes_new``
     ``[B, n, R]`` are written into the cache.  ``route_codes_ctx [B, n + H, R]`` replaces the
     cached codes for the lookup only (the n-grams ending at the new positions are read from it);
-    as in the reference, the short conv still reads the cached rows in position order, so a
-    draft tree's verification (whose conv follows each node's ancestors, ``tree.py:186-194``) is
-    not this function's.  ``route_tokens [B, n, R, len(ngrams) * mem_dim]`` are rows supplied by
+    as in the reference, the short conv still reads the cached rows in position order.  A draft
+    tree's verification, whose windows and conv follow each node's ancestors
+    (``tree.py:179-196``), is :func:`tree_memory_step`'s.  ``route_tokens [B, n, R, len(ngrams) * mem_dim]`` are rows supplied by
     the caller (the gather is skipped)."""
     mem = model.blocks[pos].memory
     m = mem.module
@@ -247,6 +255,76 @@ def memory_decode(model, pos: int, state: DecodeState, h: Tensor, h_norm: Tensor
     codes = memory_codes(model, pos, state, h_norm=h_norm, router_in=router_in)
     rows = None if row_provider is None else row_provider(pos, state, codes)
     return memory_step(model, pos, state, h, codes, route_codes_ctx, rows)
+
+
+# ------------------------------------------------------------------ draft-tree verification
+def tree_ssm_states(model, state: DecodeState, emb: Tensor, parent) -> Tensor:
+    """SSM states of the tree nodes ``emb [B, n, d]`` after the cached positions
+    (``tree_verify_step``, ``drafting/tree.py:153-161``): each node continues from its parent's
+    state, the root from the cached state at ``L - 1`` (zero at ``L = 0``); ``lng_ssm_tree``.
+    The caller writes them into ``state.ssm`` after the step, as the reference does."""
+    ssm = model.ssm
+    L = state.length
+    root = state.ssm[:, L - 1] if L > 0 else None
+    return ops.ssm_tree(ssm.decay(), ssm.inputs(emb), parent, root)
+
+
+def tree_router_input(model, mem, state: DecodeState, emb: Tensor, s_new: Tensor | None, parent) -> Tensor:
+    """Token-router features of the tree nodes (``drafting/tree.py:170-177``): each node's previous
+    token is its parent's; the root's is the last cached token (``start`` at ``L = 0``)."""
+    feats = mem.router_features
+    b, n, d = emb.shape
+    L = state.length
+    if L > 0:
+        root_prev = model.tok_emb(state.tokens[:, L - 1]).to(emb.dtype)
+    else:
+        root_prev = feats.start.to(emb.dtype).expand(b, d)
+    src = torch.as_tensor([p + 1 for p in parent], dtype=torch.long, device=emb.device)   # 0: the root's
+    prev = torch.cat((root_prev[:, None], emb), 1).index_select(1, src)
+    return feats.step(prev, emb, s_new)
+
+
+def tree_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, parent) -> Tensor:
+    """The memory block of the reference's draft-tree verification (``tree_verify_step``,
+    ``drafting/tree.py:179-196``) for the tree nodes ``h [B, n, d]`` after the ``L = state.length``
+    cached positions.  Each node's n-gram windows follow its ancestors, then the cached history
+    (``tree_ngram_codes`` / ``tree_route_tokens``); the readout runs over those rows; the output
+    projection's rows go into the conv-input cache at ``L .. L+n-1`` in node order and the short
+    conv reads each node's ancestor window of them (``tree_slots``, ``lng_causal_conv_slots``).
+    ``codes [B, n, R]`` are the nodes' route codes (``memory_codes`` over their router inputs) and
+    are cached at ``L .. L+n-1`` too.  Returns ``mixed + short_conv`` ``[B, n, d]``; the caller sets
+    ``state.length`` (after the accepted path is compacted, as the reference's loop does).  Node i's
+    output equals ``memory_step``'s for the last token of a chain decode along its root path."""
+    from drafting.tree import tree_ngram_codes, tree_route_tokens, tree_slots
+
+    mem = model.blocks[pos].memory
+    m = mem.module
+    L, n = state.length, h.shape[1]
+    if len(parent) != n:
+        raise ValueError(f"tree_memory_step: {len(parent)} parents for {n} nodes")
+    if L + n > state.max_len:
+        raise ValueError(f"cache full: {L} + {n} > {state.max_len}")
+    cache = state.codes[pos]
+    hist = m.route_history_length
+    c8 = codes.to(cache.dtype)
+    ctx, valid = tree_ngram_codes(parent, c8, cache[:, max(0, L - hist):L], hist)
+    rt = tree_route_tokens(m, ctx, valid)
+    cache[:, L:L + n] = c8
+    if m._fused_shape_ok(h, tables=False):
+        q_raw = ops.linear(h, m._folded_query_weight())
+        head = ops.memory_readout_fused_rows(q_raw, rt.to(torch.bfloat16), m._fused_weights(),
+                                             m.readout_memory_norm.weight, m.readout_memory_norm.eps, m.softmax_scale,
+                                             m.readout_sink_logit, q_rows=h, q_eps=m.readout_query_norm.eps)
+    else:
+        key, value = m._project_memory(rt.to(m.readout_kv_proj.weight.dtype))
+        head = m._manual_gqa(m._project_query(h), key, value)
+    conv_in = state.conv_in[pos]
+    _oproj_to_cache(m, head, conv_in, L, n, None)
+    conv = m.short_conv
+    slots, ok = tree_slots(parent, L, conv.left_padding)
+    slots = torch.where(ok, slots, torch.full_like(slots, -1))
+    return ops.causal_conv_slots(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps, slots,
+                                 length=L + n, residual=True)
 
 
 # ------------------------------------------------------------------ one memory layer's step

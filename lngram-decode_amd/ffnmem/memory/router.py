@@ -81,16 +81,21 @@ class TokenRouterFeatures(nn.Module):
         return self._tables_cache[1]
 
     def step(self, emb_prev: Tensor | None, emb_cur: Tensor, ssm_state: Tensor | None = None) -> Tensor:
-        """One position (decode / drafter), ``[B, d]`` inputs; ``emb_prev`` None at t = 0.  The kernel
-        runs on the two-position sequence (previous, current) and the last position is kept: its
-        previous-token half reads ``emb_prev`` (at t = 0 the one-position sequence reads ``start``)."""
-        seq = emb_cur[:, None] if emb_prev is None else torch.stack((emb_prev.to(emb_cur.dtype), emb_cur), 1)
+        """Single positions (decode / drafter / tree nodes): ``[..., d]`` inputs, every leading index an
+        independent (previous, current) pair, as the reference's elementwise ``step``
+        (``router.py:61-68``); ``emb_prev`` None at t = 0.  The kernel runs on each two-position
+        sequence (previous, current) and the last position is kept: its previous-token half reads
+        ``emb_prev`` (at t = 0 the one-position sequence reads ``start``)."""
+        lead, d = emb_cur.shape[:-1], emb_cur.shape[-1]
+        cur = emb_cur.reshape(-1, d)
+        seq = cur[:, None] if emb_prev is None else torch.stack((emb_prev.reshape(-1, d).to(cur.dtype), cur), 1)
         s = None
         if self.kind == "embed2_ssm":
             if ssm_state is None:
                 raise ValueError("embed2_ssm router needs the SSM state")
-            s = ssm_state[:, None].expand(-1, seq.shape[1], -1)
-        return self._features(seq, s)[:, -1]
+            s = ssm_state.reshape(cur.shape[0], -1)[:, None].expand(-1, seq.shape[1], -1)
+        out = self._features(seq, s)[:, -1]
+        return out.reshape(*lead, out.shape[-1])
 
 
 class TokenRouter(nn.Module):

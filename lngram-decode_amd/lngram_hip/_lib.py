@@ -88,6 +88,8 @@ SIGNATURES = {
     "lng_causal_conv": (_int, [_p, _p, _p, _int, _i64, _i64, _i32, _i32, _i32, _f, _int, _p, _p]),
     "lng_causal_conv_at": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _i64, _p, _i64, _i32, _i32, _i32, _f, _int, _p,
                                   _p]),
+    "lng_causal_conv_slots": (_int, [_p, _p, _p, _int, _i64, _i64, _i64, _p, _i64, _i32, _i32, _i32, _i32, _f, _int,
+                                      _p, _p]),
     "lng_linear_rowsq_partials": (_i32, [_i64]),
     "lng_linear_rowsq": (_int, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "lng_linear_rowscale_ok": (_i32, [_i64, _i64, _i64]),
@@ -118,6 +120,7 @@ SIGNATURES = {
     "lng_ssm_scan": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _p, _p]),
     "lng_ssm_scan_bounded": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _i32, _p, _p]),
     "lng_ssm_scan_with_bf16": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, ctypes.c_size_t, _p, _p, _p]),
+    "lng_ssm_tree": (_int, [_p, _p, _p, _p, _i64, _i32, _i32, _p, _p]),
     "lng_ssm_scan_static": (_int, [_p, _p, _p, _i64, _i64, _i32, _p, _p]),
     "lng_ssm_scan_static_status": (_int, [_p]),
     "lng_drafter_tree_levels_workspace": (ctypes.c_size_t, [_PD]),

@@ -557,6 +557,33 @@ def causal_conv_at(rows: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tenso
     return out
 
 
+def causal_conv_slots(rows: torch.Tensor, norm_w: torch.Tensor, conv_w: torch.Tensor, dilation: int, eps: float,
+                      slots: torch.Tensor, length: int | None = None, residual: bool = True) -> torch.Tensor:
+    """The short conv with each output's window given as cache rows (``lng_causal_conv_slots``):
+    ``slots [n, back + 1]`` (oldest first, ``back = (K - 1) * dilation``; the ancestor windows of
+    ``tree_slots``) index the rows ``[B, S, d]`` of every sequence; a slot outside ``[0, length)``
+    (default ``length = S``) is a zero row.  Output ``i`` also adds row ``slots[i, back]`` as the
+    residual -> ``[B, n, d]``."""
+    dev = _dev(rows, norm_w, conv_w)
+    if rows.dim() != 3 or rows.stride(-1) != 1 or rows.stride(1) != rows.shape[-1]:
+        raise ValueError("causal_conv_slots: rows must be [B, S, d] with contiguous rows")
+    b, s_len, d = rows.shape
+    length = s_len if length is None else int(length)
+    cw = _c(conv_w.reshape(d, -1).to(rows.dtype))
+    k = cw.shape[1]
+    back = (k - 1) * int(dilation)
+    sl = _c(slots.to(device=dev, dtype=torch.int32))
+    if sl.dim() != 2 or sl.shape[1] != back + 1:
+        raise ValueError(f"causal_conv_slots: slots must be [n, {back + 1}]")
+    nw = _c(norm_w.to(rows.dtype))
+    n = sl.shape[0]
+    out = torch.empty(b, n, d, dtype=rows.dtype, device=dev)
+    check(lib().lng_causal_conv_slots(_ptr(rows), _ptr(nw), _ptr(cw), dtype_code(rows.dtype), b, rows.stride(0) // d,
+                                      length, _ptr(sl), n, back, d, k, int(dilation), eps, int(bool(residual)),
+                                      _ptr(out), _stream(dev)), "causal_conv_slots")
+    return out
+
+
 def memory_readout_pack(kv: torch.Tensor) -> torch.Tensor:
     """``readout_kv_proj.weight`` ``[512, 256]`` bf16 -> the fused readout's packed KV weight
     (``lng_memory_readout_pack``: a permutation into the kernel's operand order)."""
@@ -926,6 +953,22 @@ def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None,
                                                     ws.numel(), int(spin_limit), _ptr(out), _stream(dev))
     check(_timed("ssm_scan", dev, launch), "ssm_scan")
     return (out, sb) if want_bf16 else out
+
+
+def ssm_tree(a: torch.Tensor, u: torch.Tensor, parent, s_root: torch.Tensor | None = None) -> torch.Tensor:
+    """States of a draft tree's nodes (``lng_ssm_tree``): node ``i`` continues from its parent's state,
+    the root (parent -1) from ``s_root [B, N]`` or zero; u ``[B, n, N]`` -> s ``[B, n, N]`` fp32."""
+    dev = _dev(a, u, s_root)
+    uc = _c(u.float())
+    ac = _c(a.float())
+    b, n, nch = uc.shape
+    par = torch.as_tensor(list(parent), dtype=torch.int32).to(dev)
+    if par.numel() != n:
+        raise ValueError(f"ssm_tree: {par.numel()} parents for {n} nodes")
+    sr = None if s_root is None else _c(s_root.float().reshape(b, nch))
+    out = torch.empty_like(uc)
+    check(lib().lng_ssm_tree(_ptr(ac), _ptr(uc), _ptr(sr), _ptr(par), b, n, nch, _ptr(out), _stream(dev)), "ssm_tree")
+    return out
 
 
 def ssm_scan_status(dev: torch.device) -> int:

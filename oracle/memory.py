@@ -427,6 +427,54 @@ def ssm_scan_closed_form_constant(a, u_const, t: int, s0=None) -> np.ndarray:
     return u[None] + (a[None] ** k) * (s0 - u)[None]
 
 
+# ----------------------------------------------------------------------------- draft-tree verification
+def tree_paths(parent) -> list:
+    """Root-to-node paths of a tree given by ``parent`` (``parent[0] = -1``, ``parent[i] < i``;
+    ``drafting/tree.py:37-51``)."""
+    paths = []
+    for i, p in enumerate(parent):
+        if p < 0:
+            paths.append([i])
+        else:
+            if not 0 <= p < i:
+                raise ValueError("parent[i] must lie in [0, i)")
+            paths.append(paths[p] + [i])
+    return paths
+
+
+def ssm_tree(a, u, parent, s_root=None) -> np.ndarray:
+    """SSM states of the tree nodes in ``tree_verify_step`` (``drafting/tree.py:153-161``):
+    ``s_i = a s_parent(i) + (1-a) u_i``, the root continuing from ``s_root`` (the cached state at
+    ``L - 1``, zero if None), in fp64.  a ``[N]``, u ``[B, n, N]`` -> ``[B, n, N]``."""
+    a = np.asarray(a, np.float64)
+    u = np.asarray(u, np.float64)
+    b, n, c = u.shape
+    root = np.zeros((b, c)) if s_root is None else np.asarray(s_root, np.float64)
+    out = np.empty((b, n, c))
+    for i, p in enumerate(parent):
+        sp = root if p < 0 else out[:, p]
+        out[:, i] = a * sp + (1.0 - a) * u[:, i]
+    return out
+
+
+def tree_memory_forward(params: dict, cfg: MemCfg, h_hist: torch.Tensor, codes_hist, h_nodes: torch.Tensor,
+                        codes_nodes, parent, dtype: torch.dtype | None = None) -> torch.Tensor:
+    """The memory block of ``tree_verify_step`` (``drafting/tree.py:179-196``) for tree nodes after
+    ``L`` cached positions: node i's n-gram windows (``tree_ngram_codes`` :114-127) and conv window
+    (``tree_slots`` :96-111, :186-194) follow its ancestors and then the cached history, so its
+    output is the sequence forward's at the last position of history + its root path.  h_hist
+    ``[B, L, d]`` with codes ``[B, L, R]``; h_nodes ``[B, n, d]`` with codes ``[B, n, R]`` ->
+    ``[B, n, d]``."""
+    ch = np.asarray(codes_hist)
+    cn = np.asarray(codes_nodes)
+    outs = []
+    for path in tree_paths(parent):
+        hs = torch.cat((h_hist, h_nodes[:, path]), 1)
+        cs = np.concatenate((ch, cn[:, path]), 1)
+        outs.append(memory_forward(params, cfg, hs, cs, dtype=dtype)[:, -1])
+    return torch.stack(outs, 1)
+
+
 # ----------------------------------------------------------------------------- lookup surrogate (training)
 def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor, q_logits: torch.Tensor, codes, table,
                    valid, order: int, bits: int, route_start: int, temperature: float, scale: float, exact: bool,
