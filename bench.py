@@ -522,7 +522,8 @@ def tree_verify_step(dev, iters: int, warmup: int):
     import torch
 
     from drafting.tree import tree16
-    from ffnmem.infer import DecodeState, memory_codes, memory_model, memory_step, tree_memory_step
+    from ffnmem.infer import DecodeState, memory_codes, memory_model, memory_step, static_tree_memory_step, \
+        tree_memory_step
     from lngram_hip import ops, workloads
 
     w = workloads.SB.with_shape(1, 2048)
@@ -537,25 +538,37 @@ def tree_verify_step(dev, iters: int, warmup: int):
         memory_step(model, 0, st, h[:, :ctx], memory_codes(model, 0, st, h_norm=h_norm[:, :ctx]))
     st.length = ctx
     hn, hnn = h[:, ctx:].contiguous(), h_norm[:, ctx:].contiguous()
+    L_t = torch.full((), ctx, dtype=torch.int32, device=dev)
 
-    def step():
+    def eager():
         return tree_memory_step(model, 0, st, hn, memory_codes(model, 0, st, h_norm=hnn), parent)
 
+    def static():
+        return static_tree_memory_step(model, 0, st, hn, memory_codes(model, 0, st, h_norm=hnn), parent, L_t)
+
     def run() -> dict:
-        times = []
+        out = {}
         with torch.no_grad():
-            for i in range(warmup + iters):
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                step()
-                torch.cuda.synchronize()
-                if i >= warmup:
-                    times.append((time.perf_counter() - t0) * 1e6)
+            static()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                static()
+            for name, fn in (("eager", eager), ("graph", g.replay)):
+                times = []
+                for i in range(warmup + iters):
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    fn()
+                    torch.cuda.synchronize()
+                    if i >= warmup:
+                        times.append((time.perf_counter() - t0) * 1e6)
+                out[f"{name}_median_us"] = float(np.median(times))
+                out[f"{name}_p99_us"] = float(np.percentile(times, 99))
         return {"workload": f"SB-shape memory layer, draft-tree verification: 1 sequence, {n}-node tree after {ctx} "
                             "cached positions (node codes, ancestor-window rows, fused readout over them, o-proj "
                             "into the conv cache, conv over ancestor windows)",
-                "unit": "us per tree", "iters": iters, "eager_median_us": float(np.median(times)),
-                "p99_us": float(np.percentile(times, 99))}
+                "unit": "us per tree", "iters": iters, **out}
 
     return run
 

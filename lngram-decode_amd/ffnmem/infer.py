@@ -284,6 +284,74 @@ def tree_router_input(model, mem, state: DecodeState, emb: Tensor, s_new: Tensor
     return feats.step(prev, emb, s_new)
 
 
+_TREE_INDEX: dict = {}
+
+
+def _tree_index(parent, hist: int, back: int, device) -> tuple:
+    """Device index tables of a tree shape, built once per (parent, hist, back, device):
+    ``idx [n, hist + 1]``, the n-gram window slots of every node in ``cat(history of hist codes,
+    node codes)`` (``tree_slots`` with a history of ``hist`` positions), and ``rel [n, back + 1]``
+    int32, the conv window slots relative to the cached length (negative: history positions)."""
+    from drafting.tree import tree_slots
+
+    key = (tuple(int(p) for p in parent), int(hist), int(back), str(device))
+    t = _TREE_INDEX.get(key)
+    if t is None:
+        idx, _ = tree_slots(parent, hist, hist)          # every slot lies in the window's reach
+        full, _ = tree_slots(parent, back + 1, back)     # all valid at a length of back + 1
+        t = (idx.to(device), (full - (back + 1)).to(torch.int32).to(device))
+        _TREE_INDEX[key] = t
+    return t
+
+
+def _tree_memory(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, parent, L: int,
+                 L_t: Tensor | None) -> Tensor:
+    """``tree_memory_step`` at the cached length ``L`` (host) or ``*L_t`` (device int32, L = 0)."""
+    from drafting.drafters import window_route_tokens
+
+    mem = model.blocks[pos].memory
+    m = mem.module
+    b, n = h.shape[0], h.shape[1]
+    dev = h.device
+    if len(parent) != n:
+        raise ValueError(f"tree_memory_step: {len(parent)} parents for {n} nodes")
+    cache = state.codes[pos]
+    hist = m.route_history_length
+    conv = m.short_conv
+    idx, rel = _tree_index(parent, hist, conv.left_padding, dev)
+    c8 = codes.to(cache.dtype)
+    # the node windows over (the last `hist` cached codes, the nodes' codes); a history slot before
+    # position 0 is not real (its n-grams read zero rows)
+    base = (L - hist) + torch.arange(hist, device=dev)
+    if L_t is not None:
+        base = base + L_t.to(torch.long)
+    seq = torch.cat((cache.index_select(1, base.clamp_min(0)), c8), 1)
+    real = (idx >= hist) | ((idx - hist + (L if L_t is None else L_t.to(torch.long))) >= 0)
+    r = cache.shape[-1]
+    ctx = seq.index_select(1, idx.reshape(-1)).view(b, n * (hist + 1), r)
+    rt = window_route_tokens(m, ctx.view(b * n, hist + 1, r), real[None].expand(b, n, hist + 1).reshape(b * n, -1))
+    rt = rt.view(b, n, r, -1)
+    if L_t is None:
+        cache[:, L:L + n] = c8
+    else:
+        cache.index_copy_(1, L_t.to(torch.long) + torch.arange(n, device=dev), c8)
+    if m._fused_shape_ok(h, tables=False):
+        q_raw = ops.linear(h, m._folded_query_weight())
+        head = ops.memory_readout_fused_rows(q_raw, rt.to(torch.bfloat16), m._fused_weights(),
+                                             m.readout_memory_norm.weight, m.readout_memory_norm.eps, m.softmax_scale,
+                                             m.readout_sink_logit, q_rows=h, q_eps=m.readout_query_norm.eps)
+    else:
+        key, value = m._project_memory(rt.to(m.readout_kv_proj.weight.dtype))
+        head = m._manual_gqa(m._project_query(h), key, value)
+    conv_in = state.conv_in[pos]
+    L_dev = None if L_t is None else L_t.to(torch.int32).reshape(1)
+    _oproj_to_cache(m, head, conv_in, L, n, L_dev)
+    slots = rel + (L if L_t is None else L_dev)
+    length = L + n if L_t is None else conv_in.shape[1]
+    return ops.causal_conv_slots(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps, slots,
+                                 length=length, residual=True)
+
+
 def tree_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, parent) -> Tensor:
     """The memory block of the reference's draft-tree verification (``tree_verify_step``,
     ``drafting/tree.py:179-196``) for the tree nodes ``h [B, n, d]`` after the ``L = state.length``
@@ -295,36 +363,19 @@ def tree_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes: Tens
     are cached at ``L .. L+n-1`` too.  Returns ``mixed + short_conv`` ``[B, n, d]``; the caller sets
     ``state.length`` (after the accepted path is compacted, as the reference's loop does).  Node i's
     output equals ``memory_step``'s for the last token of a chain decode along its root path."""
-    from drafting.tree import tree_ngram_codes, tree_route_tokens, tree_slots
-
-    mem = model.blocks[pos].memory
-    m = mem.module
     L, n = state.length, h.shape[1]
-    if len(parent) != n:
-        raise ValueError(f"tree_memory_step: {len(parent)} parents for {n} nodes")
     if L + n > state.max_len:
         raise ValueError(f"cache full: {L} + {n} > {state.max_len}")
-    cache = state.codes[pos]
-    hist = m.route_history_length
-    c8 = codes.to(cache.dtype)
-    ctx, valid = tree_ngram_codes(parent, c8, cache[:, max(0, L - hist):L], hist)
-    rt = tree_route_tokens(m, ctx, valid)
-    cache[:, L:L + n] = c8
-    if m._fused_shape_ok(h, tables=False):
-        q_raw = ops.linear(h, m._folded_query_weight())
-        head = ops.memory_readout_fused_rows(q_raw, rt.to(torch.bfloat16), m._fused_weights(),
-                                             m.readout_memory_norm.weight, m.readout_memory_norm.eps, m.softmax_scale,
-                                             m.readout_sink_logit, q_rows=h, q_eps=m.readout_query_norm.eps)
-    else:
-        key, value = m._project_memory(rt.to(m.readout_kv_proj.weight.dtype))
-        head = m._manual_gqa(m._project_query(h), key, value)
-    conv_in = state.conv_in[pos]
-    _oproj_to_cache(m, head, conv_in, L, n, None)
-    conv = m.short_conv
-    slots, ok = tree_slots(parent, L, conv.left_padding)
-    slots = torch.where(ok, slots, torch.full_like(slots, -1))
-    return ops.causal_conv_slots(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps, slots,
-                                 length=L + n, residual=True)
+    return _tree_memory(model, pos, state, h, codes, parent, L, None)
+
+
+def static_tree_memory_step(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, parent,
+                            L_t: Tensor) -> Tensor:
+    """``tree_memory_step`` with the cached length in ``L_t`` (a 0-d device int32): no host
+    synchronisation and shapes independent of the length, so the launches can be captured in a HIP
+    graph and replayed at any length (the tree verification of ``static_verify``-style loops).  The
+    caller keeps ``L_t + n <= state.max_len``; the device length is not checked on the host."""
+    return _tree_memory(model, pos, state, h, codes, parent, 0, L_t)
 
 
 # ------------------------------------------------------------------ one memory layer's step

@@ -15,8 +15,8 @@ import pytest
 import torch
 
 from drafting.tree import tree16, tree_slots
-from ffnmem.infer import DecodeState, memory_codes, memory_model, memory_step, tree_memory_step, \
-    tree_router_input, tree_ssm_states
+from ffnmem.infer import DecodeState, memory_codes, memory_model, memory_step, static_tree_memory_step, \
+    tree_memory_step, tree_router_input, tree_ssm_states
 from ffnmem.memory.ssm import DiagonalSSM
 from lngram_hip import ops
 from lngram_hip import workloads as wl
@@ -132,6 +132,43 @@ def test_tree_memory_step_equals_chain_decode_and_oracle(dev, shape):
     else:
         want = om.tree_memory_forward(prm, cfg, h[:, :L].cpu(), ch, hn.cpu(), cn, PARENT)
         assert om.rel_err(got.float().cpu(), want.float()) < 2e-2
+
+
+@pytest.mark.parametrize("shape", ["tiny", "sb"])
+def test_static_tree_step_graph_replays_eager(dev, shape):
+    # the fixed-shape tree step captured once in a HIP graph and replayed at other device-held
+    # lengths (1, 2 and 9 cached positions included: history windows that run past position 0);
+    # the caches are restored between replays (eager work between them) and every replay is held
+    # to the eager step at that length
+    n = len(PARENT)
+    b, hist_len = (2, 12) if shape == "tiny" else (1, 12)
+    w = (wl.TINY if shape == "tiny" else wl.SB).with_shape(b, hist_len + n)
+    mem, h, h_norm = _layer(w, dev)
+    model = memory_model(mem)
+    with torch.no_grad():
+        base = DecodeState.empty(model, b, hist_len + n)
+        memory_step(model, 0, base, h[:, :hist_len], memory_codes(model, 0, base, h_norm=h_norm[:, :hist_len]))
+        hn = h[:, hist_len:].contiguous()
+        codes_n = memory_codes(model, 0, base, h_norm=h_norm[:, hist_len:])
+        st = base.index_select(torch.arange(b, device=dev))
+        L_t = torch.full((), hist_len, dtype=torch.int32, device=dev)
+        static_tree_memory_step(model, 0, st, hn, codes_n, PARENT, L_t)      # warm: index tables built
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = static_tree_memory_step(model, 0, st, hn, codes_n, PARENT, L_t)
+        for L in (hist_len, 9, 1, 2, hist_len):
+            st.codes[0].copy_(base.codes[0])
+            st.conv_in[0].copy_(base.conv_in[0])
+            L_t.fill_(L)
+            g.replay()
+            torch.cuda.synchronize()
+            ref = base.index_select(torch.arange(b, device=dev))
+            ref.length = L
+            want = tree_memory_step(model, 0, ref, hn, codes_n, PARENT)
+            assert torch.equal(out, want), L
+            assert torch.equal(st.codes[0][:, L:L + n], ref.codes[0][:, L:L + n])
+            assert torch.equal(st.conv_in[0][:, L:L + n], ref.conv_in[0][:, L:L + n])
 
 
 def test_tree_memory_step_rejects_bad_calls(dev):
