@@ -266,7 +266,7 @@ def tree_ssm_states(model, state: DecodeState, emb: Tensor, parent) -> Tensor:
     ssm = model.ssm
     L = state.length
     root = state.ssm[:, L - 1] if L > 0 else None
-    return ops.ssm_tree(ssm.decay(), ssm.inputs(emb), parent, root)
+    return ops.ssm_tree(ssm.decay(), ssm.inputs(emb), _parent_index(parent, emb.device)[0], root)
 
 
 def tree_router_input(model, mem, state: DecodeState, emb: Tensor, s_new: Tensor | None, parent) -> Tensor:
@@ -279,12 +279,23 @@ def tree_router_input(model, mem, state: DecodeState, emb: Tensor, s_new: Tensor
         root_prev = model.tok_emb(state.tokens[:, L - 1]).to(emb.dtype)
     else:
         root_prev = feats.start.to(emb.dtype).expand(b, d)
-    src = torch.as_tensor([p + 1 for p in parent], dtype=torch.long, device=emb.device)   # 0: the root's
+    src = _parent_index(parent, emb.device)[1]          # node i's previous row: 0 the root's, p + 1 node p
     prev = torch.cat((root_prev[:, None], emb), 1).index_select(1, src)
     return feats.step(prev, emb, s_new)
 
 
 _TREE_INDEX: dict = {}
+
+
+def _parent_index(parent, device) -> tuple:
+    """``(parent int32 [n], parent + 1 int64 [n])`` on the device, built once per tree shape."""
+    key = ("parent", tuple(int(p) for p in parent), str(device))
+    t = _TREE_INDEX.get(key)
+    if t is None:
+        par = torch.as_tensor(key[1], dtype=torch.int32)
+        t = (par.to(device), (par.to(torch.long) + 1).clamp_min(0).to(device))
+        _TREE_INDEX[key] = t
+    return t
 
 
 def _tree_index(parent, hist: int, back: int, device) -> tuple:

@@ -957,12 +957,14 @@ def ssm_scan(a: torch.Tensor, u: torch.Tensor, s0: torch.Tensor | None = None,
 
 def ssm_tree(a: torch.Tensor, u: torch.Tensor, parent, s_root: torch.Tensor | None = None) -> torch.Tensor:
     """States of a draft tree's nodes (``lng_ssm_tree``): node ``i`` continues from its parent's state,
-    the root (parent -1) from ``s_root [B, N]`` or zero; u ``[B, n, N]`` -> s ``[B, n, N]`` fp32."""
+    the root (parent -1) from ``s_root [B, N]`` or zero; u ``[B, n, N]`` -> s ``[B, n, N]`` fp32.
+    ``parent``: a sequence or an int32 device tensor."""
     dev = _dev(a, u, s_root)
     uc = _c(u.float())
     ac = _c(a.float())
     b, n, nch = uc.shape
-    par = torch.as_tensor(list(parent), dtype=torch.int32).to(dev)
+    par = parent.to(device=dev, dtype=torch.int32) if isinstance(parent, torch.Tensor) else \
+        torch.as_tensor(list(parent), dtype=torch.int32).to(dev)
     if par.numel() != n:
         raise ValueError(f"ssm_tree: {par.numel()} parents for {n} nodes")
     sr = None if s_root is None else _c(s_root.float().reshape(b, nch))
