@@ -778,7 +778,9 @@ def surrogate_backward(dev, steps: int, warmup: int):
     """Set up, and return the timing run of, the lookup surrogate's backward at the SB shape: 8 x 2048
     tokens, 184 routes, mem_dim 128, bf16 tables of orders 2 and 3, approximate mode; one step = the
     route-logit gradient of both orders (one ``k_surrogate_grad`` launch per order) from resident
-    memory gradients, looked-up rows, logits and codes."""
+    memory gradients, logits and codes, each window's looked-up row read from the table as the
+    training lookup does (its saved rows are the table's rows); the same step with the saved rows
+    streamed in (``hard_memory`` given) is timed beside it."""
     import torch
 
     from lngram_hip import ops
@@ -796,31 +798,35 @@ def surrogate_backward(dev, steps: int, warmup: int):
         hard = ops.route_tokens(codes, [table], [order], bits)
         legs.append((order, table, grad, valid, hard))
 
-    def step():
+    def step(saved: bool):
         for order, table, grad, valid, hard in legs:
-            ops.surrogate_grad(grad, hard, q, codes, table, valid, order, bits, 0, 1.0, 1.0, False)
+            ops.surrogate_grad(grad, hard if saved else None, q, codes, table, valid, order, bits, 0, 1.0, 1.0,
+                               False)
 
-    def run() -> dict:
+    def timed(saved: bool):
         for _ in range(warmup):
-            step()
+            step(saved)
         torch.cuda.synchronize()
         with ops.KernelTimer("surrogate_grad") as kt:
             t0 = time.perf_counter()
             for _ in range(steps):
-                step()
+                step(saved)
             torch.cuda.synchronize()
             el = time.perf_counter() - t0
-        d = kt.durations_ms()
+        return el / steps * 1e3, kt.durations_ms()
+
+    def run() -> dict:
+        saved_ms, saved_d = timed(True)
+        ms, d = timed(False)
         per_order = {f"order_{o}_us": 1e3 * sum(d[i::2]) / len(d[i::2]) for i, o in enumerate((2, 3))}
-        ms = el / steps * 1e3
         # per (token, route, order n): the memory-gradient row, the looked-up row and n*bits
         # counterfactual rows (256 B each), 16 B of logits, 16 B of gradient, the code
         alg = B * T * R * sum((2 + n * bits) * D * 2 + 2 * bits * 4 + 1 for n in (2, 3))
         kern_ms = sum(d) / len(d) * 2
         gbs = alg / (kern_ms * 1e-3) / 1e9
-        # distinct bytes: the memory-gradient and looked-up streams, logits, gradient and codes once, plus
-        # each order's table once
-        distinct = sum(B * T * R * (2 * D * 2 + 2 * bits * 4 + 1) + (R << (bits * n)) * D * 2 for n in (2, 3))
+        # distinct bytes: the memory-gradient stream, logits, gradient and codes once, plus each order's
+        # table once (the looked-up rows come from the table)
+        distinct = sum(B * T * R * (D * 2 + 2 * bits * 4 + 1) + (R << (bits * n)) * D * 2 for n in (2, 3))
         legs.clear()
         torch.cuda.empty_cache()
         return {"workload": "lookup surrogate backward (approximate) at the SB shape: B8 x T2048, R184, mem_dim 128, "
@@ -829,6 +835,9 @@ def surrogate_backward(dev, steps: int, warmup: int):
                 "gathered_bytes": alg, "gathered_GBs": gbs, "distinct_bytes": distinct,
                 "distinct_GBs": distinct / (kern_ms * 1e-3) / 1e9,
                 "distinct_hbm_frac": distinct / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "steps": steps,
+                "with_saved_rows": {"ms_per_step": saved_ms,
+                                    **{f"order_{o}_us": 1e3 * sum(saved_d[i::2]) / len(saved_d[i::2])
+                                       for i, o in enumerate((2, 3))}},
                 "note": "gathered bytes: the rows the reference algorithm reads (the counterfactual rows of a window "
                         "lie in its route's block, so most come from L2); distinct bytes: what has to cross HBM"}
 

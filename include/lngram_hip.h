@@ -317,7 +317,10 @@ int lng_gather_sum_scaled(const void* const* tables, int table_dtype, int32_t me
  * counterfactual scores times scale * temperature * p(1-p) (exact = 0), or the alphabet-wide
  * expectation derivative (exact = 1), p = sigmoid(temperature * q).  Zero when T < order,
  * temperature == 0 or scale == 0.  mem_dim in {32, 64, 128, 256}; 1 <= order <= 4, bits <= 8.
- * Each output is a fixed sum in the reference's order (no atomics). */
+ * Each output is a fixed sum in the reference's order (no atomics).  hard_memory may be null when
+ * it is the lookup's own rows (table[row] * valid[b, t], as _lookup_route_chunk makes it,
+ * lngram_v2.py:1084-1090): the looked-up row of every window with a gradient is then read from
+ * the table (the same bits), which saves streaming [B, T, R, mem_dim] from memory. */
 int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
                        int q_dtype, const void* codes, int codes_dtype, const void* table, int64_t table_rows,
                        const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start,

@@ -6,7 +6,9 @@
 // window s = 0 .. VL-1 (VL = T - order + 1) ending at position p = s + order - 1, its row
 // idx_s = (route_start + r) * A^order + sum_k c[s+k] * A^k (A = 2^bits, oldest code least
 // significant), the masked memory gradient g_s = grad[b, p, r, :] * valid[b, p] and the current
-// row m_s = hard_memory[b, p, r, :]:
+// row m_s = hard_memory[b, p, r, :] (with hard_memory null, table[idx_s]: the lookup's hard_memory
+// is table[idx_s] * valid, so every window with a gradient reads the same bits from the table,
+// out of the route's block that the counterfactual rows come from, instead of a second stream):
 //
 //   approximate:  G[t, bit] += sign * (table[idx_s ^ (1 << (e*bits + bit))] . g_s - m_s . g_s)
 //                 for every e = 0 .. order-1 with t = s + e, sign = +1 if that bit of idx_s is 0
@@ -183,7 +185,8 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
       constexpr bool PACKED = sizeof(TM) == 2 && V == 8;
       if constexpr (PACKED && !EXACT) {
         const u32x4 gr = ld_raw16(grad, mrow * 2, nt);
-        const float cd = sum16(dot8_bf16(ld_raw16(hard, mrow * 2, nt), gr));
+        const u32x4 hr = hard ? ld_raw16(hard, mrow * 2, nt) : ld_raw16(table, (idx * D + l * V) * 2, false);
+        const float cd = sum16(dot8_bf16(hr, gr));
 #pragma unroll
         for (int e = 0; e < SG_MAXORDER; ++e) {
           if (e < order) {
@@ -211,7 +214,10 @@ __global__ __launch_bounds__(256) void k_surrogate_grad(SgArgs a) {
       load_row_nt<TM, V>(grad, mrow, nt, g);
       if constexpr (!EXACT) {
         float m[V];
-        load_row_nt<TM, V>(hard, mrow, nt, m);
+        if (hard)
+          load_row_nt<TM, V>(hard, mrow, nt, m);
+        else
+          load_row<TM, V>(table + idx * D + l * V, m);
         float cd = 0.f;
 #pragma unroll
         for (int j = 0; j < V; ++j) cd += m[j] * g[j];
@@ -374,18 +380,19 @@ __global__ __launch_bounds__(256) void k_surrogate_grad_pk(SgArgs a) {
     for (int k = 0; k < ORDER; ++k) addr |= static_cast<uint32_t>(cds[rr][lw + k]) << (k * BITS);
     return addr;
   };
-  auto load_gh = [&](int w, u32x4 (&v)[2]) {
+  // the window's memory-gradient row, its looked-up row (from hard_memory, or, when that is null,
+  // the table row the lookup read: the same bits for every window with a gradient) and the rows of
+  // its route's block of the table with bit f of its address flipped
+  auto load_rows = [&](int w, uint32_t addr, u32x4 (&gh)[2], u32x4 (&v)[NF]) {
     if (!live(w)) return;
     const int64_t mrow = (b * a.T + s_lo + w % WR + ORDER - 1) * RD + (r0 + w / WR) * D + l * 8;
-    v[0] = ld_raw16(grad, mrow * 2, nt);
-    v[1] = ld_raw16(hard, mrow * 2, nt);
-  };
-  auto load_cf = [&](int w, uint32_t addr, u32x4 (&v)[NF]) {
-    if (!live(w)) return;
+    gh[0] = ld_raw16(grad, mrow * 2, nt);
+    if (hard) gh[1] = ld_raw16(hard, mrow * 2, nt);
     const __amdgpu_buffer_rsrc_t tb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<bf16*>(table + ((static_cast<int64_t>(a.route_start) + r0 + w / WR) << (BITS * ORDER)) * D), 0,
         static_cast<int>((int64_t(1) << (BITS * ORDER)) * D * 2), BUF_DW3);
     const uint32_t off = (addr << 8) | (static_cast<uint32_t>(l) << 4);
+    if (!hard) gh[1] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tb, off, 0, 0));
 #pragma unroll
     for (int f = 0; f < NF; ++f)
       v[f] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(tb, off ^ (1u << (f + 8)), 0, 0));
@@ -423,14 +430,12 @@ __global__ __launch_bounds__(256) void k_surrogate_grad_pk(SgArgs a) {
   u32x4 gh[2][2], cf[2][NF];
   uint32_t ad[2];
   ad[0] = addr_of(grp);
-  load_gh(grp, gh[0]);
-  load_cf(grp, ad[0], cf[0]);
+  load_rows(grp, ad[0], gh[0], cf[0]);
 #pragma unroll
   for (int j = 0; j < NW; ++j) {
     if (j + 1 < NW) {
       ad[(j + 1) & 1] = addr_of(grp + 16 * (j + 1));
-      load_gh(grp + 16 * (j + 1), gh[(j + 1) & 1]);
-      load_cf(grp + 16 * (j + 1), ad[(j + 1) & 1], cf[(j + 1) & 1]);
+      load_rows(grp + 16 * (j + 1), ad[(j + 1) & 1], gh[(j + 1) & 1], cf[(j + 1) & 1]);
     }
     reduce(grp + 16 * j, ad[j & 1], gh[j & 1], cf[j & 1]);
   }
@@ -535,7 +540,7 @@ extern "C" int lng_surrogate_grad(const void* grad_memory, const void* hard_memo
     return fail(LNG_E_DTYPE, "surrogate_grad: logits and gradient f32 or bf16");
   if (codes_dtype != LNG_U8 && codes_dtype != LNG_I32 && codes_dtype != LNG_I64)
     return fail(LNG_E_DTYPE, "surrogate_grad: codes u8, i32 or i64");
-  if (!grad_memory || !hard_memory || !q_logits || !codes || !table || !grad_q)
+  if (!grad_memory || !q_logits || !codes || !table || !grad_q)
     return fail(LNG_E_ARG, "surrogate_grad: null buffer");
   const int64_t need = (static_cast<int64_t>(route_start) + R) << (bits * order);
   if (table_rows < need) return fail(LNG_E_ARG, "surrogate_grad: table has fewer rows than (route_start + R) * 2^(bits*order)");

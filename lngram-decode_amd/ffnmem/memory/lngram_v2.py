@@ -53,22 +53,30 @@ class _LngramSurrogate(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hard_memory: Tensor, q_logits: Tensor, route_codes: Tensor, table_weight: Tensor,
                 valid_mask: Tensor, order: int, bits: int, route_start: int, alphabet_size: int,
-                temperature: float, scale: float, exact: bool) -> Tensor:
+                temperature: float, scale: float, exact: bool, hard_is_lookup: Optional[bool] = None) -> Tensor:
+        """``hard_is_lookup`` (not in the reference; the lookup of this module passes True): the
+        memory is the lookup's own rows, ``table[row] * valid``, so the backward reads them from the
+        table instead of keeping a copy."""
         if int(alphabet_size) != 1 << int(bits):
             raise ValueError("alphabet_size must be 2**bits")
-        ctx.save_for_backward(q_logits, route_codes, table_weight, valid_mask, hard_memory.detach())
+        from_table = bool(hard_is_lookup)
+        saved = (q_logits, route_codes, table_weight, valid_mask)
+        ctx.save_for_backward(*(saved if from_table else saved + (hard_memory.detach(),)))
         ctx.cfg = (int(order), int(bits), int(route_start), float(temperature), float(scale), bool(exact))
+        ctx.n_inputs = 12 if hard_is_lookup is None else 13
         return hard_memory
 
     @staticmethod
     def backward(ctx, grad_memory: Optional[Tensor]):
         if grad_memory is None:
-            return (None,) * 12
-        q_logits, codes, table, valid_mask, hard = ctx.saved_tensors
+            return (None,) * ctx.n_inputs
+        saved = ctx.saved_tensors
+        q_logits, codes, table, valid_mask = saved[:4]
+        hard = saved[4] if len(saved) > 4 else None
         order, bits, route_start, temperature, scale, exact = ctx.cfg
         grad_q = ops.surrogate_grad(grad_memory, hard, q_logits.detach(), codes, table.detach(), valid_mask, order,
                                     bits, route_start, temperature, scale, exact)
-        return (grad_memory, grad_q) + (None,) * 10
+        return (grad_memory, grad_q) + (None,) * (ctx.n_inputs - 2)
 
 
 class _TableRows(torch.autograd.Function):
@@ -407,7 +415,7 @@ class _RouteNgramMemoryBase(nn.Module):
                                     route_end, segment_ids, valid_tokens)
             parts.append(_LngramSurrogate.apply(rows, q_chunk, codes, table, valid, order, self.bits_per_route,
                                                 route_start, self.alphabet_size, self.q_surrogate_temperature,
-                                                self.q_surrogate_scale, self.q_surrogate_mode == "exact"))
+                                                self.q_surrogate_scale, self.q_surrogate_mode == "exact", True))
         return torch.cat(parts, dim=-1)
 
     # ------------------------------------------------------------------ projections

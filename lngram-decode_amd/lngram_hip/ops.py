@@ -730,18 +730,21 @@ def gather_sum_scaled(tables, codes: torch.Tensor, orders, bits: int, scale_log2
     return out
 
 
-def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor, q_logits: torch.Tensor,
+def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor | None, q_logits: torch.Tensor,
                    codes: torch.Tensor, table: torch.Tensor, valid_mask: torch.Tensor | None, order: int, bits: int,
                    route_start: int, temperature: float, scale: float, exact: bool) -> torch.Tensor:
     """Route-logit gradient ``[B, T, R, bits]`` (``q_logits``' dtype) of the lookup surrogate of one
-    order (``lng_surrogate_grad``; ``_LngramSurrogate.backward``, ``lngram_v2.py:364-464``)."""
+    order (``lng_surrogate_grad``; ``_LngramSurrogate.backward``, ``lngram_v2.py:364-464``).
+    ``hard_memory`` None: it is the lookup's own rows (``table[row] * valid``), which the kernel
+    then reads from the table instead of streaming them."""
     dev = _dev(grad_memory, hard_memory, q_logits, codes, table, valid_mask)
-    b, t, r, md = hard_memory.shape
-    if tuple(grad_memory.shape) != (b, t, r, md) or tuple(q_logits.shape) != (b, t, r, bits) or \
-            tuple(codes.shape) != (b, t, r) or table.dim() != 2 or table.shape[1] != md:
+    b, t, r, md = grad_memory.shape
+    if (hard_memory is not None and tuple(hard_memory.shape) != (b, t, r, md)) or \
+            tuple(q_logits.shape) != (b, t, r, bits) or tuple(codes.shape) != (b, t, r) or table.dim() != 2 or \
+            table.shape[1] != md:
         raise ValueError("surrogate_grad: memory [B,T,R,D], q_logits [B,T,R,bits], codes [B,T,R], table [rows, D]")
     mdt = table.dtype
-    if hard_memory.dtype != mdt:
+    if hard_memory is not None and hard_memory.dtype != mdt:
         raise ValueError(f"surrogate_grad: memory dtype {hard_memory.dtype} != table dtype {mdt}")
     g = _c(grad_memory.to(mdt))
     hm, tab, q, cc = _c(hard_memory), _c(table), _c(q_logits), _c(codes)

@@ -161,6 +161,32 @@ def test_sb_shape_linear_table_closed_form(dev):
         del hard, grad, table, got, want
 
 
+@pytest.mark.parametrize("shape", ["sb_packed", "f32_d64", "bf16_d32"])
+def test_hard_rows_from_table_equal_saved_rows(dev, shape):
+    """``hard_memory`` None (the kernel reads each window's looked-up row from the table) gives the
+    same gradient, bit for bit, as passing the lookup's own rows ``table[row] * valid``: the packed
+    bf16 kernel of the SB lookup (mem_dim 128, 4-bit codes, orders 2 and 3) and the generic one, with
+    masked positions and a route offset."""
+    B, T, R, rs, D, bits, dt, orders = {"sb_packed": (2, 300, 184, 0, 128, 4, torch.bfloat16, (2, 3)),
+                                        "f32_d64": (2, 70, 5, 1, 64, 2, torch.float32, (1, 3)),
+                                        "bf16_d32": (3, 50, 7, 0, 32, 3, torch.bfloat16, (2,))}[shape]
+    gen = torch.Generator().manual_seed(31)
+    A = 1 << bits
+    for order in orders:
+        table = (torch.randn((rs + R) * A ** order, D, generator=gen) * 0.5).to(dt).to(dev)
+        codes = torch.randint(0, A, (B, T, R), generator=gen, dtype=torch.uint8).to(dev)
+        q = torch.randn(B, T, R, bits, generator=gen).to(dev)
+        grad = torch.randn(B, T, R, D, generator=gen).to(dt).to(dev)
+        valid = torch.rand(B, T, generator=gen) > 0.2
+        valid[:, :order - 1] = False
+        valid = valid.to(dev)
+        hard = ops.route_tokens(codes, [table[rs * A ** order:]], [order], bits) * valid[:, :, None, None].to(dt)
+        for exact in (False, True):
+            want = ops.surrogate_grad(grad, hard, q, codes, table, valid, order, bits, rs, 0.7, 1.3, exact)
+            got = ops.surrogate_grad(grad, None, q, codes, table, valid, order, bits, rs, 0.7, 1.3, exact)
+            assert torch.equal(got, want), (shape, order, exact)
+
+
 def test_table_grad_matches_scatter(dev):
     B, T, R, rs, D, order, bits = 2, 30, 5, 1, 64, 3, 2
     x = _random_case(17, B, T, R, rs, D, order, bits, torch.float32)
