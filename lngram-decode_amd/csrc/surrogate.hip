@@ -462,6 +462,145 @@ __global__ __launch_bounds__(256) void k_surrogate_grad_pk(SgArgs a) {
   }
 }
 
+// Order 2 for bf16 rows of 128 and 4-bit codes, with the route's block of the table (256 rows,
+// 64 KB) in LDS: the approximate mode's windows, scores and output sums as k_surrogate_grad_pk
+// (HARD: the looked-up rows streamed from hard_memory; else read from the block).  A block owns
+// one route of one sequence and 16 * NW windows (NW per 16-lane group); it copies the route's block
+// into LDS (straight from L2 by DMA) while the windows' memory-gradient rows are requested from
+// HBM, then reads every window's looked-up and eight counterfactual rows from LDS: the rows of one
+// route are shared by all its windows, so the gathers leave L2 for LDS.  Lane l of group g holds
+// 16-byte piece (l + 8 (g & 1)) & 15 of every row: one LDS pass serves lanes 0-7 with 16-23 (and
+// 8-15 with 24-31, ...), which then read opposite halves of their rows, so a pass covers all 64
+// banks whatever rows the windows name.  NT threads (NT / 16 groups); two blocks per CU: 512
+// threads with 15 windows a group fill the LDS (2 x 81.9 KB) at 4 waves per SIMD.
+template <int NW, int NT, bool HARD>
+__global__ __launch_bounds__(NT, 2) void k_surrogate_grad_o2lds(SgArgs a) {
+  constexpr int NG = NT / 16, W = NG * NW, P = W - 1, NF = 8, NWV = NT / 64;
+  static_assert(64 % NWV == 0, "the block copy is whole kilobytes per wave");
+  constexpr int64_t D = 128;
+  __shared__ __attribute__((aligned(16))) bf16 tab[256 * D];  // the route's block, row-major
+  __shared__ float sc[W][NF];                                 // window w's scores [e * 4 + bit]
+  __shared__ uint8_t cds[W + 1];                              // code at position s_lo + i
+  __shared__ uint8_t vld[W];                                  // window s_lo + w has a gradient row
+  const int tid = threadIdx.x, grp = tid >> 4, l = tid & 15, wave = tid >> 6, lane = tid & 63;
+  // block -> (route, sequence, tile): XCD x = block % 8 keeps to routes 8j + x, all of a route's
+  // (sequence, tile) blocks in a row, so the route's block of the table stays in that XCD's L2
+  const int64_t xcd = blockIdx.x & 7, k8 = blockIdx.x >> 3;
+  const int64_t per_route = a.B * a.tiles;
+  const int64_t r = (k8 / per_route) * 8 + xcd;
+  if (r >= a.R) return;  // the whole block: before any barrier
+  const int64_t rem = k8 % per_route;
+  const int64_t b = rem / a.tiles;
+  const int64_t t0 = (rem % a.tiles) * P;
+  const int64_t s_lo = t0 - 1;  // window s covers positions s, s + 1
+  const int64_t VL = a.T - 1;
+  const bool active = VL > 0 && a.temperature != 0.f && a.scale != 0.f;
+  // the tile's codes and window validity (small, through registers)
+  for (int i = tid; i < W + 1; i += NT) {
+    const int64_t pos = s_lo + i;
+    cds[i] = (pos >= 0 && pos < a.T) ? static_cast<uint8_t>(sg_code(a.codes, a.codes_dt, (b * a.T + pos) * a.R + r) & 15)
+                                     : 0;
+  }
+  for (int i = tid; i < W; i += NT) {
+    const int64_t sw = s_lo + i;
+    vld[i] = active && sw >= 0 && sw < VL && (a.valid == nullptr || a.valid[b * a.T + sw + 1]);
+  }
+  // the route's block into LDS: wave w copies kilobytes NWV i + w (lane: 16 bytes)
+  const bf16* blk = static_cast<const bf16*>(a.table) + ((static_cast<int64_t>(a.route_start) + r) << 8) * D;
+#pragma unroll
+  for (int i = 0; i < 64 / NWV; ++i) {
+    const int kb = NWV * i + wave;
+    __builtin_amdgcn_global_load_lds(blk + kb * 512 + lane * 8, (__attribute__((address_space(3))) void*)(tab + kb * 512),
+                                     16, 0, 0);
+  }
+  asm volatile("" ::: "memory");
+  // the windows' memory-gradient rows: a buffer over sequence b's rows, so a window past the end
+  // reads zeros (its scores are not used); position s_lo + w + 1 >= 0 always
+  const int pc = (l + 8 * (grp & 1)) & 15;
+  const bf16* gseq = static_cast<const bf16*>(a.grad) + b * a.T * a.R * D;
+  const __amdgpu_buffer_rsrc_t gr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(gseq), 0, static_cast<int>(a.T * a.R * D * 2), BUF_DW3);
+  const __amdgpu_buffer_rsrc_t hr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(static_cast<const bf16*>(HARD ? a.hard : a.grad) + b * a.T * a.R * D), 0,
+      static_cast<int>(a.T * a.R * D * 2), BUF_DW3);
+  auto ld = [&](__amdgpu_buffer_rsrc_t rs, uint32_t off) {
+    return a.nt ? __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, CPOL_NT))
+                : __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(off), 0, 0));
+  };
+  u32x4 gv[NW], hv[HARD ? NW : 1];
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int64_t pos = s_lo + grp + NG * j + 1;
+    const uint32_t off = static_cast<uint32_t>(((pos * a.R + r) * D + pc * 8) * 2);
+    gv[j] = ld(gr, off);
+    if constexpr (HARD) hv[j] = ld(hr, off);
+  }
+  // the block copy (issued before the gradient and looked-up row loads) has landed for this wave;
+  // the barrier makes it, the codes and the validity visible to all
+  if constexpr (HARD)
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * NW) : "memory");
+  else
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NW) : "memory");
+  __syncthreads();
+  auto row = [&](uint32_t rw) { return *reinterpret_cast<const u32x4*>(tab + rw * D + pc * 8); };
+  // a dot product's 16-lane partials summed along the row (inclusive DPP prefix): the total lands
+  // in the row's last lane, which alone forms and stores the scores
+  auto sum_last = [](float x) {
+    x += dpp_row_shr<0x111>(x, 0.f);
+    x += dpp_row_shr<0x112>(x, 0.f);
+    x += dpp_row_shr<0x114>(x, 0.f);
+    x += dpp_row_shr<0x118>(x, 0.f);
+    return x;
+  };
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int w = grp + NG * j;
+    float score[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) score[f] = 0.f;
+    if (vld[w]) {
+      const uint32_t addr = static_cast<uint32_t>(cds[w]) | (static_cast<uint32_t>(cds[w + 1]) << 4);
+      u32x4 rv[NF + 1];
+      if constexpr (HARD)
+        rv[NF] = hv[j];
+      else
+        rv[NF] = row(addr);
+#pragma unroll
+      for (int f = 0; f < NF; ++f) rv[f] = row(addr ^ (1u << f));
+      const float cd = sum_last(dot8_bf16(rv[NF], gv[j]));
+#pragma unroll
+      for (int f = 0; f < NF; ++f) {
+        const float fd = sum_last(dot8_bf16(rv[f], gv[j]));
+        score[f] = (fd - cd) * (((addr >> f) & 1) ? -1.f : 1.f);
+      }
+    }
+    if (l == 15) {
+#pragma unroll
+      for (int f = 0; f < NF; ++f) sc[w][f] = score[f];
+    }
+  }
+  __syncthreads();
+  // output (t, bit) of the route, bits fastest: the windows t (e = 0) and t - 1 (e = 1), e ascending
+  for (int i = tid; i < P * 4; i += NT) {
+    const int k = i & 3, tl = i >> 2;
+    const int64_t t = t0 + tl;
+    if (t >= a.T) break;
+    float acc = 0.f;
+    acc += sc[tl + 1][k];
+    acc += sc[tl][4 + k];
+    const int64_t oi = ((b * a.T + t) * a.R + r) * 4 + k;
+    if (active) {
+      const float qv = a.q_dt == LNG_BF16 ? to_f32(static_cast<const bf16*>(a.q)[oi]) : static_cast<const float*>(a.q)[oi];
+      const float p = 1.f / (1.f + expf(-(a.temperature * qv)));
+      acc *= a.alpha * p * (1.f - p);
+    }
+    if (a.out_dt == LNG_BF16)
+      static_cast<bf16*>(a.out)[oi] = static_cast<bf16>(acc);
+    else
+      static_cast<float*>(a.out)[oi] = acc;
+  }
+}
+
 // Table gradient of the lookup (the embedding backward behind the surrogate's pass-through,
 // lngram_v2.py:1084-1092 and :454): table_grad[row(b, t, r)] += grad[b, t, r, :] * valid[b, t] for
 // every position with an order-`order` window.  One 16-lane group per (b, t, r); fp32 atomics, so
@@ -500,6 +639,20 @@ static int sg_launch_v(const SgArgs& a, int64_t D, hipStream_t s) {
       // order 2: 8 routes x 32 windows a block (their table blocks: 512 KB; the logits and gradients
       // of 8 routes fill whole 128 B lines); order 3: one route x 128 windows (its 1 MB block of
       // the table stays in the XCD's L2, where four routes' blocks were evicted by the streams)
+      if (a.order == 2 && a.T * a.R * D * 2 < (int64_t{1} << 31)) {
+        // the route's block of the table in LDS: 480 windows in 512 threads, or, streaming the
+        // saved looked-up rows as well (more registers a lane), 256 windows in 256 threads
+        SgArgs al = a;
+        const int win = a.hard ? 256 : 480;
+        al.tiles = cdiv(a.T, win - 1);
+        const int64_t lblocks = 8 * cdiv(a.R, 8) * a.B * al.tiles;
+        if (lblocks > 0x7FFFFFFF) return fail(LNG_E_ARG, "surrogate_grad: too many blocks");
+        if (a.hard)
+          k_surrogate_grad_o2lds<16, 256, true><<<lblocks, 256, 0, s>>>(al);
+        else
+          k_surrogate_grad_o2lds<15, 512, false><<<lblocks, 512, 0, s>>>(al);
+        return check_launch("k_surrogate_grad_o2lds");
+      }
       const int rg = a.order == 2 ? 8 : 1, win = a.order == 2 ? 256 : 128;
       SgArgs ap = a;
       ap.tiles = cdiv(a.T, win / rg - (a.order - 1));
