@@ -290,11 +290,18 @@ __global__ __launch_bounds__(512) void k_ssm_scan(const float* __restrict__ a, c
         for (int j = 0; j < 4; ++j) st[j] = fmaf(av[j], st[j], bv[j] * x[i][j]);
         store4<VEC>(sb + static_cast<int64_t>(t0 + i) * N, c, N, st);
         if (sb_out) {
-          // the states rounded to bf16 as well (the token router's feature columns)
+          // the states rounded to bf16 as well (the token router's feature columns): one 8-byte
+          // store a lane when rows are whole groups of 4
           bf16* q = sb_out + static_cast<int64_t>(b) * T * N + static_cast<int64_t>(t0 + i) * N;
+          if (VEC) {
+            if (c < N)
+              *reinterpret_cast<bf16x4*>(q + c) = bf16x4{static_cast<bf16>(st[0]), static_cast<bf16>(st[1]),
+                                                         static_cast<bf16>(st[2]), static_cast<bf16>(st[3])};
+          } else {
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (c + j < N) q[c + j] = static_cast<bf16>(st[j]);
+            for (int j = 0; j < 4; ++j)
+              if (c + j < N) q[c + j] = static_cast<bf16>(st[j]);
+          }
         }
       }
     }
