@@ -327,6 +327,25 @@ int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem
                        int32_t mem_dim, int32_t order, int32_t bits, float temperature, float scale, int exact,
                        void* grad_q, int out_dtype, void* stream);
 
+/* lng_surrogate_grad with a workspace (same reference function, _LngramSurrogate.backward,
+ * lngram_v2.py:364-464): for the shapes lng_surrogate_workspace_bytes gives a size for (order 3,
+ * bf16 rows of 128, 4-bit codes, approximate mode, R <= 256, B*T <= 65536) the windows of every route
+ * are binned by the code at their newest position, so that a block reads the looked-up and eight
+ * of the twelve counterfactual rows of its windows from one 64 KB sub-block of the table held on
+ * chip; the workspace holds a route-major copy of the codes and every window's twelve scores, each
+ * written by the call before it is read (no clearing needed; calls that share a workspace must be
+ * ordered, e.g. on one stream).  Other shapes (size 0)
+ * take lng_surrogate_grad's path and ignore the workspace.  The result is a fixed sum per output in
+ * the reference's order, as lng_surrogate_grad's (the within-row summation order differs, so the
+ * two paths agree to fp32 rounding). */
+size_t lng_surrogate_workspace_bytes(int64_t B, int64_t T, int32_t R, int32_t mem_dim, int32_t order, int32_t bits,
+                                     int mem_dtype, int exact);
+int lng_surrogate_grad_ws(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
+                          int q_dtype, const void* codes, int codes_dtype, const void* table, int64_t table_rows,
+                          const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start,
+                          int32_t mem_dim, int32_t order, int32_t bits, float temperature, float scale, int exact,
+                          void* workspace, size_t workspace_bytes, void* grad_q, int out_dtype, void* stream);
+
 /* Table gradient of one order's lookup: the embedding backward behind _LngramSurrogate's
  * pass-through of the memory gradient (lngram_v2.py:1084-1092, :454).  table_grad
  * [table_rows, mem_dim] fp32 (the caller zeroes it) += grad_memory[b, t, r, :] at row

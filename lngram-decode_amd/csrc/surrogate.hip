@@ -601,6 +601,324 @@ __global__ __launch_bounds__(NT, 2) void k_surrogate_grad_o2lds(SgArgs a) {
   }
 }
 
+// ---------------------------------------------------------------- order 3 by digit-2 bins
+// Order 3 (bf16 rows of 128, 4-bit codes, approximate mode) with a workspace.  A window's looked-up
+// row and its eight digit-0 and digit-1 counterfactual rows all lie in the 256-row sub-block of its
+// route's table block that its digit 2 (the code at its newest position) selects; only the four
+// digit-2 flips lie elsewhere.  A block per (route, bin v) keeps sub-block v of its route in LDS,
+// lists the route's windows whose digit 2 is v (from a route-major copy of the codes) and gathers 9
+// of each window's 13 rows from LDS (4 from L2), writing the window's 12 scores to the workspace; a
+// last kernel sums each output's windows in the reference's order (e ascending) and applies the
+// slope.  Windows without a gradient are listed nowhere and contribute 0.
+constexpr int SG3_MAXD = 2048;   // windows a block lists in LDS at once
+constexpr int SG3_WPT = 32;      // consecutive windows a thread scans
+constexpr int SG3_MAXW = 4 * 512 * SG3_WPT;  // windows of a route (B T) this path takes
+
+__host__ __device__ constexpr size_t sg3_al(size_t x) { return (x + 255) & ~size_t{255}; }
+struct Sg3Ws {  // byte offsets in the workspace
+  size_t codes_t, scores, total, ct_stride;
+};
+__host__ __device__ inline Sg3Ws sg3_layout(int64_t B, int64_t T, int32_t R) {
+  Sg3Ws w{};
+  // a route's row holds B T codes rounded up to SG3_WPT, then SG3_WPT readable bytes
+  w.ct_stride = sg3_al(static_cast<size_t>((B * T + SG3_WPT - 1) / SG3_WPT + 1) * SG3_WPT);
+  w.codes_t = 0;                                                  // uint8 [R][ct_stride]
+  w.scores = sg3_al(static_cast<size_t>(R) * w.ct_stride);        // float [3][R][B T][4]
+  w.total = sg3_al(w.scores + static_cast<size_t>(B) * T * R * 12 * 4);
+  return w;
+}
+
+// window (b, s) has a gradient row (its newest position s + 2 is valid); 32-bit indices: this path
+// takes B * T * R < 2^28
+__device__ __forceinline__ bool sg3_live(const SgArgs& a, int b, int s) {
+  const int T = static_cast<int>(a.T);
+  return s >= 0 && s < T - 2 && (a.valid == nullptr || a.valid[b * T + s + 2]);
+}
+
+// codes [B T, R] (any code dtype) -> codes_t [R][stride] uint8: byte w = the code at flat position w
+// (low 4 bits) | 16 when the window starting at w is live; 64 x 64 tiles through LDS
+__global__ __launch_bounds__(256) void k_sg3_transpose(SgArgs a, uint8_t* __restrict__ codes_t, int stride) {
+  __shared__ uint8_t t[64][65];
+  const int T = static_cast<int>(a.T), NWIN = static_cast<int>(a.B) * T, R = a.R;
+  const int w0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int wl = i >> 6, rl = i & 63;
+    const int w = w0 + wl, r = r0 + rl;
+    uint8_t c = 0;
+    if (w < NWIN && r < R) {
+      const int b = w / T;
+      c = static_cast<uint8_t>((sg_code(a.codes, a.codes_dt, static_cast<int64_t>(w) * R + r) & 15) |
+                               (sg3_live(a, b, w - b * T) ? 16 : 0));
+    }
+    t[wl][rl] = c;
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+    const int rl = i >> 6, wl = i & 63;
+    const int w = w0 + wl, r = r0 + rl;
+    if (w < NWIN && r < R) codes_t[static_cast<int64_t>(r) * stride + w] = t[wl][rl];
+  }
+}
+
+// A block per (route, bin v): sub-block v of the route's table block in LDS; the route's windows with
+// digit 2 == v listed in LDS by one scan of the route's codes, 32 windows a thread (when more than
+// SG3_MAXD windows share the bin, the route's windows are listed again in ranges of SG3_MAXD, one list
+// at a time); 512 threads at 4 waves per SIMD (two blocks a CU); each 16-lane group takes listed
+// windows grp, grp + NG, ...: the memory-gradient row (HBM) and the four digit-2 counterfactual rows
+// (L2) of the next window are requested before the current window is reduced; its looked-up row (LDS,
+// or the saved row when HARD) and eight digit-0 and digit-1 rows come from LDS.  Lane l of group g
+// holds piece (l + 8 (g & 1)) & 15 of every row (the two halves of an LDS pass cover all 64 banks).
+// Scores of digit e to plane e: scores[e][r][b T + s][bit].
+template <bool HARD>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_sg3_main(SgArgs a, const uint8_t* __restrict__ codes_t, int stride,
+                                                     float* __restrict__ scores) {
+  constexpr int NT = 512, NG = NT / 16, NWV = NT / 64;
+  constexpr int64_t D = 128;
+  __shared__ __attribute__((aligned(16))) bf16 tab[256 * D];
+  __shared__ uint32_t dl[SG3_MAXD];  // (b T + s) << 12 | address
+  __shared__ int nl[2];
+  const int tid = threadIdx.x, grp = tid >> 4, l = tid & 15, wave = tid >> 6, lane = tid & 63;
+  const int xcd = blockIdx.x & 7, k8 = blockIdx.x >> 3;
+  const int r = (k8 >> 4) * 8 + xcd;
+  const uint32_t v = static_cast<uint32_t>(k8 & 15);
+  if (r >= a.R) return;  // the whole block: before any barrier
+  const int T = static_cast<int>(a.T), NWIN = static_cast<int>(a.B) * T;
+  const int64_t rbase = (static_cast<int64_t>(a.route_start) + r) << 12;  // the route's first table row
+  const bf16* table = static_cast<const bf16*>(a.table);
+  const bf16* sub = table + (rbase + (static_cast<int64_t>(v) << 8)) * D;
+  const uint8_t* ct = codes_t + static_cast<int64_t>(r) * stride;
+  // windows (c NT + tid) SG3_WPT + i, i < SG3_WPT, c < 4, are the thread's; bin_mask says which are
+  // live with digit 2 == v (their codes and liveness from three 16-byte loads).  The list is
+  // written in the same pass while it has room; a bin of more than SG3_MAXD windows is listed again
+  // in ranges below.
+  // bit i: window wb + i is live with digit 2 == v (q0, q1, q2 = bytes wb .. wb + 47 of the route's codes)
+  auto bin_mask = [&](u32x4 q0, u32x4 q1, u32x4 q2, int wb) {
+    const uint32_t wd[9] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w, q2.x};
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < SG3_WPT; ++i) {
+      const uint32_t cw = (wd[i >> 2] >> (8 * (i & 3))) & 0xFF;           // position wb + i
+      const uint32_t c2 = (wd[(i + 2) >> 2] >> (8 * ((i + 2) & 3))) & 15;  // position wb + i + 2
+      m |= ((cw & 16) && c2 == v && wb + i < NWIN) ? (1u << i) : 0u;
+    }
+    return m;
+  };
+  {
+    u32x4 qv[4][3];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int wb = (c * NT + tid) * SG3_WPT;
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+        qv[c][k] = wb < NWIN ? *reinterpret_cast<const u32x4*>(ct + wb + 16 * k) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int i = 0; i < 64 / NWV; ++i) {  // the sub-block copy, behind the code loads
+      const int kb = NWV * i + wave;
+      __builtin_amdgcn_global_load_lds(sub + kb * 512 + lane * 8,
+                                       (__attribute__((address_space(3))) void*)(tab + kb * 512), 16, 0, 0);
+    }
+    if (tid == 0) nl[0] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int wb = (c * NT + tid) * SG3_WPT;
+      const uint32_t wd[9] = {qv[c][0].x, qv[c][0].y, qv[c][0].z, qv[c][0].w, qv[c][1].x,
+                              qv[c][1].y, qv[c][1].z, qv[c][1].w, qv[c][2].x};
+      uint32_t m = wb < NWIN ? bin_mask(qv[c][0], qv[c][1], qv[c][2], wb) : 0u;
+      if (m) {
+        int slot = atomicAdd(&nl[0], __builtin_popcount(m));
+        for (; m; m &= m - 1, ++slot) {
+          const int i = __builtin_ctz(m);  // window wb + i: its codes are bytes i and i + 1 of wd
+          uint32_t x0 = wd[0], x1 = wd[0];
+#pragma unroll
+          for (int q = 1; q < 9; ++q) {
+            x0 = (i >> 2) == q ? wd[q] : x0;
+            x1 = ((i + 1) >> 2) == q ? wd[q] : x1;
+          }
+          const uint32_t addr = ((x0 >> (8 * (i & 3))) & 15u) | (((x1 >> (8 * ((i + 1) & 3))) & 15u) << 4) | (v << 8);
+          if (slot < SG3_MAXD) dl[slot] = (static_cast<uint32_t>(wb + i) << 12) | addr;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const int total = nl[0];
+  const int span = total <= SG3_MAXD ? NWIN : SG3_MAXD;  // windows per list
+  const int pc = (l + 8 * (grp & 1)) & 15;
+  const __amdgpu_buffer_rsrc_t trs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<bf16*>(table + rbase * D), 0, static_cast<int>(int64_t{4096} * D * 2), BUF_DW3);
+  const bf16* grad = static_cast<const bf16*>(a.grad);
+  const bf16* hard = static_cast<const bf16*>(a.hard);
+  auto row = [&](uint32_t rw) { return *reinterpret_cast<const u32x4*>(tab + rw * D + pc * 8); };
+  auto sum_last = [](float x) {
+    x += dpp_row_shr<0x111>(x, 0.f);
+    x += dpp_row_shr<0x112>(x, 0.f);
+    x += dpp_row_shr<0x114>(x, 0.f);
+    x += dpp_row_shr<0x118>(x, 0.f);
+    return x;
+  };
+  const int64_t NW = a.B * a.T * a.R;  // windows per score plane
+  struct Win {
+    u32x4 g, h, f2[4];
+  };
+  auto load = [&](uint32_t d, Win& w) {
+    const int64_t widx = d >> 12;                              // b T + s
+    const int64_t mrow = ((widx + 2) * a.R + r) * D + pc * 8;  // position s + 2 of sequence b
+    w.g = ld_raw16(grad, mrow * 2, a.nt != 0);
+    if constexpr (HARD) w.h = ld_raw16(hard, mrow * 2, a.nt != 0);
+    const uint32_t addr = d & 4095;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      w.f2[k] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              trs, ((addr ^ (256u << k)) << 8) | (static_cast<uint32_t>(pc) << 4), 0, 0));
+  };
+  auto score = [&](uint32_t d, const Win& w) {  // the window's 12 scores, digit e to plane e
+    const uint32_t addr = d & 4095, loc = addr & 255;
+    u32x4 rv[9];
+    rv[8] = HARD ? w.h : row(loc);
+#pragma unroll
+    for (int f = 0; f < 8; ++f) rv[f] = row(loc ^ (1u << f));
+    const float cd = sum_last(dot8_bf16(rv[8], w.g));
+    float sc[12];
+#pragma unroll
+    for (int f = 0; f < 8; ++f) sc[f] = (sum_last(dot8_bf16(rv[f], w.g)) - cd) * (((addr >> f) & 1) ? -1.f : 1.f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      sc[8 + k] = (sum_last(dot8_bf16(w.f2[k], w.g)) - cd) * (((addr >> (8 + k)) & 1) ? -1.f : 1.f);
+    if (l == 15) {
+      f32x4* o = reinterpret_cast<f32x4*>(scores) + static_cast<int64_t>(r) * NWIN + (d >> 12);
+      o[0] = f32x4{sc[0], sc[1], sc[2], sc[3]};
+      o[NW] = f32x4{sc[4], sc[5], sc[6], sc[7]};
+      o[2 * NW] = f32x4{sc[8], sc[9], sc[10], sc[11]};
+    }
+  };
+  for (int w0 = 0; w0 < NWIN; w0 += span) {
+    if (total > SG3_MAXD) {  // list windows [w0, w1) of the bin
+    if (tid == 0) nl[1] = 0;
+    __syncthreads();
+    const int w1 = min(NWIN, w0 + span);
+    for (int c = 0; c < 4; ++c) {
+      const int wb = (c * NT + tid) * SG3_WPT;
+      if (wb >= w1 || wb + SG3_WPT <= w0) continue;
+      const u32x4 q0 = *reinterpret_cast<const u32x4*>(ct + wb);
+      const u32x4 q1 = *reinterpret_cast<const u32x4*>(ct + wb + 16);
+      const u32x4 q2 = *reinterpret_cast<const u32x4*>(ct + wb + 32);
+      const int lo = max(w0 - wb, 0), hi = min(w1 - wb, SG3_WPT);  // 0 <= lo < hi <= 32
+      uint32_t m = bin_mask(q0, q1, q2, wb) & (hi == 32 ? ~0u : (1u << hi) - 1u) & ~((1u << lo) - 1u);
+      if (!m) continue;
+      int slot = atomicAdd(&nl[1], __builtin_popcount(m));
+      for (; m; m &= m - 1) {
+        const int w = wb + __builtin_ctz(m);
+        const uint32_t addr = static_cast<uint32_t>(ct[w] & 15) | (static_cast<uint32_t>(ct[w + 1] & 15) << 4) | (v << 8);
+        dl[slot++] = (static_cast<uint32_t>(w) << 12) | addr;
+      }
+    }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the sub-block copy (first list)
+    __syncthreads();
+    const int n = total > SG3_MAXD ? nl[1] : total;
+    // entries grp, grp + NG, ... of the list, the next window's rows requested before the current one
+    // is scored
+    if (grp < n) {
+      auto at = [&](int j) { return dl[j]; };
+      Win cur, nxt;
+      load(at(grp), cur);
+      for (int j = grp; j < n; j += NG) {
+        if (j + NG < n) load(at(j + NG), nxt);
+        score(dl[j], cur);
+        cur = nxt;
+      }
+    }
+    __syncthreads();  // before the next list overwrites this one
+  }
+}
+
+// out[b, t, r, k] = slope * (((0 + S0(t)[k]) + S1(t - 1)[k]) + S2(t - 2)[k]) with Se(w) = scores[e][r][w]
+// (w = b T + s) and 0 for a window without a gradient row (the reference's sum over e ascending).  A
+// block per tile of 64 positions x 16 routes: the scores are read along positions (one route a wave)
+// and the sums pass through LDS to be scaled and written along routes.
+__global__ __launch_bounds__(256) void k_sg3_out(SgArgs a, const float* __restrict__ scores) {
+  __shared__ f32x4 tile[64][17];
+  const int T = static_cast<int>(a.T), NWIN = static_cast<int>(a.B) * T, R = a.R;
+  const int bt0 = blockIdx.x * 64, r0 = blockIdx.y * 16, tid = threadIdx.x;
+  const int64_t NW = static_cast<int64_t>(NWIN) * R;  // windows per score plane
+  const bool active = a.T > 2 && a.temperature != 0.f && a.scale != 0.f;
+  const f32x4* sp = reinterpret_cast<const f32x4*>(scores);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = k * 256 + tid, rl = p >> 6, bl = p & 63;
+    const int r = r0 + rl, bt = bt0 + bl;
+    f32x4 acc{0.f, 0.f, 0.f, 0.f};
+    if (r < R && bt < NWIN) {
+      const int b = bt / T, t = bt - b * T;
+#pragma unroll
+      for (int e = 0; e < 3; ++e) {
+        const f32x4 v = active && sg3_live(a, b, t - e) ? sp[e * NW + static_cast<int64_t>(r) * NWIN + (bt - e)]
+                                                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] += v[q];
+      }
+    }
+    tile[bl][rl] = acc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int p = k * 256 + tid, bl = p >> 4, rl = p & 15;
+    const int r = r0 + rl, bt = bt0 + bl;
+    if (r >= R || bt >= NWIN) continue;
+    f32x4 acc = tile[bl][rl];
+    const int64_t i = static_cast<int64_t>(bt) * R + r;  // (b T + t) R + r
+    if (active) {
+      f32x4 qv;
+      if (a.q_dt == LNG_BF16) {
+        const bf16x4 qh = reinterpret_cast<const bf16x4*>(a.q)[i];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) qv[q] = static_cast<float>(qh[q]);
+      } else {
+        qv = reinterpret_cast<const f32x4*>(a.q)[i];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float pr = 1.f / (1.f + expf(-(a.temperature * qv[q])));
+        acc[q] *= a.alpha * pr * (1.f - pr);
+      }
+    }
+    if (a.out_dt == LNG_BF16) {
+      bf16x4 o;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = static_cast<bf16>(acc[q]);
+      reinterpret_cast<bf16x4*>(a.out)[i] = o;
+    } else {
+      reinterpret_cast<f32x4*>(a.out)[i] = acc;
+    }
+  }
+}
+
+// whether the binned order-3 path serves a call, and its workspace
+static bool sg3_ok(int mem_dtype, int exact, int64_t D, int32_t order, int32_t bits, int64_t B, int64_t T, int32_t R) {
+  return mem_dtype == LNG_BF16 && !exact && D == 128 && order == 3 && bits == 4 && R <= 256 && T > 2 &&
+         B * T <= SG3_MAXW && T * R * D * 2 < (int64_t{1} << 31);
+}
+
+static int sg3_launch(const SgArgs& a, uint8_t* ws, hipStream_t s) {
+  const Sg3Ws w = sg3_layout(a.B, a.T, a.R);
+  uint8_t* codes_t = ws + w.codes_t;
+  float* scores = reinterpret_cast<float*>(ws + w.scores);
+  const int stride = static_cast<int>(w.ct_stride);
+  const dim3 tg(static_cast<unsigned>(cdiv(a.B * a.T, 64)), static_cast<unsigned>(cdiv(a.R, 64)));
+  hipLaunchKernelGGL(k_sg3_transpose, tg, dim3(256), 0, s, a, codes_t, stride);
+  const unsigned mblocks = static_cast<unsigned>(8 * cdiv(a.R, 8) * 16);
+  if (a.hard)
+    hipLaunchKernelGGL(k_sg3_main<true>, dim3(mblocks), dim3(512), 0, s, a, codes_t, stride, scores);
+  else
+    hipLaunchKernelGGL(k_sg3_main<false>, dim3(mblocks), dim3(512), 0, s, a, codes_t, stride, scores);
+  hipLaunchKernelGGL(k_sg3_out, dim3(static_cast<unsigned>(cdiv(a.B * a.T, 64)), static_cast<unsigned>(cdiv(a.R, 16))),
+                     dim3(256), 0, s, a, scores);
+  return check_launch("surrogate_grad (order 3, binned)");
+}
+
 // Table gradient of the lookup (the embedding backward behind the surrogate's pass-through,
 // lngram_v2.py:1084-1092 and :454): table_grad[row(b, t, r)] += grad[b, t, r, :] * valid[b, t] for
 // every position with an order-`order` window.  One 16-lane group per (b, t, r); fp32 atomics, so
@@ -679,12 +997,11 @@ static int sg_launch_v(const SgArgs& a, int64_t D, hipStream_t s) {
 
 using namespace lng;
 
-extern "C" int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
-                                  int q_dtype, const void* codes, int codes_dtype, const void* table,
-                                  int64_t table_rows, const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R,
-                                  int32_t route_start, int32_t mem_dim, int32_t order, int32_t bits,
-                                  float temperature, float scale, int exact, void* grad_q, int out_dtype,
-                                  void* stream) {
+static int surrogate_grad_impl(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
+                               int q_dtype, const void* codes, int codes_dtype, const void* table, int64_t table_rows,
+                               const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R, int32_t route_start,
+                               int32_t mem_dim, int32_t order, int32_t bits, float temperature, float scale, int exact,
+                               void* workspace, size_t workspace_bytes, void* grad_q, int out_dtype, void* stream) {
   if (B < 0 || T < 0 || R <= 0 || route_start < 0 || order < 1 || order > SG_MAXORDER || bits < 1 ||
       bits > SG_MAXBITS || bits * order > 40)
     return fail(LNG_E_ARG, "surrogate_grad: bad shape (1 <= order <= 4, 1 <= bits <= 8)");
@@ -703,9 +1020,43 @@ extern "C" int lng_surrogate_grad(const void* grad_memory, const void* hard_memo
            order, bits, temperature, scale, static_cast<float>(static_cast<double>(scale) * temperature), grad_q,
            out_dtype, cdiv(T, SG_WIN - (order - 1)), mem_bytes < (int64_t(1) << 32) ? 1 : 0};
   hipStream_t s = as_stream(stream);
+  const bool active = T - order + 1 > 0 && temperature != 0.f && scale != 0.f;
+  if (workspace && active && sg3_ok(mem_dtype, exact, mem_dim, order, bits, B, T, R)) {
+    if (workspace_bytes < sg3_layout(B, T, R).total)
+      return fail(LNG_E_ARG, "surrogate_grad: workspace smaller than lng_surrogate_workspace_bytes");
+    return sg3_launch(a, static_cast<uint8_t*>(workspace), s);
+  }
   if (mem_dtype == LNG_BF16)
     return exact ? sg_launch_v<bf16, true>(a, mem_dim, s) : sg_launch_v<bf16, false>(a, mem_dim, s);
   return exact ? sg_launch_v<float, true>(a, mem_dim, s) : sg_launch_v<float, false>(a, mem_dim, s);
+}
+
+extern "C" int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem_dtype, const void* q_logits,
+                                  int q_dtype, const void* codes, int codes_dtype, const void* table,
+                                  int64_t table_rows, const uint8_t* valid_mask, int64_t B, int64_t T, int32_t R,
+                                  int32_t route_start, int32_t mem_dim, int32_t order, int32_t bits,
+                                  float temperature, float scale, int exact, void* grad_q, int out_dtype,
+                                  void* stream) {
+  return surrogate_grad_impl(grad_memory, hard_memory, mem_dtype, q_logits, q_dtype, codes, codes_dtype, table,
+                             table_rows, valid_mask, B, T, R, route_start, mem_dim, order, bits, temperature, scale,
+                             exact, nullptr, 0, grad_q, out_dtype, stream);
+}
+
+extern "C" size_t lng_surrogate_workspace_bytes(int64_t B, int64_t T, int32_t R, int32_t mem_dim, int32_t order,
+                                                int32_t bits, int mem_dtype, int exact) {
+  if (B <= 0 || T <= 0 || R <= 0) return 0;
+  return sg3_ok(mem_dtype, exact, mem_dim, order, bits, B, T, R) ? sg3_layout(B, T, R).total : 0;
+}
+
+extern "C" int lng_surrogate_grad_ws(const void* grad_memory, const void* hard_memory, int mem_dtype,
+                                     const void* q_logits, int q_dtype, const void* codes, int codes_dtype,
+                                     const void* table, int64_t table_rows, const uint8_t* valid_mask, int64_t B,
+                                     int64_t T, int32_t R, int32_t route_start, int32_t mem_dim, int32_t order,
+                                     int32_t bits, float temperature, float scale, int exact, void* workspace,
+                                     size_t workspace_bytes, void* grad_q, int out_dtype, void* stream) {
+  return surrogate_grad_impl(grad_memory, hard_memory, mem_dtype, q_logits, q_dtype, codes, codes_dtype, table,
+                             table_rows, valid_mask, B, T, R, route_start, mem_dim, order, bits, temperature, scale,
+                             exact, workspace, workspace_bytes, grad_q, out_dtype, stream);
 }
 
 extern "C" int lng_table_grad(const void* grad_memory, int mem_dtype, const void* codes, int codes_dtype,

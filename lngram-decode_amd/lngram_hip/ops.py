@@ -730,13 +730,31 @@ def gather_sum_scaled(tables, codes: torch.Tensor, orders, bits: int, scale_log2
     return out
 
 
+_sg_ws: dict = {}
+_sg_ws_lock = threading.Lock()
+
+
+def _surrogate_workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    """Scratch of ``lng_surrogate_grad_ws`` for (device, current stream), grown as needed: a call writes
+    every byte of it that it reads, and calls on one stream run in order."""
+    key = (dev.index, torch.cuda.current_stream(dev).cuda_stream)
+    with _sg_ws_lock:
+        ws = _sg_ws.get(key)
+        if ws is None or ws.numel() < nbytes:
+            ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _sg_ws[key] = ws
+        return ws
+
+
 def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor | None, q_logits: torch.Tensor,
                    codes: torch.Tensor, table: torch.Tensor, valid_mask: torch.Tensor | None, order: int, bits: int,
-                   route_start: int, temperature: float, scale: float, exact: bool) -> torch.Tensor:
+                   route_start: int, temperature: float, scale: float, exact: bool,
+                   workspace: bool = True) -> torch.Tensor:
     """Route-logit gradient ``[B, T, R, bits]`` (``q_logits``' dtype) of the lookup surrogate of one
     order (``lng_surrogate_grad``; ``_LngramSurrogate.backward``, ``lngram_v2.py:364-464``).
     ``hard_memory`` None: it is the lookup's own rows (``table[row] * valid``), which the kernel
-    then reads from the table instead of streaming them."""
+    then reads from the table instead of streaming them.  ``workspace``: shapes that have a
+    workspace path (``lng_surrogate_workspace_bytes``) take it (``lng_surrogate_grad_ws``)."""
     dev = _dev(grad_memory, hard_memory, q_logits, codes, table, valid_mask)
     b, t, r, md = grad_memory.shape
     if (hard_memory is not None and tuple(hard_memory.shape) != (b, t, r, md)) or \
@@ -754,10 +772,20 @@ def surrogate_grad(grad_memory: torch.Tensor, hard_memory: torch.Tensor | None, 
     if vm is not None and tuple(vm.shape) != (b, t):
         raise ValueError("surrogate_grad: valid_mask must be [B, T]")
     out = torch.empty(b, t, r, bits, dtype=q.dtype, device=dev)
-    rc = _timed("surrogate_grad", dev, lambda: lib().lng_surrogate_grad(
-        _ptr(g), _ptr(hm), dtype_code(mdt), _ptr(q), dtype_code(q.dtype), _ptr(cc), dtype_code(cc.dtype), _ptr(tab),
-        tab.shape[0], _ptr(vm), b, t, r, int(route_start), md, int(order), int(bits), float(temperature),
-        float(scale), int(bool(exact)), _ptr(out), dtype_code(out.dtype), _stream(dev)))
+    nws = lib().lng_surrogate_workspace_bytes(b, t, r, md, int(order), int(bits), dtype_code(mdt),
+                                              int(bool(exact))) if workspace else 0
+    if nws:
+        ws = _surrogate_workspace(dev, nws)
+        rc = _timed("surrogate_grad", dev, lambda: lib().lng_surrogate_grad_ws(
+            _ptr(g), _ptr(hm), dtype_code(mdt), _ptr(q), dtype_code(q.dtype), _ptr(cc), dtype_code(cc.dtype),
+            _ptr(tab), tab.shape[0], _ptr(vm), b, t, r, int(route_start), md, int(order), int(bits),
+            float(temperature), float(scale), int(bool(exact)), _ptr(ws), ws.numel(), _ptr(out),
+            dtype_code(out.dtype), _stream(dev)))
+    else:
+        rc = _timed("surrogate_grad", dev, lambda: lib().lng_surrogate_grad(
+            _ptr(g), _ptr(hm), dtype_code(mdt), _ptr(q), dtype_code(q.dtype), _ptr(cc), dtype_code(cc.dtype),
+            _ptr(tab), tab.shape[0], _ptr(vm), b, t, r, int(route_start), md, int(order), int(bits),
+            float(temperature), float(scale), int(bool(exact)), _ptr(out), dtype_code(out.dtype), _stream(dev)))
     check(rc, "surrogate_grad")
     return out
 

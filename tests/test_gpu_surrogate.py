@@ -187,6 +187,41 @@ def test_hard_rows_from_table_equal_saved_rows(dev, shape):
             assert torch.equal(got, want), (shape, order, exact)
 
 
+@pytest.mark.parametrize("saved,case", [(False, "uniform"), (True, "uniform"), (False, "skewed")])
+def test_order3_binned_path_matches_direct_path_and_oracle(dev, saved, case):
+    """Order 3 with a workspace (windows binned by their newest code, a 64 KB sub-block of the
+    table on chip per bin) against the direct kernel (fp32 rounding: the within-row summation
+    order differs) and the fp64 oracle, with masked positions and a route offset.  "skewed" puts
+    about 4,000 of a route's 5,000 windows in one bin: more than one on-chip list holds, so the
+    bin is listed in ranges."""
+    B, T, R, rs = {"uniform": (3, 400, 40, 2), "skewed": (2, 2500, 6, 1)}[case]
+    D, bits, order = 128, 4, 3
+    gen = torch.Generator().manual_seed(41)
+    A = 1 << bits
+    table = (torch.randn((rs + R) * A ** order, D, generator=gen) * 0.5).to(torch.bfloat16)
+    codes = torch.randint(0, A, (B, T, R), generator=gen, dtype=torch.uint8)
+    if case == "skewed":
+        codes[torch.rand(B, T, R, generator=gen) < 0.8] = 3
+    q = torch.randn(B, T, R, bits, generator=gen)
+    grad = torch.randn(B, T, R, D, generator=gen).to(torch.bfloat16)
+    valid = torch.rand(B, T, generator=gen) > 0.15
+    valid[:, :order - 1] = False
+    hard = ops.route_tokens(codes.to(dev), [table[rs * A ** order:].to(dev)], [order], bits) * \
+        valid.to(dev)[:, :, None, None].to(torch.bfloat16)
+    args = (grad.to(dev), hard if saved else None, q.to(dev), codes.to(dev), table.to(dev), valid.to(dev), order,
+            bits, rs, 0.9, 1.1, False)
+    assert ops.lib().lng_surrogate_workspace_bytes(B, T, R, D, order, bits, 1, 0) > 0
+    got = ops.surrogate_grad(*args)
+    direct = ops.surrogate_grad(*args, workspace=False)
+    assert om.rel_err(got.cpu(), direct.cpu()) < 1e-6
+    want = om.surrogate_grad(grad, hard.cpu(), q, codes.numpy(), table, valid.numpy(), order, bits, rs, 0.9, 1.1, False)
+    assert om.rel_err(got.cpu(), want) < 1e-5
+    again = ops.surrogate_grad(*args)                     # the workspace is reused: same result
+    assert torch.equal(again, got)
+    # the binned path takes at most 65,536 windows a route; longer calls use the direct kernel
+    assert ops.lib().lng_surrogate_workspace_bytes(1, 65537, R, D, order, bits, 1, 0) == 0
+
+
 def test_table_grad_matches_scatter(dev):
     B, T, R, rs, D, order, bits = 2, 30, 5, 1, 64, 3, 2
     x = _random_case(17, B, T, R, rs, D, order, bits, torch.float32)
