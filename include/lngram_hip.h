@@ -334,8 +334,10 @@ int lng_surrogate_grad(const void* grad_memory, const void* hard_memory, int mem
  * of the twelve counterfactual rows of its windows from one 64 KB sub-block of the table held on
  * chip; the workspace holds a route-major copy of the codes and every window's twelve scores, each
  * written by the call before it is read (no clearing needed; calls that share a workspace must be
- * ordered, e.g. on one stream).  Other shapes (size 0)
- * take lng_surrogate_grad's path and ignore the workspace.  The result is a fixed sum per output in
+ * ordered, e.g. on one stream).  The binned path needs a 256-byte aligned workspace and 16-byte
+ * aligned rows, logits and gradient (8-byte for bf16 logits and gradient); other buffers and
+ * other shapes (size 0) take lng_surrogate_grad's path and ignore the workspace.  The result is a
+ * fixed sum per output in
  * the reference's order, as lng_surrogate_grad's (the within-row summation order differs, so the
  * two paths agree to fp32 rounding). */
 size_t lng_surrogate_workspace_bytes(int64_t B, int64_t T, int32_t R, int32_t mem_dim, int32_t order, int32_t bits,

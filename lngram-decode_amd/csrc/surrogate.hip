@@ -1021,7 +1021,11 @@ static int surrogate_grad_impl(const void* grad_memory, const void* hard_memory,
            out_dtype, cdiv(T, SG_WIN - (order - 1)), mem_bytes < (int64_t(1) << 32) ? 1 : 0};
   hipStream_t s = as_stream(stream);
   const bool active = T - order + 1 > 0 && temperature != 0.f && scale != 0.f;
-  if (workspace && active && sg3_ok(mem_dtype, exact, mem_dim, order, bits, B, T, R)) {
+  // the binned path moves 16-byte vectors (8-byte for bf16 logits and gradient): it serves aligned buffers
+  auto al = [](const void* p, uintptr_t n) { return p == nullptr || (reinterpret_cast<uintptr_t>(p) & (n - 1)) == 0; };
+  const bool aligned = al(workspace, 256) && al(grad_memory, 16) && al(hard_memory, 16) && al(table, 16) &&
+                       al(q_logits, q_dtype == LNG_BF16 ? 8 : 16) && al(grad_q, out_dtype == LNG_BF16 ? 8 : 16);
+  if (workspace && active && aligned && sg3_ok(mem_dtype, exact, mem_dim, order, bits, B, T, R)) {
     if (workspace_bytes < sg3_layout(B, T, R).total)
       return fail(LNG_E_ARG, "surrogate_grad: workspace smaller than lng_surrogate_workspace_bytes");
     return sg3_launch(a, static_cast<uint8_t*>(workspace), s);

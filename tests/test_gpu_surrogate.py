@@ -222,6 +222,38 @@ def test_order3_binned_path_matches_direct_path_and_oracle(dev, saved, case):
     assert ops.lib().lng_surrogate_workspace_bytes(1, 65537, R, D, order, bits, 1, 0) == 0
 
 
+def test_order3_binned_path_takes_the_direct_kernel_for_unaligned_buffers(dev):
+    """``lng_surrogate_grad_ws`` through the C ABI with a workspace 16 bytes past a 256-byte boundary,
+    then with a gradient buffer 4 bytes past a 16-byte boundary: both calls take the direct kernel
+    (the binned path moves 16-byte vectors), so they equal ``lng_surrogate_grad`` bit for bit."""
+    B, T, R, rs, D, bits, order = 2, 300, 24, 1, 128, 4, 3
+    gen = torch.Generator().manual_seed(43)
+    A = 1 << bits
+    table = (torch.randn((rs + R) * A ** order, D, generator=gen) * 0.5).to(torch.bfloat16).to(dev)
+    codes = torch.randint(0, A, (B, T, R), generator=gen, dtype=torch.uint8).to(dev)
+    q = torch.randn(B, T, R, bits, generator=gen).to(dev)
+    grad = torch.randn(B, T, R, D, generator=gen).to(torch.bfloat16).to(dev)
+    valid = torch.ones(B, T, dtype=torch.bool)
+    valid[:, :order - 1] = False
+    valid = valid.to(dev)
+    lib = ops.lib()
+    nws = lib.lng_surrogate_workspace_bytes(B, T, R, D, order, bits, ops.dtype_code(torch.bfloat16), 0)
+    assert nws > 0
+    want = ops.surrogate_grad(grad, None, q, codes, table, valid, order, bits, rs, 0.9, 1.1, False, workspace=False)
+    ws = torch.empty(nws + 512, dtype=torch.uint8, device=dev)
+    store = torch.empty(B * T * R * bits + 1, dtype=torch.float32, device=dev)
+    for ws_off, out in ((16, store[:-1]), (0, store[1:])):
+        out.zero_()
+        rc = lib.lng_surrogate_grad_ws(
+            grad.data_ptr(), None, ops.dtype_code(grad.dtype), q.data_ptr(), ops.dtype_code(q.dtype), codes.data_ptr(),
+            ops.dtype_code(codes.dtype), table.data_ptr(), table.shape[0], valid.data_ptr(), B, T, R, rs, D, order,
+            bits, 0.9, 1.1, 0, ws.data_ptr() + ws_off, nws, out.data_ptr(), ops.dtype_code(out.dtype),
+            torch.cuda.current_stream(dev).cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(B, T, R, bits), want), ws_off
+
+
 def test_table_grad_matches_scatter(dev):
     B, T, R, rs, D, order, bits = 2, 30, 5, 1, 64, 3, 2
     x = _random_case(17, B, T, R, rs, D, order, bits, torch.float32)
