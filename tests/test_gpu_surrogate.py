@@ -222,6 +222,29 @@ def test_order3_binned_path_matches_direct_path_and_oracle(dev, saved, case):
     assert ops.lib().lng_surrogate_workspace_bytes(1, 65537, R, D, order, bits, 1, 0) == 0
 
 
+def test_order3_binned_path_at_its_largest_route(dev):
+    """B T = 65,536 windows a route, the most the binned path takes (every thread's four 32-window
+    chunks in use, each bin over the 2048-entry list, so every bin is listed in ranges), against
+    the direct kernel; one window more and the call takes the direct kernel."""
+    B, T, R, rs, D, bits, order = 2, 32768, 3, 1, 128, 4, 3
+    gen = torch.Generator().manual_seed(45)
+    A = 1 << bits
+    table = (torch.randn((rs + R) * A ** order, D, generator=gen) * 0.5).to(torch.bfloat16).to(dev)
+    codes = torch.randint(0, A, (B, T, R), generator=gen, dtype=torch.uint8).to(dev)
+    q = torch.randn(B, T, R, bits, generator=gen).to(dev)
+    grad = torch.randn(B, T, R, D, generator=gen).to(torch.bfloat16).to(dev)
+    valid = torch.rand(B, T, generator=gen) > 0.1
+    valid[:, :order - 1] = False
+    valid = valid.to(dev)
+    dt = ops.dtype_code(torch.bfloat16)
+    assert ops.lib().lng_surrogate_workspace_bytes(B, T, R, D, order, bits, dt, 0) > 0
+    assert ops.lib().lng_surrogate_workspace_bytes(B, T + 1, R, D, order, bits, dt, 0) == 0
+    args = (grad, None, q, codes, table, valid, order, bits, rs, 0.9, 1.1, False)
+    got = ops.surrogate_grad(*args)
+    direct = ops.surrogate_grad(*args, workspace=False)
+    assert om.rel_err(got.cpu(), direct.cpu()) < 1e-6
+
+
 def test_order3_binned_path_takes_the_direct_kernel_for_unaligned_buffers(dev):
     """``lng_surrogate_grad_ws`` through the C ABI with a workspace 16 bytes past a 256-byte boundary,
     then with a gradient buffer 4 bytes past a 16-byte boundary: both calls take the direct kernel
