@@ -670,8 +670,8 @@ __global__ __launch_bounds__(256) void k_sg3_transpose(SgArgs a, uint8_t* __rest
 // holds piece (l + 8 (g & 1)) & 15 of every row (the two halves of an LDS pass cover all 64 banks).
 // Scores of digit e to plane e: scores[e][r][b T + s][bit].
 template <bool HARD>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_sg3_main(SgArgs a, const uint8_t* __restrict__ codes_t, int stride,
-                                                     float* __restrict__ scores) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k_sg3_main(
+    SgArgs a, const uint8_t* __restrict__ codes_t, int stride, float* __restrict__ scores) {
   constexpr int NT = 512, NG = NT / 16, NWV = NT / 64;
   constexpr int64_t D = 128;
   __shared__ __attribute__((aligned(16))) bf16 tab[256 * D];
@@ -795,25 +795,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void k
   };
   for (int w0 = 0; w0 < NWIN; w0 += span) {
     if (total > SG3_MAXD) {  // list windows [w0, w1) of the bin
-    if (tid == 0) nl[1] = 0;
-    __syncthreads();
-    const int w1 = min(NWIN, w0 + span);
-    for (int c = 0; c < 4; ++c) {
-      const int wb = (c * NT + tid) * SG3_WPT;
-      if (wb >= w1 || wb + SG3_WPT <= w0) continue;
-      const u32x4 q0 = *reinterpret_cast<const u32x4*>(ct + wb);
-      const u32x4 q1 = *reinterpret_cast<const u32x4*>(ct + wb + 16);
-      const u32x4 q2 = *reinterpret_cast<const u32x4*>(ct + wb + 32);
-      const int lo = max(w0 - wb, 0), hi = min(w1 - wb, SG3_WPT);  // 0 <= lo < hi <= 32
-      uint32_t m = bin_mask(q0, q1, q2, wb) & (hi == 32 ? ~0u : (1u << hi) - 1u) & ~((1u << lo) - 1u);
-      if (!m) continue;
-      int slot = atomicAdd(&nl[1], __builtin_popcount(m));
-      for (; m; m &= m - 1) {
-        const int w = wb + __builtin_ctz(m);
-        const uint32_t addr = static_cast<uint32_t>(ct[w] & 15) | (static_cast<uint32_t>(ct[w + 1] & 15) << 4) | (v << 8);
-        dl[slot++] = (static_cast<uint32_t>(w) << 12) | addr;
+      if (tid == 0) nl[1] = 0;
+      __syncthreads();
+      const int w1 = min(NWIN, w0 + span);
+      for (int c = 0; c < 4; ++c) {
+        const int wb = (c * NT + tid) * SG3_WPT;
+        if (wb >= w1 || wb + SG3_WPT <= w0) continue;
+        const u32x4 q0 = *reinterpret_cast<const u32x4*>(ct + wb);
+        const u32x4 q1 = *reinterpret_cast<const u32x4*>(ct + wb + 16);
+        const u32x4 q2 = *reinterpret_cast<const u32x4*>(ct + wb + 32);
+        const int lo = max(w0 - wb, 0), hi = min(w1 - wb, SG3_WPT);  // 0 <= lo < hi <= 32
+        uint32_t m = bin_mask(q0, q1, q2, wb) & (hi == 32 ? ~0u : (1u << hi) - 1u) & ~((1u << lo) - 1u);
+        if (!m) continue;
+        int slot = atomicAdd(&nl[1], __builtin_popcount(m));
+        for (; m; m &= m - 1) {
+          const int w = wb + __builtin_ctz(m);
+          const uint32_t addr = static_cast<uint32_t>(ct[w] & 15) | (static_cast<uint32_t>(ct[w + 1] & 15) << 4) | (v << 8);
+          dl[slot++] = (static_cast<uint32_t>(w) << 12) | addr;
+        }
       }
-    }
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the sub-block copy (first list)
     __syncthreads();
