@@ -126,6 +126,21 @@ int lng_route_tokens(const void* codes, int codes_dtype, int64_t B, int64_t T, i
                      const int32_t* segment_ids, const uint8_t* valid_tokens, int32_t target_length,
                      void* out, void* stream);
 
+/* The n-gram windows of a draft tree's nodes for the memory block of tree verification
+ * (tree_ngram_codes / tree_route_tokens, drafting/tree.py:114-136, as tree_verify_step uses them,
+ * :179-196), with the nodes' codes cached, in one launch.  idx [n, hist+1] (int32) names each
+ * window slot in cat(the last hist cached codes, the n node codes); L = L0 + *L_dev (L_dev: a
+ * device int32, or null), the cached length.  Writes win [B*n, hist+1, R] u8 (the slot's code, 0
+ * where the slot is a position before 0), seg [B*n, hist+1] int32 and val [B*n, hist+1] u8 (1 where
+ * the slot is real: lng_route_tokens' segment ids and valid tokens for those windows), the node
+ * codes [B, n, R] into cache [B, max_len, R] u8 at positions L .. L+n-1, and slots [n, n_rel] =
+ * rel + L (int32; the conv windows of lng_causal_conv_slots).  The caller keeps L + n <= max_len
+ * (checked here when L_dev is null). */
+int lng_tree_windows(const void* node_codes, int node_codes_dtype, uint8_t* cache, int64_t B, int64_t max_len,
+                     int32_t R, int32_t n, int32_t hist, const int32_t* idx, int64_t L0, const int32_t* L_dev,
+                     const int32_t* rel, int32_t n_rel, uint8_t* win, int32_t* seg, uint8_t* val, int32_t* slots,
+                     void* stream);
+
 /* out[rows, dim] = RMSNorm(x) * w with one of the reference's two roundings:
  * LNG_NORM_MODEL  model.RMSNorm (model.py:39-48): normalise in fp32, round to the storage
  *                 dtype, multiply by w, round;

@@ -148,11 +148,83 @@ __global__ void k_tree_accept(const int32_t* parent, const int64_t* node_tokens,
   *path_len = len;
 }
 
+// The n-gram windows of a draft tree's nodes for the memory block of tree verification
+// (tree_ngram_codes / tree_route_tokens, drafting/tree.py:114-136 and :179-196), over a history of
+// `hist` cached codes, in one launch: idx [n][hist + 1] names each window slot in cat(history,
+// nodes); win[(b n + i)][j][r] is that slot's code (0 where the slot is not real: a history
+// position before 0), seg and val its reality (the lookup's segment ids and valid tokens); the
+// nodes' codes go into the cache at L .. L + n - 1 (disjoint from the history read) and the conv
+// slots are rel + L.  L = L0 + *L_dev (L_dev may be null).  One grid-stride pass over the four parts.
+__global__ __launch_bounds__(256) void k_tree_windows(const void* __restrict__ node_codes, int nc_dt,
+                                                      uint8_t* __restrict__ cache, int64_t stride, int32_t R,
+                                                      int64_t B, int32_t n, int32_t hist,
+                                                      const int32_t* __restrict__ idx, int64_t L0,
+                                                      const int32_t* __restrict__ L_dev,
+                                                      const int32_t* __restrict__ rel, int32_t nrel,
+                                                      uint8_t* __restrict__ win, int32_t* __restrict__ seg,
+                                                      uint8_t* __restrict__ val, int32_t* __restrict__ slots) {
+  const int64_t L = L0 + (L_dev ? static_cast<int64_t>(*L_dev) : 0);
+  const int64_t H = hist + 1;
+  const int64_t e_win = B * n * H * R, e_seg = B * n * H, e_cache = B * n * R, e_slot = static_cast<int64_t>(n) * nrel;
+  auto code = [&](int64_t i) -> uint8_t {  // node code i of [B, n, R], cast as the cache's dtype
+    switch (nc_dt) {
+      case LNG_U8: return static_cast<const uint8_t*>(node_codes)[i];
+      case LNG_I32: return static_cast<uint8_t>(static_cast<const int32_t*>(node_codes)[i]);
+      default: return static_cast<uint8_t>(static_cast<const int64_t*>(node_codes)[i]);
+    }
+  };
+  for (int64_t e = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < e_win + e_seg + e_cache + e_slot;
+       e += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    if (e < e_win) {
+      const int64_t r = e % R, bij = e / R, j = bij % H, bi = bij / H, i = bi % n, b = bi / n;
+      const int q = idx[i * H + j];
+      uint8_t c = 0;
+      if (q >= hist) {
+        c = code((b * n + (q - hist)) * R + r);
+      } else {
+        const int64_t pos = L - hist + q;
+        if (pos >= 0) c = cache[(b * stride + pos) * R + r];
+      }
+      win[e] = c;
+    } else if (e < e_win + e_seg) {
+      const int64_t k = e - e_win, j = k % H, i = (k / H) % n;
+      const int q = idx[i * H + j];
+      const bool real = q >= hist || L - hist + q >= 0;
+      seg[k] = real ? 1 : 0;
+      val[k] = real ? 1 : 0;
+    } else if (e < e_win + e_seg + e_cache) {
+      const int64_t k = e - e_win - e_seg, r = k % R, bi = k / R, i = bi % n, b = bi / n;
+      cache[(b * stride + L + i) * R + r] = code(k);
+    } else {
+      const int64_t k = e - e_win - e_seg - e_cache;
+      slots[k] = static_cast<int32_t>(rel[k] + L);
+    }
+  }
+}
+
 }  // namespace lng
 
 using namespace lng;
 
 extern "C" {
+
+int lng_tree_windows(const void* node_codes, int node_codes_dtype, uint8_t* cache, int64_t B, int64_t max_len,
+                     int32_t R, int32_t n, int32_t hist, const int32_t* idx, int64_t L0, const int32_t* L_dev,
+                     const int32_t* rel, int32_t n_rel, uint8_t* win, int32_t* seg, uint8_t* val, int32_t* slots,
+                     void* stream) {
+  if (B <= 0 || max_len <= 0 || R <= 0 || n <= 0 || hist < 0 || n_rel < 0 || L0 < 0)
+    return fail(LNG_E_ARG, "tree_windows: bad shape");
+  if (node_codes_dtype != LNG_U8 && node_codes_dtype != LNG_I32 && node_codes_dtype != LNG_I64)
+    return fail(LNG_E_DTYPE, "tree_windows: node codes u8, i32 or i64");
+  if (!node_codes || !cache || !idx || !win || !seg || !val || (n_rel && (!rel || !slots)))
+    return fail(LNG_E_ARG, "tree_windows: null buffer");
+  if (!L_dev && L0 + n > max_len) return fail(LNG_E_ARG, "tree_windows: cache full");
+  const int64_t total = B * n * (hist + 1) * (R + 1) + B * n * R + static_cast<int64_t>(n) * n_rel;
+  const unsigned grid = static_cast<unsigned>(cdiv(total, 256) < 1024 ? cdiv(total, 256) : 1024);
+  hipLaunchKernelGGL(k_tree_windows, dim3(grid), dim3(256), 0, as_stream(stream), node_codes, node_codes_dtype,
+                     cache, max_len, R, B, n, hist, idx, L0, L_dev, rel, n_rel, win, seg, val, slots);
+  return check_launch("tree_windows");
+}
 
 int lng_abi_version(void) { return 2; }
 

@@ -301,8 +301,9 @@ def _parent_index(parent, device) -> tuple:
 def _tree_index(parent, hist: int, back: int, device) -> tuple:
     """Device index tables of a tree shape, built once per (parent, hist, back, device):
     ``idx [n, hist + 1]``, the n-gram window slots of every node in ``cat(history of hist codes,
-    node codes)`` (``tree_slots`` with a history of ``hist`` positions), and ``rel [n, back + 1]``
-    int32, the conv window slots relative to the cached length (negative: history positions)."""
+    node codes)`` (``tree_slots`` with a history of ``hist`` positions), ``rel [n, back + 1]``
+    int32, the conv window slots relative to the cached length (negative: history positions), and
+    ``idx`` as int32."""
     from drafting.tree import tree_slots
 
     key = (tuple(int(p) for p in parent), int(hist), int(back), str(device))
@@ -310,7 +311,7 @@ def _tree_index(parent, hist: int, back: int, device) -> tuple:
     if t is None:
         idx, _ = tree_slots(parent, hist, hist)          # every slot lies in the window's reach
         full, _ = tree_slots(parent, back + 1, back)     # all valid at a length of back + 1
-        t = (idx.to(device), (full - (back + 1)).to(torch.int32).to(device))
+        t = (idx.to(device), (full - (back + 1)).to(torch.int32).to(device), idx.to(torch.int32).to(device))
         _TREE_INDEX[key] = t
     return t
 
@@ -318,8 +319,6 @@ def _tree_index(parent, hist: int, back: int, device) -> tuple:
 def _tree_memory(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, parent, L: int,
                  L_t: Tensor | None) -> Tensor:
     """``tree_memory_step`` at the cached length ``L`` (host) or ``*L_t`` (device int32, L = 0)."""
-    from drafting.drafters import window_route_tokens
-
     mem = model.blocks[pos].memory
     m = mem.module
     b, n = h.shape[0], h.shape[1]
@@ -329,23 +328,16 @@ def _tree_memory(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, 
     cache = state.codes[pos]
     hist = m.route_history_length
     conv = m.short_conv
-    idx, rel = _tree_index(parent, hist, conv.left_padding, dev)
-    c8 = codes.to(cache.dtype)
-    # the node windows over (the last `hist` cached codes, the nodes' codes); a history slot before
-    # position 0 is not real (its n-grams read zero rows)
-    base = (L - hist) + torch.arange(hist, device=dev)
-    if L_t is not None:
-        base = base + L_t.to(torch.long)
-    seq = torch.cat((cache.index_select(1, base.clamp_min(0)), c8), 1)
-    real = (idx >= hist) | ((idx - hist + (L if L_t is None else L_t.to(torch.long))) >= 0)
+    _, rel, idx32 = _tree_index(parent, hist, conv.left_padding, dev)
     r = cache.shape[-1]
-    ctx = seq.index_select(1, idx.reshape(-1)).view(b, n * (hist + 1), r)
-    rt = window_route_tokens(m, ctx.view(b * n, hist + 1, r), real[None].expand(b, n, hist + 1).reshape(b * n, -1))
-    rt = rt.view(b, n, r, -1)
-    if L_t is None:
-        cache[:, L:L + n] = c8
-    else:
-        cache.index_copy_(1, L_t.to(torch.long) + torch.arange(n, device=dev), c8)
+    L_dev = None if L_t is None else L_t.to(torch.int32).reshape(1)
+    # the node windows over (the last `hist` cached codes, the nodes' codes; a history slot before
+    # position 0 is not real and its n-grams read zero rows), the node codes cached at L .. L+n-1 and
+    # the conv slots, in one launch (the code caches are uint8: codes have at most 8 bits)
+    win, seg, val, slots = ops.tree_windows(cache, codes, idx32, hist, L, L_dev, rel)
+    tables = [m.tables[f"ngram_{o}"].weight for o in m.ngrams]
+    rt = ops.route_tokens(win, tables, m.ngrams, m.bits_per_route, 0, m.num_routes, seg, val, 1)
+    rt = rt[:, -1].view(b, n, r, -1)
     if m._fused_shape_ok(h, tables=False):
         q_raw = ops.linear(h, m._folded_query_weight())
         head = ops.memory_readout_fused_rows(q_raw, rt.to(torch.bfloat16), m._fused_weights(),
@@ -355,9 +347,7 @@ def _tree_memory(model, pos: int, state: DecodeState, h: Tensor, codes: Tensor, 
         key, value = m._project_memory(rt.to(m.readout_kv_proj.weight.dtype))
         head = m._manual_gqa(m._project_query(h), key, value)
     conv_in = state.conv_in[pos]
-    L_dev = None if L_t is None else L_t.to(torch.int32).reshape(1)
     _oproj_to_cache(m, head, conv_in, L, n, L_dev)
-    slots = rel + (L if L_t is None else L_dev)
     length = L + n if L_t is None else conv_in.shape[1]
     return ops.causal_conv_slots(conv_in, conv.norm.weight, conv.conv.weight, conv.dilation, conv.norm.eps, slots,
                                  length=length, residual=True)

@@ -106,6 +106,8 @@ SIGNATURES = {
                                      ctypes.c_uint32, _p, _p]),
     "lng_surrogate_grad": (_int, [_p, _p, _int, _p, _int, _p, _int, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32,
                                   _i32, _i32, _f, _f, _int, _p, _int, _p]),
+    "lng_tree_windows": (_int, [_p, _int, _p, _i64, _i64, _i32, _i32, _i32, _p, _i64, _p, _p, _i32, _p, _p, _p, _p,
+                                _p]),
     "lng_surrogate_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i32, _i32, _i32, _i32, _int, _int]),
     "lng_surrogate_grad_ws": (_int, [_p, _p, _int, _p, _int, _p, _int, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32,
                                      _i32, _f, _f, _int, _p, ctypes.c_size_t, _p, _int, _p]),

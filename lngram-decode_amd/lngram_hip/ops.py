@@ -420,6 +420,31 @@ def router_codes_at(x: torch.Tensor, w: torch.Tensor, cache: torch.Tensor, pos0:
                                     _ptr(pos0_dev), _ptr(cache), _stream(dev)), "router_codes_at")
 
 
+def tree_windows(cache: torch.Tensor, node_codes: torch.Tensor, idx: torch.Tensor, hist: int, L: int,
+                 L_dev: torch.Tensor | None, rel: torch.Tensor):
+    """The n-gram windows of a draft tree's nodes and the node codes cached (``lng_tree_windows``):
+    ``cache [B, max_len, R]`` u8 (written at ``L .. L+n-1``), ``node_codes [B, n, R]``, ``idx
+    [n, hist+1]`` and ``rel [n, k]`` int32 device tables, ``L_dev`` a device int32 added to ``L``.
+    Returns ``(win [B*n, hist+1, R] u8, seg int32, val u8 [B*n, hist+1], slots [n, k] int32)``."""
+    dev = _dev(cache, node_codes, idx, rel, L_dev)
+    if cache.dtype != torch.uint8 or not cache.is_contiguous() or cache.dim() != 3:
+        raise ValueError("tree_windows: cache must be a contiguous [B, max_len, R] uint8 tensor")
+    b, max_len, r = cache.shape
+    nc = _c(node_codes)
+    n = nc.shape[1]
+    if tuple(nc.shape) != (b, n, r) or idx.dtype != torch.int32 or rel.dtype != torch.int32:
+        raise ValueError("tree_windows: node codes [B, n, R], int32 idx and rel")
+    h1 = idx.shape[1]
+    win = torch.empty(b * n, h1, r, dtype=torch.uint8, device=dev)
+    seg = torch.empty(b * n, h1, dtype=torch.int32, device=dev)
+    val = torch.empty(b * n, h1, dtype=torch.uint8, device=dev)
+    slots = torch.empty(n, rel.shape[1], dtype=torch.int32, device=dev)
+    check(lib().lng_tree_windows(_ptr(nc), dtype_code(nc.dtype), _ptr(cache), b, max_len, r, n, int(hist),
+                                 _ptr(_c(idx)), int(L), _ptr(L_dev), _ptr(_c(rel)), rel.shape[1], _ptr(win),
+                                 _ptr(seg), _ptr(val), _ptr(slots), _stream(dev)), "tree_windows")
+    return win, seg, val, slots
+
+
 def linear_rowsq(x: torch.Tensor, w: torch.Tensor):
     """bf16 ``x [..., K] . w[N, K]^T`` plus the partial row sums of squares of the bf16 output
     (``[P, rows]`` fp32) that :func:`causal_conv_rowsq` consumes."""

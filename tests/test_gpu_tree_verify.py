@@ -225,3 +225,37 @@ def test_tree_router_input_and_states_match_path_sequences(dev, L):
         out = tree_memory_step(model, 0, st, mem.module.readout_q_proj.weight.new_zeros(1, n, w.d_model) +
                                0.5, codes, PARENT)
         assert out.shape == (1, n, w.d_model) and bool(torch.isfinite(out.float()).all())
+
+
+@pytest.mark.parametrize("L", [0, 1, 5])
+@pytest.mark.parametrize("on_device", [False, True])
+def test_tree_windows_equal_index_formulation(dev, L, on_device):
+    """``lng_tree_windows`` against the same windows built from torch index ops: the codes of each
+    node's window over (the last 2 cached codes, the node codes), zero and not real where a history
+    slot precedes position 0; the node codes cached at L .. L+n-1; the conv slots rel + L.  Lengths
+    shorter than the history included, with the length on the host or in device memory."""
+    B, R, n, hist, back = 2, 5, len(PARENT), 2, 9
+    gen = torch.Generator().manual_seed(60 + L)
+    cache = torch.randint(0, 16, (B, 40, R), generator=gen, dtype=torch.uint8).to(dev)
+    codes = torch.randint(0, 16, (B, n, R), generator=gen, dtype=torch.int32).to(dev)
+    idx, _ = tree_slots(PARENT, hist, hist)
+    full, _ = tree_slots(PARENT, back + 1, back)
+    idx, rel = idx.to(dev), (full - (back + 1)).to(torch.int32).to(dev)
+    # the index formulation
+    c8 = codes.to(torch.uint8)
+    base = (L - hist) + torch.arange(hist, device=dev)
+    seq = torch.cat((cache.index_select(1, base.clamp_min(0)), c8), 1)
+    real = (idx >= hist) | ((idx - hist + L) >= 0)
+    want_win = seq.index_select(1, idx.reshape(-1)).view(B * n, hist + 1, R) * \
+        real[None].expand(B, n, hist + 1).reshape(B * n, hist + 1, 1).to(torch.uint8)
+    want_real = real[None].expand(B, n, hist + 1).reshape(B * n, hist + 1)
+    want_cache = cache.clone()
+    want_cache[:, L:L + n] = c8
+    L_dev = torch.tensor([L], dtype=torch.int32, device=dev) if on_device else None
+    win, seg, val, slots = ops.tree_windows(cache, codes, idx.to(torch.int32), hist, 0 if on_device else L, L_dev,
+                                            rel)
+    torch.cuda.synchronize()
+    assert torch.equal(win, want_win)
+    assert torch.equal(seg, want_real.to(torch.int32)) and torch.equal(val, want_real.to(torch.uint8))
+    assert torch.equal(cache, want_cache)
+    assert torch.equal(slots, rel + L)
